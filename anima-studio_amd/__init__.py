@@ -1,0 +1,248 @@
+"""Python binding of libanima.so (the C ABI in include/anima.h), used by the tests and bench.
+
+The product's host side is the Node N-API addon under js/; this module is a second thin host
+over the same C ABI.  It never computes anything itself: if libanima.so is missing or cannot
+be loaded, every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libanima.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "anima.h")
+
+ANIMA_OK = 0
+PREC_BF16 = 0
+PREC_FP32 = 1
+
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+_LIB = None
+
+
+class AnimaError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"anima error {code}: {msg}")
+        self.code = code
+
+
+class AttnDesc(ctypes.Structure):
+    _fields_ = [
+        ("B", ctypes.c_int), ("Lq", ctypes.c_int), ("Lk", ctypes.c_int), ("H", ctypes.c_int), ("D", ctypes.c_int),
+        ("group", ctypes.c_int),
+        ("q", _vp), ("ldq", _i64), ("q_off", _i64), ("q_bstride", _i64),
+        ("k", _vp), ("ldk", _i64), ("k_off", _i64), ("k_bstride", _i64),
+        ("v", _vp), ("ldv", _i64), ("v_off", _i64), ("v_bstride", _i64),
+        ("o", _vp), ("ldo", _i64), ("o_off", _i64), ("o_bstride", _i64),
+        ("scale", ctypes.c_float),
+        ("kv_len", ctypes.POINTER(ctypes.c_int)),
+        ("precision", ctypes.c_int),
+        ("q_norm", _vp), ("k_norm", _vp), ("rope_cs", _vp), ("rope_sin_off", _i64),
+        ("eps", ctypes.c_float),
+        ("causal", ctypes.c_int),
+    ]
+
+
+def lib():
+    """Loads libanima.so (raises if it is not built)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.POINTER
+        L.anima_init.argtypes = [ctypes.c_int, P(_vp)]
+        L.anima_destroy.argtypes = [_vp]
+        L.anima_last_error.argtypes = [_vp]
+        L.anima_last_error.restype = ctypes.c_char_p
+        for n in ("anima_sync", "anima_flush", "anima_pool_trim", "anima_profile_reset", "anima_timer_start"):
+            getattr(L, n).argtypes = [_vp]
+        L.anima_mem_stats.argtypes = [_vp, P(ctypes.c_uint64), P(ctypes.c_uint64), P(ctypes.c_uint64)]
+        L.anima_alloc.argtypes = [_vp, ctypes.c_size_t, P(_vp)]
+        L.anima_free.argtypes = [_vp, _vp]
+        for n in ("anima_h2d", "anima_d2h", "anima_d2d"):
+            getattr(L, n).argtypes = [_vp, _vp, _vp, ctypes.c_size_t]
+        L.anima_profile_enable.argtypes = [_vp, ctypes.c_int]
+        L.anima_profile_report.argtypes = [_vp, ctypes.c_char_p, ctypes.c_size_t]
+        L.anima_timer_stop.argtypes = [_vp, P(ctypes.c_float)]
+        L.anima_attention.argtypes = [_vp, P(AttnDesc)]
+        L.anima_qk_norm_rope.argtypes = [_vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _i64, _vp, _vp, _vp, _i64, ctypes.c_float]
+        L.anima_rmsnorm.argtypes = [_vp, _vp, _vp, _vp, _i64, ctypes.c_int, ctypes.c_float]
+        L.anima_rope.argtypes = [_vp, _vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _i64, _i64, _i64]
+        _LIB = L
+    return _LIB
+
+
+def declared_symbols():
+    """Entry points declared in include/anima.h."""
+    import re
+
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w[\w\s\*]*?\b(anima_\w+)\s*\(", text, re.M)))
+
+
+class DeviceBuffer:
+    """A pooled device allocation (Tensor of app/gpu/device.js:10-24, untyped)."""
+
+    def __init__(self, ctx, nbytes, shape=None, dtype=None):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        self.shape = shape
+        self.dtype = np.dtype(dtype) if dtype is not None else None
+        p = _vp()
+        ctx._check(lib().anima_alloc(ctx.h, max(1, self.nbytes), ctypes.byref(p)))
+        self.ptr = p.value
+
+    def release(self):
+        if self.ptr is not None:
+            self.ctx._check(lib().anima_free(self.ctx.h, self.ptr))
+            self.ptr = None
+
+    def numpy(self):
+        out = np.empty(self.shape, self.dtype)
+        self.ctx._check(lib().anima_d2h(self.ctx.h, out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def write(self, arr):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        self.ctx._check(lib().anima_h2d(self.ctx.h, self.ptr, arr.ctypes.data, arr.nbytes))
+
+
+class Context:
+    """One HIP device + stream (GPU of app/gpu/device.js:59-232)."""
+
+    def __init__(self, device=0):
+        h = _vp()
+        rc = lib().anima_init(device, ctypes.byref(h))
+        if rc != ANIMA_OK:
+            raise AnimaError(rc, lib().anima_last_error(None).decode())
+        self.h = h.value
+
+    def close(self):
+        if self.h:
+            lib().anima_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _check(self, rc):
+        if rc != ANIMA_OK:
+            raise AnimaError(rc, lib().anima_last_error(self.h).decode())
+        return rc
+
+    def last_error(self):
+        return lib().anima_last_error(self.h).decode()
+
+    # ---- memory
+    def empty(self, shape, dtype=np.float32):
+        shape = tuple(int(s) for s in np.atleast_1d(shape))
+        return DeviceBuffer(self, int(np.prod(shape)) * np.dtype(dtype).itemsize, shape, dtype)
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        b = DeviceBuffer(self, arr.nbytes, arr.shape, arr.dtype)
+        b.write(arr)
+        return b
+
+    def sync(self):
+        self._check(lib().anima_sync(self.h))
+
+    def mem_stats(self):
+        a, p, q = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+        self._check(lib().anima_mem_stats(self.h, ctypes.byref(a), ctypes.byref(p), ctypes.byref(q)))
+        return {"allocated": a.value, "peak": p.value, "pooled": q.value}
+
+    def trim(self):
+        self._check(lib().anima_pool_trim(self.h))
+
+    # ---- profiling / timing
+    def profile(self, on=True):
+        self._check(lib().anima_profile_enable(self.h, int(on)))
+
+    def profile_reset(self):
+        self._check(lib().anima_profile_reset(self.h))
+
+    def profile_report(self):
+        buf = ctypes.create_string_buffer(1 << 16)
+        self._check(lib().anima_profile_report(self.h, buf, len(buf)))
+        return json.loads(buf.value.decode())
+
+    def timer_start(self):
+        self._check(lib().anima_timer_start(self.h))
+
+    def timer_stop(self):
+        ms = ctypes.c_float()
+        self._check(lib().anima_timer_stop(self.h, ctypes.byref(ms)))
+        return ms.value
+
+    # ---- ops
+    def attention(self, *, q, k, v, o, B, Lq, Lk, H, D, ldq, ldk, ldv, ldo=None, q_off=0, k_off=0, v_off=0,
+                  o_off=0, q_bstride=None, k_bstride=None, v_bstride=None, o_bstride=None, group=1, scale=0.0,
+                  kv_len=None, precision=PREC_BF16, q_norm=None, k_norm=None, rope_cs=None, rope_sin_off=0,
+                  eps=1e-6, causal=0):
+        ldo = ldo if ldo is not None else H * D
+        kl = (ctypes.c_int * B)(*[int(x) for x in kv_len]) if kv_len is not None else None
+        d = AttnDesc(B=B, Lq=Lq, Lk=Lk, H=H, D=D, group=group,
+                     q=_ptr(q), ldq=ldq, q_off=q_off, q_bstride=q_bstride if q_bstride is not None else Lq * ldq,
+                     k=_ptr(k), ldk=ldk, k_off=k_off, k_bstride=k_bstride if k_bstride is not None else Lk * ldk,
+                     v=_ptr(v), ldv=ldv, v_off=v_off, v_bstride=v_bstride if v_bstride is not None else Lk * ldv,
+                     o=_ptr(o), ldo=ldo, o_off=o_off, o_bstride=o_bstride if o_bstride is not None else Lq * ldo,
+                     scale=scale, kv_len=ctypes.cast(kl, ctypes.POINTER(ctypes.c_int)) if kl is not None else None,
+                     precision=precision, q_norm=_ptr(q_norm), k_norm=_ptr(k_norm), rope_cs=_ptr(rope_cs),
+                     rope_sin_off=rope_sin_off, eps=eps, causal=causal)
+        return self._check(lib().anima_attention(self.h, ctypes.byref(d)))
+
+    def qk_norm_rope(self, qkv, L, H, D, ld, qn, kn, cs, sin_off, eps=1e-6):
+        return self._check(lib().anima_qk_norm_rope(self.h, _ptr(qkv), L, H, D, ld, _ptr(qn), _ptr(kn), _ptr(cs), sin_off, eps))
+
+    def rmsnorm(self, x, w, y, rows, cols, eps=1e-6):
+        return self._check(lib().anima_rmsnorm(self.h, _ptr(x), _ptr(w), _ptr(y), rows, cols, eps))
+
+    def rope(self, x, cs, L, H, D, sin_off, row_stride=None, col_off=0):
+        return self._check(lib().anima_rope(self.h, _ptr(x), _ptr(cs), L, H, D, sin_off,
+                                            row_stride if row_stride is not None else H * D, col_off))
+
+
+def dit_rope_angles(Hp: int, Wp: int) -> np.ndarray:
+    """Angles [Hp*Wp][64] of the 3D Cosmos RoPE for one frame (app/models/common.js:238-260):
+    slots 0..21 temporal at t=0 (angle 0), 22..42 row * hf[j], 43..63 column * hf[j],
+    hf[j] = 1 / h_theta^(2j/42) with h_theta = 1e4 * 4^(42/40) (NTK-scaled)."""
+    dim_h = 42
+    h_theta = 10000.0 * 4.0 ** (dim_h / (dim_h - 2))
+    ex = (np.arange(21, dtype=np.float64) * 2 / dim_h).astype(np.float32).astype(np.float64)
+    hf = (1.0 / np.power(h_theta, ex)).astype(np.float32).astype(np.float64)
+    a = np.zeros((Hp, Wp, 64), np.float32)
+    y = np.arange(Hp, dtype=np.float64)[:, None, None]
+    x = np.arange(Wp, dtype=np.float64)[None, :, None]
+    a[:, :, 22:43] = (y * hf).astype(np.float32)
+    a[:, :, 43:64] = (x * hf).astype(np.float32)
+    return a.reshape(Hp * Wp, 64)
+
+
+def rope_table(angles: np.ndarray) -> np.ndarray:
+    """cos block then sin block, flat [2*L*half]; sin offset L*half (app/models/common.js:211-220)."""
+    a = np.asarray(angles, np.float64)
+    return np.concatenate([np.cos(a).reshape(-1), np.sin(a).reshape(-1)]).astype(np.float32)
+
+
+def dit_rope_table(Hp: int, Wp: int) -> np.ndarray:
+    return rope_table(dit_rope_angles(Hp, Wp))
+
+
+def _ptr(b):
+    if b is None:
+        return None
+    if isinstance(b, DeviceBuffer):
+        return b.ptr
+    return int(b)

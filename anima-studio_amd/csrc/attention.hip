@@ -1,0 +1,637 @@
+// Fused DiT attention for gfx950: ops.attention's flash path (app/gpu/kernels.js:158-299) with
+// the q/k RMSNorm + RoPE of qkNormRopeShader (kernels.js:304-334) folded in.
+//
+// Two kernels per call:
+//   attn_prep_kv  K rows: optional RMSNorm + RoPE, rounded to the MFMA operand type and laid
+//                 out [B][Hkv][Lkp][128]; V transposed to [B][Hkv][128][Lkp] so the P.V MFMA
+//                 reads 4 consecutive keys per 8-byte LDS load.  Rows Lk..Lkp are zero.
+//                 One pass over K and V (HBM-bound) instead of re-normalizing K in every
+//                 query tile (32x redundant VALU work at N=4096).
+//   attn_flash_*  One workgroup = 4 waves x 32 queries.  Q is loaded from the fp32 input with
+//                 RMSNorm + RoPE fused into the load and kept in registers; K/V tiles of 64
+//                 keys stream through double-buffered LDS.  Scores are computed transposed,
+//                 S^T = K Q^T, so every per-query quantity (running max, sum, rescale) is a
+//                 per-lane scalar: lane (q, half) of a 32x32 MFMA tile owns query q.
+//
+// MFMA layouts used (32x32 tiles, 64 lanes, lane = n + 32*g):
+//   A operand: lane (m + 32 g) supplies row m, k-group g;  B operand: lane (n + 32 g) supplies
+//   column n, k-group g (the same per-register k order as A);  accumulator register r of lane
+//   (n + 32 g) holds row 8*(r/4) + 4*g + (r%4), column n.
+// Softmax uses exp2 with the scale*log2(e) factor folded into one FMA and an integer running
+// offset m: p = exp2(fma(s, c, -m)).  Integer offsets make the bf16 rounding of p independent
+// of when the offset was raised (a power-of-two rescale), and the offset is raised only when
+// a block maximum exceeds it by more than 8 (p <= 256), so O is rescaled almost never.
+#include <cmath>
+
+#include "common.h"
+#include "internal.h"
+
+namespace anima {
+
+constexpr int HD = 128;        // head dim
+constexpr int BQ = 128;        // queries per workgroup (4 waves x 32)
+constexpr int BK = 64;         // keys per block
+constexpr int MAXB = 64;       // max batch handled by one launch (kv_len in kernel args)
+constexpr float RESCALE_SLACK = 8.0f;
+
+struct PrepArgs {
+  const float* k;
+  int64_t ldk, k_bs;
+  const float* v;
+  int64_t ldv, v_bs;
+  void* kb;  // [B][Hkv][Lkp][HD]
+  void* vt;  // [B][Hkv][HD][Lkp]
+  const float* kn;
+  const float* cs;
+  int64_t sin_off;
+  float eps;
+  int Hkv, Lk, Lkp;
+};
+
+template <typename T>
+__device__ __forceinline__ T cvt(float x);
+template <>
+__device__ __forceinline__ bf16 cvt<bf16>(float x) { return (bf16)x; }
+template <>
+__device__ __forceinline__ float cvt<float>(float x) { return x; }
+
+// grid (Lkp/64, Hkv, B), 256 threads.
+template <typename T, bool NORM, bool ROPE>
+__global__ __launch_bounds__(256) void attn_prep_kv(PrepArgs a) {
+  constexpr int VSP = BK + 4;  // padded LDS row (keys) of the V transpose
+  __shared__ T vs[HD * VSP];
+  const int t = threadIdx.x;
+  const int kb0 = blockIdx.x * BK, hk = blockIdx.y, b = blockIdx.z;
+  const int64_t head_row0 = ((int64_t)b * a.Hkv + hk) * a.Lkp;
+
+  // ---- K: thread = (row t/4, quarter t%4); quarter p owns dims [16p,16p+16) and +64
+  {
+    const int r = t >> 2, p = t & 3, l = kb0 + r;
+    float x[32];
+    if (l < a.Lk) {
+      const float* src = a.k + (int64_t)b * a.k_bs + (int64_t)l * a.ldk + hk * HD;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        float4 lo = *(const float4*)(src + 16 * p + 4 * j);
+        float4 hi = *(const float4*)(src + 64 + 16 * p + 4 * j);
+        x[4 * j] = lo.x; x[4 * j + 1] = lo.y; x[4 * j + 2] = lo.z; x[4 * j + 3] = lo.w;
+        x[16 + 4 * j] = hi.x; x[16 + 4 * j + 1] = hi.y; x[16 + 4 * j + 2] = hi.z; x[16 + 4 * j + 3] = hi.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; i++) x[i] = 0.0f;
+    }
+    if (NORM) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 32; i++) ss += x[i] * x[i];
+      ss += __shfl_xor(ss, 1);
+      ss += __shfl_xor(ss, 2);
+      const float rn = 1.0f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        x[i] = x[i] * rn * a.kn[16 * p + i];
+        x[16 + i] = x[16 + i] * rn * a.kn[64 + 16 * p + i];
+      }
+    }
+    if (ROPE && l < a.Lk) {
+      const float* cr = a.cs + (int64_t)l * (HD / 2) + 16 * p;
+      const float* sr = a.cs + a.sin_off + (int64_t)l * (HD / 2) + 16 * p;
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const float c = cr[i], s = sr[i];
+        const float x1 = x[i], x2 = x[16 + i];
+        x[i] = x1 * c - x2 * s;
+        x[16 + i] = x2 * c + x1 * s;
+      }
+    }
+    T* dst = (T*)a.kb + (head_row0 + l) * HD;
+    if constexpr (sizeof(T) == 2) {
+      bf16x8 o[4];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        o[0][i] = to_bf16(x[i]);
+        o[1][i] = to_bf16(x[8 + i]);
+        o[2][i] = to_bf16(x[16 + i]);
+        o[3][i] = to_bf16(x[24 + i]);
+      }
+      *(bf16x8*)(dst + 16 * p) = o[0];
+      *(bf16x8*)(dst + 16 * p + 8) = o[1];
+      *(bf16x8*)(dst + 64 + 16 * p) = o[2];
+      *(bf16x8*)(dst + 64 + 16 * p + 8) = o[3];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        *(float4*)((float*)dst + 16 * p + 4 * j) = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
+        *(float4*)((float*)dst + 64 + 16 * p + 4 * j) =
+            make_float4(x[16 + 4 * j], x[16 + 4 * j + 1], x[16 + 4 * j + 2], x[16 + 4 * j + 3]);
+      }
+    }
+  }
+
+  // ---- V: thread = (dim group t%16 -> dims 8g..8g+7, token group t/16 -> 4 tokens)
+  {
+    const int g = t & 15, tg = t >> 4;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int l = kb0 + 4 * tg + j;
+      float4 lo = make_float4(0, 0, 0, 0), hi = lo;
+      if (l < a.Lk) {
+        const float* src = a.v + (int64_t)b * a.v_bs + (int64_t)l * a.ldv + hk * HD + 8 * g;
+        lo = *(const float4*)src;
+        hi = *(const float4*)(src + 4);
+      }
+      const float e[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+      for (int i = 0; i < 8; i++) vs[(8 * g + i) * VSP + 4 * tg + j] = cvt<T>(e[i]);
+    }
+    __syncthreads();
+    // write rows of V^T: thread = (dim t/2, half t%2 -> 32 keys)
+    const int d = t >> 1, h2 = t & 1;
+    T* dst = (T*)a.vt + (((int64_t)b * a.Hkv + hk) * HD + d) * a.Lkp + kb0 + 32 * h2;
+    const T* srow = vs + d * VSP + 32 * h2;
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        bf16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = ((const bf16*)srow)[8 * i + e];
+        *(bf16x8*)((bf16*)dst + 8 * i) = o;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const float* s4 = (const float*)srow + 4 * i;
+        *(float4*)((float*)dst + 4 * i) = make_float4(s4[0], s4[1], s4[2], s4[3]);
+      }
+    }
+  }
+}
+
+struct FlashArgs {
+  const float* q;
+  int64_t ldq, q_bs;
+  const void* kb;
+  const void* vt;
+  float* o;
+  int64_t ldo, o_bs;
+  const float* qn;
+  const float* cs;
+  int64_t sin_off;
+  float eps, c;  // c = scale * log2(e)
+  int H, group, Hkv, Lq, Lkp, n_qt;
+  int kv_len[MAXB];
+};
+
+// Workgroup id -> (batch*head, query tile).  Consecutive workgroup ids are dispatched
+// round-robin over the 8 XCDs; remapping gives each XCD a contiguous range of query tiles,
+// so the workgroups that share one head's K/V run on the same XCD (same L2).
+__device__ __forceinline__ int xcd_remap(int id, int total) {
+  if ((total & 7) != 0) return id;
+  return (id & 7) * (total >> 3) + (id >> 3);
+}
+
+// Loads this lane's 64 Q values (query qi, dims 16ks + 8hf + j), applies the fused
+// RMSNorm + RoPE, and returns them in x[ks*8 + j].
+template <bool NORM, bool ROPE>
+__device__ __forceinline__ void load_q(const FlashArgs& a, int b, int h, int qi, int hf, float* x) {
+  if (qi < a.Lq) {
+    const float* src = a.q + (int64_t)b * a.q_bs + (int64_t)qi * a.ldq + h * HD + 8 * hf;
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+      float4 lo = *(const float4*)(src + 16 * ks);
+      float4 hi = *(const float4*)(src + 16 * ks + 4);
+      x[8 * ks] = lo.x; x[8 * ks + 1] = lo.y; x[8 * ks + 2] = lo.z; x[8 * ks + 3] = lo.w;
+      x[8 * ks + 4] = hi.x; x[8 * ks + 5] = hi.y; x[8 * ks + 6] = hi.z; x[8 * ks + 7] = hi.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 64; i++) x[i] = 0.0f;
+  }
+  if (NORM) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 64; i++) ss += x[i] * x[i];
+    ss += __shfl_xor(ss, 32);
+    const float rn = 1.0f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) x[8 * ks + j] = x[8 * ks + j] * rn * a.qn[16 * ks + 8 * hf + j];
+  }
+  if (ROPE && qi < a.Lq) {
+    const float* cr = a.cs + (int64_t)qi * (HD / 2) + 8 * hf;
+    const float* sr = a.cs + a.sin_off + (int64_t)qi * (HD / 2) + 8 * hf;
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const float c = cr[16 * ks + j], s = sr[16 * ks + j];
+        const float x1 = x[8 * ks + j], x2 = x[8 * (ks + 4) + j];
+        x[8 * ks + j] = x1 * c - x2 * s;
+        x[8 * (ks + 4) + j] = x2 * c + x1 * s;
+      }
+  }
+}
+
+// ------------------------------------------------------------------ bf16 MFMA kernel
+
+constexpr int KSP = HD + 8;  // K tile row stride (bf16): 272 B, 16-byte aligned rows
+constexpr int VSP = BK + 4;  // V^T tile row stride (bf16): 136 B
+constexpr int KTILE = BK * KSP;
+constexpr int VTILE = HD * VSP;
+
+template <bool NORM, bool ROPE>
+__global__ __launch_bounds__(256, 2) void attn_flash_bf16(FlashArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * (KTILE + VTILE)];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 31, hf = lane >> 5;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = id / a.n_qt, qt = id - bh * a.n_qt;
+  const int b = bh / a.H, h = bh - b * a.H, hk = h / a.group;
+  const int qi = qt * BQ + wave * 32 + lq;
+  const int Lk = a.kv_len[b];
+  const int nkb = (Lk + BK - 1) / BK;
+
+  bf16x8 qf[8];
+  {
+    float x[64];
+    load_q<NORM, ROPE>(a, b, h, qi, hf, x);
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) qf[ks][j] = to_bf16(x[8 * ks + j]);
+  }
+
+  const bf16* kg = (const bf16*)a.kb + ((int64_t)b * a.Hkv + hk) * a.Lkp * HD;
+  const bf16* vg = (const bf16*)a.vt + ((int64_t)b * a.Hkv + hk) * HD * a.Lkp;
+  // global -> LDS copy assignment: K rows (t/4, 64 B chunk t%4); V^T rows (t/2, 64 B half t%2)
+  const int kr = tid >> 2, kc = tid & 3, vr = tid >> 1, vc = tid & 1;
+  uint4 kreg[4], vreg[4];
+  auto gload = [&](int blk) {
+    const uint4* ks = (const uint4*)(kg + ((int64_t)blk * BK + kr) * HD + 32 * kc);
+    const uint4* vsrc = (const uint4*)(vg + (int64_t)vr * a.Lkp + blk * BK + 32 * vc);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      kreg[i] = ks[i];
+      vreg[i] = vsrc[i];
+    }
+  };
+  auto lstore = [&](int stage) {
+    bf16* K = smem + stage * (KTILE + VTILE);
+    bf16* V = K + KTILE;
+    uint4* kd = (uint4*)(K + kr * KSP + 32 * kc);
+    uint2* vd = (uint2*)(V + vr * VSP + 32 * vc);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      kd[i] = kreg[i];
+      vd[2 * i] = make_uint2(vreg[i].x, vreg[i].y);
+      vd[2 * i + 1] = make_uint2(vreg[i].z, vreg[i].w);
+    }
+  };
+
+  f32x16 o[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) o[i] = (f32x16){};
+  float m = -INFINITY, l = 0.0f;
+
+  gload(0);
+  lstore(0);
+  __syncthreads();
+
+  for (int kb = 0; kb < nkb; kb++) {
+    const int stage = kb & 1;
+    const bf16* K = smem + stage * (KTILE + VTILE);
+    const bf16* V = K + KTILE;
+    if (kb + 1 < nkb) gload(kb + 1);
+
+    // S^T = K Q^T: two 32-key tiles
+    f32x16 s0 = {}, s1 = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+      const bf16x8 ka = *(const bf16x8*)(K + lq * KSP + 16 * ks + 8 * hf);
+      const bf16x8 kb2 = *(const bf16x8*)(K + (32 + lq) * KSP + 16 * ks + 8 * hf);
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[ks], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb2, qf[ks], s1, 0, 0, 0);
+    }
+    if ((kb + 1) * BK > Lk) {  // keys >= kv_len in the last block
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int key = kb * BK + 8 * (r >> 2) + 4 * hf + (r & 3);
+        if (key >= Lk) s0[r] = -INFINITY;
+        if (key + 32 >= Lk) s1[r] = -INFINITY;
+      }
+    }
+    float bm = fmaxf(s0[0], s1[0]);
+#pragma unroll
+    for (int r = 1; r < 16; r++) bm = fmaxf(bm, fmaxf(s0[r], s1[r]));
+    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    const float bmc = bm * a.c;
+    const bool need = bmc > m + RESCALE_SLACK;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+      const float mn = need ? ceilf(bmc) : m;
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; i++) o[i] *= alpha;
+    }
+    bf16x8 pb[4];
+    float ls0 = 0.0f, ls1 = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], a.c, -m));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], a.c, -m));
+      ls0 += p0;
+      ls1 += p1;
+      pb[r >> 3][r & 7] = to_bf16(p0);
+      pb[2 + (r >> 3)][r & 7] = to_bf16(p1);
+    }
+    l += ls0 + ls1;
+
+    // O^T += V^T P^T: k-step s covers keys 16s .. 16s+15
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+#pragma unroll
+      for (int dt = 0; dt < 4; dt++) {
+        const bf16* vrow = V + (32 * dt + lq) * VSP + 16 * s + 4 * hf;
+        const bf16x4 lo = *(const bf16x4*)vrow;
+        const bf16x4 hi = *(const bf16x4*)(vrow + 8);
+        const bf16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[s], o[dt], 0, 0, 0);
+      }
+    }
+    if (kb + 1 < nkb) lstore(stage ^ 1);
+    __syncthreads();
+  }
+
+  l += __shfl_xor(l, 32);
+  if (qi < a.Lq) {
+    const float inv = 1.0f / l;
+    float* dst = a.o + (int64_t)b * a.o_bs + (int64_t)qi * a.ldo + h * HD + 4 * hf;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+        *(float4*)(dst + 32 * dt + 8 * g) =
+            make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+  }
+}
+
+// ------------------------------------------------------------------ fp32 MFMA kernel
+
+constexpr int KSP32 = HD + 4;  // floats
+constexpr int VSP32 = BK + 4;
+
+template <bool NORM, bool ROPE>
+__global__ __launch_bounds__(256) void attn_flash_fp32(FlashArgs a) {
+  __shared__ __attribute__((aligned(16))) float Ks[BK * KSP32];
+  __shared__ __attribute__((aligned(16))) float Vs[HD * VSP32];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 31, hf = lane >> 5;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = id / a.n_qt, qt = id - bh * a.n_qt;
+  const int b = bh / a.H, h = bh - b * a.H, hk = h / a.group;
+  const int qi = qt * BQ + wave * 32 + lq;
+  const int Lk = a.kv_len[b];
+  const int nkb = (Lk + BK - 1) / BK;
+
+  // lane keeps Q[qi][2ks + hf] for ks = 0..63 (K-group g of a 32x32x2 MFMA = dim parity)
+  float qv[64];
+  {
+    float x[64];
+    load_q<NORM, ROPE>(a, b, h, qi, hf, x);
+    // x holds dims 16ks8 + 8hf + j; redistribute across the lane pair so that lane (q, g)
+    // holds the dims of parity g.  Lane hf has dims {16k + 8hf + j}; exchange with lane^32.
+#pragma unroll
+    for (int k8 = 0; k8 < 8; k8++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const float mine = x[8 * k8 + j];
+        const float other = __shfl_xor(mine, 32);
+        // dim of `mine` = 16k8 + 8hf + j, of `other` = 16k8 + 8(1-hf) + j
+        const float lo = hf ? other : mine;  // dim 16k8 + j
+        const float hi = hf ? mine : other;   // dim 16k8 + 8 + j
+        // keep dims with parity hf: d = 2ks + hf
+        if ((j & 1) == hf) {
+          qv[(16 * k8 + j) >> 1] = lo;
+          qv[(16 * k8 + 8 + j) >> 1] = hi;
+        }
+      }
+  }
+
+  const float* kg = (const float*)a.kb + ((int64_t)b * a.Hkv + hk) * a.Lkp * HD;
+  const float* vg = (const float*)a.vt + ((int64_t)b * a.Hkv + hk) * HD * a.Lkp;
+  f32x16 o[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) o[i] = (f32x16){};
+  float m = -INFINITY, l = 0.0f;
+
+  for (int kb = 0; kb < nkb; kb++) {
+    // K tile 64 x 128 floats: thread -> row t/4, 32 floats; V^T tile 128 x 64: row t/2, 32 floats
+    {
+      const float4* ks = (const float4*)(kg + ((int64_t)kb * BK + (tid >> 2)) * HD + 32 * (tid & 3));
+      float4* kd = (float4*)(Ks + (tid >> 2) * KSP32 + 32 * (tid & 3));
+      const float4* vsrc = (const float4*)(vg + (int64_t)(tid >> 1) * a.Lkp + kb * BK + 32 * (tid & 1));
+      float4* vd = (float4*)(Vs + (tid >> 1) * VSP32 + 32 * (tid & 1));
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        kd[i] = ks[i];
+        vd[i] = vsrc[i];
+      }
+    }
+    __syncthreads();
+    f32x16 s0 = {}, s1 = {};
+#pragma unroll 16
+    for (int ks = 0; ks < 64; ks++) {
+      const float k0 = Ks[lq * KSP32 + 2 * ks + hf];
+      const float k1 = Ks[(32 + lq) * KSP32 + 2 * ks + hf];
+      s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(k0, qv[ks], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(k1, qv[ks], s1, 0, 0, 0);
+    }
+    if ((kb + 1) * BK > Lk) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int key = kb * BK + 8 * (r >> 2) + 4 * hf + (r & 3);
+        if (key >= Lk) s0[r] = -INFINITY;
+        if (key + 32 >= Lk) s1[r] = -INFINITY;
+      }
+    }
+    float bm = fmaxf(s0[0], s1[0]);
+#pragma unroll
+    for (int r = 1; r < 16; r++) bm = fmaxf(bm, fmaxf(s0[r], s1[r]));
+    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    const float bmc = bm * a.c;
+    const bool need = bmc > m + RESCALE_SLACK;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+      const float mn = need ? ceilf(bmc) : m;
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; i++) o[i] *= alpha;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      s0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], a.c, -m));
+      s1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], a.c, -m));
+      l += s0[r] + s1[r];
+    }
+    // k-step (tile t, register r): keys 32t + 8(r/4) + 4g + r%4 for k-group g
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int key = 8 * (r >> 2) + 4 * hf + (r & 3);
+#pragma unroll
+      for (int dt = 0; dt < 4; dt++) {
+        const float* vrow = Vs + (32 * dt + lq) * VSP32;
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[key], s0[r], o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 + key], s1[r], o[dt], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+
+  l += __shfl_xor(l, 32);
+  if (qi < a.Lq) {
+    const float inv = 1.0f / l;
+    float* dst = a.o + (int64_t)b * a.o_bs + (int64_t)qi * a.ldo + h * HD + 4 * hf;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+        *(float4*)(dst + 32 * dt + 8 * g) =
+            make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+  }
+}
+
+// ------------------------------------------------------------------ host launcher
+
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
+  const int group = d->group <= 0 ? 1 : d->group;
+  if (d->causal) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: causal attention is not on the DiT path (only the chunked text-encoder path of ops.js:177-207 uses it)");
+  if (d->D != HD) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: head dim %d (this build implements D=128, the DiT head size)", d->D);
+  if (d->B < 1 || d->B > MAXB) return fail(c, ANIMA_E_ARG, "anima_attention: B=%d outside [1,%d]", d->B, MAXB);
+  if (d->Lq < 1 || d->Lk < 1 || d->H < 1) return fail(c, ANIMA_E_ARG, "anima_attention: Lq=%d Lk=%d H=%d must be >= 1", d->Lq, d->Lk, d->H);
+  if (d->H % group) return fail(c, ANIMA_E_ARG, "anima_attention: H=%d not a multiple of group=%d", d->H, group);
+  if (!d->q || !d->k || !d->v || !d->o) return fail(c, ANIMA_E_ARG, "anima_attention: null q/k/v/o");
+  if (d->precision != ANIMA_PREC_BF16 && d->precision != ANIMA_PREC_FP32)
+    return fail(c, ANIMA_E_ARG, "anima_attention: unknown precision %d", d->precision);
+  const int64_t lds[4] = {d->ldq, d->ldk, d->ldv, d->ldo};
+  const int64_t offs[4] = {d->q_off, d->k_off, d->v_off, d->o_off};
+  const int64_t bss[4] = {d->q_bstride, d->k_bstride, d->v_bstride, d->o_bstride};
+  const char* nm[4] = {"q", "k", "v", "o"};
+  const int heads[4] = {d->H, d->H / group, d->H / group, d->H};
+  for (int i = 0; i < 4; i++) {
+    if (lds[i] % 4 || offs[i] % 4 || bss[i] % 4 || lds[i] < 0 || offs[i] < 0 || bss[i] < 0)
+      return fail(c, ANIMA_E_ARG, "anima_attention: %s ld/off/bstride (%lld/%lld/%lld) must be non-negative multiples of 4 (vec4 rows, as ops.js:169)",
+                  nm[i], (long long)lds[i], (long long)offs[i], (long long)bss[i]);
+    if (lds[i] < offs[i] + (int64_t)heads[i] * HD)
+      return fail(c, ANIMA_E_ARG, "anima_attention: %s rows of %lld elements cannot hold off %lld + %d heads x %d", nm[i],
+                  (long long)lds[i], (long long)offs[i], heads[i], HD);
+  }
+  if (!al16(d->q) || !al16(d->k) || !al16(d->v) || !al16(d->o)) return fail(c, ANIMA_E_ARG, "anima_attention: q/k/v/o must be 16-byte aligned");
+  int kv_len[MAXB];
+  for (int b = 0; b < d->B; b++) {
+    kv_len[b] = d->kv_len ? d->kv_len[b] : d->Lk;
+    if (kv_len[b] < 1 || kv_len[b] > d->Lk) return fail(c, ANIMA_E_ARG, "anima_attention: kv_len[%d]=%d outside [1, Lk=%d]", b, kv_len[b], d->Lk);
+  }
+  const bool rope = d->rope_cs != nullptr;
+  if (rope) {
+    const int64_t rows = d->rope_sin_off / (HD / 2);
+    if (d->rope_sin_off <= 0 || d->rope_sin_off % (HD / 2) || rows < d->Lq || rows < d->Lk)
+      return fail(c, ANIMA_E_ARG, "anima_attention: rope_sin_off=%lld must be rows*%d with rows >= max(Lq,Lk)=%d",
+                  (long long)d->rope_sin_off, HD / 2, d->Lq > d->Lk ? d->Lq : d->Lk);
+  }
+  const float scale = d->scale != 0.0f ? d->scale : 1.0f / sqrtf((float)HD);
+  const float eps = d->eps;
+  const int Hkv = d->H / group;
+  const int Lkp = (d->Lk + BK - 1) / BK * BK;
+  const bool bf = d->precision == ANIMA_PREC_BF16;
+  const size_t esz = bf ? 2 : 4;
+  const size_t plane = (size_t)d->B * Hkv * Lkp * HD * esz;
+  void* ws = nullptr;
+  int rc = workspace(c, 2 * plane, &ws);
+  if (rc) return rc;
+
+  PrepArgs p;
+  p.k = d->k + d->k_off;
+  p.ldk = d->ldk;
+  p.k_bs = d->k_bstride;
+  p.v = d->v + d->v_off;
+  p.ldv = d->ldv;
+  p.v_bs = d->v_bstride;
+  p.kb = ws;
+  p.vt = (char*)ws + plane;
+  p.kn = d->k_norm;
+  p.cs = d->rope_cs;
+  p.sin_off = d->rope_sin_off;
+  p.eps = eps;
+  p.Hkv = Hkv;
+  p.Lk = d->Lk;
+  p.Lkp = Lkp;
+  {
+    const double bytes = (double)d->B * Hkv * d->Lk * HD * 4 * 2 + 2.0 * plane;
+    Launch L(c, bf ? "attn.prep_kv_bf16" : "attn.prep_kv_fp32", 0.0, bytes);
+    dim3 grid(Lkp / BK, Hkv, d->B);
+    const bool kn = d->k_norm != nullptr;
+#define PREP(T, N, R) hipLaunchKernelGGL((attn_prep_kv<T, N, R>), grid, dim3(256), 0, c->stream, p)
+    if (bf) {
+      if (kn && rope) PREP(bf16, true, true);
+      else if (kn) PREP(bf16, true, false);
+      else if (rope) PREP(bf16, false, true);
+      else PREP(bf16, false, false);
+    } else {
+      if (kn && rope) PREP(float, true, true);
+      else if (kn) PREP(float, true, false);
+      else if (rope) PREP(float, false, true);
+      else PREP(float, false, false);
+    }
+#undef PREP
+    if ((rc = L.end())) return rc;
+  }
+
+  FlashArgs f;
+  f.q = d->q + d->q_off;
+  f.ldq = d->ldq;
+  f.q_bs = d->q_bstride;
+  f.kb = p.kb;
+  f.vt = p.vt;
+  f.o = d->o + d->o_off;
+  f.ldo = d->ldo;
+  f.o_bs = d->o_bstride;
+  f.qn = d->q_norm;
+  f.cs = d->rope_cs;
+  f.sin_off = d->rope_sin_off;
+  f.eps = eps;
+  f.c = scale * 1.4426950408889634f;
+  f.H = d->H;
+  f.group = group;
+  f.Hkv = Hkv;
+  f.Lq = d->Lq;
+  f.Lkp = Lkp;
+  f.n_qt = (d->Lq + BQ - 1) / BQ;
+  for (int b = 0; b < MAXB; b++) f.kv_len[b] = b < d->B ? kv_len[b] : 1;
+  double flops = 0;
+  for (int b = 0; b < d->B; b++) flops += 4.0 * d->Lq * (double)kv_len[b] * HD * d->H;
+  const int blocks = f.n_qt * d->H * d->B;
+  Launch L(c, bf ? "attn.flash_bf16" : "attn.flash_fp32", flops, 0.0);
+  const bool qn = d->q_norm != nullptr;
+#define FLASH(K, N, R) hipLaunchKernelGGL((K<N, R>), dim3(blocks), dim3(256), 0, c->stream, f)
+  if (bf) {
+    if (qn && rope) FLASH(attn_flash_bf16, true, true);
+    else if (qn) FLASH(attn_flash_bf16, true, false);
+    else if (rope) FLASH(attn_flash_bf16, false, true);
+    else FLASH(attn_flash_bf16, false, false);
+  } else {
+    if (qn && rope) FLASH(attn_flash_fp32, true, true);
+    else if (qn) FLASH(attn_flash_fp32, true, false);
+    else if (rope) FLASH(attn_flash_fp32, false, true);
+    else FLASH(attn_flash_fp32, false, false);
+  }
+#undef FLASH
+  return L.end();
+}
+
+}  // namespace anima

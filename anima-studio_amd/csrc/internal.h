@@ -1,0 +1,79 @@
+// Internal declarations shared by the runtime and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/anima.h"
+
+namespace anima {
+
+// Per-launch timing record (profiling mode).
+struct ProfRec {
+  const char* name;
+  double flops, bytes;
+  hipEvent_t a, b;
+};
+
+struct Stat {
+  int64_t count = 0;
+  double ms = 0, flops = 0, bytes = 0;
+};
+
+}  // namespace anima
+
+struct anima_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string err;
+  bool lost = false;
+  // pool: bucket size -> parked device buffers; live pointer -> bucket size
+  std::unordered_map<size_t, std::vector<void*>> free_lists;
+  std::unordered_map<void*, size_t> live;
+  uint64_t allocated = 0, peak = 0, pooled = 0;
+  // profiler
+  bool profiling = false;
+  std::vector<anima::ProfRec> recs;
+  std::vector<hipEvent_t> spare_events;
+  std::unordered_map<std::string, anima::Stat> stats;
+  // timer
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  // attention workspace (K in bf16/fp32, V transposed), grown on demand
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+};
+
+namespace anima {
+
+int fail(anima_ctx* c, int code, const char* fmt, ...);
+int hip_fail(anima_ctx* c, hipError_t e, const char* what);
+// Workspace of at least `bytes` (grows by synchronizing and reallocating).
+int workspace(anima_ctx* c, size_t bytes, void** out);
+
+// Launch bracket for the profiler: begin() before a kernel launch, end() after it.
+struct Launch {
+  anima_ctx* c;
+  ProfRec rec;
+  bool on;
+  Launch(anima_ctx* ctx, const char* name, double flops, double bytes);
+  // Checks the launch status; returns ANIMA_OK or a negative status.
+  int end();
+};
+
+// ---- kernel launchers (attention.hip)
+int attention_launch(anima_ctx* c, const anima_attn_desc* d);
+
+// ---- kernel launchers (rowops.hip)
+int qk_norm_rope_launch(anima_ctx* c, float* qkv, int64_t L, int H, int D, int64_t ld,
+                        const float* qn, const float* kn, const float* cs, int64_t sin_off,
+                        float eps);
+int rmsnorm_launch(anima_ctx* c, const float* x, const float* w, float* y, int64_t rows,
+                   int cols, float eps);
+int rope_launch(anima_ctx* c, float* x, const float* cs, int64_t L, int H, int D,
+                int64_t sin_off, int64_t row_stride, int64_t col_off);
+
+}  // namespace anima

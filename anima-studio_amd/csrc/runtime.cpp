@@ -1,0 +1,366 @@
+// Runtime of the C ABI: context, stream-ordered pooled allocator, copies, profiler, errors.
+// Replaces the WebGPU runtime of app/gpu/device.js (GPU, BufferPool, Profiler).
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "internal.h"
+
+namespace {
+thread_local std::string g_init_error;  // errors of anima_init (no context yet)
+
+// 1/8-power-of-two size buckets, minimum 256 B (the bucketing of app/gpu/device.js:33-39).
+size_t bucket(size_t bytes) {
+  size_t b = std::max<size_t>(256, bytes);
+  size_t p = size_t(1) << (63 - __builtin_clzll(b));
+  size_t step = std::max<size_t>(256, p / 8);
+  return (b + step - 1) / step * step;
+}
+}  // namespace
+
+namespace anima {
+
+int fail(anima_ctx* c, int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (c) c->err = buf;
+  else g_init_error = buf;
+  return code;
+}
+
+int hip_fail(anima_ctx* c, hipError_t e, const char* what) {
+  if (c && (e == hipErrorIllegalAddress || e == hipErrorLaunchFailure || e == hipErrorAssert))
+    c->lost = true;  // the device context is unusable after a fault (device lost)
+  return fail(c, e == hipErrorOutOfMemory ? ANIMA_E_OOM : ANIMA_E_HIP, "%s: %s (%d)", what,
+              hipGetErrorString(e), (int)e);
+}
+
+int workspace(anima_ctx* c, size_t bytes, void** out) {
+  if (bytes > c->ws_bytes) {
+    if (c->ws) {
+      hipError_t e = hipStreamSynchronize(c->stream);
+      if (e != hipSuccess) return hip_fail(c, e, "workspace sync");
+      hipFree(c->ws);
+      c->allocated -= c->ws_bytes;
+      c->ws = nullptr;
+      c->ws_bytes = 0;
+    }
+    size_t want = bucket(bytes);
+    hipError_t e = hipMalloc(&c->ws, want);
+    if (e != hipSuccess) {
+      c->ws = nullptr;
+      return hip_fail(c, e, "workspace hipMalloc");
+    }
+    c->ws_bytes = want;
+    c->allocated += want;
+    c->peak = std::max(c->peak, c->allocated);
+  }
+  *out = c->ws;
+  return ANIMA_OK;
+}
+
+static hipEvent_t take_event(anima_ctx* c) {
+  if (!c->spare_events.empty()) {
+    hipEvent_t e = c->spare_events.back();
+    c->spare_events.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+Launch::Launch(anima_ctx* ctx, const char* name, double flops, double bytes)
+    : c(ctx), rec{name, flops, bytes, nullptr, nullptr}, on(ctx->profiling) {
+  if (on) {
+    rec.a = take_event(c);
+    rec.b = take_event(c);
+    if (!rec.a || !rec.b) on = false;
+    else hipEventRecord(rec.a, c->stream);
+  }
+}
+
+int Launch::end() {
+  hipError_t e = hipGetLastError();
+  if (on) {
+    hipEventRecord(rec.b, c->stream);
+    c->recs.push_back(rec);
+  }
+  if (e != hipSuccess) return hip_fail(c, e, rec.name);
+  return ANIMA_OK;
+}
+
+// Resolves pending profiler records into per-name statistics (needs a synchronized stream).
+static void collect(anima_ctx* c) {
+  for (auto& r : c->recs) {
+    float ms = 0;
+    hipEventElapsedTime(&ms, r.a, r.b);
+    Stat& s = c->stats[r.name];
+    s.count++;
+    s.ms += ms;
+    s.flops += r.flops;
+    s.bytes += r.bytes;
+    c->spare_events.push_back(r.a);
+    c->spare_events.push_back(r.b);
+  }
+  c->recs.clear();
+}
+
+}  // namespace anima
+
+using namespace anima;
+
+#define CHECK_CTX(c)                                                                      \
+  do {                                                                                    \
+    if (!(c)) return fail(nullptr, ANIMA_E_ARG, "null context");                          \
+    if ((c)->lost) return fail((c), ANIMA_E_STATE, "context lost after a device error: %s", \
+                               (c)->err.c_str());                                         \
+  } while (0)
+
+extern "C" {
+
+int anima_init(int device, anima_ctx** out) {
+  if (!out) return fail(nullptr, ANIMA_E_ARG, "anima_init: out is NULL");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0) return fail(nullptr, ANIMA_E_HIP, "anima_init: no HIP device (%s)", hipGetErrorString(e));
+  if (device < 0 || device >= n) return fail(nullptr, ANIMA_E_ARG, "anima_init: device %d out of range [0,%d)", device, n);
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return fail(nullptr, ANIMA_E_HIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(nullptr, ANIMA_E_UNSUPPORTED, "anima_init: device %d is %s; this library is built for gfx950 (MI355X) only", device, prop.gcnArchName);
+  e = hipSetDevice(device);
+  if (e != hipSuccess) return fail(nullptr, ANIMA_E_HIP, "hipSetDevice: %s", hipGetErrorString(e));
+  anima_ctx* c = new anima_ctx();
+  c->device = device;
+  e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreate(&c->t0);
+  if (e == hipSuccess) e = hipEventCreate(&c->t1);
+  if (e != hipSuccess) {
+    fail(nullptr, ANIMA_E_HIP, "anima_init: %s", hipGetErrorString(e));
+    delete c;
+    return ANIMA_E_HIP;
+  }
+  *out = c;
+  return ANIMA_OK;
+}
+
+int anima_destroy(anima_ctx* c) {
+  if (!c) return ANIMA_OK;
+  hipSetDevice(c->device);
+  hipStreamSynchronize(c->stream);
+  for (auto& kv : c->free_lists)
+    for (void* p : kv.second) hipFree(p);
+  for (auto& kv : c->live) hipFree(kv.first);
+  if (c->ws) hipFree(c->ws);
+  for (auto& r : c->recs) {
+    hipEventDestroy(r.a);
+    hipEventDestroy(r.b);
+  }
+  for (hipEvent_t e : c->spare_events) hipEventDestroy(e);
+  if (c->t0) hipEventDestroy(c->t0);
+  if (c->t1) hipEventDestroy(c->t1);
+  hipStreamDestroy(c->stream);
+  delete c;
+  return ANIMA_OK;
+}
+
+const char* anima_last_error(const anima_ctx* c) { return c ? c->err.c_str() : g_init_error.c_str(); }
+
+int anima_sync(anima_ctx* c) {
+  CHECK_CTX(c);
+  hipError_t e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "anima_sync");
+  e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(c, e, "anima_sync (deferred)");
+  return ANIMA_OK;
+}
+
+int anima_flush(anima_ctx* c) {
+  CHECK_CTX(c);
+  return ANIMA_OK;
+}
+
+int anima_mem_stats(anima_ctx* c, uint64_t* allocated, uint64_t* peak, uint64_t* pooled) {
+  if (!c) return fail(nullptr, ANIMA_E_ARG, "null context");
+  if (allocated) *allocated = c->allocated;
+  if (peak) *peak = c->peak;
+  if (pooled) *pooled = c->pooled;
+  return ANIMA_OK;
+}
+
+int anima_alloc(anima_ctx* c, size_t bytes, void** out) {
+  CHECK_CTX(c);
+  if (!out) return fail(c, ANIMA_E_ARG, "anima_alloc: out is NULL");
+  size_t size = bucket(bytes);
+  auto it = c->free_lists.find(size);
+  if (it != c->free_lists.end() && !it->second.empty()) {
+    *out = it->second.back();
+    it->second.pop_back();
+    c->pooled -= size;
+    c->live[*out] = size;
+    return ANIMA_OK;
+  }
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, size);
+  if (e != hipSuccess) {
+    // release parked buffers and retry once (the pool's trim)
+    hipStreamSynchronize(c->stream);
+    for (auto& kv : c->free_lists)
+      for (void* q : kv.second) {
+        hipFree(q);
+        c->allocated -= kv.first;
+      }
+    c->free_lists.clear();
+    c->pooled = 0;
+    hipGetLastError();
+    e = hipMalloc(&p, size);
+    if (e != hipSuccess) return hip_fail(c, e, "anima_alloc");
+  }
+  c->allocated += size;
+  c->peak = std::max(c->peak, c->allocated);
+  c->live[p] = size;
+  *out = p;
+  return ANIMA_OK;
+}
+
+int anima_free(anima_ctx* c, void* p) {
+  if (!c) return fail(nullptr, ANIMA_E_ARG, "null context");
+  if (!p) return ANIMA_OK;
+  auto it = c->live.find(p);
+  if (it == c->live.end()) return fail(c, ANIMA_E_ARG, "anima_free: %p was not allocated by this context (or freed twice)", p);
+  c->free_lists[it->second].push_back(p);
+  c->pooled += it->second;
+  c->live.erase(it);
+  return ANIMA_OK;
+}
+
+int anima_pool_trim(anima_ctx* c) {
+  CHECK_CTX(c);
+  hipError_t e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "anima_pool_trim");
+  for (auto& kv : c->free_lists)
+    for (void* q : kv.second) {
+      hipFree(q);
+      c->allocated -= kv.first;
+    }
+  c->free_lists.clear();
+  c->pooled = 0;
+  return ANIMA_OK;
+}
+
+int anima_h2d(anima_ctx* c, void* dst, const void* src, size_t bytes) {
+  CHECK_CTX(c);
+  if (bytes == 0) return ANIMA_OK;
+  if (!dst || !src) return fail(c, ANIMA_E_ARG, "anima_h2d: null pointer");
+  // pageable source: hipMemcpyAsync stages it before returning, so `src` may be reused
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "anima_h2d");
+  return ANIMA_OK;
+}
+
+int anima_d2h(anima_ctx* c, void* dst, const void* src, size_t bytes) {
+  CHECK_CTX(c);
+  if (bytes == 0) return ANIMA_OK;
+  if (!dst || !src) return fail(c, ANIMA_E_ARG, "anima_d2h: null pointer");
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "anima_d2h");
+  return ANIMA_OK;
+}
+
+int anima_d2d(anima_ctx* c, void* dst, const void* src, size_t bytes) {
+  CHECK_CTX(c);
+  if (bytes == 0) return ANIMA_OK;
+  if (!dst || !src) return fail(c, ANIMA_E_ARG, "anima_d2d: null pointer");
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "anima_d2d");
+  return ANIMA_OK;
+}
+
+int anima_profile_enable(anima_ctx* c, int on) {
+  CHECK_CTX(c);
+  c->profiling = on != 0;
+  return ANIMA_OK;
+}
+
+int anima_profile_reset(anima_ctx* c) {
+  CHECK_CTX(c);
+  hipError_t e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "anima_profile_reset");
+  collect(c);
+  c->stats.clear();
+  return ANIMA_OK;
+}
+
+int anima_profile_report(anima_ctx* c, char* buf, size_t len) {
+  CHECK_CTX(c);
+  if (!buf || len == 0) return fail(c, ANIMA_E_ARG, "anima_profile_report: empty buffer");
+  hipError_t e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "anima_profile_report");
+  collect(c);
+  std::vector<std::pair<std::string, Stat>> rows(c->stats.begin(), c->stats.end());
+  std::sort(rows.begin(), rows.end(), [](auto& a, auto& b) { return a.second.ms > b.second.ms; });
+  std::string s = "[";
+  char tmp[512];
+  for (size_t i = 0; i < rows.size(); i++) {
+    snprintf(tmp, sizeof tmp, "%s{\"name\":\"%s\",\"count\":%lld,\"ms\":%.6f,\"flops\":%.6e,\"bytes\":%.6e}",
+             i ? "," : "", rows[i].first.c_str(), (long long)rows[i].second.count, rows[i].second.ms,
+             rows[i].second.flops, rows[i].second.bytes);
+    s += tmp;
+  }
+  s += "]";
+  if (s.size() + 1 > len) return fail(c, ANIMA_E_ARG, "anima_profile_report: buffer of %zu bytes, need %zu", len, s.size() + 1);
+  std::memcpy(buf, s.c_str(), s.size() + 1);
+  return ANIMA_OK;
+}
+
+int anima_timer_start(anima_ctx* c) {
+  CHECK_CTX(c);
+  hipError_t e = hipEventRecord(c->t0, c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "anima_timer_start");
+  return ANIMA_OK;
+}
+
+int anima_timer_stop(anima_ctx* c, float* ms) {
+  CHECK_CTX(c);
+  if (!ms) return fail(c, ANIMA_E_ARG, "anima_timer_stop: ms is NULL");
+  hipError_t e = hipEventRecord(c->t1, c->stream);
+  if (e == hipSuccess) e = hipEventSynchronize(c->t1);
+  if (e == hipSuccess) e = hipEventElapsedTime(ms, c->t0, c->t1);
+  if (e != hipSuccess) return hip_fail(c, e, "anima_timer_stop");
+  return ANIMA_OK;
+}
+
+int anima_attention(anima_ctx* c, const anima_attn_desc* d) {
+  CHECK_CTX(c);
+  if (!d) return fail(c, ANIMA_E_ARG, "anima_attention: null descriptor");
+  return attention_launch(c, d);
+}
+
+int anima_qk_norm_rope(anima_ctx* c, float* qkv, int64_t L, int H, int D, int64_t ld,
+                       const float* qn, const float* kn, const float* cs, int64_t sin_off, float eps) {
+  CHECK_CTX(c);
+  return qk_norm_rope_launch(c, qkv, L, H, D, ld, qn, kn, cs, sin_off, eps);
+}
+
+int anima_rmsnorm(anima_ctx* c, const float* x, const float* w, float* y, int64_t rows, int cols, float eps) {
+  CHECK_CTX(c);
+  return rmsnorm_launch(c, x, w, y, rows, cols, eps);
+}
+
+int anima_rope(anima_ctx* c, float* x, const float* cs, int64_t L, int H, int D, int64_t sin_off,
+               int64_t row_stride, int64_t col_off) {
+  CHECK_CTX(c);
+  return rope_launch(c, x, cs, L, H, D, sin_off, row_stride, col_off);
+}
+
+}  // extern "C"

@@ -1,0 +1,143 @@
+"""Benchmark of the DiT attention hot path on one MI355X.
+
+Workload (one step): fused self-attention at 1024x1024 -- B=2 (CFG cond + uncond), 16 heads x
+128, N=4096 tokens, fp32 fused QKV input [2, 4096, 6144] with q/k RMSNorm + 3D RoPE fused,
+bf16 MFMA with fp32 accumulation, fp32 output [2, 4096, 2048].  Inputs are seeded synthetic
+tensors already resident in HBM.  value = algorithmic attention FLOPs (4*B*H*N^2*D, the
+convention of app/gpu/ops.js:174) / measured time of the whole op (K/V prep + flash kernel).
+
+roofline: the flash kernel's own average duration from HIP events around each launch on the
+library's stream, against the MI355X dense bf16 MFMA peak.  cpu_baseline: the PyTorch fp32
+restatement of tools/reference.py's attention (oracle/torch_ref.py) on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "attention TFLOP/s + % MFMA peak at N=4096; DiT step ms at 1024² (1 GPU)"
+BF16_PEAK_TFLOPS = 2516.6
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    return p.parse_args()
+
+
+def cpu_baseline():
+    """PyTorch fp32 on the host cores (oracle/torch_ref.py), run in its own process so that
+    torch's bundled HIP runtime never shares a process with libanima.so."""
+    import subprocess
+
+    r = subprocess.run([sys.executable, "-m", "oracle.torch_ref", "--attention"], cwd=ROOT, capture_output=True,
+                       text=True, timeout=600)
+    if r.returncode != 0:
+        raise RuntimeError("cpu baseline failed: " + r.stderr[-2000:])
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the multi-GPU sharding is design-only)", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+
+    import __graft_entry__ as ge
+
+    m = ge._import_pkg()
+    B, Hp, Wp, H, D = 2, 64, 64, 16, 128
+    L = Hp * Wp
+    flops = 4.0 * B * H * L * L * D  # 274.878 GFLOP
+
+    # seeded synthetic inputs (numpy PCG64; the parity tests use the torch.randn restatement)
+    rng = np.random.default_rng(2024)
+    qkv = rng.standard_normal((B, L, 3 * H * D), dtype=np.float32)
+    qn = (1 + 0.02 * rng.standard_normal(D)).astype(np.float32)
+    kn = (1 + 0.02 * rng.standard_normal(D)).astype(np.float32)
+    cs = m.dit_rope_table(Hp, Wp)  # host-side table, as app/models/common.js:211-260
+
+    with m.Context(0) as ctx:
+        d_qkv, d_qn, d_kn, d_cs = ctx.upload(qkv), ctx.upload(qn), ctx.upload(kn), ctx.upload(cs)
+        d_o = ctx.empty((B, L, H * D))
+        ld = 3 * H * D
+
+        def step():
+            ctx.attention(q=d_qkv, k=d_qkv, v=d_qkv, o=d_o, B=B, Lq=L, Lk=L, H=H, D=D, ldq=ld, ldk=ld, ldv=ld,
+                          k_off=H * D, v_off=2 * H * D, precision=m.PREC_BF16, q_norm=d_qn, k_norm=d_kn,
+                          rope_cs=d_cs, rope_sin_off=L * 64)
+
+        for _ in range(args.warmup):
+            step()
+        ctx.sync()
+        print(f"bench: warmup {args.warmup} done", file=sys.stderr, flush=True)
+        ctx.timer_start()
+        for _ in range(args.steps):
+            step()
+        ms_total = ctx.timer_stop()
+        ctx.sync()
+        ms = ms_total / args.steps
+        print(f"bench: timed {args.steps} steps, {ms:.4f} ms/step", file=sys.stderr, flush=True)
+
+        # per-kernel durations (HIP events around each launch on the library stream)
+        ctx.profile(True)
+        ctx.profile_reset()
+        for _ in range(args.steps):
+            step()
+        rep = {r["name"]: r for r in ctx.profile_report()}
+        ctx.profile(False)
+        fl = rep["attn.flash_bf16"]
+        k_ms = fl["ms"] / fl["count"]
+        achieved = flops / (k_ms / 1e3) / 1e12
+        prep = rep.get("attn.prep_kv_bf16")
+        prep_ms = prep["ms"] / prep["count"] if prep else None
+        prep_gbs = prep["bytes"] / prep["count"] / (prep_ms / 1e3) / 1e9 if prep else None
+        for b in (d_qkv, d_qn, d_kn, d_cs, d_o):
+            b.release()
+
+    value = flops / (ms / 1e3) / 1e12
+    out = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "fused self-attention: B=2 (CFG), 16 heads x 128, N=4096 (1024x1024 image), "
+                               "fp32 QKV [2,4096,6144] -> q/k RMSNorm + 3D RoPE + softmax(QK^T)V, bf16 MFMA fp32 acc",
+                   "B": B, "heads": H, "head_dim": D, "tokens": L, "flops_per_step": flops},
+        "pct_mfma_peak_op": round(100 * value / BF16_PEAK_TFLOPS, 2),
+        "roofline": {"bound": "mfma", "kernel": "attn_flash_bf16", "achieved": round(achieved, 3),
+                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+                     "traffic": None, "kernel_ms": round(k_ms, 5)},
+        "prep_kernel": {"ms": round(prep_ms, 5) if prep_ms else None, "GB/s": round(prep_gbs, 1) if prep_gbs else None,
+                        "frac_hbm": round(prep_gbs / HBM_PEAK_GBS, 4) if prep_gbs else None},
+    }
+    if not args.no_cpu:
+        t = time.time()
+        out["cpu_baseline"] = cpu_baseline()
+        print(f"bench: cpu baseline {time.time() - t:.1f} s", file=sys.stderr, flush=True)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

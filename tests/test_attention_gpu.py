@@ -1,0 +1,263 @@
+"""GPU parity of the attention path through the C ABI (libanima.so) against the CPU oracle.
+
+Inputs are seeded with the torch.randn restatement (oracle.randn) at the shapes of the
+workloads: N=1024 single attention (B=1), N=4096 self-attention (B=2) and 4096x512
+cross-attention with per-batch valid key lengths (B=2).  Tolerances (stated per test):
+  fp32-MFMA kernel vs fp64 brute force:          rel L2 <= 1e-5, max|d| <= 1e-4
+  fp32-MFMA kernel vs the WGSL-order fp32 oracle: rel L2 <= 1e-5
+  bf16-MFMA kernel vs the bf16 numerics model:    rel L2 <= 3e-4
+  bf16-MFMA kernel vs fp64 brute force:           rel L2 <= 1e-2 (bf16 operand rounding)
+Row kernels (qk_norm_rope, rmsnorm, rope) are bit-exact against the oracle.
+"""
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from helpers import amd, rel_l2, max_abs, report
+
+pytestmark = pytest.mark.gpu
+
+HD = 128
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    m = amd()
+    c = m.Context(0)
+    yield c
+    c.close()
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def norm_weights(seed):
+    qn = (1 + 0.02 * orc.randn(seed, HD)).astype(np.float32)
+    kn = (1 + 0.02 * orc.randn(seed + 1, HD)).astype(np.float32)
+    return qn, kn
+
+
+def fused_inputs(seed, B, Hp, Wp, H=16):
+    L = Hp * Wp
+    qkv = orc.randn(seed, B * L * 3 * H * HD).reshape(B, L, 3 * H * HD)
+    qn, kn = norm_weights(seed + 100)
+    cs = orc.dit_rope_table(Hp, Wp)
+    return qkv, qn, kn, cs, L
+
+
+def cpu_norm_rope(qkv, qn, kn, cs, L, H):
+    return np.stack([orc.qk_norm_rope(qkv[b], L, H, HD, 3 * H * HD, qn, kn, cs, L * 64) for b in range(qkv.shape[0])])
+
+
+def run_fused(ctx, qkv, qn, kn, cs, L, H, precision):
+    m = amd()
+    B = qkv.shape[0]
+    d_qkv = ctx.upload(qkv)
+    d_qn, d_kn, d_cs = ctx.upload(qn), ctx.upload(kn), ctx.upload(cs)
+    d_o = ctx.empty((B, L, H * HD))
+    ld = 3 * H * HD
+    ctx.attention(q=d_qkv, k=d_qkv, v=d_qkv, o=d_o, B=B, Lq=L, Lk=L, H=H, D=HD, ldq=ld, ldk=ld, ldv=ld,
+                  q_off=0, k_off=H * HD, v_off=2 * H * HD, precision=precision,
+                  q_norm=d_qn, k_norm=d_kn, rope_cs=d_cs, rope_sin_off=L * 64)
+    out = d_o.numpy()
+    for b in (d_qkv, d_qn, d_kn, d_cs, d_o):
+        b.release()
+    return out
+
+
+def oracle_rows(kind, nqkv, b, rows, L, H):
+    """Oracle attention for the query rows `rows` of batch b (all heads) of a normalized qkv."""
+    ld = 3 * H * HD
+    q = np.ascontiguousarray(nqkv[b, rows])
+    kv = np.ascontiguousarray(nqkv[b])
+    o = orc.attention(kind, q, kv, kv, B=1, Lq=len(rows), Lk=L, H=H, D=HD, ldq=ld, ldk=ld, ldv=ld,
+                      q_off=0, k_off=H * HD, v_off=2 * H * HD)
+    return o[0]
+
+
+# ------------------------------------------------------------------ row kernels (bit-exact)
+
+def test_row_kernels_bit_exact(ctx):
+    case("qk_norm_rope / rmsnorm / rope, L=256 H=16")
+    qkv, qn, kn, cs, L = fused_inputs(11, 1, 16, 16)
+    x = qkv[0]
+    d = ctx.upload(x)
+    d_qn, d_kn, d_cs = ctx.upload(qn), ctx.upload(kn), ctx.upload(cs)
+    ctx.qk_norm_rope(d, L, 16, HD, 3 * 16 * HD, d_qn, d_kn, d_cs, L * 64)
+    got = d.numpy()
+    ref = orc.qk_norm_rope(x, L, 16, HD, 3 * 16 * HD, qn, kn, cs, L * 64)
+    assert np.array_equal(got, ref), report("qk_norm_rope", got, ref)
+
+    rows = np.ascontiguousarray(x[:, :2048]).reshape(-1, 128)
+    dx, dy = ctx.upload(rows), ctx.empty(rows.shape)
+    ctx.rmsnorm(dx, d_qn, dy, rows.shape[0], 128)
+    assert np.array_equal(dy.numpy(), orc.rmsnorm(rows, qn, 128))
+    wide = np.ascontiguousarray(x[:, :2048])
+    w2 = (1 + 0.1 * orc.randn(5, 2048)).astype(np.float32)
+    dx2, dy2, dw2 = ctx.upload(wide), ctx.empty(wide.shape), ctx.upload(w2)
+    ctx.rmsnorm(dx2, dw2, dy2, L, 2048)
+    assert np.array_equal(dy2.numpy(), orc.rmsnorm(wide, w2, 2048))
+
+    xr = ctx.upload(x)
+    ctx.rope(xr, d_cs, L, 16, HD, L * 64, row_stride=3 * 16 * HD, col_off=16 * HD)
+    assert np.array_equal(xr.numpy(), orc.rope(x, cs, L, 16, HD, L * 64, 3 * 16 * HD, 16 * HD))
+
+
+# ------------------------------------------------------------------ single attention, N=1024
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_attention_n1024_fused(ctx, precision):
+    case(f"attention B=1 N=1024 H=16 fused norm+rope {precision}")
+    m = amd()
+    H = 16
+    qkv, qn, kn, cs, L = fused_inputs(1, 1, 32, 32, H)
+    prec = m.PREC_FP32 if precision == "fp32" else m.PREC_BF16
+    got = run_fused(ctx, qkv, qn, kn, cs, L, H, prec)[0]
+    nqkv = cpu_norm_rope(qkv, qn, kn, cs, L, H)
+    rows = np.arange(0, L, 3)  # every third query row, all heads
+    ref64 = oracle_rows("f64", nqkv, 0, rows, L, H)
+    r, mx = report(f"{precision} vs fp64", got[rows], ref64)
+    if precision == "fp32":
+        assert r <= 1e-5 and mx <= 1e-4
+        wg = oracle_rows("wgsl", nqkv, 0, rows, L, H)
+        assert report("fp32 vs wgsl-order", got[rows], wg)[0] <= 1e-5
+    else:
+        assert r <= 1e-2
+        model = oracle_rows("bf16", nqkv, 0, rows, L, H)
+        assert report("bf16 vs bf16 model", got[rows], model)[0] <= 3e-4
+
+
+# ------------------------------------------------------------------ self-attention, N=4096, B=2
+
+@pytest.mark.parametrize("precision", ["bf16", "fp32"])
+def test_attention_n4096_b2_fused(ctx, precision):
+    case(f"attention B=2 N=4096 H=16 fused norm+rope {precision}")
+    m = amd()
+    H = 16
+    qkv, qn, kn, cs, L = fused_inputs(2, 2, 64, 64, H)
+    prec = m.PREC_FP32 if precision == "fp32" else m.PREC_BF16
+    got = run_fused(ctx, qkv, qn, kn, cs, L, H, prec)
+    nqkv = cpu_norm_rope(qkv, qn, kn, cs, L, H)
+    rng = np.random.default_rng(0)
+    rows = np.unique(np.concatenate([np.arange(0, 32), rng.choice(L, 48, replace=False), np.arange(L - 32, L)]))
+    for b in range(2):
+        ref64 = oracle_rows("f64", nqkv, b, rows, L, H)
+        r, mx = report(f"b={b} {precision} vs fp64", got[b, rows], ref64)
+        if precision == "fp32":
+            assert r <= 1e-5 and mx <= 1e-4
+        else:
+            assert r <= 1e-2
+            model = oracle_rows("bf16", nqkv, b, rows, L, H)
+            assert report(f"b={b} bf16 vs model", got[b, rows], model)[0] <= 3e-4
+    assert np.all(np.isfinite(got))
+
+
+def test_attention_constant_v_full_size(ctx):
+    """Size-independent property at N=4096, B=2: V == c for every key -> O == c."""
+    case("attention B=2 N=4096 constant V")
+    m = amd()
+    H = 16
+    qkv, qn, kn, cs, L = fused_inputs(3, 2, 64, 64, H)
+    qkv[:, :, 2 * H * HD:] = 0.625
+    for prec, tol in ((m.PREC_BF16, 4e-3), (m.PREC_FP32, 1e-5)):
+        got = run_fused(ctx, qkv, qn, kn, cs, L, H, prec)
+        assert np.max(np.abs(got - 0.625)) <= tol * 0.625, (prec, np.max(np.abs(got - 0.625)))
+
+
+# ------------------------------------------------------------------ cross-attention 4096 x 512
+
+@pytest.mark.parametrize("precision", ["bf16", "fp32"])
+def test_cross_attention_masked(ctx, precision):
+    case(f"cross-attention B=2 Lq=4096 Lk=512 kv_len mask {precision}")
+    m = amd()
+    B, Lq, Lk, H = 2, 4096, 512, 16
+    q = orc.randn(21, B * Lq * H * HD).reshape(B, Lq, H * HD)
+    k = orc.randn(22, B * Lk * H * HD).reshape(B, Lk, H * HD)
+    v = orc.randn(23, B * Lk * H * HD).reshape(B, Lk, H * HD)
+    qn, kn = norm_weights(24)
+    rng = np.random.default_rng(25)
+    kv_len = rng.integers(64, Lk + 1, size=B).astype(np.int32)
+    prec = m.PREC_FP32 if precision == "fp32" else m.PREC_BF16
+    dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
+    dqn, dkn = ctx.upload(qn), ctx.upload(kn)
+    do = ctx.empty((B, Lq, H * HD))
+    ctx.attention(q=dq, k=dk, v=dv, o=do, B=B, Lq=Lq, Lk=Lk, H=H, D=HD, ldq=H * HD, ldk=H * HD, ldv=H * HD,
+                  kv_len=kv_len, precision=prec, q_norm=dqn, k_norm=dkn)
+    got = do.numpy()
+    for x in (dq, dk, dv, dqn, dkn, do):
+        x.release()
+    rows = np.unique(np.concatenate([np.arange(0, 16), rng.choice(Lq, 48, replace=False), np.arange(Lq - 16, Lq)]))
+    for b in range(B):
+        qb = orc.rmsnorm(q[b, rows].reshape(-1, HD), qn, HD).reshape(len(rows), H * HD)
+        kb = orc.rmsnorm(k[b].reshape(-1, HD), kn, HD).reshape(Lk, H * HD)
+        args = dict(B=1, Lq=len(rows), Lk=Lk, H=H, D=HD, ldq=H * HD, ldk=H * HD, ldv=H * HD, kv_len=kv_len[b:b + 1])
+        ref64 = orc.attention("f64", qb, kb, v[b], **args)[0]
+        r, mx = report(f"b={b} Lv={kv_len[b]} {precision} vs fp64", got[b, rows], ref64)
+        if precision == "fp32":
+            assert r <= 1e-5 and mx <= 1e-4
+        else:
+            assert r <= 1e-2
+            model = orc.attention("bf16", qb, kb, v[b], **args)[0]
+            assert report(f"b={b} bf16 vs model", got[b, rows], model)[0] <= 3e-4
+
+
+# ------------------------------------------------------------------ ragged shapes, GQA, strides
+
+@pytest.mark.parametrize("precision", ["bf16", "fp32"])
+def test_attention_ragged_gqa(ctx, precision):
+    case(f"attention ragged B=3 Lq=200 Lk=77 group=2 {precision}")
+    m = amd()
+    B, Lq, Lk, H, group = 3, 200, 77, 4, 2
+    Hkv = H // group
+    ldq, ldk = H * HD + 8, Hkv * HD + 4  # padded rows
+    q = orc.randn(31, B * Lq * ldq).reshape(B, Lq, ldq)
+    kv = orc.randn(32, B * Lk * 2 * ldk).reshape(B, Lk, 2 * ldk)
+    kv_len = np.array([77, 1, 40], np.int32)
+    prec = m.PREC_FP32 if precision == "fp32" else m.PREC_BF16
+    dq, dkv = ctx.upload(q), ctx.upload(kv)
+    do = ctx.empty((B, Lq, H * HD))
+    ctx.attention(q=dq, k=dkv, v=dkv, o=do, B=B, Lq=Lq, Lk=Lk, H=H, D=HD, group=group, ldq=ldq, ldk=2 * ldk,
+                  ldv=2 * ldk, q_off=4, k_off=0, v_off=ldk, kv_len=kv_len, precision=prec, scale=0.05)
+    got = do.numpy()
+    args = dict(B=B, Lq=Lq, Lk=Lk, H=H, D=HD, group=group, ldq=ldq, ldk=2 * ldk, ldv=2 * ldk, q_off=4, k_off=0,
+                v_off=ldk, kv_len=kv_len, scale=0.05)
+    ref64 = orc.attention("f64", q, kv, kv, **args)
+    r, mx = report(f"{precision} vs fp64", got, ref64)
+    if precision == "fp32":
+        assert r <= 1e-5 and mx <= 1e-4
+    else:
+        assert r <= 1e-2
+        assert report("bf16 vs model", got, orc.attention("bf16", q, kv, kv, **args))[0] <= 3e-4
+    # kv_len == 1: every query returns that key's value row (bf16-rounded V for the bf16 kernel,
+    # scaled by bf16(p)/p with p in (1/2, 1], i.e. within 2^-8 relative)
+    v0 = kv[1, 0, ldk:ldk + Hkv * HD].reshape(Hkv, HD)
+    if precision == "bf16":
+        v0 = orc.bf16_round(v0)
+    exp = np.repeat(v0, group, axis=0).reshape(-1)
+    tol = 4e-3 if precision == "bf16" else 1e-6
+    assert np.allclose(got[1], np.tile(exp, (Lq, 1)), rtol=tol, atol=1e-6)
+
+
+def test_attention_rejects_bad_arguments(ctx):
+    case("attention argument validation")
+    m = amd()
+    d = ctx.empty((64, 3 * 128))
+    base = dict(q=d, k=d, v=d, o=d, B=1, Lq=64, Lk=64, H=1, D=128, ldq=384, ldk=384, ldv=384, ldo=384)
+    with pytest.raises(m.AnimaError) as e:
+        ctx.attention(**{**base, "D": 64, "ldo": 384})
+    assert e.value.code == -5
+    with pytest.raises(m.AnimaError) as e:
+        ctx.attention(**{**base, "causal": 1})
+    assert e.value.code == -5
+    with pytest.raises(m.AnimaError) as e:
+        ctx.attention(**{**base, "ldq": 386})
+    assert e.value.code == -1
+    with pytest.raises(m.AnimaError) as e:
+        ctx.attention(**{**base, "kv_len": [0]})
+    assert e.value.code == -1
+    with pytest.raises(m.AnimaError) as e:
+        ctx.attention(**{**base, "q_off": 300})
+    assert e.value.code == -1
+    d.release()

@@ -8,10 +8,22 @@ import math
 
 import numpy as np
 import pytest
-import torch
-import torch.nn.functional as F
 
 import oracle as orc
+
+# torch is imported lazily: the GPU test process collects this module too, and torch's bundled
+# HIP runtime must not be the one libanima.so binds to.
+torch = None
+F = None
+
+
+@pytest.fixture(autouse=True)
+def _torch():
+    global torch, F
+    import torch as _t
+    import torch.nn.functional as _F
+
+    torch, F = _t, _F
 
 
 def rel_l2(a, b):
