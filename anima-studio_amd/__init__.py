@@ -20,6 +20,10 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "anima.h")
 ANIMA_OK = 0
 PREC_BF16 = 0
 PREC_FP32 = 1
+W_BF16, W_I8, W_W4 = 0, 1, 2
+ACT = {"none": 0, "gelu": 1, "silu": 2}
+EPI_STORE, EPI_RESID, EPI_GATED = 0, 1, 2
+EW = {"silu_mul": 0, "add": 1, "silu": 2, "copy": 3}
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
@@ -49,6 +53,18 @@ class AttnDesc(ctypes.Structure):
     ]
 
 
+class Weight(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int), ("w", _vp), ("scale", _vp),
+                ("srel", _vp), ("codebook", _vp), ("bias", _vp)]
+
+
+class LinearDesc(ctypes.Structure):
+    _fields_ = [("M", _i64), ("W", ctypes.POINTER(Weight)), ("x", _vp), ("ldx", _i64), ("x_rotated", ctypes.c_int),
+                ("xq", _vp), ("xs", _vp), ("out", _vp), ("ldc", _i64), ("alpha", ctypes.c_float),
+                ("act", ctypes.c_int), ("epilogue", ctypes.c_int), ("gate", _vp), ("gate_off", _i64),
+                ("acc_out", _vp)]
+
+
 def lib():
     """Loads libanima.so (raises if it is not built)."""
     global _LIB
@@ -75,6 +91,13 @@ def lib():
         L.anima_qk_norm_rope.argtypes = [_vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _i64, _vp, _vp, _vp, _i64, ctypes.c_float]
         L.anima_rmsnorm.argtypes = [_vp, _vp, _vp, _vp, _i64, ctypes.c_int, ctypes.c_float]
         L.anima_rope.argtypes = [_vp, _vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _i64, _i64, _i64]
+        L.anima_hadamard.argtypes = [_vp, _vp, _vp, _i64]
+        L.anima_quant_rows.argtypes = [_vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _vp, _vp]
+        L.anima_layernorm_mod.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, ctypes.c_int, ctypes.c_float, ctypes.c_int,
+                                          _vp, _vp, _vp]
+        L.anima_elementwise.argtypes = [_vp, ctypes.c_int, _vp, _vp, _vp, _i64]
+        L.anima_zero.argtypes = [_vp, _vp, _i64]
+        L.anima_linear.argtypes = [_vp, ctypes.POINTER(LinearDesc)]
         _LIB = L
     return _LIB
 
@@ -203,6 +226,30 @@ class Context:
                      rope_sin_off=rope_sin_off, eps=eps, causal=causal)
         return self._check(lib().anima_attention(self.h, ctypes.byref(d)))
 
+    def hadamard(self, x, y, n):
+        return self._check(lib().anima_hadamard(self.h, _ptr(x), _ptr(y), n))
+
+    def quant_rows(self, x, M, K, rotate, q, s):
+        return self._check(lib().anima_quant_rows(self.h, _ptr(x), M, K, int(rotate), _ptr(q), _ptr(s)))
+
+    def layernorm_mod(self, x, mod, shift_off, scale_off, rows, cols, rotate=False, y=None, q=None, s=None, eps=1e-6):
+        return self._check(lib().anima_layernorm_mod(self.h, _ptr(x), _ptr(mod), shift_off, scale_off, rows, cols, eps,
+                                                     int(rotate), _ptr(y), _ptr(q), _ptr(s)))
+
+    def elementwise(self, op, a, b, y, n):
+        return self._check(lib().anima_elementwise(self.h, EW[op] if isinstance(op, str) else op, _ptr(a), _ptr(b),
+                                                   _ptr(y), n))
+
+    def zero(self, y, n):
+        return self._check(lib().anima_zero(self.h, _ptr(y), n))
+
+    def linear(self, W, M, out, *, x=None, ldx=0, x_rotated=True, xq=None, xs=None, ldc=0, alpha=0.0, act="none",
+               epilogue=EPI_STORE, gate=None, gate_off=0, acc_out=None):
+        d = LinearDesc(M=M, W=ctypes.pointer(W), x=_ptr(x), ldx=ldx, x_rotated=int(x_rotated), xq=_ptr(xq),
+                       xs=_ptr(xs), out=_ptr(out), ldc=ldc, alpha=alpha, act=ACT[act] if isinstance(act, str) else act,
+                       epilogue=epilogue, gate=_ptr(gate), gate_off=gate_off, acc_out=_ptr(acc_out))
+        return self._check(lib().anima_linear(self.h, ctypes.byref(d)))
+
     def qk_norm_rope(self, qkv, L, H, D, ld, qn, kn, cs, sin_off, eps=1e-6):
         return self._check(lib().anima_qk_norm_rope(self.h, _ptr(qkv), L, H, D, ld, _ptr(qn), _ptr(kn), _ptr(cs), sin_off, eps))
 
@@ -212,6 +259,12 @@ class Context:
     def rope(self, x, cs, L, H, D, sin_off, row_stride=None, col_off=0):
         return self._check(lib().anima_rope(self.h, _ptr(x), _ptr(cs), L, H, D, sin_off,
                                             row_stride if row_stride is not None else H * D, col_off))
+
+
+def weight(kind, N, K, w, scale=None, srel=None, codebook=None, bias=None):
+    """Linear weight object of app/weights.js:1-4 (device buffers)."""
+    return Weight(kind=kind, N=N, K=K, w=_ptr(w), scale=_ptr(scale), srel=_ptr(srel), codebook=_ptr(codebook),
+                  bias=_ptr(bias))
 
 
 def dit_rope_angles(Hp: int, Wp: int) -> np.ndarray:

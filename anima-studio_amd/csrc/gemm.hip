@@ -1,0 +1,365 @@
+// Quantized linears for gfx950: ops.linear -> matmulShader (app/gpu/gemm.js:166-280) with the
+// i8 / w4 B-loaders (gemm.js:129-159), re-designed as W8A8 on the int8 matrix cores.
+//
+//   gemm_i8   C = epi((qx @ qw^T) * s_x[m] * s_w[n]) with v_mfma_i32_32x32x32_i8 (exact int32
+//             accumulation).  Block tile 128x128, k-tile 64, 4 waves of 64x64, double-buffered
+//             LDS with 80-byte rows (conflict-free 16-byte fragment reads).
+//             W4: the weight tile is decoded in the loader, nibble -> int8 grid value through a
+//             16-entry table per 16-weight group.  The table of a group depends only on its fp8
+//             s_rel byte, so each workgroup first builds all 256 possible tables,
+//             T[s][c] = clamp(rint(codebook[c] * fp8(s)), -127, 127) (tools/quant.py:127-129),
+//             in LDS; decoding is then one 16-byte LDS read per group plus byte permutes.
+//   gemm_f32w bf16 weights (x_embedder, final layer, timestep / adaLN projections): fp32 FMA
+//             with fp32 activations, the reference's own arithmetic (gemm.js:108-128).
+#include <cmath>
+
+#include "common.h"
+#include "internal.h"
+
+namespace anima {
+
+struct GemmArgs {
+  const int8_t* qx;   // [M][K]
+  const float* sx;    // [M]
+  const void* w;      // i8 [N][K] | w4 codes [N][K/2]
+  const float* sw;    // [N]
+  const uint8_t* srel;
+  const float* cb;
+  const float* bias;
+  float* out;
+  int64_t ldc;
+  float alpha;
+  int act, epi;
+  const float* gate;
+  int64_t gate_off;
+  int32_t* acc_out;
+  int M, N, K;
+};
+
+__device__ __forceinline__ float gelu_erf(float x) {  // app/gpu/kernels.js:11-18
+  const float z = x * 0.7071067811865476f;
+  const float s = z > 0.0f ? 1.0f : (z < 0.0f ? -1.0f : 0.0f);
+  const float a = fabsf(z);
+  const float t = 1.0f / (1.0f + 0.3275911f * a);
+  const float y = 1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
+                          0.254829592f) * t * expf(-a * a);
+  return 0.5f * x * (1.0f + s * y);
+}
+
+__device__ __forceinline__ float apply_act(float r, int act) {
+  if (act == ANIMA_ACT_GELU) return gelu_erf(r);
+  if (act == ANIMA_ACT_SILU) return r / (1.0f + expf(-r));
+  return r;
+}
+
+__device__ __forceinline__ void epilogue_store(const GemmArgs& a, int m, int n, float r) {
+  if (a.bias) r = r + a.bias[n];
+  r = apply_act(r, a.act);
+  float* c = a.out + (int64_t)m * a.ldc + n;
+  if (a.epi == ANIMA_EPI_STORE) *c = r;
+  else if (a.epi == ANIMA_EPI_RESID) *c = *c + r;
+  else *c = __builtin_fmaf(a.gate[a.gate_off + n], r, *c);
+}
+
+__device__ __forceinline__ float fp8e4m3(uint32_t b) {  // app/gpu/gemm.js:144-151
+  const uint32_t e = (b >> 3) & 15u;
+  const float m = (float)(b & 7u);
+  float v = e == 0 ? m * 0.001953125f : (1.0f + m * 0.125f) * __builtin_ldexpf(1.0f, (int)e - 7);
+  return (b & 128u) ? -v : v;
+}
+
+// 4 nibbles (one per byte, values 0..15) -> 4 table bytes, table = 16 bytes in t0..t3.
+__device__ __forceinline__ uint32_t lut4(uint32_t nib, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+  const uint32_t sel = nib & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);  // entries 0..7
+  const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);  // entries 8..15
+  const uint32_t mask = ((nib >> 3) & 0x01010101u) * 0xffu;
+  return (hi & mask) | (lo & ~mask);
+}
+
+// 8 consecutive 4-bit codes (low nibble = even k) -> 8 int8 values in k order.
+__device__ __forceinline__ uint2 decode8(uint32_t w, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+  const uint32_t ev = lut4(w & 0x0f0f0f0fu, t0, t1, t2, t3);          // k = 0, 2, 4, 6
+  const uint32_t od = lut4((w >> 4) & 0x0f0f0f0fu, t0, t1, t2, t3);   // k = 1, 3, 5, 7
+  return make_uint2(__builtin_amdgcn_perm(od, ev, 0x05010400u), __builtin_amdgcn_perm(od, ev, 0x07030602u));
+}
+
+constexpr int GBM = 128, GBN = 128, GBK = 64, GROW = GBK + 16;  // LDS row stride 80 B
+
+template <bool W4>
+__global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) int8_t As[2][GBM * GROW];
+  __shared__ __attribute__((aligned(16))) int8_t Bs[2][GBN * GROW];
+  __shared__ __attribute__((aligned(16))) uint32_t lut[W4 ? 256 * 4 : 1];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 31, hf = lane >> 5;
+  const int bm = blockIdx.y * GBM, bn = blockIdx.x * GBN;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+
+  if constexpr (W4) {
+    for (int i = tid; i < 256 * 4; i += 256) {
+      const int sb = i >> 2, q = i & 3;
+      const float s = fp8e4m3((uint32_t)sb);
+      uint32_t packed = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        float v = rintf(a.cb[4 * q + j] * s);
+        v = fminf(fmaxf(v, -127.0f), 127.0f);
+        packed |= ((uint32_t)(int32_t)v & 0xffu) << (8 * j);
+      }
+      lut[i] = packed;
+    }
+  }
+
+  // loader assignment: row tid/2, 32 k at (tid&1)*32
+  const int lr = tid >> 1, lk = (tid & 1) * 32;
+  const bool arow = bm + lr < a.M, brow = bn + lr < a.N;
+  const int8_t* ag = a.qx + (int64_t)(bm + lr) * a.K + lk;
+  uint4 ar[2], br[2];
+  uint4 bcodes;
+  uint32_t bs2 = 0;
+  auto gload = [&](int kt) {
+    const int k0 = kt * GBK;
+    if (arow) {
+      ar[0] = *(const uint4*)(ag + k0);
+      ar[1] = *(const uint4*)(ag + k0 + 16);
+    } else {
+      ar[0] = ar[1] = make_uint4(0, 0, 0, 0);
+    }
+    if constexpr (!W4) {
+      if (brow) {
+        const int8_t* bg = (const int8_t*)a.w + (int64_t)(bn + lr) * a.K + k0 + lk;
+        br[0] = *(const uint4*)bg;
+        br[1] = *(const uint4*)(bg + 16);
+      } else {
+        br[0] = br[1] = make_uint4(0, 0, 0, 0);
+      }
+    } else {
+      if (brow) {
+        const uint8_t* cg = (const uint8_t*)a.w + (int64_t)(bn + lr) * (a.K / 2) + (k0 + lk) / 2;
+        bcodes = *(const uint4*)cg;
+        const uint8_t* sg = a.srel + (int64_t)(bn + lr) * (a.K / 16) + (k0 + lk) / 16;
+        bs2 = (uint32_t)sg[0] | ((uint32_t)sg[1] << 8);
+      } else {
+        bcodes = make_uint4(0, 0, 0, 0);
+        bs2 = 0xffffffffu;  // marker: zero row
+      }
+    }
+  };
+  auto lstore = [&](int st) {
+    uint4* ad = (uint4*)(As[st] + lr * GROW + lk);
+    ad[0] = ar[0];
+    ad[1] = ar[1];
+    uint4* bd = (uint4*)(Bs[st] + lr * GROW + lk);
+    if constexpr (!W4) {
+      bd[0] = br[0];
+      bd[1] = br[1];
+    } else {
+      if (bs2 == 0xffffffffu) {
+        bd[0] = bd[1] = make_uint4(0, 0, 0, 0);
+      } else {
+        const uint4 t0 = *(const uint4*)&lut[4 * (bs2 & 0xffu)];
+        const uint4 t1 = *(const uint4*)&lut[4 * ((bs2 >> 8) & 0xffu)];
+        const uint2 d0 = decode8(bcodes.x, t0.x, t0.y, t0.z, t0.w);
+        const uint2 d1 = decode8(bcodes.y, t0.x, t0.y, t0.z, t0.w);
+        const uint2 d2 = decode8(bcodes.z, t1.x, t1.y, t1.z, t1.w);
+        const uint2 d3 = decode8(bcodes.w, t1.x, t1.y, t1.z, t1.w);
+        bd[0] = make_uint4(d0.x, d0.y, d1.x, d1.y);
+        bd[1] = make_uint4(d2.x, d2.y, d3.x, d3.y);
+      }
+    }
+  };
+
+  i32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = (i32x16){};
+
+  const int nk = a.K / GBK;
+  if (W4) __syncthreads();  // table ready
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt++) {
+    const int st = kt & 1;
+    if (kt + 1 < nk) gload(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      i32x4 af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        af[i] = *(const i32x4*)(As[st] + (wm + 32 * i + lq) * GROW + 32 * ks + 16 * hf);
+        bf[i] = *(const i32x4*)(Bs[st] + (wn + 32 * i + lq) * GROW + 32 * ks + 16 * hf);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) lstore(st ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: lane (n + 32g), register r -> row 8(r/4) + 4g + r%4
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int n = bn + wn + 32 * j + lq;
+    if (n >= a.N) continue;
+    const float swn = a.sw[n];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int m = bm + wm + 32 * i + 8 * (r >> 2) + 4 * hf + (r & 3);
+        if (m >= a.M) continue;
+        const int32_t v = acc[i][j][r];
+        if (a.acc_out) a.acc_out[(int64_t)m * a.N + n] = v;
+        float y = (float)v * a.sx[m];
+        y = y * swn;
+        if (a.alpha != 1.0f) y = y * a.alpha;
+        epilogue_store(a, m, n, y);
+      }
+  }
+}
+
+// ------------------------------------------------------------------ bf16 weights, fp32 math
+
+struct F32WArgs {
+  const float* x;
+  int64_t ldx;
+  const uint16_t* w;  // bf16 [N][K]
+  const float* bias;
+  float* out;
+  int64_t ldc;
+  float alpha;
+  int act, epi;
+  const float* gate;
+  int64_t gate_off;
+  int M, N, K;
+};
+
+// 64x64 tile, 256 threads x (4x4) outputs, k-tile 16 (the small-tile layout of gemm.js:17).
+__global__ __launch_bounds__(256) void gemm_f32w_kernel(F32WArgs a) {
+  __shared__ float Xs[16][64 + 4];
+  __shared__ float Ws[16][64 + 4];
+  const int tid = threadIdx.x;
+  const int bm = blockIdx.y * 64, bn = blockIdx.x * 64;
+  const int tm = tid & 15, tn = tid >> 4;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < a.K; k0 += 16) {
+    for (int i = tid; i < 64 * 16; i += 256) {
+      const int r = i >> 4, kk = i & 15;
+      const int m = bm + r, n = bn + r, k = k0 + kk;
+      Xs[kk][r] = (m < a.M && k < a.K) ? a.x[(int64_t)m * a.ldx + k] : 0.0f;
+      Ws[kk][r] = (n < a.N && k < a.K) ? __uint_as_float((uint32_t)a.w[(int64_t)n * a.K + k] << 16) : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; kk++) {
+      float xv[4], wv[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        xv[i] = Xs[kk][tm + 16 * i];
+        wv[i] = Ws[kk][tn + 16 * i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_fmaf(xv[i], wv[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int m = bm + tm + 16 * i;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int n = bn + tn + 16 * j;
+      if (n >= a.N) continue;
+      float r = acc[i][j] * a.alpha;
+      if (a.bias) r = r + a.bias[n];
+      r = apply_act(r, a.act);
+      float* c = a.out + (int64_t)m * a.ldc + n;
+      if (a.epi == ANIMA_EPI_STORE) *c = r;
+      else if (a.epi == ANIMA_EPI_RESID) *c = *c + r;
+      else *c = __builtin_fmaf(a.gate[a.gate_off + n], r, *c);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ host
+
+static bool al(const void* p, int b) { return ((uintptr_t)p & (b - 1)) == 0; }
+
+int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
+  const anima_weight* W = d->W;
+  if (!W) return fail(c, ANIMA_E_ARG, "anima_linear: null weight");
+  const int64_t M = d->M;
+  const int N = W->N, K = W->K;
+  if (M < 0 || M > 0x7fffffff || N < 1 || K < 1) return fail(c, ANIMA_E_ARG, "anima_linear: M=%lld N=%d K=%d", (long long)M, N, K);
+  if (!d->out || !W->w) return fail(c, ANIMA_E_ARG, "anima_linear: null out or weight data");
+  if (d->act < ANIMA_ACT_NONE || d->act > ANIMA_ACT_SILU) return fail(c, ANIMA_E_ARG, "anima_linear: unknown act %d", d->act);
+  if (d->epilogue < ANIMA_EPI_STORE || d->epilogue > ANIMA_EPI_GATED) return fail(c, ANIMA_E_ARG, "anima_linear: unknown epilogue %d", d->epilogue);
+  if (d->epilogue == ANIMA_EPI_GATED && !d->gate) return fail(c, ANIMA_E_ARG, "anima_linear: gated epilogue without gate");
+  const int64_t ldc = d->ldc ? d->ldc : N;
+  if (ldc < N) return fail(c, ANIMA_E_ARG, "anima_linear: ldc=%lld < N=%d", (long long)ldc, N);
+  const float alpha = d->alpha != 0.0f ? d->alpha : 1.0f;
+  if (M == 0) return ANIMA_OK;
+
+  if (W->kind == ANIMA_W_BF16) {
+    if (!d->x) return fail(c, ANIMA_E_ARG, "anima_linear: bf16 weights need fp32 x");
+    if (d->acc_out || d->xq) return fail(c, ANIMA_E_ARG, "anima_linear: acc_out / xq apply to i8/w4 weights only");
+    const int64_t ldx = d->ldx ? d->ldx : K;
+    if (ldx < K) return fail(c, ANIMA_E_ARG, "anima_linear: ldx < K");
+    F32WArgs f{d->x, ldx, (const uint16_t*)W->w, W->bias, d->out, ldc, alpha, d->act, d->epilogue, d->gate, d->gate_off,
+               (int)M, N, K};
+    Launch L(c, "gemm.bf16", 2.0 * M * N * K, 0.0);
+    hipLaunchKernelGGL(gemm_f32w_kernel, dim3((N + 63) / 64, (unsigned)((M + 63) / 64)), dim3(256), 0, c->stream, f);
+    return L.end();
+  }
+  if (W->kind != ANIMA_W_I8 && W->kind != ANIMA_W_W4) return fail(c, ANIMA_E_ARG, "anima_linear: unknown weight kind %d", W->kind);
+  const bool w4 = W->kind == ANIMA_W_W4;
+  if (K % GBK) return fail(c, ANIMA_E_ARG, "anima_linear: K=%d must be a multiple of %d for quantized weights", K, GBK);
+  if (!W->scale || (w4 && (!W->srel || !W->codebook))) return fail(c, ANIMA_E_ARG, "anima_linear: missing scale/s_rel/codebook");
+  if (!al(W->w, 16)) return fail(c, ANIMA_E_ARG, "anima_linear: weight data must be 16-byte aligned");
+
+  const int8_t* qx = d->xq;
+  const float* sx = d->xs;
+  void* tmp = nullptr;
+  if (!qx) {
+    if (!d->x) return fail(c, ANIMA_E_ARG, "anima_linear: no input (x or xq)");
+    const int64_t ldx = d->ldx ? d->ldx : K;
+    if (ldx != K) return fail(c, ANIMA_E_ARG, "anima_linear: quantized weights need contiguous x (ldx == K)");
+    if (K > 8192 || (!d->x_rotated && K % 256)) return fail(c, ANIMA_E_ARG, "anima_linear: K=%d (<= 8192, %% 256 == 0 to rotate)", K);
+    int rc = anima_alloc(c, (size_t)M * K + (size_t)M * 4 + 256, &tmp);
+    if (rc) return rc;
+    int8_t* q = (int8_t*)tmp;
+    float* s = (float*)((char*)tmp + ((size_t)M * K + 255) / 256 * 256);
+    rc = quant_rows_launch(c, d->x, M, K, d->x_rotated ? 0 : 1, q, s);
+    if (rc) {
+      anima_free(c, tmp);
+      return rc;
+    }
+    qx = q;
+    sx = s;
+  } else {
+    if (!sx) return fail(c, ANIMA_E_ARG, "anima_linear: xq without xs");
+    if (!al(qx, 16)) return fail(c, ANIMA_E_ARG, "anima_linear: xq must be 16-byte aligned");
+  }
+  GemmArgs g{qx, sx, W->w, W->scale, W->srel, W->codebook, W->bias, d->out, ldc, alpha, d->act, d->epilogue,
+             d->gate, d->gate_off, d->acc_out, (int)M, N, K};
+  int rc;
+  {
+    Launch L(c, w4 ? "gemm.w4a8" : "gemm.i8", 2.0 * M * N * K, 0.0);
+    dim3 grid((N + GBN - 1) / GBN, (unsigned)((M + GBM - 1) / GBM));
+    if (w4) hipLaunchKernelGGL(gemm_i8_kernel<true>, grid, dim3(256), 0, c->stream, g);
+    else hipLaunchKernelGGL(gemm_i8_kernel<false>, grid, dim3(256), 0, c->stream, g);
+    rc = L.end();
+  }
+  if (tmp) anima_free(c, tmp);  // stream-ordered reuse
+  return rc;
+}
+
+}  // namespace anima

@@ -75,5 +75,14 @@ int rmsnorm_launch(anima_ctx* c, const float* x, const float* w, float* y, int64
                    int cols, float eps);
 int rope_launch(anima_ctx* c, float* x, const float* cs, int64_t L, int H, int D,
                 int64_t sin_off, int64_t row_stride, int64_t col_off);
+int hadamard_launch(anima_ctx* c, const float* x, float* y, int64_t n);
+int quant_rows_launch(anima_ctx* c, const float* x, int64_t M, int K, int rotate, int8_t* q, float* s);
+int layernorm_mod_launch(anima_ctx* c, const float* x, const float* mod, int64_t shift_off, int64_t scale_off,
+                         int64_t rows, int cols, float eps, int rotate, float* y, int8_t* q, float* s);
+int elementwise_launch(anima_ctx* c, int op, const float* a, const float* b, float* y, int64_t n);
+int zero_launch(anima_ctx* c, float* y, int64_t n);
+
+// ---- kernel launchers (gemm.hip)
+int linear_launch(anima_ctx* c, const anima_linear_desc* d);
 
 }  // namespace anima

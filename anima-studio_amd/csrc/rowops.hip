@@ -73,6 +73,235 @@ __global__ __launch_bounds__(256) void rope_kernel(float* X, const float* CS, in
   }
 }
 
+// In-place 4-stage radix-4 butterfly over each 256-group of S[0..cols) (app/gpu/kernels.js:124-140),
+// 256 threads, quads strided over the row.  Caller synchronizes before and after.
+__device__ __forceinline__ void butterfly_rows(float* S, int cols) {
+  const int t = threadIdx.x;
+  const int quads = cols >> 2;
+  int stride = 1;
+  for (int d = 0; d < 4; d++) {
+    for (int q = t; q < quads; q += 256) {
+      const int g = q >> 6, w = q & 63;
+      const int i0 = g * 256 + (w / stride) * stride * 4 + w % stride;
+      const float a = S[i0], b = S[i0 + stride], c = S[i0 + 2 * stride], e = S[i0 + 3 * stride];
+      S[i0] = a + b + c - e;
+      S[i0 + stride] = a + b - c + e;
+      S[i0 + 2 * stride] = a - b + c + e;
+      S[i0 + 3 * stride] = -a + b + c + e;
+    }
+    __syncthreads();
+    stride *= 4;
+  }
+}
+
+// Block-wide reduction in the order of the shaders' "red[t] += red[t + s]" loops (s = 128..1).
+__device__ __forceinline__ float block_tree_sum(float v, float* red) {
+  const int t = threadIdx.x;
+  red[t] = v;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (t < s) red[t] = red[t] + red[t + s];
+    __syncthreads();
+  }
+  const float r = red[0];
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  return r;
+}
+
+// Per-token int8 of the row held in S (256 threads): s = amax/127, q = clamp(rint(x/s)).
+__device__ __forceinline__ void quant_row(const float* S, int cols, float* red, int8_t* q, float* s_out) {
+  const int t = threadIdx.x;
+  float amax = 0.0f;
+  for (int c = t; c < cols; c += 256) amax = fmaxf(amax, fabsf(S[c]));
+  amax = block_max(amax, red);
+  const float s = amax / 127.0f;
+  if (t == 0) *s_out = s;
+  for (int c4 = t; c4 < (cols >> 2); c4 += 256) {
+    char4 o;
+    int8_t* ob = (int8_t*)&o;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float v = amax == 0.0f ? 0.0f : rintf(S[4 * c4 + j] / s);
+      v = fminf(fmaxf(v, -127.0f), 127.0f);
+      ob[j] = (int8_t)v;
+    }
+    *(char4*)(q + 4 * c4) = o;
+  }
+}
+
+// One wave per 256-group (app/gpu/kernels.js:366-388), 4 groups per workgroup.
+__global__ __launch_bounds__(256) void hadamard_kernel(const float* X, float* Y, int64_t groups) {
+  __shared__ float S[4][256];
+  const int w = threadIdx.x >> 6, t = threadIdx.x & 63;
+  const int64_t g = (int64_t)blockIdx.x * 4 + w;
+  const bool live = g < groups;
+  float* s = S[w];
+  if (live)
+    for (int j = 0; j < 4; j++) s[t + 64 * j] = X[g * 256 + t + 64 * j];
+  __syncthreads();
+  int stride = 1;
+  for (int d = 0; d < 4; d++) {
+    const int lo = t % stride;
+    const int i0 = (t / stride) * stride * 4 + lo;
+    const float a = s[i0], b = s[i0 + stride], c = s[i0 + 2 * stride], e = s[i0 + 3 * stride];
+    __syncthreads();
+    s[i0] = a + b + c - e;
+    s[i0 + stride] = a + b - c + e;
+    s[i0 + 2 * stride] = a - b + c + e;
+    s[i0 + 3 * stride] = -a + b + c + e;
+    __syncthreads();
+    stride *= 4;
+  }
+  if (live)
+    for (int j = 0; j < 4; j++) Y[g * 256 + t + 64 * j] = s[t + 64 * j] * 0.0625f;
+}
+
+// One workgroup per row: optional ConvRot rotation, then per-token int8.
+__global__ __launch_bounds__(256) void quant_rows_kernel(const float* X, int K, int rotate, int8_t* Q, float* S_out) {
+  extern __shared__ float S[];
+  __shared__ float red[256];
+  const int64_t row = blockIdx.x;
+  const float* x = X + row * K;
+  for (int c4 = threadIdx.x; c4 < (K >> 2); c4 += 256) *(float4*)(S + 4 * c4) = *(const float4*)(x + 4 * c4);
+  __syncthreads();
+  if (rotate) {
+    butterfly_rows(S, K);
+    for (int c = threadIdx.x; c < K; c += 256) S[c] = S[c] * 0.0625f;
+    __syncthreads();
+  }
+  quant_row(S, K, red, Q + row * K, S_out + row);
+}
+
+// LayerNorm (no affine) + adaLN modulation (+ Hadamard) (+ int8), one workgroup per row
+// (app/gpu/kernels.js:108-145).
+__global__ __launch_bounds__(256) void layernorm_mod_kernel(const float* X, const float* MOD, int64_t shift_off,
+                                                            int64_t scale_off, int cols, float eps, int rotate, float* Y,
+                                                            int8_t* Q, float* S_out) {
+  extern __shared__ float S[];
+  __shared__ float red[256];
+  const int t = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const float* x = X + row * cols;
+  float s = 0.0f;
+  for (int c = t; c < cols; c += 256) s += x[c];
+  const float mean = block_tree_sum(s, red) / (float)cols;
+  float v = 0.0f;
+  for (int c = t; c < cols; c += 256) {
+    const float d = x[c] - mean;
+    v += d * d;
+  }
+  const float r = 1.0f / sqrtf(block_tree_sum(v, red) / (float)cols + eps);
+  for (int c = t; c < cols; c += 256) S[c] = (x[c] - mean) * r * (1.0f + MOD[scale_off + c]) + MOD[shift_off + c];
+  __syncthreads();
+  if (rotate) {
+    butterfly_rows(S, cols);
+    for (int c = t; c < cols; c += 256) S[c] = S[c] * 0.0625f;
+    __syncthreads();
+  }
+  if (Y)
+    for (int c = t; c < cols; c += 256) Y[row * cols + c] = S[c];
+  if (Q) quant_row(S, cols, red, Q + row * cols, S_out + row);
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+__global__ __launch_bounds__(256) void elementwise_kernel(int op, const float* A, const float* B, float* Y, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const float a = A ? A[i] : 0.0f;
+    float y;
+    switch (op) {
+      case ANIMA_EW_SILU_MUL: y = silu_f(a) * B[i]; break;
+      case ANIMA_EW_ADD: y = a + B[i]; break;
+      case ANIMA_EW_SILU: y = silu_f(a); break;
+      default: y = a; break;
+    }
+    Y[i] = y;
+  }
+}
+
+// 16-byte copy / fill (elementwise copy on aligned buffers, zero).
+__global__ __launch_bounds__(256) void copy4_kernel(const float4* A, float4* Y, int64_t n4) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256)
+    Y[i] = A ? A[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
+static unsigned grid_for(int64_t n) { return (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, 8192)); }
+
+int hadamard_launch(anima_ctx* c, const float* x, float* y, int64_t n) {
+  if (!x || !y) return fail(c, ANIMA_E_ARG, "anima_hadamard: null pointer");
+  if (n < 0 || n % 256) return fail(c, ANIMA_E_ARG, "anima_hadamard: n=%lld must be a multiple of 256", (long long)n);
+  if (n == 0) return ANIMA_OK;
+  const int64_t groups = n / 256;
+  Launch lc(c, "hadamard", 0.0, (double)n * 8);
+  hipLaunchKernelGGL(hadamard_kernel, dim3((unsigned)((groups + 3) / 4)), dim3(256), 0, c->stream, x, y, groups);
+  return lc.end();
+}
+
+int quant_rows_launch(anima_ctx* c, const float* x, int64_t M, int K, int rotate, int8_t* q, float* s) {
+  if (!x || !q || !s) return fail(c, ANIMA_E_ARG, "anima_quant_rows: null pointer");
+  if (M < 0 || K < 4 || K % 4 || K > 8192 || (rotate && K % 256))
+    return fail(c, ANIMA_E_ARG, "anima_quant_rows: M=%lld K=%d (K %% 4 == 0, <= 8192, %% 256 == 0 when rotating)", (long long)M, K);
+  if (M > 0x7fffffff) return fail(c, ANIMA_E_ARG, "anima_quant_rows: M too large");
+  if (((uintptr_t)x & 15) || ((uintptr_t)q & 3)) return fail(c, ANIMA_E_ARG, "anima_quant_rows: x must be 16-byte and q 4-byte aligned");
+  if (M == 0) return ANIMA_OK;
+  Launch lc(c, rotate ? "hadamard_quant" : "quant_rows", 0.0, (double)M * K * 5 + M * 4.0);
+  hipLaunchKernelGGL(quant_rows_kernel, dim3((unsigned)M), dim3(256), (size_t)K * 4, c->stream, x, K, rotate, q, s);
+  return lc.end();
+}
+
+int layernorm_mod_launch(anima_ctx* c, const float* x, const float* mod, int64_t shift_off, int64_t scale_off,
+                         int64_t rows, int cols, float eps, int rotate, float* y, int8_t* q, float* s) {
+  if (!x || !mod) return fail(c, ANIMA_E_ARG, "anima_layernorm_mod: null x or mod");
+  if (!y && !q) return fail(c, ANIMA_E_ARG, "anima_layernorm_mod: no output (y or q)");
+  if (q && (!s || !rotate)) return fail(c, ANIMA_E_ARG, "anima_layernorm_mod: int8 output needs s and rotate");
+  if (rows < 0 || rows > 0x7fffffff || cols < 4 || cols % 4 || cols > 8192 || (rotate && cols % 256))
+    return fail(c, ANIMA_E_ARG, "anima_layernorm_mod: rows=%lld cols=%d", (long long)rows, cols);
+  if (shift_off < 0 || scale_off < 0) return fail(c, ANIMA_E_ARG, "anima_layernorm_mod: negative offsets");
+  if (q && ((uintptr_t)q & 3)) return fail(c, ANIMA_E_ARG, "anima_layernorm_mod: q must be 4-byte aligned");
+  if (rows == 0) return ANIMA_OK;
+  const double bytes = (double)rows * cols * 4 + (y ? rows * (double)cols * 4 : 0) + (q ? rows * (double)cols + rows * 4.0 : 0);
+  Launch lc(c, q ? "layernorm_mod_rot_quant" : (rotate ? "layernorm_mod_rot" : "layernorm_mod"), 0.0, bytes);
+  hipLaunchKernelGGL(layernorm_mod_kernel, dim3((unsigned)rows), dim3(256), (size_t)cols * 4, c->stream, x, mod, shift_off,
+                     scale_off, cols, eps, rotate, y, q, s);
+  return lc.end();
+}
+
+int elementwise_launch(anima_ctx* c, int op, const float* a, const float* b, float* y, int64_t n) {
+  if (op < ANIMA_EW_SILU_MUL || op > ANIMA_EW_COPY) return fail(c, ANIMA_E_ARG, "anima_elementwise: unknown op %d", op);
+  if (!a || !y || ((op == ANIMA_EW_SILU_MUL || op == ANIMA_EW_ADD) && !b)) return fail(c, ANIMA_E_ARG, "anima_elementwise: null pointer");
+  if (n < 0) return fail(c, ANIMA_E_ARG, "anima_elementwise: n < 0");
+  if (n == 0) return ANIMA_OK;
+  static const char* names[] = {"elementwise.silu_mul", "elementwise.add", "elementwise.silu", "elementwise.copy"};
+  const int nin = (op == ANIMA_EW_SILU_MUL || op == ANIMA_EW_ADD) ? 2 : 1;
+  Launch lc(c, names[op], 0.0, (double)n * 4 * (nin + 1));
+  if (op == ANIMA_EW_COPY && n % 4 == 0 && !((uintptr_t)a & 15) && !((uintptr_t)y & 15))
+    hipLaunchKernelGGL(copy4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, c->stream, (const float4*)a, (float4*)y, n / 4);
+  else
+    hipLaunchKernelGGL(elementwise_kernel, dim3(grid_for(n)), dim3(256), 0, c->stream, op, a, b, y, n);
+  return lc.end();
+}
+
+int zero_launch(anima_ctx* c, float* y, int64_t n) {
+  if (!y || n < 0) return fail(c, ANIMA_E_ARG, "anima_zero: bad arguments");
+  if (n == 0) return ANIMA_OK;
+  Launch lc(c, "zero", 0.0, (double)n * 4);
+  if (n % 4 == 0 && !((uintptr_t)y & 15))
+    hipLaunchKernelGGL(copy4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, c->stream, (const float4*)nullptr, (float4*)y, n / 4);
+  else
+    hipLaunchKernelGGL(elementwise_kernel, dim3(grid_for(n)), dim3(256), 0, c->stream, (int)ANIMA_EW_COPY, (const float*)nullptr,
+                       (const float*)nullptr, y, n);
+  return lc.end();
+}
+
 int qk_norm_rope_launch(anima_ctx* c, float* qkv, int64_t L, int H, int D, int64_t ld, const float* qn,
                         const float* kn, const float* cs, int64_t sin_off, float eps) {
   if (!qkv || !qn || !kn || !cs) return fail(c, ANIMA_E_ARG, "anima_qk_norm_rope: null pointer");

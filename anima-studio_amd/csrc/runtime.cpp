@@ -363,4 +363,36 @@ int anima_rope(anima_ctx* c, float* x, const float* cs, int64_t L, int H, int D,
   return rope_launch(c, x, cs, L, H, D, sin_off, row_stride, col_off);
 }
 
+int anima_hadamard(anima_ctx* c, const float* x, float* y, int64_t n) {
+  CHECK_CTX(c);
+  return hadamard_launch(c, x, y, n);
+}
+
+int anima_quant_rows(anima_ctx* c, const float* x, int64_t M, int K, int rotate, int8_t* q, float* s) {
+  CHECK_CTX(c);
+  return quant_rows_launch(c, x, M, K, rotate, q, s);
+}
+
+int anima_layernorm_mod(anima_ctx* c, const float* x, const float* mod, int64_t shift_off, int64_t scale_off,
+                        int64_t rows, int cols, float eps, int rotate, float* y, int8_t* q, float* s) {
+  CHECK_CTX(c);
+  return layernorm_mod_launch(c, x, mod, shift_off, scale_off, rows, cols, eps, rotate, y, q, s);
+}
+
+int anima_elementwise(anima_ctx* c, int op, const float* a, const float* b, float* y, int64_t n) {
+  CHECK_CTX(c);
+  return elementwise_launch(c, op, a, b, y, n);
+}
+
+int anima_zero(anima_ctx* c, float* y, int64_t n) {
+  CHECK_CTX(c);
+  return zero_launch(c, y, n);
+}
+
+int anima_linear(anima_ctx* c, const anima_linear_desc* d) {
+  CHECK_CTX(c);
+  if (!d) return fail(c, ANIMA_E_ARG, "anima_linear: null descriptor");
+  return linear_launch(c, d);
+}
+
 }  // extern "C"

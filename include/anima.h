@@ -126,6 +126,85 @@ int anima_rmsnorm(anima_ctx* ctx, const float* x, const float* w, float* y, int6
 int anima_rope(anima_ctx* ctx, float* x, const float* cs, int64_t L, int H, int D,
                int64_t sin_off, int64_t row_stride, int64_t col_off);
 
+/* ops.rotate (app/gpu/ops.js:38-44; kernels.js:360-388): y = x @ H per contiguous group of 256
+ * features, H = kron(H4,H4,H4,H4)/16.  n % 256 == 0; y may equal x. */
+int anima_hadamard(anima_ctx* ctx, const float* x, float* y, int64_t n);
+/* Per-token dynamic int8 quantization of rows x[M][K] (no reference counterpart: the reference
+ * keeps activations fp32).  With rotate != 0 the ConvRot Hadamard of anima_hadamard is applied
+ * first (K % 256 == 0).  s[m] = amax_k|x_r[m,k]| / 127 (0 for an all-zero row),
+ * q[m,k] = clamp(rint(x_r[m,k] / s[m]), -127, 127).  K % 4 == 0, K <= 8192. */
+int anima_quant_rows(anima_ctx* ctx, const float* x, int64_t M, int K, int rotate, int8_t* q,
+                     float* s);
+/* ops.layernormMod (app/gpu/ops.js:129-137; kernels.js:95-145): LayerNorm without affine,
+ * y = LN(x) * (1 + mod[scale_off + c]) + mod[shift_off + c], then the ConvRot Hadamard when
+ * rotate != 0.  Writes the fp32 result to y (if non-NULL) and/or its per-token int8
+ * quantization to q, s (if non-NULL; requires rotate).  cols % 256 == 0 when rotating,
+ * cols <= 8192. */
+int anima_layernorm_mod(anima_ctx* ctx, const float* x, const float* mod, int64_t shift_off,
+                        int64_t scale_off, int64_t rows, int cols, float eps, int rotate, float* y,
+                        int8_t* q, float* s);
+
+#define ANIMA_EW_SILU_MUL 0 /* y = silu(a) * b */
+#define ANIMA_EW_ADD 1      /* y = a + b */
+#define ANIMA_EW_SILU 2     /* y = silu(a) */
+#define ANIMA_EW_COPY 3     /* y = a */
+/* ops.elementwise (app/gpu/ops.js:154-160; kernels.js:391-413). */
+int anima_elementwise(anima_ctx* ctx, int op, const float* a, const float* b, float* y, int64_t n);
+/* ops.zero (app/gpu/ops.js:89-93; kernels.js:415-423). */
+int anima_zero(anima_ctx* ctx, float* y, int64_t n);
+
+/* ---------------------------------------------------------------- linears */
+
+#define ANIMA_W_BF16 0 /* bf16 [N][K]; fp32 activations, fp32 accumulation (gemm.js:108-128) */
+#define ANIMA_W_I8 1   /* int8 [N][K] + weight_scale [N] (comfy_quant int8_tensorwise+convrot) */
+#define ANIMA_W_W4 2   /* 4-bit codes [N][K/2] (low nibble = even k) + s_rel e4m3 [N][K/16] +
+                          s_channel [N] + codebook [16] (comfy_quant asym_w4a8_int8+convrot) */
+#define ANIMA_ACT_NONE 0
+#define ANIMA_ACT_GELU 1 /* erf GELU (kernels.js:9-20) */
+#define ANIMA_ACT_SILU 2
+#define ANIMA_EPI_STORE 0 /* out = r */
+#define ANIMA_EPI_RESID 1 /* out += r */
+#define ANIMA_EPI_GATED 2 /* out = fma(gate[gate_off + n], r, out) */
+
+/* Linear weight object of app/weights.js:1-4, 118-147 (device pointers). */
+typedef struct {
+  int kind, N, K;
+  const void* w;
+  const float* scale;      /* i8: weight_scale [N]; w4: weight_s_channel [N] */
+  const uint8_t* srel;     /* w4: [N][K/16] fp8 e4m3 */
+  const float* codebook;   /* w4: [16] */
+  const float* bias;       /* [N] or NULL */
+} anima_weight;
+
+typedef struct {
+  int64_t M;
+  const anima_weight* W;
+  /* fp32 input x[M][ldx].  For i8/w4 weights the input must be ConvRot-rotated: x_rotated = 1
+   * means x already is (ops.linear's opts.xr), 0 rotates it here (ops.js:52-54). */
+  const float* x;
+  int64_t ldx;
+  int x_rotated;
+  /* i8/w4 only: pre-quantized rotated activations (anima_quant_rows / anima_layernorm_mod);
+   * when set, x is ignored. */
+  const int8_t* xq;
+  const float* xs;
+  float* out;
+  int64_t ldc;   /* 0 -> N */
+  float alpha;   /* 0 -> 1 */
+  int act;       /* ANIMA_ACT_* */
+  int epilogue;  /* ANIMA_EPI_* */
+  const float* gate;
+  int64_t gate_off;
+  int32_t* acc_out; /* i8/w4 only, optional: the raw int32 accumulators [M][N] */
+} anima_linear_desc;
+
+/* ops.linear (app/gpu/ops.js:48-66) -> matmulShader (gemm.js:166-280):
+ * r = alpha * (x @ dec(W)^T); i8/w4: dec is the int8 grid and r is scaled by s_x[m] * s_w[n]
+ * (W8A8: activations quantized per token after the ConvRot rotation); then + bias[n], act,
+ * and the store / residual / gated-residual epilogue of gemm.js:186-192.
+ * i8/w4 need K % 64 == 0 (and K <= 8192 when x is quantized here). */
+int anima_linear(anima_ctx* ctx, const anima_linear_desc* desc);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,249 @@
+"""GPU parity of the quantized-linear side of the attention sublayer through the C ABI:
+ConvRot Hadamard, per-token int8 quantization, LayerNorm+adaLN(+Hadamard)(+int8), elementwise
+ops, and the int8 / W4A8 MFMA GEMMs with the reference's epilogues.
+
+Bars: Hadamard, quantization and LayerNorm are bit-exact against the oracle; GEMM int32
+accumulators are bit-exact (sampled rows against the oracle, every row and column through exact
+int64 checksums); the fp32 epilogue (acc * s_x * s_w, bias, gate) is bit-exact; GELU/SiLU
+outputs within 1e-6 relative (device expf).  W8A8 against the reference's W8A32 semantics
+(fp32 activations) is reported and bounded by 3e-2 rel L2 (activation quantization noise).
+"""
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from helpers import amd, rel_l2, report
+
+pytestmark = pytest.mark.gpu
+
+FIXED_LUT = np.array([-0.980602, -0.794529, -0.638165, -0.500986, -0.377321, -0.263187, -0.155210, -0.050720,
+                      0.052541, 0.156985, 0.265284, 0.379533, 0.502636, 0.638953, 0.794876, 0.980671], np.float32)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = amd().Context(0)
+    yield c
+    c.close()
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def int8_weight(seed, N, K):
+    """clip(round(40 N(0,1)), +-127) int8 weights, s_w = U(0.5, 1.5) / (127 sqrt(K))."""
+    w = np.clip(np.rint(40 * orc.randn(seed, N * K)), -127, 127).astype(np.int8).reshape(N, K)
+    rng = np.random.default_rng(seed)
+    s = (rng.uniform(0.5, 1.5, N) / (127 * np.sqrt(K))).astype(np.float32)
+    return w, s
+
+
+def w4_weight(seed, N, K):
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(0, 256, size=(N, K // 2), dtype=np.uint8)
+    srel = rng.integers(0x60, 0x70, size=(N, K // 16), dtype=np.uint8)  # e4m3 values 32..120
+    s = (rng.uniform(0.5, 1.5, N) / (127 * np.sqrt(K))).astype(np.float32)
+    return codes, srel, s
+
+
+# ------------------------------------------------------------------ row kernels
+
+def test_hadamard_and_quant_bit_exact(ctx):
+    case("hadamard / quant_rows M=512 K=2048 and K=8192")
+    x = orc.randn(41, 512 * 2048).reshape(512, 2048) * 3
+    dx, dy = ctx.upload(x), ctx.empty(x.shape)
+    ctx.hadamard(dx, dy, x.size)
+    xr = orc.hadamard256(x)
+    assert np.array_equal(dy.numpy(), xr)
+    for rotate, src in ((1, x), (0, xr)):
+        dq, ds = ctx.empty((512, 2048), np.int8), ctx.empty(512)
+        ctx.quant_rows(ctx.upload(src), 512, 2048, rotate, dq, ds)
+        q, s = orc.token_quant(xr)
+        assert np.array_equal(ds.numpy(), s) and np.array_equal(dq.numpy(), q)
+    x8 = orc.randn(42, 64 * 8192).reshape(64, 8192)
+    x8[3] = 0.0  # all-zero row: s = 0, q = 0
+    dq, ds = ctx.empty((64, 8192), np.int8), ctx.empty(64)
+    ctx.quant_rows(ctx.upload(x8), 64, 8192, 1, dq, ds)
+    q, s = orc.token_quant(orc.hadamard256(x8))
+    assert np.array_equal(ds.numpy(), s) and np.array_equal(dq.numpy(), q)
+    assert s[3] == 0 and not q[3].any()
+
+
+@pytest.mark.parametrize("cols,rotate", [(2048, True), (2048, False), (1024, True)])
+def test_layernorm_mod_bit_exact(ctx, cols, rotate):
+    case(f"layernorm_mod rows=300 cols={cols} rotate={rotate}")
+    rows = 300
+    x = (orc.randn(43, rows * cols).reshape(rows, cols) * 2 + 0.5).astype(np.float32)
+    mod = (0.1 * orc.randn(44, 3 * cols)).astype(np.float32)
+    dx, dm, dy = ctx.upload(x), ctx.upload(mod), ctx.empty(x.shape)
+    dq = ctx.empty((rows, cols), np.int8) if rotate else None
+    ds = ctx.empty(rows) if rotate else None
+    ctx.layernorm_mod(dx, dm, 0, cols, rows, cols, rotate=rotate, y=dy, q=dq, s=ds)
+    ref = orc.layernorm_mod(x, mod, 0, cols, cols, rotate=rotate)
+    got = dy.numpy()
+    assert np.array_equal(got, ref), report("layernorm_mod", got, ref)
+    if rotate:
+        q, s = orc.token_quant(ref)
+        assert np.array_equal(ds.numpy(), s) and np.array_equal(dq.numpy(), q)
+
+
+def test_elementwise_and_zero(ctx):
+    case("elementwise silu_mul/add/silu/copy, zero")
+    n = 10007
+    a = orc.randn(45, n) * 4
+    b = orc.randn(46, n)
+    da, db, dy = ctx.upload(a), ctx.upload(b), ctx.empty(n)
+    silu = a.astype(np.float64) / (1 + np.exp(-a.astype(np.float64)))
+    for op, ref in (("silu_mul", silu * b), ("add", a.astype(np.float64) + b), ("silu", silu), ("copy", a)):
+        ctx.elementwise(op, da, db, dy, n)
+        got = dy.numpy()
+        assert np.allclose(got, ref, rtol=1e-6, atol=1e-6), op
+    ctx.zero(dy, n)
+    assert not dy.numpy().any()
+
+
+# ------------------------------------------------------------------ int8 / W4A8 GEMM
+
+def checksums_ok(qx, qw_int8, acc):
+    """Exact int64 row and column sums of acc = qx @ qw^T."""
+    qx64, qw64 = qx.astype(np.int64), qw_int8.astype(np.int64)
+    acc64 = acc.astype(np.int64)
+    rows = qx64 @ qw64.sum(0)
+    cols = qw64 @ qx64.sum(0)
+    return np.array_equal(acc64.sum(1), rows) and np.array_equal(acc64.sum(0), cols)
+
+
+@pytest.mark.parametrize("kind", ["i8", "w4"])
+def test_qkv_projection_full_size(ctx, kind):
+    """x [2,4096,2048] -> ConvRot + per-token int8 -> QKV 2048 -> 6144 (one stacked GEMM)."""
+    case(f"QKV projection M=8192 N=6144 K=2048 {kind}")
+    m = amd()
+    M, K, N = 8192, 2048, 6144
+    x = orc.randn(51, M * K).reshape(M, K)
+    dx = ctx.upload(x)
+    dq, ds = ctx.empty((M, K), np.int8), ctx.empty(M)
+    ctx.quant_rows(dx, M, K, 1, dq, ds)
+    xr = orc.hadamard256(x)
+    qx, sx = orc.token_quant(xr)
+    assert np.array_equal(dq.numpy(), qx) and np.array_equal(ds.numpy(), sx)
+    if kind == "i8":
+        qw, sw = int8_weight(52, N, K)
+        dw, dsw = ctx.upload(qw), ctx.upload(sw)
+        W = m.weight(m.W_I8, N, K, dw, scale=dsw)
+        qw_grid = qw
+    else:
+        codes, srel, sw = w4_weight(53, N, K)
+        dw, dsw, dsr, dcb = ctx.upload(codes), ctx.upload(sw), ctx.upload(srel), ctx.upload(FIXED_LUT)
+        W = m.weight(m.W_W4, N, K, dw, scale=dsw, srel=dsr, codebook=dcb)
+        qw_grid = orc.w4_decode(codes, srel, FIXED_LUT, N, K)
+    dout, dacc = ctx.empty((M, N)), ctx.empty((M, N), np.int32)
+    ctx.linear(W, M, dout, xq=dq, xs=ds, acc_out=dacc)
+    acc = dacc.numpy()
+    out = dout.numpy()
+    assert checksums_ok(qx, qw_grid, acc), "int32 accumulator checksums"
+    rows = np.unique(np.concatenate([np.arange(0, 8), np.random.default_rng(0).choice(M, 24, replace=False), [M - 1]]))
+    ref_acc = orc.gemm_i8(qx[rows], qw_grid)
+    assert np.array_equal(acc[rows], ref_acc)
+    assert np.array_equal(out[rows], orc.linear_epilogue(ref_acc, sx[rows], sw))
+    # the reference's semantics: fp32 rotated activations x int grid weights, scale in the epilogue
+    w8a32 = (xr[rows].astype(np.float64) @ qw_grid.astype(np.float64).T) * sw
+    r, _ = report(f"{kind} W8A8 vs W8A32 (reference semantics)", out[rows], w8a32)
+    assert r < 3e-2
+    # the same GEMM from the fp32 input (rotation + quantization inside anima_linear)
+    dout2 = ctx.empty((M, N))
+    ctx.linear(W, M, dout2, x=dx, x_rotated=False)
+    assert np.array_equal(dout2.numpy(), out)
+    for b in (dx, dq, ds, dout, dacc, dout2, dw, dsw):
+        b.release()
+
+
+@pytest.mark.parametrize("kind", ["i8", "w4"])
+def test_out_projection_gated_epilogue(ctx, kind):
+    """Out projection 2048 -> 2048 with the gated residual into x (dit.js:289, gemm.js:192)."""
+    case(f"out projection gated residual M=1000 {kind}")
+    m = amd()
+    M, K, N = 1000, 2048, 2048
+    a = orc.randn(61, M * K).reshape(M, K)
+    resid = orc.randn(62, M * N).reshape(M, N)
+    mod = orc.randn(63, 3 * N).astype(np.float32)
+    qx, sx = orc.token_quant(orc.hadamard256(a))
+    if kind == "i8":
+        qw, sw = int8_weight(64, N, K)
+        dw = ctx.upload(qw)
+        W = m.weight(m.W_I8, N, K, dw, scale=ctx.upload(sw), bias=ctx.upload(0.1 * orc.randn(65, N)))
+        grid = qw
+    else:
+        codes, srel, sw = w4_weight(66, N, K)
+        W = m.weight(m.W_W4, N, K, ctx.upload(codes), scale=ctx.upload(sw), srel=ctx.upload(srel),
+                     codebook=ctx.upload(FIXED_LUT), bias=ctx.upload(0.1 * orc.randn(65, N)))
+        grid = orc.w4_decode(codes, srel, FIXED_LUT, N, K)
+    bias = (0.1 * orc.randn(65, N)).astype(np.float32)
+    dout = ctx.upload(resid)
+    ctx.linear(W, M, dout, x=ctx.upload(a), x_rotated=False, epilogue=m.EPI_GATED, gate=ctx.upload(mod),
+               gate_off=2 * N)
+    ref = orc.linear_epilogue(orc.gemm_i8(qx, grid), sx, sw, bias=bias, epi=2, gate=mod, g_off=2 * N, c=resid)
+    got = dout.numpy()
+    assert np.array_equal(got, ref), report("gated", got, ref)
+    # plain residual
+    dout = ctx.upload(resid)
+    ctx.linear(W, M, dout, xq=ctx.upload(qx), xs=ctx.upload(sx), epilogue=m.EPI_RESID)
+    assert np.array_equal(dout.numpy(), orc.linear_epilogue(orc.gemm_i8(qx, grid), sx, sw, bias=bias, epi=1, c=resid))
+
+
+@pytest.mark.parametrize("act", ["gelu", "silu"])
+def test_mlp1_activation_epilogue(ctx, act):
+    case(f"mlp1 2048 -> 8192 {act} M=200 and mlp2 8192 -> 2048")
+    m = amd()
+    M, K, N = 200, 2048, 8192
+    x = orc.randn(71, M * K).reshape(M, K)
+    qw, sw = int8_weight(72, N, K)
+    W = m.weight(m.W_I8, N, K, ctx.upload(qw), scale=ctx.upload(sw))
+    dh = ctx.empty((M, N))
+    ctx.linear(W, M, dh, x=ctx.upload(x), x_rotated=False, act=act)
+    qx, sx = orc.token_quant(orc.hadamard256(x))
+    ref = orc.linear_epilogue(orc.gemm_i8(qx, qw), sx, sw, act=1 if act == "gelu" else 2)
+    got = dh.numpy()
+    assert rel_l2(got, ref) < 1e-6 and np.max(np.abs(got - ref)) <= 1e-6 * np.max(np.abs(ref))
+    # mlp2: K = 8192 input rotated + quantized inside the op
+    qw2, sw2 = int8_weight(73, 2048, N)
+    W2 = m.weight(m.W_I8, 2048, N, ctx.upload(qw2), scale=ctx.upload(sw2))
+    dy = ctx.empty((M, 2048))
+    ctx.linear(W2, M, dy, x=dh, x_rotated=False)
+    qh, sh = orc.token_quant(orc.hadamard256(got))
+    assert np.array_equal(dy.numpy(), orc.linear_epilogue(orc.gemm_i8(qh, qw2), sh, sw2))
+
+
+def test_bf16_weight_linears(ctx):
+    case("bf16 weights: x_embedder K=68, GEMV M=1")
+    m = amd()
+    for (M, K, N, act) in ((300, 68, 2048, "none"), (1, 2048, 6144, "silu"), (97, 2048, 64, "none")):
+        x = orc.randn(81 + K, M * K).reshape(M, K)
+        w32 = orc.bf16_round(0.05 * orc.randn(82 + N, N * K)).reshape(N, K)
+        wb = (w32.view(np.uint32) >> 16).astype(np.uint16)
+        bias = orc.randn(83, N).astype(np.float32)
+        W = m.weight(m.W_BF16, N, K, ctx.upload(wb), bias=ctx.upload(bias))
+        dy = ctx.empty((M, N))
+        ctx.linear(W, M, dy, x=ctx.upload(x), act=act)
+        ref = x.astype(np.float64) @ w32.astype(np.float64).T + bias
+        if act == "silu":
+            ref = ref / (1 + np.exp(-ref))
+        r, _ = report(f"bf16 M={M} K={K} N={N}", dy.numpy(), ref)
+        assert r < 1e-6
+
+
+def test_linear_rejects_bad_arguments(ctx):
+    case("linear argument validation")
+    m = amd()
+    buf = ctx.empty(1 << 16)
+    W = m.weight(m.W_I8, 64, 100, buf, scale=buf)
+    with pytest.raises(m.AnimaError) as e:
+        ctx.linear(W, 4, buf, xq=buf, xs=buf)
+    assert e.value.code == -1  # K % 64
+    W = m.weight(7, 64, 128, buf, scale=buf)
+    with pytest.raises(m.AnimaError):
+        ctx.linear(W, 4, buf, xq=buf, xs=buf)
+    W = m.weight(m.W_I8, 64, 128, buf, scale=buf)
+    with pytest.raises(m.AnimaError):
+        ctx.linear(W, 4, buf, xq=buf, xs=buf, epilogue=m.EPI_GATED)  # no gate
