@@ -302,6 +302,59 @@ int zero_launch(anima_ctx* c, float* y, int64_t n) {
   return lc.end();
 }
 
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  uint64_t z = x + 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void fill_kernel(void* dst, int64_t n, int kind, uint64_t seed, float lo, float hi,
+                                                   int64_t imul) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const uint64_t h = splitmix64(seed * 0xD1B54A32D192ED03ull + (uint64_t)i);
+    switch (kind) {
+      case ANIMA_FILL_U8: {
+        const int64_t a = (int64_t)lo, b = (int64_t)hi;
+        ((uint8_t*)dst)[i] = (uint8_t)(a + (int64_t)(h % (uint64_t)(b - a + 1)));
+        break;
+      }
+      case ANIMA_FILL_I8N: {
+        const int64_t sum = (int64_t)(h & 0xff) + (int64_t)((h >> 8) & 0xff) + (int64_t)((h >> 16) & 0xff) +
+                            (int64_t)((h >> 24) & 0xff);
+        int64_t v = ((sum - 510) * imul) >> 12;
+        v = v < -127 ? -127 : (v > 127 ? 127 : v);
+        ((int8_t*)dst)[i] = (int8_t)v;
+        break;
+      }
+      case ANIMA_FILL_F32N: {
+        const float u = (float)(h & 0xffff) * (1.0f / 65536.0f) + (float)((h >> 16) & 0xffff) * (1.0f / 65536.0f) +
+                        (float)((h >> 32) & 0xffff) * (1.0f / 65536.0f) + (float)((h >> 48) & 0xffff) * (1.0f / 65536.0f);
+        ((float*)dst)[i] = (u - 2.0f) * 1.7320508f * lo + hi;
+        break;
+      }
+      default: {
+        const float u = (float)(h >> 40) * (1.0f / 16777216.0f);
+        const float v = lo + (hi - lo) * u;
+        if (kind == ANIMA_FILL_F32) ((float*)dst)[i] = v;
+        else ((bf16*)dst)[i] = to_bf16(v);
+        break;
+      }
+    }
+  }
+}
+
+int fill_random_launch(anima_ctx* c, void* dst, int64_t n, int kind, uint64_t seed, float lo, float hi) {
+  if (!dst || n < 0) return fail(c, ANIMA_E_ARG, "anima_fill_random: bad arguments");
+  if (kind < ANIMA_FILL_U8 || kind > ANIMA_FILL_F32N) return fail(c, ANIMA_E_ARG, "anima_fill_random: unknown kind %d", kind);
+  if (kind == ANIMA_FILL_U8 && !(lo >= 0 && hi <= 255 && lo <= hi)) return fail(c, ANIMA_E_ARG, "anima_fill_random: u8 range [%g,%g]", lo, hi);
+  if (n == 0) return ANIMA_OK;
+  const int64_t imul = (int64_t)llrint((double)lo * 4096.0 / 147.8017);
+  Launch lc(c, "fill_random", 0.0, (double)n);
+  hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n)), dim3(256), 0, c->stream, dst, n, kind, seed, lo, hi, imul);
+  return lc.end();
+}
+
 int qk_norm_rope_launch(anima_ctx* c, float* qkv, int64_t L, int H, int D, int64_t ld, const float* qn,
                         const float* kn, const float* cs, int64_t sin_off, float eps) {
   if (!qkv || !qn || !kn || !cs) return fail(c, ANIMA_E_ARG, "anima_qk_norm_rope: null pointer");

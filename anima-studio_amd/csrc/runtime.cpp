@@ -389,6 +389,11 @@ int anima_zero(anima_ctx* c, float* y, int64_t n) {
   return zero_launch(c, y, n);
 }
 
+int anima_fill_random(anima_ctx* c, void* dst, int64_t n, int kind, uint64_t seed, float lo, float hi) {
+  CHECK_CTX(c);
+  return fill_random_launch(c, dst, n, kind, seed, lo, hi);
+}
+
 int anima_linear(anima_ctx* c, const anima_linear_desc* d) {
   CHECK_CTX(c);
   if (!d) return fail(c, ANIMA_E_ARG, "anima_linear: null descriptor");

@@ -1,0 +1,479 @@
+/*
+ * N-API addon over the C ABI of libanima.so (include/anima.h).
+ *
+ * The JS side (gpu.mjs / ops.mjs) keeps the op interface of the reference's app/gpu/ops.js and
+ * app/gpu/device.js; this file only marshals arguments.  Device pointers cross the boundary as
+ * JS Numbers (user-space virtual addresses are below 2^53), the context as an external.
+ * Every negative status becomes a thrown Error carrying anima_last_error().
+ */
+#include <node_api.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/anima.h"
+
+#define NAPI_CALL(env, call)                                    \
+  do {                                                          \
+    if ((call) != napi_ok) {                                    \
+      napi_throw_error((env), NULL, "N-API call failed: " #call); \
+      return NULL;                                              \
+    }                                                           \
+  } while (0)
+
+static napi_value throw_status(napi_env env, anima_ctx* c, int rc) {
+  char msg[1200];
+  snprintf(msg, sizeof msg, "anima error %d: %s", rc, anima_last_error(c));
+  napi_throw_error(env, NULL, msg);
+  return NULL;
+}
+
+#define CHECK_RC(env, c, expr)                   \
+  do {                                           \
+    int rc_ = (expr);                            \
+    if (rc_ != ANIMA_OK) return throw_status(env, c, rc_); \
+  } while (0)
+
+static int get_args(napi_env env, napi_callback_info info, size_t want, napi_value* argv) {
+  size_t argc = want;
+  if (napi_get_cb_info(env, info, &argc, argv, NULL, NULL) != napi_ok) return -1;
+  for (size_t i = argc; i < want; i++) napi_get_undefined(env, &argv[i]);
+  return (int)argc;
+}
+
+static int is_nullish(napi_env env, napi_value v) {
+  napi_valuetype t;
+  if (napi_typeof(env, v, &t) != napi_ok) return 1;
+  return t == napi_undefined || t == napi_null;
+}
+
+static double num(napi_env env, napi_value v) {
+  double d = 0;
+  if (is_nullish(env, v)) return 0;
+  napi_get_value_double(env, v, &d);
+  return d;
+}
+
+static int64_t i64(napi_env env, napi_value v) { return (int64_t)num(env, v); }
+static void* ptr(napi_env env, napi_value v) { return (void*)(uintptr_t)num(env, v); }
+
+static napi_value prop(napi_env env, napi_value obj, const char* name) {
+  napi_value v;
+  bool has = false;
+  napi_has_named_property(env, obj, name, &has);
+  if (!has) {
+    napi_get_undefined(env, &v);
+    return v;
+  }
+  napi_get_named_property(env, obj, name, &v);
+  return v;
+}
+
+static double pnum(napi_env env, napi_value obj, const char* name) { return num(env, prop(env, obj, name)); }
+static void* pptr(napi_env env, napi_value obj, const char* name) { return ptr(env, prop(env, obj, name)); }
+
+static anima_ctx* ctx_of(napi_env env, napi_value v) {
+  void* p = NULL;
+  if (napi_get_value_external(env, v, &p) != napi_ok) return NULL;
+  return (anima_ctx*)p;
+}
+
+static napi_value make_num(napi_env env, double d) {
+  napi_value v;
+  napi_create_double(env, d, &v);
+  return v;
+}
+
+/* typed array -> (data, byte length) */
+static int typed(napi_env env, napi_value v, void** data, size_t* bytes) {
+  napi_typedarray_type type;
+  size_t len, off;
+  napi_value ab;
+  void* d;
+  if (napi_get_typedarray_info(env, v, &type, &len, &d, &ab, &off) != napi_ok) return -1;
+  size_t es = 1;
+  switch (type) {
+    case napi_int16_array: case napi_uint16_array: es = 2; break;
+    case napi_int32_array: case napi_uint32_array: case napi_float32_array: es = 4; break;
+    case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: es = 8; break;
+    default: es = 1;
+  }
+  *data = d;
+  *bytes = len * es;
+  return 0;
+}
+
+/* ------------------------------------------------------------------ runtime */
+
+static void ctx_finalize(napi_env env, void* data, void* hint) {
+  (void)env;
+  (void)hint;
+  (void)data; /* destroyed explicitly by destroy(); a leaked context is reclaimed at exit */
+}
+
+static napi_value js_init(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  anima_ctx* c = NULL;
+  CHECK_RC(env, NULL, anima_init((int)num(env, argv[0]), &c));
+  napi_value ext;
+  NAPI_CALL(env, napi_create_external(env, c, ctx_finalize, NULL, &ext));
+  return ext;
+}
+
+static napi_value js_destroy(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  anima_destroy(ctx_of(env, argv[0]));
+  return NULL;
+}
+
+static napi_value js_sync(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  CHECK_RC(env, c, anima_sync(c));
+  return NULL;
+}
+
+static napi_value js_alloc(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  void* p = NULL;
+  CHECK_RC(env, c, anima_alloc(c, (size_t)num(env, argv[1]), &p));
+  return make_num(env, (double)(uintptr_t)p);
+}
+
+static napi_value js_free(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  CHECK_RC(env, c, anima_free(c, ptr(env, argv[1])));
+  return NULL;
+}
+
+static napi_value js_trim(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  CHECK_RC(env, c, anima_pool_trim(c));
+  return NULL;
+}
+
+static napi_value js_mem_stats(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  uint64_t a = 0, p = 0, q = 0;
+  CHECK_RC(env, c, anima_mem_stats(c, &a, &p, &q));
+  napi_value o;
+  NAPI_CALL(env, napi_create_object(env, &o));
+  napi_set_named_property(env, o, "allocated", make_num(env, (double)a));
+  napi_set_named_property(env, o, "peak", make_num(env, (double)p));
+  napi_set_named_property(env, o, "pooled", make_num(env, (double)q));
+  return o;
+}
+
+/* h2d(ctx, dst, typedArray) */
+static napi_value js_h2d(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  get_args(env, info, 3, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  void* data;
+  size_t bytes;
+  if (typed(env, argv[2], &data, &bytes)) {
+    napi_throw_type_error(env, NULL, "h2d: expected a typed array");
+    return NULL;
+  }
+  CHECK_RC(env, c, anima_h2d(c, ptr(env, argv[1]), data, bytes));
+  return NULL;
+}
+
+/* d2h(ctx, src, typedArray) fills the typed array */
+static napi_value js_d2h(napi_env env, napi_callback_info info) {
+  napi_value argv[3];
+  get_args(env, info, 3, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  void* data;
+  size_t bytes;
+  if (typed(env, argv[2], &data, &bytes)) {
+    napi_throw_type_error(env, NULL, "d2h: expected a typed array");
+    return NULL;
+  }
+  CHECK_RC(env, c, anima_d2h(c, data, ptr(env, argv[1]), bytes));
+  return NULL;
+}
+
+static napi_value js_d2d(napi_env env, napi_callback_info info) {
+  napi_value argv[4];
+  get_args(env, info, 4, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  CHECK_RC(env, c, anima_d2d(c, ptr(env, argv[1]), ptr(env, argv[2]), (size_t)num(env, argv[3])));
+  return NULL;
+}
+
+static napi_value js_profile_enable(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  bool on = false;
+  napi_get_value_bool(env, argv[1], &on);
+  CHECK_RC(env, c, anima_profile_enable(c, on ? 1 : 0));
+  return NULL;
+}
+
+static napi_value js_profile_reset(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  CHECK_RC(env, c, anima_profile_reset(c));
+  return NULL;
+}
+
+static napi_value js_profile_report(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  static char buf[1 << 17];
+  CHECK_RC(env, c, anima_profile_report(c, buf, sizeof buf));
+  napi_value s;
+  NAPI_CALL(env, napi_create_string_utf8(env, buf, NAPI_AUTO_LENGTH, &s));
+  return s;
+}
+
+static napi_value js_timer_start(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  CHECK_RC(env, c, anima_timer_start(c));
+  return NULL;
+}
+
+static napi_value js_timer_stop(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  float ms = 0;
+  CHECK_RC(env, c, anima_timer_stop(c, &ms));
+  return make_num(env, ms);
+}
+
+/* ------------------------------------------------------------------ ops */
+
+/* attention(ctx, desc) -- desc mirrors anima_attn_desc (pointers as Numbers, kvLen array) */
+static napi_value js_attention(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  napi_value o = argv[1];
+  anima_attn_desc d;
+  memset(&d, 0, sizeof d);
+  d.B = (int)pnum(env, o, "B");
+  d.Lq = (int)pnum(env, o, "Lq");
+  d.Lk = (int)pnum(env, o, "Lk");
+  d.H = (int)pnum(env, o, "H");
+  d.D = (int)pnum(env, o, "D");
+  d.group = (int)pnum(env, o, "group");
+  d.q = (const float*)pptr(env, o, "q");
+  d.k = (const float*)pptr(env, o, "k");
+  d.v = (const float*)pptr(env, o, "v");
+  d.o = (float*)pptr(env, o, "o");
+  d.ldq = (int64_t)pnum(env, o, "ldq");
+  d.ldk = (int64_t)pnum(env, o, "ldk");
+  d.ldv = (int64_t)pnum(env, o, "ldv");
+  d.ldo = (int64_t)pnum(env, o, "ldo");
+  d.q_off = (int64_t)pnum(env, o, "qOff");
+  d.k_off = (int64_t)pnum(env, o, "kOff");
+  d.v_off = (int64_t)pnum(env, o, "vOff");
+  d.o_off = (int64_t)pnum(env, o, "oOff");
+  d.q_bstride = (int64_t)pnum(env, o, "qBatch");
+  d.k_bstride = (int64_t)pnum(env, o, "kBatch");
+  d.v_bstride = (int64_t)pnum(env, o, "vBatch");
+  d.o_bstride = (int64_t)pnum(env, o, "oBatch");
+  d.scale = (float)pnum(env, o, "scale");
+  d.precision = (int)pnum(env, o, "precision");
+  d.q_norm = (const float*)pptr(env, o, "qNorm");
+  d.k_norm = (const float*)pptr(env, o, "kNorm");
+  d.rope_cs = (const float*)pptr(env, o, "cs");
+  d.rope_sin_off = (int64_t)pnum(env, o, "sinOff");
+  d.eps = (float)pnum(env, o, "eps");
+  d.causal = (int)pnum(env, o, "causal");
+  int kv[64];
+  napi_value kvl = prop(env, o, "kvLen");
+  if (!is_nullish(env, kvl)) {
+    uint32_t n = 0;
+    napi_get_array_length(env, kvl, &n);
+    if (n > 64 || (int)n < d.B) {
+      napi_throw_range_error(env, NULL, "attention: kvLen must hold B (<= 64) entries");
+      return NULL;
+    }
+    for (uint32_t i = 0; i < n; i++) {
+      napi_value e;
+      napi_get_element(env, kvl, i, &e);
+      kv[i] = (int)num(env, e);
+    }
+    d.kv_len = kv;
+  }
+  CHECK_RC(env, c, anima_attention(c, &d));
+  return NULL;
+}
+
+/* qkNormRope(ctx, qkv, L, H, D, ld, qn, kn, cs, sinOff, eps) */
+static napi_value js_qk_norm_rope(napi_env env, napi_callback_info info) {
+  napi_value a[11];
+  get_args(env, info, 11, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_qk_norm_rope(c, (float*)ptr(env, a[1]), i64(env, a[2]), (int)num(env, a[3]), (int)num(env, a[4]),
+                                      i64(env, a[5]), (const float*)ptr(env, a[6]), (const float*)ptr(env, a[7]),
+                                      (const float*)ptr(env, a[8]), i64(env, a[9]), (float)num(env, a[10])));
+  return NULL;
+}
+
+/* rmsnorm(ctx, x, w, y, rows, cols, eps) */
+static napi_value js_rmsnorm(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  get_args(env, info, 7, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_rmsnorm(c, (const float*)ptr(env, a[1]), (const float*)ptr(env, a[2]), (float*)ptr(env, a[3]),
+                                 i64(env, a[4]), (int)num(env, a[5]), (float)num(env, a[6])));
+  return NULL;
+}
+
+/* rope(ctx, x, cs, L, H, D, sinOff, rowStride, colOff) */
+static napi_value js_rope(napi_env env, napi_callback_info info) {
+  napi_value a[9];
+  get_args(env, info, 9, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_rope(c, (float*)ptr(env, a[1]), (const float*)ptr(env, a[2]), i64(env, a[3]), (int)num(env, a[4]),
+                              (int)num(env, a[5]), i64(env, a[6]), i64(env, a[7]), i64(env, a[8])));
+  return NULL;
+}
+
+/* hadamard(ctx, x, y, n) */
+static napi_value js_hadamard(napi_env env, napi_callback_info info) {
+  napi_value a[4];
+  get_args(env, info, 4, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_hadamard(c, (const float*)ptr(env, a[1]), (float*)ptr(env, a[2]), i64(env, a[3])));
+  return NULL;
+}
+
+/* quantRows(ctx, x, M, K, rotate, q, s) */
+static napi_value js_quant_rows(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  get_args(env, info, 7, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_quant_rows(c, (const float*)ptr(env, a[1]), i64(env, a[2]), (int)num(env, a[3]),
+                                    (int)num(env, a[4]), (int8_t*)ptr(env, a[5]), (float*)ptr(env, a[6])));
+  return NULL;
+}
+
+/* layernormMod(ctx, x, mod, shiftOff, scaleOff, rows, cols, eps, rotate, y, q, s) */
+static napi_value js_layernorm_mod(napi_env env, napi_callback_info info) {
+  napi_value a[12];
+  get_args(env, info, 12, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_layernorm_mod(c, (const float*)ptr(env, a[1]), (const float*)ptr(env, a[2]), i64(env, a[3]),
+                                       i64(env, a[4]), i64(env, a[5]), (int)num(env, a[6]), (float)num(env, a[7]),
+                                       (int)num(env, a[8]), (float*)ptr(env, a[9]), (int8_t*)ptr(env, a[10]),
+                                       (float*)ptr(env, a[11])));
+  return NULL;
+}
+
+/* elementwise(ctx, op, a, b, y, n) */
+static napi_value js_elementwise(napi_env env, napi_callback_info info) {
+  napi_value a[6];
+  get_args(env, info, 6, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_elementwise(c, (int)num(env, a[1]), (const float*)ptr(env, a[2]), (const float*)ptr(env, a[3]),
+                                     (float*)ptr(env, a[4]), i64(env, a[5])));
+  return NULL;
+}
+
+/* zero(ctx, y, n) */
+static napi_value js_zero(napi_env env, napi_callback_info info) {
+  napi_value a[3];
+  get_args(env, info, 3, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_zero(c, (float*)ptr(env, a[1]), i64(env, a[2])));
+  return NULL;
+}
+
+/* fillRandom(ctx, dst, n, kind, seed, lo, hi) -- seed < 2^53 */
+static napi_value js_fill_random(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  get_args(env, info, 7, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_fill_random(c, ptr(env, a[1]), i64(env, a[2]), (int)num(env, a[3]), (uint64_t)num(env, a[4]),
+                                     (float)num(env, a[5]), (float)num(env, a[6])));
+  return NULL;
+}
+
+/* linear(ctx, W, desc): W = {kind, N, K, w, scale, srel, codebook, bias}, desc mirrors
+ * anima_linear_desc (x, ldx, xRotated, xq, xs, out, ldc, alpha, act, epilogue, gate, gOff, accOut) */
+static napi_value js_linear(napi_env env, napi_callback_info info) {
+  napi_value a[3];
+  get_args(env, info, 3, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  napi_value wo = a[1], o = a[2];
+  anima_weight w;
+  memset(&w, 0, sizeof w);
+  w.kind = (int)pnum(env, wo, "kindId");
+  w.N = (int)pnum(env, wo, "N");
+  w.K = (int)pnum(env, wo, "K");
+  w.w = pptr(env, wo, "buf");
+  w.scale = (const float*)pptr(env, wo, "scale");
+  w.srel = (const uint8_t*)pptr(env, wo, "srel");
+  w.codebook = (const float*)pptr(env, wo, "codebook");
+  w.bias = (const float*)pptr(env, wo, "bias");
+  anima_linear_desc d;
+  memset(&d, 0, sizeof d);
+  d.M = (int64_t)pnum(env, o, "M");
+  d.W = &w;
+  d.x = (const float*)pptr(env, o, "x");
+  d.ldx = (int64_t)pnum(env, o, "ldx");
+  d.x_rotated = (int)pnum(env, o, "xRotated");
+  d.xq = (const int8_t*)pptr(env, o, "xq");
+  d.xs = (const float*)pptr(env, o, "xs");
+  d.out = (float*)pptr(env, o, "out");
+  d.ldc = (int64_t)pnum(env, o, "ldc");
+  d.alpha = (float)pnum(env, o, "alpha");
+  d.act = (int)pnum(env, o, "act");
+  d.epilogue = (int)pnum(env, o, "epilogue");
+  d.gate = (const float*)pptr(env, o, "gate");
+  d.gate_off = (int64_t)pnum(env, o, "gOff");
+  d.acc_out = (int32_t*)pptr(env, o, "accOut");
+  CHECK_RC(env, c, anima_linear(c, &d));
+  return NULL;
+}
+
+/* lastError(ctx | null) */
+static napi_value js_last_error(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  get_args(env, info, 1, a);
+  anima_ctx* c = is_nullish(env, a[0]) ? NULL : ctx_of(env, a[0]);
+  napi_value s;
+  NAPI_CALL(env, napi_create_string_utf8(env, anima_last_error(c), NAPI_AUTO_LENGTH, &s));
+  return s;
+}
+
+static napi_value Init(napi_env env, napi_value exports) {
+#define FN(name, f) {name, NULL, f, NULL, NULL, NULL, napi_enumerable, NULL}
+  napi_property_descriptor desc[] = {
+      FN("init", js_init), FN("destroy", js_destroy), FN("sync", js_sync), FN("alloc", js_alloc),
+      FN("free", js_free), FN("trim", js_trim), FN("memStats", js_mem_stats), FN("h2d", js_h2d),
+      FN("d2h", js_d2h), FN("d2d", js_d2d), FN("profileEnable", js_profile_enable),
+      FN("profileReset", js_profile_reset), FN("profileReport", js_profile_report),
+      FN("timerStart", js_timer_start), FN("timerStop", js_timer_stop), FN("attention", js_attention),
+      FN("qkNormRope", js_qk_norm_rope), FN("rmsnorm", js_rmsnorm), FN("rope", js_rope),
+      FN("hadamard", js_hadamard), FN("quantRows", js_quant_rows), FN("layernormMod", js_layernorm_mod),
+      FN("elementwise", js_elementwise), FN("zero", js_zero), FN("fillRandom", js_fill_random),
+      FN("linear", js_linear), FN("lastError", js_last_error),
+  };
+#undef FN
+  if (napi_define_properties(env, exports, sizeof desc / sizeof desc[0], desc) != napi_ok) return NULL;
+  return exports;
+}
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, Init)

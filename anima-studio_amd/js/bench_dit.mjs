@@ -1,0 +1,98 @@
+// One full DiT step at 1024x1024 through the JS -> N-API -> HIP path: B=2 (CFG cond + uncond),
+// 28 blocks, hidden 2048, 16x128 heads, MLP 8192, self + cross attention to 512x1024 contexts,
+// seeded random-init weights in the W4A8 "mixed" layout (blocks 0 and 27 int8).
+// A step is timeCond(sigma) + forward() (the per-prompt context K/V are cached beforehand, as in
+// app/pipeline.js:195-211).  Prints one JSON line.
+//
+//   node bench_dit.mjs [--size 1024] [--blocks 28] [--mode w4a8|int8|bf16] [--steps 3] [--warmup 1] [--profile]
+
+import { GPU, native } from "./gpu.mjs";
+import { SyntheticWeights } from "./weights.mjs";
+import { AnimaDiT } from "./dit.mjs";
+
+function arg(name, def) {
+  const i = process.argv.indexOf("--" + name);
+  if (i < 0) return def;
+  const v = process.argv[i + 1];
+  return v === undefined || v.startsWith("--") ? true : v;
+}
+
+// Box-Muller over a 32-bit LCG: seeded synthetic latents (host side, like the noise of rng.js).
+function normals(n, seed) {
+  const out = new Float32Array(n);
+  let s = seed >>> 0;
+  const u = () => {
+    s = (Math.imul(s, 1664525) + 1013904223) >>> 0;
+    return (s + 1) / 4294967297;
+  };
+  for (let i = 0; i < n; i += 2) {
+    const r = Math.sqrt(-2 * Math.log(u()));
+    const t = 2 * Math.PI * u();
+    out[i] = r * Math.cos(t);
+    if (i + 1 < n) out[i + 1] = r * Math.sin(t);
+  }
+  return out;
+}
+
+async function main() {
+  const size = Number(arg("size", 1024));
+  const nBlocks = Number(arg("blocks", 28));
+  const mode = arg("mode", "w4a8");
+  const steps = Number(arg("steps", 3));
+  const warmup = Number(arg("warmup", 1));
+  const profile = !!arg("profile", false);
+  const B = 2, Lk = 512;
+  const h = size / 8, w = size / 8;
+
+  const gpu = await GPU.create({ profile });
+  const src = new SyntheticWeights(gpu, 1234, { mode, blocks: nBlocks });
+  const dit = AnimaDiT.synthetic(gpu, src);
+  const ctxs = [0, 1].map((b) => {
+    const t = gpu.empty([Lk, 1024]);
+    native.fillRandom(gpu.ctx, t.buf, t.size, 4, 77 + b, 1.0, 0.0); // ~N(0,1)
+    return t;
+  });
+  const cond = dit.prepareContext(ctxs);
+  const latents = [normals(16 * h * w, 1), normals(16 * h * w, 2)];
+  await gpu.sync();
+  process.stderr.write(`bench_dit: model ready (${nBlocks} blocks, ${mode}), ${(gpu.pool.allocated / 2 ** 30).toFixed(2)} GiB\n`);
+
+  const step = async () => {
+    const tc = dit.timeCond(0.9);
+    const v = await dit.forward(latents, h, w, cond, tc);
+    tc.release();
+    return v;
+  };
+  let v = null;
+  for (let i = 0; i < warmup; i++) v = await step();
+  await gpu.sync();
+  if (gpu.profiler) gpu.profiler.reset();
+  gpu.timerStart();
+  for (let i = 0; i < steps; i++) v = await step();
+  const ms = gpu.timerStop() / steps;
+  await gpu.sync();
+  let finite = true;
+  for (const x of v) for (let i = 0; i < x.length; i += 97) if (!Number.isFinite(x[i])) { finite = false; break; }
+  const L = (h / 2) * (w / 2);
+  // algorithmic FLOPs per step (2*M*N*K GEMMs, 4*Lq*Lk*D*H attention; app/gpu/ops.js:31, 174)
+  const M = B * L;
+  const perBlock = 2 * M * D_(3 * 2048, 2048) + 2 * M * D_(2048, 2048) * 3 + 2 * M * D_(8192, 2048) * 2 +
+    4 * B * L * L * 128 * 16 + 4 * B * L * Lk * 128 * 16;
+  const flops = nBlocks * perBlock + 2 * M * 2048 * 68 + 2 * M * 64 * 2048;
+  const out = { dit_step_ms: Number(ms.toFixed(3)), size, blocks: nBlocks, mode, B, tokens: L, steps, warmup,
+    flops_per_step: flops, tflops: Number((flops / (ms / 1e3) / 1e12).toFixed(2)), finite,
+    peak_gib: Number((gpu.pool.peak / 2 ** 30).toFixed(2)) };
+  if (gpu.profiler) out.kernels = await gpu.profiler.report();
+  console.log(JSON.stringify(out));
+  cond.release();
+  gpu.destroy();
+}
+
+function D_(n, k) {
+  return n * k;
+}
+
+main().catch((e) => {
+  process.stderr.write(String(e && e.stack ? e.stack : e) + "\n");
+  process.exit(1);
+});

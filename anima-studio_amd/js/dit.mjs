@@ -1,0 +1,231 @@
+// Anima DiT (Cosmos-Predict2 MiniTrainDIT, 28 blocks) on the gfx950 op layer.
+// Restates the call order of app/models/dit.js (timeCond 196-225, prepareContext 232-249,
+// forward 253-325) with two MI355X-side changes:
+//   * CFG runs as one batched B=2 pass (cond + uncond) instead of two B=1 passes
+//     (app/pipeline.js:260-265); each batch element attends to its own cached context K/V.
+//   * Quantized linears run W8A8: LayerNorm + adaLN + ConvRot + per-token int8 are one kernel
+//     (layernormModQ) feeding the int8-MFMA GEMM; q/k RMSNorm + RoPE are fused into attention.
+
+import * as ops from "./ops.mjs";
+import { concatLinears } from "./weights.mjs";
+import { ditRopeTable, timestepEmbedding, patchify, unpatchify } from "./common.mjs";
+
+const D = 2048;
+const HEADS = 16;
+const HD = 128;
+const MLP = 8192;
+const CTX_DIM = 1024;
+const ADALN_RANK = 256;
+
+function releaseAll(xs) {
+  for (const x of xs) if (x && x.release) x.release();
+}
+
+// LayerNorm + adaLN for inputs that feed W: int8 { xq } when W is quantized (W8A8), else the
+// fp32 modulated rows (normFor of app/models/dit.js:34-38).
+function normFor(gpu, x, mod, W) {
+  if (ops.needsRotation(W)) return { xq: ops.layernormModQ(gpu, x, mod, 0, D, D) };
+  return { n: ops.layernormMod(gpu, x, mod, 0, D, D, false) };
+}
+
+function project(gpu, nf, W, M, opts) {
+  const o = Object.assign({ M }, opts || {});
+  if (nf.xq) o.xq = nf.xq;
+  return ops.linear(gpu, nf.n || null, W, o);
+}
+
+function releaseNorm(nf) {
+  if (nf.xq) nf.xq.release();
+  if (nf.n) nf.n.release();
+}
+
+export class AnimaDiT {
+  // From a safetensors checkpoint in the web-asset layout (app/models/dit.js:82-129).
+  static load(gpu, st, nBlocks) {
+    const m = new AnimaDiT(gpu);
+    const attn = (p, o) => ({
+      q: st.linear(gpu, p + "q_proj."), k: st.linear(gpu, p + "k_proj."), v: st.linear(gpu, p + "v_proj."),
+      o: st.linear(gpu, p + o + "."), qn: st.vector(gpu, p + "q_norm.weight"), kn: st.vector(gpu, p + "k_norm.weight"),
+    });
+    m.xEmbed = st.linear(gpu, "x_embedder.proj.1.");
+    m.t1 = st.linear(gpu, "t_embedder.1.linear_1.");
+    m.t2 = st.linear(gpu, "t_embedder.1.linear_2.");
+    m.tNorm = st.vector(gpu, "t_embedding_norm.weight");
+    m.blocks = [];
+    const n = nBlocks || 28;
+    for (let i = 0; i < n; i++) {
+      const p = `blocks.${i}.`;
+      const mod = (nm) => [st.linear(gpu, p + nm + ".1."), st.linear(gpu, p + nm + ".2.")];
+      const self = attn(p + "self_attn.", "output_proj");
+      self.qkv = concatLinears(gpu, [self.q, self.k, self.v]);
+      if (!self.qkv) throw new Error(`block ${i}: q/k/v formats cannot be stacked`);
+      delete self.q; delete self.k; delete self.v;
+      m.blocks.push({
+        modSelf: mod("adaln_modulation_self_attn"), modCross: mod("adaln_modulation_cross_attn"),
+        modMlp: mod("adaln_modulation_mlp"), self, cross: attn(p + "cross_attn.", "output_proj"),
+        l1: st.linear(gpu, p + "mlp.layer1."), l2: st.linear(gpu, p + "mlp.layer2."),
+      });
+    }
+    m.finalMod = [st.linear(gpu, "final_layer.adaln_modulation.1."), st.linear(gpu, "final_layer.adaln_modulation.2.")];
+    m.finalLinear = st.linear(gpu, "final_layer.linear.");
+    return m;
+  }
+
+  // Seeded random-init weights of the same architecture (SyntheticWeights).
+  static synthetic(gpu, src) {
+    const m = new AnimaDiT(gpu);
+    const bf = (name, N, K) => src.bf16Linear(gpu, name, N, K, 1.0);
+    m.xEmbed = bf("x_embedder.proj.1", D, 68);
+    m.t1 = bf("t_embedder.1.linear_1", D, D);
+    m.t2 = bf("t_embedder.1.linear_2", 3 * D, D);
+    m.tNorm = src.vector(gpu, "t_embedding_norm.weight", D);
+    m.blocks = [];
+    for (let i = 0; i < src.nBlocks; i++) {
+      const p = `blocks.${i}.`;
+      const mod = (nm) => [bf(p + nm + ".1", ADALN_RANK, D), src.bf16Linear(gpu, p + nm + ".2", 3 * D, ADALN_RANK, 0.1)];
+      const L = (nm, N, K) => src.blockLinear(gpu, p + nm, N, K, i);
+      m.blocks.push({
+        modSelf: mod("adaln_modulation_self_attn"), modCross: mod("adaln_modulation_cross_attn"),
+        modMlp: mod("adaln_modulation_mlp"),
+        self: { qkv: L("self_attn.qkv", 3 * D, D), o: L("self_attn.output_proj", D, D),
+          qn: src.vector(gpu, p + "self_attn.q_norm.weight", HD), kn: src.vector(gpu, p + "self_attn.k_norm.weight", HD) },
+        cross: { q: L("cross_attn.q_proj", D, D), k: L("cross_attn.k_proj", D, CTX_DIM), v: L("cross_attn.v_proj", D, CTX_DIM),
+          o: L("cross_attn.output_proj", D, D),
+          qn: src.vector(gpu, p + "cross_attn.q_norm.weight", HD), kn: src.vector(gpu, p + "cross_attn.k_norm.weight", HD) },
+        l1: L("mlp.layer1", MLP, D), l2: L("mlp.layer2", D, MLP),
+      });
+    }
+    m.finalMod = [bf("final_layer.adaln_modulation.1", ADALN_RANK, D), src.bf16Linear(gpu, "final_layer.adaln_modulation.2", 2 * D, ADALN_RANK, 0.1)];
+    m.finalLinear = bf("final_layer.linear", 64, D);
+    return m;
+  }
+
+  constructor(gpu) {
+    this.gpu = gpu;
+  }
+
+  // Everything that depends only on sigma (app/models/dit.js:196-225).
+  timeCond(sigma) {
+    const gpu = this.gpu;
+    const t = gpu.fromArray(timestepEmbedding(sigma), [1, D]);
+    const h = ops.linear(gpu, t, this.t1, { act: "silu" });
+    const lora = ops.linear(gpu, h, this.t2); // adaln_lora [1, 6144]
+    h.release();
+    const emb = ops.rmsnorm(gpu, t, this.tNorm, D);
+    t.release();
+    const semb = ops.elementwise(gpu, "silu", emb);
+    emb.release();
+    const mod = (ws, n) => {
+      const out = gpu.empty([1, n]);
+      ops.elementwise(gpu, "copy", lora, null, out); // the first n entries
+      const hh = ops.linear(gpu, semb, ws[0]);
+      ops.linear(gpu, hh, ws[1], { out, resid: true });
+      hh.release();
+      return out;
+    };
+    const blocks = this.blocks.map((b) => ({ self: mod(b.modSelf, 3 * D), cross: mod(b.modCross, 3 * D), mlp: mod(b.modMlp, 3 * D) }));
+    const final = mod(this.finalMod, 2 * D);
+    semb.release();
+    lora.release();
+    return {
+      blocks, final,
+      release() {
+        for (const b of blocks) releaseAll([b.self, b.cross, b.mlp]);
+        final.release();
+      },
+    };
+  }
+
+  // Cross-attention K/V of every block for B prompts (app/models/dit.js:232-249): contexts are
+  // stacked into one [B*Lk, 1024] buffer; per block k = RMSNorm(ctx Wk) (per head), v = ctx Wv,
+  // each [B*Lk, 2048].  Takes ownership of the context tensors.
+  prepareContext(ctxs) {
+    const gpu = this.gpu;
+    const B = ctxs.length;
+    const Lk = ctxs[0].shape[0];
+    const ctx = gpu.empty([B * Lk, CTX_DIM]);
+    ctxs.forEach((c, b) => {
+      if (c.shape[0] !== Lk) throw new Error("prepareContext: contexts must have the same length (pad to 512)");
+      gpu.copy(ctx.at(b * Lk * CTX_DIM), c, Lk * CTX_DIM * 4);
+      c.release();
+    });
+    const quant = this.blocks.some((b) => ops.needsRotation(b.cross.k));
+    const xq = quant ? ops.quantRows(gpu, ctx, CTX_DIM, true) : null;
+    const kv = this.blocks.map((b) => {
+      const k = ops.linear(gpu, ctx, b.cross.k, xq ? { xq, M: B * Lk } : { M: B * Lk });
+      ops.rmsnorm(gpu, k, b.cross.kn, HD, 1e-6, k);
+      const v = ops.linear(gpu, ctx, b.cross.v, xq ? { xq, M: B * Lk } : { M: B * Lk });
+      return { k, v };
+    });
+    if (xq) xq.release();
+    return {
+      ctx, kv, Lk, B,
+      release() {
+        ctx.release();
+        for (const e of kv) releaseAll([e.k, e.v]);
+      },
+    };
+  }
+
+  // latents: B Float32Arrays [16, h, w]; cond: prepareContext(...) with the same B; tc: timeCond.
+  // Returns B flow velocities [16, h, w] (app/models/dit.js:253-325).
+  async forward(latents, h, w, cond, tc, onBlock) {
+    const gpu = this.gpu;
+    const B = latents.length;
+    if (cond.B !== B) throw new Error(`forward: ${B} latents but ${cond.B} contexts`);
+    const Hp = h / 2, Wp = w / 2, L = Hp * Wp, M = B * L;
+    const patches = new Float32Array(M * 68);
+    latents.forEach((lat, b) => patchify(lat, h, w, patches, b * L * 68));
+    const xin = gpu.fromArray(patches, [M, 68]);
+    const x = ops.linear(gpu, xin, this.xEmbed);
+    xin.release();
+    const cs = ditRopeTable(gpu, Hp, Wp);
+
+    for (let i = 0; i < this.blocks.length; i++) {
+      const b = this.blocks[i];
+      const m = tc.blocks[i];
+
+      // self-attention: stacked QKV GEMM, then attention with q/k RMSNorm + RoPE fused
+      let nf = normFor(gpu, x, m.self, b.self.qkv);
+      const qkv = project(gpu, nf, b.self.qkv, M, { name: "dit.self.qkv" });
+      releaseNorm(nf);
+      let a = ops.attention(gpu, { q: qkv, k: qkv, v: qkv, B, Lq: L, Lk: L, H: HEADS, D: HD, ldq: 3 * D, ldk: 3 * D,
+        ldv: 3 * D, qOff: 0, kOff: D, vOff: 2 * D, qNorm: b.self.qn, kNorm: b.self.kn, cs });
+      qkv.release();
+      ops.linear(gpu, a, b.self.o, { M, out: x, resid: true, gate: m.self, gOff: 2 * D });
+      a.release();
+
+      // cross-attention against the per-prompt cached keys/values (q RMSNorm fused, no RoPE)
+      nf = normFor(gpu, x, m.cross, b.cross.q);
+      const q = project(gpu, nf, b.cross.q, M);
+      releaseNorm(nf);
+      const kv = cond.kv[i];
+      a = ops.attention(gpu, { q, k: kv.k, v: kv.v, B, Lq: L, Lk: cond.Lk, H: HEADS, D: HD, ldq: D, ldk: D, ldv: D,
+        qNorm: b.cross.qn });
+      q.release();
+      ops.linear(gpu, a, b.cross.o, { M, out: x, resid: true, gate: m.cross, gOff: 2 * D });
+      a.release();
+
+      // MLP
+      nf = normFor(gpu, x, m.mlp, b.l1);
+      const hdn = project(gpu, nf, b.l1, M, { act: "gelu" });
+      releaseNorm(nf);
+      ops.linear(gpu, hdn, b.l2, { M, out: x, resid: true, gate: m.mlp, gOff: 2 * D });
+      hdn.release();
+
+      gpu.flush();
+      if (onBlock) await onBlock(i, x);
+    }
+    cs.release();
+
+    const n = ops.layernormMod(gpu, x, tc.final, 0, D, D, false);
+    x.release();
+    const out = ops.linear(gpu, n, this.finalLinear); // [M, 64] = (p1 p2 c)
+    n.release();
+    const o = await gpu.read(out);
+    out.release();
+    const vs = [];
+    for (let bb = 0; bb < B; bb++) vs.push(unpatchify(o, h, w, bb * L * 64));
+    return vs;
+  }
+}

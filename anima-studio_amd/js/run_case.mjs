@@ -1,0 +1,119 @@
+// Runs one op case through the JS op layer (ops.mjs -> N-API -> libanima.so) for the parity
+// tests: reads a JSON spec whose inputs are raw little-endian files, writes the outputs the same
+// way.  node run_case.mjs case.json
+//
+// Cases:
+//   attention  fused self-attention from a QKV file with q/k RMSNorm and the JS-built RoPE table
+//   qknr       ops.qkNormRope in place
+//   linear     ops.linear (i8 / w4 / bf16 weight files), with xr / resid / gate options
+//   lnmod      ops.layernormMod (rotate) and ops.layernormModQ
+//   dit        AnimaDiT.load(safetensors) -> timeCond -> prepareContext -> forward
+
+import fs from "fs";
+import { GPU } from "./gpu.mjs";
+import * as ops from "./ops.mjs";
+import { ditRopeTable } from "./common.mjs";
+import { SafeTensors } from "./weights.mjs";
+import { AnimaDiT } from "./dit.mjs";
+
+const ARR = { f32: Float32Array, i8: Int8Array, u8: Uint8Array, u16: Uint16Array, i32: Int32Array };
+
+function load(path, dtype) {
+  const b = fs.readFileSync(path);
+  const ab = b.buffer.slice(b.byteOffset, b.byteOffset + b.length);
+  return new ARR[dtype || "f32"](ab);
+}
+
+function save(path, arr) {
+  fs.writeFileSync(path, Buffer.from(arr.buffer, arr.byteOffset, arr.byteLength));
+}
+
+function weightFromFiles(gpu, w) {
+  const W = { kind: w.kind, N: w.N, K: w.K, name: "case" };
+  if (w.kind === "i8") {
+    W.buf = gpu.upload(load(w.w, "i8"));
+    W.scale = gpu.upload(load(w.scale));
+  } else if (w.kind === "w4") {
+    W.buf = gpu.upload(load(w.w, "u8"));
+    W.srel = gpu.upload(load(w.srel, "u8"));
+    W.scale = gpu.upload(load(w.scale));
+    W.codebookData = load(w.codebook);
+    W.codebook = gpu.upload(W.codebookData);
+  } else {
+    W.buf = gpu.upload(load(w.w, "u16"));
+  }
+  if (w.bias) W.bias = gpu.upload(load(w.bias));
+  return W;
+}
+
+async function main() {
+  const spec = JSON.parse(fs.readFileSync(process.argv[2], "utf8"));
+  const gpu = await GPU.create({});
+  const c = spec;
+  if (c.case === "attention") {
+    const L = c.Hp * c.Wp, H = c.H, D = 128;
+    const qkv = gpu.fromArray(load(c.qkv), [c.B * L, 3 * H * D]);
+    const qn = gpu.upload(load(c.qn)), kn = gpu.upload(load(c.kn));
+    const cs = ditRopeTable(gpu, c.Hp, c.Wp);
+    const o = ops.attention(gpu, { q: qkv, k: qkv, v: qkv, B: c.B, Lq: L, Lk: L, H, D, ldq: 3 * H * D, ldk: 3 * H * D,
+      ldv: 3 * H * D, qOff: 0, kOff: H * D, vOff: 2 * H * D, qNorm: qn, kNorm: kn, cs, precision: c.precision });
+    save(c.out, await gpu.read(o));
+    save(c.out + ".cs", await gpu.read(cs));
+  } else if (c.case === "qknr") {
+    const L = c.Hp * c.Wp, H = c.H, D = 128;
+    const qkv = gpu.fromArray(load(c.qkv), [L, 3 * H * D]);
+    const cs = ditRopeTable(gpu, c.Hp, c.Wp);
+    ops.qkNormRope(gpu, qkv, gpu.upload(load(c.qn)), gpu.upload(load(c.kn)), cs, L, H, D);
+    save(c.out, await gpu.read(qkv));
+  } else if (c.case === "linear") {
+    const W = weightFromFiles(gpu, c.W);
+    const x = gpu.fromArray(load(c.x), [c.M, W.K]);
+    const opts = { act: c.act || "none" };
+    if (c.xr) opts.xr = x;
+    if (c.resid) {
+      opts.out = gpu.fromArray(load(c.resid), [c.M, W.N]);
+      opts.resid = true;
+      if (c.gate) {
+        opts.gate = gpu.upload(load(c.gate));
+        opts.gOff = c.gOff;
+      }
+    }
+    const y = ops.linear(gpu, x, W, opts);
+    save(c.out, await gpu.read(y));
+  } else if (c.case === "lnmod") {
+    const x = gpu.fromArray(load(c.x), [c.rows, c.cols]);
+    const mod = gpu.upload(load(c.mod));
+    const y = ops.layernormMod(gpu, x, mod, 0, c.cols, c.cols, !!c.rotate);
+    save(c.out, await gpu.read(y));
+    if (c.rotate) {
+      const q = ops.layernormModQ(gpu, x, mod, 0, c.cols, c.cols);
+      save(c.out + ".q", await gpu.read(q.q));
+      save(c.out + ".s", await gpu.read(q.s));
+    }
+  } else if (c.case === "dit") {
+    const st = SafeTensors.open(c.weights);
+    const dit = AnimaDiT.load(gpu, st, c.blocks);
+    const tc = dit.timeCond(c.sigma);
+    const ctxs = c.ctx.map((p) => gpu.fromArray(load(p), [c.Lk, 1024]));
+    const cond = dit.prepareContext(ctxs);
+    const lat = c.latents.map((p) => load(p));
+    const h = c.h, w = c.w;
+    const blockOut = [];
+    const v = await dit.forward(lat, h, w, cond, tc, async (i, x) => {
+      if (i === 0) blockOut.push(await gpu.read(x));
+    });
+    v.forEach((vb, b) => save(c.out + "." + b, vb));
+    save(c.out + ".block0", blockOut[0]);
+    st.close();
+  } else {
+    throw new Error("unknown case " + c.case);
+  }
+  await gpu.sync();
+  gpu.destroy();
+  console.log(JSON.stringify({ ok: true, case: c.case }));
+}
+
+main().catch((e) => {
+  process.stderr.write(String(e && e.stack ? e.stack : e) + "\n");
+  process.exit(1);
+});

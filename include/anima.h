@@ -153,6 +153,21 @@ int anima_elementwise(anima_ctx* ctx, int op, const float* a, const float* b, fl
 /* ops.zero (app/gpu/ops.js:89-93; kernels.js:415-423). */
 int anima_zero(anima_ctx* ctx, float* y, int64_t n);
 
+/* Seeded synthetic data on the device, for benchmarks and tests (no reference counterpart: the
+ * reference loads real checkpoints).  Element i draws h = splitmix64(seed * 0xD1B54A32D192ED03 + i):
+ *   ANIMA_FILL_U8    uint8   lo + h % (hi - lo + 1)                (integers lo..hi)
+ *   ANIMA_FILL_I8N   int8    clamp(((b0+b1+b2+b3 - 510) * round(lo * 4096 / 147.8017)) >> 12, +-127)
+ *                            (b_j = bytes of h: Irwin-Hall approximation of N(0, lo^2))
+ *   ANIMA_FILL_F32   fp32    lo + (hi - lo) * ((h >> 40) * 2^-24)
+ *   ANIMA_FILL_BF16  bf16    the ANIMA_FILL_F32 value rounded to nearest even
+ *   ANIMA_FILL_F32N  fp32    (u0+u1+u2+u3 - 2) * 1.7320508 * lo + hi, u_j = 16-bit fields of h / 65536 */
+#define ANIMA_FILL_U8 0
+#define ANIMA_FILL_I8N 1
+#define ANIMA_FILL_F32 2
+#define ANIMA_FILL_BF16 3
+#define ANIMA_FILL_F32N 4
+int anima_fill_random(anima_ctx* ctx, void* dst, int64_t n, int kind, uint64_t seed, float lo, float hi);
+
 /* ---------------------------------------------------------------- linears */
 
 #define ANIMA_W_BF16 0 /* bf16 [N][K]; fp32 activations, fp32 accumulation (gemm.js:108-128) */
