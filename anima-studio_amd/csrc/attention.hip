@@ -151,11 +151,16 @@ __global__ __launch_bounds__(256) void attn_prep_kv(PrepArgs a) {
     T* dst = (T*)a.vt + (((int64_t)b * a.Hkv + hk) * HD + d) * a.Lkp + kb0 + 32 * h2;
     const T* srow = vs + d * VSP + 32 * h2;
     if constexpr (sizeof(T) == 2) {
+      // bf16 MFMA layout: each 16-key group stored as keys [0-3, 8-11, 4-7, 12-15]
 #pragma unroll
       for (int i = 0; i < 4; i++) {
+        const int g16 = (i >> 1) * 16, half = i & 1;
         bf16x8 o;
 #pragma unroll
-        for (int e = 0; e < 8; e++) o[e] = ((const bf16*)srow)[8 * i + e];
+        for (int e = 0; e < 4; e++) {
+          o[e] = ((const bf16*)srow)[g16 + 4 * half + e];
+          o[4 + e] = ((const bf16*)srow)[g16 + 8 + 4 * half + e];
+        }
         *(bf16x8*)((bf16*)dst + 8 * i) = o;
       }
     } else {
@@ -236,14 +241,75 @@ __device__ __forceinline__ void load_q(const FlashArgs& a, int b, int h, int qi,
 
 // ------------------------------------------------------------------ bf16 MFMA kernel
 
-constexpr int KSP = HD + 8;  // K tile row stride (bf16): 272 B, 16-byte aligned rows
-constexpr int VSP = BK + 4;  // V^T tile row stride (bf16): 136 B
+constexpr int KSP = HD + 8;  // K tile row stride (bf16): 272 B, conflict-free 16-byte reads
+constexpr int VSP = BK + 8;  // V^T tile row stride (bf16): 144 B, 16-byte aligned rows
 constexpr int KTILE = BK * KSP;
 constexpr int VTILE = HD * VSP;
+constexpr int STAGE = KTILE + VTILE;
+
+// One 64-key block for one wave: S^T = K Q^T on two 32-key tiles, online softmax with the
+// integer offset m, then O^T += V^T P^T.  MASK: keys >= Lk get -inf (last partial block only).
+template <bool MASK>
+__device__ __forceinline__ void flash_block_bf16(const bf16* __restrict__ K, const bf16* __restrict__ V,
+                                                 const bf16x8 (&qf)[8], f32x16 (&o)[4], float& m, float& l,
+                                                 float c, int key0, int Lk, int lq, int hf) {
+  f32x16 s0 = {}, s1 = {};
+#pragma unroll
+  for (int ks = 0; ks < 8; ks++) {
+    const bf16x8 ka = *(const bf16x8*)(K + lq * KSP + 16 * ks + 8 * hf);
+    const bf16x8 kb = *(const bf16x8*)(K + (32 + lq) * KSP + 16 * ks + 8 * hf);
+    s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[ks], s0, 0, 0, 0);
+    s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb, qf[ks], s1, 0, 0, 0);
+  }
+  if (MASK) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int key = key0 + 8 * (r >> 2) + 4 * hf + (r & 3);
+      if (key >= Lk) s0[r] = -INFINITY;
+      if (key + 32 >= Lk) s1[r] = -INFINITY;
+    }
+  }
+  float bm = fmaxf(fmaxf(s0[0], s1[0]), fmaxf(s0[1], s1[1]));
+#pragma unroll
+  for (int r = 2; r < 16; r++) bm = fmaxf(bm, fmaxf(s0[r], s1[r]));
+  bm = fmaxf(bm, __shfl_xor(bm, 32));
+  const float bmc = bm * c;
+  const bool need = bmc > m + RESCALE_SLACK;
+  if (__builtin_amdgcn_ballot_w64(need)) {
+    const float mn = need ? ceilf(bmc) : m;
+    const float alpha = __builtin_amdgcn_exp2f(m - mn);
+    m = mn;
+    l *= alpha;
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] *= alpha;
+  }
+  bf16x8 pb[4];
+  float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], c, -m));
+    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], c, -m));
+    ls[r & 1] += p0;
+    ls[2 + (r & 1)] += p1;
+    pb[r >> 3][r & 7] = to_bf16(p0);
+    pb[2 + (r >> 3)][r & 7] = to_bf16(p1);
+  }
+  l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+  // V^T rows hold each 16-key group as keys [0-3, 8-11, 4-7, 12-15], so the 8 keys of lane half
+  // hf for k-step s (16s + 4hf + {0..3} and 16s + 8 + 4hf + {0..3}) are one 16-byte read.
+#pragma unroll
+  for (int s = 0; s < 4; s++) {
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) {
+      const bf16x8 va = *(const bf16x8*)(V + (32 * dt + lq) * VSP + 16 * s + 8 * hf);
+      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[s], o[dt], 0, 0, 0);
+    }
+  }
+}
 
 template <bool NORM, bool ROPE>
 __global__ __launch_bounds__(256, 2) void attn_flash_bf16(FlashArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * (KTILE + VTILE)];
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * STAGE];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 31, hf = lane >> 5;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
@@ -252,6 +318,7 @@ __global__ __launch_bounds__(256, 2) void attn_flash_bf16(FlashArgs a) {
   const int qi = qt * BQ + wave * 32 + lq;
   const int Lk = a.kv_len[b];
   const int nkb = (Lk + BK - 1) / BK;
+  const bool tail = (Lk % BK) != 0;
 
   bf16x8 qf[8];
   {
@@ -263,107 +330,54 @@ __global__ __launch_bounds__(256, 2) void attn_flash_bf16(FlashArgs a) {
       for (int j = 0; j < 8; j++) qf[ks][j] = to_bf16(x[8 * ks + j]);
   }
 
-  const bf16* kg = (const bf16*)a.kb + ((int64_t)b * a.Hkv + hk) * a.Lkp * HD;
-  const bf16* vg = (const bf16*)a.vt + ((int64_t)b * a.Hkv + hk) * HD * a.Lkp;
   // global -> LDS copy assignment: K rows (t/4, 64 B chunk t%4); V^T rows (t/2, 64 B half t%2)
   const int kr = tid >> 2, kc = tid & 3, vr = tid >> 1, vc = tid & 1;
-  uint4 kreg[4], vreg[4];
-  auto gload = [&](int blk) {
-    const uint4* ks = (const uint4*)(kg + ((int64_t)blk * BK + kr) * HD + 32 * kc);
-    const uint4* vsrc = (const uint4*)(vg + (int64_t)vr * a.Lkp + blk * BK + 32 * vc);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      kreg[i] = ks[i];
-      vreg[i] = vsrc[i];
-    }
-  };
-  auto lstore = [&](int stage) {
-    bf16* K = smem + stage * (KTILE + VTILE);
-    bf16* V = K + KTILE;
-    uint4* kd = (uint4*)(K + kr * KSP + 32 * kc);
-    uint2* vd = (uint2*)(V + vr * VSP + 32 * vc);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      kd[i] = kreg[i];
-      vd[2 * i] = make_uint2(vreg[i].x, vreg[i].y);
-      vd[2 * i + 1] = make_uint2(vreg[i].z, vreg[i].w);
-    }
-  };
+  const uint4* kg = (const uint4*)((const bf16*)a.kb + (((int64_t)b * a.Hkv + hk) * a.Lkp + kr) * HD + 32 * kc);
+  const uint4* vg = (const uint4*)((const bf16*)a.vt + (((int64_t)b * a.Hkv + hk) * HD + vr) * a.Lkp + 32 * vc);
+  const int kstep = BK * HD / 8;  // uint4 per K block
+  const int vstep = BK / 8;       // uint4 per V^T block
+  uint4 k0, k1, k2, k3, v0, v1, v2, v3;
+#define GLOAD(blk)                                                         \
+  {                                                                        \
+    const uint4* ks_ = kg + (int64_t)(blk) * kstep;                        \
+    const uint4* vs_ = vg + (int64_t)(blk) * vstep;                        \
+    k0 = ks_[0]; k1 = ks_[1]; k2 = ks_[2]; k3 = ks_[3];                    \
+    v0 = vs_[0]; v1 = vs_[1]; v2 = vs_[2]; v3 = vs_[3];                    \
+  }
+#define LSTORE(st)                                                         \
+  {                                                                        \
+    uint4* kd_ = (uint4*)(smem + (st) * STAGE + kr * KSP + 32 * kc);       \
+    uint4* vd_ = (uint4*)(smem + (st) * STAGE + KTILE + vr * VSP + 32 * vc); \
+    kd_[0] = k0; kd_[1] = k1; kd_[2] = k2; kd_[3] = k3;                    \
+    vd_[0] = v0; vd_[1] = v1; vd_[2] = v2; vd_[3] = v3;                    \
+  }
 
   f32x16 o[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) o[i] = (f32x16){};
   float m = -INFINITY, l = 0.0f;
+  const float c = a.c;
 
-  gload(0);
-  lstore(0);
+  GLOAD(0);
+  LSTORE(0);
   __syncthreads();
-
-  for (int kb = 0; kb < nkb; kb++) {
-    const int stage = kb & 1;
-    const bf16* K = smem + stage * (KTILE + VTILE);
-    const bf16* V = K + KTILE;
-    if (kb + 1 < nkb) gload(kb + 1);
-
-    // S^T = K Q^T: two 32-key tiles
-    f32x16 s0 = {}, s1 = {};
-#pragma unroll
-    for (int ks = 0; ks < 8; ks++) {
-      const bf16x8 ka = *(const bf16x8*)(K + lq * KSP + 16 * ks + 8 * hf);
-      const bf16x8 kb2 = *(const bf16x8*)(K + (32 + lq) * KSP + 16 * ks + 8 * hf);
-      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[ks], s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb2, qf[ks], s1, 0, 0, 0);
-    }
-    if ((kb + 1) * BK > Lk) {  // keys >= kv_len in the last block
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int key = kb * BK + 8 * (r >> 2) + 4 * hf + (r & 3);
-        if (key >= Lk) s0[r] = -INFINITY;
-        if (key + 32 >= Lk) s1[r] = -INFINITY;
-      }
-    }
-    float bm = fmaxf(s0[0], s1[0]);
-#pragma unroll
-    for (int r = 1; r < 16; r++) bm = fmaxf(bm, fmaxf(s0[r], s1[r]));
-    bm = fmaxf(bm, __shfl_xor(bm, 32));
-    const float bmc = bm * a.c;
-    const bool need = bmc > m + RESCALE_SLACK;
-    if (__builtin_amdgcn_ballot_w64(need)) {
-      const float mn = need ? ceilf(bmc) : m;
-      const float alpha = __builtin_amdgcn_exp2f(m - mn);
-      m = mn;
-      l *= alpha;
-#pragma unroll
-      for (int i = 0; i < 4; i++) o[i] *= alpha;
-    }
-    bf16x8 pb[4];
-    float ls0 = 0.0f, ls1 = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], a.c, -m));
-      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], a.c, -m));
-      ls0 += p0;
-      ls1 += p1;
-      pb[r >> 3][r & 7] = to_bf16(p0);
-      pb[2 + (r >> 3)][r & 7] = to_bf16(p1);
-    }
-    l += ls0 + ls1;
-
-    // O^T += V^T P^T: k-step s covers keys 16s .. 16s+15
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-#pragma unroll
-      for (int dt = 0; dt < 4; dt++) {
-        const bf16* vrow = V + (32 * dt + lq) * VSP + 16 * s + 4 * hf;
-        const bf16x4 lo = *(const bf16x4*)vrow;
-        const bf16x4 hi = *(const bf16x4*)(vrow + 8);
-        const bf16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[s], o[dt], 0, 0, 0);
-      }
-    }
-    if (kb + 1 < nkb) lstore(stage ^ 1);
+  // Full blocks, double-buffered; the last block is the only one that can be partial and is
+  // processed after the loop with the key mask (it is already in its stage by then).
+  const int nfull = Lk / BK;
+  for (int kb = 0; kb < nfull; kb++) {
+    const int st = kb & 1;
+    const bool more = kb + 1 < nkb;
+    if (more) GLOAD(kb + 1);
+    flash_block_bf16<false>(smem + st * STAGE, smem + st * STAGE + KTILE, qf, o, m, l, c, kb * BK, Lk, lq, hf);
+    if (more) LSTORE(st ^ 1);
     __syncthreads();
   }
+  if (tail) {
+    const int st = nfull & 1;
+    flash_block_bf16<true>(smem + st * STAGE, smem + st * STAGE + KTILE, qf, o, m, l, c, nfull * BK, Lk, lq, hf);
+  }
+#undef GLOAD
+#undef LSTORE
 
   l += __shfl_xor(l, 32);
   if (qi < a.Lq) {

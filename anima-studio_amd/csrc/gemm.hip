@@ -289,6 +289,52 @@ __global__ __launch_bounds__(256) void gemm_f32w_kernel(F32WArgs a) {
   }
 }
 
+// Small-M (M <= 8) bf16-weight GEMV: one wave per output column n, lanes stride K in 8-element
+// chunks, fp32 FMA, wave reduction (timestep / adaLN projections, M = 1).
+constexpr int GEMV_MAXM = 8;
+__global__ __launch_bounds__(256) void gemv_f32w_kernel(F32WArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= a.N) return;
+  float acc[GEMV_MAXM];
+#pragma unroll
+  for (int m = 0; m < GEMV_MAXM; m++) acc[m] = 0.0f;
+  const uint16_t* wr = a.w + (int64_t)n * a.K;
+  for (int k = lane * 8; k < a.K; k += 512) {
+    const uint4 wv = *(const uint4*)(wr + k);
+    float wf[8];
+    const uint32_t u[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      wf[2 * j] = __uint_as_float(u[j] << 16);
+      wf[2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
+    }
+#pragma unroll
+    for (int m = 0; m < GEMV_MAXM; m++) {
+      if (m >= a.M) break;
+      const float4 x0 = *(const float4*)(a.x + (int64_t)m * a.ldx + k);
+      const float4 x1 = *(const float4*)(a.x + (int64_t)m * a.ldx + k + 4);
+      const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int j = 0; j < 8; j++) acc[m] = __builtin_fmaf(xv[j], wf[j], acc[m]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < GEMV_MAXM; m++) {
+    if (m >= a.M) break;
+    const float tot = wave_sum(acc[m]);
+    if (lane == 0) {
+      float r = tot * a.alpha;
+      if (a.bias) r = r + a.bias[n];
+      r = apply_act(r, a.act);
+      float* c = a.out + (int64_t)m * a.ldc + n;
+      if (a.epi == ANIMA_EPI_STORE) *c = r;
+      else if (a.epi == ANIMA_EPI_RESID) *c = *c + r;
+      else *c = __builtin_fmaf(a.gate[a.gate_off + n], r, *c);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ host
 
 static bool al(const void* p, int b) { return ((uintptr_t)p & (b - 1)) == 0; }
@@ -315,6 +361,11 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
     if (ldx < K) return fail(c, ANIMA_E_ARG, "anima_linear: ldx < K");
     F32WArgs f{d->x, ldx, (const uint16_t*)W->w, W->bias, d->out, ldc, alpha, d->act, d->epilogue, d->gate, d->gate_off,
                (int)M, N, K};
+    if (M <= GEMV_MAXM && K % 8 == 0 && ldx % 4 == 0 && al(d->x, 16) && al(W->w, 16)) {
+      Launch L(c, "gemv.bf16", 2.0 * M * N * K, 2.0 * N * K);
+      hipLaunchKernelGGL(gemv_f32w_kernel, dim3((N + 3) / 4), dim3(256), 0, c->stream, f);
+      return L.end();
+    }
     Launch L(c, "gemm.bf16", 2.0 * M * N * K, 0.0);
     hipLaunchKernelGGL(gemm_f32w_kernel, dim3((N + 63) / 64, (unsigned)((M + 63) / 64)), dim3(256), 0, c->stream, f);
     return L.end();

@@ -33,6 +33,10 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-dit", action="store_true", help="skip the full DiT step leg")
+    p.add_argument("--dit-steps", type=int, default=3)
+    p.add_argument("--copy-mb", type=int, default=0,
+                   help="only run the elementwise copy kernel on a buffer of this many MiB (HBM counter calibration)")
     return p.parse_args()
 
 
@@ -48,6 +52,23 @@ def cpu_baseline():
     return json.loads(r.stdout.strip().splitlines()[-1])
 
 
+def dit_step(args):
+    """One full 28-block W4A8 DiT step at 1024x1024, B=2, through the JS -> N-API -> HIP path."""
+    import subprocess
+
+    js = os.path.join(ROOT, "anima-studio_amd", "js", "bench_dit.mjs")
+    r = subprocess.run(["node", js, "--steps", str(args.dit_steps), "--warmup", "1"], cwd=ROOT, capture_output=True,
+                       text=True, timeout=600)
+    if r.returncode != 0:
+        raise RuntimeError("bench_dit.mjs failed: " + r.stderr[-2000:])
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    return {"ms": d["dit_step_ms"], "tflops": d["tflops"], "finite": d["finite"],
+            "config": "Anima DiT 28 blocks, 1024x1024 (4096 tokens), B=2 CFG, hidden 2048, 16x128 heads, MLP 8192, "
+                      "self + cross attention to 512x1024 contexts, W4A8 mixed (blocks 0/27 int8), seeded random weights; "
+                      "step = timeCond + forward through node bench_dit.mjs",
+            "steps": args.dit_steps}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -59,6 +80,16 @@ def main():
     import __graft_entry__ as ge
 
     m = ge._import_pkg()
+    if args.copy_mb:
+        n = args.copy_mb * (1 << 20) // 4
+        with m.Context(0) as ctx:
+            a, b = ctx.empty(n), ctx.empty(n)
+            ctx.zero(a, n)
+            for _ in range(args.warmup + args.steps):
+                ctx.elementwise("copy", a, None, b, n)
+            ctx.sync()
+        print(json.dumps({"copy_mb": args.copy_mb, "launches": args.warmup + args.steps}), flush=True)
+        return
     B, Hp, Wp, H, D = 2, 64, 64, 16, 128
     L = Hp * Wp
     flops = 4.0 * B * H * L * L * D  # 274.878 GFLOP
@@ -132,6 +163,10 @@ def main():
         "prep_kernel": {"ms": round(prep_ms, 5) if prep_ms else None, "GB/s": round(prep_gbs, 1) if prep_gbs else None,
                         "frac_hbm": round(prep_gbs / HBM_PEAK_GBS, 4) if prep_gbs else None},
     }
+    if not args.no_dit:
+        t = time.time()
+        out["dit_step"] = dit_step(args)
+        print(f"bench: dit step {time.time() - t:.1f} s", file=sys.stderr, flush=True)
     if not args.no_cpu:
         t = time.time()
         out["cpu_baseline"] = cpu_baseline()
