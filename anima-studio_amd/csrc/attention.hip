@@ -21,6 +21,8 @@
 // offset m: p = exp2(fma(s, c, -m)).  Integer offsets make the bf16 rounding of p independent
 // of when the offset was raised (a power-of-two rescale), and the offset is raised only when
 // a block maximum exceeds it by more than 8 (p <= 256), so O is rescaled almost never.
+// The bf16 kernel normalizes by the sum of the bf16-rounded p (the weights the P.V MFMA
+// actually uses), the fp32 kernel by the sum of p.
 #include <cmath>
 
 #include "common.h"
@@ -241,75 +243,110 @@ __device__ __forceinline__ void load_q(const FlashArgs& a, int b, int h, int qi,
 
 // ------------------------------------------------------------------ bf16 MFMA kernel
 
-constexpr int KSP = HD + 8;  // K tile row stride (bf16): 272 B, conflict-free 16-byte reads
-constexpr int VSP = BK + 8;  // V^T tile row stride (bf16): 144 B, 16-byte aligned rows
-constexpr int KTILE = BK * KSP;
-constexpr int VTILE = HD * VSP;
-constexpr int STAGE = KTILE + VTILE;
+// LDS tiles of one stage for KB keys per block: K [KB][HD] rows of 272 B (conflict-free 16-byte
+// fragment reads), V^T [HD][KB] rows of 2*KB + 16 B (16-byte aligned).
+// max / sum of a value over the lane pair (l, l ^ 32) on the VALU: v_permlane32_swap exchanges
+// the upper half of its first operand with the lower half of its second, so with both operands
+// equal to x the two results hold x and its partner (in either order) in every lane.
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
-// One 64-key block for one wave: S^T = K Q^T on two 32-key tiles, online softmax with the
-// integer offset m, then O^T += V^T P^T.  MASK: keys >= Lk get -inf (last partial block only).
-template <bool MASK>
-__device__ __forceinline__ void flash_block_bf16(const bf16* __restrict__ K, const bf16* __restrict__ V,
-                                                 const bf16x8 (&qf)[8], f32x16 (&o)[4], float& m, float& l,
-                                                 float c, int key0, int Lk, int lq, int hf) {
-  f32x16 s0 = {}, s1 = {};
+template <int KB>
+struct Tiles {
+  static constexpr int KSP = HD + 8;
+  static constexpr int VSP = KB + 8;
+  static constexpr int KTILE = KB * KSP;
+  static constexpr int STAGE = KTILE + HD * VSP;
+};
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// One KB-key block for one wave of 32 queries: S^T = K Q^T on KB/32 key tiles, online softmax
+// with the integer offset m, then O^T += V^T P^T.  Accumulator register r of key tile t holds
+// key 32t + 8(r/4) + 4hf + r%4; P.V k-step s (16 keys) takes registers 8(s%2)..+7 of tile s/2,
+// i.e. keys 16s + 8(j/4) + 4hf + j%4.  V^T rows hold each 16-key group as keys
+// [0-3, 8-11, 4-7, 12-15], so the matching 8 keys of lane half hf are one 16-byte read.
+// MASK: keys >= Lk get -inf (last block only).
+template <int KB, bool MASK>
+__device__ __forceinline__ void flash_block(const bf16* __restrict__ K, const bf16* __restrict__ V,
+                                            const bf16x8 (&qf)[8], f32x16 (&o)[4], float& m, float& l, float c,
+                                            int key0, int Lk, int lq, int hf) {
+  constexpr int NKT = KB / 32, NKS = KB / 16;
+  constexpr int KSP = Tiles<KB>::KSP, VSP = Tiles<KB>::VSP;
+  f32x16 s[NKT];
+#pragma unroll
+  for (int t = 0; t < NKT; t++) s[t] = (f32x16){};
 #pragma unroll
   for (int ks = 0; ks < 8; ks++) {
-    const bf16x8 ka = *(const bf16x8*)(K + lq * KSP + 16 * ks + 8 * hf);
-    const bf16x8 kb = *(const bf16x8*)(K + (32 + lq) * KSP + 16 * ks + 8 * hf);
-    s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[ks], s0, 0, 0, 0);
-    s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb, qf[ks], s1, 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < NKT; t++) {
+      const bf16x8 kf = *(const bf16x8*)(K + (32 * t + lq) * KSP + 16 * ks + 8 * hf);
+      s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[t], 0, 0, 0);
+    }
   }
   if (MASK) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int key = key0 + 8 * (r >> 2) + 4 * hf + (r & 3);
-      if (key >= Lk) s0[r] = -INFINITY;
-      if (key + 32 >= Lk) s1[r] = -INFINITY;
-    }
-  }
-  float bm = fmaxf(fmaxf(s0[0], s1[0]), fmaxf(s0[1], s1[1]));
+    for (int t = 0; t < NKT; t++)
 #pragma unroll
-  for (int r = 2; r < 16; r++) bm = fmaxf(bm, fmaxf(s0[r], s1[r]));
-  bm = fmaxf(bm, __shfl_xor(bm, 32));
+      for (int r = 0; r < 16; r++)
+        if (key0 + 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3) >= Lk) s[t][r] = -INFINITY;
+  }
+  float bm = s[0][0];
+#pragma unroll
+  for (int t = 0; t < NKT; t++)
+#pragma unroll
+    for (int r = (t == 0 ? 1 : 0); r < 16; r += 2) bm = r + 1 < 16 ? fmaxf(bm, fmaxf(s[t][r], s[t][r + 1])) : fmaxf(bm, s[t][r]);
+  bm = pair_max(bm);
   const float bmc = bm * c;
   const bool need = bmc > m + RESCALE_SLACK;
-  if (__builtin_amdgcn_ballot_w64(need)) {
+  if (__builtin_amdgcn_ballot_w64(need)) {  // rare: the running offset moves up
     const float mn = need ? ceilf(bmc) : m;
     const float alpha = __builtin_amdgcn_exp2f(m - mn);
-    m = mn;
     l *= alpha;
 #pragma unroll
     for (int i = 0; i < 4; i++) o[i] *= alpha;
+    m = mn;
   }
-  bf16x8 pb[4];
-  float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  bf16x8 pb[NKS];
 #pragma unroll
-  for (int r = 0; r < 16; r++) {
-    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], c, -m));
-    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], c, -m));
-    ls[r & 1] += p0;
-    ls[2 + (r & 1)] += p1;
-    pb[r >> 3][r & 7] = to_bf16(p0);
-    pb[2 + (r >> 3)][r & 7] = to_bf16(p1);
+  for (int t = 0; t < NKT; t++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) pb[2 * t + (r >> 3)][r & 7] = to_bf16(__builtin_amdgcn_exp2f(__builtin_fmaf(s[t][r], c, -m)));
+  // row sum of the rounded probabilities (exact convex weights) with bf16 dot2
+  const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
+  float l0 = 0.0f, l1 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NKS; i++) {
+    l0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 0, 1), ones, l0, false);
+    l1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 2, 3), ones, l1, false);
+    l0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 4, 5), ones, l0, false);
+    l1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 6, 7), ones, l1, false);
   }
-  l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
-  // V^T rows hold each 16-key group as keys [0-3, 8-11, 4-7, 12-15], so the 8 keys of lane half
-  // hf for k-step s (16s + 4hf + {0..3} and 16s + 8 + 4hf + {0..3}) are one 16-byte read.
+  l += l0 + l1;
 #pragma unroll
-  for (int s = 0; s < 4; s++) {
+  for (int sk = 0; sk < NKS; sk++) {
 #pragma unroll
     for (int dt = 0; dt < 4; dt++) {
-      const bf16x8 va = *(const bf16x8*)(V + (32 * dt + lq) * VSP + 16 * s + 8 * hf);
-      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[s], o[dt], 0, 0, 0);
+      const bf16x8 va = *(const bf16x8*)(V + (32 * dt + lq) * VSP + 16 * sk + 8 * hf);
+      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[sk], o[dt], 0, 0, 0);
     }
   }
 }
 
-template <bool NORM, bool ROPE>
-__global__ __launch_bounds__(256, 2) void attn_flash_bf16(FlashArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * STAGE];
+// 4 waves x 32 queries per workgroup; K/V blocks of KB keys double-buffered in LDS, the next
+// block prefetched into registers while the current one is consumed (one barrier per block).
+template <int KB, bool NORM, bool ROPE>
+__global__ __launch_bounds__(256, KB == 32 ? 3 : 2) void attn_flash_bf16(FlashArgs a) {
+  using T = Tiles<KB>;
+  constexpr int UK = KB / 16;  // uint4 per thread for each of the K and V^T block copies
+  static_assert(UK == 2 || UK == 4, "32 or 64 keys per block");
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * T::STAGE];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 31, hf = lane >> 5;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
@@ -317,8 +354,7 @@ __global__ __launch_bounds__(256, 2) void attn_flash_bf16(FlashArgs a) {
   const int b = bh / a.H, h = bh - b * a.H, hk = h / a.group;
   const int qi = qt * BQ + wave * 32 + lq;
   const int Lk = a.kv_len[b];
-  const int nkb = (Lk + BK - 1) / BK;
-  const bool tail = (Lk % BK) != 0;
+  const int nkb = (Lk + KB - 1) / KB;
 
   bf16x8 qf[8];
   {
@@ -330,26 +366,28 @@ __global__ __launch_bounds__(256, 2) void attn_flash_bf16(FlashArgs a) {
       for (int j = 0; j < 8; j++) qf[ks][j] = to_bf16(x[8 * ks + j]);
   }
 
-  // global -> LDS copy assignment: K rows (t/4, 64 B chunk t%4); V^T rows (t/2, 64 B half t%2)
-  const int kr = tid >> 2, kc = tid & 3, vr = tid >> 1, vc = tid & 1;
-  const uint4* kg = (const uint4*)((const bf16*)a.kb + (((int64_t)b * a.Hkv + hk) * a.Lkp + kr) * HD + 32 * kc);
-  const uint4* vg = (const uint4*)((const bf16*)a.vt + (((int64_t)b * a.Hkv + hk) * HD + vr) * a.Lkp + 32 * vc);
-  const int kstep = BK * HD / 8;  // uint4 per K block
-  const int vstep = BK / 8;       // uint4 per V^T block
+  // global -> LDS copy assignment: K row t/(256/KB), KB bytes at (t%(256/KB))*KB;
+  // V^T row t/2, KB bytes (KB/2 keys) at (t%2)*KB/2 keys
+  constexpr int TPR = 256 / KB;
+  const int kr = tid / TPR, kc = tid % TPR, vr = tid >> 1, vc = tid & 1;
+  const uint4* kg = (const uint4*)((const bf16*)a.kb + (((int64_t)b * a.Hkv + hk) * a.Lkp + kr) * HD + kc * (KB / 2));
+  const uint4* vg = (const uint4*)((const bf16*)a.vt + (((int64_t)b * a.Hkv + hk) * HD + vr) * a.Lkp + vc * (KB / 2));
+  // prefetch registers (named, not an array: arrays indexed inside these copies were not
+  // promoted to registers by the compiler and went through scratch memory)
   uint4 k0, k1, k2, k3, v0, v1, v2, v3;
-#define GLOAD(blk)                                                         \
-  {                                                                        \
-    const uint4* ks_ = kg + (int64_t)(blk) * kstep;                        \
-    const uint4* vs_ = vg + (int64_t)(blk) * vstep;                        \
-    k0 = ks_[0]; k1 = ks_[1]; k2 = ks_[2]; k3 = ks_[3];                    \
-    v0 = vs_[0]; v1 = vs_[1]; v2 = vs_[2]; v3 = vs_[3];                    \
+#define GLOAD(blk)                                                                          \
+  {                                                                                         \
+    const uint4* ks_ = kg + (int64_t)(blk) * (KB * HD / 8);                                 \
+    const uint4* vs_ = vg + (int64_t)(blk) * (KB / 8);                                      \
+    k0 = ks_[0]; k1 = ks_[1]; v0 = vs_[0]; v1 = vs_[1];                                     \
+    if constexpr (UK == 4) { k2 = ks_[2]; k3 = ks_[3]; v2 = vs_[2]; v3 = vs_[3]; }          \
   }
-#define LSTORE(st)                                                         \
-  {                                                                        \
-    uint4* kd_ = (uint4*)(smem + (st) * STAGE + kr * KSP + 32 * kc);       \
-    uint4* vd_ = (uint4*)(smem + (st) * STAGE + KTILE + vr * VSP + 32 * vc); \
-    kd_[0] = k0; kd_[1] = k1; kd_[2] = k2; kd_[3] = k3;                    \
-    vd_[0] = v0; vd_[1] = v1; vd_[2] = v2; vd_[3] = v3;                    \
+#define LSTORE(st)                                                                          \
+  {                                                                                         \
+    uint4* kd_ = (uint4*)(smem + (st) * T::STAGE + kr * T::KSP + kc * (KB / 2));            \
+    uint4* vd_ = (uint4*)(smem + (st) * T::STAGE + T::KTILE + vr * T::VSP + vc * (KB / 2)); \
+    kd_[0] = k0; kd_[1] = k1; vd_[0] = v0; vd_[1] = v1;                                     \
+    if constexpr (UK == 4) { kd_[2] = k2; kd_[3] = k3; vd_[2] = v2; vd_[3] = v3; }          \
   }
 
   f32x16 o[4];
@@ -361,25 +399,25 @@ __global__ __launch_bounds__(256, 2) void attn_flash_bf16(FlashArgs a) {
   GLOAD(0);
   LSTORE(0);
   __syncthreads();
-  // Full blocks, double-buffered; the last block is the only one that can be partial and is
-  // processed after the loop with the key mask (it is already in its stage by then).
-  const int nfull = Lk / BK;
+  // Full blocks; the last block is the only one that can be partial and is processed after the
+  // loop with the key mask (it is already in its stage by then).
+  const int nfull = Lk / KB;
   for (int kb = 0; kb < nfull; kb++) {
     const int st = kb & 1;
     const bool more = kb + 1 < nkb;
     if (more) GLOAD(kb + 1);
-    flash_block_bf16<false>(smem + st * STAGE, smem + st * STAGE + KTILE, qf, o, m, l, c, kb * BK, Lk, lq, hf);
+    flash_block<KB, false>(smem + st * T::STAGE, smem + st * T::STAGE + T::KTILE, qf, o, m, l, c, kb * KB, Lk, lq, hf);
     if (more) LSTORE(st ^ 1);
     __syncthreads();
   }
-  if (tail) {
+  if (nfull < nkb) {
     const int st = nfull & 1;
-    flash_block_bf16<true>(smem + st * STAGE, smem + st * STAGE + KTILE, qf, o, m, l, c, nfull * BK, Lk, lq, hf);
+    flash_block<KB, true>(smem + st * T::STAGE, smem + st * T::STAGE + T::KTILE, qf, o, m, l, c, nfull * KB, Lk, lq, hf);
   }
 #undef GLOAD
 #undef LSTORE
 
-  l += __shfl_xor(l, 32);
+  l = pair_sum(l);
   if (qi < a.Lq) {
     const float inv = 1.0f / l;
     float* dst = a.o + (int64_t)b * a.o_bs + (int64_t)qi * a.ldo + h * HD + 4 * hf;
@@ -391,6 +429,8 @@ __global__ __launch_bounds__(256, 2) void attn_flash_bf16(FlashArgs a) {
             make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
   }
 }
+
+constexpr int FLASH_KB = 64;  // keys per block of the bf16 kernel
 
 // ------------------------------------------------------------------ fp32 MFMA kernel
 
@@ -633,11 +673,12 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
   Launch L(c, bf ? "attn.flash_bf16" : "attn.flash_fp32", flops, 0.0);
   const bool qn = d->q_norm != nullptr;
 #define FLASH(K, N, R) hipLaunchKernelGGL((K<N, R>), dim3(blocks), dim3(256), 0, c->stream, f)
+#define FLASHB(T, N, R) hipLaunchKernelGGL((attn_flash_bf16<T, N, R>), dim3(blocks), dim3(256), 0, c->stream, f)
   if (bf) {
-    if (qn && rope) FLASH(attn_flash_bf16, true, true);
-    else if (qn) FLASH(attn_flash_bf16, true, false);
-    else if (rope) FLASH(attn_flash_bf16, false, true);
-    else FLASH(attn_flash_bf16, false, false);
+    if (qn && rope) FLASHB(FLASH_KB, true, true);
+    else if (qn) FLASHB(FLASH_KB, true, false);
+    else if (rope) FLASHB(FLASH_KB, false, true);
+    else FLASHB(FLASH_KB, false, false);
   } else {
     if (qn && rope) FLASH(attn_flash_fp32, true, true);
     else if (qn) FLASH(attn_flash_fp32, true, false);
@@ -645,6 +686,7 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
     else FLASH(attn_flash_fp32, false, false);
   }
 #undef FLASH
+#undef FLASHB
   return L.end();
 }
 

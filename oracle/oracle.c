@@ -373,8 +373,8 @@ void orc_attention_bf16(const orc_attn* a) {
         for (int d = 0; d < D; d++) o[d] = 0.0;
         for (int j = 0; j < n; j++) {
           float p = exp2f(fmaf(s[j], c, -m));
-          l += (double)p;
           double pb = (double)orc_bf16_round(p);
+          l += pb;
           for (int d = 0; d < D; d++) o[d] += pb * (double)vb[(size_t)j * D + d];
         }
         float* out = a->o + b * a->o_bs + (int64_t)i * a->ldo + a->o_off + (int64_t)h * D;

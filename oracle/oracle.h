@@ -66,7 +66,7 @@ void orc_attention_f64(const orc_attn* a);
 void orc_attention_wgsl(const orc_attn* a);
 /* bf16-MFMA numerics model of this build's kernel: Q, K, V rounded to bf16 (round to
  * nearest even), fp32 scores, p = exp2(fma(s, scale*log2e, -m)) with an integer row
- * offset m, l = sum(p), O = sum(bf16(p) * V) / l. */
+ * offset m, O = sum(bf16(p) * V) / sum(bf16(p)). */
 void orc_attention_bf16(const orc_attn* a);
 
 /* bf16 round-to-nearest-even of an fp32 value, returned as fp32. */
