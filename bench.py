@@ -52,6 +52,22 @@ def cpu_baseline():
     return json.loads(r.stdout.strip().splitlines()[-1])
 
 
+def profiled_traffic(kernel="attn_flash_bf16"):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (copy-kernel calibrated, profiles/attn_flash_bf16_b2_n4096.md), or None."""
+    path = os.path.join(ROOT, "profiles", "attn_flash_bf16_b2_n4096.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 6 and kernel in cells[0]:
+            try:
+                return int(round((float(cells[3]) + float(cells[4])) * 1e6))
+            except ValueError:
+                return None
+    return None
+
+
 def dit_step(args):
     """One full 28-block W4A8 DiT step at 1024x1024, B=2, through the JS -> N-API -> HIP path."""
     import subprocess
@@ -159,7 +175,8 @@ def main():
         "pct_mfma_peak_op": round(100 * value / BF16_PEAK_TFLOPS, 2),
         "roofline": {"bound": "mfma", "kernel": "attn_flash_bf16", "achieved": round(achieved, 3),
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-                     "traffic": None, "kernel_ms": round(k_ms, 5)},
+                     "traffic": profiled_traffic(), "traffic_source": "profiles/attn_flash_bf16_b2_n4096.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+                     "kernel_ms": round(k_ms, 5)},
         "prep_kernel": {"ms": round(prep_ms, 5) if prep_ms else None, "GB/s": round(prep_gbs, 1) if prep_gbs else None,
                         "frac_hbm": round(prep_gbs / HBM_PEAK_GBS, 4) if prep_gbs else None},
     }
