@@ -17,12 +17,13 @@
 //   A operand: lane (m + 32 g) supplies row m, k-group g;  B operand: lane (n + 32 g) supplies
 //   column n, k-group g (the same per-register k order as A);  accumulator register r of lane
 //   (n + 32 g) holds row 8*(r/4) + 4*g + (r%4), column n.
-// Softmax uses exp2 with the scale*log2(e) factor folded into one FMA and an integer running
-// offset m: p = exp2(fma(s, c, -m)).  Integer offsets make the bf16 rounding of p independent
-// of when the offset was raised (a power-of-two rescale), and the offset is raised only when
-// a block maximum exceeds it by more than 8 (p <= 256), so O is rescaled almost never.
-// The bf16 kernel normalizes by the sum of the bf16-rounded p (the weights the P.V MFMA
-// actually uses), the fp32 kernel by the sum of p.
+// Softmax uses exp2 and an integer running offset m.  The bf16 kernel rounds Q*c (c =
+// scale*log2(e)) to bf16 and starts the S accumulators at -m, so p = exp2(S) directly; it has
+// no per-block maximum (an overflow check on the row sums replaces it) and normalizes by the
+// sum of the bf16-rounded p (the weights the P.V MFMA actually uses).  The fp32 kernel uses
+// p = exp2(fma(s, c, -m)), raises m when a block maximum exceeds it by more than 8, and
+// normalizes by the sum of p.  Integer offsets make the rounding of p independent of when
+// the offset was raised (a power-of-two rescale).
 #include <cmath>
 
 #include "common.h"
@@ -267,28 +268,41 @@ struct Tiles {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-// One KB-key block for one wave of 32 queries: S^T = K Q^T on KB/32 key tiles, online softmax
-// with the integer offset m, then O^T += V^T P^T.  Accumulator register r of key tile t holds
-// key 32t + 8(r/4) + 4hf + r%4; P.V k-step s (16 keys) takes registers 8(s%2)..+7 of tile s/2,
-// i.e. keys 16s + 8(j/4) + 4hf + j%4.  V^T rows hold each 16-key group as keys
-// [0-3, 8-11, 4-7, 12-15], so the matching 8 keys of lane half hf are one 16-byte read.
-// MASK: keys >= Lk get -inf (last block only).
-template <int KB, bool MASK>
+// One KB-key block for one wave of 32 queries.  Q arrives pre-scaled by c = scale*log2(e), and
+// the running offset is folded into the accumulator init of S^T = K Q^T (srcC = -m), so the
+// MFMA yields x = s*c - m directly and p = exp2(x) needs no other VALU work.
+//
+// The offset m is an integer that only moves up.  The first block sets it to ceil(block max);
+// later blocks do not compute a maximum at all: the 16 probabilities a lane holds for one key
+// tile are summed anyway (the row sum l), and that sum bounds each of them, so a tile whose
+// lane sum stays <= 2^64 cannot have overflowed.  Only when a lane sum exceeds 2^64 (or is inf)
+// the wave takes the rare path: raise m by ceil(max x) of that tile, rescale O and l by the
+// exact power of two, and recompute the tile's probabilities.  Because m is an integer, the
+// bf16 rounding of every p is independent of when m moved (an exact power-of-two scale), and
+// the largest weight of the first block is >= 1/2, so l never underflows.
+//
+// Accumulator register r of key tile t holds key 32t + 8(r/4) + 4hf + r%4; P.V k-step s
+// (16 keys) takes registers 8(s%2)..+7 of tile s/2, i.e. keys 16s + 8(j/4) + 4hf + j%4.  V^T
+// rows hold each 16-key group as keys [0-3, 8-11, 4-7, 12-15], so the matching 8 keys of lane
+// half hf are one 16-byte read.  The P.V product of tile t is issued right after its
+// probabilities, so its MFMAs overlap the exponentials of tile t+1.
+// MASK: keys >= Lk get -inf (last block only).  FIRST: the block that initializes m.
+constexpr float P_LIMIT = 18446744073709551616.0f;  // 2^64
+
+template <int KB, bool MASK, bool FIRST>
 __device__ __forceinline__ void flash_block(const bf16* __restrict__ K, const bf16* __restrict__ V,
-                                            const bf16x8 (&qf)[8], f32x16 (&o)[4], float& m, float& l, float c,
-                                            int key0, int Lk, int lq, int hf) {
-  constexpr int NKT = KB / 32, NKS = KB / 16;
+                                            const bf16x8 (&qf)[8], f32x16 (&o)[4], float& m, f32x16& negm,
+                                            float& l, int key0, int Lk, int lq, int hf) {
+  constexpr int NKT = KB / 32;
   constexpr int KSP = Tiles<KB>::KSP, VSP = Tiles<KB>::VSP;
   f32x16 s[NKT];
 #pragma unroll
-  for (int t = 0; t < NKT; t++) s[t] = (f32x16){};
+  for (int t = 0; t < NKT; t++) {
+    const bf16* kr = K + (32 * t + lq) * KSP + 8 * hf;
+    s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)kr, qf[0], FIRST ? (f32x16){} : negm, 0, 0, 0);
 #pragma unroll
-  for (int ks = 0; ks < 8; ks++) {
-#pragma unroll
-    for (int t = 0; t < NKT; t++) {
-      const bf16x8 kf = *(const bf16x8*)(K + (32 * t + lq) * KSP + 16 * ks + 8 * hf);
-      s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[t], 0, 0, 0);
-    }
+    for (int ks = 1; ks < 8; ks++)
+      s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)(kr + 16 * ks), qf[ks], s[t], 0, 0, 0);
   }
   if (MASK) {
 #pragma unroll
@@ -297,44 +311,61 @@ __device__ __forceinline__ void flash_block(const bf16* __restrict__ K, const bf
       for (int r = 0; r < 16; r++)
         if (key0 + 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3) >= Lk) s[t][r] = -INFINITY;
   }
-  float bm = s[0][0];
+  if (FIRST) {  // the first block holds at least one valid key of every query: bm is finite
+    float bm = s[0][0];
 #pragma unroll
-  for (int t = 0; t < NKT; t++)
+    for (int t = 0; t < NKT; t++)
 #pragma unroll
-    for (int r = (t == 0 ? 1 : 0); r < 16; r += 2) bm = r + 1 < 16 ? fmaxf(bm, fmaxf(s[t][r], s[t][r + 1])) : fmaxf(bm, s[t][r]);
-  bm = pair_max(bm);
-  const float bmc = bm * c;
-  const bool need = bmc > m + RESCALE_SLACK;
-  if (__builtin_amdgcn_ballot_w64(need)) {  // rare: the running offset moves up
-    const float mn = need ? ceilf(bmc) : m;
-    const float alpha = __builtin_amdgcn_exp2f(m - mn);
-    l *= alpha;
+      for (int r = (t == 0 ? 1 : 0); r < 16; r++) bm = fmaxf(bm, s[t][r]);
+    m = ceilf(pair_max(bm));
 #pragma unroll
-    for (int i = 0; i < 4; i++) o[i] *= alpha;
-    m = mn;
+    for (int t = 0; t < NKT; t++) s[t] -= m;
+    negm = -m;
   }
-  bf16x8 pb[NKS];
-#pragma unroll
-  for (int t = 0; t < NKT; t++)
-#pragma unroll
-    for (int r = 0; r < 16; r++) pb[2 * t + (r >> 3)][r & 7] = to_bf16(__builtin_amdgcn_exp2f(__builtin_fmaf(s[t][r], c, -m)));
-  // row sum of the rounded probabilities (exact convex weights) with bf16 dot2
   const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
-  float l0 = 0.0f, l1 = 0.0f;
 #pragma unroll
-  for (int i = 0; i < NKS; i++) {
-    l0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 0, 1), ones, l0, false);
-    l1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 2, 3), ones, l1, false);
-    l0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 4, 5), ones, l0, false);
-    l1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb[i], pb[i], 6, 7), ones, l1, false);
+  for (int t = 0; t < NKT; t++) {
+    bf16x8 p0, p1;
+    float l0 = 0.0f, l1 = 0.0f;
+#define ANIMA_PROBS()                                                                                        \
+  {                                                                                                          \
+    _Pragma("unroll") for (int r = 0; r < 8; r++) {                                                          \
+      p0[r] = to_bf16(__builtin_amdgcn_exp2f(s[t][r]));                                                      \
+      p1[r] = to_bf16(__builtin_amdgcn_exp2f(s[t][8 + r]));                                                  \
+    }                                                                                                        \
+    l0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p0, p0, 0, 1), ones, 0.0f, false);          \
+    l1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p0, p0, 2, 3), ones, 0.0f, false);          \
+    l0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p0, p0, 4, 5), ones, l0, false);            \
+    l1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p0, p0, 6, 7), ones, l1, false);            \
+    l0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p1, p1, 0, 1), ones, l0, false);            \
+    l1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p1, p1, 2, 3), ones, l1, false);            \
+    l0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p1, p1, 4, 5), ones, l0, false);            \
+    l1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p1, p1, 6, 7), ones, l1, false);            \
   }
-  l += l0 + l1;
+    ANIMA_PROBS();
+    if (!FIRST && __builtin_expect(__builtin_amdgcn_ballot_w64(!(l0 + l1 <= P_LIMIT)) != 0, 0)) {
+      // rare: some probability of this tile exceeds 2^64; move the offset up to its maximum
+      float bm = s[t][0];
 #pragma unroll
-  for (int sk = 0; sk < NKS; sk++) {
+      for (int r = 1; r < 16; r++) bm = fmaxf(bm, s[t][r]);
+      const float d = fmaxf(ceilf(pair_max(bm)), 0.0f);
+      const float alpha = __builtin_amdgcn_exp2f(-d);
+      m += d;
+      negm -= d;
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; i++) o[i] *= alpha;
+#pragma unroll
+      for (int u = t; u < NKT; u++) s[u] -= d;
+      ANIMA_PROBS();
+    }
+#undef ANIMA_PROBS
+    l += l0 + l1;
 #pragma unroll
     for (int dt = 0; dt < 4; dt++) {
-      const bf16x8 va = *(const bf16x8*)(V + (32 * dt + lq) * VSP + 16 * sk + 8 * hf);
-      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[sk], o[dt], 0, 0, 0);
+      const bf16* vr = V + (32 * dt + lq) * VSP + 32 * t + 8 * hf;
+      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)vr, p0, o[dt], 0, 0, 0);
+      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)(vr + 16), p1, o[dt], 0, 0, 0);
     }
   }
 }
@@ -363,7 +394,7 @@ __global__ __launch_bounds__(256, KB == 32 ? 3 : 2) void attn_flash_bf16(FlashAr
 #pragma unroll
     for (int ks = 0; ks < 8; ks++)
 #pragma unroll
-      for (int j = 0; j < 8; j++) qf[ks][j] = to_bf16(x[8 * ks + j]);
+      for (int j = 0; j < 8; j++) qf[ks][j] = to_bf16(x[8 * ks + j] * a.c);
   }
 
   // global -> LDS copy assignment: K row t/(256/KB), KB bytes at (t%(256/KB))*KB;
@@ -393,26 +424,33 @@ __global__ __launch_bounds__(256, KB == 32 ? 3 : 2) void attn_flash_bf16(FlashAr
   f32x16 o[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) o[i] = (f32x16){};
-  float m = -INFINITY, l = 0.0f;
-  const float c = a.c;
+  float m = 0.0f, l = 0.0f;
+  f32x16 negm = {};
 
   GLOAD(0);
   LSTORE(0);
   __syncthreads();
-  // Full blocks; the last block is the only one that can be partial and is processed after the
-  // loop with the key mask (it is already in its stage by then).
+  // Block 0 sets the offset; the last block is the only one that can be partial and is
+  // processed after the loop with the key mask (it is already in its stage by then).
   const int nfull = Lk / KB;
-  for (int kb = 0; kb < nfull; kb++) {
+  if (nkb > 1) GLOAD(1);
+  if (nfull > 0) flash_block<KB, false, true>(smem, smem + T::KTILE, qf, o, m, negm, l, 0, Lk, lq, hf);
+  else flash_block<KB, true, true>(smem, smem + T::KTILE, qf, o, m, negm, l, 0, Lk, lq, hf);
+  if (nkb > 1) LSTORE(1);
+  __syncthreads();
+  for (int kb = 1; kb < nfull; kb++) {
     const int st = kb & 1;
     const bool more = kb + 1 < nkb;
     if (more) GLOAD(kb + 1);
-    flash_block<KB, false>(smem + st * T::STAGE, smem + st * T::STAGE + T::KTILE, qf, o, m, l, c, kb * KB, Lk, lq, hf);
+    flash_block<KB, false, false>(smem + st * T::STAGE, smem + st * T::STAGE + T::KTILE, qf, o, m, negm, l, kb * KB,
+                                  Lk, lq, hf);
     if (more) LSTORE(st ^ 1);
     __syncthreads();
   }
-  if (nfull < nkb) {
+  if (nfull < nkb && nfull > 0) {
     const int st = nfull & 1;
-    flash_block<KB, true>(smem + st * T::STAGE, smem + st * T::STAGE + T::KTILE, qf, o, m, l, c, nfull * KB, Lk, lq, hf);
+    flash_block<KB, true, false>(smem + st * T::STAGE, smem + st * T::STAGE + T::KTILE, qf, o, m, negm, l, nfull * KB,
+                                 Lk, lq, hf);
   }
 #undef GLOAD
 #undef LSTORE
@@ -429,7 +467,6 @@ __global__ __launch_bounds__(256, KB == 32 ? 3 : 2) void attn_flash_bf16(FlashAr
             make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
   }
 }
-
 constexpr int FLASH_KB = 64;  // keys per block of the bf16 kernel
 
 // ------------------------------------------------------------------ fp32 MFMA kernel

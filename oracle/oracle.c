@@ -359,20 +359,19 @@ void orc_attention_bf16(const orc_attn* a) {
       }
       for (int i = 0; i < a->Lq; i++) {
         const float* q = a->q + b * a->q_bs + (int64_t)i * a->ldq + a->q_off + (int64_t)h * D;
-        for (int d = 0; d < D; d++) qb[d] = orc_bf16_round(q[d]);
+        for (int d = 0; d < D; d++) qb[d] = orc_bf16_round(q[d] * c);
         float mx = -INFINITY;
         for (int j = 0; j < n; j++) {
           double acc = 0.0;
           for (int d = 0; d < D; d++) acc += (double)qb[d] * (double)kb[(size_t)j * D + d];
           s[j] = (float)acc;
-          float sc = s[j] * c;
-          if (sc > mx) mx = sc;
+          if (s[j] > mx) mx = s[j];
         }
         const float m = ceilf(mx);
         double l = 0.0;
         for (int d = 0; d < D; d++) o[d] = 0.0;
         for (int j = 0; j < n; j++) {
-          float p = exp2f(fmaf(s[j], c, -m));
+          float p = exp2f(s[j] - m);
           double pb = (double)orc_bf16_round(p);
           l += pb;
           for (int d = 0; d < D; d++) o[d] += pb * (double)vb[(size_t)j * D + d];

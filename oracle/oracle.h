@@ -64,9 +64,11 @@ void orc_attention_f64(const orc_attn* a);
 /* fp32 step-by-step restatement of flashAttentionShader (app/gpu/kernels.js:158-299):
  * 64-row x 32-key tiles, key mask -1e30, natural exp, partial-sum order of the shader. */
 void orc_attention_wgsl(const orc_attn* a);
-/* bf16-MFMA numerics model of this build's kernel: Q, K, V rounded to bf16 (round to
- * nearest even), fp32 scores, p = exp2(fma(s, scale*log2e, -m)) with an integer row
- * offset m, O = sum(bf16(p) * V) / sum(bf16(p)). */
+/* bf16-MFMA numerics model of this build's kernel: Q*c (c = scale*log2e), K and V rounded to
+ * bf16 (round to nearest even), fp32 scores s = bf16(Q c) . bf16(K), p = exp2(s - m) with an
+ * integer row offset m, O = sum(bf16(p) * V) / sum(bf16(p)).  (With an integer m the value
+ * of m only scales every p by the same power of two; the kernel's lazily raised offset and
+ * this row maximum give the same weights.) */
 void orc_attention_bf16(const orc_attn* a);
 
 /* bf16 round-to-nearest-even of an fp32 value, returned as fp32. */

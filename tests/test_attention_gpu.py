@@ -239,6 +239,41 @@ def test_attention_ragged_gqa(ctx, precision):
     assert np.allclose(got[1], np.tile(exp, (Lq, 1)), rtol=tol, atol=1e-6)
 
 
+@pytest.mark.parametrize("precision", ["bf16", "fp32"])
+def test_attention_late_large_scores(ctx, precision):
+    """Scores that grow block by block: keys 64-127 align with the queries at 2x, keys 192-255 at
+    6x (log2-domain scores ~98, past the 2^64 probability limit of the lazily raised offset) and
+    the partial last block at 9x (~147: exp2 overflows to inf before the offset is raised)."""
+    case(f"attention late large scores Lq=64 Lk=300 {precision}")
+    m = amd()
+    H, Lq, Lk = 2, 64, 300
+    u = orc.randn(41, H * HD).reshape(H, HD)
+    q = (u[None] + 0.1 * orc.randn(42, Lq * H * HD).reshape(Lq, H, HD)).reshape(Lq, H * HD).astype(np.float32)
+    gain = np.full(Lk, 0.0, np.float32)
+    gain[64:128], gain[192:256], gain[256:] = 2.0, 6.0, 9.0
+    k = (0.05 * orc.randn(43, Lk * H * HD).reshape(Lk, H, HD) + gain[:, None, None] * u[None]).reshape(Lk, H * HD)
+    k = k.astype(np.float32)
+    v = orc.randn(44, Lk * H * HD).reshape(Lk, H * HD)
+    prec = m.PREC_FP32 if precision == "fp32" else m.PREC_BF16
+    dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
+    do = ctx.empty((Lq, H * HD))
+    ctx.attention(q=dq, k=dk, v=dv, o=do, B=1, Lq=Lq, Lk=Lk, H=H, D=HD, ldq=H * HD, ldk=H * HD, ldv=H * HD,
+                  precision=prec)
+    got = do.numpy()
+    assert np.all(np.isfinite(got))
+    args = dict(B=1, Lq=Lq, Lk=Lk, H=H, D=HD, ldq=H * HD, ldk=H * HD, ldv=H * HD)
+    r, mx = report(f"{precision} vs fp64", got, orc.attention("f64", q, k, v, **args))
+    if precision == "fp32":
+        # raw scores reach ~1150, whose fp32 spacing (1.2e-4) alone moves a weight by ~1e-5
+        assert r <= 1e-4 and mx <= 1e-4
+        assert report("fp32 vs WGSL-order oracle", got, orc.attention("wgsl", q, k, v, **args))[0] <= 1e-4
+    else:
+        # scores this large make the softmax sensitive to the bf16 rounding of Q and K (a 2^-9
+        # relative change of a score of ~147 moves its weight by ~20%), so the fp64 distance is
+        # only reported; the bar is the bf16 numerics model
+        assert report("bf16 vs model", got, orc.attention("bf16", q, k, v, **args))[0] <= 3e-4
+
+
 def test_attention_rejects_bad_arguments(ctx):
     case("attention argument validation")
     m = amd()
