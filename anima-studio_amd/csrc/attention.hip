@@ -268,6 +268,46 @@ struct Tiles {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
+// LDS addressing of the K and V^T fragments a lane reads (tile t = 32 keys, k-step ks = 16 dims,
+// dim tile dt = 32 dims, h = 16-key half of a key tile).
+// Padded layout: K rows of KB keys x (128 + 8) bf16, V^T rows of 128 dims x (KB + 8) bf16.
+template <int KB>
+struct PadAddr {
+  const bf16* kb;  // K + lq*KSP + 8hf
+  const bf16* vb;  // V + lq*VSP + 8hf
+  __device__ __forceinline__ PadAddr(const bf16* K, const bf16* V, int lq, int hf)
+      : kb(K + lq * Tiles<KB>::KSP + 8 * hf), vb(V + lq * Tiles<KB>::VSP + 8 * hf) {}
+  __device__ __forceinline__ bf16x8 k(int t, int ks) const {
+    return *(const bf16x8*)(kb + t * 32 * Tiles<KB>::KSP + 16 * ks);
+  }
+  __device__ __forceinline__ bf16x8 v(int t, int dt, int h) const {
+    return *(const bf16x8*)(vb + dt * 32 * Tiles<KB>::VSP + 32 * t + 16 * h);
+  }
+};
+
+// Swizzled layout of 64-key blocks (direct-to-LDS copies cannot pad rows): K rows of 256 B whose
+// 16-byte unit u sits at slot u ^ (row % 16); V^T rows of 128 B with unit u at u ^ ((row/2) % 8).
+// Any 16 consecutive rows of either tile then map one unit index to 16 distinct bank groups.
+constexpr int SWZ_KT = 64 * HD * 2;  // K tile bytes; the V^T tile follows
+struct SwzOfs {
+  int k[8], v[4];  // lane parts: k[ks] (row lq of key tile 0), v[2t+h] (row lq of dim tile 0)
+  __device__ __forceinline__ SwzOfs(int lq, int hf) {
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) k[ks] = lq * 256 + 16 * ((2 * ks + hf) ^ (lq & 15));
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = SWZ_KT + lq * 128 + 16 * ((2 * j + hf) ^ ((lq >> 1) & 7));
+  }
+};
+struct SwzAddr {
+  const char* st;  // stage base
+  const SwzOfs& of;
+  __device__ __forceinline__ SwzAddr(const char* s, const SwzOfs& o) : st(s), of(o) {}
+  __device__ __forceinline__ bf16x8 k(int t, int ks) const { return *(const bf16x8*)(st + of.k[ks] + t * 32 * 256); }
+  __device__ __forceinline__ bf16x8 v(int t, int dt, int h) const {
+    return *(const bf16x8*)(st + of.v[2 * t + h] + dt * 32 * 128);
+  }
+};
+
 // One KB-key block for one wave of 32 queries.  Q arrives pre-scaled by c = scale*log2(e), and
 // the running offset is folded into the accumulator init of S^T = K Q^T (srcC = -m), so the
 // MFMA yields x = s*c - m directly and p = exp2(x) needs no other VALU work.
@@ -289,20 +329,16 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 // MASK: keys >= Lk get -inf (last block only).  FIRST: the block that initializes m.
 constexpr float P_LIMIT = 18446744073709551616.0f;  // 2^64
 
-template <int KB, bool MASK, bool FIRST>
-__device__ __forceinline__ void flash_block(const bf16* __restrict__ K, const bf16* __restrict__ V,
-                                            const bf16x8 (&qf)[8], f32x16 (&o)[4], float& m, f32x16& negm,
-                                            float& l, int key0, int Lk, int lq, int hf) {
+template <int KB, bool MASK, bool FIRST, class Addr>
+__device__ __forceinline__ void flash_block(const Addr& A, const bf16x8 (&qf)[8], f32x16 (&o)[4], float& m,
+                                            f32x16& negm, float& l, int key0, int Lk, int hf) {
   constexpr int NKT = KB / 32;
-  constexpr int KSP = Tiles<KB>::KSP, VSP = Tiles<KB>::VSP;
   f32x16 s[NKT];
 #pragma unroll
   for (int t = 0; t < NKT; t++) {
-    const bf16* kr = K + (32 * t + lq) * KSP + 8 * hf;
-    s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)kr, qf[0], FIRST ? (f32x16){} : negm, 0, 0, 0);
+    s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.k(t, 0), qf[0], FIRST ? (f32x16){} : negm, 0, 0, 0);
 #pragma unroll
-    for (int ks = 1; ks < 8; ks++)
-      s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)(kr + 16 * ks), qf[ks], s[t], 0, 0, 0);
+    for (int ks = 1; ks < 8; ks++) s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.k(t, ks), qf[ks], s[t], 0, 0, 0);
   }
   if (MASK) {
 #pragma unroll
@@ -363,12 +399,115 @@ __device__ __forceinline__ void flash_block(const bf16* __restrict__ K, const bf
     l += l0 + l1;
 #pragma unroll
     for (int dt = 0; dt < 4; dt++) {
-      const bf16* vr = V + (32 * dt + lq) * VSP + 32 * t + 8 * hf;
-      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)vr, p0, o[dt], 0, 0, 0);
-      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)(vr + 16), p1, o[dt], 0, 0, 0);
+      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.v(t, dt, 0), p0, o[dt], 0, 0, 0);
+      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A.v(t, dt, 1), p1, o[dt], 0, 0, 0);
     }
   }
 }
+
+// Main-path block (64 keys, no mask, offset already set), hand-ordered: sched_barrier(0) fences
+// keep the written order, so each MFMA finds its K / V^T fragment loaded four reads earlier and
+// the exponentials of one key tile sit between the MFMAs of the next product.
+#define ANIMA_SB() __builtin_amdgcn_sched_barrier(0)
+template <class Addr>
+__device__ __forceinline__ void flash_block_main(const Addr& A, const bf16x8 (&qf)[8], f32x16 (&o)[4], float& m,
+                                                 f32x16& negm, float& l) {
+  // fragment i of the block: K reads 0..15 (tile i/8, k-step i%8), V^T reads 16..31
+  // (key tile (i-16)/8, dim tile ((i-16)%8)/2, 16-key half (i-16)%2)
+#define FRAG(i) ((i) < 16 ? A.k((i) >> 3, (i) & 7) : A.v(((i) - 16) >> 3, (((i) - 16) & 7) >> 1, ((i) - 16) & 1))
+  bf16x8 f[4];
+  f32x16 s0, s1;
+  bf16x8 p[4];  // p[0], p[1]: tile 0;  p[2], p[3]: tile 1
+  const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
+  float la = 0.0f, lb = 0.0f;
+  f[0] = FRAG(0); f[1] = FRAG(1); f[2] = FRAG(2); f[3] = FRAG(3);
+  ANIMA_SB();
+  // 2 probabilities of tile T (registers 2k, 2k+1 of S) -> p, row-sum partial
+#define PROB2(S, T, k)                                                                                \
+  {                                                                                                   \
+    bf16x8& pp_ = p[2 * (T) + ((k) >> 2)];                                                            \
+    pp_[2 * ((k) & 3)] = to_bf16(__builtin_amdgcn_exp2f(S[2 * (k)]));                                 \
+    pp_[2 * ((k) & 3) + 1] = to_bf16(__builtin_amdgcn_exp2f(S[2 * (k) + 1]));                         \
+    float& acc_ = ((k) & 1) ? lb : la;                                                                \
+    const bf16x2 pr_ = {pp_[2 * ((k) & 3)], pp_[2 * ((k) & 3) + 1]};                                 \
+    acc_ = __builtin_amdgcn_fdot2_f32_bf16(pr_, ones, acc_, false);                                   \
+  }
+  // S tile 0: MFMAs 0..7, reads 4..11
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i & 3], qf[i], i == 0 ? negm : s0, 0, 0, 0);
+    f[i & 3] = FRAG(i + 4);
+    ANIMA_SB();
+  }
+  // S tile 1: MFMAs 8..15, reads 12..19; tile-0 probabilities between them
+#pragma unroll
+  for (int i = 8; i < 16; i++) {
+    s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i & 3], qf[i - 8], i == 8 ? negm : s1, 0, 0, 0);
+    f[i & 3] = FRAG(i + 4);
+    PROB2(s0, 0, i - 8);
+    ANIMA_SB();
+  }
+  float lt = la + lb;
+  if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(lt <= P_LIMIT)) != 0, 0)) {
+    float bm = s0[0];
+#pragma unroll
+    for (int r = 1; r < 16; r++) bm = fmaxf(bm, s0[r]);
+    const float d = fmaxf(ceilf(pair_max(bm)), 0.0f);
+    const float alpha = __builtin_amdgcn_exp2f(-d);
+    m += d;
+    negm -= d;
+    l *= alpha;
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] *= alpha;
+    s0 -= d;
+    s1 -= d;
+    la = lb = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) PROB2(s0, 0, k);
+    lt = la + lb;
+  }
+  l += lt;
+  la = lb = 0.0f;
+  ANIMA_SB();
+  // P.V tile 0: MFMAs 16..23 (fragments 16..23), reads 20..27; tile-1 probabilities
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    o[j >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[j & 3], p[j & 1], o[j >> 1], 0, 0, 0);
+    f[j & 3] = FRAG(j + 20);
+    PROB2(s1, 1, j);
+    ANIMA_SB();
+  }
+  lt = la + lb;
+  if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(lt <= P_LIMIT)) != 0, 0)) {
+    float bm = s1[0];
+#pragma unroll
+    for (int r = 1; r < 16; r++) bm = fmaxf(bm, s1[r]);
+    const float d = fmaxf(ceilf(pair_max(bm)), 0.0f);
+    const float alpha = __builtin_amdgcn_exp2f(-d);
+    m += d;
+    negm -= d;
+    l *= alpha;
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] *= alpha;
+    s1 -= d;
+    la = lb = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) PROB2(s1, 1, k);
+    lt = la + lb;
+  }
+  l += lt;
+  ANIMA_SB();
+  // P.V tile 1: MFMAs 24..31 (fragments 24..31), reads 28..31
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    o[j >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[j & 3], p[2 + (j & 1)], o[j >> 1], 0, 0, 0);
+    if (j < 4) f[j & 3] = FRAG(j + 28);
+    ANIMA_SB();
+  }
+#undef PROB2
+#undef FRAG
+}
+#undef ANIMA_SB
 
 // 4 waves x 32 queries per workgroup; K/V blocks of KB keys double-buffered in LDS, the next
 // block prefetched into registers while the current one is consumed (one barrier per block).
@@ -434,23 +573,26 @@ __global__ __launch_bounds__(256, KB == 32 ? 3 : 2) void attn_flash_bf16(FlashAr
   // processed after the loop with the key mask (it is already in its stage by then).
   const int nfull = Lk / KB;
   if (nkb > 1) GLOAD(1);
-  if (nfull > 0) flash_block<KB, false, true>(smem, smem + T::KTILE, qf, o, m, negm, l, 0, Lk, lq, hf);
-  else flash_block<KB, true, true>(smem, smem + T::KTILE, qf, o, m, negm, l, 0, Lk, lq, hf);
+  if (nfull > 0) flash_block<KB, false, true>(PadAddr<KB>(smem, smem + T::KTILE, lq, hf), qf, o, m, negm, l, 0, Lk, hf);
+  else flash_block<KB, true, true>(PadAddr<KB>(smem, smem + T::KTILE, lq, hf), qf, o, m, negm, l, 0, Lk, hf);
   if (nkb > 1) LSTORE(1);
   __syncthreads();
   for (int kb = 1; kb < nfull; kb++) {
     const int st = kb & 1;
     const bool more = kb + 1 < nkb;
     if (more) GLOAD(kb + 1);
-    flash_block<KB, false, false>(smem + st * T::STAGE, smem + st * T::STAGE + T::KTILE, qf, o, m, negm, l, kb * KB,
-                                  Lk, lq, hf);
+    if constexpr (KB == 64)
+      flash_block_main(PadAddr<KB>(smem + st * T::STAGE, smem + st * T::STAGE + T::KTILE, lq, hf), qf, o, m, negm, l);
+    else
+      flash_block<KB, false, false>(PadAddr<KB>(smem + st * T::STAGE, smem + st * T::STAGE + T::KTILE, lq, hf), qf, o,
+                                    m, negm, l, kb * KB, Lk, hf);
     if (more) LSTORE(st ^ 1);
     __syncthreads();
   }
   if (nfull < nkb && nfull > 0) {
     const int st = nfull & 1;
-    flash_block<KB, true, false>(smem + st * T::STAGE, smem + st * T::STAGE + T::KTILE, qf, o, m, negm, l, nfull * KB,
-                                 Lk, lq, hf);
+    flash_block<KB, true, false>(PadAddr<KB>(smem + st * T::STAGE, smem + st * T::STAGE + T::KTILE, lq, hf), qf, o, m,
+                                 negm, l, nfull * KB, Lk, hf);
   }
 #undef GLOAD
 #undef LSTORE
@@ -468,6 +610,145 @@ __global__ __launch_bounds__(256, KB == 32 ? 3 : 2) void attn_flash_bf16(FlashAr
   }
 }
 constexpr int FLASH_KB = 64;  // keys per block of the bf16 kernel
+
+// ------------------------------------------------------------------ bf16 kernel, 8 waves
+
+// attn_flash_w8: one workgroup = 8 waves x 32 queries (two waves per SIMD, the per-wave block
+// code of attn_flash_bf16), so each K/V block copied into LDS serves 256 queries (half the copy
+// traffic per query of the 4-wave kernel).  Blocks of 64 keys go straight from global memory
+// into three swizzled LDS stages (global_load_lds_dwordx4, no register staging), issued two
+// blocks ahead of the compute.
+constexpr int W8_BQ = 256;
+constexpr int W8_KB = 64;
+constexpr int W8_ST = 2 * SWZ_KT;  // stage bytes: K tile + V^T tile
+constexpr int W8_NST = 3;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Lane byte offsets (relative to the block's first K row / first V^T key) of this wave's share
+// of a block: 2 + 2 copies of one KiB (K rows 4i..4i+3 and V^T dim rows 8i..8i+7 for
+// i = 2*wave + c), lanes permuted so that the LDS image is the swizzled layout.
+struct W8Load {
+  int k[2], v[2];
+  __device__ __forceinline__ W8Load(int64_t lkp, int wave, int lane) {
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const int i = 2 * wave + c;
+      const int row = 4 * i + (lane >> 4);
+      k[c] = row * (HD * 2) + 16 * ((lane & 15) ^ (row & 15));
+      const int d = 8 * i + (lane >> 3);
+      v[c] = (int)(d * lkp * 2) + 16 * ((lane & 7) ^ ((d >> 1) & 7));
+    }
+  }
+};
+
+// Buffer resources over one head's K rows and V^T rows (raw buffers, byte offsets; reads past
+// num_records return zero).
+struct W8Src {
+  __amdgpu_buffer_rsrc_t k, v;
+};
+
+__device__ __forceinline__ void w8_load(const W8Src& src, const W8Load& lo, int blk, char* stage, int wave) {
+#pragma unroll
+  for (int c = 0; c < 2; c++)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.k, (lds_void_t*)(stage + (2 * wave + c) * 1024), 16, lo.k[c],
+                                             blk * (W8_KB * HD * 2), 0, 0);
+#pragma unroll
+  for (int c = 0; c < 2; c++)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.v, (lds_void_t*)(stage + SWZ_KT + (2 * wave + c) * 1024), 16, lo.v[c],
+                                             blk * (W8_KB * 2), 0, 0);
+}
+
+// Workgroup barrier without a memory fence: the LDS copies a barrier publishes are covered by
+// the explicit vmcnt waits before it, and LDS reads are complete once their MFMAs have issued.
+// The empty asm statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void w8_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// vmcnt(n) only (expcnt and lgkmcnt at their no-wait maxima), gfx9 s_waitcnt encoding.
+#define W8_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+
+template <bool NORM, bool ROPE>
+__global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
+  __shared__ __attribute__((aligned(1024))) char smem[W8_NST * W8_ST];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 31, hf = lane >> 5;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = id / a.n_qt, qt = id - bh * a.n_qt;
+  const int b = bh / a.H, h = bh - b * a.H, hk = h / a.group;
+  const int qi = qt * W8_BQ + wave * 32 + lq;
+  const int Lk = a.kv_len[b];
+  const int nkb = (Lk + W8_KB - 1) / W8_KB;
+  const int head_bytes = a.Lkp * HD * 2;
+  W8Src src;
+  src.k = __builtin_amdgcn_make_buffer_rsrc((void*)((const bf16*)a.kb + ((int64_t)b * a.Hkv + hk) * a.Lkp * HD), (short)0,
+                                            head_bytes, 0x00020000);
+  src.v = __builtin_amdgcn_make_buffer_rsrc((void*)((const bf16*)a.vt + ((int64_t)b * a.Hkv + hk) * HD * a.Lkp), (short)0,
+                                            head_bytes, 0x00020000);
+
+  // blocks 0 and 1 start loading before Q is read and normalized
+  const W8Load lo(a.Lkp, wave, lane);
+  w8_load(src, lo, 0, smem, wave);
+  if (nkb > 1) w8_load(src, lo, 1, smem + W8_ST, wave);
+
+  bf16x8 qf[8];
+  {
+    float x[64];
+    load_q<NORM, ROPE>(a, b, h, qi, hf, x);
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) qf[ks][j] = to_bf16(x[8 * ks + j] * a.c);
+  }
+  const SwzOfs of(lq, hf);
+  f32x16 o[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) o[i] = (f32x16){};
+  float m = 0.0f, l = 0.0f;
+  f32x16 negm = {};
+
+  // Block j lives in stage j % 3.  At the top of iteration j a wave waits for its own copies of
+  // block j (the 4 of block j+1 may still be in flight), the barrier publishes everyone's and
+  // also ends every wave's reads of block j-1, whose stage is then refilled with block j+2.
+  const int nfull = Lk / W8_KB;
+  if (nkb > 1) W8_WAIT_VM(4);
+  else W8_WAIT_VM(0);
+  w8_barrier();
+  if (nkb > 2) w8_load(src, lo, 2, smem + 2 * W8_ST, wave);
+  if (nfull > 0) flash_block<W8_KB, false, true>(SwzAddr(smem, of), qf, o, m, negm, l, 0, Lk, hf);
+  else flash_block<W8_KB, true, true>(SwzAddr(smem, of), qf, o, m, negm, l, 0, Lk, hf);
+  int st = 0;
+  for (int j = 1; j < nfull; j++) {
+    st = st == 2 ? 0 : st + 1;
+    if (j + 1 < nkb) W8_WAIT_VM(4);
+    else W8_WAIT_VM(0);
+    w8_barrier();
+    if (j + 2 < nkb) w8_load(src, lo, j + 2, smem + (st == 0 ? 2 : st - 1) * W8_ST, wave);
+    flash_block_main(SwzAddr(smem + st * W8_ST, of), qf, o, m, negm, l);
+  }
+  if (nfull < nkb && nfull > 0) {
+    st = st == 2 ? 0 : st + 1;
+    W8_WAIT_VM(0);
+    w8_barrier();
+    flash_block<W8_KB, true, false>(SwzAddr(smem + st * W8_ST, of), qf, o, m, negm, l, nfull * W8_KB, Lk, hf);
+  }
+
+  l = pair_sum(l);
+  if (qi < a.Lq) {
+    const float inv = 1.0f / l;
+    float* dst = a.o + (int64_t)b * a.o_bs + (int64_t)qi * a.ldo + h * HD + 4 * hf;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+        *(float4*)(dst + 32 * dt + 8 * g) =
+            make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+  }
+}
+#undef W8_WAIT_VM
 
 // ------------------------------------------------------------------ fp32 MFMA kernel
 
@@ -702,16 +983,25 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
   f.Hkv = Hkv;
   f.Lq = d->Lq;
   f.Lkp = Lkp;
-  f.n_qt = (d->Lq + BQ - 1) / BQ;
+  // 8-wave workgroups (256 queries) when that grid still gives every CU a workgroup
+  const bool w8 = bf && (int64_t)((d->Lq + W8_BQ - 1) / W8_BQ) * d->H * d->B >= c->num_cus;
+  f.n_qt = w8 ? (d->Lq + W8_BQ - 1) / W8_BQ : (d->Lq + BQ - 1) / BQ;
   for (int b = 0; b < MAXB; b++) f.kv_len[b] = b < d->B ? kv_len[b] : 1;
   double flops = 0;
   for (int b = 0; b < d->B; b++) flops += 4.0 * d->Lq * (double)kv_len[b] * HD * d->H;
   const int blocks = f.n_qt * d->H * d->B;
-  Launch L(c, bf ? "attn.flash_bf16" : "attn.flash_fp32", flops, 0.0);
+  Launch L(c, w8 ? "attn.flash_bf16" : bf ? "attn.flash_bf16_4w" : "attn.flash_fp32", flops, 0.0);
   const bool qn = d->q_norm != nullptr;
 #define FLASH(K, N, R) hipLaunchKernelGGL((K<N, R>), dim3(blocks), dim3(256), 0, c->stream, f)
 #define FLASHB(T, N, R) hipLaunchKernelGGL((attn_flash_bf16<T, N, R>), dim3(blocks), dim3(256), 0, c->stream, f)
-  if (bf) {
+  if (w8) {
+#define FLASH8(N, R) hipLaunchKernelGGL((attn_flash_w8<N, R>), dim3(blocks), dim3(512), 0, c->stream, f)
+    if (qn && rope) FLASH8(true, true);
+    else if (qn) FLASH8(true, false);
+    else if (rope) FLASH8(false, true);
+    else FLASH8(false, false);
+#undef FLASH8
+  } else if (bf) {
     if (qn && rope) FLASHB(FLASH_KB, true, true);
     else if (qn) FLASHB(FLASH_KB, true, false);
     else if (rope) FLASHB(FLASH_KB, false, true);

@@ -28,6 +28,7 @@ struct Stat {
 
 struct anima_ctx {
   int device = 0;
+  int num_cus = 256;  // compute units of the device (grid-size decisions)
   hipStream_t stream = nullptr;
   std::string err;
   bool lost = false;

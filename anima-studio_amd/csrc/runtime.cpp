@@ -141,6 +141,7 @@ int anima_init(int device, anima_ctx** out) {
   if (e != hipSuccess) return fail(nullptr, ANIMA_E_HIP, "hipSetDevice: %s", hipGetErrorString(e));
   anima_ctx* c = new anima_ctx();
   c->device = device;
+  c->num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreate(&c->t0);
   if (e == hipSuccess) e = hipEventCreate(&c->t1);

@@ -274,6 +274,45 @@ def test_attention_late_large_scores(ctx, precision):
         assert report("bf16 vs model", got, orc.attention("bf16", q, k, v, **args))[0] <= 3e-4
 
 
+def test_attention_8wave_kernel_key_lengths(ctx):
+    """16 batches x 16 heads x 256 queries: 256 workgroups of 256 queries, the grid that selects the
+    8-wave direct-to-LDS kernel (checked through the profiler name).  Per-batch key lengths cover 1,
+    2 and 3+ blocks of 64 with and without a partial tail; batches 8-15 get keys that align with the
+    queries at 2x / 6x / 9x in later blocks (the overflow-triggered offset raise)."""
+    case("attention 8-wave kernel B=16 H=16 Lq=256 Lk=320 ragged key lengths")
+    m = amd()
+    B, H, Lq, Lk = 16, 16, 256, 320
+    kv_len = np.array([1, 63, 64, 65, 128, 129, 192, 200, 256, 257, 300, 320, 320, 320, 31, 2], np.int32)
+    q = orc.randn(51, B * Lq * H * HD).reshape(B, Lq, H, HD)
+    k = orc.randn(52, B * Lk * H * HD).reshape(B, Lk, H, HD)
+    v = orc.randn(53, B * Lk * H * HD).reshape(B, Lk, H, HD).reshape(B, Lk, H * HD)
+    u = orc.randn(54, H * HD).reshape(H, HD)
+    gain = np.zeros(Lk, np.float32)
+    gain[64:128], gain[192:256], gain[256:] = 2.0, 6.0, 9.0
+    q[8:] = u[None, None] + 0.1 * q[8:]
+    k[8:] = 0.05 * k[8:] + gain[None, :, None, None] * u[None, None]
+    q = q.reshape(B, Lq, H * HD).astype(np.float32)
+    k = k.reshape(B, Lk, H * HD).astype(np.float32)
+    dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
+    do = ctx.empty((B, Lq, H * HD))
+    ctx.profile(True)
+    ctx.profile_reset()
+    ctx.attention(q=dq, k=dk, v=dv, o=do, B=B, Lq=Lq, Lk=Lk, H=H, D=HD, ldq=H * HD, ldk=H * HD, ldv=H * HD,
+                  kv_len=kv_len, precision=m.PREC_BF16)
+    names = {r["name"] for r in ctx.profile_report()}
+    ctx.profile(False)
+    assert "attn.flash_bf16" in names, names
+    got = do.numpy()
+    assert np.all(np.isfinite(got))
+    args = dict(B=B, Lq=Lq, Lk=Lk, H=H, D=HD, ldq=H * HD, ldk=H * HD, ldv=H * HD, kv_len=kv_len)
+    model = orc.attention("bf16", q, k, v, **args)
+    for b in range(B):
+        assert report(f"b={b} kv_len={kv_len[b]} bf16 vs model", got[b], model[b])[0] <= 3e-4
+    # batches 0-7 (no contrived scores): the fp64 distance stays at the bf16-operand level
+    ref64 = orc.attention("f64", q[:8], k[:8], v[:8], **{**args, "B": 8, "kv_len": kv_len[:8]})
+    assert report("b<8 bf16 vs fp64", got[:8], ref64)[0] <= 1e-2
+
+
 def test_attention_rejects_bad_arguments(ctx):
     case("attention argument validation")
     m = amd()
