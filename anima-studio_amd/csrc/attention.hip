@@ -191,14 +191,6 @@ struct FlashArgs {
   int kv_len[MAXB];
 };
 
-// Workgroup id -> (batch*head, query tile).  Consecutive workgroup ids are dispatched
-// round-robin over the 8 XCDs; remapping gives each XCD a contiguous range of query tiles,
-// so the workgroups that share one head's K/V run on the same XCD (same L2).
-__device__ __forceinline__ int xcd_remap(int id, int total) {
-  if ((total & 7) != 0) return id;
-  return (id & 7) * (total >> 3) + (id >> 3);
-}
-
 // Loads this lane's 64 Q values (query qi, dims 16ks + 8hf + j), applies the fused
 // RMSNorm + RoPE, and returns them in x[ks*8 + j].
 template <bool NORM, bool ROPE>

@@ -37,4 +37,12 @@ __device__ __forceinline__ float tree_sum_down(float v, int n) {
   return v;
 }
 
+// Workgroup id -> work item.  Consecutive workgroup ids are dispatched round-robin over the 8
+// XCDs; remapping gives each XCD a contiguous range of work items, so neighbouring items (one
+// attention head's query tiles, one GEMM row of tiles) run on the same XCD and share its L2.
+__device__ __forceinline__ int xcd_remap(int id, int total) {
+  if ((total & 7) != 0) return id;
+  return (id & 7) * (total >> 3) + (id >> 3);
+}
+
 }  // namespace anima

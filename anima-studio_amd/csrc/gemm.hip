@@ -223,6 +223,198 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
   }
 }
 
+// Epilogue of one 32x32 accumulator tile for lane (n + 32g): register r holds row
+// m0 + 8(r/4) + r%4 (m0 already includes 4g) of column n.  Every load the tile needs (row scales,
+// the residual C) is issued before the first store, so the tile waits for memory once instead
+// of once per element (a load after a store to the same buffer may not be moved above it).
+// Arithmetic order is that of epilogue_store.
+__device__ __forceinline__ void epilogue_tile(const GemmArgs& a, i32x16 v, int m0, int n) {
+  if (n >= a.N) return;
+  const float swn = a.sw[n];
+  const float bias = a.bias ? a.bias[n] : 0.0f;
+  const float gate = a.epi == ANIMA_EPI_GATED ? a.gate[a.gate_off + n] : 0.0f;
+  float sxv[16], cv[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int m = m0 + 8 * (r >> 2) + (r & 3);
+    const bool ok = m < a.M;
+    sxv[r] = ok ? a.sx[m] : 0.0f;
+    cv[r] = ok && a.epi != ANIMA_EPI_STORE ? a.out[(int64_t)m * a.ldc + n] : 0.0f;
+  }
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int m = m0 + 8 * (r >> 2) + (r & 3);
+    if (m >= a.M) continue;
+    if (a.acc_out) a.acc_out[(int64_t)m * a.N + n] = v[r];
+    float y = (float)v[r] * sxv[r];
+    y = y * swn;
+    if (a.alpha != 1.0f) y = y * a.alpha;
+    if (a.bias) y = y + bias;
+    y = apply_act(y, a.act);
+    float* c = a.out + (int64_t)m * a.ldc + n;
+    if (a.epi == ANIMA_EPI_STORE) *c = y;
+    else if (a.epi == ANIMA_EPI_RESID) *c = cv[r] + y;
+    else *c = __builtin_fmaf(gate, y, cv[r]);
+  }
+}
+
+// ------------------------------------------------------------------ 256x256 int8 kernel
+//
+// gemm_i8_256: persistent workgroups (one per CU), each walking a list of 256 x 256 output
+// tiles as one stream of k stages, so the next tile's first copies are in flight while the
+// current tile's epilogue runs.  8 waves (two per SIMD); wave w owns
+// rows (w%2)*128 .. +128 and columns (w/2)*64 .. +64 (4 x 2 MFMA tiles, 128 accumulator
+// registers).  K advances in stages of 64 bytes; four LDS stages (A tile + B tile, 16 KiB each)
+// are filled three stages ahead by buffer_load_dwordx4 ... lds straight from global memory.
+// Buffer resources cover the workgroup's rows only, so rows past M (N) read as zero.
+// LDS tile layout: row r (an M row of A or an N row of B) holds four 16-byte k units; unit u is
+// stored at slot u ^ ((r / 4) % 4), which spreads one unit index of 16 consecutive rows over
+// 16 distinct bank groups (rows 4 apart would otherwise share banks in 64-byte rows).
+constexpr int G2_BK = 64;               // k bytes per stage
+constexpr int G2_TILE = 256 * G2_BK;    // bytes of one operand tile
+constexpr int G2_ST = 2 * G2_TILE;      // stage: A tile, then B tile
+constexpr int G2_NST = 4;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Workgroup barrier without a memory fence: LDS copies are covered by explicit vmcnt waits and
+// LDS reads complete before the MFMAs that consume them issue; the empty asm statements stop
+// the compiler from moving memory accesses across it.
+__device__ __forceinline__ void g2_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// vmcnt(n) only (expcnt and lgkmcnt at their no-wait maxima), gfx9 s_waitcnt encoding.
+#define G2_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+
+__global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
+  __shared__ __attribute__((aligned(1024))) char smem[G2_NST * G2_ST];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 31, hf = lane >> 5;
+  const int ntn = (a.N + 255) / 256;
+  const int ntiles = ntn * ((a.M + 255) / 256);
+  const int wm = (wave & 1) * 128, wn = (wave >> 1) * 64;
+  const int K = a.K;
+  const int nk = K / G2_BK;
+
+  // Persistent workgroups: with one workgroup per CU (gridDim.x a multiple of 8, dispatched
+  // round-robin over the XCDs), XCD x owns the contiguous tile range [x*R, (x+1)*R) and its
+  // workgroups stride through it, so the tiles of one row of A stay on one L2.  Otherwise
+  // workgroup b takes tiles b, b + gridDim.x, ...
+  const bool xcd = (gridDim.x & 7) == 0;
+  const int per = xcd ? (ntiles + 7) / 8 : ntiles;
+  const int first = xcd ? (blockIdx.x & 7) * per + (blockIdx.x >> 3) : blockIdx.x;
+  const int stride = xcd ? (int)(gridDim.x >> 3) : (int)gridDim.x;
+  const int last = xcd ? min(ntiles, ((int)(blockIdx.x & 7) + 1) * per) : ntiles;
+  const int mine = first < last ? (last - first + stride - 1) / stride : 0;
+  const int total = mine * nk;  // stages of this workgroup's stream (tile-major)
+
+  // this wave's two 1 KiB chunks of each tile: rows 16*(2*wave + c) + lane/4, unit permuted
+  const int row0 = 32 * wave + (lane >> 2), row1 = row0 + 16;
+  const int loff0 = row0 * K + 16 * ((lane & 3) ^ ((row0 >> 2) & 3));
+  const int loff1 = row1 * K + 16 * ((lane & 3) ^ ((row1 >> 2) & 3));
+  // stage g of the stream: tile g / nk, k bytes (g % nk) * 64, LDS stage g % 4.  Buffer
+  // resources cover the tile's rows only, so rows past M (N) read as zero.
+#define G2_ISSUE(g_)                                                                                          \
+  {                                                                                                           \
+    const int k_ = (g_) / nk, s_ = (g_) - k_ * nk;                                                            \
+    const int t_ = first + k_ * stride, tm_ = t_ / ntn;                                                       \
+    const int bm_ = tm_ * 256, bn_ = (t_ - tm_ * ntn) * 256;                                                  \
+    const __amdgpu_buffer_rsrc_t ra_ = __builtin_amdgcn_make_buffer_rsrc(                                     \
+        (void*)(a.qx + (int64_t)bm_ * K), (short)0, min(256, a.M - bm_) * K, 0x00020000);                     \
+    const __amdgpu_buffer_rsrc_t rb_ = __builtin_amdgcn_make_buffer_rsrc(                                     \
+        (void*)((const int8_t*)a.w + (int64_t)bn_ * K), (short)0, min(256, a.N - bn_) * K, 0x00020000);        \
+    char* st_ = smem + ((g_) & (G2_NST - 1)) * G2_ST;                                                         \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_, (lds_void_t*)(st_ + (2 * wave) * 1024), 16, loff0, s_ * G2_BK, 0, 0); \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_, (lds_void_t*)(st_ + (2 * wave + 1) * 1024), 16, loff1, s_ * G2_BK, 0, 0); \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_, (lds_void_t*)(st_ + G2_TILE + (2 * wave) * 1024), 16, loff0,          \
+                                             s_ * G2_BK, 0, 0);                                               \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_, (lds_void_t*)(st_ + G2_TILE + (2 * wave + 1) * 1024), 16, loff1,      \
+                                             s_ * G2_BK, 0, 0);                                               \
+  }
+  // fragment lane offsets: row lq of a 32-row tile, unit 2*ks + hf (k-step ks of 32 bytes)
+  int fofs[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) fofs[ks] = lq * G2_BK + 16 * ((2 * ks + hf) ^ ((lq >> 2) & 3));
+
+  i32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = (i32x16){};
+
+  // Stage g is published (barrier) one iteration before it is computed, so the fragment reads
+  // of its first k-step run under the MFMAs of stage g-1's second k-step.
+  i32x4 af0[4], bf0[2], af1[4], bf1[2];
+  if (total > 0) G2_ISSUE(0);
+  if (total > 1) G2_ISSUE(1);
+  if (total > 2) G2_ISSUE(2);
+  if (total > 2) G2_WAIT_VM(8);
+  else if (total > 1) G2_WAIT_VM(4);
+  else G2_WAIT_VM(0);
+  g2_barrier();
+  if (total > 0) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) af0[i] = *(const i32x4*)(smem + (wm + 32 * i) * G2_BK + fofs[0]);
+#pragma unroll
+    for (int j = 0; j < 2; j++) bf0[j] = *(const i32x4*)(smem + G2_TILE + (wn + 32 * j) * G2_BK + fofs[0]);
+  }
+  int s = 0, k = 0;  // stage within the tile, tile index within this workgroup's list
+  for (int g = 0; g < total; g++) {
+    // publish stage g+1: this wave's copies of it are done once at most those of g+2 are
+    // pending; the barrier also ends every wave's reads of stage g-1, which is refilled with g+3
+    if (g + 2 < total) G2_WAIT_VM(4);
+    else G2_WAIT_VM(0);
+    g2_barrier();
+    if (g + 3 < total) G2_ISSUE(g + 3);
+    // Hand-ordered (sched_barrier fences keep the written order): each MFMA of one k-step is
+    // followed by one fragment read for the next k-step, B fragments first, so a fragment is
+    // read at least three MFMAs (~100 cycles) before its first use.  The second k-step reads
+    // stage g+1 (unconditionally: after the last stage this reads a stale stage whose values
+    // are unused; a branch here would make the compiler drain all LDS reads first).
+    const char* st = smem + (g & (G2_NST - 1)) * G2_ST;
+    const char* sn = smem + ((g + 1) & (G2_NST - 1)) * G2_ST;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      acc[q >> 1][q & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af0[q >> 1], bf0[q & 1], acc[q >> 1][q & 1], 0, 0, 0);
+      if (q < 2) bf1[q] = *(const i32x4*)(st + G2_TILE + (wn + 32 * q) * G2_BK + fofs[1]);
+      else if (q < 6) af1[q - 2] = *(const i32x4*)(st + (wm + 32 * (q - 2)) * G2_BK + fofs[1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      acc[q >> 1][q & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af1[q >> 1], bf1[q & 1], acc[q >> 1][q & 1], 0, 0, 0);
+      if (q < 2) bf0[q] = *(const i32x4*)(sn + G2_TILE + (wn + 32 * q) * G2_BK + fofs[0]);
+      else if (q < 6) af0[q - 2] = *(const i32x4*)(sn + (wm + 32 * (q - 2)) * G2_BK + fofs[0]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (++s == nk) {
+      // tile done: epilogue (the next tile's first stages are already in flight), one 32x32
+      // tile at a time, written out (a loop over the tiles is not fully unrolled at this size,
+      // and a run-time tile index would put the accumulators in scratch memory)
+      const int t = first + k * stride, tm = t / ntn;
+      const int m0 = tm * 256 + wm + 4 * hf, n0 = (t - tm * ntn) * 256 + wn + lq;
+      epilogue_tile(a, acc[0][0], m0, n0);
+      epilogue_tile(a, acc[0][1], m0, n0 + 32);
+      epilogue_tile(a, acc[1][0], m0 + 32, n0);
+      epilogue_tile(a, acc[1][1], m0 + 32, n0 + 32);
+      epilogue_tile(a, acc[2][0], m0 + 64, n0);
+      epilogue_tile(a, acc[2][1], m0 + 64, n0 + 32);
+      epilogue_tile(a, acc[3][0], m0 + 96, n0);
+      epilogue_tile(a, acc[3][1], m0 + 96, n0 + 32);
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = (i32x16){};
+      s = 0;
+      k++;
+    }
+  }
+}
+#undef G2_WAIT_VM
+#undef G2_ISSUE
+
 // ------------------------------------------------------------------ bf16 weights, fp32 math
 
 struct F32WArgs {
@@ -404,9 +596,14 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
   int rc;
   {
     Launch L(c, w4 ? "gemm.w4a8" : "gemm.i8", 2.0 * M * N * K, 0.0);
-    dim3 grid((N + GBN - 1) / GBN, (unsigned)((M + GBM - 1) / GBM));
-    if (w4) hipLaunchKernelGGL(gemm_i8_kernel<true>, grid, dim3(256), 0, c->stream, g);
-    else hipLaunchKernelGGL(gemm_i8_kernel<false>, grid, dim3(256), 0, c->stream, g);
+    const int64_t tiles256 = (int64_t)((N + 255) / 256) * ((M + 255) / 256);
+    if (!w4 && tiles256 >= c->num_cus && tiles256 <= 0x7fffffff) {
+      hipLaunchKernelGGL(gemm_i8_256, dim3((unsigned)c->num_cus), dim3(512), 0, c->stream, g);
+    } else {
+      dim3 grid((N + GBN - 1) / GBN, (unsigned)((M + GBM - 1) / GBM));
+      if (w4) hipLaunchKernelGGL(gemm_i8_kernel<true>, grid, dim3(256), 0, c->stream, g);
+      else hipLaunchKernelGGL(gemm_i8_kernel<false>, grid, dim3(256), 0, c->stream, g);
+    }
     rc = L.end();
   }
   if (tmp) anima_free(c, tmp);  // stream-ordered reuse

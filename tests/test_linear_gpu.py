@@ -192,6 +192,34 @@ def test_out_projection_gated_epilogue(ctx, kind):
     assert np.array_equal(dout.numpy(), orc.linear_epilogue(orc.gemm_i8(qx, grid), sx, sw, bias=bias, epi=1, c=resid))
 
 
+def test_i8_256_tile_kernel_ragged_edges(ctx):
+    """M=4000, N=4100: 16 x 17 tiles of 256 (the 256x256 direct-to-LDS kernel), partial last
+    row and column tiles (rows / columns past the edge read as zero through the buffer bounds);
+    gated residual + bias epilogue and the int32 accumulators bit-exact on sampled rows,
+    including the last ones, and the accumulator checksums over the whole product."""
+    case("int8 256x256-tile kernel M=4000 N=4100 K=1024 gated + bias")
+    m = amd()
+    M, K, N = 4000, 1024, 4100
+    x = orc.randn(91, M * K).reshape(M, K)
+    qx, sx = orc.token_quant(orc.hadamard256(x))
+    qw, sw = int8_weight(92, N, K)
+    bias = (0.1 * orc.randn(93, N)).astype(np.float32)
+    mod = orc.randn(94, 3 * N).astype(np.float32)
+    resid = orc.randn(95, M * N).reshape(M, N)
+    W = m.weight(m.W_I8, N, K, ctx.upload(qw), scale=ctx.upload(sw), bias=ctx.upload(bias))
+    dout, dacc = ctx.upload(resid), ctx.empty((M, N), np.int32)
+    ctx.linear(W, M, dout, xq=ctx.upload(qx), xs=ctx.upload(sx), epilogue=m.EPI_GATED, gate=ctx.upload(mod),
+               gate_off=N, acc_out=dacc)
+    acc, got = dacc.numpy(), dout.numpy()
+    assert checksums_ok(qx, qw, acc), "int32 accumulator checksums"
+    rows = np.unique(np.concatenate([np.arange(0, 4), np.random.default_rng(1).choice(M, 16, replace=False),
+                                     np.arange(M - 20, M)]))
+    ref_acc = orc.gemm_i8(qx[rows], qw)
+    assert np.array_equal(acc[rows], ref_acc)
+    ref = orc.linear_epilogue(ref_acc, sx[rows], sw, bias=bias, epi=2, gate=mod, g_off=N, c=resid[rows])
+    assert np.array_equal(got[rows], ref), report("gated", got[rows], ref)
+
+
 @pytest.mark.parametrize("act", ["gelu", "silu"])
 def test_mlp1_activation_epilogue(ctx, act):
     case(f"mlp1 2048 -> 8192 {act} M=200 and mlp2 8192 -> 2048")
