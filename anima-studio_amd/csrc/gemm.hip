@@ -415,6 +415,44 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
 #undef G2_WAIT_VM
 #undef G2_ISSUE
 
+// ------------------------------------------------------------------ W4 -> int8 decode pass
+//
+// For the 256x256 kernel a W4 weight is decoded once per call into an int8 workspace (the
+// in-GEMM decode repeats it for every 256-row band of M).  Thread = 32 weights: 16 bytes of
+// codes (low nibble = even k) and their two fp8 s_rel bytes; the 16-entry tables of all 256
+// s_rel values are built in LDS per workgroup exactly as in gemm_i8_kernel<true>.
+__global__ __launch_bounds__(256) void w4_decode_kernel(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ srel,
+                                                        const float* __restrict__ cb, int8_t* __restrict__ out, int64_t nchunk,
+                                                        int K) {
+  __shared__ __attribute__((aligned(16))) uint32_t lut[256 * 4];
+  for (int i = threadIdx.x; i < 256 * 4; i += 256) {
+    const float s = fp8e4m3((uint32_t)(i >> 2));
+    uint32_t packed = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float v = rintf(cb[4 * (i & 3) + j] * s);
+      v = fminf(fmaxf(v, -127.0f), 127.0f);
+      packed |= ((uint32_t)(int32_t)v & 0xffu) << (8 * j);
+    }
+    lut[i] = packed;
+  }
+  __syncthreads();
+  const int cpr = K / 32;  // chunks of 32 weights per row
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nchunk; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = i / cpr;
+    const int c = (int)(i - row * cpr);
+    const uint4 w = *(const uint4*)(codes + row * (K / 2) + 16 * c);
+    const uint8_t* sp = srel + row * (K / 16) + 2 * c;
+    const uint4 t0 = *(const uint4*)&lut[4 * sp[0]];
+    const uint4 t1 = *(const uint4*)&lut[4 * sp[1]];
+    const uint2 d0 = decode8(w.x, t0.x, t0.y, t0.z, t0.w), d1 = decode8(w.y, t0.x, t0.y, t0.z, t0.w);
+    const uint2 d2 = decode8(w.z, t1.x, t1.y, t1.z, t1.w), d3 = decode8(w.w, t1.x, t1.y, t1.z, t1.w);
+    uint4* o = (uint4*)(out + row * K + 32 * c);
+    o[0] = make_uint4(d0.x, d0.y, d1.x, d1.y);
+    o[1] = make_uint4(d2.x, d2.y, d3.x, d3.y);
+  }
+}
+
 // ------------------------------------------------------------------ bf16 weights, fp32 math
 
 struct F32WArgs {
@@ -593,11 +631,29 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
   }
   GemmArgs g{qx, sx, W->w, W->scale, W->srel, W->codebook, W->bias, d->out, ldc, alpha, d->act, d->epilogue,
              d->gate, d->gate_off, d->acc_out, (int)M, N, K};
-  int rc;
-  {
+  int rc = ANIMA_OK;
+  // Grids that give every CU a 256x256 tile run the persistent 256 kernel; a W4 weight is then
+  // decoded once into an int8 workspace first.  Smaller grids run the 128x128 kernel, which
+  // decodes W4 inside the GEMM.
+  const int64_t tiles256 = (int64_t)((N + 255) / 256) * ((M + 255) / 256);
+  const bool big = tiles256 >= c->num_cus && tiles256 <= 0x7fffffff;
+  void* wdec = nullptr;
+  if (big && w4) {
+    if ((rc = anima_alloc(c, (size_t)N * K, &wdec))) {
+      if (tmp) anima_free(c, tmp);
+      return rc;
+    }
+    const int64_t nchunk = (int64_t)N * (K / 32);
+    Launch L(c, "w4.decode", 0.0, (double)N * K * 1.5 + (double)N * K / 16);
+    const int64_t blocks = (nchunk + 255) / 256;
+    hipLaunchKernelGGL(w4_decode_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, c->stream,
+                       (const uint8_t*)W->w, W->srel, W->codebook, (int8_t*)wdec, nchunk, K);
+    rc = L.end();
+    g.w = wdec;
+  }
+  if (rc == ANIMA_OK) {
     Launch L(c, w4 ? "gemm.w4a8" : "gemm.i8", 2.0 * M * N * K, 0.0);
-    const int64_t tiles256 = (int64_t)((N + 255) / 256) * ((M + 255) / 256);
-    if (!w4 && tiles256 >= c->num_cus && tiles256 <= 0x7fffffff) {
+    if (big) {
       hipLaunchKernelGGL(gemm_i8_256, dim3((unsigned)c->num_cus), dim3(512), 0, c->stream, g);
     } else {
       dim3 grid((N + GBN - 1) / GBN, (unsigned)((M + GBM - 1) / GBM));
@@ -606,7 +662,8 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
     }
     rc = L.end();
   }
-  if (tmp) anima_free(c, tmp);  // stream-ordered reuse
+  if (wdec) anima_free(c, wdec);  // stream-ordered reuse
+  if (tmp) anima_free(c, tmp);
   return rc;
 }
 

@@ -192,21 +192,29 @@ def test_out_projection_gated_epilogue(ctx, kind):
     assert np.array_equal(dout.numpy(), orc.linear_epilogue(orc.gemm_i8(qx, grid), sx, sw, bias=bias, epi=1, c=resid))
 
 
-def test_i8_256_tile_kernel_ragged_edges(ctx):
-    """M=4000, N=4100: 16 x 17 tiles of 256 (the 256x256 direct-to-LDS kernel), partial last
-    row and column tiles (rows / columns past the edge read as zero through the buffer bounds);
-    gated residual + bias epilogue and the int32 accumulators bit-exact on sampled rows,
-    including the last ones, and the accumulator checksums over the whole product."""
-    case("int8 256x256-tile kernel M=4000 N=4100 K=1024 gated + bias")
+@pytest.mark.parametrize("kind", ["i8", "w4"])
+def test_256_tile_kernel_ragged_edges(ctx, kind):
+    """M=4000, N=4100: 16 x 17 tiles of 256 (the 256x256 persistent kernel), partial last row
+    and column tiles (rows / columns past the edge read as zero through the buffer bounds; W4
+    rows past N decode to zero); gated residual + bias epilogue and the int32 accumulators
+    bit-exact on sampled rows, including the last ones, and the accumulator checksums over the
+    whole product."""
+    case(f"256x256-tile kernel M=4000 N=4100 K=1024 gated + bias {kind}")
     m = amd()
     M, K, N = 4000, 1024, 4100
     x = orc.randn(91, M * K).reshape(M, K)
     qx, sx = orc.token_quant(orc.hadamard256(x))
-    qw, sw = int8_weight(92, N, K)
     bias = (0.1 * orc.randn(93, N)).astype(np.float32)
     mod = orc.randn(94, 3 * N).astype(np.float32)
     resid = orc.randn(95, M * N).reshape(M, N)
-    W = m.weight(m.W_I8, N, K, ctx.upload(qw), scale=ctx.upload(sw), bias=ctx.upload(bias))
+    if kind == "i8":
+        qw, sw = int8_weight(92, N, K)
+        W = m.weight(m.W_I8, N, K, ctx.upload(qw), scale=ctx.upload(sw), bias=ctx.upload(bias))
+    else:
+        codes, srel, sw = w4_weight(96, N, K)
+        W = m.weight(m.W_W4, N, K, ctx.upload(codes), scale=ctx.upload(sw), srel=ctx.upload(srel),
+                     codebook=ctx.upload(FIXED_LUT), bias=ctx.upload(bias))
+        qw = orc.w4_decode(codes, srel, FIXED_LUT, N, K)
     dout, dacc = ctx.upload(resid), ctx.empty((M, N), np.int32)
     ctx.linear(W, M, dout, xq=ctx.upload(qx), xs=ctx.upload(sx), epilogue=m.EPI_GATED, gate=ctx.upload(mod),
                gate_off=N, acc_out=dacc)
