@@ -117,20 +117,20 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return r;
 }
 
-// Per-token int8 of the row held in S (256 threads): s = amax/127, q = clamp(rint(x/s)).
+// Per-token int8 of the row held in S (256 threads): s = amax/127, q = clamp(rint(x * (127/amax))).
 __device__ __forceinline__ void quant_row(const float* S, int cols, float* red, int8_t* q, float* s_out) {
   const int t = threadIdx.x;
   float amax = 0.0f;
   for (int c = t; c < cols; c += 256) amax = fmaxf(amax, fabsf(S[c]));
   amax = block_max(amax, red);
-  const float s = amax / 127.0f;
+  const float s = amax / 127.0f, inv = 127.0f / amax;
   if (t == 0) *s_out = s;
   for (int c4 = t; c4 < (cols >> 2); c4 += 256) {
     char4 o;
     int8_t* ob = (int8_t*)&o;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      float v = amax == 0.0f ? 0.0f : rintf(S[4 * c4 + j] / s);
+      float v = amax == 0.0f ? 0.0f : rintf(S[4 * c4 + j] * inv);
       v = fminf(fmaxf(v, -127.0f), 127.0f);
       ob[j] = (int8_t)v;
     }
@@ -165,24 +165,9 @@ __global__ __launch_bounds__(256) void hadamard_kernel(const float* X, float* Y,
     for (int j = 0; j < 4; j++) Y[g * 256 + t + 64 * j] = s[t + 64 * j] * 0.0625f;
 }
 
-// One workgroup per row: optional ConvRot rotation, then per-token int8.
-__global__ __launch_bounds__(256) void quant_rows_kernel(const float* X, int K, int rotate, int8_t* Q, float* S_out) {
-  extern __shared__ float S[];
-  __shared__ float red[256];
-  const int64_t row = blockIdx.x;
-  const float* x = X + row * K;
-  for (int c4 = threadIdx.x; c4 < (K >> 2); c4 += 256) *(float4*)(S + 4 * c4) = *(const float4*)(x + 4 * c4);
-  __syncthreads();
-  if (rotate) {
-    butterfly_rows(S, K);
-    for (int c = threadIdx.x; c < K; c += 256) S[c] = S[c] * 0.0625f;
-    __syncthreads();
-  }
-  quant_row(S, K, red, Q + row * K, S_out + row);
-}
-
 // LayerNorm (no affine) + adaLN modulation (+ Hadamard) (+ int8), one workgroup per row
-// (app/gpu/kernels.js:108-145).
+// (app/gpu/kernels.js:108-145); used for rows over 2048 columns and when the rows or the
+// modulation vectors are not 16-byte aligned (the wave-per-row kernel below reads float4s).
 __global__ __launch_bounds__(256) void layernorm_mod_kernel(const float* X, const float* MOD, int64_t shift_off,
                                                             int64_t scale_off, int cols, float eps, int rotate, float* Y,
                                                             int8_t* Q, float* S_out) {
@@ -210,6 +195,209 @@ __global__ __launch_bounds__(256) void layernorm_mod_kernel(const float* X, cons
   if (Y)
     for (int c = t; c < cols; c += 256) Y[row * cols + c] = S[c];
   if (Q) quant_row(S, cols, red, Q + row * cols, S_out + row);
+}
+
+// ------------------------------------------------------------------ conflict-free row variants
+//
+// The row lives in LDS with 4 floats of padding after every 64 (element p at p + 4*(p/64)).
+// Butterfly stage 1 (stride 1) is done in registers on the float4 chunks as they are loaded;
+// stages 2-4 go through LDS, and with the padding every access of those stages is free of bank
+// conflicts: stride 4 and stride 64 keep the natural quad order, stride 16 gives lane
+// (16a + m) the quad m of 64-block 4a + c (c = 0..3 per pass), so the 64 lanes of an
+// instruction hit 64 distinct banks.  T = 64 * WPR threads work on one row (WPR waves; one wave
+// needs no barriers because a wave's own LDS accesses complete in issue order).
+__device__ __forceinline__ int padx(int p) { return p + 4 * (p >> 6); }
+
+__device__ __forceinline__ float4 bfly4(float4 v) {
+  return make_float4(v.x + v.y + v.z - v.w, v.x + v.y - v.z + v.w, v.x - v.y + v.z + v.w, -v.x + v.y + v.z + v.w);
+}
+
+template <int WPR>
+__device__ __forceinline__ void row_sync() {
+  if constexpr (WPR > 1) __syncthreads();
+}
+
+// Stages 2-4 over the padded row S (stage 1 already applied), T = 64*WPR threads, thread tr.
+template <int WPR>
+__device__ __forceinline__ void butterfly_stages234(float* S, int cols, int tr) {
+  constexpr int T = 64 * WPR;
+  const int quads = cols >> 2;
+  // stride 4: quad w -> elements 16(w/4) + w%4 + 4k
+  for (int w = tr; w < quads; w += T) {
+    const int i0 = 16 * (w >> 2) + (w & 3);
+    const float a = S[padx(i0)], b = S[padx(i0 + 4)], c = S[padx(i0 + 8)], e = S[padx(i0 + 12)];
+    S[padx(i0)] = a + b + c - e;
+    S[padx(i0 + 4)] = a + b - c + e;
+    S[padx(i0 + 8)] = a - b + c + e;
+    S[padx(i0 + 12)] = -a + b + c + e;
+  }
+  row_sync<WPR>();
+  // stride 16: thread (wave wv, lane 16a + m) -> quad m of 64-block 4a + c + 16 (wv + WPR i)
+  {
+    const int wv = tr >> 6, aa = (tr >> 4) & 3, mm = tr & 15;
+    const int nblk = cols >> 6;
+    for (int base = 16 * wv; base < nblk; base += 16 * WPR)
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const int blk = base + 4 * aa + c;
+        if (blk < nblk) {
+          const int i0 = 64 * blk + mm;
+          const float a = S[padx(i0)], b = S[padx(i0 + 16)], cc = S[padx(i0 + 32)], e = S[padx(i0 + 48)];
+          S[padx(i0)] = a + b + cc - e;
+          S[padx(i0 + 16)] = a + b - cc + e;
+          S[padx(i0 + 32)] = a - b + cc + e;
+          S[padx(i0 + 48)] = -a + b + cc + e;
+        }
+      }
+  }
+  row_sync<WPR>();
+  // stride 64: quad w -> elements 256(w/64) + w%64 + 64k
+  for (int w = tr; w < quads; w += T) {
+    const int i0 = 256 * (w >> 6) + (w & 63);
+    const float a = S[padx(i0)], b = S[padx(i0 + 64)], c = S[padx(i0 + 128)], e = S[padx(i0 + 192)];
+    S[padx(i0)] = a + b + c - e;
+    S[padx(i0 + 64)] = a + b - c + e;
+    S[padx(i0 + 128)] = a - b + c + e;
+    S[padx(i0 + 192)] = -a + b + c + e;
+  }
+  row_sync<WPR>();
+}
+
+// Row maximum of |v| over T threads (WPR waves share `red`).
+template <int WPR>
+__device__ __forceinline__ float row_max(float v, float* red, int tr) {
+  v = wave_max(v);
+  if constexpr (WPR == 1) {
+    return v;
+  } else {
+    if ((tr & 63) == 0) red[tr >> 6] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int i = 1; i < WPR; i++) r = fmaxf(r, red[i]);
+    return r;
+  }
+}
+
+// Rotated (x 1/16 if rotate) padded row -> optional fp32 Y, optional int8 q + per-row s
+// (s = amax/127, q = clamp(rint(v * (127/amax)))).
+template <int WPR>
+__device__ __forceinline__ void quant_row_padded(const float* S, int cols, int tr, int rotate, float* red, float* Y,
+                                                 int8_t* q, float* s_out) {
+  constexpr int T = 64 * WPR;
+  const int c4n = cols >> 2;
+  float amax = 0.0f;
+  for (int c4 = tr; c4 < c4n; c4 += T) {
+    float4 v = *(const float4*)(S + padx(4 * c4));
+    if (rotate) v = make_float4(v.x * 0.0625f, v.y * 0.0625f, v.z * 0.0625f, v.w * 0.0625f);
+    if (Y) *(float4*)(Y + 4 * c4) = v;
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+  if (!q) return;
+  amax = row_max<WPR>(amax, red, tr);
+  const float sc = amax / 127.0f, inv = 127.0f / amax;
+  if (tr == 0) *s_out = sc;
+  for (int c4 = tr; c4 < c4n; c4 += T) {
+    float4 v = *(const float4*)(S + padx(4 * c4));
+    if (rotate) v = make_float4(v.x * 0.0625f, v.y * 0.0625f, v.z * 0.0625f, v.w * 0.0625f);
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    char4 o;
+    int8_t* ob = (int8_t*)&o;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float t = amax == 0.0f ? 0.0f : rintf(e[j] * inv);
+      t = fminf(fmaxf(t, -127.0f), 127.0f);
+      ob[j] = (int8_t)t;
+    }
+    *(char4*)(q + 4 * c4) = o;
+  }
+}
+
+// Padded row floats of a row of `cols` (cols % 64 == 0 or the tail is unused padding-free).
+__host__ __device__ constexpr int padded_cols(int cols) { return cols + 4 * ((cols + 63) / 64); }
+
+// rows of K: optional rotation (K % 256 == 0), per-token int8.  WPR waves per row; a workgroup
+// holds 4 / WPR rows; dynamic LDS = rows per workgroup * padded_cols(K) floats.
+template <int WPR>
+__global__ __launch_bounds__(256) void quant_rows_pad_kernel(const float* X, int64_t M, int K, int rotate, int8_t* Q,
+                                                             float* S_out) {
+  extern __shared__ float SH[];
+  __shared__ float red[4];
+  constexpr int T = 64 * WPR;
+  const int tr = threadIdx.x % T;
+  const int64_t row = (int64_t)blockIdx.x * (4 / WPR) + threadIdx.x / T;
+  if (row >= M) return;  // (a whole row's threads leave together; WPR > 1 launches one row per workgroup)
+  float* S = SH + (size_t)(threadIdx.x / T) * padded_cols(K);
+  const float* x = X + row * K;
+  for (int c4 = tr; c4 < (K >> 2); c4 += T) {
+    const float4 v = *(const float4*)(x + 4 * c4);
+    *(float4*)(S + padx(4 * c4)) = rotate ? bfly4(v) : v;
+  }
+  row_sync<WPR>();
+  if (rotate) butterfly_stages234<WPR>(S, K, tr);
+  quant_row_padded<WPR>(S, K, tr, rotate, red, nullptr, Q + row * K, S_out + row);
+}
+
+// LayerNorm (no affine) + adaLN (+ Hadamard) (+ int8), one wave per row (app/gpu/kernels.js:108-145).
+// Lane l holds the float4 chunks l, l+64, ... i.e. elements 4l + j + 256i, exactly the elements
+// the reference's 256-thread loops give to threads 4l + j, so the strided partial sums and the
+// 128..1 tree ("red[t] += red[t + s]") are reproduced term for term (wave_tree_sum4).
+__device__ __forceinline__ float wave_tree_sum4(float p0, float p1, float p2, float p3) {
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) {
+    const float q0 = __shfl_down(p0, s), q1 = __shfl_down(p1, s), q2 = __shfl_down(p2, s), q3 = __shfl_down(p3, s);
+    p0 = p0 + q0;
+    p1 = p1 + q1;
+    p2 = p2 + q2;
+    p3 = p3 + q3;
+  }
+  p0 = p0 + p2;
+  p1 = p1 + p3;
+  return __shfl(p0 + p1, 0);
+}
+
+__global__ __launch_bounds__(256) void layernorm_mod_wave_kernel(const float* X, const float* MOD, int64_t shift_off,
+                                                                 int64_t scale_off, int64_t rows, int cols, float eps,
+                                                                 int rotate, float* Y, int8_t* Q, float* S_out) {
+  extern __shared__ float SH[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= rows) return;
+  float* S = SH + (size_t)wave * padded_cols(cols);
+  const float* x = X + row * cols;
+  const int c4n = cols >> 2;
+  // raw row into LDS; per-thread partial sums of the virtual threads 4*lane + j
+  float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+  for (int c4 = lane; c4 < c4n; c4 += 64) {
+    const float4 v = *(const float4*)(x + 4 * c4);
+    *(float4*)(S + padx(4 * c4)) = v;
+    p0 += v.x;
+    p1 += v.y;
+    p2 += v.z;
+    p3 += v.w;
+  }
+  const float mean = wave_tree_sum4(p0, p1, p2, p3) / (float)cols;
+  p0 = p1 = p2 = p3 = 0.0f;
+  for (int c4 = lane; c4 < c4n; c4 += 64) {
+    const float4 v = *(const float4*)(S + padx(4 * c4));
+    const float d0 = v.x - mean, d1 = v.y - mean, d2 = v.z - mean, d3 = v.w - mean;
+    p0 += d0 * d0;
+    p1 += d1 * d1;
+    p2 += d2 * d2;
+    p3 += d3 * d3;
+  }
+  const float r = 1.0f / sqrtf(wave_tree_sum4(p0, p1, p2, p3) / (float)cols + eps);
+  for (int c4 = lane; c4 < c4n; c4 += 64) {
+    const float4 v = *(const float4*)(S + padx(4 * c4));
+    const float4 sc = *(const float4*)(MOD + scale_off + 4 * c4);
+    const float4 sh = *(const float4*)(MOD + shift_off + 4 * c4);
+    const float4 n = make_float4((v.x - mean) * r * (1.0f + sc.x) + sh.x, (v.y - mean) * r * (1.0f + sc.y) + sh.y,
+                                 (v.z - mean) * r * (1.0f + sc.z) + sh.z, (v.w - mean) * r * (1.0f + sc.w) + sh.w);
+    *(float4*)(S + padx(4 * c4)) = rotate ? bfly4(n) : n;
+  }
+  if (rotate) butterfly_stages234<1>(S, cols, lane);
+  quant_row_padded<1>(S, cols, lane, rotate, nullptr, Y ? Y + row * cols : nullptr, Q ? Q + row * cols : nullptr,
+                      Q ? S_out + row : nullptr);
 }
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
@@ -254,7 +442,12 @@ int quant_rows_launch(anima_ctx* c, const float* x, int64_t M, int K, int rotate
   if (((uintptr_t)x & 15) || ((uintptr_t)q & 3)) return fail(c, ANIMA_E_ARG, "anima_quant_rows: x must be 16-byte and q 4-byte aligned");
   if (M == 0) return ANIMA_OK;
   Launch lc(c, rotate ? "hadamard_quant" : "quant_rows", 0.0, (double)M * K * 5 + M * 4.0);
-  hipLaunchKernelGGL(quant_rows_kernel, dim3((unsigned)M), dim3(256), (size_t)K * 4, c->stream, x, K, rotate, q, s);
+  if (K > 2048)  // four waves per row, one row per workgroup (at most 35 KB of LDS)
+    hipLaunchKernelGGL(quant_rows_pad_kernel<4>, dim3((unsigned)M), dim3(256), (size_t)padded_cols(K) * 4, c->stream, x, M,
+                       K, rotate, q, s);
+  else  // one wave per row, four rows per workgroup
+    hipLaunchKernelGGL(quant_rows_pad_kernel<1>, dim3((unsigned)((M + 3) / 4)), dim3(256), (size_t)4 * padded_cols(K) * 4,
+                       c->stream, x, M, K, rotate, q, s);
   return lc.end();
 }
 
@@ -270,8 +463,16 @@ int layernorm_mod_launch(anima_ctx* c, const float* x, const float* mod, int64_t
   if (rows == 0) return ANIMA_OK;
   const double bytes = (double)rows * cols * 4 + (y ? rows * (double)cols * 4 : 0) + (q ? rows * (double)cols + rows * 4.0 : 0);
   Launch lc(c, q ? "layernorm_mod_rot_quant" : (rotate ? "layernorm_mod_rot" : "layernorm_mod"), 0.0, bytes);
-  hipLaunchKernelGGL(layernorm_mod_kernel, dim3((unsigned)rows), dim3(256), (size_t)cols * 4, c->stream, x, mod, shift_off,
-                     scale_off, cols, eps, rotate, y, q, s);
+  const bool vec = cols <= 2048 && !((uintptr_t)x & 15) && !((uintptr_t)(mod + shift_off) & 15) &&
+                   !((uintptr_t)(mod + scale_off) & 15) && !((uintptr_t)y & 15);
+  if (vec) {  // float4 rows: one wave per row
+    hipLaunchKernelGGL(layernorm_mod_wave_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256),
+                       (size_t)4 * padded_cols(cols) * 4, c->stream, x, mod, shift_off, scale_off, rows, cols, eps, rotate, y,
+                       q, s);
+  } else {
+    hipLaunchKernelGGL(layernorm_mod_kernel, dim3((unsigned)rows), dim3(256), (size_t)cols * 4, c->stream, x, mod, shift_off,
+                       scale_off, cols, eps, rotate, y, q, s);
+  }
   return lc.end();
 }
 

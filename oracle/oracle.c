@@ -392,10 +392,10 @@ void orc_token_quant(const float* X, int64_t M, int K, int8_t* Q, float* S) {
     const float* x = X + m * K;
     float amax = 0.0f;
     for (int k = 0; k < K; k++) amax = fmaxf(amax, fabsf(x[k]));
-    float s = amax / 127.0f;
+    float s = amax / 127.0f, inv = 127.0f / amax;
     S[m] = s;
     for (int k = 0; k < K; k++) {
-      float v = amax == 0.0f ? 0.0f : rintf(x[k] / s);
+      float v = amax == 0.0f ? 0.0f : rintf(x[k] * inv);
       if (v > 127.0f) v = 127.0f;
       if (v < -127.0f) v = -127.0f;
       Q[m * K + k] = (int8_t)v;

@@ -75,7 +75,8 @@ void orc_attention_bf16(const orc_attn* a);
 float orc_bf16_round(float x);
 
 /* Per-token dynamic int8 quantization (no reference implementation; this build's
- * definition): s = amax/127 (0 if amax == 0), q = clamp(rint(x / s), -127, 127). */
+ * definition): s = amax/127 (0 if amax == 0), q = clamp(rint(x * (127/amax)), -127, 127)
+ * (one fp32 multiply by the rounded inverse, not a division, per element). */
 void orc_token_quant(const float* X, int64_t M, int K, int8_t* Q, float* S);
 /* acc[m][n] = sum_k qx[m][k] * qw[n][k], exact int32. */
 void orc_gemm_i8(const int8_t* QX, const int8_t* QW, int64_t M, int N, int K, int32_t* ACC);

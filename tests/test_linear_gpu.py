@@ -71,17 +71,20 @@ def test_hadamard_and_quant_bit_exact(ctx):
     assert s[3] == 0 and not q[3].any()
 
 
-@pytest.mark.parametrize("cols,rotate", [(2048, True), (2048, False), (1024, True)])
-def test_layernorm_mod_bit_exact(ctx, cols, rotate):
-    case(f"layernorm_mod rows=300 cols={cols} rotate={rotate}")
+@pytest.mark.parametrize("cols,rotate,shift", [(2048, True, 0), (2048, False, 0), (1024, True, 0), (8192, True, 0),
+                                               (2048, True, 2)])
+def test_layernorm_mod_bit_exact(ctx, cols, rotate, shift):
+    """shift = 0: the wave-per-row kernel; shift = 2 (modulation vectors not 16-byte aligned): the
+    workgroup-per-row kernel."""
+    case(f"layernorm_mod rows=300 cols={cols} rotate={rotate} shift_off={shift}")
     rows = 300
     x = (orc.randn(43, rows * cols).reshape(rows, cols) * 2 + 0.5).astype(np.float32)
     mod = (0.1 * orc.randn(44, 3 * cols)).astype(np.float32)
     dx, dm, dy = ctx.upload(x), ctx.upload(mod), ctx.empty(x.shape)
     dq = ctx.empty((rows, cols), np.int8) if rotate else None
     ds = ctx.empty(rows) if rotate else None
-    ctx.layernorm_mod(dx, dm, 0, cols, rows, cols, rotate=rotate, y=dy, q=dq, s=ds)
-    ref = orc.layernorm_mod(x, mod, 0, cols, cols, rotate=rotate)
+    ctx.layernorm_mod(dx, dm, shift, cols, rows, cols, rotate=rotate, y=dy, q=dq, s=ds)
+    ref = orc.layernorm_mod(x, mod, shift, cols, cols, rotate=rotate)
     got = dy.numpy()
     assert np.array_equal(got, ref), report("layernorm_mod", got, ref)
     if rotate:

@@ -287,6 +287,12 @@ def test_token_quant_properties():
     # idempotent on its own grid
     q2, s2 = orc.token_quant(s[:, None] * q.astype(np.float32))
     assert np.array_equal(q2, q)
+    # the definition in numpy float32: s = amax/127, q = clip(rint(x * (127/amax)))
+    amax = np.abs(x).max(1).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        inv = np.float32(127.0) / amax
+    qn = np.where(amax[:, None] == 0, 0, np.clip(np.rint(x * inv[:, None]), -127, 127)).astype(np.int8)
+    assert np.array_equal(s, amax / np.float32(127.0)) and np.array_equal(q, qn)
 
 
 def test_gemm_i8_matches_int64_matmul():
