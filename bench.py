@@ -52,10 +52,13 @@ def cpu_baseline():
     return json.loads(r.stdout.strip().splitlines()[-1])
 
 
-def profiled_traffic(kernel="attn_flash_bf16"):
+PROFILE = "profiles/attn_flash_w8_b2_n4096.md"
+
+
+def profiled_traffic(kernel="attn_flash_w8"):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
-    (copy-kernel calibrated, profiles/attn_flash_bf16_b2_n4096.md), or None."""
-    path = os.path.join(ROOT, "profiles", "attn_flash_bf16_b2_n4096.md")
+    (copy-kernel calibrated), or None."""
+    path = os.path.join(ROOT, PROFILE)
     if not os.path.exists(path):
         return None
     for line in open(path):
@@ -173,9 +176,9 @@ def main():
                                "fp32 QKV [2,4096,6144] -> q/k RMSNorm + 3D RoPE + softmax(QK^T)V, bf16 MFMA fp32 acc",
                    "B": B, "heads": H, "head_dim": D, "tokens": L, "flops_per_step": flops},
         "pct_mfma_peak_op": round(100 * value / BF16_PEAK_TFLOPS, 2),
-        "roofline": {"bound": "mfma", "kernel": "attn_flash_bf16", "achieved": round(achieved, 3),
+        "roofline": {"bound": "mfma", "kernel": "attn_flash_w8", "achieved": round(achieved, 3),
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-                     "traffic": profiled_traffic(), "traffic_source": "profiles/attn_flash_bf16_b2_n4096.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+                     "traffic": profiled_traffic(), "traffic_source": PROFILE + " (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
                      "kernel_ms": round(k_ms, 5)},
         "prep_kernel": {"ms": round(prep_ms, 5) if prep_ms else None, "GB/s": round(prep_gbs, 1) if prep_gbs else None,
                         "frac_hbm": round(prep_gbs / HBM_PEAK_GBS, 4) if prep_gbs else None},
