@@ -97,6 +97,8 @@ def lib():
                                           _vp, _vp, _vp]
         L.anima_elementwise.argtypes = [_vp, ctypes.c_int, _vp, _vp, _vp, _i64]
         L.anima_zero.argtypes = [_vp, _vp, _i64]
+        L.anima_patchify.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]
+        L.anima_unpatchify.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]
         L.anima_linear.argtypes = [_vp, ctypes.POINTER(LinearDesc)]
         _LIB = L
     return _LIB
@@ -242,6 +244,12 @@ class Context:
 
     def zero(self, y, n):
         return self._check(lib().anima_zero(self.h, _ptr(y), n))
+
+    def patchify(self, latents, B, h, w, patches):
+        return self._check(lib().anima_patchify(self.h, _ptr(latents), B, h, w, _ptr(patches)))
+
+    def unpatchify(self, o, B, h, w, latents):
+        return self._check(lib().anima_unpatchify(self.h, _ptr(o), B, h, w, _ptr(latents)))
 
     def linear(self, W, M, out, *, x=None, ldx=0, x_rotated=True, xq=None, xs=None, ldc=0, alpha=0.0, act="none",
                epilogue=EPI_STORE, gate=None, gate_off=0, acc_out=None):

@@ -614,6 +614,8 @@ constexpr int W8_BQ = 256;
 constexpr int W8_KB = 64;
 constexpr int W8_ST = 2 * SWZ_KT;  // stage bytes: K tile + V^T tile
 constexpr int W8_NST = 3;
+constexpr int W8_OROW = 64 + 4;  // floats per row of the output staging (padded against bank conflicts)
+static_assert(8 * 32 * W8_OROW * 4 <= W8_NST * W8_ST, "output staging must fit in the stages");
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -729,15 +731,33 @@ __global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
   }
 
   l = pair_sum(l);
-  if (qi < a.Lq) {
-    const float inv = 1.0f / l;
-    float* dst = a.o + (int64_t)b * a.o_bs + (int64_t)qi * a.ldo + h * HD + 4 * hf;
+  const float inv = 1.0f / l;
+  // The output leaves through LDS so that every store instruction writes whole 256-byte row
+  // segments: straight from the MFMA layout each instruction would put 32 bytes into each of 32
+  // rows, and the partially written lines double the HBM write traffic.  Each wave transposes its
+  // own 32 x 128 block in two 64-column halves through a private slice of the (now idle) stages.
+  w8_barrier();  // every wave is done reading the key/value stages
+  float* ow = (float*)smem + wave * (32 * W8_OROW);
+  const int rr = lane >> 4, cc = 4 * (lane & 15);
+  float* dst = a.o + (int64_t)b * a.o_bs + h * HD + cc;
+  const int q0 = qt * W8_BQ + wave * 32;
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++)
+  for (int half = 0; half < 2; half++) {
 #pragma unroll
-      for (int g = 0; g < 4; g++)
-        *(float4*)(dst + 32 * dt + 8 * g) =
-            make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+    for (int d2 = 0; d2 < 2; d2++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const f32x16& v = o[2 * half + d2];
+        *(float4*)(ow + lq * W8_OROW + 32 * d2 + 8 * g + 4 * hf) =
+            make_float4(v[4 * g] * inv, v[4 * g + 1] * inv, v[4 * g + 2] * inv, v[4 * g + 3] * inv);
+      }
+    // one wave's LDS accesses complete in program order: no wait between these writes and reads
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int r = 4 * k + rr;
+      const float4 v = *(const float4*)(ow + r * W8_OROW + cc);
+      if (q0 + r < a.Lq) *(float4*)(dst + (int64_t)(q0 + r) * a.ldo + 64 * half) = v;
+    }
   }
 }
 #undef W8_WAIT_VM

@@ -82,6 +82,8 @@ int layernorm_mod_launch(anima_ctx* c, const float* x, const float* mod, int64_t
                          int64_t rows, int cols, float eps, int rotate, float* y, int8_t* q, float* s);
 int elementwise_launch(anima_ctx* c, int op, const float* a, const float* b, float* y, int64_t n);
 int zero_launch(anima_ctx* c, float* y, int64_t n);
+// forward: src = latents, dst = patches; inverse: src = final-layer output, dst = latents
+int patchify_launch(anima_ctx* c, const float* src, float* dst, int B, int h, int w, bool inverse);
 int fill_random_launch(anima_ctx* c, void* dst, int64_t n, int kind, uint64_t seed, float lo, float hi);
 
 // ---- kernel launchers (gemm.hip)

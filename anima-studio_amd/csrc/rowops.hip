@@ -503,6 +503,53 @@ int zero_launch(anima_ctx* c, float* y, int64_t n) {
   return lc.end();
 }
 
+// Patch layout of the DiT input/output (app/models/dit.js:55-78).  Forward: one thread per patch
+// element, [B*Hp*Wp][68] <- latents [B][16][h][w] (columns 64..67 zero).  Inverse: one thread per
+// latent element, latents <- [B*Hp*Wp][64] in (p1 p2 c) order.
+__global__ __launch_bounds__(256) void patchify_kernel(const float* lat, float* P, int h, int w, int64_t n) {
+  const int Wp = w / 2, L = (h / 2) * Wp;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = i / 68;
+    const int k = (int)(i - row * 68);
+    const int64_t b = row / L;
+    const int p = (int)(row - b * L), y = p / Wp, x = p - y * Wp;
+    float v = 0.0f;
+    if (k < 64) {
+      const int c = k >> 2, m = (k >> 1) & 1, nn = k & 1;
+      v = lat[((b * 16 + c) * h + 2 * y + m) * (int64_t)w + 2 * x + nn];
+    }
+    P[i] = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void unpatchify_kernel(const float* O, float* lat, int h, int w, int64_t n) {
+  const int Wp = w / 2, L = (h / 2) * Wp;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t bc = i / ((int64_t)h * w);
+    const int r = (int)(i - bc * h * w), yy = r / w, xx = r - yy * w;
+    const int64_t b = bc / 16;
+    const int c = (int)(bc - b * 16);
+    const int64_t row = b * L + (yy >> 1) * Wp + (xx >> 1);
+    lat[i] = O[row * 64 + (yy & 1) * 32 + (xx & 1) * 16 + c];
+  }
+}
+
+int patchify_launch(anima_ctx* c, const float* src, float* dst, int B, int h, int w, bool inverse) {
+  const char* fn = inverse ? "anima_unpatchify" : "anima_patchify";
+  if (!src || !dst) return fail(c, ANIMA_E_ARG, "%s: null pointer", fn);
+  if (B <= 0 || h <= 0 || w <= 0 || (h & 1) || (w & 1))
+    return fail(c, ANIMA_E_ARG, "%s: B=%d h=%d w=%d (positive, h and w even)", fn, B, h, w);
+  const int64_t nl = (int64_t)B * 16 * h * w, np = (int64_t)B * (h / 2) * (w / 2);
+  if (!inverse) {
+    Launch lc(c, "patchify", 0.0, (double)nl * 4 + (double)np * 68 * 4);
+    hipLaunchKernelGGL(patchify_kernel, dim3(grid_for(np * 68)), dim3(256), 0, c->stream, src, dst, h, w, np * 68);
+    return lc.end();
+  }
+  Launch lc(c, "unpatchify", 0.0, (double)nl * 8);
+  hipLaunchKernelGGL(unpatchify_kernel, dim3(grid_for(nl)), dim3(256), 0, c->stream, src, dst, h, w, nl);
+  return lc.end();
+}
+
 __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
   uint64_t z = x + 0x9e3779b97f4a7c15ull;
   z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;

@@ -390,6 +390,16 @@ int anima_zero(anima_ctx* c, float* y, int64_t n) {
   return zero_launch(c, y, n);
 }
 
+int anima_patchify(anima_ctx* c, const float* latents, int B, int h, int w, float* patches) {
+  CHECK_CTX(c);
+  return patchify_launch(c, latents, patches, B, h, w, false);
+}
+
+int anima_unpatchify(anima_ctx* c, const float* o, int B, int h, int w, float* latents) {
+  CHECK_CTX(c);
+  return patchify_launch(c, o, latents, B, h, w, true);
+}
+
 int anima_fill_random(anima_ctx* c, void* dst, int64_t n, int kind, uint64_t seed, float lo, float hi) {
   CHECK_CTX(c);
   return fill_random_launch(c, dst, n, kind, seed, lo, hi);

@@ -391,6 +391,26 @@ static napi_value js_elementwise(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* patchify(ctx, latents, B, h, w, patches) */
+static napi_value js_patchify(napi_env env, napi_callback_info info) {
+  napi_value a[6];
+  get_args(env, info, 6, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_patchify(c, (const float*)ptr(env, a[1]), (int)num(env, a[2]), (int)num(env, a[3]),
+                                  (int)num(env, a[4]), (float*)ptr(env, a[5])));
+  return NULL;
+}
+
+/* unpatchify(ctx, o, B, h, w, latents) */
+static napi_value js_unpatchify(napi_env env, napi_callback_info info) {
+  napi_value a[6];
+  get_args(env, info, 6, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_unpatchify(c, (const float*)ptr(env, a[1]), (int)num(env, a[2]), (int)num(env, a[3]),
+                                    (int)num(env, a[4]), (float*)ptr(env, a[5])));
+  return NULL;
+}
+
 /* zero(ctx, y, n) */
 static napi_value js_zero(napi_env env, napi_callback_info info) {
   napi_value a[3];
@@ -468,7 +488,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       FN("timerStart", js_timer_start), FN("timerStop", js_timer_stop), FN("attention", js_attention),
       FN("qkNormRope", js_qk_norm_rope), FN("rmsnorm", js_rmsnorm), FN("rope", js_rope),
       FN("hadamard", js_hadamard), FN("quantRows", js_quant_rows), FN("layernormMod", js_layernorm_mod),
-      FN("elementwise", js_elementwise), FN("zero", js_zero), FN("fillRandom", js_fill_random),
+      FN("elementwise", js_elementwise), FN("zero", js_zero), FN("patchify", js_patchify), FN("unpatchify", js_unpatchify), FN("fillRandom", js_fill_random),
       FN("linear", js_linear), FN("lastError", js_last_error),
   };
 #undef FN

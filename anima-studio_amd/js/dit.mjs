@@ -8,7 +8,8 @@
 
 import * as ops from "./ops.mjs";
 import { concatLinears } from "./weights.mjs";
-import { ditRopeTable, timestepEmbedding, patchify, unpatchify } from "./common.mjs";
+import { ditRopeTable, timestepEmbedding } from "./common.mjs";
+import { native } from "./gpu.mjs";
 
 const D = 2048;
 const HEADS = 16;
@@ -102,6 +103,23 @@ export class AnimaDiT {
 
   constructor(gpu) {
     this.gpu = gpu;
+    this.ropeCache = new Map(); // "HpxWp" -> device RoPE table; depends only on the token grid
+  }
+
+  ropeTable(Hp, Wp) {
+    const key = `${Hp}x${Wp}`;
+    let t = this.ropeCache.get(key);
+    if (!t) {
+      t = ditRopeTable(this.gpu, Hp, Wp);
+      this.ropeCache.set(key, t);
+    }
+    return t;
+  }
+
+  // Frees the device tables cached across forward calls (the weights belong to their loader).
+  releaseCaches() {
+    for (const t of this.ropeCache.values()) t.release();
+    this.ropeCache.clear();
   }
 
   // Everything that depends only on sigma (app/models/dit.js:196-225).
@@ -174,12 +192,20 @@ export class AnimaDiT {
     const B = latents.length;
     if (cond.B !== B) throw new Error(`forward: ${B} latents but ${cond.B} contexts`);
     const Hp = h / 2, Wp = w / 2, L = Hp * Wp, M = B * L;
-    const patches = new Float32Array(M * 68);
-    latents.forEach((lat, b) => patchify(lat, h, w, patches, b * L * 68));
-    const xin = gpu.fromArray(patches, [M, 68]);
+    // latents go up as they are; the patch layout (dit.js:55-65) is built on the device
+    const per = 16 * h * w;
+    const host = new Float32Array(B * per);
+    latents.forEach((lat, b) => {
+      if (lat.length !== per) throw new Error(`forward: latent ${b} has ${lat.length} values, expected ${per}`);
+      host.set(lat, b * per);
+    });
+    const lat = gpu.fromArray(host, [B, 16, h, w]);
+    const xin = gpu.empty([M, 68]);
+    native.patchify(gpu.ctx, lat.buf, B, h, w, xin.buf);
+    lat.release();
     const x = ops.linear(gpu, xin, this.xEmbed);
     xin.release();
-    const cs = ditRopeTable(gpu, Hp, Wp);
+    const cs = this.ropeTable(Hp, Wp);
 
     for (let i = 0; i < this.blocks.length; i++) {
       const b = this.blocks[i];
@@ -216,16 +242,18 @@ export class AnimaDiT {
       gpu.flush();
       if (onBlock) await onBlock(i, x);
     }
-    cs.release();
 
     const n = ops.layernormMod(gpu, x, tc.final, 0, D, D, false);
     x.release();
     const out = ops.linear(gpu, n, this.finalLinear); // [M, 64] = (p1 p2 c)
     n.release();
-    const o = await gpu.read(out);
+    const v = gpu.empty([B, 16, h, w]);
+    native.unpatchify(gpu.ctx, out.buf, B, h, w, v.buf); // dit.js:68-78 on the device
     out.release();
+    const o = await gpu.read(v);
+    v.release();
     const vs = [];
-    for (let bb = 0; bb < B; bb++) vs.push(unpatchify(o, h, w, bb * L * 64));
+    for (let bb = 0; bb < B; bb++) vs.push(o.slice(bb * per, (bb + 1) * per));
     return vs;
   }
 }

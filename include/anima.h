@@ -153,6 +153,14 @@ int anima_elementwise(anima_ctx* ctx, int op, const float* a, const float* b, fl
 /* ops.zero (app/gpu/ops.js:89-93; kernels.js:415-423). */
 int anima_zero(anima_ctx* ctx, float* y, int64_t n);
 
+/* patchify on the device (app/models/dit.js:55-65, a host loop in the reference): latents
+ * [B][16][h][w] -> patches [B*(h/2)*(w/2)][68], "c (h m) (w n) -> (h w) (c m n)", columns 64..67
+ * (the padding-mask channel) zero.  h, w even. */
+int anima_patchify(anima_ctx* ctx, const float* latents, int B, int h, int w, float* patches);
+/* unpatchify on the device (app/models/dit.js:68-78): final-layer output [B*(h/2)*(w/2)][64] in
+ * (p1 p2 c) order -> latents [B][16][h][w], "(h w) (p1 p2 c) -> c (h p1) (w p2)".  h, w even. */
+int anima_unpatchify(anima_ctx* ctx, const float* o, int B, int h, int w, float* latents);
+
 /* Seeded synthetic data on the device, for benchmarks and tests (no reference counterpart: the
  * reference loads real checkpoints).  Element i draws h = splitmix64(seed * 0xD1B54A32D192ED03 + i):
  *   ANIMA_FILL_U8    uint8   lo + h % (hi - lo + 1)                (integers lo..hi)

@@ -107,6 +107,33 @@ def test_elementwise_and_zero(ctx):
     assert not dy.numpy().any()
 
 
+@pytest.mark.parametrize("B,h,w", [(2, 128, 128), (1, 6, 10)])
+def test_patchify_unpatchify(ctx, B, h, w):
+    """Device patch layout against numpy reshapes of the reference's rearrange patterns
+    "c (h m) (w n) -> (h w) (c m n)" (+ zero mask channel) and "(h w) (p1 p2 c) -> c (h p1) (w p2)"
+    (dit.js:55-78); pure data movement, so bit-exact."""
+    case(f"patchify / unpatchify B={B} h={h} w={w}")
+    Hp, Wp = h // 2, w // 2
+    lat = orc.randn(47, B * 16 * h * w).reshape(B, 16, h, w)
+    want = lat.reshape(B, 16, Hp, 2, Wp, 2).transpose(0, 2, 4, 1, 3, 5).reshape(B * Hp * Wp, 64)
+    want = np.concatenate([want, np.zeros((B * Hp * Wp, 4), np.float32)], axis=1)
+    dl, dp = ctx.upload(lat), ctx.empty((B * Hp * Wp, 68))
+    ctx.patchify(dl, B, h, w, dp)
+    assert np.array_equal(dp.numpy(), want)
+    o = orc.randn(48, B * Hp * Wp * 64).reshape(B * Hp * Wp, 64)
+    want_v = o.reshape(B, Hp, Wp, 2, 2, 16).transpose(0, 5, 1, 3, 2, 4).reshape(B, 16, h, w)
+    do, dv = ctx.upload(o), ctx.empty((B, 16, h, w))
+    ctx.unpatchify(do, B, h, w, dv)
+    assert np.array_equal(dv.numpy(), want_v)
+    # round trip: the input columns are (c m n), the output columns (p1 p2 c)
+    cmn = dp.numpy()[:, :64].reshape(-1, 16, 2, 2)
+    dq = ctx.upload(np.ascontiguousarray(cmn.transpose(0, 2, 3, 1).reshape(-1, 64)))
+    ctx.unpatchify(dq, B, h, w, dv)
+    assert np.array_equal(dv.numpy(), lat)
+    with pytest.raises(amd().AnimaError):
+        ctx.patchify(dl, B, h - 1, w, dp)
+
+
 # ------------------------------------------------------------------ int8 / W4A8 GEMM
 
 def checksums_ok(qx, qw_int8, acc):
