@@ -61,7 +61,7 @@ __device__ __forceinline__ float cvt<float>(float x) { return x; }
 // grid (Lkp/64, Hkv, B), 256 threads.
 template <typename T, bool NORM, bool ROPE>
 __global__ __launch_bounds__(256) void attn_prep_kv(PrepArgs a) {
-  constexpr int VSP = BK + 4;  // padded LDS row (keys) of the V transpose
+  constexpr int VSP = BK + (sizeof(T) == 2 ? 2 : 4);  // padded LDS row (keys) of the V transpose
   __shared__ T vs[HD * VSP];
   const int t = threadIdx.x;
   const int kb0 = blockIdx.x * BK, hk = blockIdx.y, b = blockIdx.z;
@@ -132,9 +132,12 @@ __global__ __launch_bounds__(256) void attn_prep_kv(PrepArgs a) {
     }
   }
 
-  // ---- V: thread = (dim group t%16 -> dims 8g..8g+7, token group t/16 -> 4 tokens)
+  // ---- V: thread = (dim group g -> dims 8g..8g+7, token group tg -> tokens 4tg..4tg+3); each
+  // half-wave holds dim groups 0-7 or 8-15 and four token groups, so with the 66-element LDS rows
+  // its 8-byte writes (four tokens of one dim) cover all 64 banks once.
   {
-    const int g = t & 15, tg = t >> 4;
+    const int g = (t & 7) | (((t >> 5) & 1) << 3), tg = ((t >> 3) & 3) | ((t >> 6) << 2);
+    float e[4][8];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const int l = kb0 + 4 * tg + j;
@@ -144,9 +147,14 @@ __global__ __launch_bounds__(256) void attn_prep_kv(PrepArgs a) {
         lo = *(const float4*)src;
         hi = *(const float4*)(src + 4);
       }
-      const float e[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      e[j][0] = lo.x; e[j][1] = lo.y; e[j][2] = lo.z; e[j][3] = lo.w;
+      e[j][4] = hi.x; e[j][5] = hi.y; e[j][6] = hi.z; e[j][7] = hi.w;
+    }
 #pragma unroll
-      for (int i = 0; i < 8; i++) vs[(8 * g + i) * VSP + 4 * tg + j] = cvt<T>(e[i]);
+    for (int i = 0; i < 8; i++) {
+      T* row = vs + (8 * g + i) * VSP + 4 * tg;
+#pragma unroll
+      for (int j = 0; j < 4; j++) row[j] = cvt<T>(e[j][i]);
     }
     __syncthreads();
     // write rows of V^T: thread = (dim t/2, half t%2 -> 32 keys)
