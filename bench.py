@@ -25,6 +25,7 @@ sys.path.insert(0, ROOT)
 METRIC = "attention TFLOP/s + % MFMA peak at N=4096; DiT step ms at 1024² (1 GPU)"
 BF16_PEAK_TFLOPS = 2516.6
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5033.2
 
 
 def parse():
@@ -35,6 +36,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-dit", action="store_true", help="skip the full DiT step leg")
     p.add_argument("--dit-steps", type=int, default=3)
+    p.add_argument("--no-linears", action="store_true", help="skip the quantized-linear leg")
     p.add_argument("--copy-mb", type=int, default=0,
                    help="only run the elementwise copy kernel on a buffer of this many MiB (HBM counter calibration)")
     return p.parse_args()
@@ -86,6 +88,59 @@ def dit_step(args):
                       "self + cross attention to 512x1024 contexts, W4A8 mixed (blocks 0/27 int8), seeded random weights; "
                       "step = timeCond + forward through node bench_dit.mjs",
             "steps": args.dit_steps}
+
+
+LINEAR_SHAPES = (("qkv", 6144, 2048, "store"), ("out", 2048, 2048, "gated"), ("mlp1", 8192, 2048, "gelu"),
+                 ("mlp2", 2048, 8192, "gated"))
+
+
+def linears(m, ctx, reps):
+    """The DiT block's quantized linears at M = B*N = 8192 tokens (int8 and W4 weights, per-token
+    int8 activations, the block's epilogues): kernel time from HIP events around each launch,
+    summed over the launch's kernels (W4: the decode pass included)."""
+    import numpy as np
+
+    M = 8192
+    rng = np.random.default_rng(7)
+    res = {}
+    for kind in ("i8", "w4"):
+        for name, N, K, epi in LINEAR_SHAPES:
+            bufs = [ctx.upload(rng.integers(-127, 128, size=(M, K), dtype=np.int8)),
+                    ctx.upload(rng.uniform(0.001, 0.01, M).astype(np.float32)),
+                    ctx.upload(rng.uniform(0.001, 0.01, N).astype(np.float32))]
+            xq, xs, sw = bufs
+            if kind == "i8":
+                bufs.append(ctx.upload(rng.integers(-127, 128, size=(N, K), dtype=np.int8)))
+                W = m.weight(m.W_I8, N, K, bufs[-1], scale=sw)
+            else:
+                bufs += [ctx.upload(rng.integers(0, 256, size=(N, K // 2), dtype=np.uint8)),
+                         ctx.upload(rng.integers(0x60, 0x70, size=(N, K // 16), dtype=np.uint8)),
+                         ctx.upload(np.linspace(-1, 1, 16).astype(np.float32))]
+                W = m.weight(m.W_W4, N, K, bufs[-3], scale=sw, srel=bufs[-2], codebook=bufs[-1])
+            out = ctx.empty((M, N))
+            gate = ctx.upload(rng.uniform(0, 1, 3 * N).astype(np.float32))
+            bufs += [out, gate]
+            kw = dict(xq=xq, xs=xs)
+            if epi == "gated":
+                kw.update(epilogue=m.EPI_GATED, gate=gate, gate_off=N)
+            elif epi == "gelu":
+                kw.update(act="gelu")
+            for _ in range(2):
+                ctx.linear(W, M, out, **kw)
+            ctx.sync()
+            ctx.profile(True)
+            ctx.profile_reset()
+            for _ in range(reps):
+                ctx.linear(W, M, out, **kw)
+            rep = ctx.profile_report()
+            ctx.profile(False)
+            ms = sum(r["ms"] for r in rep) / reps
+            ops = 2.0 * M * N * K
+            res[f"{kind}.{name}"] = {"M": M, "N": N, "K": K, "epilogue": epi, "ms": round(ms, 4),
+                                     "TOPS": round(ops / ms / 1e9, 1), "frac_int8_peak": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4)}
+            for b in bufs:
+                b.release()
+    return res
 
 
 def main():
@@ -157,6 +212,11 @@ def main():
         prep_gbs = prep["bytes"] / prep["count"] / (prep_ms / 1e3) / 1e9 if prep else None
         for b in (d_qkv, d_qn, d_kn, d_cs, d_o):
             b.release()
+        lin = None
+        if not args.no_linears:
+            t = time.time()
+            lin = linears(m, ctx, 10)
+            print(f"bench: linears {time.time() - t:.1f} s", file=sys.stderr, flush=True)
 
     value = flops / (ms / 1e3) / 1e12
     out = {
@@ -183,6 +243,8 @@ def main():
         "prep_kernel": {"ms": round(prep_ms, 5) if prep_ms else None, "GB/s": round(prep_gbs, 1) if prep_gbs else None,
                         "frac_hbm": round(prep_gbs / HBM_PEAK_GBS, 4) if prep_gbs else None},
     }
+    if lin is not None:
+        out["linears"] = lin
     if not args.no_dit:
         t = time.time()
         out["dit_step"] = dit_step(args)
