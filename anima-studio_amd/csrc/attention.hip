@@ -409,19 +409,18 @@ __device__ __forceinline__ void flash_block(const Addr& A, const bf16x8 (&qf)[8]
 // keep the written order, so each MFMA finds its K / V^T fragment loaded four reads earlier and
 // the exponentials of one key tile sit between the MFMAs of the next product.
 #define ANIMA_SB() __builtin_amdgcn_sched_barrier(0)
-template <class Addr>
-__device__ __forceinline__ void flash_block_main(const Addr& A, const bf16x8 (&qf)[8], f32x16 (&o)[4], float& m,
-                                                 f32x16& negm, float& l) {
+// On entry f holds fragments 0..3 of block A; with NEXT, fragments 0..3 of block N (already
+// published) are read during the last MFMAs and left in f, otherwise f is left undefined.
+template <class Addr, bool NEXT>
+__device__ __forceinline__ void flash_block_main(const Addr& A, const Addr& N, bf16x8 (&f)[4], const bf16x8 (&qf)[8],
+                                                 f32x16 (&o)[4], float& m, f32x16& negm, float& l) {
   // fragment i of the block: K reads 0..15 (tile i/8, k-step i%8), V^T reads 16..31
   // (key tile (i-16)/8, dim tile ((i-16)%8)/2, 16-key half (i-16)%2)
 #define FRAG(i) ((i) < 16 ? A.k((i) >> 3, (i) & 7) : A.v(((i) - 16) >> 3, (((i) - 16) & 7) >> 1, ((i) - 16) & 1))
-  bf16x8 f[4];
   f32x16 s0, s1;
   bf16x8 p[4];  // p[0], p[1]: tile 0;  p[2], p[3]: tile 1
   const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
   float la = 0.0f, lb = 0.0f;
-  f[0] = FRAG(0); f[1] = FRAG(1); f[2] = FRAG(2); f[3] = FRAG(3);
-  ANIMA_SB();
   // 2 probabilities of tile T (registers 2k, 2k+1 of S) -> p, row-sum partial
 #define PROB2(S, T, k)                                                                                \
   {                                                                                                   \
@@ -497,11 +496,12 @@ __device__ __forceinline__ void flash_block_main(const Addr& A, const bf16x8 (&q
   }
   l += lt;
   ANIMA_SB();
-  // P.V tile 1: MFMAs 24..31 (fragments 24..31), reads 28..31
+  // P.V tile 1: MFMAs 24..31 (fragments 24..31), reads 28..31, then block N's 0..3
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     o[j >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[j & 3], p[2 + (j & 1)], o[j >> 1], 0, 0, 0);
     if (j < 4) f[j & 3] = FRAG(j + 28);
+    else if (NEXT) f[j & 3] = N.k(0, j - 4);
     ANIMA_SB();
   }
 #undef PROB2
@@ -581,9 +581,11 @@ __global__ __launch_bounds__(256, KB == 32 ? 3 : 2) void attn_flash_bf16(FlashAr
     const int st = kb & 1;
     const bool more = kb + 1 < nkb;
     if (more) GLOAD(kb + 1);
-    if constexpr (KB == 64)
-      flash_block_main(PadAddr<KB>(smem + st * T::STAGE, smem + st * T::STAGE + T::KTILE, lq, hf), qf, o, m, negm, l);
-    else
+    if constexpr (KB == 64) {
+      const PadAddr<KB> A(smem + st * T::STAGE, smem + st * T::STAGE + T::KTILE, lq, hf);
+      bf16x8 f[4] = {A.k(0, 0), A.k(0, 1), A.k(0, 2), A.k(0, 3)};
+      flash_block_main<PadAddr<KB>, false>(A, A, f, qf, o, m, negm, l);
+    } else
       flash_block<KB, false, false>(PadAddr<KB>(smem + st * T::STAGE, smem + st * T::STAGE + T::KTILE, lq, hf), qf, o,
                                     m, negm, l, kb * KB, Lk, hf);
     if (more) LSTORE(st ^ 1);
@@ -616,12 +618,13 @@ constexpr int FLASH_KB = 64;  // keys per block of the bf16 kernel
 // attn_flash_w8: one workgroup = 8 waves x 32 queries (two waves per SIMD, the per-wave block
 // code of attn_flash_bf16), so each K/V block copied into LDS serves 256 queries (half the copy
 // traffic per query of the 4-wave kernel).  Blocks of 64 keys go straight from global memory
-// into three swizzled LDS stages (global_load_lds_dwordx4, no register staging), issued two
-// blocks ahead of the compute.
+// into four swizzled LDS stages (buffer_load ... lds, no register staging), issued three blocks
+// ahead of the compute and published one block ahead, so that each block's first fragments are
+// read while the previous block's last MFMAs run.
 constexpr int W8_BQ = 256;
 constexpr int W8_KB = 64;
 constexpr int W8_ST = 2 * SWZ_KT;  // stage bytes: K tile + V^T tile
-constexpr int W8_NST = 3;
+constexpr int W8_NST = 4;
 constexpr int W8_OROW = 64 + 4;  // floats per row of the output staging (padded against bank conflicts)
 static_assert(8 * 32 * W8_OROW * 4 <= W8_NST * W8_ST, "output staging must fit in the stages");
 
@@ -691,10 +694,11 @@ __global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
   src.v = __builtin_amdgcn_make_buffer_rsrc((void*)((const bf16*)a.vt + ((int64_t)b * a.Hkv + hk) * HD * a.Lkp), (short)0,
                                             head_bytes, 0x00020000);
 
-  // blocks 0 and 1 start loading before Q is read and normalized
+  // blocks 0, 1 and 2 start loading before Q is read and normalized
   const W8Load lo(a.Lkp, wave, lane);
   w8_load(src, lo, 0, smem, wave);
   if (nkb > 1) w8_load(src, lo, 1, smem + W8_ST, wave);
+  if (nkb > 2) w8_load(src, lo, 2, smem + 2 * W8_ST, wave);
 
   bf16x8 qf[8];
   {
@@ -712,31 +716,35 @@ __global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
   float m = 0.0f, l = 0.0f;
   f32x16 negm = {};
 
-  // Block j lives in stage j % 3.  At the top of iteration j a wave waits for its own copies of
-  // block j (the 4 of block j+1 may still be in flight), the barrier publishes everyone's and
-  // also ends every wave's reads of block j-1, whose stage is then refilled with block j+2.
+  // Block j lives in stage j % 4.  The barrier at the top of iteration j publishes block j+1 (a
+  // wave first waits for its own copies of it; the 4 of block j+2 may still be in flight), so
+  // block j's last MFMAs can carry the reads of block j+1's first fragments.  The barrier also
+  // ends every wave's reads of block j-1, whose stage is then refilled with block j+3.  The
+  // barrier before block 0 publishes blocks 0 and 1; a partial last block needs no barrier of
+  // its own (published one iteration ahead, and its stage is not refilled).
   const int nfull = Lk / W8_KB;
-  if (nkb > 1) W8_WAIT_VM(4);
+  if (nkb > 2) W8_WAIT_VM(4);
   else W8_WAIT_VM(0);
   w8_barrier();
-  if (nkb > 2) w8_load(src, lo, 2, smem + 2 * W8_ST, wave);
+  if (nkb > 3) w8_load(src, lo, 3, smem + 3 * W8_ST, wave);
   if (nfull > 0) flash_block<W8_KB, false, true>(SwzAddr(smem, of), qf, o, m, negm, l, 0, Lk, hf);
   else flash_block<W8_KB, true, true>(SwzAddr(smem, of), qf, o, m, negm, l, 0, Lk, hf);
-  int st = 0;
+  bf16x8 f[4];
+  {
+    const SwzAddr A1(smem + W8_ST, of);
+#pragma unroll
+    for (int i = 0; i < 4; i++) f[i] = A1.k(0, i);
+  }
   for (int j = 1; j < nfull; j++) {
-    st = st == 2 ? 0 : st + 1;
-    if (j + 1 < nkb) W8_WAIT_VM(4);
+    if (j + 2 < nkb) W8_WAIT_VM(4);
     else W8_WAIT_VM(0);
     w8_barrier();
-    if (j + 2 < nkb) w8_load(src, lo, j + 2, smem + (st == 0 ? 2 : st - 1) * W8_ST, wave);
-    flash_block_main(SwzAddr(smem + st * W8_ST, of), qf, o, m, negm, l);
+    if (j + 3 < nkb) w8_load(src, lo, j + 3, smem + ((j + 3) & 3) * W8_ST, wave);
+    flash_block_main<SwzAddr, true>(SwzAddr(smem + (j & 3) * W8_ST, of), SwzAddr(smem + ((j + 1) & 3) * W8_ST, of), f,
+                                    qf, o, m, negm, l);
   }
-  if (nfull < nkb && nfull > 0) {
-    st = st == 2 ? 0 : st + 1;
-    W8_WAIT_VM(0);
-    w8_barrier();
-    flash_block<W8_KB, true, false>(SwzAddr(smem + st * W8_ST, of), qf, o, m, negm, l, nfull * W8_KB, Lk, hf);
-  }
+  if (nfull < nkb && nfull > 0)
+    flash_block<W8_KB, true, false>(SwzAddr(smem + (nfull & 3) * W8_ST, of), qf, o, m, negm, l, nfull * W8_KB, Lk, hf);
 
   l = pair_sum(l);
   const float inv = 1.0f / l;

@@ -258,6 +258,77 @@ __device__ __forceinline__ void epilogue_tile(const GemmArgs& a, i32x16 v, int m
   }
 }
 
+// ------------------------------------------------------------------ 256x256 epilogue
+//
+// The 256x256 kernel multiplies with the weight fragment as srcA, so each 32x32 accumulator
+// tile is C^T: for lane (l, g) register r holds row m = (tile row) + l and column
+// n + 8(r/4) + r%4 with n = (tile column) + 4g.  Four consecutive columns of one row sit in four
+// consecutive registers and move as one 16-byte access; the row scale is one value per lane.
+// Arithmetic order is that of epilogue_store.
+struct EpiCols {  // per-column operands of one 32-column tile for this lane: columns n + 8q + e
+  f32x4 sw[4], gate[4];  // (a bias, rare, is read where it is added)
+};
+
+__device__ __forceinline__ void epi_cols(const GemmArgs& a, int n, EpiCols& c) {
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const bool ok = n + 8 * q < a.N;  // N % 4 == 0: a 4-column group is all in or all out
+    const int nq = ok ? n + 8 * q : 0;
+    c.sw[q] = *(const f32x4*)(a.sw + nq);
+    c.gate[q] = a.epi == ANIMA_EPI_GATED ? *(const f32x4*)(a.gate + a.gate_off + nq) : (f32x4){};
+  }
+}
+
+// residual C of one tile (RESID / GATED), rows past M and columns past N read as zero
+__device__ __forceinline__ void epi_load_c(const GemmArgs& a, int m, int n, f32x4 (&cv)[4]) {
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const bool ok = m < a.M && n + 8 * q < a.N;
+    cv[q] = ok ? *(const f32x4*)(a.out + (int64_t)m * a.ldc + n + 8 * q) : (f32x4){};
+  }
+}
+
+template <int EPI>
+__device__ __forceinline__ void epi_store_t(const GemmArgs& a, const i32x16& v, int m, int n, float sx,
+                                            const EpiCols& c, const f32x4 (&cv)[4]) {
+  if (m >= a.M) return;
+  float* orow = a.out + (int64_t)m * a.ldc;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int nq = n + 8 * q;
+    if (nq >= a.N) continue;
+    if (a.acc_out) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) a.acc_out[(int64_t)m * a.N + nq + e] = v[4 * q + e];
+    }
+    f32x4 y;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      float t = (float)v[4 * q + e] * sx;
+      y[e] = t * c.sw[q][e];
+    }
+    if (a.alpha != 1.0f) y = y * a.alpha;
+    if (a.bias) y = y + *(const f32x4*)(a.bias + nq);
+    if (a.act == ANIMA_ACT_GELU) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) y[e] = gelu_erf(y[e]);
+    } else if (a.act == ANIMA_ACT_SILU) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) y[e] = y[e] / (1.0f + expf(-y[e]));
+    }
+    f32x4 o;
+    if constexpr (EPI == ANIMA_EPI_STORE) {
+      o = y;
+    } else if constexpr (EPI == ANIMA_EPI_RESID) {
+      o = cv[q] + y;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) o[e] = __builtin_fmaf(c.gate[q][e], y[e], cv[q][e]);
+    }
+    *(f32x4*)(orow + nq) = o;
+  }
+}
+
 // ------------------------------------------------------------------ 256x256 int8 kernel
 //
 // gemm_i8_256: persistent workgroups (one per CU), each walking a list of 256 x 256 output
@@ -288,6 +359,7 @@ __device__ __forceinline__ void g2_barrier() {
 // vmcnt(n) only (expcnt and lgkmcnt at their no-wait maxima), gfx9 s_waitcnt encoding.
 #define G2_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
 
+template <int EPI>
 __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
   __shared__ __attribute__((aligned(1024))) char smem[G2_NST * G2_ST];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -314,24 +386,36 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
   const int row0 = 32 * wave + (lane >> 2), row1 = row0 + 16;
   const int loff0 = row0 * K + 16 * ((lane & 3) ^ ((row0 >> 2) & 3));
   const int loff1 = row1 * K + 16 * ((lane & 3) ^ ((row1 >> 2) & 3));
-  // stage g of the stream: tile g / nk, k bytes (g % nk) * 64, LDS stage g % 4.  Buffer
-  // resources cover the tile's rows only, so rows past M (N) read as zero.
-#define G2_ISSUE(g_)                                                                                          \
+  // The copy stream runs three stages ahead of the compute: ig = next stage to copy (LDS stage
+  // ig % 4), is = its k-stage within tile it; ra / rb are tile it's buffer resources, which
+  // cover the tile's rows only, so rows past M (N) read as zero.  Advanced incrementally (no
+  // division per stage).
+  int ig = 0, is = 0, it = 0;
+  __amdgpu_buffer_rsrc_t ra, rb;
+#define G2_RSRC()                                                                                             \
   {                                                                                                           \
-    const int k_ = (g_) / nk, s_ = (g_) - k_ * nk;                                                            \
-    const int t_ = first + k_ * stride, tm_ = t_ / ntn;                                                       \
+    const int t_ = first + it * stride, tm_ = t_ / ntn;                                                       \
     const int bm_ = tm_ * 256, bn_ = (t_ - tm_ * ntn) * 256;                                                  \
-    const __amdgpu_buffer_rsrc_t ra_ = __builtin_amdgcn_make_buffer_rsrc(                                     \
-        (void*)(a.qx + (int64_t)bm_ * K), (short)0, min(256, a.M - bm_) * K, 0x00020000);                     \
-    const __amdgpu_buffer_rsrc_t rb_ = __builtin_amdgcn_make_buffer_rsrc(                                     \
-        (void*)((const int8_t*)a.w + (int64_t)bn_ * K), (short)0, min(256, a.N - bn_) * K, 0x00020000);        \
-    char* st_ = smem + ((g_) & (G2_NST - 1)) * G2_ST;                                                         \
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_, (lds_void_t*)(st_ + (2 * wave) * 1024), 16, loff0, s_ * G2_BK, 0, 0); \
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_, (lds_void_t*)(st_ + (2 * wave + 1) * 1024), 16, loff1, s_ * G2_BK, 0, 0); \
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_, (lds_void_t*)(st_ + G2_TILE + (2 * wave) * 1024), 16, loff0,          \
-                                             s_ * G2_BK, 0, 0);                                               \
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_, (lds_void_t*)(st_ + G2_TILE + (2 * wave + 1) * 1024), 16, loff1,      \
-                                             s_ * G2_BK, 0, 0);                                               \
+    ra = __builtin_amdgcn_make_buffer_rsrc((void*)(a.qx + (int64_t)bm_ * K), (short)0, min(256, a.M - bm_) * K, \
+                                           0x00020000);                                                       \
+    rb = __builtin_amdgcn_make_buffer_rsrc((void*)((const int8_t*)a.w + (int64_t)bn_ * K), (short)0,           \
+                                           min(256, a.N - bn_) * K, 0x00020000);                              \
+  }
+#define G2_ISSUE()                                                                                            \
+  {                                                                                                           \
+    char* st_ = smem + (ig & (G2_NST - 1)) * G2_ST;                                                           \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(st_ + (2 * wave) * 1024), 16, loff0, is * G2_BK, 0, 0); \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(st_ + (2 * wave + 1) * 1024), 16, loff1, is * G2_BK, 0, \
+                                             0);                                                              \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(st_ + G2_TILE + (2 * wave) * 1024), 16, loff0,  \
+                                             is * G2_BK, 0, 0);                                               \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(st_ + G2_TILE + (2 * wave + 1) * 1024), 16, loff1, \
+                                             is * G2_BK, 0, 0);                                               \
+    ig++;                                                                                                     \
+    if (++is == nk) {                                                                                         \
+      is = 0;                                                                                                 \
+      if (++it < mine) G2_RSRC();                                                                             \
+    }                                                                                                         \
   }
   // fragment lane offsets: row lq of a 32-row tile, unit 2*ks + hf (k-step ks of 32 bytes)
   int fofs[2];
@@ -347,9 +431,10 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
   // Stage g is published (barrier) one iteration before it is computed, so the fragment reads
   // of its first k-step run under the MFMAs of stage g-1's second k-step.
   i32x4 af0[4], bf0[2], af1[4], bf1[2];
-  if (total > 0) G2_ISSUE(0);
-  if (total > 1) G2_ISSUE(1);
-  if (total > 2) G2_ISSUE(2);
+  if (total > 0) G2_RSRC();
+  if (total > 0) G2_ISSUE();
+  if (total > 1) G2_ISSUE();
+  if (total > 2) G2_ISSUE();
   if (total > 2) G2_WAIT_VM(8);
   else if (total > 1) G2_WAIT_VM(4);
   else G2_WAIT_VM(0);
@@ -367,7 +452,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
     if (g + 2 < total) G2_WAIT_VM(4);
     else G2_WAIT_VM(0);
     g2_barrier();
-    if (g + 3 < total) G2_ISSUE(g + 3);
+    if (g + 3 < total) G2_ISSUE();
     // Hand-ordered (sched_barrier fences keep the written order): each MFMA of one k-step is
     // followed by one fragment read for the next k-step, B fragments first, so a fragment is
     // read at least three MFMAs (~100 cycles) before its first use.  The second k-step reads
@@ -377,14 +462,14 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
     const char* sn = smem + ((g + 1) & (G2_NST - 1)) * G2_ST;
 #pragma unroll
     for (int q = 0; q < 8; q++) {
-      acc[q >> 1][q & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af0[q >> 1], bf0[q & 1], acc[q >> 1][q & 1], 0, 0, 0);
+      acc[q >> 1][q & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf0[q & 1], af0[q >> 1], acc[q >> 1][q & 1], 0, 0, 0);
       if (q < 2) bf1[q] = *(const i32x4*)(st + G2_TILE + (wn + 32 * q) * G2_BK + fofs[1]);
       else if (q < 6) af1[q - 2] = *(const i32x4*)(st + (wm + 32 * (q - 2)) * G2_BK + fofs[1]);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int q = 0; q < 8; q++) {
-      acc[q >> 1][q & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af1[q >> 1], bf1[q & 1], acc[q >> 1][q & 1], 0, 0, 0);
+      acc[q >> 1][q & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf1[q & 1], af1[q >> 1], acc[q >> 1][q & 1], 0, 0, 0);
       if (q < 2) bf0[q] = *(const i32x4*)(sn + G2_TILE + (wn + 32 * q) * G2_BK + fofs[0]);
       else if (q < 6) af0[q - 2] = *(const i32x4*)(sn + (wm + 32 * (q - 2)) * G2_BK + fofs[0]);
       __builtin_amdgcn_sched_barrier(0);
@@ -393,16 +478,31 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
       // tile done: epilogue (the next tile's first stages are already in flight), one 32x32
       // tile at a time, written out (a loop over the tiles is not fully unrolled at this size,
       // and a run-time tile index would put the accumulators in scratch memory)
+      // The residual loads of the next 32x32 tile are issued before the current tile's
+      // stores, so each tile's wait overlaps the previous tile's arithmetic.
       const int t = first + k * stride, tm = t / ntn;
-      const int m0 = tm * 256 + wm + 4 * hf, n0 = (t - tm * ntn) * 256 + wn + lq;
-      epilogue_tile(a, acc[0][0], m0, n0);
-      epilogue_tile(a, acc[0][1], m0, n0 + 32);
-      epilogue_tile(a, acc[1][0], m0 + 32, n0);
-      epilogue_tile(a, acc[1][1], m0 + 32, n0 + 32);
-      epilogue_tile(a, acc[2][0], m0 + 64, n0);
-      epilogue_tile(a, acc[2][1], m0 + 64, n0 + 32);
-      epilogue_tile(a, acc[3][0], m0 + 96, n0);
-      epilogue_tile(a, acc[3][1], m0 + 96, n0 + 32);
+      const int m0 = tm * 256 + wm + lq, n0 = (t - tm * ntn) * 256 + wn + 4 * hf;
+      float sxv[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) sxv[i] = m0 + 32 * i < a.M ? a.sx[m0 + 32 * i] : 0.0f;
+      EpiCols cc;  // column operands of the current 32-column tile (reloaded for the second)
+      epi_cols(a, n0, cc);
+      f32x4 cA[4], cB[4];
+#define G2_C(buf, i, j) \
+  if constexpr (EPI != ANIMA_EPI_STORE) epi_load_c(a, m0 + 32 * (i), n0 + 32 * (j), buf);
+#define G2_T(buf, i, j, cc) epi_store_t<EPI>(a, acc[i][j], m0 + 32 * (i), n0 + 32 * (j), sxv[i], cc, buf);
+      G2_C(cA, 0, 0)
+      G2_C(cB, 1, 0) G2_T(cA, 0, 0, cc)
+      G2_C(cA, 2, 0) G2_T(cB, 1, 0, cc)
+      G2_C(cB, 3, 0) G2_T(cA, 2, 0, cc)
+      G2_C(cA, 0, 1) G2_T(cB, 3, 0, cc)
+      epi_cols(a, n0 + 32, cc);
+      G2_C(cB, 1, 1) G2_T(cA, 0, 1, cc)
+      G2_C(cA, 2, 1) G2_T(cB, 1, 1, cc)
+      G2_C(cB, 3, 1) G2_T(cA, 2, 1, cc)
+      G2_T(cB, 3, 1, cc)
+#undef G2_C
+#undef G2_T
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -414,6 +514,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
 }
 #undef G2_WAIT_VM
 #undef G2_ISSUE
+#undef G2_RSRC
 
 // ------------------------------------------------------------------ W4 -> int8 decode pass
 //
@@ -635,8 +736,12 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
   // Grids that give every CU a 256x256 tile run the persistent 256 kernel; a W4 weight is then
   // decoded once into an int8 workspace first.  Smaller grids run the 128x128 kernel, which
   // decodes W4 inside the GEMM.
+  // The 256 kernel's epilogue moves 16-byte column groups: it needs N % 4 == 0 and 16-byte
+  // aligned output rows, scales, bias and gate.
   const int64_t tiles256 = (int64_t)((N + 255) / 256) * ((M + 255) / 256);
-  const bool big = tiles256 >= c->num_cus && tiles256 <= 0x7fffffff;
+  const bool vec = N % 4 == 0 && g.ldc % 4 == 0 && al(g.out, 16) && al(g.sw, 16) && (!g.bias || al(g.bias, 16)) &&
+                   (g.epi != ANIMA_EPI_GATED || al(g.gate + g.gate_off, 16));
+  const bool big = vec && tiles256 >= c->num_cus && tiles256 <= 0x7fffffff;
   void* wdec = nullptr;
   if (big && w4) {
     if ((rc = anima_alloc(c, (size_t)N * K, &wdec))) {
@@ -654,7 +759,12 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
   if (rc == ANIMA_OK) {
     Launch L(c, w4 ? "gemm.w4a8" : "gemm.i8", 2.0 * M * N * K, 0.0);
     if (big) {
-      hipLaunchKernelGGL(gemm_i8_256, dim3((unsigned)c->num_cus), dim3(512), 0, c->stream, g);
+      if (g.epi == ANIMA_EPI_STORE)
+        hipLaunchKernelGGL(gemm_i8_256<ANIMA_EPI_STORE>, dim3((unsigned)c->num_cus), dim3(512), 0, c->stream, g);
+      else if (g.epi == ANIMA_EPI_RESID)
+        hipLaunchKernelGGL(gemm_i8_256<ANIMA_EPI_RESID>, dim3((unsigned)c->num_cus), dim3(512), 0, c->stream, g);
+      else
+        hipLaunchKernelGGL(gemm_i8_256<ANIMA_EPI_GATED>, dim3((unsigned)c->num_cus), dim3(512), 0, c->stream, g);
     } else {
       dim3 grid((N + GBN - 1) / GBN, (unsigned)((M + GBM - 1) / GBM));
       if (w4) hipLaunchKernelGGL(gemm_i8_kernel<true>, grid, dim3(256), 0, c->stream, g);
