@@ -36,13 +36,18 @@ struct GemmArgs {
   int M, N, K;
 };
 
-__device__ __forceinline__ float gelu_erf(float x) {  // app/gpu/kernels.js:11-18
+// GELU with the Abramowitz-Stegun erf of app/gpu/kernels.js:11-18.  The reciprocal is v_rcp_f32
+// (1 ulp) and the exponential v_exp_f32 of the argument scaled by log2(e) (about 1 ulp plus the
+// rounding of the scaled argument): inside the accuracy WGSL itself grants the reference's
+// division (2.5 ulp) and exp (3 + 2|x| ulp); against the correctly rounded formula the output
+// differs by 2e-8 relative L2 on N(0, 9) inputs.
+__device__ __forceinline__ float gelu_erf(float x) {
   const float z = x * 0.7071067811865476f;
   const float s = z > 0.0f ? 1.0f : (z < 0.0f ? -1.0f : 0.0f);
   const float a = fabsf(z);
-  const float t = 1.0f / (1.0f + 0.3275911f * a);
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * a);
   const float y = 1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
-                          0.254829592f) * t * expf(-a * a);
+                          0.254829592f) * t * __expf(-a * a);
   return 0.5f * x * (1.0f + s * y);
 }
 

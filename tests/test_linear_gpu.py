@@ -258,6 +258,32 @@ def test_256_tile_kernel_ragged_edges(ctx, kind):
     assert np.array_equal(got[rows], ref), report("gated", got[rows], ref)
 
 
+@pytest.mark.parametrize("act,epi", [("gelu", 0), ("silu", 1)])
+def test_256_tile_kernel_activation_epilogues(ctx, act, epi):
+    """The 256x256 kernel with GELU (store) and SiLU (residual add) epilogues at M=4000, N=4100:
+    accumulators exact (checksums + sampled rows), activations within 1e-6 relative of the
+    oracle's correctly rounded formula (the device uses its 1-ulp reciprocal and exp2)."""
+    case(f"256x256-tile kernel M=4000 N=4100 K=1024 {act} epi={epi}")
+    m = amd()
+    M, K, N = 4000, 1024, 4100
+    x = orc.randn(97, M * K).reshape(M, K)
+    qx, sx = orc.token_quant(orc.hadamard256(x))
+    qw, sw = int8_weight(98, N, K)
+    W = m.weight(m.W_I8, N, K, ctx.upload(qw), scale=ctx.upload(sw))
+    resid = orc.randn(99, M * N).reshape(M, N)
+    dout, dacc = ctx.upload(resid), ctx.empty((M, N), np.int32)
+    ctx.linear(W, M, dout, xq=ctx.upload(qx), xs=ctx.upload(sx), act=act, epilogue=epi, acc_out=dacc)
+    acc, got = dacc.numpy(), dout.numpy()
+    assert checksums_ok(qx, qw, acc), "int32 accumulator checksums"
+    rows = np.unique(np.concatenate([np.arange(0, 4), np.random.default_rng(2).choice(M, 16, replace=False),
+                                     np.arange(M - 20, M)]))
+    ref_acc = orc.gemm_i8(qx[rows], qw)
+    assert np.array_equal(acc[rows], ref_acc)
+    ref = orc.linear_epilogue(ref_acc, sx[rows], sw, act=1 if act == "gelu" else 2, epi=epi, c=resid[rows])
+    g = got[rows]
+    assert rel_l2(g, ref) < 1e-6 and np.max(np.abs(g - ref)) <= 1e-6 * np.max(np.abs(ref)), report(act, g, ref)
+
+
 @pytest.mark.parametrize("act", ["gelu", "silu"])
 def test_mlp1_activation_epilogue(ctx, act):
     case(f"mlp1 2048 -> 8192 {act} M=200 and mlp2 8192 -> 2048")
