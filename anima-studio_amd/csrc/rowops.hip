@@ -329,9 +329,17 @@ __global__ __launch_bounds__(256) void quant_rows_pad_kernel(const float* X, int
   if (row >= M) return;  // (a whole row's threads leave together; WPR > 1 launches one row per workgroup)
   float* S = SH + (size_t)(threadIdx.x / T) * padded_cols(K);
   const float* x = X + row * K;
-  for (int c4 = tr; c4 < (K >> 2); c4 += T) {
-    const float4 v = *(const float4*)(x + 4 * c4);
-    *(float4*)(S + padx(4 * c4)) = rotate ? bfly4(v) : v;
+  // every load of the row is issued before the first use (K <= 8 * 4 * T)
+  float4 v[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int c4 = tr + T * i;
+    v[i] = c4 < (K >> 2) ? *(const float4*)(x + 4 * c4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int c4 = tr + T * i;
+    if (c4 < (K >> 2)) *(float4*)(S + padx(4 * c4)) = rotate ? bfly4(v[i]) : v[i];
   }
   row_sync<WPR>();
   if (rotate) butterfly_stages234<WPR>(S, K, tr);
@@ -366,20 +374,32 @@ __global__ __launch_bounds__(256) void layernorm_mod_wave_kernel(const float* X,
   float* S = SH + (size_t)wave * padded_cols(cols);
   const float* x = X + row * cols;
   const int c4n = cols >> 2;
-  // raw row into LDS; per-thread partial sums of the virtual threads 4*lane + j
+  // the row stays in registers (every load issued before the first use; cols <= 2048);
+  // per-thread partial sums of the virtual threads 4*lane + j
+  float4 xv[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int c4 = lane + 64 * i;
+    xv[i] = c4 < c4n ? *(const float4*)(x + 4 * c4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
   float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
-  for (int c4 = lane; c4 < c4n; c4 += 64) {
-    const float4 v = *(const float4*)(x + 4 * c4);
-    *(float4*)(S + padx(4 * c4)) = v;
-    p0 += v.x;
-    p1 += v.y;
-    p2 += v.z;
-    p3 += v.w;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int c4 = lane + 64 * i;
+    if (c4 < c4n) {
+      const float4 v = xv[i];
+      p0 += v.x;
+      p1 += v.y;
+      p2 += v.z;
+      p3 += v.w;
+    }
   }
   const float mean = wave_tree_sum4(p0, p1, p2, p3) / (float)cols;
   p0 = p1 = p2 = p3 = 0.0f;
-  for (int c4 = lane; c4 < c4n; c4 += 64) {
-    const float4 v = *(const float4*)(S + padx(4 * c4));
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    if (lane + 64 * i >= c4n) break;
+    const float4 v = xv[i];
     const float d0 = v.x - mean, d1 = v.y - mean, d2 = v.z - mean, d3 = v.w - mean;
     p0 += d0 * d0;
     p1 += d1 * d1;
@@ -387,8 +407,11 @@ __global__ __launch_bounds__(256) void layernorm_mod_wave_kernel(const float* X,
     p3 += d3 * d3;
   }
   const float r = 1.0f / sqrtf(wave_tree_sum4(p0, p1, p2, p3) / (float)cols + eps);
-  for (int c4 = lane; c4 < c4n; c4 += 64) {
-    const float4 v = *(const float4*)(S + padx(4 * c4));
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int c4 = lane + 64 * i;
+    if (c4 >= c4n) break;
+    const float4 v = xv[i];
     const float4 sc = *(const float4*)(MOD + scale_off + 4 * c4);
     const float4 sh = *(const float4*)(MOD + shift_off + 4 * c4);
     const float4 n = make_float4((v.x - mean) * r * (1.0f + sc.x) + sh.x, (v.y - mean) * r * (1.0f + sc.y) + sh.y,
