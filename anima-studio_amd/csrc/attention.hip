@@ -291,11 +291,13 @@ struct PadAddr {
 constexpr int SWZ_KT = 64 * HD * 2;  // K tile bytes; the V^T tile follows
 struct SwzOfs {
   int k[8], v[4];  // lane parts: k[ks] (row lq of key tile 0), v[2t+h] (row lq of dim tile 0)
-  __device__ __forceinline__ SwzOfs(int lq, int hf) {
+  // base: a constant added to every part, so that a stage address can stay within the 16-bit
+  // immediate offset of ds_read
+  __device__ __forceinline__ SwzOfs(int lq, int hf, int base = 0) {
 #pragma unroll
-    for (int ks = 0; ks < 8; ks++) k[ks] = lq * 256 + 16 * ((2 * ks + hf) ^ (lq & 15));
+    for (int ks = 0; ks < 8; ks++) k[ks] = base + lq * 256 + 16 * ((2 * ks + hf) ^ (lq & 15));
 #pragma unroll
-    for (int j = 0; j < 4; j++) v[j] = SWZ_KT + lq * 128 + 16 * ((2 * j + hf) ^ ((lq >> 1) & 7));
+    for (int j = 0; j < 4; j++) v[j] = base + SWZ_KT + lq * 128 + 16 * ((2 * j + hf) ^ ((lq >> 1) & 7));
   }
 };
 struct SwzAddr {
@@ -735,14 +737,29 @@ __global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) f[i] = A1.k(0, i);
   }
-  for (int j = 1; j < nfull; j++) {
-    if (j + 2 < nkb) W8_WAIT_VM(4);
-    else W8_WAIT_VM(0);
-    w8_barrier();
-    if (j + 3 < nkb) w8_load(src, lo, j + 3, smem + ((j + 3) & 3) * W8_ST, wave);
-    flash_block_main<SwzAddr, true>(SwzAddr(smem + (j & 3) * W8_ST, of), SwzAddr(smem + ((j + 1) & 3) * W8_ST, of), f,
-                                    qf, o, m, negm, l);
+  // The loop is unrolled over the four stages so that every LDS address is a lane offset plus an
+  // immediate: stages 0 and 1 use the offsets of `of`, stages 2 and 3 those of `of2` (+64 KiB),
+  // which keeps each immediate below 64 KiB.
+  const SwzOfs of2(lq, hf, 2 * W8_ST);
+#define W8_ADDR(ST) SwzAddr(smem + ((ST) & 1) * W8_ST, (ST) < 2 ? of : of2)
+#define W8_ITER(ST)                                                                                    \
+  {                                                                                                    \
+    if (j >= nfull) break;                                                                             \
+    if (j + 2 < nkb) W8_WAIT_VM(4);                                                                    \
+    else W8_WAIT_VM(0);                                                                                \
+    w8_barrier();                                                                                      \
+    if (j + 3 < nkb) w8_load(src, lo, j + 3, smem + (((ST) + 3) & 3) * W8_ST, wave);                   \
+    flash_block_main<SwzAddr, true>(W8_ADDR(ST), W8_ADDR(((ST) + 1) & 3), f, qf, o, m, negm, l);        \
+    j++;                                                                                               \
   }
+  for (int j = 1;;) {
+    W8_ITER(1)
+    W8_ITER(2)
+    W8_ITER(3)
+    W8_ITER(0)
+  }
+#undef W8_ITER
+#undef W8_ADDR
   if (nfull < nkb && nfull > 0)
     flash_block<W8_KB, true, false>(SwzAddr(smem + (nfull & 3) * W8_ST, of), qf, o, m, negm, l, nfull * W8_KB, Lk, hf);
 
