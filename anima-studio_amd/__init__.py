@@ -97,6 +97,8 @@ def lib():
                                           _vp, _vp, _vp]
         L.anima_elementwise.argtypes = [_vp, ctypes.c_int, _vp, _vp, _vp, _i64]
         L.anima_zero.argtypes = [_vp, _vp, _i64]
+        L.anima_linear_grouped_bf16.argtypes = [_vp, ctypes.c_int, _i64, ctypes.c_int, ctypes.c_int, _vp, _i64, _i64, _vp,
+                                                 _i64, _vp, _i64, _vp, _i64, _i64]
         L.anima_patchify.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]
         L.anima_unpatchify.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]
         L.anima_linear.argtypes = [_vp, ctypes.POINTER(LinearDesc)]
@@ -244,6 +246,12 @@ class Context:
 
     def zero(self, y, n):
         return self._check(lib().anima_zero(self.h, _ptr(y), n))
+
+    def linear_grouped_bf16(self, G, M, N, K, x, ldx, x_gstride, w, w_gstride, bias, bias_gstride, out, ldc,
+                            out_gstride):
+        return self._check(lib().anima_linear_grouped_bf16(self.h, G, M, N, K, _ptr(x), ldx, x_gstride, _ptr(w),
+                                                           w_gstride, _ptr(bias), bias_gstride, _ptr(out), ldc,
+                                                           out_gstride))
 
     def patchify(self, latents, B, h, w, patches):
         return self._check(lib().anima_patchify(self.h, _ptr(latents), B, h, w, _ptr(patches)))

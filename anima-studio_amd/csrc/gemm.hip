@@ -573,6 +573,9 @@ struct F32WArgs {
   const float* gate;
   int64_t gate_off;
   int M, N, K;
+  // grouped GEMV only: group g = blockIdx.y reads x + g*x_gs, w + g*w_gs, bias + g*bias_gs and
+  // writes out + g*out_gs (all zero for a single product)
+  int64_t x_gs, w_gs, bias_gs, out_gs;
 };
 
 // 64x64 tile, 256 threads x (4x4) outputs, k-tile 16 (the small-tile layout of gemm.js:17).
@@ -632,6 +635,11 @@ __global__ __launch_bounds__(256) void gemv_f32w_kernel(F32WArgs a) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= a.N) return;
+  const int64_t grp = blockIdx.y;
+  a.x += grp * a.x_gs;
+  a.w += grp * a.w_gs;
+  if (a.bias) a.bias += grp * a.bias_gs;
+  a.out += grp * a.out_gs;
   float acc[GEMV_MAXM];
 #pragma unroll
   for (int m = 0; m < GEMV_MAXM; m++) acc[m] = 0.0f;
@@ -780,6 +788,24 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
   if (wdec) anima_free(c, wdec);  // stream-ordered reuse
   if (tmp) anima_free(c, tmp);
   return rc;
+}
+
+int linear_grouped_bf16_launch(anima_ctx* c, int G, int64_t M, int N, int K, const float* x, int64_t ldx,
+                               int64_t x_gs, const uint16_t* w, int64_t w_gs, const float* bias, int64_t bias_gs,
+                               float* out, int64_t ldc, int64_t out_gs) {
+  if (!x || !w || !out) return fail(c, ANIMA_E_ARG, "anima_linear_grouped_bf16: null x, w or out");
+  if (G < 1 || G > 65535 || M < 1 || M > GEMV_MAXM || N < 1 || K < 8 || K % 8)
+    return fail(c, ANIMA_E_ARG, "anima_linear_grouped_bf16: G=%d M=%lld N=%d K=%d (1 <= G <= 65535, 1 <= M <= %d, K %% 8 == 0)",
+                G, (long long)M, N, K, GEMV_MAXM);
+  if (ldx < K || ldc < N || x_gs < 0 || w_gs < 0 || bias_gs < 0 || out_gs < 0)
+    return fail(c, ANIMA_E_ARG, "anima_linear_grouped_bf16: bad leading dimension or group stride");
+  if (!al(x, 16) || !al(w, 16) || ldx % 4 || x_gs % 4 || w_gs % 8)
+    return fail(c, ANIMA_E_ARG, "anima_linear_grouped_bf16: x and w must be 16-byte aligned (ldx, x stride %% 4, w stride %% 8)");
+  F32WArgs f{x, ldx, w, bias, out, ldc, 1.0f, ANIMA_ACT_NONE, ANIMA_EPI_STORE, nullptr, 0, (int)M, N, K,
+             x_gs, w_gs, bias_gs, out_gs};
+  Launch L(c, "gemv.bf16.grouped", 2.0 * G * M * N * K, 2.0 * G * N * K);
+  hipLaunchKernelGGL(gemv_f32w_kernel, dim3((N + 3) / 4, (unsigned)G), dim3(256), 0, c->stream, f);
+  return L.end();
 }
 
 }  // namespace anima

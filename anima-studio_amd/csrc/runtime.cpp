@@ -411,4 +411,12 @@ int anima_linear(anima_ctx* c, const anima_linear_desc* d) {
   return linear_launch(c, d);
 }
 
+int anima_linear_grouped_bf16(anima_ctx* c, int G, int64_t M, int N, int K, const float* x, int64_t ldx,
+                              int64_t x_gstride, const uint16_t* w, int64_t w_gstride, const float* bias,
+                              int64_t bias_gstride, float* out, int64_t ldc, int64_t out_gstride) {
+  CHECK_CTX(c);
+  return linear_grouped_bf16_launch(c, G, M, N, K, x, ldx, x_gstride, w, w_gstride, bias, bias_gstride, out, ldc,
+                                    out_gstride);
+}
+
 }  // extern "C"

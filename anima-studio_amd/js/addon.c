@@ -391,6 +391,19 @@ static napi_value js_elementwise(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* linearGroupedBf16(ctx, G, M, N, K, x, ldx, xStride, w, wStride, bias, biasStride, out, ldc, outStride) */
+static napi_value js_linear_grouped_bf16(napi_env env, napi_callback_info info) {
+  napi_value a[15];
+  get_args(env, info, 15, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_linear_grouped_bf16(c, (int)num(env, a[1]), i64(env, a[2]), (int)num(env, a[3]),
+                                             (int)num(env, a[4]), (const float*)ptr(env, a[5]), i64(env, a[6]),
+                                             i64(env, a[7]), (const uint16_t*)ptr(env, a[8]), i64(env, a[9]),
+                                             (const float*)ptr(env, a[10]), i64(env, a[11]), (float*)ptr(env, a[12]),
+                                             i64(env, a[13]), i64(env, a[14])));
+  return NULL;
+}
+
 /* patchify(ctx, latents, B, h, w, patches) */
 static napi_value js_patchify(napi_env env, napi_callback_info info) {
   napi_value a[6];
@@ -488,7 +501,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       FN("timerStart", js_timer_start), FN("timerStop", js_timer_stop), FN("attention", js_attention),
       FN("qkNormRope", js_qk_norm_rope), FN("rmsnorm", js_rmsnorm), FN("rope", js_rope),
       FN("hadamard", js_hadamard), FN("quantRows", js_quant_rows), FN("layernormMod", js_layernorm_mod),
-      FN("elementwise", js_elementwise), FN("zero", js_zero), FN("patchify", js_patchify), FN("unpatchify", js_unpatchify), FN("fillRandom", js_fill_random),
+      FN("elementwise", js_elementwise), FN("zero", js_zero), FN("patchify", js_patchify), FN("linearGroupedBf16", js_linear_grouped_bf16), FN("unpatchify", js_unpatchify), FN("fillRandom", js_fill_random),
       FN("linear", js_linear), FN("lastError", js_last_error),
   };
 #undef FN

@@ -69,6 +69,7 @@ export class AnimaDiT {
     }
     m.finalMod = [st.linear(gpu, "final_layer.adaln_modulation.1."), st.linear(gpu, "final_layer.adaln_modulation.2.")];
     m.finalLinear = st.linear(gpu, "final_layer.linear.");
+    m.fuseModulation();
     return m;
   }
 
@@ -98,12 +99,33 @@ export class AnimaDiT {
     }
     m.finalMod = [bf("final_layer.adaln_modulation.1", ADALN_RANK, D), src.bf16Linear(gpu, "final_layer.adaln_modulation.2", 2 * D, ADALN_RANK, 0.1)];
     m.finalLinear = bf("final_layer.linear", 64, D);
+    m.fuseModulation();
     return m;
   }
 
   constructor(gpu) {
     this.gpu = gpu;
     this.ropeCache = new Map(); // "HpxWp" -> device RoPE table; depends only on the token grid
+    this.modFused = null;
+  }
+
+  // The 3 * blocks + 1 adaLN modulation linears all read the same SiLU(t-embedding) (dit.js:205-
+  // 222): their first stages are stacked into one [(3B+1)*256, 2048] weight (one GEMV) and the
+  // blocks' second stages into one [3B*6144, 256] weight run as one grouped GEMV, with adaln_lora
+  // added as a bias shared by every group (the same sum as the reference's lora + W2 h).  Only
+  // for bias-free bf16 weights (the checkpoint format); otherwise the per-linear path stays.
+  fuseModulation() {
+    const first = [], second = [];
+    for (const b of this.blocks) {
+      first.push(b.modSelf[0], b.modCross[0], b.modMlp[0]);
+      second.push(b.modSelf[1], b.modCross[1], b.modMlp[1]);
+    }
+    first.push(this.finalMod[0]);
+    const ok = (ws) => ws.every((w) => w.kind === "bf16" && w.K === ws[0].K && w.N === ws[0].N && !w.bias);
+    if (!ok(first) || !ok(second) || this.finalMod[1].kind !== "bf16" || this.finalMod[1].bias) return;
+    this.modFused = { w1: concatLinears(this.gpu, first), w2: concatLinears(this.gpu, second), final2: this.finalMod[1] };
+    for (const b of this.blocks) { delete b.modSelf; delete b.modCross; delete b.modMlp; }
+    this.finalMod = null;
   }
 
   ropeTable(Hp, Wp) {
@@ -133,6 +155,31 @@ export class AnimaDiT {
     t.release();
     const semb = ops.elementwise(gpu, "silu", emb);
     emb.release();
+    if (this.modFused) {
+      const { w1, w2, final2 } = this.modFused;
+      const G = 3 * this.blocks.length, R = ADALN_RANK;
+      const h1 = ops.linear(gpu, semb, w1); // [1, (G + 1) * 256]
+      const all = gpu.empty([G, 3 * D]);
+      native.linearGroupedBf16(gpu.ctx, G, 1, 3 * D, R, h1.buf, (G + 1) * R, R, w2.buf.buf, 3 * D * R, lora.buf, 0,
+        all.buf, 3 * D, 3 * D);
+      const final = gpu.empty([1, 2 * D]);
+      native.linearGroupedBf16(gpu.ctx, 1, 1, 2 * D, R, h1.at(G * R), R, 0, final2.buf.buf, 0, lora.buf, 0, final.buf,
+        2 * D, 0);
+      h1.release();
+      semb.release();
+      lora.release();
+      const blocks = this.blocks.map((_, i) => ({
+        self: all.view(3 * i * 3 * D, [1, 3 * D]), cross: all.view((3 * i + 1) * 3 * D, [1, 3 * D]),
+        mlp: all.view((3 * i + 2) * 3 * D, [1, 3 * D]),
+      }));
+      return {
+        blocks, final,
+        release() {
+          all.release();
+          final.release();
+        },
+      };
+    }
     const mod = (ws, n) => {
       const out = gpu.empty([1, n]);
       ops.elementwise(gpu, "copy", lora, null, out); // the first n entries

@@ -36,6 +36,14 @@ export class Tensor {
   at(i) {
     return this.buf + i * ESIZE[this.dtype];
   }
+  // non-owning view of elements [i, i + prod(shape)); its release() only drops the reference
+  view(i, shape) {
+    const t = new Tensor(this.gpu, this.at(i), shape, shape.reduce((a, b) => a * b, 1) * ESIZE[this.dtype], this.dtype);
+    t.release = () => {
+      t.buf = 0;
+    };
+    return t;
+  }
   release() {
     if (this.buf) native.free(this.gpu.ctx, this.buf);
     this.buf = 0;

@@ -228,6 +228,17 @@ typedef struct {
  * i8/w4 need K % 64 == 0 (and K <= 8192 when x is quantized here). */
 int anima_linear(anima_ctx* ctx, const anima_linear_desc* desc);
 
+/* G independent small-M bf16-weight products in one launch, for the adaLN modulation linears of
+ * timeCond (app/models/dit.js:196-225 runs one per block and kind, all on the same sigma):
+ *   out[g*out_gstride + m*ldc + n] = sum_k x[g*x_gstride + m*ldx + k] * w[g*w_gstride + n*K + k]
+ *                                    (+ bias[g*bias_gstride + n])
+ * for g < G, m < M, n < N, with the fp32 FMA order of anima_linear's bf16 GEMV.  M <= 8,
+ * K % 8 == 0, x and w 16-byte aligned, ldx and x_gstride multiples of 4, w_gstride of 8; a
+ * bias_gstride of 0 adds the same bias to every group. */
+int anima_linear_grouped_bf16(anima_ctx* ctx, int G, int64_t M, int N, int K, const float* x, int64_t ldx,
+                              int64_t x_gstride, const uint16_t* w, int64_t w_gstride, const float* bias,
+                              int64_t bias_gstride, float* out, int64_t ldc, int64_t out_gstride);
+
 #ifdef __cplusplus
 }
 #endif
