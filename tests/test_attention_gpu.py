@@ -313,6 +313,57 @@ def test_attention_8wave_kernel_key_lengths(ctx):
     assert report("b<8 bf16 vs fp64", got[:8], ref64)[0] <= 1e-2
 
 
+@pytest.mark.parametrize("gqa", [False, True])
+def test_attention_8wave_kernel_partial_query_tile(ctx, gqa):
+    """B=4 H=16 Lq=1000: 4 x 16 x 4 = 256 workgroups of 256 queries (the 8-wave kernel), the last
+    query tile a quarter full (rows past Lq are neither computed into nor stored).  Without GQA:
+    fused q/k RMSNorm + RoPE on a 25 x 40 token grid; with GQA (2 query heads per K/V head):
+    padded rows, ragged key lengths.  Sampled rows (every 7th and the last 40) against the bf16
+    numerics model and float64."""
+    case(f"attention 8-wave kernel B=4 H=16 Lq=1000 partial query tile gqa={gqa}")
+    m = amd()
+    B, H = 4, 16
+    rows = np.unique(np.concatenate([np.arange(0, 1000, 7), np.arange(960, 1000)]))
+    if not gqa:
+        qkv, qn, kn, cs, L = fused_inputs(61, B, 25, 40, H)
+        ctx.profile(True)
+        ctx.profile_reset()
+        got = run_fused(ctx, qkv, qn, kn, cs, L, H, m.PREC_BF16)
+        names = {r["name"] for r in ctx.profile_report()}
+        ctx.profile(False)
+        nqkv = cpu_norm_rope(qkv, qn, kn, cs, L, H)
+        for b in range(B):
+            model = oracle_rows("bf16", nqkv, b, rows, L, H)
+            assert report(f"b={b} bf16 vs model", got[b, rows], model)[0] <= 3e-4
+        assert report("b=0 bf16 vs fp64", got[0, rows], oracle_rows("f64", nqkv, 0, rows, L, H))[0] <= 1e-2
+    else:
+        Lq, Lk, group = 1000, 777, 2
+        Hkv = H // group
+        ldq, ldk = H * HD + 4, 2 * Hkv * HD + 8
+        q = orc.randn(62, B * Lq * ldq).reshape(B, Lq, ldq)
+        kv = orc.randn(63, B * Lk * ldk).reshape(B, Lk, ldk)
+        kv_len = np.array([777, 500, 64, 1], np.int32)
+        dq, dkv = ctx.upload(q), ctx.upload(kv)
+        do = ctx.empty((B, Lq, H * HD))
+        ctx.profile(True)
+        ctx.profile_reset()
+        ctx.attention(q=dq, k=dkv, v=dkv, o=do, B=B, Lq=Lq, Lk=Lk, H=H, D=HD, group=group, ldq=ldq, ldk=ldk,
+                      ldv=ldk, q_off=0, k_off=0, v_off=Hkv * HD, kv_len=kv_len, precision=m.PREC_BF16)
+        names = {r["name"] for r in ctx.profile_report()}
+        ctx.profile(False)
+        got = do.numpy()
+        qs = np.ascontiguousarray(q[:, rows])
+        args = dict(B=B, Lq=len(rows), Lk=Lk, H=H, D=HD, group=group, ldq=ldq, ldk=ldk, ldv=ldk, q_off=0, k_off=0,
+                    v_off=Hkv * HD, kv_len=kv_len)
+        model = orc.attention("bf16", qs, kv, kv, **args)
+        for b in range(B):
+            assert report(f"b={b} kv_len={kv_len[b]} bf16 vs model", got[b, rows], model[b])[0] <= 3e-4
+        ref64 = orc.attention("f64", qs, kv, kv, **args)
+        assert report("bf16 vs fp64", got[:, rows], ref64)[0] <= 1e-2
+    assert "attn.flash_bf16" in names, names
+    assert np.all(np.isfinite(got))
+
+
 def test_attention_rejects_bad_arguments(ctx):
     case("attention argument validation")
     m = amd()
