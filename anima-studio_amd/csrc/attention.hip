@@ -91,18 +91,29 @@ __global__ __launch_bounds__(256) void attn_prep_kv(PrepArgs a) {
       ss += __shfl_xor(ss, 1);
       ss += __shfl_xor(ss, 2);
       const float rn = 1.0f / sqrtf(ss / (float)HD + a.eps);
+      float w[32];  // norm weights of dims 16p.. and 64+16p.., as 16-byte loads
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        *(float4*)(w + 4 * j) = *(const float4*)(a.kn + 16 * p + 4 * j);
+        *(float4*)(w + 16 + 4 * j) = *(const float4*)(a.kn + 64 + 16 * p + 4 * j);
+      }
 #pragma unroll
       for (int i = 0; i < 16; i++) {
-        x[i] = x[i] * rn * a.kn[16 * p + i];
-        x[16 + i] = x[16 + i] * rn * a.kn[64 + 16 * p + i];
+        x[i] = x[i] * rn * w[i];
+        x[16 + i] = x[16 + i] * rn * w[16 + i];
       }
     }
     if (ROPE && l < a.Lk) {
       const float* cr = a.cs + (int64_t)l * (HD / 2) + 16 * p;
-      const float* sr = a.cs + a.sin_off + (int64_t)l * (HD / 2) + 16 * p;
+      float cv[16], sv[16];  // 16-byte loads (the table is 16-byte aligned, rows of 64)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        *(float4*)(cv + 4 * j) = *(const float4*)(cr + 4 * j);
+        *(float4*)(sv + 4 * j) = *(const float4*)(cr + a.sin_off + 4 * j);
+      }
 #pragma unroll
       for (int i = 0; i < 16; i++) {
-        const float c = cr[i], s = sr[i];
+        const float c = cv[i], s = sv[i];
         const float x1 = x[i], x2 = x[16 + i];
         x[i] = x1 * c - x2 * s;
         x[16 + i] = x2 * c + x1 * s;
@@ -949,6 +960,8 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
                   (long long)lds[i], (long long)offs[i], heads[i], HD);
   }
   if (!al16(d->q) || !al16(d->k) || !al16(d->v) || !al16(d->o)) return fail(c, ANIMA_E_ARG, "anima_attention: q/k/v/o must be 16-byte aligned");
+  if ((d->q_norm && !al16(d->q_norm)) || (d->k_norm && !al16(d->k_norm)))
+    return fail(c, ANIMA_E_ARG, "anima_attention: q_norm/k_norm must be 16-byte aligned");
   int kv_len[MAXB];
   for (int b = 0; b < d->B; b++) {
     kv_len[b] = d->kv_len ? d->kv_len[b] : d->Lk;
@@ -960,6 +973,7 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
     if (d->rope_sin_off <= 0 || d->rope_sin_off % (HD / 2) || rows < d->Lq || rows < d->Lk)
       return fail(c, ANIMA_E_ARG, "anima_attention: rope_sin_off=%lld must be rows*%d with rows >= max(Lq,Lk)=%d",
                   (long long)d->rope_sin_off, HD / 2, d->Lq > d->Lk ? d->Lq : d->Lk);
+    if (!al16(d->rope_cs)) return fail(c, ANIMA_E_ARG, "anima_attention: rope_cs must be 16-byte aligned");
   }
   const float scale = d->scale != 0.0f ? d->scale : 1.0f / sqrtf((float)HD);
   const float eps = d->eps;
