@@ -346,6 +346,118 @@ __global__ __launch_bounds__(256) void quant_rows_pad_kernel(const float* X, int
   quant_row_padded<WPR>(S, K, tr, rotate, red, nullptr, Q + row * K, S_out + row);
 }
 
+// ------------------------------------------------------------------ register-resident rows
+//
+// Rows of K % 1024 == 0 columns: lane L of a row's LR = K/64 lanes holds the 64 consecutive
+// elements 64L..64L+63, so a 256-element Hadamard block sits in 4 consecutive lanes (a DPP quad).
+// Butterfly stages 1-3 (strides 1, 4, 16) combine elements of one lane; stage 4 (stride 64)
+// combines the four lanes of the quad through DPP broadcasts.  Each stage applies the 4-point
+// formula of the reference in its order: out_k = ((x0 s0 + x1 s1) + x2 s2) + x3 s3 with
+// s_m = -1 exactly when m = 3 - k (kernels.js:359-388), so every fp32 result equals the LDS
+// variant's.  No LDS except the cross-wave maximum of rows wider than a wave.
+
+// 4-point butterfly of the reference on four values held by one lane (outputs in place)
+__device__ __forceinline__ void bfly4_ref(float& a, float& b, float& c, float& e) {
+  const float o0 = a + b + c - e, o1 = a + b - c + e, o2 = a - b + c + e, o3 = -a + b + c + e;
+  a = o0;
+  b = o1;
+  c = o2;
+  e = o3;
+}
+
+// value of quad position M (lane (L & ~3) + M) at every lane of the quad
+template <int M>
+__device__ __forceinline__ float quad_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), M * 0x55, 0xf, 0xf, true));
+}
+
+// Hadamard (x 1/16) of the lane's 64 elements: stages 1-3 in registers, stage 4 across the quad.
+__device__ __forceinline__ void hadamard64_quad(float (&v)[64], int k) {
+#pragma unroll
+  for (int s = 1; s <= 16; s *= 4)
+#pragma unroll
+    for (int b = 0; b < 64; b++)
+      if ((b / s) % 4 == 0) bfly4_ref(v[b], v[b + s], v[b + 2 * s], v[b + 3 * s]);
+  const float s0 = k == 3 ? -1.0f : 1.0f, s1 = k == 2 ? -1.0f : 1.0f, s2 = k == 1 ? -1.0f : 1.0f,
+              s3 = k == 0 ? -1.0f : 1.0f;
+#pragma unroll
+  for (int p = 0; p < 64; p++) {
+    const float x0 = quad_bcast<0>(v[p]), x1 = quad_bcast<1>(v[p]), x2 = quad_bcast<2>(v[p]),
+                x3 = quad_bcast<3>(v[p]);
+    float t = x0 * s0;
+    t = __builtin_fmaf(x1, s1, t);
+    t = __builtin_fmaf(x2, s2, t);
+    t = __builtin_fmaf(x3, s3, t);
+    v[p] = t * 0.0625f;
+  }
+}
+
+// Row maximum over the LR lanes of a row (LR <= 64: within the wave; 128: two waves via LDS).
+template <int LR>
+__device__ __forceinline__ float rows_max(float v, float* red) {
+#pragma unroll
+  for (int s = 1; s < (LR < 64 ? LR : 64); s *= 2) v = fmaxf(v, __shfl_xor(v, s));
+  if constexpr (LR > 64) {
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    v = fmaxf(red[w & ~1], red[w | 1]);
+  }
+  return v;
+}
+
+// Per-token int8 of the lane's 64 values (q = clamp(rint(v * (127/amax))), s = amax/127).
+__device__ __forceinline__ void quant64_store(const float (&v)[64], float amax, int8_t* q) {
+  // an all-zero row: inv = 0 gives q = 0, as the definition's special case
+  const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    uint32_t w[4];
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        float t = rintf(v[16 * g + 4 * d + j] * inv);
+        t = fminf(fmaxf(t, -127.0f), 127.0f);
+        packed |= ((uint32_t)(int32_t)t & 0xffu) << (8 * j);
+      }
+      w[d] = packed;
+    }
+    *(uint4*)(q + 16 * g) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// rows of K = 64 * LR columns (K % 1024 == 0, K <= 8192), optional Hadamard, per-token int8.
+// 256 threads: 256 / LR rows per workgroup (LR = 128: one row over two waves, two per workgroup).
+template <int LR>
+__global__ __launch_bounds__(256) void quant_rows_reg_kernel(const float* X, int64_t M, int rotate, int8_t* Q,
+                                                             float* S_out) {
+  constexpr int K = 64 * LR;
+  __shared__ float red[4];
+  const int L = threadIdx.x % LR;
+  const int64_t row = (int64_t)blockIdx.x * (256 / LR) + threadIdx.x / LR;
+  const bool live = row < M;  // (dead rows still take part in the cross-wave maximum)
+  const float* x = X + (live ? row : 0) * K + 64 * L;
+  float v[64];
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const float4 t = *(const float4*)(x + 4 * i);
+    v[4 * i] = t.x;
+    v[4 * i + 1] = t.y;
+    v[4 * i + 2] = t.z;
+    v[4 * i + 3] = t.w;
+  }
+  if (rotate) hadamard64_quad(v, L & 3);
+  float am = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 64; i++) am = fmaxf(am, fabsf(v[i]));
+  am = rows_max<LR>(am, red);
+  if (!live) return;
+  if (L == 0) S_out[row] = am / 127.0f;
+  quant64_store(v, am, Q + row * K + 64 * L);
+}
+
 // LayerNorm (no affine) + adaLN (+ Hadamard) (+ int8), one wave per row (app/gpu/kernels.js:108-145).
 // Lane l holds the float4 chunks l, l+64, ... i.e. elements 4l + j + 256i, exactly the elements
 // the reference's 256-thread loops give to threads 4l + j, so the strided partial sums and the
@@ -465,6 +577,17 @@ int quant_rows_launch(anima_ctx* c, const float* x, int64_t M, int K, int rotate
   if (((uintptr_t)x & 15) || ((uintptr_t)q & 3)) return fail(c, ANIMA_E_ARG, "anima_quant_rows: x must be 16-byte and q 4-byte aligned");
   if (M == 0) return ANIMA_OK;
   Launch lc(c, rotate ? "hadamard_quant" : "quant_rows", 0.0, (double)M * K * 5 + M * 4.0);
+  if (K % 1024 == 0 && !((uintptr_t)q & 15)) {  // register-resident rows
+    const unsigned rows_per = 256 / (K / 64);
+    const dim3 grid((unsigned)((M + rows_per - 1) / rows_per));
+    switch (K) {
+      case 1024: hipLaunchKernelGGL(quant_rows_reg_kernel<16>, grid, dim3(256), 0, c->stream, x, M, rotate, q, s); break;
+      case 2048: hipLaunchKernelGGL(quant_rows_reg_kernel<32>, grid, dim3(256), 0, c->stream, x, M, rotate, q, s); break;
+      case 4096: hipLaunchKernelGGL(quant_rows_reg_kernel<64>, grid, dim3(256), 0, c->stream, x, M, rotate, q, s); break;
+      default: hipLaunchKernelGGL(quant_rows_reg_kernel<128>, grid, dim3(256), 0, c->stream, x, M, rotate, q, s); break;
+    }
+    return lc.end();
+  }
   if (K > 2048)  // four waves per row, one row per workgroup (at most 35 KB of LDS)
     hipLaunchKernelGGL(quant_rows_pad_kernel<4>, dim3((unsigned)M), dim3(256), (size_t)padded_cols(K) * 4, c->stream, x, M,
                        K, rotate, q, s);
