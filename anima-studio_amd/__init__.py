@@ -20,7 +20,7 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "anima.h")
 ANIMA_OK = 0
 PREC_BF16 = 0
 PREC_FP32 = 1
-W_BF16, W_I8, W_W4 = 0, 1, 2
+W_BF16, W_I8, W_W4, W_F32 = 0, 1, 2, 3
 ACT = {"none": 0, "gelu": 1, "silu": 2}
 EPI_STORE, EPI_RESID, EPI_GATED = 0, 1, 2
 EW = {"silu_mul": 0, "add": 1, "silu": 2, "copy": 3}
@@ -62,7 +62,7 @@ class LinearDesc(ctypes.Structure):
     _fields_ = [("M", _i64), ("W", ctypes.POINTER(Weight)), ("x", _vp), ("ldx", _i64), ("x_rotated", ctypes.c_int),
                 ("xq", _vp), ("xs", _vp), ("out", _vp), ("ldc", _i64), ("alpha", ctypes.c_float),
                 ("act", ctypes.c_int), ("epilogue", ctypes.c_int), ("gate", _vp), ("gate_off", _i64),
-                ("acc_out", _vp)]
+                ("acc_out", _vp), ("add", _vp), ("ld_add", _i64)]
 
 
 def lib():
@@ -260,10 +260,11 @@ class Context:
         return self._check(lib().anima_unpatchify(self.h, _ptr(o), B, h, w, _ptr(latents)))
 
     def linear(self, W, M, out, *, x=None, ldx=0, x_rotated=True, xq=None, xs=None, ldc=0, alpha=0.0, act="none",
-               epilogue=EPI_STORE, gate=None, gate_off=0, acc_out=None):
+               epilogue=EPI_STORE, gate=None, gate_off=0, acc_out=None, add=None, ld_add=0):
         d = LinearDesc(M=M, W=ctypes.pointer(W), x=_ptr(x), ldx=ldx, x_rotated=int(x_rotated), xq=_ptr(xq),
                        xs=_ptr(xs), out=_ptr(out), ldc=ldc, alpha=alpha, act=ACT[act] if isinstance(act, str) else act,
-                       epilogue=epilogue, gate=_ptr(gate), gate_off=gate_off, acc_out=_ptr(acc_out))
+                       epilogue=epilogue, gate=_ptr(gate), gate_off=gate_off, acc_out=_ptr(acc_out), add=_ptr(add),
+                       ld_add=ld_add)
         return self._check(lib().anima_linear(self.h, ctypes.byref(d)))
 
     def qk_norm_rope(self, qkv, L, H, D, ld, qn, kn, cs, sin_off, eps=1e-6):

@@ -34,6 +34,8 @@ struct GemmArgs {
   int64_t gate_off;
   int32_t* acc_out;
   int M, N, K;
+  const float* add;  // optional [M][ld_add] term after the bias
+  int64_t ld_add;
 };
 
 // GELU with the Abramowitz-Stegun erf of app/gpu/kernels.js:11-18.  The reciprocal is v_rcp_f32
@@ -59,6 +61,7 @@ __device__ __forceinline__ float apply_act(float r, int act) {
 
 __device__ __forceinline__ void epilogue_store(const GemmArgs& a, int m, int n, float r) {
   if (a.bias) r = r + a.bias[n];
+  if (a.add) r = r + a.add[(int64_t)m * a.ld_add + n];
   r = apply_act(r, a.act);
   float* c = a.out + (int64_t)m * a.ldc + n;
   if (a.epi == ANIMA_EPI_STORE) *c = r;
@@ -228,41 +231,6 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
   }
 }
 
-// Epilogue of one 32x32 accumulator tile for lane (n + 32g): register r holds row
-// m0 + 8(r/4) + r%4 (m0 already includes 4g) of column n.  Every load the tile needs (row scales,
-// the residual C) is issued before the first store, so the tile waits for memory once instead
-// of once per element (a load after a store to the same buffer may not be moved above it).
-// Arithmetic order is that of epilogue_store.
-__device__ __forceinline__ void epilogue_tile(const GemmArgs& a, i32x16 v, int m0, int n) {
-  if (n >= a.N) return;
-  const float swn = a.sw[n];
-  const float bias = a.bias ? a.bias[n] : 0.0f;
-  const float gate = a.epi == ANIMA_EPI_GATED ? a.gate[a.gate_off + n] : 0.0f;
-  float sxv[16], cv[16];
-#pragma unroll
-  for (int r = 0; r < 16; r++) {
-    const int m = m0 + 8 * (r >> 2) + (r & 3);
-    const bool ok = m < a.M;
-    sxv[r] = ok ? a.sx[m] : 0.0f;
-    cv[r] = ok && a.epi != ANIMA_EPI_STORE ? a.out[(int64_t)m * a.ldc + n] : 0.0f;
-  }
-#pragma unroll
-  for (int r = 0; r < 16; r++) {
-    const int m = m0 + 8 * (r >> 2) + (r & 3);
-    if (m >= a.M) continue;
-    if (a.acc_out) a.acc_out[(int64_t)m * a.N + n] = v[r];
-    float y = (float)v[r] * sxv[r];
-    y = y * swn;
-    if (a.alpha != 1.0f) y = y * a.alpha;
-    if (a.bias) y = y + bias;
-    y = apply_act(y, a.act);
-    float* c = a.out + (int64_t)m * a.ldc + n;
-    if (a.epi == ANIMA_EPI_STORE) *c = y;
-    else if (a.epi == ANIMA_EPI_RESID) *c = cv[r] + y;
-    else *c = __builtin_fmaf(gate, y, cv[r]);
-  }
-}
-
 // ------------------------------------------------------------------ 256x256 epilogue
 //
 // The 256x256 kernel multiplies with the weight fragment as srcA, so each 32x32 accumulator
@@ -314,6 +282,7 @@ __device__ __forceinline__ void epi_store_t(const GemmArgs& a, const i32x16& v, 
     }
     if (a.alpha != 1.0f) y = y * a.alpha;
     if (a.bias) y = y + *(const f32x4*)(a.bias + nq);
+    if (a.add) y = y + *(const f32x4*)(a.add + (int64_t)m * a.ld_add + nq);
     if (a.act == ANIMA_ACT_GELU) {
 #pragma unroll
       for (int e = 0; e < 4; e++) y[e] = gelu_erf(y[e]);
@@ -564,7 +533,7 @@ __global__ __launch_bounds__(256) void w4_decode_kernel(const uint8_t* __restric
 struct F32WArgs {
   const float* x;
   int64_t ldx;
-  const uint16_t* w;  // bf16 [N][K]
+  const void* w;  // bf16 [N][K] (fp32 [N][K] when wf32)
   const float* bias;
   float* out;
   int64_t ldc;
@@ -576,6 +545,9 @@ struct F32WArgs {
   // grouped GEMV only: group g = blockIdx.y reads x + g*x_gs, w + g*w_gs, bias + g*bias_gs and
   // writes out + g*out_gs (all zero for a single product)
   int64_t x_gs, w_gs, bias_gs, out_gs;
+  const float* add;  // optional [M][ld_add] term after the bias
+  int64_t ld_add;
+  int wf32;  // fp32 weights (tile kernel only)
 };
 
 // 64x64 tile, 256 threads x (4x4) outputs, k-tile 16 (the small-tile layout of gemm.js:17).
@@ -591,7 +563,9 @@ __global__ __launch_bounds__(256) void gemm_f32w_kernel(F32WArgs a) {
       const int r = i >> 4, kk = i & 15;
       const int m = bm + r, n = bn + r, k = k0 + kk;
       Xs[kk][r] = (m < a.M && k < a.K) ? a.x[(int64_t)m * a.ldx + k] : 0.0f;
-      Ws[kk][r] = (n < a.N && k < a.K) ? __uint_as_float((uint32_t)a.w[(int64_t)n * a.K + k] << 16) : 0.0f;
+      Ws[kk][r] = !(n < a.N && k < a.K) ? 0.0f
+                  : a.wf32 ? ((const float*)a.w)[(int64_t)n * a.K + k]
+                           : __uint_as_float((uint32_t)((const uint16_t*)a.w)[(int64_t)n * a.K + k] << 16);
     }
     __syncthreads();
 #pragma unroll
@@ -619,6 +593,7 @@ __global__ __launch_bounds__(256) void gemm_f32w_kernel(F32WArgs a) {
       if (n >= a.N) continue;
       float r = acc[i][j] * a.alpha;
       if (a.bias) r = r + a.bias[n];
+      if (a.add) r = r + a.add[(int64_t)m * a.ld_add + n];
       r = apply_act(r, a.act);
       float* c = a.out + (int64_t)m * a.ldc + n;
       if (a.epi == ANIMA_EPI_STORE) *c = r;
@@ -637,13 +612,13 @@ __global__ __launch_bounds__(256) void gemv_f32w_kernel(F32WArgs a) {
   if (n >= a.N) return;
   const int64_t grp = blockIdx.y;
   a.x += grp * a.x_gs;
-  a.w += grp * a.w_gs;
+  a.w = (const uint16_t*)a.w + grp * a.w_gs;
   if (a.bias) a.bias += grp * a.bias_gs;
   a.out += grp * a.out_gs;
   float acc[GEMV_MAXM];
 #pragma unroll
   for (int m = 0; m < GEMV_MAXM; m++) acc[m] = 0.0f;
-  const uint16_t* wr = a.w + (int64_t)n * a.K;
+  const uint16_t* wr = (const uint16_t*)a.w + (int64_t)n * a.K;
   for (int k = lane * 8; k < a.K; k += 512) {
     const uint4 wv = *(const uint4*)(wr + k);
     float wf[8];
@@ -670,6 +645,7 @@ __global__ __launch_bounds__(256) void gemv_f32w_kernel(F32WArgs a) {
     if (lane == 0) {
       float r = tot * a.alpha;
       if (a.bias) r = r + a.bias[n];
+      if (a.add) r = r + a.add[(int64_t)m * a.ld_add + n];
       r = apply_act(r, a.act);
       float* c = a.out + (int64_t)m * a.ldc + n;
       if (a.epi == ANIMA_EPI_STORE) *c = r;
@@ -696,21 +672,24 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
   const int64_t ldc = d->ldc ? d->ldc : N;
   if (ldc < N) return fail(c, ANIMA_E_ARG, "anima_linear: ldc=%lld < N=%d", (long long)ldc, N);
   const float alpha = d->alpha != 0.0f ? d->alpha : 1.0f;
+  const int64_t ld_add = d->ld_add ? d->ld_add : N;
+  if (d->add && ld_add < N) return fail(c, ANIMA_E_ARG, "anima_linear: ld_add=%lld < N=%d", (long long)ld_add, N);
   if (M == 0) return ANIMA_OK;
 
-  if (W->kind == ANIMA_W_BF16) {
-    if (!d->x) return fail(c, ANIMA_E_ARG, "anima_linear: bf16 weights need fp32 x");
+  if (W->kind == ANIMA_W_BF16 || W->kind == ANIMA_W_F32) {
+    const bool f32 = W->kind == ANIMA_W_F32;
+    if (!d->x) return fail(c, ANIMA_E_ARG, "anima_linear: bf16/fp32 weights need fp32 x");
     if (d->acc_out || d->xq) return fail(c, ANIMA_E_ARG, "anima_linear: acc_out / xq apply to i8/w4 weights only");
     const int64_t ldx = d->ldx ? d->ldx : K;
     if (ldx < K) return fail(c, ANIMA_E_ARG, "anima_linear: ldx < K");
-    F32WArgs f{d->x, ldx, (const uint16_t*)W->w, W->bias, d->out, ldc, alpha, d->act, d->epilogue, d->gate, d->gate_off,
-               (int)M, N, K};
-    if (M <= GEMV_MAXM && K % 8 == 0 && ldx % 4 == 0 && al(d->x, 16) && al(W->w, 16)) {
+    F32WArgs f{d->x, ldx, W->w, W->bias, d->out, ldc, alpha, d->act, d->epilogue, d->gate, d->gate_off,
+               (int)M, N, K, 0, 0, 0, 0, d->add, ld_add, f32 ? 1 : 0};
+    if (!f32 && M <= GEMV_MAXM && K % 8 == 0 && ldx % 4 == 0 && al(d->x, 16) && al(W->w, 16)) {
       Launch L(c, "gemv.bf16", 2.0 * M * N * K, 2.0 * N * K);
       hipLaunchKernelGGL(gemv_f32w_kernel, dim3((N + 3) / 4), dim3(256), 0, c->stream, f);
       return L.end();
     }
-    Launch L(c, "gemm.bf16", 2.0 * M * N * K, 0.0);
+    Launch L(c, f32 ? "gemm.f32" : "gemm.bf16", 2.0 * M * N * K, 0.0);
     hipLaunchKernelGGL(gemm_f32w_kernel, dim3((N + 63) / 64, (unsigned)((M + 63) / 64)), dim3(256), 0, c->stream, f);
     return L.end();
   }
@@ -744,7 +723,7 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
     if (!al(qx, 16)) return fail(c, ANIMA_E_ARG, "anima_linear: xq must be 16-byte aligned");
   }
   GemmArgs g{qx, sx, W->w, W->scale, W->srel, W->codebook, W->bias, d->out, ldc, alpha, d->act, d->epilogue,
-             d->gate, d->gate_off, d->acc_out, (int)M, N, K};
+             d->gate, d->gate_off, d->acc_out, (int)M, N, K, d->add, ld_add};
   int rc = ANIMA_OK;
   // Grids that give every CU a 256x256 tile run the persistent 256 kernel; a W4 weight is then
   // decoded once into an int8 workspace first.  Smaller grids run the 128x128 kernel, which
@@ -753,7 +732,7 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
   // aligned output rows, scales, bias and gate.
   const int64_t tiles256 = (int64_t)((N + 255) / 256) * ((M + 255) / 256);
   const bool vec = N % 4 == 0 && g.ldc % 4 == 0 && al(g.out, 16) && al(g.sw, 16) && (!g.bias || al(g.bias, 16)) &&
-                   (g.epi != ANIMA_EPI_GATED || al(g.gate + g.gate_off, 16));
+                   (g.epi != ANIMA_EPI_GATED || al(g.gate + g.gate_off, 16)) && (!g.add || (al(g.add, 16) && g.ld_add % 4 == 0));
   const bool big = vec && tiles256 >= c->num_cus && tiles256 <= 0x7fffffff;
   void* wdec = nullptr;
   if (big && w4) {
@@ -802,7 +781,7 @@ int linear_grouped_bf16_launch(anima_ctx* c, int G, int64_t M, int N, int K, con
   if (!al(x, 16) || !al(w, 16) || ldx % 4 || x_gs % 4 || w_gs % 8)
     return fail(c, ANIMA_E_ARG, "anima_linear_grouped_bf16: x and w must be 16-byte aligned (ldx, x stride %% 4, w stride %% 8)");
   F32WArgs f{x, ldx, w, bias, out, ldc, 1.0f, ANIMA_ACT_NONE, ANIMA_EPI_STORE, nullptr, 0, (int)M, N, K,
-             x_gs, w_gs, bias_gs, out_gs};
+             x_gs, w_gs, bias_gs, out_gs, nullptr, 0, 0};
   Launch L(c, "gemv.bf16.grouped", 2.0 * G * M * N * K, 2.0 * G * N * K);
   hipLaunchKernelGGL(gemv_f32w_kernel, dim3((N + 3) / 4, (unsigned)G), dim3(256), 0, c->stream, f);
   return L.end();

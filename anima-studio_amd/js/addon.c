@@ -477,6 +477,8 @@ static napi_value js_linear(napi_env env, napi_callback_info info) {
   d.gate = (const float*)pptr(env, o, "gate");
   d.gate_off = (int64_t)pnum(env, o, "gOff");
   d.acc_out = (int32_t*)pptr(env, o, "accOut");
+  d.add = (const float*)pptr(env, o, "add");
+  d.ld_add = (int64_t)pnum(env, o, "ldAdd");
   CHECK_RC(env, c, anima_linear(c, &d));
   return NULL;
 }

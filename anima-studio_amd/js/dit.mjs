@@ -25,13 +25,16 @@ function releaseAll(xs) {
 // LayerNorm + adaLN for inputs that feed W: int8 { xq } when W is quantized (W8A8), else the
 // fp32 modulated rows (normFor of app/models/dit.js:34-38).
 function normFor(gpu, x, mod, W) {
-  if (ops.needsRotation(W)) return { xq: ops.layernormModQ(gpu, x, mod, 0, D, D) };
+  if (ops.needsRotation(W)) return { xq: ops.layernormModQ(gpu, x, mod, 0, D, D, !!(W.lora && W.lora.length)) };
   return { n: ops.layernormMod(gpu, x, mod, 0, D, D, false) };
 }
 
 function project(gpu, nf, W, M, opts) {
   const o = Object.assign({ M }, opts || {});
-  if (nf.xq) o.xq = nf.xq;
+  if (nf.xq) {
+    o.xq = nf.xq;
+    if (nf.xq.xr) o.xr = nf.xq.xr;
+  }
   return ops.linear(gpu, nf.n || null, W, o);
 }
 
@@ -89,7 +92,9 @@ export class AnimaDiT {
       m.blocks.push({
         modSelf: mod("adaln_modulation_self_attn"), modCross: mod("adaln_modulation_cross_attn"),
         modMlp: mod("adaln_modulation_mlp"),
-        self: { qkv: L("self_attn.qkv", 3 * D, D), o: L("self_attn.output_proj", D, D),
+        // the stacked q/k/v carry their parts' module names (as concatLinears' output), for LoRAs
+        self: { qkv: Object.assign(L("self_attn.qkv", 3 * D, D), { parts: ["q_proj", "k_proj", "v_proj"].map((nm, j) =>
+          ({ name: p + "self_attn." + nm, off: j * D, n: D })) }), o: L("self_attn.output_proj", D, D),
           qn: src.vector(gpu, p + "self_attn.q_norm.weight", HD), kn: src.vector(gpu, p + "self_attn.k_norm.weight", HD) },
         cross: { q: L("cross_attn.q_proj", D, D), k: L("cross_attn.k_proj", D, CTX_DIM), v: L("cross_attn.v_proj", D, CTX_DIM),
           o: L("cross_attn.output_proj", D, D),

@@ -4,12 +4,13 @@
 // Extensions beyond the reference interface (all optional arguments):
 //   attention: B / qBatch / kBatch / vBatch / oBatch (batched CFG), kvLen (per-batch valid keys),
 //              qNorm / kNorm / cs (q/k RMSNorm + RoPE fused into the attention loads), precision.
-//   linear:    opts.xq = { q, s } per-token int8 activations (layernormModQ / quantRows).
+//   linear:    opts.xq = { q, s } per-token int8 activations (layernormModQ / quantRows); with a
+//              LoRA on a quantized weight the fp32 rotated input opts.xr is needed as well.
 //   layernormModQ: LayerNorm + adaLN + ConvRot + per-token int8 in one pass.
 
 import { native } from "./gpu.mjs";
 
-const KIND = { bf16: 0, i8: 1, w4: 2 };
+const KIND = { bf16: 0, i8: 1, w4: 2, f32: 3 };
 const ACT = { none: 0, gelu: 1, silu: 2 };
 const EW = { silu_mul: 0, add: 1, silu: 2, copy: 3 };
 const ptr = (t) => (t ? (typeof t === "number" ? t : t.buf) : 0);
@@ -33,7 +34,6 @@ export function quantRows(gpu, x, K, rotateFirst) {
 }
 
 function weightArg(W) {
-  if (W.lora && W.lora.length) throw new Error(`${W.name || "linear"}: LoRA deltas are not implemented by this build`);
   if (!(W.kind in KIND)) throw new Error(`unsupported weight kind ${W.kind}`);
   return { kindId: KIND[W.kind], N: W.N, K: W.K, buf: ptr(W.buf), scale: ptr(W.scale), srel: ptr(W.srel),
     codebook: ptr(W.codebook), bias: ptr(W.bias) };
@@ -45,9 +45,22 @@ function weightArg(W) {
 export function linear(gpu, x, W, opts) {
   const o = opts || {};
   const M = o.M !== undefined ? o.M : (o.xq ? o.xq.s.size : x.size / W.K);
+  // LoRAs: delta = sum_i scale_i B_i (A_i x_in), added in the epilogue before act / gate
+  // (ops.js:55-62); x_in is the rotated input for quantized weights (A was rotated at load).
+  let delta = null, tmp = null;
+  if (W.lora && W.lora.length) {
+    let xin = x;
+    if (needsRotation(W)) {
+      if (o.xr) xin = o.xr;
+      else if (x) xin = tmp = rotate(gpu, x);
+      else throw new Error(`${W.name || "linear"}: a LoRA on a quantized weight needs the fp32 input (x or opts.xr)`);
+    }
+    delta = loraDelta(gpu, xin, W, M);
+  }
   const out = o.out || gpu.empty([M, W.N]);
   const d = { M, out: out.buf, ldc: o.ldc || 0, alpha: o.alpha || 0, act: ACT[o.act || "none"],
-    epilogue: o.resid ? (o.gate ? 2 : 1) : 0, gate: ptr(o.gate), gOff: o.gOff || 0, accOut: ptr(o.accOut) };
+    epilogue: o.resid ? (o.gate ? 2 : 1) : 0, gate: ptr(o.gate), gOff: o.gOff || 0, accOut: ptr(o.accOut),
+    add: delta ? delta.buf : 0, ldAdd: delta ? W.N : 0 };
   if (needsRotation(W) && o.xq) {
     d.xq = o.xq.q.buf;
     d.xs = o.xq.s.buf;
@@ -61,7 +74,29 @@ export function linear(gpu, x, W, opts) {
   const w = weightArg(W);
   if (o.bias) w.bias = ptr(o.bias);
   native.linear(gpu.ctx, w, d);
+  if (delta) delta.release();
+  if (tmp) tmp.release();
   return out;
+}
+
+// [M, W.N] low-rank update (ops.js:70-87).  Entries { A: [r, K] f32, B: [n, r] f32, r, scale,
+// off, n }, off / n selecting the output columns (a slice of a stacked q/k/v weight).  A
+// full-width entry, if any, initializes the delta; everything else accumulates into it.
+function loraDelta(gpu, xin, W, M) {
+  const D = gpu.empty([M, W.N]);
+  const isFull = (e) => e.off === 0 && e.n === W.N;
+  const entries = W.lora.slice().sort((a, b) => isFull(b) - isFull(a));
+  let first = entries.some(isFull);
+  if (!first) zero(gpu, D);
+  for (const e of entries) {
+    const t = linear(gpu, xin, { kind: "f32", N: e.r, K: W.K, buf: e.A }, { M });
+    const store = first && isFull(e);
+    linear(gpu, t, { kind: "f32", N: e.n, K: e.r, buf: e.B }, { M, out: D.view(e.off, [M, e.n]), ldc: W.N,
+      alpha: e.scale, resid: !store });
+    if (store) first = false;
+    t.release();
+  }
+  return D;
 }
 
 export function zero(gpu, t) {
@@ -83,13 +118,15 @@ export function layernormMod(gpu, x, mod, shiftOff, scaleOff, cols, rotateOut) {
   return y;
 }
 
-// LayerNorm + adaLN + ConvRot + per-token int8: { q, s } for linear(..., { xq }).
-export function layernormModQ(gpu, x, mod, shiftOff, scaleOff, cols) {
+// LayerNorm + adaLN + ConvRot + per-token int8: { q, s } for linear(..., { xq }); withRotated
+// also returns the fp32 rotated rows as xr (the input of a LoRA side path).
+export function layernormModQ(gpu, x, mod, shiftOff, scaleOff, cols, withRotated) {
   const rows = x.size / cols;
   const q = gpu.empty([rows, cols], "i8");
   const s = gpu.empty([rows]);
-  native.layernormMod(gpu.ctx, x.buf, ptr(mod), shiftOff, scaleOff, rows, cols, 1e-6, 1, 0, q.buf, s.buf);
-  return { q, s, release() { q.release(); s.release(); } };
+  const xr = withRotated ? gpu.empty([rows, cols]) : null;
+  native.layernormMod(gpu.ctx, x.buf, ptr(mod), shiftOff, scaleOff, rows, cols, 1e-6, 1, xr ? xr.buf : 0, q.buf, s.buf);
+  return { q, s, xr, release() { q.release(); s.release(); if (xr) xr.release(); } };
 }
 
 // In-place per-head RMSNorm + RoPE on the q and k parts of a fused QKV buffer [L, 3*H*D] (ops.js:140-145).

@@ -8,6 +8,9 @@
 //   linear     ops.linear (i8 / w4 / bf16 weight files), with xr / resid / gate options
 //   lnmod      ops.layernormMod (rotate) and ops.layernormModQ
 //   dit        AnimaDiT.load(safetensors) -> timeCond -> prepareContext -> forward
+//   lora       ops.linear with LoRA entries given as files (A already in the weight's input basis)
+//   lorafile   loadLora(safetensors) onto a 1-block synthetic DiT, then the block's stacked qkv
+//              and mlp.layer2 linears with and without the attached LoRA
 
 import fs from "fs";
 import { GPU } from "./gpu.mjs";
@@ -15,6 +18,8 @@ import * as ops from "./ops.mjs";
 import { ditRopeTable } from "./common.mjs";
 import { SafeTensors } from "./weights.mjs";
 import { AnimaDiT } from "./dit.mjs";
+import { SyntheticWeights } from "./weights.mjs";
+import { linearRegistry, loadLora, attachLoras, destroyLora } from "./lora.mjs";
 
 const ARR = { f32: Float32Array, i8: Int8Array, u8: Uint8Array, u16: Uint16Array, i32: Int32Array };
 
@@ -80,6 +85,31 @@ async function main() {
     }
     const y = ops.linear(gpu, x, W, opts);
     save(c.out, await gpu.read(y));
+  } else if (c.case === "lora") {
+    const W = weightFromFiles(gpu, c.W);
+    const x = gpu.fromArray(load(c.x), [c.M, W.K]);
+    const base = ops.linear(gpu, x, W, {});
+    save(c.out + ".base", await gpu.read(base));
+    W.lora = c.lora.map((e) => ({ A: gpu.upload(load(e.A)), B: gpu.upload(load(e.B)), r: e.r, scale: e.scale, off: e.off, n: e.n }));
+    const y = ops.linear(gpu, x, W, {});
+    save(c.out, await gpu.read(y));
+  } else if (c.case === "lorafile") {
+    const src = new SyntheticWeights(gpu, 7, { mode: c.mode, blocks: 1 });
+    const dit = AnimaDiT.synthetic(gpu, src);
+    const regs = { dit: linearRegistry(dit), te: null };
+    const L = loadLora(gpu, c.lora, regs);
+    const x = gpu.fromArray(load(c.x), [c.M, 2048]);
+    const h = gpu.fromArray(load(c.h), [c.M, 8192]);
+    const b = dit.blocks[0];
+    save(c.out + ".qkv.base", await gpu.read(ops.linear(gpu, x, b.self.qkv, {})));
+    save(c.out + ".l2.base", await gpu.read(ops.linear(gpu, h, b.l2, {})));
+    attachLoras(regs, [{ lora: L, strength: c.strength }]);
+    save(c.out + ".qkv", await gpu.read(ops.linear(gpu, x, b.self.qkv, {})));
+    save(c.out + ".l2", await gpu.read(ops.linear(gpu, h, b.l2, {})));
+    const entries = [b.self.qkv, b.l2].map((W) => W.lora.map((e) => ({ r: e.r, scale: e.scale, off: e.off, n: e.n })));
+    console.log(JSON.stringify({ matched: L.matched, total: L.total, unsupported: L.unsupported, skipped: L.skipped, entries }));
+    attachLoras(regs, []);
+    destroyLora(L);
   } else if (c.case === "lnmod") {
     const x = gpu.fromArray(load(c.x), [c.rows, c.cols]);
     const mod = gpu.upload(load(c.mod));

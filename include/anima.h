@@ -182,6 +182,8 @@ int anima_fill_random(anima_ctx* ctx, void* dst, int64_t n, int kind, uint64_t s
 #define ANIMA_W_I8 1   /* int8 [N][K] + weight_scale [N] (comfy_quant int8_tensorwise+convrot) */
 #define ANIMA_W_W4 2   /* 4-bit codes [N][K/2] (low nibble = even k) + s_rel e4m3 [N][K/16] +
                           s_channel [N] + codebook [16] (comfy_quant asym_w4a8_int8+convrot) */
+#define ANIMA_W_F32 3  /* fp32 [N][K]; fp32 activations, fp32 accumulation: the LoRA A / B matrices
+                          of app/lora.js:103-134, run by ops.js:70-87 as kind "f32" */
 #define ANIMA_ACT_NONE 0
 #define ANIMA_ACT_GELU 1 /* erf GELU (kernels.js:9-20) */
 #define ANIMA_ACT_SILU 2
@@ -219,6 +221,10 @@ typedef struct {
   const float* gate;
   int64_t gate_off;
   int32_t* acc_out; /* i8/w4 only, optional: the raw int32 accumulators [M][N] */
+  /* optional fp32 term add[m*ld_add + n] added after the bias and before the activation: the ADD
+   * input of gemm.js:189 that carries the LoRA delta of ops.js:55-62 (ld_add 0 -> N) */
+  const float* add;
+  int64_t ld_add;
 } anima_linear_desc;
 
 /* ops.linear (app/gpu/ops.js:48-66) -> matmulShader (gemm.js:166-280):

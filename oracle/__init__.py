@@ -60,7 +60,8 @@ def lib():
         L.orc_fp8e4m3.argtypes = [ctypes.c_uint8]
         L.orc_fp8e4m3.restype = ctypes.c_float
         L.orc_w4_decode.argtypes = [_u8p, _u8p, _f32p, ctypes.c_int, ctypes.c_int, _i8p]
-        L.orc_linear_epilogue.argtypes = [_i32p, _i64, ctypes.c_int, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int, _f32p, _i64, _f32p, _i64]
+        L.orc_linear_epilogue.argtypes = [_i32p, _i64, ctypes.c_int, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int, _f32p, _i64, _f32p, _i64,
+                                          _f32p]
         L.orc_gelu.argtypes = [ctypes.c_float]
         L.orc_gelu.restype = ctypes.c_float
         L.orc_silu.argtypes = [ctypes.c_float]
@@ -215,16 +216,18 @@ def w4_decode(codes, srel, codebook, N, K):
     return out
 
 
-def linear_epilogue(acc, sx, sw, *, bias=None, act=0, epi=0, gate=None, g_off=0, c=None):
+def linear_epilogue(acc, sx, sw, *, bias=None, act=0, epi=0, gate=None, g_off=0, c=None, add=None):
+    """add: optional [M, N] term after the bias (the LoRA delta, gemm.js:189)."""
     acc = _c(acc, np.int32)
     M, N = acc.shape
     sx = _c(sx, np.float32) if sx is not None else None
     sw = _c(sw, np.float32)
     bias = _c(bias, np.float32) if bias is not None else None
     gate = _c(gate, np.float32) if gate is not None else None
+    add = _c(add, np.float32) if add is not None else None
     out = np.zeros((M, N), np.float32) if c is None else np.array(c, dtype=np.float32, copy=True, order="C")
     lib().orc_linear_epilogue(_p(acc, _i32p), M, N, _p(sx, _f32p), _p(sw, _f32p), _p(bias, _f32p), act, epi,
-                              _p(gate, _f32p), g_off, _p(out, _f32p), N)
+                              _p(gate, _f32p), g_off, _p(out, _f32p), N, _p(add, _f32p))
     return out
 
 

@@ -450,13 +450,14 @@ float orc_silu(float x) { return x / (1.0f + expf(-x)); } /* app/gpu/kernels.js:
 
 void orc_linear_epilogue(const int32_t* ACC, int64_t M, int N, const float* sx, const float* sw,
                          const float* bias, int act, int epi, const float* gate, int64_t g_off,
-                         float* C, int64_t ldc) { /* app/gpu/gemm.js:186-192 */
+                         float* C, int64_t ldc, const float* add) { /* app/gpu/gemm.js:186-192 */
   for (int64_t m = 0; m < M; m++)
     for (int n = 0; n < N; n++) {
       float r = (float)ACC[m * N + n];
       if (sx) r = r * sx[m];
       r = r * sw[n];
       if (bias) r = r + bias[n];
+      if (add) r = r + add[m * N + n];
       if (act == 1) r = orc_gelu(r);
       if (act == 2) r = orc_silu(r);
       float* c = C + m * ldc + n;

@@ -93,7 +93,7 @@ void orc_w4_decode(const uint8_t* codes, const uint8_t* srel, const float* codeb
  * epi: 0 store, 1 resid, 2 gated resid.  sx == NULL means 1. */
 void orc_linear_epilogue(const int32_t* ACC, int64_t M, int N, const float* sx, const float* sw,
                          const float* bias, int act, int epi, const float* gate, int64_t g_off,
-                         float* C, int64_t ldc);
+                         float* C, int64_t ldc, const float* add);
 /* erf-GELU with Abramowitz-Stegun 7.1.26 (app/gpu/kernels.js:9-20). */
 float orc_gelu(float x);
 float orc_silu(float x);

@@ -123,3 +123,100 @@ def test_js_dit_step_synthetic_smoke():
     out = json.loads(r.stdout.strip().splitlines()[-1])
     print(out, flush=True)
     assert out["finite"] and out["dit_step_ms"] > 0
+
+
+# ------------------------------------------------------------------ LoRA side paths (ops.js:55-87)
+
+def lora_delta(xin, entries, N):
+    """sum_e scale_e * (xin A_e^T) B_e^T on columns [off, off + n), in float64."""
+    d = np.zeros((xin.shape[0], N))
+    for e in entries:
+        d[:, e["off"]:e["off"] + e["n"]] += e["scale"] * ((xin.astype(np.float64) @ e["A"].T.astype(np.float64))
+                                                           @ e["B"].T.astype(np.float64))
+    return d
+
+
+@pytest.mark.parametrize("kind", ["i8", "bf16"])
+def test_js_linear_lora(tmp_path, kind):
+    """ops.linear with two LoRA entries (a full-width one and a column slice): the delta enters
+    the epilogue after the bias and before the store (gemm.js:189).  i8: the int8 accumulators
+    and the W8A8 epilogue are the oracle's; the only difference is the fp32 delta, so the result
+    is within 1e-6 of the oracle epilogue fed the float64 delta; bf16: within 1e-6 of float64."""
+    M, K, N = 300, 1024, 512
+    x = orc.randn(111, M * K).reshape(M, K)
+    rng = np.random.default_rng(12)
+    ents = [dict(r=8, scale=0.5, off=0, n=N), dict(r=4, scale=2.0, off=128, n=256)]
+    for i, e in enumerate(ents):
+        e["A"] = (0.05 * orc.randn(112 + i, e["r"] * K)).reshape(e["r"], K).astype(np.float32)
+        e["B"] = (0.05 * orc.randn(114 + i, e["n"] * e["r"])).reshape(e["n"], e["r"]).astype(np.float32)
+    W = {"kind": kind, "N": N, "K": K}
+    if kind == "i8":
+        qw = np.clip(np.rint(40 * orc.randn(116, N * K)), -127, 127).astype(np.int8).reshape(N, K)
+        sw = (rng.uniform(0.5, 1.5, N) / (127 * np.sqrt(K))).astype(np.float32)
+        W.update(w=write(tmp_path, "w.bin", qw), scale=write(tmp_path, "sw.bin", sw))
+        # the A matrices live in the rotated basis of the quantized weight's input
+        for e in ents:
+            e["A"] = orc.hadamard256(e["A"])
+    else:
+        w32 = orc.bf16_round(0.05 * orc.randn(117, N * K)).reshape(N, K)
+        W["w"] = write(tmp_path, "w.bin", (w32.view(np.uint32) >> 16).astype(np.uint16))
+    spec_l = [dict(A=write(tmp_path, f"a{i}.bin", e["A"]), B=write(tmp_path, f"b{i}.bin", e["B"]), r=e["r"],
+                   scale=e["scale"], off=e["off"], n=e["n"]) for i, e in enumerate(ents)]
+    out = str(tmp_path / "y.bin")
+    run_case(tmp_path, {"case": "lora", "M": M, "W": W, "x": write(tmp_path, "x.bin", x), "lora": spec_l, "out": out})
+    got, base = read(out).reshape(M, N), read(out + ".base").reshape(M, N)
+    if kind == "i8":
+        xr = orc.hadamard256(x)
+        delta = lora_delta(xr, ents, N)
+        qx, sx = orc.token_quant(xr)
+        acc = orc.gemm_i8(qx, qw)
+        assert np.array_equal(base, orc.linear_epilogue(acc, sx, sw))
+        ref = orc.linear_epilogue(acc, sx, sw, add=delta.astype(np.float32))
+    else:
+        delta = lora_delta(x, ents, N)
+        ref = x.astype(np.float64) @ w32.astype(np.float64).T + delta
+    r, _ = report(f"{kind} linear + LoRA", got, ref)
+    assert r < 1e-6
+    assert report(f"{kind} LoRA delta alone", got.astype(np.float64) - base, delta)[0] < 1e-4
+
+
+def test_js_lora_file(tmp_path):
+    """loadLora on a 1-block synthetic DiT from a safetensors file in PEFT and kohya naming: the
+    k_proj slice of the stacked qkv and mlp.layer2 (alpha / r scaling) match, a LoKr tensor is
+    counted unsupported, a module of a missing block is skipped; A is rotated on the device for
+    the int8 layers.  Columns outside the LoRA's slice are bit-identical to the plain linear."""
+    from safetensors.numpy import save_file
+
+    M = 64
+    rk, rl = 8, 4
+    Ak = (0.05 * orc.randn(121, rk * 2048)).reshape(rk, 2048).astype(np.float32)
+    Bk = (0.05 * orc.randn(122, 2048 * rk)).reshape(2048, rk).astype(np.float32)
+    Al = (0.05 * orc.randn(123, rl * 8192)).reshape(rl, 8192).astype(np.float32)
+    Bl = (0.05 * orc.randn(124, 2048 * rl)).reshape(2048, rl).astype(np.float32)
+    tensors = {
+        "diffusion_model.blocks.0.self_attn.k_proj.lora_A.weight": Ak,
+        "diffusion_model.blocks.0.self_attn.k_proj.lora_B.weight": Bk,
+        "lora_unet_blocks_0_mlp_layer2.lora_down.weight": Al,
+        "lora_unet_blocks_0_mlp_layer2.lora_up.weight": Bl,
+        "lora_unet_blocks_0_mlp_layer2.alpha": np.array(2.0, np.float32),
+        "diffusion_model.blocks.0.cross_attn.q_proj.lokr_w1": np.zeros((4, 4), np.float32),
+        "diffusion_model.blocks.9.mlp.layer1.lora_A.weight": np.zeros((2, 2048), np.float32),
+        "diffusion_model.blocks.9.mlp.layer1.lora_B.weight": np.zeros((8192, 2), np.float32),
+    }
+    path = str(tmp_path / "lora.safetensors")
+    save_file(tensors, path)
+    x = orc.randn(125, M * 2048).reshape(M, 2048)
+    h = orc.randn(126, M * 8192).reshape(M, 8192)
+    out = str(tmp_path / "y")
+    r = run_case(tmp_path, {"case": "lorafile", "mode": "int8", "lora": path, "strength": 1.5, "M": M,
+                            "x": write(tmp_path, "x.bin", x), "h": write(tmp_path, "h.bin", h), "out": out})
+    info = json.loads(next(ln for ln in r.stdout.splitlines() if '"matched"' in ln))
+    assert (info["matched"], info["total"], info["unsupported"], info["skipped"]) == (2, 3, 1, 1), info
+    assert info["entries"] == [[{"r": rk, "scale": 1.5, "off": 2048, "n": 2048}], [{"r": rl, "scale": 0.75, "off": 0, "n": 2048}]]
+    q, qb = read(out + ".qkv").reshape(M, 6144), read(out + ".qkv.base").reshape(M, 6144)
+    assert np.array_equal(q[:, :2048], qb[:, :2048]) and np.array_equal(q[:, 4096:], qb[:, 4096:])
+    dk = lora_delta(orc.hadamard256(x), [dict(A=orc.hadamard256(Ak), B=Bk, scale=1.5, off=0, n=2048)], 2048)
+    assert report("k_proj LoRA delta", q[:, 2048:4096].astype(np.float64) - qb[:, 2048:4096], dk)[0] < 1e-4
+    l, lb = read(out + ".l2").reshape(M, 2048), read(out + ".l2.base").reshape(M, 2048)
+    dl = lora_delta(orc.hadamard256(h), [dict(A=orc.hadamard256(Al), B=Bl, scale=0.75, off=0, n=2048)], 2048)
+    assert report("mlp.layer2 LoRA delta", l.astype(np.float64) - lb, dl)[0] < 1e-4

@@ -325,6 +325,60 @@ def test_bf16_weight_linears(ctx):
         assert r < 1e-6
 
 
+@pytest.mark.parametrize("M", [4000, 200])
+def test_linear_add_term(ctx, M):
+    """The optional fp32 add term (the LoRA delta input of gemm.js:189) after the bias: M=4000
+    runs the 256-tile kernel (16-byte add rows, ld_add > N), M=200 the 128-tile kernel; gated
+    epilogue, bit-exact against the oracle epilogue."""
+    case(f"linear add term M={M} N=4100 K=1024 gated + bias")
+    m = amd()
+    K, N = 1024, 4100
+    ld_add = N + 4
+    x = orc.randn(131, M * K).reshape(M, K)
+    qx, sx = orc.token_quant(orc.hadamard256(x))
+    qw, sw = int8_weight(132, N, K)
+    bias = (0.1 * orc.randn(133, N)).astype(np.float32)
+    gate = orc.randn(134, 3 * N).astype(np.float32)
+    resid = orc.randn(135, M * N).reshape(M, N)
+    add = orc.randn(136, M * ld_add).reshape(M, ld_add)
+    W = m.weight(m.W_I8, N, K, ctx.upload(qw), scale=ctx.upload(sw), bias=ctx.upload(bias))
+    dout, dacc = ctx.upload(resid), ctx.empty((M, N), np.int32)
+    ctx.linear(W, M, dout, xq=ctx.upload(qx), xs=ctx.upload(sx), epilogue=m.EPI_GATED, gate=ctx.upload(gate), gate_off=N,
+               acc_out=dacc, add=ctx.upload(add), ld_add=ld_add)
+    acc, got = dacc.numpy(), dout.numpy()
+    assert checksums_ok(qx, qw, acc)
+    rows = np.unique(np.concatenate([np.arange(0, 4), np.random.default_rng(3).choice(M, 12, replace=False),
+                                     np.arange(M - 8, M)]))
+    ref_acc = orc.gemm_i8(qx[rows], qw)
+    assert np.array_equal(acc[rows], ref_acc)
+    ref = orc.linear_epilogue(ref_acc, sx[rows], sw, bias=bias, epi=2, gate=gate, g_off=N, c=resid[rows],
+                              add=np.ascontiguousarray(add[rows, :N]))
+    assert np.array_equal(got[rows], ref), report("add term", got[rows], ref)
+
+
+def test_f32_weight_linears(ctx):
+    """fp32 weights (the LoRA A / B matrices): tall-skinny and short-K shapes against float64,
+    with alpha, column offset into a wider output (ldc) and residual accumulation."""
+    case("fp32 weights: LoRA A (N=16, K=2048) and B (N=2048, K=16)")
+    m = amd()
+    M = 300
+    x = orc.randn(141, M * 2048).reshape(M, 2048)
+    A = (0.05 * orc.randn(142, 16 * 2048)).reshape(16, 2048).astype(np.float32)
+    B = (0.05 * orc.randn(143, 2048 * 16)).reshape(2048, 16).astype(np.float32)
+    WA = m.weight(m.W_F32, 16, 2048, ctx.upload(A))
+    t = ctx.empty((M, 16))
+    ctx.linear(WA, M, t, x=ctx.upload(x))
+    t_ref = x.astype(np.float64) @ A.T
+    assert report("x A^T", t.numpy(), t_ref)[0] < 1e-6
+    WB = m.weight(m.W_F32, 2048, 16, ctx.upload(B))
+    base = orc.randn(144, M * 2560).reshape(M, 2560)
+    dd = ctx.upload(base)
+    ctx.linear(WB, M, dd.ptr + 256 * 4, x=t, ldc=2560, alpha=0.5, epilogue=m.EPI_RESID)
+    ref = base.astype(np.float64)
+    ref[:, 256:2304] += 0.5 * (t.numpy().astype(np.float64) @ B.T)
+    assert report("+= 0.5 t B^T into columns 256..2303", dd.numpy(), ref)[0] < 1e-6
+
+
 def test_grouped_bf16_gemv(ctx):
     """G products in one launch (the adaLN modulation stage of timeCond): every group bit-exact
     against its own anima_linear GEMV call with the same bias, and within 1e-6 of float64."""
