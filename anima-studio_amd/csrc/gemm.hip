@@ -603,6 +603,246 @@ __global__ __launch_bounds__(256) void gemm_f32w_kernel(F32WArgs a) {
   }
 }
 
+// fp32-weight linear on the fp32 matrix cores (v_mfma_f32_32x32x2_f32): the LoRA B products
+// (short K = rank).  Each wave owns a 32 x 32 output tile and four waves make a 64 x 64 block; in a
+// k-tile of 32, lane (l, h) holds x[row l][16h..16h+15] and W[col l][16h..16h+15] (16-byte global
+// loads, no LDS) and MFMA s multiplies k = 16h + s, so the two lane halves cover the 32 k values.
+// Epilogue of gemm_f32w_kernel.
+__global__ __launch_bounds__(256) void gemm_f32m_kernel(F32WArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lq = lane & 31, hf = lane >> 5;
+  const int m0 = blockIdx.y * 64 + (wave & 1) * 32;
+  const int n0 = blockIdx.x * 64 + (wave >> 1) * 32;
+  const int m = m0 + lq, n = n0 + lq;
+  const bool mok = m < a.M, nok = n < a.N;
+  const float* xr = a.x + (int64_t)(mok ? m : 0) * a.ldx + 16 * hf;
+  const float* wr = (const float*)a.w + (int64_t)(nok ? n : 0) * a.K + 16 * hf;
+  f32x16 acc = {};
+  const int nkt = (a.K + 31) / 32;
+  for (int kt = 0; kt < nkt; kt++) {
+    const int k0 = 32 * kt;
+    float xv[16], wv[16];
+    if (k0 + 32 <= a.K) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float4 t = mok ? *(const float4*)(xr + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float4 u = nok ? *(const float4*)(wr + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        xv[4 * j] = t.x; xv[4 * j + 1] = t.y; xv[4 * j + 2] = t.z; xv[4 * j + 3] = t.w;
+        wv[4 * j] = u.x; wv[4 * j + 1] = u.y; wv[4 * j + 2] = u.z; wv[4 * j + 3] = u.w;
+      }
+    } else {  // the last, partial k-tile
+#pragma unroll
+      for (int s = 0; s < 16; s++) {
+        const bool kok = k0 + 16 * hf + s < a.K;
+        xv[s] = mok && kok ? xr[k0 + s] : 0.0f;
+        wv[s] = nok && kok ? wr[k0 + s] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 16; s++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xv[s], wv[s], acc, 0, 0, 0);
+  }
+  if (!nok) return;
+  // output layout: lane (l, h), register r -> row 8(r/4) + 4h + r%4 of the tile, column l
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int mm = m0 + 8 * (r >> 2) + 4 * hf + (r & 3);
+    if (mm >= a.M) continue;
+    float v = acc[r] * a.alpha;
+    if (a.bias) v = v + a.bias[n];
+    if (a.add) v = v + a.add[(int64_t)mm * a.ld_add + n];
+    v = apply_act(v, a.act);
+    float* c = a.out + (int64_t)mm * a.ldc + n;
+    if (a.epi == ANIMA_EPI_STORE) *c = v;
+    else if (a.epi == ANIMA_EPI_RESID) *c = *c + v;
+    else *c = __builtin_fmaf(a.gate[a.gate_off + n], v, *c);
+  }
+}
+
+// The same product with the operands swapped (W rows as MFMA A, x rows as MFMA B), so the result
+// is C^T in the MFMA layout: lane (l, h) holds output row m0 + l and, in register group g, the four
+// consecutive columns n0 + 8g + 4h .. + 3, which the epilogue moves as 16-byte loads / stores.
+// Needs N % 4 == 0 and 16-byte aligned out / add / bias / gate rows; the LoRA B products (output
+// width = model width, K = rank) are write-bound, so this is their kernel.
+__global__ __launch_bounds__(256) void gemm_f32m_t_kernel(F32WArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lq = lane & 31, hf = lane >> 5;
+  const int m0 = blockIdx.y * 64 + (wave & 1) * 32;
+  const int n0 = blockIdx.x * 64 + (wave >> 1) * 32;
+  const int m = m0 + lq, n = n0 + lq;
+  const bool mok = m < a.M, nok = n < a.N;
+  const float* xr = a.x + (int64_t)(mok ? m : 0) * a.ldx + 16 * hf;
+  const float* wr = (const float*)a.w + (int64_t)(nok ? n : 0) * a.K + 16 * hf;
+  f32x16 acc = {};
+  const int nkt = (a.K + 31) / 32;
+  for (int kt = 0; kt < nkt; kt++) {
+    const int k0 = 32 * kt;
+    float xv[16], wv[16];
+    if (k0 + 32 <= a.K) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float4 t = mok ? *(const float4*)(xr + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float4 u = nok ? *(const float4*)(wr + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        xv[4 * j] = t.x; xv[4 * j + 1] = t.y; xv[4 * j + 2] = t.z; xv[4 * j + 3] = t.w;
+        wv[4 * j] = u.x; wv[4 * j + 1] = u.y; wv[4 * j + 2] = u.z; wv[4 * j + 3] = u.w;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 16; s++) {
+        const bool kok = k0 + 16 * hf + s < a.K;
+        xv[s] = mok && kok ? xr[k0 + s] : 0.0f;
+        wv[s] = nok && kok ? wr[k0 + s] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 16; s++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(wv[s], xv[s], acc, 0, 0, 0);
+  }
+  if (!mok) return;
+  float* crow = a.out + (int64_t)m * a.ldc;
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    const int nb = n0 + 8 * g + 4 * hf;
+    if (nb >= a.N) continue;
+    f32x4 v = {acc[4 * g] * a.alpha, acc[4 * g + 1] * a.alpha, acc[4 * g + 2] * a.alpha, acc[4 * g + 3] * a.alpha};
+    if (a.bias) v = v + *(const f32x4*)(a.bias + nb);
+    if (a.add) v = v + *(const f32x4*)(a.add + (int64_t)m * a.ld_add + nb);
+    if (a.act != ANIMA_ACT_NONE) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[i] = apply_act(v[i], a.act);
+    }
+    f32x4* c = (f32x4*)(crow + nb);
+    if (a.epi == ANIMA_EPI_STORE) {
+      *c = v;
+    } else if (a.epi == ANIMA_EPI_RESID) {
+      *c = *c + v;
+    } else {
+      const f32x4 gt = *(const f32x4*)(a.gate + a.gate_off + nb);
+      const f32x4 o = *c;
+      f32x4 r;
+#pragma unroll
+      for (int i = 0; i < 4; i++) r[i] = __builtin_fmaf(gt[i], v[i], o[i]);
+      *c = r;
+    }
+  }
+}
+
+// Tall-skinny fp32 product (the LoRA A side: N = stacked rank <= 128, K = model width): HBM-bound
+// on x, so one x tile feeds RT column tiles of 32, and eight waves split the k-tiles (wave w takes
+// k-tiles w, w + 8, ...) to keep enough loads in flight; the partial sums are added in a fixed
+// tree order through LDS (deterministic).  Block: 32 rows x 32 RT columns.  Lane layout and
+// epilogue as gemm_f32m_kernel.
+constexpr int SK_WAVES = 8;
+template <int RT>
+__global__ __launch_bounds__(64 * SK_WAVES) void gemm_f32m_skinny_kernel(F32WArgs a) {
+  __shared__ float part[SK_WAVES / 2 * 64 * 16 * RT];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lq = lane & 31, hf = lane >> 5;
+  const int m0 = blockIdx.y * 32, nb = blockIdx.x * 32 * RT;
+  const int m = m0 + lq;
+  const bool mok = m < a.M;
+  const float* xr = a.x + (int64_t)(mok ? m : 0) * a.ldx + 16 * hf;
+  const float* wr[RT];
+  bool nok[RT];
+#pragma unroll
+  for (int t = 0; t < RT; t++) {
+    const int n = nb + 32 * t + lq;
+    nok[t] = n < a.N;
+    wr[t] = (const float*)a.w + (int64_t)(nok[t] ? n : 0) * a.K + 16 * hf;
+  }
+  f32x16 acc[RT];
+#pragma unroll
+  for (int t = 0; t < RT; t++) acc[t] = f32x16{};
+  // k-tile loads; the loop issues tile i + 1's loads before tile i's MFMAs (register double buffer)
+  auto load = [&](int kt, float4 (&xv)[4], float4 (&wv)[RT][4]) {
+    const int k0 = 32 * kt;
+    if (k0 + 32 <= a.K) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        xv[j] = mok ? *(const float4*)(xr + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int t = 0; t < RT; t++) wv[t][j] = nok[t] ? *(const float4*)(wr[t] + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+    } else {  // the last, partial k-tile
+      float xs[16], ws[RT][16];
+#pragma unroll
+      for (int s = 0; s < 16; s++) {
+        const bool kok = k0 + 16 * hf + s < a.K;
+        xs[s] = mok && kok ? xr[k0 + s] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < RT; t++) ws[t][s] = nok[t] && kok ? wr[t][k0 + s] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        xv[j] = make_float4(xs[4 * j], xs[4 * j + 1], xs[4 * j + 2], xs[4 * j + 3]);
+#pragma unroll
+        for (int t = 0; t < RT; t++) wv[t][j] = make_float4(ws[t][4 * j], ws[t][4 * j + 1], ws[t][4 * j + 2], ws[t][4 * j + 3]);
+      }
+    }
+  };
+  auto mma = [&](const float4 (&xv)[4], const float4 (&wv)[RT][4]) {
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int t = 0; t < RT; t++) {
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(xv[j].x, wv[t][j].x, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(xv[j].y, wv[t][j].y, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(xv[j].z, wv[t][j].z, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(xv[j].w, wv[t][j].w, acc[t], 0, 0, 0);
+      }
+  };
+  const int nkt = (a.K + 31) / 32;
+  if (wave < nkt) {
+    float4 xa[4], wa[RT][4], xb[4], wb[RT][4];
+    load(wave, xa, wa);
+    int kt = wave;
+    for (;;) {
+      const bool more = kt + SK_WAVES < nkt;
+      if (more) load(kt + SK_WAVES, xb, wb);
+      mma(xa, wa);
+      if (!more) break;
+      kt += SK_WAVES;
+      const bool more2 = kt + SK_WAVES < nkt;
+      if (more2) load(kt + SK_WAVES, xa, wa);
+      mma(xb, wb);
+      if (!more2) break;
+      kt += SK_WAVES;
+    }
+  }
+  // tree reduction: waves [h, 2h) hand their sums to waves [0, h), h = 4, 2, 1
+#pragma unroll
+  for (int h = SK_WAVES / 2; h >= 1; h >>= 1) {
+    if (wave >= h && wave < 2 * h) {
+#pragma unroll
+      for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) part[(((wave - h) * RT + t) * 64 + lane) * 16 + r] = acc[t][r];
+    }
+    __syncthreads();
+    if (wave < h) {
+#pragma unroll
+      for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = acc[t][r] + part[((wave * RT + t) * 64 + lane) * 16 + r];
+    }
+    __syncthreads();
+  }
+  if (wave > 0) return;
+#pragma unroll
+  for (int t = 0; t < RT; t++) {
+    if (!nok[t]) continue;
+    const int n = nb + 32 * t + lq;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int mm = m0 + 8 * (r >> 2) + 4 * hf + (r & 3);
+      if (mm >= a.M) continue;
+      float v = acc[t][r] * a.alpha;
+      if (a.bias) v = v + a.bias[n];
+      if (a.add) v = v + a.add[(int64_t)mm * a.ld_add + n];
+      v = apply_act(v, a.act);
+      float* c = a.out + (int64_t)mm * a.ldc + n;
+      if (a.epi == ANIMA_EPI_STORE) *c = v;
+      else if (a.epi == ANIMA_EPI_RESID) *c = *c + v;
+      else *c = __builtin_fmaf(a.gate[a.gate_off + n], v, *c);
+    }
+  }
+}
+
 // Small-M (M <= 8) bf16-weight GEMV: one wave per output column n, lanes stride K in 8-element
 // chunks, fp32 FMA, wave reduction (timestep / adaLN projections, M = 1).
 constexpr int GEMV_MAXM = 8;
@@ -690,6 +930,24 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
       return L.end();
     }
     Launch L(c, f32 ? "gemm.f32" : "gemm.bf16", 2.0 * M * N * K, 0.0);
+    if (f32 && K % 4 == 0 && ldx % 4 == 0 && al(d->x, 16) && al(W->w, 16)) {  // fp32 matrix cores
+      const dim3 sk((unsigned)((N + 127) / 128), (unsigned)((M + 31) / 32));
+      if (N <= 32 && K >= 512)
+        hipLaunchKernelGGL(gemm_f32m_skinny_kernel<1>, sk, dim3(64 * SK_WAVES), 0, c->stream, f);
+      else if (N <= 64 && K >= 512)
+        hipLaunchKernelGGL(gemm_f32m_skinny_kernel<2>, sk, dim3(64 * SK_WAVES), 0, c->stream, f);
+      else if (N <= 96 && K >= 512)
+        hipLaunchKernelGGL(gemm_f32m_skinny_kernel<3>, sk, dim3(64 * SK_WAVES), 0, c->stream, f);
+      else if (N <= 256 && K >= 512)
+        hipLaunchKernelGGL(gemm_f32m_skinny_kernel<4>, sk, dim3(64 * SK_WAVES), 0, c->stream, f);
+      else if (N % 4 == 0 && ldc % 4 == 0 && al(d->out, 16) && (!W->bias || al(W->bias, 16)) &&
+               (!d->add || (al(d->add, 16) && ld_add % 4 == 0)) &&
+               (d->epilogue != ANIMA_EPI_GATED || al(d->gate + d->gate_off, 16)))
+        hipLaunchKernelGGL(gemm_f32m_t_kernel, dim3((N + 63) / 64, (unsigned)((M + 63) / 64)), dim3(256), 0, c->stream, f);
+      else
+        hipLaunchKernelGGL(gemm_f32m_kernel, dim3((N + 63) / 64, (unsigned)((M + 63) / 64)), dim3(256), 0, c->stream, f);
+      return L.end();
+    }
     hipLaunchKernelGGL(gemm_f32w_kernel, dim3((N + 63) / 64, (unsigned)((M + 63) / 64)), dim3(256), 0, c->stream, f);
     return L.end();
   }

@@ -5,10 +5,12 @@
 // app/pipeline.js:195-211).  Prints one JSON line.
 //
 //   node bench_dit.mjs [--size 1024] [--blocks 28] [--mode w4a8|int8|bf16] [--steps 3] [--warmup 1] [--profile]
+//                     [--lora-rank R]   (seeded rank-R LoRAs on every block linear, strength 1)
 
 import { GPU, native } from "./gpu.mjs";
 import { SyntheticWeights } from "./weights.mjs";
 import { AnimaDiT } from "./dit.mjs";
+import { linearRegistry, attachLoras, rotatedA } from "./lora.mjs";
 
 function arg(name, def) {
   const i = process.argv.indexOf("--" + name);
@@ -53,6 +55,26 @@ async function main() {
     return t;
   });
   const cond = dit.prepareContext(ctxs);
+  const loraRank = Number(arg("lora-rank", 0));
+  const loraBufs = [];
+  const regs = { dit: linearRegistry(dit), te: null };
+  if (loraRank > 0) {
+    // one synthetic LoRA module per block linear (stacked q/k/v per part), in the layout loadLora
+    // produces: A [r, K], A H for ConvRot targets, B [n, r], scale alpha / r = 1
+    const modules = [];
+    let seed = 900;
+    for (const [name, t] of regs.dit) {
+      if (!name.startsWith("blocks_")) continue;
+      const A = gpu.empty([loraRank * t.W.K]), B = gpu.empty([t.n * loraRank]);
+      native.fillRandom(gpu.ctx, A.buf, A.size, 4, seed++, 0.02, 0.0);
+      native.fillRandom(gpu.ctx, B.buf, B.size, 4, seed++, 0.02, 0.0);
+      const Ar = t.W.kind === "i8" || t.W.kind === "w4" ? rotatedA(gpu, A, A.size) : null;
+      loraBufs.push(A, B);
+      if (Ar) loraBufs.push(Ar);
+      modules.push({ target: t, A, Ar, B, r: loraRank, alphaScale: 1 });
+    }
+    attachLoras(regs, [{ lora: { modules }, strength: 1 }]);
+  }
   const latents = [normals(16 * h * w, 1), normals(16 * h * w, 2)];
   await gpu.sync();
   process.stderr.write(`bench_dit: model ready (${nBlocks} blocks, ${mode}), ${(gpu.pool.allocated / 2 ** 30).toFixed(2)} GiB\n`);
@@ -79,12 +101,14 @@ async function main() {
   const perBlock = 2 * M * D_(3 * 2048, 2048) + 2 * M * D_(2048, 2048) * 3 + 2 * M * D_(8192, 2048) * 2 +
     4 * B * L * L * 128 * 16 + 4 * B * L * Lk * 128 * 16;
   const flops = nBlocks * perBlock + 2 * M * 2048 * 68 + 2 * M * 64 * 2048;
-  const out = { dit_step_ms: Number(ms.toFixed(3)), size, blocks: nBlocks, mode, B, tokens: L, steps, warmup,
+  const out = { dit_step_ms: Number(ms.toFixed(3)), size, blocks: nBlocks, mode, B, tokens: L, steps, warmup, lora_rank: loraRank,
     flops_per_step: flops, tflops: Number((flops / (ms / 1e3) / 1e12).toFixed(2)), finite,
     peak_gib: Number((gpu.pool.peak / 2 ** 30).toFixed(2)) };
   if (gpu.profiler) out.kernels = await gpu.profiler.report();
   console.log(JSON.stringify(out));
   cond.release();
+  attachLoras(regs, []);
+  for (const t of loraBufs) t.release();
   gpu.destroy();
 }
 

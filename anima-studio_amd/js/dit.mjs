@@ -43,6 +43,14 @@ function releaseNorm(nf) {
   if (nf.n) nf.n.release();
 }
 
+// out (an M = 1 row) += scale * B (A x) for one LoRA entry of a linear whose product runs outside
+// ops.linear (the grouped modulation GEMV); x is that linear's input row.
+function loraPart(gpu, x, e, out) {
+  const t = ops.linear(gpu, x, { kind: "f32", N: e.r, K: x.size, buf: e.A }, { M: 1 });
+  ops.linear(gpu, t, { kind: "f32", N: e.n, K: e.r, buf: e.B }, { M: 1, out, alpha: e.scale, resid: true });
+  t.release();
+}
+
 export class AnimaDiT {
   // From a safetensors checkpoint in the web-asset layout (app/models/dit.js:82-129).
   static load(gpu, st, nBlocks) {
@@ -76,8 +84,9 @@ export class AnimaDiT {
     return m;
   }
 
-  // Seeded random-init weights of the same architecture (SyntheticWeights).
-  static synthetic(gpu, src) {
+  // Seeded random-init weights of the same architecture (SyntheticWeights).  opts.fuse = false
+  // keeps the per-linear adaLN modulation path.
+  static synthetic(gpu, src, opts) {
     const m = new AnimaDiT(gpu);
     const bf = (name, N, K) => src.bf16Linear(gpu, name, N, K, 1.0);
     m.xEmbed = bf("x_embedder.proj.1", D, 68);
@@ -104,7 +113,7 @@ export class AnimaDiT {
     }
     m.finalMod = [bf("final_layer.adaln_modulation.1", ADALN_RANK, D), src.bf16Linear(gpu, "final_layer.adaln_modulation.2", 2 * D, ADALN_RANK, 0.1)];
     m.finalLinear = bf("final_layer.linear", 64, D);
-    m.fuseModulation();
+    if (!opts || opts.fuse !== false) m.fuseModulation();
     return m;
   }
 
@@ -170,6 +179,9 @@ export class AnimaDiT {
       const final = gpu.empty([1, 2 * D]);
       native.linearGroupedBf16(gpu.ctx, 1, 1, 2 * D, R, h1.at(G * R), R, 0, final2.buf.buf, 0, lora.buf, 0, final.buf,
         2 * D, 0);
+      // LoRAs on second stages: part j of w2 is group j, which reads h1's j-th 256-slice
+      if (w2.lora) for (const e of w2.lora) loraPart(gpu, h1.view((e.off / (3 * D)) * R, [1, R]), e, all.view(e.off, [1, e.n]));
+      if (final2.lora) for (const e of final2.lora) loraPart(gpu, h1.view(G * R, [1, R]), e, final.view(e.off, [1, e.n]));
       h1.release();
       semb.release();
       lora.release();

@@ -6,12 +6,13 @@
 // ("lora_unet_<module with underscores>.lora_down.weight" / ".lora_up.weight" + ".alpha"),
 // matched against the model's linears by module name with dots and underscores equivalent.
 // LoKr / LoHa / DoRA tensors are counted as unsupported and skipped.  A ConvRot (i8 / w4) layer
-// sees the rotated input x H, and x A^T = (x H)(A H)^T, so A is rotated once at load time, on the
-// device, with the same per-256-group Hadamard as the activations.  This build runs the DiT
-// only, so text-encoder modules never match.
+// may hold only the rotated input x H, and x A^T = (x H)(A H)^T, so for those layers A H is also
+// made once at load time (Ar), on the device, with the same per-256-group Hadamard as the
+// activations.  This build runs the DiT only, so text-encoder modules never match.
 
 import { SafeTensors } from "./weights.mjs";
 import { native } from "./gpu.mjs";
+import { stackLora, releaseLoraStack } from "./ops.mjs";
 
 const needsRotation = (W) => W.kind === "i8" || W.kind === "w4";
 const norm = (name) => name.replace(/\./g, "_");
@@ -117,16 +118,11 @@ export function loadLora(gpu, path, regs) {
         skipped++;
         continue;
       }
-      let A = gpu.upload(st.f32(keys.A));
-      if (needsRotation(target.W)) {
-        const Ar = gpu.empty([r * target.W.K]);
-        native.hadamard(gpu.ctx, A.buf, Ar.buf, r * target.W.K);
-        A.release();
-        A = Ar;
-      }
+      const A = gpu.upload(st.f32(keys.A));
+      const Ar = needsRotation(target.W) ? rotatedA(gpu, A, r * target.W.K) : null;
       const B = gpu.upload(st.f32(keys.B));
       const alpha = keys.alpha ? st.f32(keys.alpha)[0] : null;
-      modules.push({ target, A, B, r, alphaScale: alpha ? alpha / r : 1 });
+      modules.push({ target, A, Ar, B, r, alphaScale: alpha ? alpha / r : 1 });
     }
     return { modules, matched: modules.length, total: groups.size, unsupported, skipped };
   } finally {
@@ -134,21 +130,38 @@ export function loadLora(gpu, path, regs) {
   }
 }
 
+// A H: each row of A through the per-256-group Hadamard of the ConvRot activations.
+export function rotatedA(gpu, A, n) {
+  const Ar = gpu.empty([n]);
+  native.hadamard(gpu.ctx, A.buf || A, Ar.buf, n);
+  return Ar;
+}
+
 export function destroyLora(L) {
   for (const m of L.modules) {
     m.A.release();
+    if (m.Ar) m.Ar.release();
     m.B.release();
   }
 }
 
 // Replaces every side path in the registries with the given [{ lora, strength }]
-// (app/lora.js:140-149).
+// (app/lora.js:140-149).  A linear with several entries (q/k/v parts, stacked LoRAs) gets its A
+// matrices stacked on the device so that one product reads the shared input; attachLoras(regs, [])
+// releases the stacks.
 export function attachLoras(regs, active) {
-  for (const reg of [regs.dit, regs.te]) if (reg) for (const { W } of reg.values()) W.lora = [];
+  const ws = new Set();
+  for (const reg of [regs.dit, regs.te]) if (reg) for (const { W } of reg.values()) ws.add(W);
+  for (const W of ws) {
+    releaseLoraStack(W);
+    W.lora = [];
+  }
   for (const { lora, strength } of active) {
     if (!strength) continue;
     for (const m of lora.modules) {
-      m.target.W.lora.push({ A: m.A, B: m.B, r: m.r, scale: strength * m.alphaScale, off: m.target.off, n: m.target.n });
+      m.target.W.lora.push({ A: m.A, Ar: m.Ar, B: m.B, r: m.r, scale: strength * m.alphaScale, off: m.target.off,
+        n: m.target.n });
     }
   }
+  for (const W of ws) if (W.lora.length > 1) stackLora(W.lora[0].A.gpu, W);
 }

@@ -45,18 +45,18 @@ function weightArg(W) {
 export function linear(gpu, x, W, opts) {
   const o = opts || {};
   const M = o.M !== undefined ? o.M : (o.xq ? o.xq.s.size : x.size / W.K);
-  // LoRAs: delta = sum_i scale_i B_i (A_i x_in), added in the epilogue before act / gate
-  // (ops.js:55-62); x_in is the rotated input for quantized weights (A was rotated at load).
-  let delta = null, tmp = null;
-  if (W.lora && W.lora.length) {
-    let xin = x;
-    if (needsRotation(W)) {
-      if (o.xr) xin = o.xr;
-      else if (x) xin = tmp = rotate(gpu, x);
-      else throw new Error(`${W.name || "linear"}: a LoRA on a quantized weight needs the fp32 input (x or opts.xr)`);
-    }
-    delta = loraDelta(gpu, xin, W, M);
-  }
+  // LoRAs: y += sum_i scale_i B_i (A_i x), after the bias and before act / gate (ops.js:55-62).
+  // The reference feeds ConvRot layers' LoRAs the rotated input and a rotated A; since
+  // (x H)(A H)^T = x A^T, the unrotated x and A are used when x is at hand (no rotation pass), and
+  // the rotated pair (opts.xr, entry.Ar) only when the caller holds just the rotated input.
+  const lora = W.lora && W.lora.length ? W.lora : null;
+  const rot = !!(lora && needsRotation(W) && o.xr);
+  const xin = rot ? o.xr : x;
+  if (lora && !xin) throw new Error(`${W.name || "linear"}: a LoRA on a quantized weight needs the fp32 input (x or opts.xr)`);
+  // A plain store (no activation, no residual) takes the LoRA products afterwards, accumulated
+  // straight into the output; otherwise they form a delta that the epilogue adds.
+  const late = lora && !o.resid && ACT[o.act || "none"] === 0;
+  const delta = lora && !late ? loraDelta(gpu, xin, W, M, rot) : null;
   const out = o.out || gpu.empty([M, W.N]);
   const d = { M, out: out.buf, ldc: o.ldc || 0, alpha: o.alpha || 0, act: ACT[o.act || "none"],
     epilogue: o.resid ? (o.gate ? 2 : 1) : 0, gate: ptr(o.gate), gOff: o.gOff || 0, accOut: ptr(o.accOut),
@@ -74,29 +74,84 @@ export function linear(gpu, x, W, opts) {
   const w = weightArg(W);
   if (o.bias) w.bias = ptr(o.bias);
   native.linear(gpu.ctx, w, d);
+  if (late) loraInto(gpu, xin, W, M, out, o.ldc || W.N, false, rot);
   if (delta) delta.release();
-  if (tmp) tmp.release();
   return out;
 }
 
-// [M, W.N] low-rank update (ops.js:70-87).  Entries { A: [r, K] f32, B: [n, r] f32, r, scale,
-// off, n }, off / n selecting the output columns (a slice of a stacked q/k/v weight).  A
-// full-width entry, if any, initializes the delta; everything else accumulates into it.
-function loraDelta(gpu, xin, W, M) {
-  const D = gpu.empty([M, W.N]);
+// Adds (or, storeFirst, stores where it comes first over a column range) every LoRA entry's
+// scale * B (A x_in) into columns [off, off + n) of out (row stride ldc) (ops.js:70-87).
+// Entries { A: [r, K] f32, Ar: A H (ConvRot targets), B: [n, r] f32, r, scale, off, n }: the
+// whole weight, or one part of a stacked q/k/v weight (parts are disjoint); rot selects Ar (x_in
+// rotated).  With a stack (stackLora), all A x_in come from one product over the stacked A,
+// reading x_in once.
+function loraInto(gpu, xin, W, M, out, ldc, storeFirst, rot) {
+  const S = W.loraStack && W.loraStack.lora === W.lora ? W.loraStack : null;
+  const Aof = (e) => {
+    if (rot && !e.Ar) throw new Error(`${W.name || "linear"}: LoRA entry without the rotated A for a rotated input`);
+    return rot ? e.Ar : e.A;
+  };
+  const down = S ? linear(gpu, xin, { kind: "f32", N: S.R, K: W.K, buf: rot ? S.Ar : S.A }, { M }) : null;
+  const covered = new Uint8Array(W.N);
   const isFull = (e) => e.off === 0 && e.n === W.N;
   const entries = W.lora.slice().sort((a, b) => isFull(b) - isFull(a));
-  let first = entries.some(isFull);
-  if (!first) zero(gpu, D);
   for (const e of entries) {
-    const t = linear(gpu, xin, { kind: "f32", N: e.r, K: W.K, buf: e.A }, { M });
-    const store = first && isFull(e);
-    linear(gpu, t, { kind: "f32", N: e.n, K: e.r, buf: e.B }, { M, out: D.view(e.off, [M, e.n]), ldc: W.N,
-      alpha: e.scale, resid: !store });
-    if (store) first = false;
-    t.release();
+    const t = S ? down.view(S.roff.get(e), [M, e.r]) : linear(gpu, xin, { kind: "f32", N: e.r, K: W.K, buf: Aof(e) }, { M });
+    const store = storeFirst && covered[e.off] === 0;
+    linear(gpu, t, { kind: "f32", N: e.n, K: e.r, buf: e.B }, { M, ldx: S ? S.R : 0, out: out.view(e.off, [M, e.n]),
+      ldc, alpha: e.scale, resid: !store });
+    covered.fill(1, e.off, e.off + e.n);
+    if (!S) t.release();
   }
+  if (down) down.release();
+}
+
+// The [M, W.N] LoRA delta for the epilogue's add term.  The reference zeroes it (or stores the
+// first full-width entry) and accumulates the rest; when the entries cover every column, storing
+// the first entry over each column range gives the same sums (0 + v is v) without the clearing pass.
+function loraDelta(gpu, xin, W, M, rot) {
+  const D = gpu.empty([M, W.N]);
+  const covered = new Uint8Array(W.N);
+  for (const e of W.lora) covered.fill(1, e.off, e.off + e.n);
+  const clear = covered.includes(0);
+  if (clear) zero(gpu, D);
+  loraInto(gpu, xin, W, M, D, W.N, !clear, rot);
   return D;
+}
+
+// Stacks the A (and, when every entry has one, Ar) matrices of W's LoRA entries into [sum r, K]
+// tensors so that loraInto runs one A product per call (the entries share x_in).  Valid while
+// W.lora is the same array; the stack is owned by W and freed by releaseLoraStack.  No-op for
+// fewer than two entries.
+export function stackLora(gpu, W) {
+  releaseLoraStack(W);
+  if (!W.lora || W.lora.length < 2) return null;
+  const R = W.lora.reduce((s, e) => s + e.r, 0);
+  const stack = (key) => {
+    const A = gpu.empty([R, W.K]);
+    let r0 = 0;
+    for (const e of W.lora) {
+      gpu.copy(A.at(r0 * W.K), e[key], e.r * W.K * 4);
+      r0 += e.r;
+    }
+    return A;
+  };
+  const roff = new Map();
+  let r0 = 0;
+  for (const e of W.lora) {
+    roff.set(e, r0);
+    r0 += e.r;
+  }
+  W.loraStack = { A: stack("A"), Ar: W.lora.every((e) => e.Ar) ? stack("Ar") : null, R, roff, lora: W.lora };
+  return W.loraStack;
+}
+
+export function releaseLoraStack(W) {
+  if (W.loraStack) {
+    W.loraStack.A.release();
+    if (W.loraStack.Ar) W.loraStack.Ar.release();
+  }
+  W.loraStack = null;
 }
 
 export function zero(gpu, t) {

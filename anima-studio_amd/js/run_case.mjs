@@ -8,9 +8,12 @@
 //   linear     ops.linear (i8 / w4 / bf16 weight files), with xr / resid / gate options
 //   lnmod      ops.layernormMod (rotate) and ops.layernormModQ
 //   dit        AnimaDiT.load(safetensors) -> timeCond -> prepareContext -> forward
-//   lora       ops.linear with LoRA entries given as files (A already in the weight's input basis)
+//   lora       ops.linear with LoRA entries given as files (A in the input's basis), optional act,
+//              stacked A matrices and a rotated-only input
 //   lorafile   loadLora(safetensors) onto a 1-block synthetic DiT, then the block's stacked qkv
 //              and mlp.layer2 linears with and without the attached LoRA
+//   loramod    timeCond of a 1-block synthetic DiT with LoRAs on the adaLN modulation linears,
+//              on the fused (grouped GEMV) and the per-linear modulation paths
 
 import fs from "fs";
 import { GPU } from "./gpu.mjs";
@@ -19,7 +22,7 @@ import { ditRopeTable } from "./common.mjs";
 import { SafeTensors } from "./weights.mjs";
 import { AnimaDiT } from "./dit.mjs";
 import { SyntheticWeights } from "./weights.mjs";
-import { linearRegistry, loadLora, attachLoras, destroyLora } from "./lora.mjs";
+import { linearRegistry, loadLora, attachLoras, destroyLora, rotatedA } from "./lora.mjs";
 
 const ARR = { f32: Float32Array, i8: Int8Array, u8: Uint8Array, u16: Uint16Array, i32: Int32Array };
 
@@ -88,11 +91,18 @@ async function main() {
   } else if (c.case === "lora") {
     const W = weightFromFiles(gpu, c.W);
     const x = gpu.fromArray(load(c.x), [c.M, W.K]);
-    const base = ops.linear(gpu, x, W, {});
+    const base = ops.linear(gpu, x, W, { act: c.act });
     save(c.out + ".base", await gpu.read(base));
-    W.lora = c.lora.map((e) => ({ A: gpu.upload(load(e.A)), B: gpu.upload(load(e.B)), r: e.r, scale: e.scale, off: e.off, n: e.n }));
-    const y = ops.linear(gpu, x, W, {});
+    W.lora = c.lora.map((e) => {
+      const A = gpu.upload(load(e.A));
+      const Ar = ops.needsRotation(W) ? rotatedA(gpu, A, e.r * W.K) : null;
+      return { A, Ar, B: gpu.upload(load(e.B)), r: e.r, scale: e.scale, off: e.off, n: e.n };
+    });
+    if (c.stack) ops.stackLora(gpu, W);
+    // rotated: the caller holds only the rotated input (the fused LayerNorm path)
+    const y = ops.linear(gpu, c.rotated ? null : x, W, { act: c.act, M: c.M, xr: c.rotated ? ops.rotate(gpu, x) : undefined });
     save(c.out, await gpu.read(y));
+    ops.releaseLoraStack(W);
   } else if (c.case === "lorafile") {
     const src = new SyntheticWeights(gpu, 7, { mode: c.mode, blocks: 1 });
     const dit = AnimaDiT.synthetic(gpu, src);
@@ -110,6 +120,34 @@ async function main() {
     console.log(JSON.stringify({ matched: L.matched, total: L.total, unsupported: L.unsupported, skipped: L.skipped, entries }));
     attachLoras(regs, []);
     destroyLora(L);
+  } else if (c.case === "loramod") {
+    const mods = async (tc) => {
+      const parts = [tc.blocks[0].self, tc.blocks[0].cross, tc.blocks[0].mlp, tc.final];
+      const arrs = [];
+      for (const t of parts) arrs.push(await gpu.read(t));
+      const out = new Float32Array(arrs.reduce((a, x) => a + x.length, 0));
+      let o = 0;
+      for (const x of arrs) { out.set(x, o); o += x.length; }
+      return out;
+    };
+    const info = {};
+    for (const fuse of [true, false]) {
+      const tag = fuse ? "fused" : "plain";
+      const dit = AnimaDiT.synthetic(gpu, new SyntheticWeights(gpu, 7, { mode: c.mode, blocks: 1 }), { fuse });
+      const regs = { dit: linearRegistry(dit), te: null };
+      const tc0 = dit.timeCond(c.sigma);
+      save(`${c.out}.${tag}.base`, await mods(tc0));
+      tc0.release();
+      const L = loadLora(gpu, c.lora, regs);
+      attachLoras(regs, [{ lora: L, strength: c.strength }]);
+      const tc = dit.timeCond(c.sigma);
+      save(`${c.out}.${tag}`, await mods(tc));
+      tc.release();
+      info[tag] = { matched: L.matched, skipped: L.skipped };
+      attachLoras(regs, []);
+      destroyLora(L);
+    }
+    console.log(JSON.stringify(info));
   } else if (c.case === "lnmod") {
     const x = gpu.fromArray(load(c.x), [c.rows, c.cols]);
     const mod = gpu.upload(load(c.mod));

@@ -136,12 +136,18 @@ def lora_delta(xin, entries, N):
     return d
 
 
-@pytest.mark.parametrize("kind", ["i8", "bf16"])
-def test_js_linear_lora(tmp_path, kind):
+@pytest.mark.parametrize("kind,act,stack,rotated", [("i8", "none", False, False), ("bf16", "none", False, False),
+                                                    ("i8", "gelu", True, False), ("bf16", "gelu", False, False),
+                                                    ("i8", "none", True, True), ("i8", "gelu", False, True)])
+def test_js_linear_lora(tmp_path, kind, act, stack, rotated):
     """ops.linear with two LoRA entries (a full-width one and a column slice): the delta enters
-    the epilogue after the bias and before the store (gemm.js:189).  i8: the int8 accumulators
-    and the W8A8 epilogue are the oracle's; the only difference is the fp32 delta, so the result
-    is within 1e-6 of the oracle epilogue fed the float64 delta; bf16: within 1e-6 of float64."""
+    after the bias and before the activation (gemm.js:189): through the epilogue's add term with
+    an activation, accumulated into the stored output without one; stack: one product over the
+    stacked A matrices; rotated: the caller passes only the rotated input, so the rotated A (made
+    on the device) is used.  The reference formula for ConvRot layers is B (A H)(x H)^T; the
+    unrotated x A^T equals it up to fp32 rounding.  i8: the int8 accumulators and the W8A8
+    epilogue are the oracle's; the only difference is the fp32 delta, so the result is within 1e-6
+    of the oracle epilogue fed the float64 delta; bf16: within 1e-6 of float64."""
     M, K, N = 300, 1024, 512
     x = orc.randn(111, M * K).reshape(M, K)
     rng = np.random.default_rng(12)
@@ -154,30 +160,36 @@ def test_js_linear_lora(tmp_path, kind):
         qw = np.clip(np.rint(40 * orc.randn(116, N * K)), -127, 127).astype(np.int8).reshape(N, K)
         sw = (rng.uniform(0.5, 1.5, N) / (127 * np.sqrt(K))).astype(np.float32)
         W.update(w=write(tmp_path, "w.bin", qw), scale=write(tmp_path, "sw.bin", sw))
-        # the A matrices live in the rotated basis of the quantized weight's input
-        for e in ents:
-            e["A"] = orc.hadamard256(e["A"])
     else:
         w32 = orc.bf16_round(0.05 * orc.randn(117, N * K)).reshape(N, K)
         W["w"] = write(tmp_path, "w.bin", (w32.view(np.uint32) >> 16).astype(np.uint16))
     spec_l = [dict(A=write(tmp_path, f"a{i}.bin", e["A"]), B=write(tmp_path, f"b{i}.bin", e["B"]), r=e["r"],
                    scale=e["scale"], off=e["off"], n=e["n"]) for i, e in enumerate(ents)]
     out = str(tmp_path / "y.bin")
-    run_case(tmp_path, {"case": "lora", "M": M, "W": W, "x": write(tmp_path, "x.bin", x), "lora": spec_l, "out": out})
+    run_case(tmp_path, {"case": "lora", "M": M, "W": W, "x": write(tmp_path, "x.bin", x), "lora": spec_l, "out": out,
+                        "act": act, "stack": stack, "rotated": rotated})
     got, base = read(out).reshape(M, N), read(out + ".base").reshape(M, N)
+    actid = {"none": 0, "gelu": 1}[act]
     if kind == "i8":
         xr = orc.hadamard256(x)
-        delta = lora_delta(xr, ents, N)
+        delta = lora_delta(xr, [dict(e, A=orc.hadamard256(e["A"])) for e in ents], N)
         qx, sx = orc.token_quant(xr)
         acc = orc.gemm_i8(qx, qw)
-        assert np.array_equal(base, orc.linear_epilogue(acc, sx, sw))
-        ref = orc.linear_epilogue(acc, sx, sw, add=delta.astype(np.float32))
+        base_ref = orc.linear_epilogue(acc, sx, sw, act=actid)
+        if act == "none":
+            assert np.array_equal(base, base_ref)
+        else:  # GELU on the hardware reciprocal / exponential: ~2e-8 relative
+            assert report("i8 gelu base", base, base_ref)[0] < 1e-6
+        ref = orc.linear_epilogue(acc, sx, sw, act=actid, add=delta.astype(np.float32))
     else:
         delta = lora_delta(x, ents, N)
         ref = x.astype(np.float64) @ w32.astype(np.float64).T + delta
-    r, _ = report(f"{kind} linear + LoRA", got, ref)
+        if act == "gelu":
+            ref = np.vectorize(orc.gelu)(ref)
+    r, _ = report(f"{kind} {act} linear + LoRA", got, ref)
     assert r < 1e-6
-    assert report(f"{kind} LoRA delta alone", got.astype(np.float64) - base, delta)[0] < 1e-4
+    if act == "none":
+        assert report(f"{kind} LoRA delta alone", got.astype(np.float64) - base, delta)[0] < 1e-4
 
 
 def test_js_lora_file(tmp_path):
@@ -220,3 +232,38 @@ def test_js_lora_file(tmp_path):
     l, lb = read(out + ".l2").reshape(M, 2048), read(out + ".l2.base").reshape(M, 2048)
     dl = lora_delta(orc.hadamard256(h), [dict(A=orc.hadamard256(Al), B=Bl, scale=0.75, off=0, n=2048)], 2048)
     assert report("mlp.layer2 LoRA delta", l.astype(np.float64) - lb, dl)[0] < 1e-4
+
+
+def test_js_lora_modulation(tmp_path):
+    """LoRAs on adaLN modulation linears (a first stage, a second stage and the final layer's
+    second stage): timeCond on the fused path (one stacked first-stage GEMV + one grouped
+    second-stage GEMV, the LoRA products applied per part) equals the per-linear path within fp32
+    summation-order noise, and the LoRAs change the outputs they target."""
+    from safetensors.numpy import save_file
+
+    r1, r2, rf = 4, 8, 4
+    T = {}
+    def mod(name, r, n, k, seed):
+        T[f"diffusion_model.{name}.lora_A.weight"] = (0.1 * orc.randn(seed, r * k)).reshape(r, k).astype(np.float32)
+        T[f"diffusion_model.{name}.lora_B.weight"] = (0.1 * orc.randn(seed + 1, n * r)).reshape(n, r).astype(np.float32)
+    mod("blocks.0.adaln_modulation_cross_attn.1", r1, 256, 2048, 131)
+    mod("blocks.0.adaln_modulation_mlp.2", r2, 6144, 256, 133)
+    mod("final_layer.adaln_modulation.2", rf, 4096, 256, 135)
+    path = str(tmp_path / "lora.safetensors")
+    save_file(T, path)
+    out = str(tmp_path / "m")
+    r = run_case(tmp_path, {"case": "loramod", "mode": "int8", "lora": path, "strength": 1.0, "sigma": 0.7, "out": out})
+    info = json.loads(next(ln for ln in r.stdout.splitlines() if '"fused"' in ln))
+    assert info["fused"] == info["plain"] == {"matched": 3, "skipped": 0}, info
+    fused, plain = read(out + ".fused"), read(out + ".plain")
+    fb, pb = read(out + ".fused.base"), read(out + ".plain.base")
+    assert report("modulation without LoRA: fused vs per-linear", fb, pb.astype(np.float64))[0] < 1e-6
+    assert report("modulation with LoRA: fused vs per-linear", fused, plain.astype(np.float64))[0] < 1e-6
+    D = 2048
+    segs = {"self": (0, 3 * D), "cross": (3 * D, 6 * D), "mlp": (6 * D, 9 * D), "final": (9 * D, 11 * D)}
+    for name, (a, b) in segs.items():
+        changed = np.abs(fused[a:b] - fb[a:b]).max()
+        if name == "self":
+            assert changed == 0, name
+        else:
+            assert changed > 1e-3 * np.abs(fb[a:b]).max(), (name, changed)

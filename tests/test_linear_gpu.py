@@ -379,6 +379,24 @@ def test_f32_weight_linears(ctx):
     assert report("+= 0.5 t B^T into columns 256..2303", dd.numpy(), ref)[0] < 1e-6
 
 
+@pytest.mark.parametrize("N,K,M", [(32, 2048, 257), (64, 1040, 64), (96, 2048, 300), (200, 8192, 45)])
+def test_f32_tall_skinny(ctx, N, K, M):
+    """The tall-skinny fp32 product (stacked LoRA A matrices, N <= 256, K >= 512): every column
+    tile count, a partial last k-tile (K = 1040), partial row / column blocks, bias + store and
+    a ldx wider than K, against float64."""
+    case(f"fp32 tall-skinny N={N} K={K} M={M}")
+    m = amd()
+    ldx = K + 12
+    x = orc.randn(151, M * ldx).reshape(M, ldx)
+    A = (0.05 * orc.randn(152, N * K)).reshape(N, K).astype(np.float32)
+    bias = orc.randn(153, N).astype(np.float32)
+    W = m.weight(m.W_F32, N, K, ctx.upload(A), bias=ctx.upload(bias))
+    t = ctx.empty((M, N))
+    ctx.linear(W, M, t, x=ctx.upload(x), ldx=ldx, alpha=0.75)
+    ref = 0.75 * (x[:, :K].astype(np.float64) @ A.T.astype(np.float64)) + bias
+    assert report("0.75 x A^T + b", t.numpy(), ref)[0] < 1e-6
+
+
 def test_grouped_bf16_gemv(ctx):
     """G products in one launch (the adaLN modulation stage of timeCond): every group bit-exact
     against its own anima_linear GEMV call with the same bias, and within 1e-6 of float64."""
