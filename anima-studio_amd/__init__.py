@@ -65,6 +65,16 @@ class LinearDesc(ctypes.Structure):
                 ("acc_out", _vp), ("add", _vp), ("ld_add", _i64)]
 
 
+SAMPLER = {"euler": 0, "euler_a": 1, "dpmpp_2m": 2, "er_sde": 3}
+
+
+class SamplerDesc(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int), ("n", _i64), ("x", _vp), ("v", _vp), ("v_uncond", _vp),
+                ("cfg", ctypes.c_double), ("sigma", ctypes.c_double), ("final_step", ctypes.c_int),
+                ("stage", ctypes.c_int), ("den_out", _vp), ("old", _vp), ("old_d", _vp), ("eps", _vp),
+                ("c", ctypes.c_double * 10)]
+
+
 def lib():
     """Loads libanima.so (raises if it is not built)."""
     global _LIB
@@ -102,6 +112,7 @@ def lib():
         L.anima_patchify.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]
         L.anima_unpatchify.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]
         L.anima_linear.argtypes = [_vp, ctypes.POINTER(LinearDesc)]
+        L.anima_sampler_step.argtypes = [_vp, ctypes.POINTER(SamplerDesc)]
         _LIB = L
     return _LIB
 
@@ -266,6 +277,14 @@ class Context:
                        epilogue=epilogue, gate=_ptr(gate), gate_off=gate_off, acc_out=_ptr(acc_out), add=_ptr(add),
                        ld_add=ld_add)
         return self._check(lib().anima_linear(self.h, ctypes.byref(d)))
+
+    def sampler_step(self, kind, n, x, v, *, v_uncond=None, cfg=1.0, sigma, final_step=False, stage=0, den_out=None,
+                     old=None, old_d=None, eps=None, c=()):
+        cc = (ctypes.c_double * 10)(*[float(t) for t in c])
+        d = SamplerDesc(kind=SAMPLER[kind] if isinstance(kind, str) else kind, n=n, x=_ptr(x), v=_ptr(v),
+                        v_uncond=_ptr(v_uncond), cfg=cfg, sigma=sigma, final_step=int(final_step), stage=stage,
+                        den_out=_ptr(den_out), old=_ptr(old), old_d=_ptr(old_d), eps=_ptr(eps), c=cc)
+        return self._check(lib().anima_sampler_step(self.h, ctypes.byref(d)))
 
     def qk_norm_rope(self, qkv, L, H, D, ld, qn, kn, cs, sin_off, eps=1e-6):
         return self._check(lib().anima_qk_norm_rope(self.h, _ptr(qkv), L, H, D, ld, _ptr(qn), _ptr(kn), _ptr(cs), sin_off, eps))

@@ -400,6 +400,11 @@ int anima_unpatchify(anima_ctx* c, const float* o, int B, int h, int w, float* l
   return patchify_launch(c, o, latents, B, h, w, true);
 }
 
+int anima_sampler_step(anima_ctx* c, const anima_sampler_desc* d) {
+  CHECK_CTX(c);
+  return sampler_step_launch(c, d);
+}
+
 int anima_fill_random(anima_ctx* c, void* dst, int64_t n, int kind, uint64_t seed, float lo, float hi) {
   CHECK_CTX(c);
   return fill_random_launch(c, dst, n, kind, seed, lo, hi);

@@ -483,6 +483,44 @@ static napi_value js_linear(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* samplerStep(ctx, {kind, n, x, v, vUncond, cfg, sigma, final, stage, den, old, oldD, eps, c: [10]}) */
+static napi_value js_sampler_step(napi_env env, napi_callback_info info) {
+  napi_value a[2];
+  get_args(env, info, 2, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  napi_value o = a[1];
+  anima_sampler_desc d;
+  memset(&d, 0, sizeof d);
+  d.kind = (int)pnum(env, o, "kind");
+  d.n = (int64_t)pnum(env, o, "n");
+  d.x = (float*)pptr(env, o, "x");
+  d.v = (const float*)pptr(env, o, "v");
+  d.v_uncond = (const float*)pptr(env, o, "vUncond");
+  d.cfg = pnum(env, o, "cfg");
+  d.sigma = pnum(env, o, "sigma");
+  bool fin = false;
+  napi_value fv = prop(env, o, "final");
+  if (!is_nullish(env, fv)) napi_get_value_bool(env, fv, &fin);
+  d.final_step = fin ? 1 : 0;
+  d.stage = (int)pnum(env, o, "stage");
+  d.den_out = (float*)pptr(env, o, "den");
+  d.old = (float*)pptr(env, o, "old");
+  d.old_d = (float*)pptr(env, o, "oldD");
+  d.eps = (const float*)pptr(env, o, "eps");
+  napi_value cv = prop(env, o, "c");
+  if (!is_nullish(env, cv)) {
+    uint32_t len = 0;
+    napi_get_array_length(env, cv, &len);
+    for (uint32_t i = 0; i < len && i < 10; i++) {
+      napi_value e;
+      napi_get_element(env, cv, i, &e);
+      d.c[i] = num(env, e);
+    }
+  }
+  CHECK_RC(env, c, anima_sampler_step(c, &d));
+  return NULL;
+}
+
 /* lastError(ctx | null) */
 static napi_value js_last_error(napi_env env, napi_callback_info info) {
   napi_value a[1];
@@ -504,7 +542,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       FN("qkNormRope", js_qk_norm_rope), FN("rmsnorm", js_rmsnorm), FN("rope", js_rope),
       FN("hadamard", js_hadamard), FN("quantRows", js_quant_rows), FN("layernormMod", js_layernorm_mod),
       FN("elementwise", js_elementwise), FN("zero", js_zero), FN("patchify", js_patchify), FN("linearGroupedBf16", js_linear_grouped_bf16), FN("unpatchify", js_unpatchify), FN("fillRandom", js_fill_random),
-      FN("linear", js_linear), FN("lastError", js_last_error),
+      FN("linear", js_linear), FN("samplerStep", js_sampler_step), FN("lastError", js_last_error),
   };
 #undef FN
   if (napi_define_properties(env, exports, sizeof desc / sizeof desc[0], desc) != napi_ok) return NULL;

@@ -6,11 +6,14 @@
 //
 //   node bench_dit.mjs [--size 1024] [--blocks 28] [--mode w4a8|int8|bf16] [--steps 3] [--warmup 1] [--profile]
 //                     [--lora-rank R]   (seeded rank-R LoRAs on every block linear, strength 1)
+//                     [--generate N [--sampler euler_a] [--cfg 4]]  (also time an N-step sampling run:
+//                      the device loop of pipeline.mjs and the reference's host loop)
 
 import { GPU, native } from "./gpu.mjs";
 import { SyntheticWeights } from "./weights.mjs";
 import { AnimaDiT } from "./dit.mjs";
 import { linearRegistry, attachLoras, rotatedA } from "./lora.mjs";
+import { LatentPipeline } from "./pipeline.mjs";
 
 function arg(name, def) {
   const i = process.argv.indexOf("--" + name);
@@ -105,6 +108,19 @@ async function main() {
     flops_per_step: flops, tflops: Number((flops / (ms / 1e3) / 1e12).toFixed(2)), finite,
     peak_gib: Number((gpu.pool.peak / 2 ** 30).toFixed(2)) };
   if (gpu.profiler) out.kernels = await gpu.profiler.report();
+  const genSteps = Number(arg("generate", 0));
+  if (genSteps > 0) {
+    // a whole sampling run (text encoding and VAE excluded): N DiT steps + the sampler between them
+    const pipe = new LatentPipeline(gpu, dit);
+    const opts = { cond, width: size, height: size, steps: genSteps, sampler: arg("sampler", "euler_a"),
+      cfg: Number(arg("cfg", 4)), seed: 1, scheduler: "simple" };
+    await pipe.generate(Object.assign({}, opts, { steps: 1 })); // first-use allocations
+    const dev = await pipe.generate(opts);
+    const host = await pipe.generateHost(opts);
+    pipe.clearTimeCache();
+    out.generate = { sampler: opts.sampler, steps: genSteps, cfg: opts.cfg,
+      device_ms_per_step: Number(dev.timings.perStep.toFixed(2)), host_loop_ms_per_step: Number(host.timings.perStep.toFixed(2)) };
+  }
   console.log(JSON.stringify(out));
   cond.release();
   attachLoras(regs, []);

@@ -254,8 +254,6 @@ export class AnimaDiT {
   async forward(latents, h, w, cond, tc, onBlock) {
     const gpu = this.gpu;
     const B = latents.length;
-    if (cond.B !== B) throw new Error(`forward: ${B} latents but ${cond.B} contexts`);
-    const Hp = h / 2, Wp = w / 2, L = Hp * Wp, M = B * L;
     // latents go up as they are; the patch layout (dit.js:55-65) is built on the device
     const per = 16 * h * w;
     const host = new Float32Array(B * per);
@@ -264,9 +262,25 @@ export class AnimaDiT {
       host.set(lat, b * per);
     });
     const lat = gpu.fromArray(host, [B, 16, h, w]);
+    const v = await this.forwardDevice(lat, h, w, cond, tc, onBlock);
+    lat.release();
+    const o = await gpu.read(v);
+    v.release();
+    const vs = [];
+    for (let bb = 0; bb < B; bb++) vs.push(o.slice(bb * per, (bb + 1) * per));
+    return vs;
+  }
+
+  // forward on device tensors: lat [B, 16, h, w] -> velocities [B, 16, h, w] (a new tensor);
+  // nothing is read back.
+  async forwardDevice(lat, h, w, cond, tc, onBlock) {
+    const gpu = this.gpu;
+    const B = lat.shape[0];
+    if (cond.B !== B) throw new Error(`forward: ${B} latents but ${cond.B} contexts`);
+    if (lat.size !== B * 16 * h * w) throw new Error(`forward: latents of ${lat.size} values for B=${B} ${h}x${w}`);
+    const Hp = h / 2, Wp = w / 2, L = Hp * Wp, M = B * L;
     const xin = gpu.empty([M, 68]);
     native.patchify(gpu.ctx, lat.buf, B, h, w, xin.buf);
-    lat.release();
     const x = ops.linear(gpu, xin, this.xEmbed);
     xin.release();
     const cs = this.ropeTable(Hp, Wp);
@@ -314,10 +328,6 @@ export class AnimaDiT {
     const v = gpu.empty([B, 16, h, w]);
     native.unpatchify(gpu.ctx, out.buf, B, h, w, v.buf); // dit.js:68-78 on the device
     out.release();
-    const o = await gpu.read(v);
-    v.release();
-    const vs = [];
-    for (let bb = 0; bb < B; bb++) vs.push(o.slice(bb * per, (bb + 1) * per));
-    return vs;
+    return v;
   }
 }

@@ -149,7 +149,14 @@ export function destroyLora(L) {
 // (app/lora.js:140-149).  A linear with several entries (q/k/v parts, stacked LoRAs) gets its A
 // matrices stacked on the device so that one product reads the shared input; attachLoras(regs, [])
 // releases the stacks.
+let generation = 0;
+// Counts attachLoras calls: results cached across calls (timeCond) key on it.
+export function loraGeneration() {
+  return generation;
+}
+
 export function attachLoras(regs, active) {
+  generation++;
   const ws = new Set();
   for (const reg of [regs.dit, regs.te]) if (reg) for (const { W } of reg.values()) ws.add(W);
   for (const W of ws) {

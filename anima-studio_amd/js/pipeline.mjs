@@ -1,0 +1,129 @@
+// The sampling half of AnimaPipeline.generate (app/pipeline.js:225-293) on the device: initial
+// noise, the sigma schedule, per step timeCond -> DiT velocities (cond and uncond batched as B=2)
+// -> CFG combine + denoised + sampler update in one kernel (anima_sampler_step), then the latent
+// comes back once at the end.  Text encoding and the VAE are outside this build: the caller
+// passes the conditioning made by AnimaDiT.prepareContext ([positive] or, with CFG,
+// [positive, negative]).
+//
+// Noise is drawn on the host with the reference's torch.randn port (rng.mjs), in the reference's
+// order, and uploaded; drawing it after the step's DiT work is enqueued overlaps it with that work.
+// timeCond results are cached per sigma (they depend only on sigma and on the weights / LoRAs).
+
+import { native } from "./gpu.mjs";
+import { TorchGenerator } from "./rng.mjs";
+import { SCHEDULERS, SamplerPlan, sample } from "./samplers.mjs";
+import { loraGeneration } from "./lora.mjs";
+
+const TIME_CACHE_MAX = 64;
+
+export class LatentPipeline {
+  constructor(gpu, dit) {
+    this.gpu = gpu;
+    this.dit = dit;
+    this.timeCache = new Map(); // key -> timeCond result (device tensors), in insertion (LRU) order
+    this.stats = { timeCondHits: 0, timeCondMisses: 0 };
+  }
+
+  // dit.timeCond(sigma), cached.  The key includes the LoRA generation, so attaching LoRAs
+  // (which may touch the time embedder and the adaLN modulation) starts a fresh set.
+  timeCond(sigma) {
+    const key = `${sigma}|${loraGeneration()}`;
+    let tc = this.timeCache.get(key);
+    if (tc) {
+      this.stats.timeCondHits++;
+      this.timeCache.delete(key);
+      this.timeCache.set(key, tc);
+      return tc;
+    }
+    this.stats.timeCondMisses++;
+    tc = this.dit.timeCond(sigma);
+    this.timeCache.set(key, tc);
+    while (this.timeCache.size > TIME_CACHE_MAX) {
+      const [k, old] = this.timeCache.entries().next().value;
+      old.release();
+      this.timeCache.delete(k);
+    }
+    return tc;
+  }
+
+  clearTimeCache() {
+    for (const tc of this.timeCache.values()) tc.release();
+    this.timeCache.clear();
+  }
+
+  // opts: { cond, cfg = 1, width, height, steps, sampler, seed = 0, shift = 3, scheduler = "simple",
+  //         onStep(i, readDenoised) }.  cond.B must be 2 when cfg != 1 (positive, negative), else 1.
+  // Returns { latent: Float32Array [16, h, w], sigmas, timings }.
+  async generate(opts) {
+    const gpu = this.gpu;
+    const { cond, width, height, steps, sampler } = opts;
+    const cfg = opts.cfg === undefined ? 1 : opts.cfg;
+    const seed = opts.seed || 0, shift = opts.shift === undefined ? 3 : opts.shift;
+    const guided = cfg !== 1;
+    const B = guided ? 2 : 1;
+    if (cond.B !== B) throw new Error(`generate: cfg ${cfg} needs ${B} prompt(s) in cond, got ${cond.B}`);
+    const h = height / 8, w = width / 8, n = 16 * h * w;
+    const t0 = Date.now();
+    const sigmas = (SCHEDULERS[opts.scheduler] || SCHEDULERS.simple)(steps, shift);
+    const plan = new SamplerPlan(sampler, sigmas, shift);
+    const noise0 = new TorchGenerator(seed).randn(n);
+    const x = gpu.fromArray(noise0.map((v) => v * sigmas[0]), [1, 16, h, w]);
+    const gen = new TorchGenerator(seed); // the sampler's own generator (samplers.js:105)
+    const lat = gpu.empty([B, 16, h, w]);
+    const old = gpu.empty([n]), oldD = plan.name === "er_sde" ? gpu.empty([n]) : null;
+    const den = opts.onStep ? gpu.empty([n]) : null;
+    try {
+      for (let i = 0; i < plan.steps; i++) {
+        const st = plan.step(i);
+        const tc = this.timeCond(st.sigma);
+        for (let b = 0; b < B; b++) gpu.copy(lat.at(b * n), x, n * 4);
+        const v = await this.dit.forwardDevice(lat, h, w, cond, tc);
+        const eps = st.noise ? gpu.fromArray(gen.randn(n), [n]) : null;
+        native.samplerStep(gpu.ctx, {
+          kind: st.kind, n, x: x.buf, v: v.buf, vUncond: guided ? v.at(n) : 0, cfg, sigma: st.sigma,
+          final: st.final, stage: st.stage, den: den ? den.buf : 0, old: plan.kind >= 2 ? old.buf : 0,
+          oldD: oldD ? oldD.buf : 0, eps: eps ? eps.buf : 0, c: st.c,
+        });
+        v.release();
+        if (eps) eps.release();
+        if (opts.onStep) await opts.onStep(i, () => gpu.read(den));
+      }
+      const latent = await gpu.read(x);
+      const ms = Date.now() - t0;
+      return { latent, sigmas, timings: { sample: ms, perStep: ms / plan.steps } };
+    } finally {
+      for (const t of [x, lat, old, oldD, den]) if (t) t.release();
+    }
+  }
+
+  // The same sampling with the reference's host loop: velocities come back every step, and CFG,
+  // the denoised estimate and the sampler update run over Float32Arrays (pipeline.js:276-283,
+  // samplers.js:104-218).  For parity checks and as the drop-in's baseline.
+  async generateHost(opts) {
+    const { cond, width, height, steps, sampler } = opts;
+    const cfg = opts.cfg === undefined ? 1 : opts.cfg;
+    const seed = opts.seed || 0, shift = opts.shift === undefined ? 3 : opts.shift;
+    const guided = cfg !== 1;
+    if (cond.B !== (guided ? 2 : 1)) throw new Error(`generateHost: cfg ${cfg} needs ${guided ? 2 : 1} prompt(s)`);
+    const h = height / 8, w = width / 8, n = 16 * h * w;
+    const t0 = Date.now();
+    const sigmas = (SCHEDULERS[opts.scheduler] || SCHEDULERS.simple)(steps, shift);
+    const noise0 = new TorchGenerator(seed).randn(n);
+    const x0 = noise0.map((v) => v * sigmas[0]);
+    const denoise = async (xin, sigma) => {
+      const tc = this.timeCond(sigma);
+      const vs = await this.dit.forward(guided ? [xin, xin] : [xin], h, w, cond, tc);
+      const v = vs[0];
+      if (guided) {
+        const vn = vs[1];
+        for (let j = 0; j < n; j++) v[j] = vn[j] + cfg * (v[j] - vn[j]);
+      }
+      const den = new Float32Array(n);
+      for (let j = 0; j < n; j++) den[j] = xin[j] - sigma * v[j];
+      return den;
+    };
+    const latent = await sample(sampler, denoise, x0, sigmas, { seed, shift });
+    const ms = Date.now() - t0;
+    return { latent, sigmas, timings: { sample: ms, perStep: ms / (sigmas.length - 1) } };
+  }
+}

@@ -14,6 +14,8 @@
 //              and mlp.layer2 linears with and without the attached LoRA
 //   loramod    timeCond of a 1-block synthetic DiT with LoRAs on the adaLN modulation linears,
 //              on the fused (grouped GEMV) and the per-linear modulation paths
+//   generate   LatentPipeline.generate (device loop) and generateHost (the reference's host loop)
+//              on a synthetic DiT, per sampler / scheduler / cfg
 
 import fs from "fs";
 import { GPU } from "./gpu.mjs";
@@ -23,6 +25,8 @@ import { SafeTensors } from "./weights.mjs";
 import { AnimaDiT } from "./dit.mjs";
 import { SyntheticWeights } from "./weights.mjs";
 import { linearRegistry, loadLora, attachLoras, destroyLora, rotatedA } from "./lora.mjs";
+import { LatentPipeline } from "./pipeline.mjs";
+import { TorchGenerator } from "./rng.mjs";
 
 const ARR = { f32: Float32Array, i8: Int8Array, u8: Uint8Array, u16: Uint16Array, i32: Int32Array };
 
@@ -148,6 +152,25 @@ async function main() {
       destroyLora(L);
     }
     console.log(JSON.stringify(info));
+  } else if (c.case === "generate") {
+    const dit = AnimaDiT.synthetic(gpu, new SyntheticWeights(gpu, 5, { mode: c.mode, blocks: c.blocks || 1 }));
+    const pipe = new LatentPipeline(gpu, dit);
+    const runs = {};
+    for (const run of c.runs) {
+      const B = run.cfg !== 1 ? 2 : 1;
+      const ctxs = [];
+      for (let b = 0; b < B; b++) ctxs.push(gpu.fromArray(new TorchGenerator(100 + b).randn(c.Lk * 1024), [c.Lk, 1024]));
+      const cond = dit.prepareContext(ctxs);
+      const opts = Object.assign({ cond, width: c.size, height: c.size }, run);
+      const dev = await pipe.generate(opts);
+      const host = await pipe.generateHost(opts);
+      save(`${c.out}.${run.key}.dev`, dev.latent);
+      save(`${c.out}.${run.key}.host`, host.latent);
+      runs[run.key] = { steps: dev.sigmas.length - 1 };
+      cond.release();
+    }
+    console.log(JSON.stringify({ runs, stats: pipe.stats }));
+    pipe.clearTimeCache();
   } else if (c.case === "lnmod") {
     const x = gpu.fromArray(load(c.x), [c.rows, c.cols]);
     const mod = gpu.upload(load(c.mod));

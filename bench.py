@@ -78,8 +78,8 @@ def dit_step(args):
     import subprocess
 
     js = os.path.join(ROOT, "anima-studio_amd", "js", "bench_dit.mjs")
-    r = subprocess.run(["node", js, "--steps", str(args.dit_steps), "--warmup", "1"], cwd=ROOT, capture_output=True,
-                       text=True, timeout=600)
+    r = subprocess.run(["node", js, "--steps", str(args.dit_steps), "--warmup", "1", "--generate", "8", "--sampler",
+                        "euler_a", "--cfg", "4"], cwd=ROOT, capture_output=True, text=True, timeout=600)
     if r.returncode != 0:
         raise RuntimeError("bench_dit.mjs failed: " + r.stderr[-2000:])
     d = json.loads(r.stdout.strip().splitlines()[-1])
@@ -87,7 +87,9 @@ def dit_step(args):
             "config": "Anima DiT 28 blocks, 1024x1024 (4096 tokens), B=2 CFG, hidden 2048, 16x128 heads, MLP 8192, "
                       "self + cross attention to 512x1024 contexts, W4A8 mixed (blocks 0/27 int8), seeded random weights; "
                       "step = timeCond + forward through node bench_dit.mjs",
-            "steps": args.dit_steps}
+            "steps": args.dit_steps,
+            # an 8-step euler_a run with CFG 4: the device sampling loop vs the reference's host loop
+            "sampling": d.get("generate")}
 
 
 LINEAR_SHAPES = (("qkv", 6144, 2048, "store"), ("out", 2048, 2048, "gated"), ("mlp1", 8192, 2048, "gelu"),

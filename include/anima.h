@@ -161,6 +161,45 @@ int anima_patchify(anima_ctx* ctx, const float* latents, int B, int h, int w, fl
  * (p1 p2 c) order -> latents [B][16][h][w], "(h w) (p1 p2 c) -> c (h p1) (w p2)".  h, w even. */
 int anima_unpatchify(anima_ctx* ctx, const float* o, int B, int h, int w, float* latents);
 
+/* One sampler step on the device, replacing the host loops of app/pipeline.js:276-283 (CFG
+ * combine v = vu + cfg (vc - vu), denoised = x - sigma v) and of app/samplers.js:104-218 (the
+ * per-sampler update of x).  Every value the reference stores into a Float32Array is formed here
+ * in double precision from the same operands in the same order, without fused multiply-adds, and
+ * rounded to float at the same point, so that on equal inputs x, den, old and old_d are
+ * bit-identical to the reference's.  The scalar coefficients c[] are computed by the host exactly
+ * as the reference computes them (see each kind):
+ *   EULER     c0 = s1/s, c1 = 1 - s1/s:                      x = c0 x + c1 den
+ *   EULER_A   c0 = r, c1 = 1 - r, c2 = k, c3 = renoise:       t = c0 x + c1 den; x = c2 t + eps c3
+ *   DPMPP_2M  c0 = ratio, c1 = -expm1(-h); stage 1 adds c2 = 1 + 1/(2 r), c3 = -1/(2 r):
+ *             dd = stage ? c2 den + c3 old : den;             x = c0 x + c1 dd
+ *   ER_SDE    c0 = (alpha_t / alpha_s) r, c1 = alpha_t (1 - r): x = c0 x + c1 den; stage >= 2:
+ *             c2, c3 = +-1/(l_s - l_{i-1}), c4: dD = c2 den + c3 old, x = x + c4 dD, old_d = dD;
+ *             stage 3: c5, c6 = +-2/(l_s - l_{i-2}), c7: dU = c5 dD + c6 old_d, x = x + c7 dU;
+ *             eps != NULL: c8 = alpha_t, c9 = nz: x = x + (c8 eps) c9
+ * final_step != 0 (next sigma 0): x = den.  old (DPMPP_2M, ER_SDE) is read when needed and then
+ * overwritten with den; den_out (optional) receives den. */
+#define ANIMA_SAMPLER_EULER 0
+#define ANIMA_SAMPLER_EULER_A 1
+#define ANIMA_SAMPLER_DPMPP_2M 2
+#define ANIMA_SAMPLER_ER_SDE 3
+typedef struct anima_sampler_desc {
+  int kind;
+  int64_t n;             /* latent elements of one image */
+  float* x;              /* [n] in / out */
+  const float* v;        /* [n] velocity of the (positive) conditioning */
+  const float* v_uncond; /* [n] velocity of the negative prompt, NULL without CFG */
+  double cfg;
+  double sigma;
+  int final_step;        /* next sigma is 0 */
+  int stage;             /* DPMPP_2M: 0 first step, 1 later; ER_SDE: 1, 2 or 3 */
+  float* den_out;        /* [n] or NULL */
+  float* old;            /* [n] previous den (DPMPP_2M, ER_SDE), else NULL */
+  float* old_d;          /* [n] previous first difference (ER_SDE), else NULL */
+  const float* eps;      /* [n] noise (EULER_A, ER_SDE) or NULL */
+  double c[10];
+} anima_sampler_desc;
+int anima_sampler_step(anima_ctx* ctx, const anima_sampler_desc* d);
+
 /* Seeded synthetic data on the device, for benchmarks and tests (no reference counterpart: the
  * reference loads real checkpoints).  Element i draws h = splitmix64(seed * 0xD1B54A32D192ED03 + i):
  *   ANIMA_FILL_U8    uint8   lo + h % (hi - lo + 1)                (integers lo..hi)
