@@ -103,6 +103,7 @@ def lib():
         L.anima_rope.argtypes = [_vp, _vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _i64, _i64, _i64]
         L.anima_hadamard.argtypes = [_vp, _vp, _vp, _i64]
         L.anima_quant_rows.argtypes = [_vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _vp, _vp]
+        L.anima_quant_rows_act.argtypes = [_vp, _vp, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp]
         L.anima_layernorm_mod.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, ctypes.c_int, ctypes.c_float, ctypes.c_int,
                                           _vp, _vp, _vp]
         L.anima_elementwise.argtypes = [_vp, ctypes.c_int, _vp, _vp, _vp, _i64]
@@ -244,7 +245,10 @@ class Context:
     def hadamard(self, x, y, n):
         return self._check(lib().anima_hadamard(self.h, _ptr(x), _ptr(y), n))
 
-    def quant_rows(self, x, M, K, rotate, q, s):
+    def quant_rows(self, x, M, K, rotate, q, s, act="none"):
+        if act != "none":
+            return self._check(lib().anima_quant_rows_act(self.h, _ptr(x), M, K, ACT[act], int(rotate), _ptr(q),
+                                                          _ptr(s)))
         return self._check(lib().anima_quant_rows(self.h, _ptr(x), M, K, int(rotate), _ptr(q), _ptr(s)))
 
     def layernorm_mod(self, x, mod, shift_off, scale_off, rows, cols, rotate=False, y=None, q=None, s=None, eps=1e-6):

@@ -18,6 +18,25 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // fp32 -> bf16, round to nearest even (v_cvt_pk_bf16_f32 on gfx950).
 __device__ __forceinline__ bf16 to_bf16(float x) { return (bf16)x; }
 
+// GELU with the Abramowitz-Stegun erf of app/gpu/kernels.js:11-18.  The reciprocal is v_rcp_f32
+// (1 ulp) and the exponential v_exp_f32 of the argument scaled by log2(e) (about 1 ulp plus the
+// rounding of the scaled argument): inside the accuracy WGSL itself grants the reference's
+// division (2.5 ulp) and exp (3 + 2|x| ulp); against the correctly rounded formula the output
+// differs by 2e-8 relative L2 on N(0, 9) inputs.
+__device__ __forceinline__ float gelu_erf(float x) {
+  const float z = x * 0.7071067811865476f;
+  const float s = z > 0.0f ? 1.0f : (z < 0.0f ? -1.0f : 0.0f);
+  const float a = fabsf(z);
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * a);
+  const float y = 1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
+                          0.254829592f) * t * __expf(-a * a);
+  return 0.5f * x * (1.0f + s * y);
+}
+
+// The activations of the linear epilogues (ANIMA_ACT_*), shared by the GEMM epilogues and the
+// row kernels that apply a linear's activation after the fact (anima_quant_rows_act).
+__device__ __forceinline__ float silu_f(float r) { return r / (1.0f + expf(-r)); }
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int s = 32; s > 0; s >>= 1) v += __shfl_xor(v, s);

@@ -38,24 +38,10 @@ struct GemmArgs {
   int64_t ld_add;
 };
 
-// GELU with the Abramowitz-Stegun erf of app/gpu/kernels.js:11-18.  The reciprocal is v_rcp_f32
-// (1 ulp) and the exponential v_exp_f32 of the argument scaled by log2(e) (about 1 ulp plus the
-// rounding of the scaled argument): inside the accuracy WGSL itself grants the reference's
-// division (2.5 ulp) and exp (3 + 2|x| ulp); against the correctly rounded formula the output
-// differs by 2e-8 relative L2 on N(0, 9) inputs.
-__device__ __forceinline__ float gelu_erf(float x) {
-  const float z = x * 0.7071067811865476f;
-  const float s = z > 0.0f ? 1.0f : (z < 0.0f ? -1.0f : 0.0f);
-  const float a = fabsf(z);
-  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * a);
-  const float y = 1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
-                          0.254829592f) * t * __expf(-a * a);
-  return 0.5f * x * (1.0f + s * y);
-}
 
 __device__ __forceinline__ float apply_act(float r, int act) {
   if (act == ANIMA_ACT_GELU) return gelu_erf(r);
-  if (act == ANIMA_ACT_SILU) return r / (1.0f + expf(-r));
+  if (act == ANIMA_ACT_SILU) return silu_f(r);
   return r;
 }
 
@@ -288,7 +274,7 @@ __device__ __forceinline__ void epi_store_t(const GemmArgs& a, const i32x16& v, 
       for (int e = 0; e < 4; e++) y[e] = gelu_erf(y[e]);
     } else if (a.act == ANIMA_ACT_SILU) {
 #pragma unroll
-      for (int e = 0; e < 4; e++) y[e] = y[e] / (1.0f + expf(-y[e]));
+      for (int e = 0; e < 4; e++) y[e] = silu_f(y[e]);
     }
     f32x4 o;
     if constexpr (EPI == ANIMA_EPI_STORE) {
@@ -657,11 +643,32 @@ __global__ __launch_bounds__(256) void gemm_f32m_kernel(F32WArgs a) {
   }
 }
 
+// Weight element loads of the fp32-MFMA kernels: fp32 weights, or bf16 weights widened exactly
+// (bf16 << 16) so the products and sums are those of the fp32 weights.  Four consecutive values:
+// one 16-byte load (fp32) or one 8-byte load (bf16).
+template <bool BF>
+__device__ __forceinline__ float4 ld_w4(const void* w, int64_t i) {
+  if constexpr (BF) {
+    const uint2 u = *(const uint2*)((const uint16_t*)w + i);
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                       __uint_as_float(u.y & 0xffff0000u));
+  } else {
+    return *(const float4*)((const float*)w + i);
+  }
+}
+template <bool BF>
+__device__ __forceinline__ float ld_w1(const void* w, int64_t i) {
+  if constexpr (BF) return __uint_as_float((uint32_t)((const uint16_t*)w)[i] << 16);
+  else return ((const float*)w)[i];
+}
+
 // The same product with the operands swapped (W rows as MFMA A, x rows as MFMA B), so the result
 // is C^T in the MFMA layout: lane (l, h) holds output row m0 + l and, in register group g, the four
 // consecutive columns n0 + 8g + 4h .. + 3, which the epilogue moves as 16-byte loads / stores.
 // Needs N % 4 == 0 and 16-byte aligned out / add / bias / gate rows; the LoRA B products (output
-// width = model width, K = rank) are write-bound, so this is their kernel.
+// width = model width, K = rank) are write-bound, so this is their kernel, and with bf16 weights
+// (BF) that of the x_embedder (K = 68).
+template <bool BF>
 __global__ __launch_bounds__(256) void gemm_f32m_t_kernel(F32WArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lq = lane & 31, hf = lane >> 5;
   const int m0 = blockIdx.y * 64 + (wave & 1) * 32;
@@ -669,7 +676,7 @@ __global__ __launch_bounds__(256) void gemm_f32m_t_kernel(F32WArgs a) {
   const int m = m0 + lq, n = n0 + lq;
   const bool mok = m < a.M, nok = n < a.N;
   const float* xr = a.x + (int64_t)(mok ? m : 0) * a.ldx + 16 * hf;
-  const float* wr = (const float*)a.w + (int64_t)(nok ? n : 0) * a.K + 16 * hf;
+  const int64_t wr = (int64_t)(nok ? n : 0) * a.K + 16 * hf;
   f32x16 acc = {};
   const int nkt = (a.K + 31) / 32;
   for (int kt = 0; kt < nkt; kt++) {
@@ -679,7 +686,7 @@ __global__ __launch_bounds__(256) void gemm_f32m_t_kernel(F32WArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         const float4 t = mok ? *(const float4*)(xr + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        const float4 u = nok ? *(const float4*)(wr + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float4 u = nok ? ld_w4<BF>(a.w, wr + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         xv[4 * j] = t.x; xv[4 * j + 1] = t.y; xv[4 * j + 2] = t.z; xv[4 * j + 3] = t.w;
         wv[4 * j] = u.x; wv[4 * j + 1] = u.y; wv[4 * j + 2] = u.z; wv[4 * j + 3] = u.w;
       }
@@ -688,7 +695,7 @@ __global__ __launch_bounds__(256) void gemm_f32m_t_kernel(F32WArgs a) {
       for (int s = 0; s < 16; s++) {
         const bool kok = k0 + 16 * hf + s < a.K;
         xv[s] = mok && kok ? xr[k0 + s] : 0.0f;
-        wv[s] = nok && kok ? wr[k0 + s] : 0.0f;
+        wv[s] = nok && kok ? ld_w1<BF>(a.w, wr + k0 + s) : 0.0f;
       }
     }
 #pragma unroll
@@ -729,7 +736,7 @@ __global__ __launch_bounds__(256) void gemm_f32m_t_kernel(F32WArgs a) {
 // tree order through LDS (deterministic).  Block: 32 rows x 32 RT columns.  Lane layout and
 // epilogue as gemm_f32m_kernel.
 constexpr int SK_WAVES = 8;
-template <int RT>
+template <int RT, bool BF>
 __global__ __launch_bounds__(64 * SK_WAVES) void gemm_f32m_skinny_kernel(F32WArgs a) {
   __shared__ float part[SK_WAVES / 2 * 64 * 16 * RT];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lq = lane & 31, hf = lane >> 5;
@@ -737,13 +744,13 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_f32m_skinny_kernel(F32WArg
   const int m = m0 + lq;
   const bool mok = m < a.M;
   const float* xr = a.x + (int64_t)(mok ? m : 0) * a.ldx + 16 * hf;
-  const float* wr[RT];
+  int64_t wr[RT];
   bool nok[RT];
 #pragma unroll
   for (int t = 0; t < RT; t++) {
     const int n = nb + 32 * t + lq;
     nok[t] = n < a.N;
-    wr[t] = (const float*)a.w + (int64_t)(nok[t] ? n : 0) * a.K + 16 * hf;
+    wr[t] = (int64_t)(nok[t] ? n : 0) * a.K + 16 * hf;
   }
   f32x16 acc[RT];
 #pragma unroll
@@ -756,7 +763,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_f32m_skinny_kernel(F32WArg
       for (int j = 0; j < 4; j++) {
         xv[j] = mok ? *(const float4*)(xr + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (int t = 0; t < RT; t++) wv[t][j] = nok[t] ? *(const float4*)(wr[t] + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int t = 0; t < RT; t++) wv[t][j] = nok[t] ? ld_w4<BF>(a.w, wr[t] + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       }
     } else {  // the last, partial k-tile
       float xs[16], ws[RT][16];
@@ -765,7 +772,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_f32m_skinny_kernel(F32WArg
         const bool kok = k0 + 16 * hf + s < a.K;
         xs[s] = mok && kok ? xr[k0 + s] : 0.0f;
 #pragma unroll
-        for (int t = 0; t < RT; t++) ws[t][s] = nok[t] && kok ? wr[t][k0 + s] : 0.0f;
+        for (int t = 0; t < RT; t++) ws[t][s] = nok[t] && kok ? ld_w1<BF>(a.w, wr[t] + k0 + s) : 0.0f;
       }
 #pragma unroll
       for (int j = 0; j < 4; j++) {
@@ -930,22 +937,27 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
       return L.end();
     }
     Launch L(c, f32 ? "gemm.f32" : "gemm.bf16", 2.0 * M * N * K, 0.0);
-    if (f32 && K % 4 == 0 && ldx % 4 == 0 && al(d->x, 16) && al(W->w, 16)) {  // fp32 matrix cores
-      const dim3 sk((unsigned)((N + 127) / 128), (unsigned)((M + 31) / 32));
-      if (N <= 32 && K >= 512)
-        hipLaunchKernelGGL(gemm_f32m_skinny_kernel<1>, sk, dim3(64 * SK_WAVES), 0, c->stream, f);
-      else if (N <= 64 && K >= 512)
-        hipLaunchKernelGGL(gemm_f32m_skinny_kernel<2>, sk, dim3(64 * SK_WAVES), 0, c->stream, f);
-      else if (N <= 96 && K >= 512)
-        hipLaunchKernelGGL(gemm_f32m_skinny_kernel<3>, sk, dim3(64 * SK_WAVES), 0, c->stream, f);
-      else if (N <= 256 && K >= 512)
-        hipLaunchKernelGGL(gemm_f32m_skinny_kernel<4>, sk, dim3(64 * SK_WAVES), 0, c->stream, f);
-      else if (N % 4 == 0 && ldc % 4 == 0 && al(d->out, 16) && (!W->bias || al(W->bias, 16)) &&
-               (!d->add || (al(d->add, 16) && ld_add % 4 == 0)) &&
-               (d->epilogue != ANIMA_EPI_GATED || al(d->gate + d->gate_off, 16)))
-        hipLaunchKernelGGL(gemm_f32m_t_kernel, dim3((N + 63) / 64, (unsigned)((M + 63) / 64)), dim3(256), 0, c->stream, f);
-      else
-        hipLaunchKernelGGL(gemm_f32m_kernel, dim3((N + 63) / 64, (unsigned)((M + 63) / 64)), dim3(256), 0, c->stream, f);
+    // fp32 matrix cores: x rows 16-byte aligned; weight rows 16-byte (fp32) / 8-byte (bf16) aligned
+    if (K % 4 == 0 && ldx % 4 == 0 && al(d->x, 16) && al(W->w, f32 ? 16 : 8)) {
+      const dim3 sk((unsigned)((N + 127) / 128), (unsigned)((M + 31) / 32)), blk(64 * SK_WAVES);
+      const dim3 g64((N + 63) / 64, (unsigned)((M + 63) / 64));
+      const bool vec = N % 4 == 0 && ldc % 4 == 0 && al(d->out, 16) && (!W->bias || al(W->bias, 16)) &&
+                       (!d->add || (al(d->add, 16) && ld_add % 4 == 0)) &&
+                       (d->epilogue != ANIMA_EPI_GATED || al(d->gate + d->gate_off, 16));
+#define F32M_SKINNY(RT)                                                                  \
+  do {                                                                                   \
+    if (f32) hipLaunchKernelGGL((gemm_f32m_skinny_kernel<RT, false>), sk, blk, 0, c->stream, f); \
+    else hipLaunchKernelGGL((gemm_f32m_skinny_kernel<RT, true>), sk, blk, 0, c->stream, f);      \
+  } while (0)
+      if (N <= 32 && K >= 512) F32M_SKINNY(1);
+      else if (N <= 64 && K >= 512) F32M_SKINNY(2);
+      else if (N <= 96 && K >= 512) F32M_SKINNY(3);
+      else if (N <= 256 && K >= 512) F32M_SKINNY(4);
+      else if (vec && f32) hipLaunchKernelGGL(gemm_f32m_t_kernel<false>, g64, dim3(256), 0, c->stream, f);
+      else if (vec) hipLaunchKernelGGL(gemm_f32m_t_kernel<true>, g64, dim3(256), 0, c->stream, f);
+      else if (f32) hipLaunchKernelGGL(gemm_f32m_kernel, g64, dim3(256), 0, c->stream, f);
+      else hipLaunchKernelGGL(gemm_f32w_kernel, g64, dim3(256), 0, c->stream, f);
+#undef F32M_SKINNY
       return L.end();
     }
     hipLaunchKernelGGL(gemm_f32w_kernel, dim3((N + 63) / 64, (unsigned)((M + 63) / 64)), dim3(256), 0, c->stream, f);
@@ -969,7 +981,7 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
     if (rc) return rc;
     int8_t* q = (int8_t*)tmp;
     float* s = (float*)((char*)tmp + ((size_t)M * K + 255) / 256 * 256);
-    rc = quant_rows_launch(c, d->x, M, K, d->x_rotated ? 0 : 1, q, s);
+    rc = quant_rows_launch(c, d->x, M, K, d->x_rotated ? 0 : 1, ANIMA_ACT_NONE, q, s);
     if (rc) {
       anima_free(c, tmp);
       return rc;

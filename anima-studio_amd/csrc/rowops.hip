@@ -318,9 +318,17 @@ __host__ __device__ constexpr int padded_cols(int cols) { return cols + 4 * ((co
 
 // rows of K: optional rotation (K % 256 == 0), per-token int8.  WPR waves per row; a workgroup
 // holds 4 / WPR rows; dynamic LDS = rows per workgroup * padded_cols(K) floats.
+// activation of the preceding linear (ANIMA_ACT_*), applied to a loaded float4
+__device__ __forceinline__ float act1(float v, int act) {
+  return act == ANIMA_ACT_GELU ? gelu_erf(v) : act == ANIMA_ACT_SILU ? silu_f(v) : v;
+}
+__device__ __forceinline__ float4 act4(float4 v, int act) {
+  return make_float4(act1(v.x, act), act1(v.y, act), act1(v.z, act), act1(v.w, act));
+}
+
 template <int WPR>
-__global__ __launch_bounds__(256) void quant_rows_pad_kernel(const float* X, int64_t M, int K, int rotate, int8_t* Q,
-                                                             float* S_out) {
+__global__ __launch_bounds__(256) void quant_rows_pad_kernel(const float* X, int64_t M, int K, int rotate, int act,
+                                                             int8_t* Q, float* S_out) {
   extern __shared__ float SH[];
   __shared__ float red[4];
   constexpr int T = 64 * WPR;
@@ -336,6 +344,10 @@ __global__ __launch_bounds__(256) void quant_rows_pad_kernel(const float* X, int
     const int c4 = tr + T * i;
     v[i] = c4 < (K >> 2) ? *(const float4*)(x + 4 * c4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
+  if (act != ANIMA_ACT_NONE) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = act4(v[i], act);
+  }
 #pragma unroll
   for (int i = 0; i < 8; i++) {
     const int c4 = tr + T * i;
@@ -348,7 +360,7 @@ __global__ __launch_bounds__(256) void quant_rows_pad_kernel(const float* X, int
 
 // ------------------------------------------------------------------ register-resident rows
 //
-// Rows of K % 1024 == 0 columns: lane L of a row's LR = K/64 lanes holds the 64 consecutive
+// Rows of K = 1024, 2048, 4096 or 8192 columns: lane L of a row's LR = K/64 lanes holds the 64 consecutive
 // elements 64L..64L+63, so a 256-element Hadamard block sits in 4 consecutive lanes (a DPP quad).
 // Butterfly stages 1-3 (strides 1, 4, 16) combine elements of one lane; stage 4 (stride 64)
 // combines the four lanes of the quad through DPP broadcasts.  Each stage applies the 4-point
@@ -428,10 +440,10 @@ __device__ __forceinline__ void quant64_store(const float (&v)[64], float amax, 
   }
 }
 
-// rows of K = 64 * LR columns (K % 1024 == 0, K <= 8192), optional Hadamard, per-token int8.
+// rows of K = 64 * LR columns (LR = 16, 32, 64, 128), optional activation and Hadamard, per-token int8.
 // 256 threads: 256 / LR rows per workgroup (LR = 128: one row over two waves, two per workgroup).
 template <int LR>
-__global__ __launch_bounds__(256) void quant_rows_reg_kernel(const float* X, int64_t M, int rotate, int8_t* Q,
+__global__ __launch_bounds__(256) void quant_rows_reg_kernel(const float* X, int64_t M, int rotate, int act, int8_t* Q,
                                                              float* S_out) {
   constexpr int K = 64 * LR;
   __shared__ float red[4];
@@ -447,6 +459,10 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(const float* X, int
     v[4 * i + 1] = t.y;
     v[4 * i + 2] = t.z;
     v[4 * i + 3] = t.w;
+  }
+  if (act != ANIMA_ACT_NONE) {
+#pragma unroll
+    for (int i = 0; i < 64; i++) v[i] = act1(v[i], act);
   }
   if (rotate) hadamard64_quad(v, L & 3);
   float am = 0.0f;
@@ -535,8 +551,6 @@ __global__ __launch_bounds__(256) void layernorm_mod_wave_kernel(const float* X,
                       Q ? S_out + row : nullptr);
 }
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
-
 __global__ __launch_bounds__(256) void elementwise_kernel(int op, const float* A, const float* B, float* Y, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
     const float a = A ? A[i] : 0.0f;
@@ -569,31 +583,33 @@ int hadamard_launch(anima_ctx* c, const float* x, float* y, int64_t n) {
   return lc.end();
 }
 
-int quant_rows_launch(anima_ctx* c, const float* x, int64_t M, int K, int rotate, int8_t* q, float* s) {
+int quant_rows_launch(anima_ctx* c, const float* x, int64_t M, int K, int rotate, int act, int8_t* q, float* s) {
   if (!x || !q || !s) return fail(c, ANIMA_E_ARG, "anima_quant_rows: null pointer");
+  if (act < ANIMA_ACT_NONE || act > ANIMA_ACT_SILU) return fail(c, ANIMA_E_ARG, "anima_quant_rows_act: unknown act %d", act);
   if (M < 0 || K < 4 || K % 4 || K > 8192 || (rotate && K % 256))
     return fail(c, ANIMA_E_ARG, "anima_quant_rows: M=%lld K=%d (K %% 4 == 0, <= 8192, %% 256 == 0 when rotating)", (long long)M, K);
   if (M > 0x7fffffff) return fail(c, ANIMA_E_ARG, "anima_quant_rows: M too large");
   if (((uintptr_t)x & 15) || ((uintptr_t)q & 3)) return fail(c, ANIMA_E_ARG, "anima_quant_rows: x must be 16-byte and q 4-byte aligned");
   if (M == 0) return ANIMA_OK;
-  Launch lc(c, rotate ? "hadamard_quant" : "quant_rows", 0.0, (double)M * K * 5 + M * 4.0);
-  if (K % 1024 == 0 && !((uintptr_t)q & 15)) {  // register-resident rows
+  Launch lc(c, act ? "act_hadamard_quant" : rotate ? "hadamard_quant" : "quant_rows", 0.0, (double)M * K * 5 + M * 4.0);
+  // register-resident rows for the widths with a kernel instance (a row of K = 64 LR columns)
+  if ((K == 1024 || K == 2048 || K == 4096 || K == 8192) && !((uintptr_t)q & 15)) {
     const unsigned rows_per = 256 / (K / 64);
     const dim3 grid((unsigned)((M + rows_per - 1) / rows_per));
     switch (K) {
-      case 1024: hipLaunchKernelGGL(quant_rows_reg_kernel<16>, grid, dim3(256), 0, c->stream, x, M, rotate, q, s); break;
-      case 2048: hipLaunchKernelGGL(quant_rows_reg_kernel<32>, grid, dim3(256), 0, c->stream, x, M, rotate, q, s); break;
-      case 4096: hipLaunchKernelGGL(quant_rows_reg_kernel<64>, grid, dim3(256), 0, c->stream, x, M, rotate, q, s); break;
-      default: hipLaunchKernelGGL(quant_rows_reg_kernel<128>, grid, dim3(256), 0, c->stream, x, M, rotate, q, s); break;
+      case 1024: hipLaunchKernelGGL(quant_rows_reg_kernel<16>, grid, dim3(256), 0, c->stream, x, M, rotate, act, q, s); break;
+      case 2048: hipLaunchKernelGGL(quant_rows_reg_kernel<32>, grid, dim3(256), 0, c->stream, x, M, rotate, act, q, s); break;
+      case 4096: hipLaunchKernelGGL(quant_rows_reg_kernel<64>, grid, dim3(256), 0, c->stream, x, M, rotate, act, q, s); break;
+      case 8192: hipLaunchKernelGGL(quant_rows_reg_kernel<128>, grid, dim3(256), 0, c->stream, x, M, rotate, act, q, s); break;
     }
     return lc.end();
   }
   if (K > 2048)  // four waves per row, one row per workgroup (at most 35 KB of LDS)
     hipLaunchKernelGGL(quant_rows_pad_kernel<4>, dim3((unsigned)M), dim3(256), (size_t)padded_cols(K) * 4, c->stream, x, M,
-                       K, rotate, q, s);
+                       K, rotate, act, q, s);
   else  // one wave per row, four rows per workgroup
     hipLaunchKernelGGL(quant_rows_pad_kernel<1>, dim3((unsigned)((M + 3) / 4)), dim3(256), (size_t)4 * padded_cols(K) * 4,
-                       c->stream, x, M, K, rotate, q, s);
+                       c->stream, x, M, K, rotate, act, q, s);
   return lc.end();
 }
 

@@ -371,7 +371,12 @@ int anima_hadamard(anima_ctx* c, const float* x, float* y, int64_t n) {
 
 int anima_quant_rows(anima_ctx* c, const float* x, int64_t M, int K, int rotate, int8_t* q, float* s) {
   CHECK_CTX(c);
-  return quant_rows_launch(c, x, M, K, rotate, q, s);
+  return quant_rows_launch(c, x, M, K, rotate, ANIMA_ACT_NONE, q, s);
+}
+
+int anima_quant_rows_act(anima_ctx* c, const float* x, int64_t M, int K, int act, int rotate, int8_t* q, float* s) {
+  CHECK_CTX(c);
+  return quant_rows_launch(c, x, M, K, rotate, act, q, s);
 }
 
 int anima_layernorm_mod(anima_ctx* c, const float* x, const float* mod, int64_t shift_off, int64_t scale_off,

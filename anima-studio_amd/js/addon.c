@@ -359,13 +359,18 @@ static napi_value js_hadamard(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
-/* quantRows(ctx, x, M, K, rotate, q, s) */
+/* quantRows(ctx, x, M, K, rotate, q, s[, act]) */
 static napi_value js_quant_rows(napi_env env, napi_callback_info info) {
-  napi_value a[7];
-  get_args(env, info, 7, a);
+  napi_value a[8];
+  get_args(env, info, 8, a);
   anima_ctx* c = ctx_of(env, a[0]);
-  CHECK_RC(env, c, anima_quant_rows(c, (const float*)ptr(env, a[1]), i64(env, a[2]), (int)num(env, a[3]),
-                                    (int)num(env, a[4]), (int8_t*)ptr(env, a[5]), (float*)ptr(env, a[6])));
+  const int act = (int)num(env, a[7]); /* optional: the activation applied first (anima_quant_rows_act) */
+  if (act)
+    CHECK_RC(env, c, anima_quant_rows_act(c, (const float*)ptr(env, a[1]), i64(env, a[2]), (int)num(env, a[3]), act,
+                                          (int)num(env, a[4]), (int8_t*)ptr(env, a[5]), (float*)ptr(env, a[6])));
+  else
+    CHECK_RC(env, c, anima_quant_rows(c, (const float*)ptr(env, a[1]), i64(env, a[2]), (int)num(env, a[3]),
+                                      (int)num(env, a[4]), (int8_t*)ptr(env, a[5]), (float*)ptr(env, a[6])));
   return NULL;
 }
 

@@ -310,12 +310,23 @@ export class AnimaDiT {
       ops.linear(gpu, a, b.cross.o, { M, out: x, resid: true, gate: m.cross, gOff: 2 * D });
       a.release();
 
-      // MLP
+      // MLP.  With a quantized layer2 (and no LoRA on it, which needs the fp32 GELU output),
+      // layer1 stores its pre-activation and the GELU runs in layer2's Hadamard + int8 pass, off
+      // the GEMM epilogue; the int8 rows are the same.
       nf = normFor(gpu, x, m.mlp, b.l1);
-      const hdn = project(gpu, nf, b.l1, M, { act: "gelu" });
-      releaseNorm(nf);
-      ops.linear(gpu, hdn, b.l2, { M, out: x, resid: true, gate: m.mlp, gOff: 2 * D });
-      hdn.release();
+      if (ops.needsRotation(b.l2) && !(b.l2.lora && b.l2.lora.length)) {
+        const pre = project(gpu, nf, b.l1, M);
+        releaseNorm(nf);
+        const hq = ops.quantRows(gpu, pre, MLP, true, "gelu");
+        pre.release();
+        ops.linear(gpu, null, b.l2, { M, xq: hq, out: x, resid: true, gate: m.mlp, gOff: 2 * D });
+        hq.release();
+      } else {
+        const hdn = project(gpu, nf, b.l1, M, { act: "gelu" });
+        releaseNorm(nf);
+        ops.linear(gpu, hdn, b.l2, { M, out: x, resid: true, gate: m.mlp, gOff: 2 * D });
+        hdn.release();
+      }
 
       gpu.flush();
       if (onBlock) await onBlock(i, x);

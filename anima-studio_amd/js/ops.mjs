@@ -25,11 +25,11 @@ export function rotate(gpu, x) {
 }
 
 // Per-token int8 quantization of rows [M, K] (optionally ConvRot-rotating first).
-export function quantRows(gpu, x, K, rotateFirst) {
+export function quantRows(gpu, x, K, rotateFirst, act) {
   const M = x.size / K;
   const q = gpu.empty([M, K], "i8");
   const s = gpu.empty([M]);
-  native.quantRows(gpu.ctx, x.buf, M, K, rotateFirst ? 1 : 0, q.buf, s.buf);
+  native.quantRows(gpu.ctx, x.buf, M, K, rotateFirst ? 1 : 0, q.buf, s.buf, ACT[act || "none"]);
   return { q, s, release() { q.release(); s.release(); } };
 }
 

@@ -135,6 +135,13 @@ int anima_hadamard(anima_ctx* ctx, const float* x, float* y, int64_t n);
  * q[m,k] = clamp(rint(x_r[m,k] / s[m]), -127, 127).  K % 4 == 0, K <= 8192. */
 int anima_quant_rows(anima_ctx* ctx, const float* x, int64_t M, int K, int rotate, int8_t* q,
                      float* s);
+/* anima_quant_rows of act(x) (ANIMA_ACT_*, the epilogue activations of anima_linear, the same
+ * functions): a linear that feeds a quantized linear can store its pre-activation output and
+ * leave the activation to this pass (the MLP's GELU between mlp.layer1 and mlp.layer2,
+ * app/models/dit.js:306-311).  The int8 rows equal those of anima_quant_rows on the stored
+ * activation output. */
+int anima_quant_rows_act(anima_ctx* ctx, const float* x, int64_t M, int K, int act, int rotate,
+                         int8_t* q, float* s);
 /* ops.layernormMod (app/gpu/ops.js:129-137; kernels.js:95-145): LayerNorm without affine,
  * y = LN(x) * (1 + mod[scale_off + c]) + mod[shift_off + c], then the ConvRot Hadamard when
  * rotate != 0.  Writes the fp32 result to y (if non-NULL) and/or its per-token int8

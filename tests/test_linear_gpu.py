@@ -92,6 +92,39 @@ def test_layernorm_mod_bit_exact(ctx, cols, rotate, shift):
         assert np.array_equal(ds.numpy(), s) and np.array_equal(dq.numpy(), q)
 
 
+@pytest.mark.parametrize("K,act,rotate", [(8192, "gelu", True), (2048, "silu", True), (768, "gelu", True),
+                                          (3072, "gelu", False)])
+def test_quant_rows_act(ctx, K, act, rotate):
+    """anima_quant_rows_act: the activation of a linear applied in the Hadamard + int8 pass.  Its
+    int8 rows and scales are bit-identical to anima_quant_rows on the output of an int8 linear
+    with the same activation in its epilogue (same pre-activation values, same activation code);
+    register-resident (K % 1024 == 0) and LDS kernels, with and without the rotation."""
+    case(f"quant_rows_act K={K} act={act} rotate={rotate}")
+    m = amd()
+    M, Kin = 300, 1024
+    x = orc.randn(61, M * Kin).reshape(M, Kin)
+    qx, sx = orc.token_quant(orc.hadamard256(x))
+    qw, sw = int8_weight(62, K, Kin)
+    W = m.weight(m.W_I8, K, Kin, ctx.upload(qw), scale=ctx.upload(sw))
+    dqx, dsx = ctx.upload(qx), ctx.upload(sx)
+    pre, post = ctx.empty((M, K)), ctx.empty((M, K))
+    ctx.linear(W, M, pre, xq=dqx, xs=dsx, alpha=3.0)
+    ctx.linear(W, M, post, xq=dqx, xs=dsx, alpha=3.0, act=act)
+    q1, s1 = ctx.empty((M, K), np.int8), ctx.empty(M)
+    q2, s2 = ctx.empty((M, K), np.int8), ctx.empty(M)
+    ctx.quant_rows(pre, M, K, rotate, q1, s1, act=act)
+    ctx.quant_rows(post, M, K, rotate, q2, s2)
+    assert np.array_equal(s1.numpy(), s2.numpy()) and np.array_equal(q1.numpy(), q2.numpy())
+    # against the oracle's activation (correctly rounded formula): the int8 codes may differ by one
+    # where the 1-ulp device activation crosses a rounding boundary
+    p64 = pre.numpy().astype(np.float64)
+    a = np.vectorize(orc.gelu if act == "gelu" else orc.silu)(p64).astype(np.float32)
+    q, s = orc.token_quant(orc.hadamard256(a) if rotate else a)
+    assert np.allclose(s1.numpy(), s, rtol=1e-6, atol=0)
+    d = np.abs(q1.numpy().astype(np.int32) - q.astype(np.int32))
+    assert d.max() <= 1 and (d > 0).mean() < 1e-3
+
+
 def test_elementwise_and_zero(ctx):
     case("elementwise silu_mul/add/silu/copy, zero")
     n = 10007
@@ -308,9 +341,13 @@ def test_mlp1_activation_epilogue(ctx, act):
 
 
 def test_bf16_weight_linears(ctx):
-    case("bf16 weights: x_embedder K=68, GEMV M=1")
+    """bf16 weights widened exactly into the fp32 matrix-core kernels (x_embedder K=68 with a
+    partial k-tile, final layer N=64 and a ragged N=200 on the tall-skinny kernel, a GELU epilogue
+    on the swapped-operand kernel) and the M=1 GEMV, against float64."""
+    case("bf16 weights: x_embedder K=68, final layer, GEMV M=1")
     m = amd()
-    for (M, K, N, act) in ((300, 68, 2048, "none"), (1, 2048, 6144, "silu"), (97, 2048, 64, "none")):
+    for (M, K, N, act) in ((300, 68, 2048, "none"), (1, 2048, 6144, "silu"), (97, 2048, 64, "none"),
+                           (64, 1040, 200, "none"), (257, 1024, 516, "gelu")):
         x = orc.randn(81 + K, M * K).reshape(M, K)
         w32 = orc.bf16_round(0.05 * orc.randn(82 + N, N * K)).reshape(N, K)
         wb = (w32.view(np.uint32) >> 16).astype(np.uint16)
@@ -321,6 +358,8 @@ def test_bf16_weight_linears(ctx):
         ref = x.astype(np.float64) @ w32.astype(np.float64).T + bias
         if act == "silu":
             ref = ref / (1 + np.exp(-ref))
+        elif act == "gelu":
+            ref = np.vectorize(orc.gelu)(ref)
         r, _ = report(f"bf16 M={M} K={K} N={N}", dy.numpy(), ref)
         assert r < 1e-6
 
