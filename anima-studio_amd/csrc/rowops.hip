@@ -551,6 +551,111 @@ __global__ __launch_bounds__(256) void layernorm_mod_wave_kernel(const float* X,
                       Q ? S_out + row : nullptr);
 }
 
+// LayerNorm + adaLN (+ Hadamard) (+ int8) for rows of 64 LR columns (LR = 16, 32), LR lanes per
+// row, 256 / LR rows per workgroup, no workgroup barrier.  Statistics: lane l holds the VT = 256 / LR
+// consecutive elements VT l + j of every 256-column block, i.e. exactly the elements the
+// reference's 256-thread loops give to threads VT l + j (kernels.js:108-145), so the strided
+// partial sums and the "red[t] += red[t + s]" tree are reproduced term for term (the partner of
+// t = VT l + j at level s >= VT is lane l + s / VT, below VT it is in-lane).  The modulated row then
+// crosses LDS once (padded by 4 floats per 64: conflict-free 16-byte writes and reads) into the
+// register-Hadamard layout (lane l holds 64 l .. 64 l + 63) and leaves as int8 and / or fp32.
+template <int LR>
+__device__ __forceinline__ float seg_tree_sum(float (&p)[256 / LR]) {
+  constexpr int VT = 256 / LR;
+#pragma unroll
+  for (int s = 128; s >= 1; s >>= 1) {
+    if (s >= VT) {
+#pragma unroll
+      for (int j = 0; j < VT; j++) {
+        const float q = __shfl_down(p[j], s / VT, LR);
+        p[j] = p[j] + q;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < s; j++) p[j] = p[j] + p[j + s];
+    }
+  }
+  return __shfl(p[0], 0, LR);
+}
+
+template <int LR>
+__global__ __launch_bounds__(256) void layernorm_mod_reg_kernel(const float* X, const float* MOD, int64_t shift_off,
+                                                                int64_t scale_off, int64_t rows, float eps, int rotate,
+                                                                float* Y, int8_t* Q, float* S_out) {
+  constexpr int COLS = 64 * LR, VT = 256 / LR, NB = COLS / 256, RPW = 256 / LR, RS = COLS + 4 * LR;
+  __shared__ __attribute__((aligned(16))) float SH[RPW * RS];
+  const int l = threadIdx.x % LR, rl = threadIdx.x / LR;
+  const int64_t row = (int64_t)blockIdx.x * RPW + rl;
+  if (row >= rows) return;  // (a row's lanes leave together; nothing below spans rows)
+  const float* x = X + row * COLS + VT * l;
+  float v[64];  // v[VT i + j] = x[256 i + VT l + j]
+#pragma unroll
+  for (int i = 0; i < NB; i++)
+#pragma unroll
+    for (int q = 0; q < VT / 4; q++) {
+      const float4 t = *(const float4*)(x + 256 * i + 4 * q);
+      v[VT * i + 4 * q] = t.x;
+      v[VT * i + 4 * q + 1] = t.y;
+      v[VT * i + 4 * q + 2] = t.z;
+      v[VT * i + 4 * q + 3] = t.w;
+    }
+  float p[VT];
+#pragma unroll
+  for (int j = 0; j < VT; j++) p[j] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NB; i++)
+#pragma unroll
+    for (int j = 0; j < VT; j++) p[j] += v[VT * i + j];
+  const float mean = seg_tree_sum<LR>(p) / (float)COLS;
+#pragma unroll
+  for (int j = 0; j < VT; j++) p[j] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NB; i++)
+#pragma unroll
+    for (int j = 0; j < VT; j++) {
+      const float d = v[VT * i + j] - mean;
+      p[j] += d * d;
+    }
+  const float r = 1.0f / sqrtf(seg_tree_sum<LR>(p) / (float)COLS + eps);
+  float* S = SH + rl * RS;
+#pragma unroll
+  for (int i = 0; i < NB; i++)
+#pragma unroll
+    for (int q = 0; q < VT / 4; q++) {
+      const int c = 256 * i + VT * l + 4 * q;
+      const float4 sc = *(const float4*)(MOD + scale_off + c);
+      const float4 sh = *(const float4*)(MOD + shift_off + c);
+      const float* t = v + VT * i + 4 * q;
+      *(float4*)(S + c + 4 * (c >> 6)) =
+          make_float4((t[0] - mean) * r * (1.0f + sc.x) + sh.x, (t[1] - mean) * r * (1.0f + sc.y) + sh.y,
+                      (t[2] - mean) * r * (1.0f + sc.z) + sh.z, (t[3] - mean) * r * (1.0f + sc.w) + sh.w);
+    }
+  // (LDS operations of one wave complete in order: the row's lanes all belong to this wave)
+  float w[64];
+#pragma unroll
+  for (int q = 0; q < 16; q++) {
+    const float4 t = *(const float4*)(S + 68 * l + 4 * q);
+    w[4 * q] = t.x;
+    w[4 * q + 1] = t.y;
+    w[4 * q + 2] = t.z;
+    w[4 * q + 3] = t.w;
+  }
+  if (rotate) hadamard64_quad(w, l & 3);
+  if (Y) {
+    float* y = Y + row * COLS + 64 * l;
+#pragma unroll
+    for (int q = 0; q < 16; q++) *(float4*)(y + 4 * q) = make_float4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+  }
+  if (Q) {
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 64; i++) am = fmaxf(am, fabsf(w[i]));
+    am = rows_max<LR>(am, nullptr);
+    if (l == 0) S_out[row] = am / 127.0f;
+    quant64_store(w, am, Q + row * COLS + 64 * l);
+  }
+}
+
 __global__ __launch_bounds__(256) void elementwise_kernel(int op, const float* A, const float* B, float* Y, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
     const float a = A ? A[i] : 0.0f;
@@ -627,7 +732,14 @@ int layernorm_mod_launch(anima_ctx* c, const float* x, const float* mod, int64_t
   Launch lc(c, q ? "layernorm_mod_rot_quant" : (rotate ? "layernorm_mod_rot" : "layernorm_mod"), 0.0, bytes);
   const bool vec = cols <= 2048 && !((uintptr_t)x & 15) && !((uintptr_t)(mod + shift_off) & 15) &&
                    !((uintptr_t)(mod + scale_off) & 15) && !((uintptr_t)y & 15);
-  if (vec) {  // float4 rows: one wave per row
+  if (vec && (cols == 1024 || cols == 2048) && !((uintptr_t)q & 15)) {  // register rows, one LDS round trip
+    if (cols == 2048)
+      hipLaunchKernelGGL(layernorm_mod_reg_kernel<32>, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, c->stream, x, mod,
+                         shift_off, scale_off, rows, eps, rotate, y, q, s);
+    else
+      hipLaunchKernelGGL(layernorm_mod_reg_kernel<16>, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, c->stream, x, mod,
+                         shift_off, scale_off, rows, eps, rotate, y, q, s);
+  } else if (vec) {  // float4 rows: one wave per row
     hipLaunchKernelGGL(layernorm_mod_wave_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256),
                        (size_t)4 * padded_cols(cols) * 4, c->stream, x, mod, shift_off, scale_off, rows, cols, eps, rotate, y,
                        q, s);
