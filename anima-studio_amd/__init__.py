@@ -20,7 +20,7 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "anima.h")
 ANIMA_OK = 0
 PREC_BF16 = 0
 PREC_FP32 = 1
-W_BF16, W_I8, W_W4, W_F32 = 0, 1, 2, 3
+W_BF16, W_I8, W_W4, W_F32, W_F32S3 = 0, 1, 2, 3, 4
 ACT = {"none": 0, "gelu": 1, "silu": 2}
 EPI_STORE, EPI_RESID, EPI_GATED = 0, 1, 2
 EW = {"silu_mul": 0, "add": 1, "silu": 2, "copy": 3}
@@ -114,6 +114,7 @@ def lib():
         L.anima_unpatchify.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]
         L.anima_linear.argtypes = [_vp, ctypes.POINTER(LinearDesc)]
         L.anima_sampler_step.argtypes = [_vp, ctypes.POINTER(SamplerDesc)]
+        L.anima_split3_bf16.argtypes = [_vp, _vp, _vp, _i64]
         _LIB = L
     return _LIB
 
@@ -281,6 +282,9 @@ class Context:
                        epilogue=epilogue, gate=_ptr(gate), gate_off=gate_off, acc_out=_ptr(acc_out), add=_ptr(add),
                        ld_add=ld_add)
         return self._check(lib().anima_linear(self.h, ctypes.byref(d)))
+
+    def split3_bf16(self, src, dst, n):
+        return self._check(lib().anima_split3_bf16(self.h, _ptr(src), _ptr(dst), n))
 
     def sampler_step(self, kind, n, x, v, *, v_uncond=None, cfg=1.0, sigma, final_step=False, stage=0, den_out=None,
                      old=None, old_d=None, eps=None, c=()):

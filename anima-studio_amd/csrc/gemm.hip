@@ -610,8 +610,9 @@ __global__ __launch_bounds__(256) void gemm_f32m_kernel(F32WArgs a) {
     if (k0 + 32 <= a.K) {
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const float4 t = mok ? *(const float4*)(xr + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        const float4 u = nok ? *(const float4*)(wr + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float4 t0 = *(const float4*)(xr + k0 + 4 * j), u0 = *(const float4*)(wr + k0 + 4 * j);
+        const float4 t = mok ? t0 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float4 u = nok ? u0 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         xv[4 * j] = t.x; xv[4 * j + 1] = t.y; xv[4 * j + 2] = t.z; xv[4 * j + 3] = t.w;
         wv[4 * j] = u.x; wv[4 * j + 1] = u.y; wv[4 * j + 2] = u.z; wv[4 * j + 3] = u.w;
       }
@@ -685,8 +686,11 @@ __global__ __launch_bounds__(256) void gemm_f32m_t_kernel(F32WArgs a) {
     if (k0 + 32 <= a.K) {
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const float4 t = mok ? *(const float4*)(xr + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        const float4 u = nok ? ld_w4<BF>(a.w, wr + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        // unconditional in-bounds loads (rows clamped), then selects: no branch per load
+        const float4 t0 = *(const float4*)(xr + k0 + 4 * j);
+        const float4 u0 = ld_w4<BF>(a.w, wr + k0 + 4 * j);
+        const float4 t = mok ? t0 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float4 u = nok ? u0 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         xv[4 * j] = t.x; xv[4 * j + 1] = t.y; xv[4 * j + 2] = t.z; xv[4 * j + 3] = t.w;
         wv[4 * j] = u.x; wv[4 * j + 1] = u.y; wv[4 * j + 2] = u.z; wv[4 * j + 3] = u.w;
       }
@@ -761,9 +765,20 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_f32m_skinny_kernel(F32WArg
     if (k0 + 32 <= a.K) {
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        xv[j] = mok ? *(const float4*)(xr + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if constexpr (RT <= 3) {  // unconditional in-bounds loads (rows clamped), then selects
+          const float4 x0 = *(const float4*)(xr + k0 + 4 * j);
+          xv[j] = mok ? x0 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (int t = 0; t < RT; t++) wv[t][j] = nok[t] ? ld_w4<BF>(a.w, wr[t] + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          for (int t = 0; t < RT; t++) {
+            const float4 w0 = ld_w4<BF>(a.w, wr[t] + k0 + 4 * j);
+            wv[t][j] = nok[t] ? w0 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          }
+        } else {  // (the temporaries of the select form would not fit in registers)
+          xv[j] = mok ? *(const float4*)(xr + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+          for (int t = 0; t < RT; t++)
+            wv[t][j] = nok[t] ? ld_w4<BF>(a.w, wr[t] + k0 + 4 * j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
       }
     } else {  // the last, partial k-tile
       float xs[16], ws[RT][16];
@@ -850,6 +865,234 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_f32m_skinny_kernel(F32WArg
   }
 }
 
+// ------------------------------------------------------------------ split-bf16 products
+//
+// ANIMA_W_F32S3: an fp32 matrix stored as three bf16 planes w0 + w1 + w2 (each the bf16 rounding of
+// what the previous planes leave; the differences are exact in fp32, so |w - w0 - w1 - w2| <=
+// 2^-24 |w|).  The activations are split the same way in registers, and x.w = sum_{i+j<=2} x_i w_j
+// (the dropped terms are below 2^-24 of the product) runs as six v_mfma_f32_32x32x16_bf16 per
+// 16-k slice with fp32 accumulation: fp32-level accuracy at about a third of the fp32 matrix-core
+// time.  Both operands of one MFMA hold k = 8h .. 8h + 7 in lane half h, so the k order is the same
+// on both sides.  Output layouts and epilogues are those of the fp32 kernels.
+
+// three bf16 pieces of 8 fp32 values, two at a time (packed round-to-nearest-even conversions;
+// bf16 -> fp32 is exact, so each remainder is exact)
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split3_pair(f32x2_t v, bf16x2_t& h, bf16x2_t& m, bf16x2_t& l) {
+  h = __builtin_convertvector(v, bf16x2_t);
+  const f32x2_t r = v - __builtin_convertvector(h, f32x2_t);
+  m = __builtin_convertvector(r, bf16x2_t);
+  l = __builtin_convertvector(r - __builtin_convertvector(m, f32x2_t), bf16x2_t);
+}
+__device__ __forceinline__ void split3(float4 a, float4 b, bf16x8 (&o)[3]) {
+  bf16x2_t h0, m0, l0, h1, m1, l1, h2, m2, l2, h3, m3, l3;
+  split3_pair(f32x2_t{a.x, a.y}, h0, m0, l0);
+  split3_pair(f32x2_t{a.z, a.w}, h1, m1, l1);
+  split3_pair(f32x2_t{b.x, b.y}, h2, m2, l2);
+  split3_pair(f32x2_t{b.z, b.w}, h3, m3, l3);
+  o[0] = bf16x8{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+  o[1] = bf16x8{m0[0], m0[1], m1[0], m1[1], m2[0], m2[1], m3[0], m3[1]};
+  o[2] = bf16x8{l0[0], l0[1], l1[0], l1[1], l2[0], l2[1], l3[0], l3[1]};
+}
+
+// acc += sum_{i+j<=2} a_i b_j, smallest terms first
+__device__ __forceinline__ f32x16 mfma_s3(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f32x16 acc) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 ld_bf8(const uint16_t* p) {
+  const uint4 u = *(const uint4*)p;
+  bf16x8 r;
+  __builtin_memcpy(&r, &u, 16);
+  return r;
+}
+
+// Tall-skinny split product (the stacked LoRA A side, N <= 256, long K): the structure of
+// gemm_f32m_skinny_kernel (32 rows x 32 RT columns, eight waves over the k-slices, fixed-order
+// LDS tree), one 16-k slice per step.
+template <int RT>
+__global__ __launch_bounds__(64 * SK_WAVES) void gemm_s3_skinny_kernel(F32WArgs a) {
+  __shared__ float part[SK_WAVES / 2 * 64 * 16 * RT];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lq = lane & 31, hf = lane >> 5;
+  const int m0 = blockIdx.y * 32, nb = blockIdx.x * 32 * RT;
+  const int m = m0 + lq;
+  const bool mok = m < a.M;
+  const float* xr = a.x + (int64_t)(mok ? m : 0) * a.ldx + 8 * hf;
+  const uint16_t* W = (const uint16_t*)a.w;
+  const int64_t plane = (int64_t)a.N * a.K;
+  int64_t wr[RT];
+  bool nok[RT];
+#pragma unroll
+  for (int t = 0; t < RT; t++) {
+    const int n = nb + 32 * t + lq;
+    nok[t] = n < a.N;
+    wr[t] = (int64_t)(nok[t] ? n : 0) * a.K + 8 * hf;
+  }
+  f32x16 acc[RT];
+#pragma unroll
+  for (int t = 0; t < RT; t++) acc[t] = f32x16{};
+  const int nsl = (a.K + 15) / 16;
+  const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  const bf16x8 z8 = {};
+  // one 16-k slice per step, the next slice's loads issued before this slice's MFMAs
+#define S3_LOAD(SL, X0, X1, WV)                                                                  \
+  {                                                                                              \
+    const int k0_ = 16 * (SL);                                                                   \
+    const bool kok_ = k0_ + 8 * hf < a.K; /* K % 8 == 0: a lane's 8 values are all in or out */ \
+    const int kc_ = kok_ ? k0_ : 0;       /* unconditional in-bounds loads, then selects */     \
+    const float4 t0_ = *(const float4*)(xr + kc_), t1_ = *(const float4*)(xr + kc_ + 4);        \
+    X0 = mok && kok_ ? t0_ : z4;                                                                 \
+    X1 = mok && kok_ ? t1_ : z4;                                                                 \
+    _Pragma("unroll") for (int t = 0; t < RT; t++)                                               \
+    _Pragma("unroll") for (int p = 0; p < 3; p++) {                                              \
+      const bf16x8 u_ = ld_bf8(W + p * plane + wr[t] + kc_);                                     \
+      WV[t][p] = nok[t] && kok_ ? u_ : z8;                                                       \
+    }                                                                                            \
+  }
+#define S3_MMA(X0, X1, WV)                                                   \
+  {                                                                          \
+    bf16x8 xs_[3];                                                           \
+    split3(X0, X1, xs_);                                                     \
+    _Pragma("unroll") for (int t = 0; t < RT; t++) acc[t] = mfma_s3(xs_, WV[t], acc[t]); \
+  }
+  if (wave < nsl) {
+    float4 xa0, xa1, xb0, xb1;
+    bf16x8 wa[RT][3], wb[RT][3];
+    S3_LOAD(wave, xa0, xa1, wa)
+    for (int sl = wave;;) {
+      const bool more = sl + SK_WAVES < nsl;
+      if (more) S3_LOAD(sl + SK_WAVES, xb0, xb1, wb)
+      S3_MMA(xa0, xa1, wa)
+      if (!more) break;
+      sl += SK_WAVES;
+      const bool more2 = sl + SK_WAVES < nsl;
+      if (more2) S3_LOAD(sl + SK_WAVES, xa0, xa1, wa)
+      S3_MMA(xb0, xb1, wb)
+      if (!more2) break;
+      sl += SK_WAVES;
+    }
+  }
+#undef S3_LOAD
+#undef S3_MMA
+#pragma unroll
+  for (int h = SK_WAVES / 2; h >= 1; h >>= 1) {
+    if (wave >= h && wave < 2 * h) {
+#pragma unroll
+      for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) part[(((wave - h) * RT + t) * 64 + lane) * 16 + r] = acc[t][r];
+    }
+    __syncthreads();
+    if (wave < h) {
+#pragma unroll
+      for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = acc[t][r] + part[((wave * RT + t) * 64 + lane) * 16 + r];
+    }
+    __syncthreads();
+  }
+  if (wave > 0) return;
+#pragma unroll
+  for (int t = 0; t < RT; t++) {
+    if (!nok[t]) continue;
+    const int n = nb + 32 * t + lq;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int mm = m0 + 8 * (r >> 2) + 4 * hf + (r & 3);
+      if (mm >= a.M) continue;
+      float v = acc[t][r] * a.alpha;
+      if (a.bias) v = v + a.bias[n];
+      if (a.add) v = v + a.add[(int64_t)mm * a.ld_add + n];
+      v = apply_act(v, a.act);
+      float* c = a.out + (int64_t)mm * a.ldc + n;
+      if (a.epi == ANIMA_EPI_STORE) *c = v;
+      else if (a.epi == ANIMA_EPI_RESID) *c = *c + v;
+      else *c = __builtin_fmaf(a.gate[a.gate_off + n], v, *c);
+    }
+  }
+}
+
+// Split product with the operands swapped (the LoRA B side, K = rank): the C^T layout and 16-byte
+// epilogue of gemm_f32m_t_kernel.
+__global__ __launch_bounds__(256) void gemm_s3_t_kernel(F32WArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lq = lane & 31, hf = lane >> 5;
+  const int m0 = blockIdx.y * 64 + (wave & 1) * 32;
+  const int n0 = blockIdx.x * 64 + (wave >> 1) * 32;
+  const int m = m0 + lq, n = n0 + lq;
+  const bool mok = m < a.M, nok = n < a.N;
+  const float* xr = a.x + (int64_t)(mok ? m : 0) * a.ldx + 8 * hf;
+  const uint16_t* W = (const uint16_t*)a.w;
+  const int64_t plane = (int64_t)a.N * a.K, wr = (int64_t)(nok ? n : 0) * a.K + 8 * hf;
+  const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  const bf16x8 z8 = {};
+  f32x16 acc = {};
+  for (int k0 = 0; k0 < a.K; k0 += 32) {  // two 16-k slices per load round trip
+    float4 x[2][2];
+    bf16x8 wv[2][3], xs[3];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {  // unconditional in-bounds loads (clamped offsets), then selects
+      const int k = k0 + 16 * h;
+      const bool kok = k + 8 * hf < a.K;
+      const int kc = kok ? k : 0;
+      const float4 t0 = *(const float4*)(xr + kc), t1 = *(const float4*)(xr + kc + 4);
+      x[h][0] = mok && kok ? t0 : z4;
+      x[h][1] = mok && kok ? t1 : z4;
+#pragma unroll
+      for (int p = 0; p < 3; p++) {
+        const bf16x8 u = ld_bf8(W + p * plane + wr + kc);
+        wv[h][p] = nok && kok ? u : z8;
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      split3(x[h][0], x[h][1], xs);
+      acc = mfma_s3(wv[h], xs, acc);
+    }
+  }
+  if (!mok) return;
+  float* crow = a.out + (int64_t)m * a.ldc;
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    const int nbk = n0 + 8 * g + 4 * hf;
+    if (nbk >= a.N) continue;
+    f32x4 v = {acc[4 * g] * a.alpha, acc[4 * g + 1] * a.alpha, acc[4 * g + 2] * a.alpha, acc[4 * g + 3] * a.alpha};
+    if (a.bias) v = v + *(const f32x4*)(a.bias + nbk);
+    if (a.add) v = v + *(const f32x4*)(a.add + (int64_t)m * a.ld_add + nbk);
+    if (a.act != ANIMA_ACT_NONE) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[i] = apply_act(v[i], a.act);
+    }
+    f32x4* c = (f32x4*)(crow + nbk);
+    if (a.epi == ANIMA_EPI_STORE) {
+      *c = v;
+    } else if (a.epi == ANIMA_EPI_RESID) {
+      *c = *c + v;
+    } else {
+      const f32x4 gt = *(const f32x4*)(a.gate + a.gate_off + nbk);
+      const f32x4 o = *c;
+      f32x4 r;
+#pragma unroll
+      for (int i = 0; i < 4; i++) r[i] = __builtin_fmaf(gt[i], v[i], o[i]);
+      *c = r;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void split3_kernel(const float* src, uint16_t* dst, int64_t n8, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (int64_t)gridDim.x * 256) {
+    bf16x8 o[3];
+    split3(*(const float4*)(src + 8 * i), *(const float4*)(src + 8 * i + 4), o);
+#pragma unroll
+    for (int p = 0; p < 3; p++) __builtin_memcpy(dst + p * n + 8 * i, &o[p], 16);
+  }
+}
+
 // Small-M (M <= 8) bf16-weight GEMV: one wave per output column n, lanes stride K in 8-element
 // chunks, fp32 FMA, wave reduction (timestep / adaLN projections, M = 1).
 constexpr int GEMV_MAXM = 8;
@@ -923,6 +1166,29 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
   if (d->add && ld_add < N) return fail(c, ANIMA_E_ARG, "anima_linear: ld_add=%lld < N=%d", (long long)ld_add, N);
   if (M == 0) return ANIMA_OK;
 
+  if (W->kind == ANIMA_W_F32S3) {
+    if (!d->x) return fail(c, ANIMA_E_ARG, "anima_linear: split weights need fp32 x");
+    if (d->acc_out || d->xq) return fail(c, ANIMA_E_ARG, "anima_linear: acc_out / xq apply to i8/w4 weights only");
+    const int64_t ldx = d->ldx ? d->ldx : K;
+    if (ldx < K) return fail(c, ANIMA_E_ARG, "anima_linear: ldx < K");
+    if (K % 8 || ldx % 4 || !al(d->x, 16) || !al(W->w, 16))
+      return fail(c, ANIMA_E_ARG, "anima_linear: split weights need K %% 8 == 0, ldx %% 4 == 0, 16-byte aligned x and w");
+    F32WArgs f{d->x, ldx, W->w, W->bias, d->out, ldc, alpha, d->act, d->epilogue, d->gate, d->gate_off,
+               (int)M, N, K, 0, 0, 0, 0, d->add, ld_add, 0};
+    Launch L(c, "gemm.f32s3", 2.0 * M * N * K, 0.0);
+    const dim3 sk((unsigned)((N + 127) / 128), (unsigned)((M + 31) / 32)), blk(64 * SK_WAVES);
+    if (N <= 32 && K >= 512) hipLaunchKernelGGL(gemm_s3_skinny_kernel<1>, sk, blk, 0, c->stream, f);
+    else if (N <= 64 && K >= 512) hipLaunchKernelGGL(gemm_s3_skinny_kernel<2>, sk, blk, 0, c->stream, f);
+    else if (N <= 96 && K >= 512) hipLaunchKernelGGL(gemm_s3_skinny_kernel<3>, sk, blk, 0, c->stream, f);
+    else if (N <= 256 && K >= 512) hipLaunchKernelGGL(gemm_s3_skinny_kernel<4>, sk, blk, 0, c->stream, f);
+    else if (N % 4 == 0 && ldc % 4 == 0 && al(d->out, 16) && (!W->bias || al(W->bias, 16)) &&
+             (!d->add || (al(d->add, 16) && ld_add % 4 == 0)) &&
+             (d->epilogue != ANIMA_EPI_GATED || al(d->gate + d->gate_off, 16)))
+      hipLaunchKernelGGL(gemm_s3_t_kernel, dim3((N + 63) / 64, (unsigned)((M + 63) / 64)), dim3(256), 0, c->stream, f);
+    else
+      return fail(c, ANIMA_E_ARG, "anima_linear: split weights with N > 256 need N %% 4 == 0 and 16-byte aligned out / bias / add / gate rows");
+    return L.end();
+  }
   if (W->kind == ANIMA_W_BF16 || W->kind == ANIMA_W_F32) {
     const bool f32 = W->kind == ANIMA_W_F32;
     if (!d->x) return fail(c, ANIMA_E_ARG, "anima_linear: bf16/fp32 weights need fp32 x");
@@ -1057,4 +1323,16 @@ int linear_grouped_bf16_launch(anima_ctx* c, int G, int64_t M, int N, int K, con
   return L.end();
 }
 
+}  // namespace anima
+
+namespace anima {
+int split3_launch(anima_ctx* c, const float* src, uint16_t* dst, int64_t n) {
+  if (!src || !dst || n < 0 || n % 8) return fail(c, ANIMA_E_ARG, "anima_split3_bf16: n=%lld (n %% 8 == 0) or null pointer", (long long)n);
+  if (!al(src, 16) || !al(dst, 16)) return fail(c, ANIMA_E_ARG, "anima_split3_bf16: pointers must be 16-byte aligned");
+  if (n == 0) return ANIMA_OK;
+  Launch L(c, "split3", 0.0, (double)n * 10);
+  const int64_t n8 = n / 8, blocks = (n8 + 255) / 256;
+  hipLaunchKernelGGL(split3_kernel, dim3((unsigned)(blocks < 8192 ? blocks : 8192)), dim3(256), 0, c->stream, src, dst, n8, n);
+  return L.end();
+}
 }  // namespace anima

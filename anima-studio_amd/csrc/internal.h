@@ -85,6 +85,8 @@ int zero_launch(anima_ctx* c, float* y, int64_t n);
 // forward: src = latents, dst = patches; inverse: src = final-layer output, dst = latents
 int patchify_launch(anima_ctx* c, const float* src, float* dst, int B, int h, int w, bool inverse);
 
+int split3_launch(anima_ctx* c, const float* src, uint16_t* dst, int64_t n);
+
 // ---- kernel launchers (sampler.hip)
 int sampler_step_launch(anima_ctx* c, const anima_sampler_desc* d);
 int fill_random_launch(anima_ctx* c, void* dst, int64_t n, int kind, uint64_t seed, float lo, float hi);

@@ -405,6 +405,11 @@ int anima_unpatchify(anima_ctx* c, const float* o, int B, int h, int w, float* l
   return patchify_launch(c, o, latents, B, h, w, true);
 }
 
+int anima_split3_bf16(anima_ctx* c, const float* src, uint16_t* dst, int64_t n) {
+  CHECK_CTX(c);
+  return split3_launch(c, src, dst, n);
+}
+
 int anima_sampler_step(anima_ctx* c, const anima_sampler_desc* d) {
   CHECK_CTX(c);
   return sampler_step_launch(c, d);

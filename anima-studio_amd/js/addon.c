@@ -488,6 +488,15 @@ static napi_value js_linear(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* split3(ctx, src, dst, n) */
+static napi_value js_split3(napi_env env, napi_callback_info info) {
+  napi_value a[4];
+  get_args(env, info, 4, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_split3_bf16(c, (const float*)ptr(env, a[1]), (uint16_t*)ptr(env, a[2]), i64(env, a[3])));
+  return NULL;
+}
+
 /* samplerStep(ctx, {kind, n, x, v, vUncond, cfg, sigma, final, stage, den, old, oldD, eps, c: [10]}) */
 static napi_value js_sampler_step(napi_env env, napi_callback_info info) {
   napi_value a[2];
@@ -547,7 +556,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       FN("qkNormRope", js_qk_norm_rope), FN("rmsnorm", js_rmsnorm), FN("rope", js_rope),
       FN("hadamard", js_hadamard), FN("quantRows", js_quant_rows), FN("layernormMod", js_layernorm_mod),
       FN("elementwise", js_elementwise), FN("zero", js_zero), FN("patchify", js_patchify), FN("linearGroupedBf16", js_linear_grouped_bf16), FN("unpatchify", js_unpatchify), FN("fillRandom", js_fill_random),
-      FN("linear", js_linear), FN("samplerStep", js_sampler_step), FN("lastError", js_last_error),
+      FN("linear", js_linear), FN("samplerStep", js_sampler_step), FN("split3", js_split3), FN("lastError", js_last_error),
   };
 #undef FN
   if (napi_define_properties(env, exports, sizeof desc / sizeof desc[0], desc) != napi_ok) return NULL;

@@ -12,7 +12,7 @@
 
 import { SafeTensors } from "./weights.mjs";
 import { native } from "./gpu.mjs";
-import { stackLora, releaseLoraStack } from "./ops.mjs";
+import { stackLora, releaseLoraStack, splitPlanes } from "./ops.mjs";
 
 const needsRotation = (W) => W.kind === "i8" || W.kind === "w4";
 const norm = (name) => name.replace(/\./g, "_");
@@ -147,8 +147,8 @@ export function destroyLora(L) {
 
 // Replaces every side path in the registries with the given [{ lora, strength }]
 // (app/lora.js:140-149).  A linear with several entries (q/k/v parts, stacked LoRAs) gets its A
-// matrices stacked on the device so that one product reads the shared input; attachLoras(regs, [])
-// releases the stacks.
+// matrices stacked on the device so that one product reads the shared input, and every matrix
+// gets its three bf16 planes for the split-product kernels; attachLoras(regs, []) releases both.
 let generation = 0;
 // Counts attachLoras calls: results cached across calls (timeCond) key on it.
 export function loraGeneration() {
@@ -161,13 +161,18 @@ export function attachLoras(regs, active) {
   for (const reg of [regs.dit, regs.te]) if (reg) for (const { W } of reg.values()) ws.add(W);
   for (const W of ws) {
     releaseLoraStack(W);
+    if (W.lora) for (const e of W.lora) if (e.owned) for (const t of e.owned) t.release();
     W.lora = [];
   }
   for (const { lora, strength } of active) {
     if (!strength) continue;
     for (const m of lora.modules) {
-      m.target.W.lora.push({ A: m.A, Ar: m.Ar, B: m.B, r: m.r, scale: strength * m.alphaScale, off: m.target.off,
-        n: m.target.n });
+      const gpu = m.A.gpu, K = m.target.W.K;
+      // bf16 planes of the matrices for the split-product kernels (freed on the next attach)
+      const As = splitPlanes(gpu, m.A, m.r * K), Ars = m.Ar ? splitPlanes(gpu, m.Ar, m.r * K) : null;
+      const Bs = m.r % 8 === 0 ? splitPlanes(gpu, m.B, m.target.n * m.r) : null;
+      m.target.W.lora.push({ A: m.A, Ar: m.Ar, B: m.B, As, Ars, Bs, owned: [As, Ars, Bs].filter((t) => t), r: m.r,
+        scale: strength * m.alphaScale, off: m.target.off, n: m.target.n });
     }
   }
   for (const W of ws) if (W.lora.length > 1) stackLora(W.lora[0].A.gpu, W);

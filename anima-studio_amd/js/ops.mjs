@@ -10,7 +10,7 @@
 
 import { native } from "./gpu.mjs";
 
-const KIND = { bf16: 0, i8: 1, w4: 2, f32: 3 };
+const KIND = { bf16: 0, i8: 1, w4: 2, f32: 3, f32s3: 4 };
 const ACT = { none: 0, gelu: 1, silu: 2 };
 const EW = { silu_mul: 0, add: 1, silu: 2, copy: 3 };
 const ptr = (t) => (t ? (typeof t === "number" ? t : t.buf) : 0);
@@ -87,18 +87,21 @@ export function linear(gpu, x, W, opts) {
 // reading x_in once.
 function loraInto(gpu, xin, W, M, out, ldc, storeFirst, rot) {
   const S = W.loraStack && W.loraStack.lora === W.lora ? W.loraStack : null;
+  // a matrix as a weight object: its three bf16 planes (kind f32s3, made by splitPlanes) when
+  // present, else the fp32 matrix
+  const mat = (f32, s3, N, K) => (s3 ? { kind: "f32s3", N, K, buf: s3 } : { kind: "f32", N, K, buf: f32 });
   const Aof = (e) => {
     if (rot && !e.Ar) throw new Error(`${W.name || "linear"}: LoRA entry without the rotated A for a rotated input`);
-    return rot ? e.Ar : e.A;
+    return rot ? mat(e.Ar, e.Ars, e.r, W.K) : mat(e.A, e.As, e.r, W.K);
   };
-  const down = S ? linear(gpu, xin, { kind: "f32", N: S.R, K: W.K, buf: rot ? S.Ar : S.A }, { M }) : null;
+  const down = S ? linear(gpu, xin, rot ? mat(S.Ar, S.Ars, S.R, W.K) : mat(S.A, S.As, S.R, W.K), { M }) : null;
   const covered = new Uint8Array(W.N);
   const isFull = (e) => e.off === 0 && e.n === W.N;
   const entries = W.lora.slice().sort((a, b) => isFull(b) - isFull(a));
   for (const e of entries) {
-    const t = S ? down.view(S.roff.get(e), [M, e.r]) : linear(gpu, xin, { kind: "f32", N: e.r, K: W.K, buf: Aof(e) }, { M });
+    const t = S ? down.view(S.roff.get(e), [M, e.r]) : linear(gpu, xin, Aof(e), { M });
     const store = storeFirst && covered[e.off] === 0;
-    linear(gpu, t, { kind: "f32", N: e.n, K: e.r, buf: e.B }, { M, ldx: S ? S.R : 0, out: out.view(e.off, [M, e.n]),
+    linear(gpu, t, mat(e.B, e.Bs, e.n, e.r), { M, ldx: S ? S.R : 0, out: out.view(e.off, [M, e.n]),
       ldc, alpha: e.scale, resid: !store });
     covered.fill(1, e.off, e.off + e.n);
     if (!S) t.release();
@@ -142,16 +145,25 @@ export function stackLora(gpu, W) {
     roff.set(e, r0);
     r0 += e.r;
   }
-  W.loraStack = { A: stack("A"), Ar: W.lora.every((e) => e.Ar) ? stack("Ar") : null, R, roff, lora: W.lora };
+  const A = stack("A"), Ar = W.lora.every((e) => e.Ar) ? stack("Ar") : null;
+  W.loraStack = { A, Ar, As: splitPlanes(gpu, A, R * W.K), Ars: Ar ? splitPlanes(gpu, Ar, R * W.K) : null, R, roff,
+    lora: W.lora };
   return W.loraStack;
 }
 
 export function releaseLoraStack(W) {
-  if (W.loraStack) {
-    W.loraStack.A.release();
-    if (W.loraStack.Ar) W.loraStack.Ar.release();
-  }
+  const S = W.loraStack;
+  if (S) for (const t of [S.A, S.Ar, S.As, S.Ars]) if (t) t.release();
   W.loraStack = null;
+}
+
+// The three bf16 planes of an fp32 matrix of n values (anima_split3_bf16, the f32s3 weight form),
+// or null when n % 8 != 0 (the fp32 kernels then take the matrix as it is).
+export function splitPlanes(gpu, t, n) {
+  if (n % 8) return null;
+  const p = gpu.empty([3 * n], "u16");
+  native.split3(gpu.ctx, t.buf || t, p.buf, n);
+  return p;
 }
 
 export function zero(gpu, t) {

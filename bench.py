@@ -83,7 +83,12 @@ def dit_step(args):
     if r.returncode != 0:
         raise RuntimeError("bench_dit.mjs failed: " + r.stderr[-2000:])
     d = json.loads(r.stdout.strip().splitlines()[-1])
+    # the same step with rank-32 LoRAs on every block linear (strength 1)
+    rl = subprocess.run(["node", js, "--steps", str(args.dit_steps), "--warmup", "1", "--lora-rank", "32"], cwd=ROOT,
+                        capture_output=True, text=True, timeout=600)
+    lora = json.loads(rl.stdout.strip().splitlines()[-1]) if rl.returncode == 0 else None
     return {"ms": d["dit_step_ms"], "tflops": d["tflops"], "finite": d["finite"],
+            "lora_rank32_ms": lora["dit_step_ms"] if lora else None,
             "config": "Anima DiT 28 blocks, 1024x1024 (4096 tokens), B=2 CFG, hidden 2048, 16x128 heads, MLP 8192, "
                       "self + cross attention to 512x1024 contexts, W4A8 mixed (blocks 0/27 int8), seeded random weights; "
                       "step = timeCond + forward through node bench_dit.mjs",

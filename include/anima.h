@@ -135,6 +135,11 @@ int anima_hadamard(anima_ctx* ctx, const float* x, float* y, int64_t n);
  * q[m,k] = clamp(rint(x_r[m,k] / s[m]), -127, 127).  K % 4 == 0, K <= 8192. */
 int anima_quant_rows(anima_ctx* ctx, const float* x, int64_t M, int K, int rotate, int8_t* q,
                      float* s);
+/* Splits fp32 src[n] into three bf16 planes dst[3][n]: dst0 = bf16(src), dst1 = bf16(src - dst0),
+ * dst2 = bf16(src - dst0 - dst1) (round to nearest even; each difference is exact in fp32), the
+ * ANIMA_W_F32S3 layout (no reference counterpart: the load-time form of the LoRA matrices of
+ * app/lora.js:103-134).  n % 8 == 0, 16-byte aligned pointers. */
+int anima_split3_bf16(anima_ctx* ctx, const float* src, uint16_t* dst, int64_t n);
 /* anima_quant_rows of act(x) (ANIMA_ACT_*, the epilogue activations of anima_linear, the same
  * functions): a linear that feeds a quantized linear can store its pre-activation output and
  * leave the activation to this pass (the MLP's GELU between mlp.layer1 and mlp.layer2,
@@ -230,6 +235,11 @@ int anima_fill_random(anima_ctx* ctx, void* dst, int64_t n, int kind, uint64_t s
                           s_channel [N] + codebook [16] (comfy_quant asym_w4a8_int8+convrot) */
 #define ANIMA_W_F32 3  /* fp32 [N][K]; fp32 activations, fp32 accumulation: the LoRA A / B matrices
                           of app/lora.js:103-134, run by ops.js:70-87 as kind "f32" */
+#define ANIMA_W_F32S3 4 /* an fp32 [N][K] matrix as three bf16 planes [3][N][K] (anima_split3_bf16:
+                           w = w0 + w1 + w2 to within 2^-24 |w|); the product runs on the bf16 matrix
+                           cores as sum_{i+j<=2} x_i w_j with x split the same way on the fly, fp32
+                           accumulation: fp32-level accuracy (not bit-identical to ANIMA_W_F32) at
+                           ~1/3 of the fp32 matrix-core time.  K % 8 == 0.  The same LoRA matrices. */
 #define ANIMA_ACT_NONE 0
 #define ANIMA_ACT_GELU 1 /* erf GELU (kernels.js:9-20) */
 #define ANIMA_ACT_SILU 2

@@ -436,6 +436,78 @@ def test_f32_tall_skinny(ctx, N, K, M):
     assert report("0.75 x A^T + b", t.numpy(), ref)[0] < 1e-6
 
 
+def split3_host(a):
+    """The three bf16 planes of anima_split3_bf16, restated: each plane is the round-to-nearest-
+    even bf16 of what the previous planes leave (the differences are exact in fp32)."""
+    a = np.asarray(a, np.float32)
+    h = orc.bf16_round(a)
+    r = (a - h).astype(np.float32)
+    m = orc.bf16_round(r)
+    l_ = orc.bf16_round((r - m).astype(np.float32))
+    return [h, m, l_]
+
+
+def bits16(a):
+    return (np.asarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def test_split3_planes(ctx):
+    """anima_split3_bf16: every plane bit-exact against the restatement; the three planes sum to
+    the fp32 input within 2^-24 relative (and exactly for values with <= 24 significant bits)."""
+    case("split3 bf16 planes")
+    n = 8 * 12345
+    x = (orc.randn(161, n) * np.exp(orc.randn(162, n))).astype(np.float32)
+    x[:8] = [0.0, -0.0, 1.0, -3.5, 1e-30, 3.0e38, 2 ** -20, 1.0 + 2 ** -23]
+    dst = ctx.empty((3, n), np.uint16)
+    ctx.split3_bf16(ctx.upload(x), dst, n)
+    got = dst.numpy()
+    ref = split3_host(x)
+    for p in range(3):
+        assert np.array_equal(got[p], bits16(ref[p])), p
+    tot = sum(r.astype(np.float64) for r in ref)
+    assert np.all(np.abs(tot - x) <= 2.0 ** -24 * np.abs(x.astype(np.float64)) + 1e-45)
+    with pytest.raises(amd().AnimaError):
+        ctx.split3_bf16(ctx.upload(x), dst, 12)
+
+
+@pytest.mark.parametrize("N,K,M,epi", [(32, 2048, 257, "store"), (96, 2048, 300, "store"), (200, 1040, 45, "store"),
+                                      (2048, 32, 300, "resid"), (2048, 8, 97, "gated"), (516, 24, 64, "store")])
+def test_split3_linears(ctx, N, K, M, epi):
+    """ANIMA_W_F32S3 (fp32 matrices as three bf16 planes, products split the same way on the
+    bf16 matrix cores): the tall-skinny LoRA-A shapes (partial k-slices, ragged N) and the
+    swapped-operand LoRA-B shapes (K = rank 32 / 8 / 24, store / residual into a wider output /
+    gated) within 1e-6 of float64, as the fp32 kernels."""
+    case(f"split3 linear N={N} K={K} M={M} {epi}")
+    m = amd()
+    ldx = K + 8
+    x = orc.randn(171, M * ldx).reshape(M, ldx)
+    w = (0.05 * orc.randn(172, N * K)).reshape(N, K).astype(np.float32)
+    dw = ctx.empty((3, N, K), np.uint16)
+    ctx.split3_bf16(ctx.upload(w), dw, N * K)
+    W = m.weight(m.W_F32S3, N, K, dw)
+    ref = 0.5 * (x[:, :K].astype(np.float64) @ w.T.astype(np.float64))
+    ldc = N + 12
+    base = orc.randn(173, M * ldc).reshape(M, ldc)
+    gate = orc.randn(174, N).astype(np.float32)
+    dout = ctx.upload(base)
+    kw = dict(x=ctx.upload(x), ldx=ldx, ldc=ldc, alpha=0.5)
+    if epi == "resid":
+        kw["epilogue"] = m.EPI_RESID
+    elif epi == "gated":
+        kw.update(epilogue=m.EPI_GATED, gate=ctx.upload(gate))
+    ctx.linear(W, M, dout, **kw)
+    want = base.astype(np.float64)
+    if epi == "store":
+        want[:, :N] = ref
+    elif epi == "resid":
+        want[:, :N] += ref
+    else:
+        want[:, :N] += gate.astype(np.float64) * ref
+    got = dout.numpy()
+    assert np.array_equal(got[:, N:], base[:, N:])
+    assert report(f"split3 {epi}", got[:, :N], want[:, :N])[0] < 1e-6
+
+
 def test_grouped_bf16_gemv(ctx):
     """G products in one launch (the adaLN modulation stage of timeCond): every group bit-exact
     against its own anima_linear GEMV call with the same bias, and within 1e-6 of float64."""
