@@ -50,6 +50,7 @@ class AttnDesc(ctypes.Structure):
         ("q_norm", _vp), ("k_norm", _vp), ("rope_cs", _vp), ("rope_sin_off", _i64),
         ("eps", ctypes.c_float),
         ("causal", ctypes.c_int),
+        ("kv_prep", _vp),
     ]
 
 
@@ -98,6 +99,9 @@ def lib():
         L.anima_profile_report.argtypes = [_vp, ctypes.c_char_p, ctypes.c_size_t]
         L.anima_timer_stop.argtypes = [_vp, P(ctypes.c_float)]
         L.anima_attention.argtypes = [_vp, P(AttnDesc)]
+        L.anima_attention_prepare_kv.argtypes = [_vp, P(AttnDesc), _vp]
+        L.anima_attention_kv_bytes.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.anima_attention_kv_bytes.restype = _i64
         L.anima_qk_norm_rope.argtypes = [_vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _i64, _vp, _vp, _vp, _i64, ctypes.c_float]
         L.anima_rmsnorm.argtypes = [_vp, _vp, _vp, _vp, _i64, ctypes.c_int, ctypes.c_float]
         L.anima_rope.argtypes = [_vp, _vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _i64, _i64, _i64]
@@ -230,7 +234,9 @@ class Context:
     def attention(self, *, q, k, v, o, B, Lq, Lk, H, D, ldq, ldk, ldv, ldo=None, q_off=0, k_off=0, v_off=0,
                   o_off=0, q_bstride=None, k_bstride=None, v_bstride=None, o_bstride=None, group=1, scale=0.0,
                   kv_len=None, precision=PREC_BF16, q_norm=None, k_norm=None, rope_cs=None, rope_sin_off=0,
-                  eps=1e-6, causal=0):
+                  eps=1e-6, causal=0, kv_prep=None, prepare_into=None):
+        """anima_attention; kv_prep: K/V converted by a call with prepare_into (which runs
+        anima_attention_prepare_kv into that buffer instead of the attention)."""
         ldo = ldo if ldo is not None else H * D
         kl = (ctypes.c_int * B)(*[int(x) for x in kv_len]) if kv_len is not None else None
         d = AttnDesc(B=B, Lq=Lq, Lk=Lk, H=H, D=D, group=group,
@@ -240,8 +246,14 @@ class Context:
                      o=_ptr(o), ldo=ldo, o_off=o_off, o_bstride=o_bstride if o_bstride is not None else Lq * ldo,
                      scale=scale, kv_len=ctypes.cast(kl, ctypes.POINTER(ctypes.c_int)) if kl is not None else None,
                      precision=precision, q_norm=_ptr(q_norm), k_norm=_ptr(k_norm), rope_cs=_ptr(rope_cs),
-                     rope_sin_off=rope_sin_off, eps=eps, causal=causal)
+                     rope_sin_off=rope_sin_off, eps=eps, causal=causal, kv_prep=_ptr(kv_prep))
+        if prepare_into is not None:
+            return self._check(lib().anima_attention_prepare_kv(self.h, ctypes.byref(d), _ptr(prepare_into)))
         return self._check(lib().anima_attention(self.h, ctypes.byref(d)))
+
+    @staticmethod
+    def attention_kv_bytes(B, Hkv, Lk, precision=PREC_BF16):
+        return lib().anima_attention_kv_bytes(B, Hkv, Lk, precision)
 
     def hadamard(self, x, y, n):
         return self._check(lib().anima_hadamard(self.h, _ptr(x), _ptr(y), n))

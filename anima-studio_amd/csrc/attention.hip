@@ -936,14 +936,16 @@ __global__ __launch_bounds__(256) void attn_flash_fp32(FlashArgs a) {
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
+// Argument checks of anima_attention (fills kv_len[] with the valid key counts).
+static int attention_check(anima_ctx* c, const anima_attn_desc* d, int (&kv_len)[MAXB]) {
   const int group = d->group <= 0 ? 1 : d->group;
   if (d->causal) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: causal attention is not on the DiT path (only the chunked text-encoder path of ops.js:177-207 uses it)");
   if (d->D != HD) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: head dim %d (this build implements D=128, the DiT head size)", d->D);
   if (d->B < 1 || d->B > MAXB) return fail(c, ANIMA_E_ARG, "anima_attention: B=%d outside [1,%d]", d->B, MAXB);
   if (d->Lq < 1 || d->Lk < 1 || d->H < 1) return fail(c, ANIMA_E_ARG, "anima_attention: Lq=%d Lk=%d H=%d must be >= 1", d->Lq, d->Lk, d->H);
   if (d->H % group) return fail(c, ANIMA_E_ARG, "anima_attention: H=%d not a multiple of group=%d", d->H, group);
-  if (!d->q || !d->k || !d->v || !d->o) return fail(c, ANIMA_E_ARG, "anima_attention: null q/k/v/o");
+  const bool prepared = d->kv_prep != nullptr;
+  if (!d->q || !d->o || (!prepared && (!d->k || !d->v))) return fail(c, ANIMA_E_ARG, "anima_attention: null q/k/v/o");
   if (d->precision != ANIMA_PREC_BF16 && d->precision != ANIMA_PREC_FP32)
     return fail(c, ANIMA_E_ARG, "anima_attention: unknown precision %d", d->precision);
   const int64_t lds[4] = {d->ldq, d->ldk, d->ldv, d->ldo};
@@ -952,6 +954,7 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
   const char* nm[4] = {"q", "k", "v", "o"};
   const int heads[4] = {d->H, d->H / group, d->H / group, d->H};
   for (int i = 0; i < 4; i++) {
+    if (prepared && (i == 1 || i == 2)) continue;  // K / V come converted
     if (lds[i] % 4 || offs[i] % 4 || bss[i] % 4 || lds[i] < 0 || offs[i] < 0 || bss[i] < 0)
       return fail(c, ANIMA_E_ARG, "anima_attention: %s ld/off/bstride (%lld/%lld/%lld) must be non-negative multiples of 4 (vec4 rows, as ops.js:169)",
                   nm[i], (long long)lds[i], (long long)offs[i], (long long)bss[i]);
@@ -959,10 +962,10 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
       return fail(c, ANIMA_E_ARG, "anima_attention: %s rows of %lld elements cannot hold off %lld + %d heads x %d", nm[i],
                   (long long)lds[i], (long long)offs[i], heads[i], HD);
   }
-  if (!al16(d->q) || !al16(d->k) || !al16(d->v) || !al16(d->o)) return fail(c, ANIMA_E_ARG, "anima_attention: q/k/v/o must be 16-byte aligned");
+  if (!al16(d->q) || !al16(d->o) || (!prepared && (!al16(d->k) || !al16(d->v))) || (prepared && !al16(d->kv_prep)))
+    return fail(c, ANIMA_E_ARG, "anima_attention: q/k/v/o (or kv_prep) must be 16-byte aligned");
   if ((d->q_norm && !al16(d->q_norm)) || (d->k_norm && !al16(d->k_norm)))
     return fail(c, ANIMA_E_ARG, "anima_attention: q_norm/k_norm must be 16-byte aligned");
-  int kv_len[MAXB];
   for (int b = 0; b < d->B; b++) {
     kv_len[b] = d->kv_len ? d->kv_len[b] : d->Lk;
     if (kv_len[b] < 1 || kv_len[b] > d->Lk) return fail(c, ANIMA_E_ARG, "anima_attention: kv_len[%d]=%d outside [1, Lk=%d]", b, kv_len[b], d->Lk);
@@ -975,17 +978,19 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
                   (long long)d->rope_sin_off, HD / 2, d->Lq > d->Lk ? d->Lq : d->Lk);
     if (!al16(d->rope_cs)) return fail(c, ANIMA_E_ARG, "anima_attention: rope_cs must be 16-byte aligned");
   }
-  const float scale = d->scale != 0.0f ? d->scale : 1.0f / sqrtf((float)HD);
-  const float eps = d->eps;
+  return ANIMA_OK;
+}
+
+// The K/V prep of one attention call into dst ([K plane][V^T plane], each B Hkv Lkp HD elements).
+static int prep_kv_launch(anima_ctx* c, const anima_attn_desc* d, void* dst) {
+  const int group = d->group <= 0 ? 1 : d->group;
   const int Hkv = d->H / group;
   const int Lkp = (d->Lk + BK - 1) / BK * BK;
   const bool bf = d->precision == ANIMA_PREC_BF16;
-  const size_t esz = bf ? 2 : 4;
-  const size_t plane = (size_t)d->B * Hkv * Lkp * HD * esz;
-  void* ws = nullptr;
-  int rc = workspace(c, 2 * plane, &ws);
-  if (rc) return rc;
-
+  const bool rope = d->rope_cs != nullptr;
+  const float eps = d->eps;
+  const size_t plane = (size_t)d->B * Hkv * Lkp * HD * (bf ? 2 : 4);
+  int rc = ANIMA_OK;
   PrepArgs p;
   p.k = d->k + d->k_off;
   p.ldk = d->ldk;
@@ -993,8 +998,8 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
   p.v = d->v + d->v_off;
   p.ldv = d->ldv;
   p.v_bs = d->v_bstride;
-  p.kb = ws;
-  p.vt = (char*)ws + plane;
+  p.kb = dst;
+  p.vt = (char*)dst + plane;
   p.kn = d->k_norm;
   p.cs = d->rope_cs;
   p.sin_off = d->rope_sin_off;
@@ -1023,12 +1028,34 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
     if ((rc = L.end())) return rc;
   }
 
+  return ANIMA_OK;
+}
+
+int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
+  int kv_len[MAXB];
+  int rc = attention_check(c, d, kv_len);
+  if (rc) return rc;
+  const int group = d->group <= 0 ? 1 : d->group;
+  const bool rope = d->rope_cs != nullptr;
+  const float scale = d->scale != 0.0f ? d->scale : 1.0f / sqrtf((float)HD);
+  const float eps = d->eps;
+  const int Hkv = d->H / group;
+  const int Lkp = (d->Lk + BK - 1) / BK * BK;
+  const bool bf = d->precision == ANIMA_PREC_BF16;
+  const size_t esz = bf ? 2 : 4;
+  const size_t plane = (size_t)d->B * Hkv * Lkp * HD * esz;
+  void* ws = (void*)d->kv_prep;
+  if (!ws) {
+    if ((rc = workspace(c, 2 * plane, &ws))) return rc;
+    if ((rc = prep_kv_launch(c, d, ws))) return rc;
+  }
+
   FlashArgs f;
   f.q = d->q + d->q_off;
   f.ldq = d->ldq;
   f.q_bs = d->q_bstride;
-  f.kb = p.kb;
-  f.vt = p.vt;
+  f.kb = ws;
+  f.vt = (char*)ws + plane;
   f.o = d->o + d->o_off;
   f.ldo = d->ldo;
   f.o_bs = d->o_bstride;
@@ -1076,4 +1103,22 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
   return L.end();
 }
 
+}  // namespace anima
+
+namespace anima {
+int64_t attention_kv_bytes(int B, int Hkv, int Lk, int precision) {
+  if (B < 1 || Hkv < 1 || Lk < 1) return 0;
+  const int64_t Lkp = (Lk + BK - 1) / BK * BK;
+  return 2 * (int64_t)B * Hkv * Lkp * HD * (precision == ANIMA_PREC_BF16 ? 2 : 4);
+}
+
+int attention_prepare_kv_launch(anima_ctx* c, const anima_attn_desc* d, void* dst) {
+  if (!d || !dst) return fail(c, ANIMA_E_ARG, "anima_attention_prepare_kv: null descriptor or output");
+  if (d->kv_prep) return fail(c, ANIMA_E_ARG, "anima_attention_prepare_kv: desc->kv_prep must be NULL");
+  if (!al16(dst)) return fail(c, ANIMA_E_ARG, "anima_attention_prepare_kv: kv_prep must be 16-byte aligned");
+  int kv_len[MAXB];
+  int rc = attention_check(c, d, kv_len);  // the full call's checks (q / o included)
+  if (rc) return rc;
+  return prep_kv_launch(c, d, dst);
+}
 }  // namespace anima

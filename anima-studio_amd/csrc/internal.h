@@ -67,6 +67,8 @@ struct Launch {
 
 // ---- kernel launchers (attention.hip)
 int attention_launch(anima_ctx* c, const anima_attn_desc* d);
+int attention_prepare_kv_launch(anima_ctx* c, const anima_attn_desc* d, void* dst);
+int64_t attention_kv_bytes(int B, int Hkv, int Lk, int precision);
 
 // ---- kernel launchers (rowops.hip)
 int qk_norm_rope_launch(anima_ctx* c, float* qkv, int64_t L, int H, int D, int64_t ld,

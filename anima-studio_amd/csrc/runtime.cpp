@@ -347,6 +347,13 @@ int anima_attention(anima_ctx* c, const anima_attn_desc* d) {
   return attention_launch(c, d);
 }
 
+int anima_attention_prepare_kv(anima_ctx* c, const anima_attn_desc* d, void* kv_prep) {
+  CHECK_CTX(c);
+  return attention_prepare_kv_launch(c, d, kv_prep);
+}
+
+int64_t anima_attention_kv_bytes(int B, int Hkv, int Lk, int precision) { return attention_kv_bytes(B, Hkv, Lk, precision); }
+
 int anima_qk_norm_rope(anima_ctx* c, float* qkv, int64_t L, int H, int D, int64_t ld,
                        const float* qn, const float* kn, const float* cs, int64_t sin_off, float eps) {
   CHECK_CTX(c);

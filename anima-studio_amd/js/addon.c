@@ -299,6 +299,8 @@ static napi_value js_attention(napi_env env, napi_callback_info info) {
   d.rope_sin_off = (int64_t)pnum(env, o, "sinOff");
   d.eps = (float)pnum(env, o, "eps");
   d.causal = (int)pnum(env, o, "causal");
+  d.kv_prep = pptr(env, o, "kvPrep");
+  void* prepare_into = pptr(env, o, "prepareInto"); /* run anima_attention_prepare_kv into it */
   int kv[64];
   napi_value kvl = prop(env, o, "kvLen");
   if (!is_nullish(env, kvl)) {
@@ -315,8 +317,17 @@ static napi_value js_attention(napi_env env, napi_callback_info info) {
     }
     d.kv_len = kv;
   }
-  CHECK_RC(env, c, anima_attention(c, &d));
+  if (prepare_into) CHECK_RC(env, c, anima_attention_prepare_kv(c, &d, prepare_into));
+  else CHECK_RC(env, c, anima_attention(c, &d));
   return NULL;
+}
+
+/* attentionKvBytes(B, Hkv, Lk, precision) */
+static napi_value js_attention_kv_bytes(napi_env env, napi_callback_info info) {
+  napi_value a[4];
+  get_args(env, info, 4, a);
+  return make_num(env, (double)anima_attention_kv_bytes((int)num(env, a[0]), (int)num(env, a[1]), (int)num(env, a[2]),
+                                                        (int)num(env, a[3])));
 }
 
 /* qkNormRope(ctx, qkv, L, H, D, ld, qn, kn, cs, sinOff, eps) */
@@ -556,7 +567,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       FN("qkNormRope", js_qk_norm_rope), FN("rmsnorm", js_rmsnorm), FN("rope", js_rope),
       FN("hadamard", js_hadamard), FN("quantRows", js_quant_rows), FN("layernormMod", js_layernorm_mod),
       FN("elementwise", js_elementwise), FN("zero", js_zero), FN("patchify", js_patchify), FN("linearGroupedBf16", js_linear_grouped_bf16), FN("unpatchify", js_unpatchify), FN("fillRandom", js_fill_random),
-      FN("linear", js_linear), FN("samplerStep", js_sampler_step), FN("split3", js_split3), FN("lastError", js_last_error),
+      FN("linear", js_linear), FN("samplerStep", js_sampler_step), FN("attentionKvBytes", js_attention_kv_bytes), FN("split3", js_split3), FN("lastError", js_last_error),
   };
 #undef FN
   if (napi_define_properties(env, exports, sizeof desc / sizeof desc[0], desc) != napi_ok) return NULL;

@@ -233,18 +233,22 @@ export class AnimaDiT {
     });
     const quant = this.blocks.some((b) => ops.needsRotation(b.cross.k));
     const xq = quant ? ops.quantRows(gpu, ctx, CTX_DIM, true) : null;
+    // per block: k = RMSNorm(ctx Wk), v = ctx Wv, then converted once to the attention operand
+    // layout (bf16 K rows, bf16 V^T) and kept; the fp32 k / v are released
     const kv = this.blocks.map((b) => {
       const k = ops.linear(gpu, ctx, b.cross.k, xq ? { xq, M: B * Lk } : { M: B * Lk });
       ops.rmsnorm(gpu, k, b.cross.kn, HD, 1e-6, k);
       const v = ops.linear(gpu, ctx, b.cross.v, xq ? { xq, M: B * Lk } : { M: B * Lk });
-      return { k, v };
+      const prep = ops.attentionPrepareKV(gpu, { q: k, k, v, B, Lq: Lk, Lk, H: HEADS, D: HD, ldq: D, ldk: D, ldv: D });
+      releaseAll([k, v]);
+      return { prep };
     });
     if (xq) xq.release();
     return {
       ctx, kv, Lk, B,
       release() {
         ctx.release();
-        for (const e of kv) releaseAll([e.k, e.v]);
+        for (const e of kv) e.prep.release();
       },
     };
   }
@@ -304,8 +308,7 @@ export class AnimaDiT {
       const q = project(gpu, nf, b.cross.q, M);
       releaseNorm(nf);
       const kv = cond.kv[i];
-      a = ops.attention(gpu, { q, k: kv.k, v: kv.v, B, Lq: L, Lk: cond.Lk, H: HEADS, D: HD, ldq: D, ldk: D, ldv: D,
-        qNorm: b.cross.qn });
+      a = ops.attention(gpu, { q, kvPrep: kv.prep, B, Lq: L, Lk: cond.Lk, H: HEADS, D: HD, ldq: D, qNorm: b.cross.qn });
       q.release();
       ops.linear(gpu, a, b.cross.o, { M, out: x, resid: true, gate: m.cross, gOff: 2 * D });
       a.release();

@@ -215,13 +215,32 @@ export function elementwise(gpu, op, a, b, out) {
 // Multi-head attention (ops.js:166-208), fused flash path on the matrix cores.
 //  q: [Lq, ldq] with head h at column qOff + h*D; k, v: [Lk, ldk]/[Lk, ldv] with kv head
 //  h/group at kOff/vOff + (h/group)*D.  Output [B*Lq, H*D].
+// a.kvPrep: K/V converted beforehand by attentionPrepareKV (then a.k / a.v are not needed).
 export function attention(gpu, a) {
   const B = a.B || 1;
   const H = a.H, D = a.D;
   const o = a.out || gpu.empty([B * a.Lq, H * D]);
-  native.attention(gpu.ctx, {
+  native.attention(gpu.ctx, attnDesc(a, B, H, D, o, { kvPrep: ptr(a.kvPrep) }));
+  return o;
+}
+
+// The K/V half of attention on its own, into a new buffer for later attention(..., { kvPrep }):
+// keys and values that serve many calls (the per-prompt cross-attention K/V) are converted once.
+// a.q / a.out are still checked as for the full call (the query side is not computed).
+export function attentionPrepareKV(gpu, a) {
+  const B = a.B || 1;
+  const H = a.H, D = a.D;
+  const bytes = native.attentionKvBytes(B, H / (a.group || 1), a.Lk, a.precision === "fp32" ? 1 : 0);
+  const prep = gpu.empty([bytes], "u8");
+  const o = a.out || { buf: a.q.buf };
+  native.attention(gpu.ctx, attnDesc(a, B, H, D, o, { prepareInto: prep.buf }));
+  return prep;
+}
+
+function attnDesc(a, B, H, D, o, extra) {
+  return Object.assign({
     B, Lq: a.Lq, Lk: a.Lk, H, D, group: a.group || 1,
-    q: a.q.buf, k: a.k.buf, v: a.v.buf, o: o.buf,
+    q: a.q.buf, k: a.k ? a.k.buf : 0, v: a.v ? a.v.buf : 0, o: o.buf,
     ldq: a.ldq, ldk: a.ldk, ldv: a.ldv, ldo: a.ldo || H * D,
     qOff: a.qOff || 0, kOff: a.kOff || 0, vOff: a.vOff || 0, oOff: a.oOff || 0,
     qBatch: a.qBatch !== undefined ? a.qBatch : a.Lq * a.ldq,
@@ -231,8 +250,7 @@ export function attention(gpu, a) {
     scale: a.scale || 0, kvLen: a.kvLen || null, precision: a.precision === "fp32" ? 1 : 0,
     qNorm: ptr(a.qNorm), kNorm: ptr(a.kNorm), cs: ptr(a.cs), sinOff: a.cs ? a.cs.sinOff : 0, eps: 1e-6,
     causal: a.causal ? 1 : 0,
-  });
-  return o;
+  }, extra);
 }
 
 // VAE / text-encoder ops of the reference are outside the DiT attention path.

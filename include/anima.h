@@ -102,6 +102,9 @@ typedef struct {
   int64_t rope_sin_off;
   float eps;
   int causal; /* must be 0: the causal chunked path of the text encoder is not on this path */
+  /* Optional: K and V already converted by anima_attention_prepare_kv (same B, H / group, Lk and
+   * precision); then k, v, their strides, k_norm and the key side of rope_cs are not read. */
+  const void* kv_prep;
 } anima_attn_desc;
 
 /* ops.attention (app/gpu/ops.js:166-208) on the flash path (kernels.js:158-299), plus the fused
@@ -110,6 +113,13 @@ typedef struct {
  * q/k/v/o element (b, row, head h, dim d) lives at ptr[b*bstride + row*ld + off + h*D + d]
  * (kv head h/group for k and v). */
 int anima_attention(anima_ctx* ctx, const anima_attn_desc* desc);
+/* The K/V half of anima_attention on its own: K rows RMS-normalized (k_norm) and rotated (rope_cs)
+ * and V transposed, rounded to the MFMA operand type, written to kv_prep
+ * (anima_attention_kv_bytes(B, H / group, Lk, precision) bytes, 16-byte aligned) for later
+ * anima_attention calls with desc->kv_prep: keys and values that serve many calls (the per-prompt
+ * cross-attention K/V of app/models/dit.js:232-249) are converted once. */
+int anima_attention_prepare_kv(anima_ctx* ctx, const anima_attn_desc* desc, void* kv_prep);
+int64_t anima_attention_kv_bytes(int B, int Hkv, int Lk, int precision);
 
 /* ---------------------------------------------------------------- row ops */
 

@@ -170,6 +170,8 @@ def test_attention_constant_v_full_size(ctx):
 
 @pytest.mark.parametrize("precision", ["bf16", "fp32"])
 def test_cross_attention_masked(ctx, precision):
+    """Masked cross-attention against fp64 / the bf16 model; the same call on K/V prepared once
+    by anima_attention_prepare_kv is bit-identical."""
     case(f"cross-attention B=2 Lq=4096 Lk=512 kv_len mask {precision}")
     m = amd()
     B, Lq, Lk, H = 2, 4096, 512, 16
@@ -186,7 +188,16 @@ def test_cross_attention_masked(ctx, precision):
     ctx.attention(q=dq, k=dk, v=dv, o=do, B=B, Lq=Lq, Lk=Lk, H=H, D=HD, ldq=H * HD, ldk=H * HD, ldv=H * HD,
                   kv_len=kv_len, precision=prec, q_norm=dqn, k_norm=dkn)
     got = do.numpy()
-    for x in (dq, dk, dv, dqn, dkn, do):
+    # K/V converted once (anima_attention_prepare_kv) and reused: the same output, bit for bit
+    prep = ctx.empty(m.Context.attention_kv_bytes(B, H, Lk, prec), np.uint8)
+    common = dict(B=B, Lq=Lq, Lk=Lk, H=H, D=HD, ldq=H * HD, ldk=H * HD, ldv=H * HD, kv_len=kv_len, precision=prec,
+                  q_norm=dqn, k_norm=dkn)
+    ctx.attention(q=dq, k=dk, v=dv, o=do, prepare_into=prep, **common)
+    do2 = ctx.empty((B, Lq, H * HD))
+    for _ in range(2):
+        ctx.attention(q=dq, k=None, v=None, o=do2, kv_prep=prep, **common)
+        assert np.array_equal(do2.numpy(), got)
+    for x in (dq, dk, dv, dqn, dkn, do, do2, prep):
         x.release()
     rows = np.unique(np.concatenate([np.arange(0, 16), rng.choice(Lq, 48, replace=False), np.arange(Lq - 16, Lq)]))
     for b in range(B):
