@@ -119,6 +119,10 @@ def lib():
         L.anima_linear.argtypes = [_vp, ctypes.POINTER(LinearDesc)]
         L.anima_sampler_step.argtypes = [_vp, ctypes.POINTER(SamplerDesc)]
         L.anima_split3_bf16.argtypes = [_vp, _vp, _vp, _i64]
+        L.anima_graph_begin.argtypes = [_vp]
+        L.anima_graph_end.argtypes = [_vp, P(_vp)]
+        L.anima_graph_launch.argtypes = [_vp, _vp]
+        L.anima_graph_destroy.argtypes = [_vp, _vp]
         _LIB = L
     return _LIB
 
@@ -229,6 +233,23 @@ class Context:
         ms = ctypes.c_float()
         self._check(lib().anima_timer_stop(self.h, ctypes.byref(ms)))
         return ms.value
+
+    # ---- recorded submission (HIP graphs)
+    def graph_begin(self):
+        """Starts capturing this context's work (anima_graph_begin)."""
+        self._check(lib().anima_graph_begin(self.h))
+
+    def graph_end(self):
+        """Ends the capture and returns a replayable graph handle."""
+        g = _vp()
+        self._check(lib().anima_graph_end(self.h, ctypes.byref(g)))
+        return g.value
+
+    def graph_launch(self, g):
+        self._check(lib().anima_graph_launch(self.h, g))
+
+    def graph_destroy(self, g):
+        self._check(lib().anima_graph_destroy(self.h, g))
 
     # ---- ops
     def attention(self, *, q, k, v, o, B, Lq, Lk, H, D, ldq, ldk, ldv, ldo=None, q_off=0, k_off=0, v_off=0,

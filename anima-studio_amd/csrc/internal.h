@@ -6,6 +6,7 @@
 #include <cstdint>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "../../include/anima.h"
@@ -46,6 +47,20 @@ struct anima_ctx {
   // attention workspace (K in bf16/fp32, V transposed), grown on demand
   void* ws = nullptr;
   size_t ws_bytes = 0;
+  // stream capture (anima_graph_begin .. anima_graph_end): buffers freed while capturing are
+  // parked in cap_free, reused only by later allocations of the same capture, and owned by the
+  // graph at the end (its replays keep using them); cap_ws: the capture used the workspace
+  bool capturing = false;
+  bool cap_ws = false;
+  std::unordered_map<size_t, std::vector<void*>> cap_free;
+  std::unordered_set<anima_graph*> graphs;
+};
+
+// A captured, instantiated HIP graph and the device buffers only its replays use.
+struct anima_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  std::vector<std::pair<void*, size_t>> owned;
 };
 
 namespace anima {

@@ -42,6 +42,12 @@ int hip_fail(anima_ctx* c, hipError_t e, const char* what) {
 }
 
 int workspace(anima_ctx* c, size_t bytes, void** out) {
+  if (c->capturing) {
+    if (bytes > c->ws_bytes)
+      return fail(c, ANIMA_E_STATE, "workspace of %zu bytes needed while capturing a graph (%zu available): run the work once before capturing",
+                  bytes, c->ws_bytes);
+    c->cap_ws = true;
+  }
   if (bytes > c->ws_bytes) {
     if (c->ws) {
       hipError_t e = hipStreamSynchronize(c->stream);
@@ -77,7 +83,7 @@ static hipEvent_t take_event(anima_ctx* c) {
 }
 
 Launch::Launch(anima_ctx* ctx, const char* name, double flops, double bytes)
-    : c(ctx), rec{name, flops, bytes, nullptr, nullptr}, on(ctx->profiling) {
+    : c(ctx), rec{name, flops, bytes, nullptr, nullptr}, on(ctx->profiling && !ctx->capturing) {
   if (on) {
     rec.a = take_event(c);
     rec.b = take_event(c);
@@ -123,6 +129,37 @@ using namespace anima;
                                (c)->err.c_str());                                         \
   } while (0)
 
+#define NOT_CAPTURING(c, what)                                                                 \
+  do {                                                                                         \
+    if ((c)->capturing) return fail((c), ANIMA_E_STATE, "%s: not allowed while capturing a graph", what); \
+  } while (0)
+
+static void release_graph(anima_ctx* c, anima_graph* g, bool to_pool) {
+  if (g->exec) hipGraphExecDestroy(g->exec);
+  if (g->graph) hipGraphDestroy(g->graph);
+  for (auto& b : g->owned) {
+    if (to_pool) {
+      c->free_lists[b.second].push_back(b.first);
+      c->pooled += b.second;
+    } else {
+      hipFree(b.first);
+    }
+  }
+  delete g;
+}
+
+// Ends a failed capture: buffers parked for it go back to the pool.
+static void drop_capture(anima_ctx* c) {
+  for (auto& kv : c->cap_free)
+    for (void* p : kv.second) {
+      c->free_lists[kv.first].push_back(p);
+      c->pooled += kv.first;
+    }
+  c->cap_free.clear();
+  c->capturing = false;
+  c->cap_ws = false;
+}
+
 extern "C" {
 
 int anima_init(int device, anima_ctx** out) {
@@ -157,7 +194,15 @@ int anima_init(int device, anima_ctx** out) {
 int anima_destroy(anima_ctx* c) {
   if (!c) return ANIMA_OK;
   hipSetDevice(c->device);
+  if (c->capturing) {
+    hipGraph_t g = nullptr;
+    hipStreamEndCapture(c->stream, &g);
+    if (g) hipGraphDestroy(g);
+    drop_capture(c);
+  }
   hipStreamSynchronize(c->stream);
+  for (anima_graph* g : c->graphs) release_graph(c, g, false);
+  c->graphs.clear();
   for (auto& kv : c->free_lists)
     for (void* p : kv.second) hipFree(p);
   for (auto& kv : c->live) hipFree(kv.first);
@@ -178,6 +223,7 @@ const char* anima_last_error(const anima_ctx* c) { return c ? c->err.c_str() : g
 
 int anima_sync(anima_ctx* c) {
   CHECK_CTX(c);
+  NOT_CAPTURING(c, "anima_sync");
   hipError_t e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "anima_sync");
   e = hipGetLastError();
@@ -202,6 +248,15 @@ int anima_alloc(anima_ctx* c, size_t bytes, void** out) {
   CHECK_CTX(c);
   if (!out) return fail(c, ANIMA_E_ARG, "anima_alloc: out is NULL");
   size_t size = bucket(bytes);
+  if (c->capturing) {
+    auto ct = c->cap_free.find(size);
+    if (ct != c->cap_free.end() && !ct->second.empty()) {
+      *out = ct->second.back();
+      ct->second.pop_back();
+      c->live[*out] = size;
+      return ANIMA_OK;
+    }
+  }
   auto it = c->free_lists.find(size);
   if (it != c->free_lists.end() && !it->second.empty()) {
     *out = it->second.back();
@@ -212,6 +267,7 @@ int anima_alloc(anima_ctx* c, size_t bytes, void** out) {
   }
   void* p = nullptr;
   hipError_t e = hipMalloc(&p, size);
+  if (e != hipSuccess && c->capturing) return hip_fail(c, e, "anima_alloc (while capturing a graph)");
   if (e != hipSuccess) {
     // release parked buffers and retry once (the pool's trim)
     hipStreamSynchronize(c->stream);
@@ -238,6 +294,11 @@ int anima_free(anima_ctx* c, void* p) {
   if (!p) return ANIMA_OK;
   auto it = c->live.find(p);
   if (it == c->live.end()) return fail(c, ANIMA_E_ARG, "anima_free: %p was not allocated by this context (or freed twice)", p);
+  if (c->capturing) {  // reserved for the graph being captured
+    c->cap_free[it->second].push_back(p);
+    c->live.erase(it);
+    return ANIMA_OK;
+  }
   c->free_lists[it->second].push_back(p);
   c->pooled += it->second;
   c->live.erase(it);
@@ -246,6 +307,7 @@ int anima_free(anima_ctx* c, void* p) {
 
 int anima_pool_trim(anima_ctx* c) {
   CHECK_CTX(c);
+  NOT_CAPTURING(c, "anima_pool_trim");
   hipError_t e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "anima_pool_trim");
   for (auto& kv : c->free_lists)
@@ -260,6 +322,7 @@ int anima_pool_trim(anima_ctx* c) {
 
 int anima_h2d(anima_ctx* c, void* dst, const void* src, size_t bytes) {
   CHECK_CTX(c);
+  NOT_CAPTURING(c, "anima_h2d");
   if (bytes == 0) return ANIMA_OK;
   if (!dst || !src) return fail(c, ANIMA_E_ARG, "anima_h2d: null pointer");
   // pageable source: hipMemcpyAsync stages it before returning, so `src` may be reused
@@ -270,6 +333,7 @@ int anima_h2d(anima_ctx* c, void* dst, const void* src, size_t bytes) {
 
 int anima_d2h(anima_ctx* c, void* dst, const void* src, size_t bytes) {
   CHECK_CTX(c);
+  NOT_CAPTURING(c, "anima_d2h");
   if (bytes == 0) return ANIMA_OK;
   if (!dst || !src) return fail(c, ANIMA_E_ARG, "anima_d2h: null pointer");
   hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream);
@@ -295,6 +359,7 @@ int anima_profile_enable(anima_ctx* c, int on) {
 
 int anima_profile_reset(anima_ctx* c) {
   CHECK_CTX(c);
+  NOT_CAPTURING(c, "anima_profile_reset");
   hipError_t e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "anima_profile_reset");
   collect(c);
@@ -304,6 +369,7 @@ int anima_profile_reset(anima_ctx* c) {
 
 int anima_profile_report(anima_ctx* c, char* buf, size_t len) {
   CHECK_CTX(c);
+  NOT_CAPTURING(c, "anima_profile_report");
   if (!buf || len == 0) return fail(c, ANIMA_E_ARG, "anima_profile_report: empty buffer");
   hipError_t e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "anima_profile_report");
@@ -326,6 +392,7 @@ int anima_profile_report(anima_ctx* c, char* buf, size_t len) {
 
 int anima_timer_start(anima_ctx* c) {
   CHECK_CTX(c);
+  NOT_CAPTURING(c, "anima_timer_start");
   hipError_t e = hipEventRecord(c->t0, c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "anima_timer_start");
   return ANIMA_OK;
@@ -333,6 +400,7 @@ int anima_timer_start(anima_ctx* c) {
 
 int anima_timer_stop(anima_ctx* c, float* ms) {
   CHECK_CTX(c);
+  NOT_CAPTURING(c, "anima_timer_stop");
   if (!ms) return fail(c, ANIMA_E_ARG, "anima_timer_stop: ms is NULL");
   hipError_t e = hipEventRecord(c->t1, c->stream);
   if (e == hipSuccess) e = hipEventSynchronize(c->t1);
@@ -439,6 +507,72 @@ int anima_linear_grouped_bf16(anima_ctx* c, int G, int64_t M, int N, int K, cons
   CHECK_CTX(c);
   return linear_grouped_bf16_launch(c, G, M, N, K, x, ldx, x_gstride, w, w_gstride, bias, bias_gstride, out, ldc,
                                     out_gstride);
+}
+
+int anima_graph_begin(anima_ctx* c) {
+  CHECK_CTX(c);
+  NOT_CAPTURING(c, "anima_graph_begin");
+  hipError_t e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed);
+  if (e != hipSuccess) return hip_fail(c, e, "anima_graph_begin");
+  c->capturing = true;
+  c->cap_ws = false;
+  c->cap_free.clear();
+  return ANIMA_OK;
+}
+
+int anima_graph_end(anima_ctx* c, anima_graph** out) {
+  CHECK_CTX(c);
+  if (!out) return fail(c, ANIMA_E_ARG, "anima_graph_end: out is NULL");
+  *out = nullptr;
+  if (!c->capturing) return fail(c, ANIMA_E_STATE, "anima_graph_end: no capture in progress");
+  hipGraph_t graph = nullptr;
+  hipError_t e = hipStreamEndCapture(c->stream, &graph);
+  if (e != hipSuccess) {
+    if (graph) hipGraphDestroy(graph);
+    drop_capture(c);
+    return hip_fail(c, e, "anima_graph_end (capture)");
+  }
+  hipGraphExec_t exec = nullptr;
+  e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    hipGraphDestroy(graph);
+    drop_capture(c);
+    return hip_fail(c, e, "anima_graph_end (instantiate)");
+  }
+  anima_graph* g = new anima_graph();
+  g->graph = graph;
+  g->exec = exec;
+  for (auto& kv : c->cap_free)
+    for (void* p : kv.second) g->owned.emplace_back(p, kv.first);
+  c->cap_free.clear();
+  if (c->cap_ws && c->ws) {  // the replays use this workspace: the context takes a new one
+    g->owned.emplace_back(c->ws, c->ws_bytes);
+    c->ws = nullptr;
+    c->ws_bytes = 0;
+  }
+  c->capturing = false;
+  c->cap_ws = false;
+  c->graphs.insert(g);
+  *out = g;
+  return ANIMA_OK;
+}
+
+int anima_graph_launch(anima_ctx* c, anima_graph* g) {
+  CHECK_CTX(c);
+  NOT_CAPTURING(c, "anima_graph_launch");
+  if (!g || !c->graphs.count(g)) return fail(c, ANIMA_E_ARG, "anima_graph_launch: not a graph of this context");
+  hipError_t e = hipGraphLaunch(g->exec, c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "anima_graph_launch");
+  return ANIMA_OK;
+}
+
+int anima_graph_destroy(anima_ctx* c, anima_graph* g) {
+  if (!c) return fail(nullptr, ANIMA_E_ARG, "null context");
+  if (!g) return ANIMA_OK;
+  if (!c->graphs.count(g)) return fail(c, ANIMA_E_ARG, "anima_graph_destroy: not a graph of this context (or destroyed twice)");
+  c->graphs.erase(g);
+  release_graph(c, g, true);
+  return ANIMA_OK;
 }
 
 }  // extern "C"

@@ -556,6 +556,40 @@ static napi_value js_last_error(napi_env env, napi_callback_info info) {
   return s;
 }
 
+/* recorded submission: graph handles are host addresses passed as Numbers (< 2^53) */
+static napi_value js_graph_begin(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  CHECK_RC(env, c, anima_graph_begin(c));
+  return NULL;
+}
+
+static napi_value js_graph_end(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  anima_graph* g = NULL;
+  CHECK_RC(env, c, anima_graph_end(c, &g));
+  return make_num(env, (double)(uintptr_t)g);
+}
+
+static napi_value js_graph_launch(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  CHECK_RC(env, c, anima_graph_launch(c, (anima_graph*)ptr(env, argv[1])));
+  return NULL;
+}
+
+static napi_value js_graph_destroy(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  CHECK_RC(env, c, anima_graph_destroy(c, (anima_graph*)ptr(env, argv[1])));
+  return NULL;
+}
+
 static napi_value Init(napi_env env, napi_value exports) {
 #define FN(name, f) {name, NULL, f, NULL, NULL, NULL, napi_enumerable, NULL}
   napi_property_descriptor desc[] = {
@@ -568,6 +602,8 @@ static napi_value Init(napi_env env, napi_value exports) {
       FN("hadamard", js_hadamard), FN("quantRows", js_quant_rows), FN("layernormMod", js_layernorm_mod),
       FN("elementwise", js_elementwise), FN("zero", js_zero), FN("patchify", js_patchify), FN("linearGroupedBf16", js_linear_grouped_bf16), FN("unpatchify", js_unpatchify), FN("fillRandom", js_fill_random),
       FN("linear", js_linear), FN("samplerStep", js_sampler_step), FN("attentionKvBytes", js_attention_kv_bytes), FN("split3", js_split3), FN("lastError", js_last_error),
+      FN("graphBegin", js_graph_begin), FN("graphEnd", js_graph_end), FN("graphLaunch", js_graph_launch),
+      FN("graphDestroy", js_graph_destroy),
   };
 #undef FN
   if (napi_define_properties(env, exports, sizeof desc / sizeof desc[0], desc) != napi_ok) return NULL;

@@ -8,10 +8,13 @@
 //                     [--lora-rank R]   (seeded rank-R LoRAs on every block linear, strength 1)
 //                     [--generate N [--sampler euler_a] [--cfg 4]]  (also time an N-step sampling run:
 //                      the device loop of pipeline.mjs and the reference's host loop)
+//                     [--graph [--rounds 3]]  (also the forward replayed from a HIP graph recorded
+//                      once, ForwardGraph: graph and eager blocks of --steps steps alternate,
+//                      medians; dit_step_ms stays the eager step, graph_step_ms the replay)
 
 import { GPU, native } from "./gpu.mjs";
 import { SyntheticWeights } from "./weights.mjs";
-import { AnimaDiT } from "./dit.mjs";
+import { AnimaDiT, ForwardGraph } from "./dit.mjs";
 import { linearRegistry, attachLoras, rotatedA } from "./lora.mjs";
 import { LatentPipeline } from "./pipeline.mjs";
 
@@ -82,9 +85,28 @@ async function main() {
   await gpu.sync();
   process.stderr.write(`bench_dit: model ready (${nBlocks} blocks, ${mode}), ${(gpu.pool.allocated / 2 ** 30).toFixed(2)} GiB\n`);
 
-  const step = async () => {
+  const useGraph = !!arg("graph", false);
+  const rounds = Number(arg("rounds", 3));
+  let fg = null, latT = null;
+  const per = 16 * h * w, host = new Float32Array(B * per);
+  if (useGraph) {
+    latT = gpu.empty([B, 16, h, w]);
+    const tc0 = dit.timeCond(0.9);
+    fg = await ForwardGraph.capture(dit, latT, h, w, cond, tc0);
+    tc0.release();
+  }
+  // a step: timeCond, latents up, the forward, velocities back (dit.forward's host work)
+  const step = async (eager) => {
     const tc = dit.timeCond(0.9);
-    const v = await dit.forward(latents, h, w, cond, tc);
+    let v;
+    if (fg && !eager) {
+      latents.forEach((lat, b) => host.set(lat, b * per));
+      gpu.write(latT, host);
+      const o = await gpu.read(fg.run(tc));
+      v = latents.map((_, b) => o.slice(b * per, (b + 1) * per));
+    } else {
+      v = await dit.forward(latents, h, w, cond, tc);
+    }
     tc.release();
     return v;
   };
@@ -92,9 +114,27 @@ async function main() {
   for (let i = 0; i < warmup; i++) v = await step();
   await gpu.sync();
   if (gpu.profiler) gpu.profiler.reset();
-  gpu.timerStart();
-  for (let i = 0; i < steps; i++) v = await step();
-  const ms = gpu.timerStop() / steps;
+  const timed = async (eager) => {
+    gpu.timerStart();
+    for (let i = 0; i < steps; i++) v = await step(eager);
+    return gpu.timerStop() / steps;
+  };
+  const median = (xs) => xs.slice().sort((a, b) => a - b)[xs.length >> 1];
+  let ms, graphMs = null;
+  if (fg) {
+    // graph replays and eager forwards (launched kernel by kernel) in alternating blocks of
+    // `steps` steps; medians over the rounds
+    await step(true);
+    const g = [], e = [];
+    for (let r = 0; r < rounds; r++) {
+      g.push(await timed(false));
+      e.push(await timed(true));
+    }
+    graphMs = median(g);
+    ms = median(e);
+  } else {
+    ms = await timed(false);
+  }
   await gpu.sync();
   let finite = true;
   for (const x of v) for (let i = 0; i < x.length; i += 97) if (!Number.isFinite(x[i])) { finite = false; break; }
@@ -104,7 +144,8 @@ async function main() {
   const perBlock = 2 * M * D_(3 * 2048, 2048) + 2 * M * D_(2048, 2048) * 3 + 2 * M * D_(8192, 2048) * 2 +
     4 * B * L * L * 128 * 16 + 4 * B * L * Lk * 128 * 16;
   const flops = nBlocks * perBlock + 2 * M * 2048 * 68 + 2 * M * 64 * 2048;
-  const out = { dit_step_ms: Number(ms.toFixed(3)), size, blocks: nBlocks, mode, B, tokens: L, steps, warmup, lora_rank: loraRank,
+  const out = { dit_step_ms: Number(ms.toFixed(3)), size, blocks: nBlocks, mode, B, tokens: L, steps, warmup, lora_rank: loraRank, graph: useGraph,
+    graph_step_ms: graphMs === null ? null : Number(graphMs.toFixed(3)),
     flops_per_step: flops, tflops: Number((flops / (ms / 1e3) / 1e12).toFixed(2)), finite,
     peak_gib: Number((gpu.pool.peak / 2 ** 30).toFixed(2)) };
   if (gpu.profiler) out.kernels = await gpu.profiler.report();
@@ -122,6 +163,8 @@ async function main() {
       device_ms_per_step: Number(dev.timings.perStep.toFixed(2)), host_loop_ms_per_step: Number(host.timings.perStep.toFixed(2)) };
   }
   console.log(JSON.stringify(out));
+  if (fg) fg.release();
+  if (latT) latT.release();
   cond.release();
   attachLoras(regs, []);
   for (const t of loraBufs) t.release();

@@ -185,17 +185,7 @@ export class AnimaDiT {
       h1.release();
       semb.release();
       lora.release();
-      const blocks = this.blocks.map((_, i) => ({
-        self: all.view(3 * i * 3 * D, [1, 3 * D]), cross: all.view((3 * i + 1) * 3 * D, [1, 3 * D]),
-        mlp: all.view((3 * i + 2) * 3 * D, [1, 3 * D]),
-      }));
-      return {
-        blocks, final,
-        release() {
-          all.release();
-          final.release();
-        },
-      };
+      return this.timeCondFrom([all, final], true);
     }
     const mod = (ws, n) => {
       const out = gpu.empty([1, n]);
@@ -205,17 +195,45 @@ export class AnimaDiT {
       hh.release();
       return out;
     };
-    const blocks = this.blocks.map((b) => ({ self: mod(b.modSelf, 3 * D), cross: mod(b.modCross, 3 * D), mlp: mod(b.modMlp, 3 * D) }));
-    const final = mod(this.finalMod, 2 * D);
+    const parts = [];
+    for (const b of this.blocks) parts.push(mod(b.modSelf, 3 * D), mod(b.modCross, 3 * D), mod(b.modMlp, 3 * D));
+    parts.push(mod(this.finalMod, 2 * D));
     semb.release();
     lora.release();
+    return this.timeCondFrom(parts, false);
+  }
+
+  // A timeCond result over its tensors: fused, [all [3*blocks, 3D], final [1, 2D]] (blocks are
+  // views into `all`); otherwise [self, cross, mlp per block..., final].  `parts` lists them in
+  // that order (timeCondSlot / copyTimeCond).
+  timeCondFrom(parts, fused) {
+    let blocks;
+    if (fused) {
+      const all = parts[0];
+      blocks = this.blocks.map((_, i) => ({
+        self: all.view(3 * i * 3 * D, [1, 3 * D]), cross: all.view((3 * i + 1) * 3 * D, [1, 3 * D]),
+        mlp: all.view((3 * i + 2) * 3 * D, [1, 3 * D]),
+      }));
+    } else {
+      blocks = this.blocks.map((_, i) => ({ self: parts[3 * i], cross: parts[3 * i + 1], mlp: parts[3 * i + 2] }));
+    }
     return {
-      blocks, final,
+      blocks, final: parts[parts.length - 1], parts, fused,
       release() {
-        for (const b of blocks) releaseAll([b.self, b.cross, b.mlp]);
-        final.release();
+        releaseAll(parts);
       },
     };
+  }
+
+  // Uninitialized device tensors shaped like the timeCond result `like` (a fixed home for the
+  // modulation vectors of a recorded forward, filled by copyTimeCond).
+  timeCondSlot(like) {
+    return this.timeCondFrom(like.parts.map((t) => this.gpu.empty(t.shape)), like.fused);
+  }
+
+  copyTimeCond(dst, src) {
+    if (dst.parts.length !== src.parts.length) throw new Error("copyTimeCond: different timeCond layouts");
+    dst.parts.forEach((t, i) => this.gpu.copy(t, src.parts[i], src.parts[i].bytes));
   }
 
   // Cross-attention K/V of every block for B prompts (app/models/dit.js:232-249): contexts are
@@ -343,5 +361,64 @@ export class AnimaDiT {
     native.unpatchify(gpu.ctx, out.buf, B, h, w, v.buf); // dit.js:68-78 on the device
     out.release();
     return v;
+  }
+}
+
+// forwardDevice recorded once into a HIP graph (anima_graph_*) and replayed: the same ~600
+// kernels with the same arguments, submitted as one graph launch instead of one launch each.
+// A replay reads `lat` and the graph's timeCond slot as they are when it runs and overwrites
+// `v`.  Capture needs the pool and the workspace to hold every buffer the forward uses and the
+// RoPE table to be cached: with `warm` it runs the forward once eagerly first; without, the
+// caller has just run forwardDevice for the same shapes.  Recording itself executes nothing.
+export class ForwardGraph {
+  constructor(dit, graph, lat, v, tc) {
+    this.dit = dit;
+    this.gpu = dit.gpu;
+    this.graph = graph;
+    this.lat = lat;
+    this.v = v;
+    this.tc = tc;
+  }
+
+  // lat: the [B, 16, h, w] input tensor (kept allocated by the caller while the graph lives);
+  // tcLike: a timeCond result (its layout and initial values).
+  static async capture(dit, lat, h, w, cond, tcLike, warm) {
+    const gpu = dit.gpu;
+    const tc = dit.timeCondSlot(tcLike);
+    dit.copyTimeCond(tc, tcLike);
+    if (warm !== false) (await dit.forwardDevice(lat, h, w, cond, tc)).release();
+    native.graphBegin(gpu.ctx);
+    let v = null, graph = 0;
+    try {
+      v = await dit.forwardDevice(lat, h, w, cond, tc);
+    } finally {
+      if (v) graph = native.graphEnd(gpu.ctx);
+      else {
+        try {
+          native.graphDestroy(gpu.ctx, native.graphEnd(gpu.ctx));
+        } catch (e) {
+          // the capture was already invalid: graphEnd discarded it
+        }
+        tc.release();
+      }
+    }
+    return new ForwardGraph(dit, graph, lat, v, tc);
+  }
+
+  // Replays the forward with the modulation vectors of timeCond result `tc` (copied into the
+  // slot unless it is the slot); returns the velocities [B, 16, h, w] (owned by the graph).
+  run(tc) {
+    if (tc && tc !== this.tc) this.dit.copyTimeCond(this.tc, tc);
+    native.graphLaunch(this.gpu.ctx, this.graph);
+    return this.v;
+  }
+
+  release() {
+    if (this.graph) native.graphDestroy(this.gpu.ctx, this.graph);
+    this.graph = 0;
+    if (this.v) this.v.release();
+    this.v = null;
+    if (this.tc) this.tc.release();
+    this.tc = null;
   }
 }

@@ -8,9 +8,13 @@
 // Noise is drawn on the host with the reference's torch.randn port (rng.mjs), in the reference's
 // order, and uploaded; drawing it after the step's DiT work is enqueued overlaps it with that work.
 // timeCond results are cached per sigma (they depend only on sigma and on the weights / LoRAs).
+// With opts.graph, step 0's forward runs eagerly and, while the device executes it, the forward
+// is recorded into a HIP graph (dit.mjs ForwardGraph) that every later step replays with its
+// own timeCond.
 
 import { native } from "./gpu.mjs";
 import { TorchGenerator } from "./rng.mjs";
+import { ForwardGraph } from "./dit.mjs";
 import { SCHEDULERS, SamplerPlan, sample } from "./samplers.mjs";
 import { loraGeneration } from "./lora.mjs";
 
@@ -52,7 +56,8 @@ export class LatentPipeline {
   }
 
   // opts: { cond, cfg = 1, width, height, steps, sampler, seed = 0, shift = 3, scheduler = "simple",
-  //         onStep(i, readDenoised) }.  cond.B must be 2 when cfg != 1 (positive, negative), else 1.
+  //         onStep(i, readDenoised), graph = false }.  cond.B must be 2 when cfg != 1 (positive,
+  //         negative), else 1.
   // Returns { latent: Float32Array [16, h, w], sigmas, timings }.
   async generate(opts) {
     const gpu = this.gpu;
@@ -72,26 +77,30 @@ export class LatentPipeline {
     const lat = gpu.empty([B, 16, h, w]);
     const old = gpu.empty([n]), oldD = plan.name === "er_sde" ? gpu.empty([n]) : null;
     const den = opts.onStep ? gpu.empty([n]) : null;
+    const useGraph = opts.graph === true && plan.steps > 1;
+    let fg = null;
     try {
       for (let i = 0; i < plan.steps; i++) {
         const st = plan.step(i);
         const tc = this.timeCond(st.sigma);
         for (let b = 0; b < B; b++) gpu.copy(lat.at(b * n), x, n * 4);
-        const v = await this.dit.forwardDevice(lat, h, w, cond, tc);
+        const v = fg ? fg.run(tc) : await this.dit.forwardDevice(lat, h, w, cond, tc);
         const eps = st.noise ? gpu.fromArray(gen.randn(n), [n]) : null;
         native.samplerStep(gpu.ctx, {
           kind: st.kind, n, x: x.buf, v: v.buf, vUncond: guided ? v.at(n) : 0, cfg, sigma: st.sigma,
           final: st.final, stage: st.stage, den: den ? den.buf : 0, old: plan.kind >= 2 ? old.buf : 0,
           oldD: oldD ? oldD.buf : 0, eps: eps ? eps.buf : 0, c: st.c,
         });
-        v.release();
+        if (!fg) v.release();
         if (eps) eps.release();
         if (opts.onStep) await opts.onStep(i, () => gpu.read(den));
+        if (useGraph && !fg) fg = await ForwardGraph.capture(this.dit, lat, h, w, cond, tc, false);
       }
       const latent = await gpu.read(x);
       const ms = Date.now() - t0;
       return { latent, sigmas, timings: { sample: ms, perStep: ms / plan.steps } };
     } finally {
+      if (fg) fg.release();
       for (const t of [x, lat, old, oldD, den]) if (t) t.release();
     }
   }

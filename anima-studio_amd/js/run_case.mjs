@@ -16,13 +16,15 @@
 //              on the fused (grouped GEMV) and the per-linear modulation paths
 //   generate   LatentPipeline.generate (device loop) and generateHost (the reference's host loop)
 //              on a synthetic DiT, per sampler / scheduler / cfg
+//   graph      ForwardGraph replays against eager forwardDevice on a synthetic DiT: one replay per
+//              sigma, a new input latent and an eager forward before each
 
 import fs from "fs";
 import { GPU } from "./gpu.mjs";
 import * as ops from "./ops.mjs";
 import { ditRopeTable } from "./common.mjs";
 import { SafeTensors } from "./weights.mjs";
-import { AnimaDiT } from "./dit.mjs";
+import { AnimaDiT, ForwardGraph } from "./dit.mjs";
 import { SyntheticWeights } from "./weights.mjs";
 import { linearRegistry, loadLora, attachLoras, destroyLora, rotatedA } from "./lora.mjs";
 import { LatentPipeline } from "./pipeline.mjs";
@@ -171,6 +173,33 @@ async function main() {
     }
     console.log(JSON.stringify({ runs, stats: pipe.stats }));
     pipe.clearTimeCache();
+  } else if (c.case === "graph") {
+    const dit = AnimaDiT.synthetic(gpu, new SyntheticWeights(gpu, 9, { mode: c.mode, blocks: c.blocks }));
+    const ctxs = [0, 1].map((b) => gpu.fromArray(new TorchGenerator(200 + b).randn(c.Lk * 1024), [c.Lk, 1024]));
+    const cond = dit.prepareContext(ctxs);
+    const h = c.size / 8, w = c.size / 8, n = 2 * 16 * h * w;
+    const lat = gpu.empty([2, 16, h, w]);
+    const tcs = c.sigmas.map((sg) => dit.timeCond(sg));
+    gpu.write(lat, new TorchGenerator(300).randn(n));
+    const fg = await ForwardGraph.capture(dit, lat, h, w, cond, tcs[0]);
+    const diffs = [];
+    for (let r = 0; r < tcs.length; r++) {
+      gpu.write(lat, new TorchGenerator(400 + r).randn(n));
+      const ev = await dit.forwardDevice(lat, h, w, cond, tcs[r]);
+      const e = await gpu.read(ev);
+      ev.release();
+      const g = await gpu.read(fg.run(tcs[r]));
+      let nd = 0;
+      for (let i = 0; i < n; i++) if (e[i] !== g[i]) nd++;
+      diffs.push(nd);
+      save(`${c.out}.eager${r}`, e);
+      save(`${c.out}.graph${r}`, g);
+    }
+    fg.release();
+    for (const tc of tcs) tc.release();
+    lat.release();
+    cond.release();
+    console.log(JSON.stringify({ graph: { diffs, n } }));
   } else if (c.case === "lnmod") {
     const x = gpu.fromArray(load(c.x), [c.rows, c.cols]);
     const mod = gpu.upload(load(c.mod));

@@ -75,6 +75,26 @@ int anima_profile_report(anima_ctx* ctx, char* buf, size_t len);
 int anima_timer_start(anima_ctx* ctx);
 int anima_timer_stop(anima_ctx* ctx, float* ms);
 
+/* Recorded submission.  The reference records its dispatches into command encoders and submits
+ * them in batches (app/gpu/device.js:1-5, 183-216), re-recording every forward.  Here the
+ * context stream's work between anima_graph_begin and anima_graph_end is captured once into a
+ * HIP graph and anima_graph_launch replays it (same kernels, same arguments, same device
+ * addresses; inputs are read as they are when the replay runs).
+ * While capturing, host copies (anima_h2d, anima_d2h), synchronization (anima_sync,
+ * anima_pool_trim, the profiler report, the timer) and workspace growth fail with
+ * ANIMA_E_STATE: run the work once eagerly first, so the pool and the workspace already hold
+ * what it needs.  Buffers freed during the capture stay reserved for the graph until
+ * anima_graph_destroy; buffers still allocated at the end (outputs) and those allocated before
+ * the capture (inputs, weights) remain the caller's and must stay allocated while the graph is
+ * replayed.  Profiling is suspended during the capture. */
+typedef struct anima_graph anima_graph;
+int anima_graph_begin(anima_ctx* ctx);
+/* Ends the capture; on success *graph is replayable.  On failure the capture is discarded. */
+int anima_graph_end(anima_ctx* ctx, anima_graph** graph);
+int anima_graph_launch(anima_ctx* ctx, anima_graph* graph);
+/* Releases the graph; its reserved buffers go back to the pool (stream-ordered). */
+int anima_graph_destroy(anima_ctx* ctx, anima_graph* graph);
+
 /* ---------------------------------------------------------------- attention */
 
 #define ANIMA_PREC_BF16 0 /* bf16 MFMA, fp32 accumulate */

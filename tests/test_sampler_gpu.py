@@ -88,14 +88,18 @@ def test_js_generate_device_equals_host(tmp_path):
     """LatentPipeline.generate (velocities stay on the device; one fused kernel per step) against
     generateHost (velocities read back; CFG, denoised and the update over Float32Arrays, as
     app/pipeline.js and app/samplers.js do) on a 1-block synthetic DiT at 64x64: identical
-    latents for every sampler, with and without CFG, both schedulers.  The host run reuses the
-    device run's timeCond results from the cache."""
+    latents for every sampler, with and without CFG, both schedulers, also with the device loop's
+    forwards replayed from a HIP graph.  The host run reuses the device run's timeCond results
+    from the cache."""
     case("js generate: device loop vs host loop")
     runs = []
     for nm in SAMPLERS:
         runs.append(dict(key=f"{nm}_cfg", sampler=nm, scheduler="simple", steps=6, cfg=4.0, seed=11))
     runs.append(dict(key="euler_a_nocfg", sampler="euler_a", scheduler="beta", steps=8, cfg=1, seed=3))
     runs.append(dict(key="er_sde_beta", sampler="er_sde", scheduler="beta", steps=7, cfg=2.5, seed=4))
+    # steps 1.. replayed from the forward recorded into a HIP graph
+    runs.append(dict(key="dpmpp_2m_graph", sampler="dpmpp_2m", scheduler="simple", steps=6, cfg=4.0, seed=12, graph=True))
+    runs.append(dict(key="euler_a_nocfg_graph", sampler="euler_a", scheduler="beta", steps=5, cfg=1, seed=13, graph=True))
     out = str(tmp_path / "g")
     r = run_case(tmp_path, {"case": "generate", "mode": "int8", "size": 64, "Lk": 8, "runs": runs, "out": out})
     info = json.loads(next(ln for ln in r.stdout.splitlines() if '"runs"' in ln))
