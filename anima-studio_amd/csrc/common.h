@@ -19,18 +19,24 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ bf16 to_bf16(float x) { return (bf16)x; }
 
 // GELU with the Abramowitz-Stegun erf of app/gpu/kernels.js:11-18.  The reciprocal is v_rcp_f32
-// (1 ulp) and the exponential v_exp_f32 of the argument scaled by log2(e) (about 1 ulp plus the
-// rounding of the scaled argument): inside the accuracy WGSL itself grants the reference's
-// division (2.5 ulp) and exp (3 + 2|x| ulp); against the correctly rounded formula the output
-// differs by 2e-8 relative L2 on N(0, 9) inputs.
+// (1 ulp) and the exponential v_exp_f32 (2^x) of -a^2 scaled by log2(e) (about 1 ulp plus the
+// rounding of the scaled argument); the polynomial runs on FMAs, which WGSL lets the reference's
+// compiler use as well.  Inside the accuracy WGSL grants the reference's division (2.5 ulp) and
+// exp (3 + 2|x| ulp); against the correctly rounded formula the output differs by about 2e-8
+// relative L2 on N(0, 9) inputs.  sign(z) * y is copysign(y, z): at z = 0 the result is 0.5 x
+// either way (x = 0 there, or so small that y ~ 1e-9 vanishes in 1 + y).
 __device__ __forceinline__ float gelu_erf(float x) {
   const float z = x * 0.7071067811865476f;
-  const float s = z > 0.0f ? 1.0f : (z < 0.0f ? -1.0f : 0.0f);
   const float a = fabsf(z);
-  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * a);
-  const float y = 1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
-                          0.254829592f) * t * __expf(-a * a);
-  return 0.5f * x * (1.0f + s * y);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, a, 1.0f));
+  float p = __builtin_fmaf(1.061405429f, t, -1.453152027f);
+  p = __builtin_fmaf(p, t, 1.421413741f);
+  p = __builtin_fmaf(p, t, -0.284496736f);
+  p = __builtin_fmaf(p, t, 0.254829592f);
+  const float e = __builtin_amdgcn_exp2f(a * a * -1.4426950408889634f);
+  const float y = __builtin_fmaf(-(p * t), e, 1.0f);
+  const float h = 0.5f * x;
+  return __builtin_fmaf(h, __builtin_copysignf(y, z), h);
 }
 
 // The activations of the linear epilogues (ANIMA_ACT_*), shared by the GEMM epilogues and the

@@ -377,13 +377,9 @@ __device__ __forceinline__ void bfly4_ref(float& a, float& b, float& c, float& e
   e = o3;
 }
 
-// value of quad position M (lane (L & ~3) + M) at every lane of the quad
-template <int M>
-__device__ __forceinline__ float quad_bcast(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), M * 0x55, 0xf, 0xf, true));
-}
-
-// Hadamard (x 1/16) of the lane's 64 elements: stages 1-3 in registers, stage 4 across the quad.
+// Hadamard (x 1/16 unless !SCALE) of the lane's 64 elements: stages 1-3 in registers, stage 4
+// across the quad.
+template <bool SCALE = true>
 __device__ __forceinline__ void hadamard64_quad(float (&v)[64], int k) {
 #pragma unroll
   for (int s = 1; s <= 16; s *= 4)
@@ -392,15 +388,22 @@ __device__ __forceinline__ void hadamard64_quad(float (&v)[64], int k) {
       if ((b / s) % 4 == 0) bfly4_ref(v[b], v[b + s], v[b + 2 * s], v[b + 3 * s]);
   const float s0 = k == 3 ? -1.0f : 1.0f, s1 = k == 2 ? -1.0f : 1.0f, s2 = k == 1 ? -1.0f : 1.0f,
               s3 = k == 0 ? -1.0f : 1.0f;
+  // t = x0 s0, then t = fma(x_m, s_m, t) for m = 1..3, where x_m is v[p] of quad lane m: the DPP
+  // forms of v_mul / v_fmac read x_m straight from lane m (one instruction per term instead of a
+  // DPP move plus a VOP3 FMA).  s_nop 1: the two wait states gfx9 requires between a VALU write
+  // of v[p] and a DPP read of it.
 #pragma unroll
   for (int p = 0; p < 64; p++) {
-    const float x0 = quad_bcast<0>(v[p]), x1 = quad_bcast<1>(v[p]), x2 = quad_bcast<2>(v[p]),
-                x3 = quad_bcast<3>(v[p]);
-    float t = x0 * s0;
-    t = __builtin_fmaf(x1, s1, t);
-    t = __builtin_fmaf(x2, s2, t);
-    t = __builtin_fmaf(x3, s3, t);
-    v[p] = t * 0.0625f;
+    float t;
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_mul_f32_dpp %0, %1, %2 quad_perm:[0,0,0,0] row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %3 quad_perm:[1,1,1,1] row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %4 quad_perm:[2,2,2,2] row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %5 quad_perm:[3,3,3,3] row_mask:0xf bank_mask:0xf"
+        : "=&v"(t)
+        : "v"(v[p]), "v"(s0), "v"(s1), "v"(s2), "v"(s3));
+    v[p] = SCALE ? t * 0.0625f : t;
   }
 }
 
@@ -464,13 +467,16 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(const float* X, int
 #pragma unroll
     for (int i = 0; i < 64; i++) v[i] = act1(v[i], act);
   }
-  if (rotate) hadamard64_quad(v, L & 3);
+  // The Hadamard's final 1/16 is left out: scaling a row by a power of two scales its maximum
+  // the same way and leaves q = rint(v * (127 / amax)) unchanged (127 / (amax / 16) is exactly
+  // 16 * (127 / amax) and the products are equal), so only the stored scale takes it.
+  if (rotate) hadamard64_quad<false>(v, L & 3);
   float am = 0.0f;
 #pragma unroll
   for (int i = 0; i < 64; i++) am = fmaxf(am, fabsf(v[i]));
   am = rows_max<LR>(am, red);
   if (!live) return;
-  if (L == 0) S_out[row] = am / 127.0f;
+  if (L == 0) S_out[row] = (rotate ? am * 0.0625f : am) / 127.0f;
   quant64_store(v, am, Q + row * K + 64 * L);
 }
 
