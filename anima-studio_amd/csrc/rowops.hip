@@ -369,8 +369,10 @@ __global__ __launch_bounds__(256) void quant_rows_pad_kernel(const float* X, int
 // variant's.  No LDS except the cross-wave maximum of rows wider than a wave.
 
 // 4-point butterfly of the reference on four values held by one lane (outputs in place)
+// (-a + b is -(a - b) exactly, so the four outputs share a + b and a - b.)
 __device__ __forceinline__ void bfly4_ref(float& a, float& b, float& c, float& e) {
-  const float o0 = a + b + c - e, o1 = a + b - c + e, o2 = a - b + c + e, o3 = -a + b + c + e;
+  const float u = a + b, w = a - b;
+  const float o0 = (u + c) - e, o1 = (u - c) + e, o2 = (w + c) + e, o3 = (c - w) + e;
   a = o0;
   b = o1;
   c = o2;
@@ -422,22 +424,27 @@ __device__ __forceinline__ float rows_max(float v, float* red) {
 }
 
 // Per-token int8 of the lane's 64 values (q = clamp(rint(v * (127/amax))), s = amax/127).
+// Rounding by the 1.5 * 2^23 add: for |r| < 2^22, r + C lies in [2^23, 2^24), where the float
+// spacing is 1, so it equals C + rint(r) (ties to even; C is even) and its low byte is rint(r) in
+// two's complement; the clamp to C -/+ 127 in float is the clamp to -/+127 (a NaN goes to -127
+// as with fmaxf / fminf on the integer).
 __device__ __forceinline__ void quant64_store(const float (&v)[64], float amax, int8_t* q) {
   // an all-zero row: inv = 0 gives q = 0, as the definition's special case
   const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+  constexpr float C = 12582912.0f;
 #pragma unroll
   for (int g = 0; g < 4; g++) {
     uint32_t w[4];
 #pragma unroll
     for (int d = 0; d < 4; d++) {
-      uint32_t packed = 0;
+      uint32_t b[4];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        float t = rintf(v[16 * g + 4 * d + j] * inv);
-        t = fminf(fmaxf(t, -127.0f), 127.0f);
-        packed |= ((uint32_t)(int32_t)t & 0xffu) << (8 * j);
+        const float t = v[16 * g + 4 * d + j] * inv + C;
+        b[j] = __float_as_uint(fminf(fmaxf(t, C - 127.0f), C + 127.0f));
       }
-      w[d] = packed;
+      // bytes 0 of b0, b1 (low half) and of b2, b3 (high half)
+      w[d] = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u) | __builtin_amdgcn_perm(b[3], b[2], 0x04000c0cu);
     }
     *(uint4*)(q + 16 * g) = make_uint4(w[0], w[1], w[2], w[3]);
   }
