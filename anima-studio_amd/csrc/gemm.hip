@@ -342,7 +342,11 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
   const int mine = first < last ? (last - first + stride - 1) / stride : 0;
   const int total = mine * nk;  // stages of this workgroup's stream (tile-major)
 
-  // this wave's two 1 KiB chunks of each tile: rows 16*(2*wave + c) + lane/4, unit permuted
+  // Copies: waves 0-3 (one per SIMD; wave w shares its SIMD with wave w + 4) issue all of them, so
+  // the other wave of each SIMD runs an MFMA stream free of copy and M0 set-up instructions
+  // (3-4% faster than eight issuing waves).  Wave w < 4 moves the 1 KiB chunks of rows
+  // 16*(2*w + c) + lane/4 and the same rows + 128 of each tile (unit permuted); rows r and r + 128
+  // share the permutation.
   const int row0 = 32 * wave + (lane >> 2), row1 = row0 + 16;
   const int loff0 = row0 * K + 16 * ((lane & 3) ^ ((row0 >> 2) & 3));
   const int loff1 = row1 * K + 16 * ((lane & 3) ^ ((row1 >> 2) & 3));
@@ -364,13 +368,16 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
 #define G2_ISSUE()                                                                                            \
   {                                                                                                           \
     char* st_ = smem + (ig & (G2_NST - 1)) * G2_ST;                                                           \
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(st_ + (2 * wave) * 1024), 16, loff0, is * G2_BK, 0, 0); \
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(st_ + (2 * wave + 1) * 1024), 16, loff1, is * G2_BK, 0, \
-                                             0);                                                              \
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(st_ + G2_TILE + (2 * wave) * 1024), 16, loff0,  \
-                                             is * G2_BK, 0, 0);                                               \
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(st_ + G2_TILE + (2 * wave + 1) * 1024), 16, loff1, \
-                                             is * G2_BK, 0, 0);                                               \
+    if (wave < 4) {                                                                                           \
+      _Pragma("unroll") for (int h_ = 0; h_ < 2; h_++) {                                                      \
+        const int so_ = is * G2_BK + h_ * 128 * K;                                                            \
+        char* sw_ = st_ + (2 * wave + 8 * h_) * 1024;                                                         \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sw_), 16, loff0, so_, 0, 0);               \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sw_ + 1024), 16, loff1, so_, 0, 0);        \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(sw_ + G2_TILE), 16, loff0, so_, 0, 0);     \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(sw_ + G2_TILE + 1024), 16, loff1, so_, 0, 0); \
+      }                                                                                                       \
+    }                                                                                                         \
     ig++;                                                                                                     \
     if (++is == nk) {                                                                                         \
       is = 0;                                                                                                 \
@@ -395,8 +402,8 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
   if (total > 0) G2_ISSUE();
   if (total > 1) G2_ISSUE();
   if (total > 2) G2_ISSUE();
-  if (total > 2) G2_WAIT_VM(8);
-  else if (total > 1) G2_WAIT_VM(4);
+  if (total > 2) G2_WAIT_VM(16);
+  else if (total > 1) G2_WAIT_VM(8);
   else G2_WAIT_VM(0);
   g2_barrier();
   if (total > 0) {
@@ -409,7 +416,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
   for (int g = 0; g < total; g++) {
     // publish stage g+1: this wave's copies of it are done once at most those of g+2 are
     // pending; the barrier also ends every wave's reads of stage g-1, which is refilled with g+3
-    if (g + 2 < total) G2_WAIT_VM(4);
+    if (g + 2 < total) G2_WAIT_VM(8);
     else G2_WAIT_VM(0);
     g2_barrier();
     if (g + 3 < total) G2_ISSUE();
