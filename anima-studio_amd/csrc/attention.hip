@@ -666,15 +666,22 @@ struct W8Src {
   __amdgpu_buffer_rsrc_t k, v;
 };
 
-__device__ __forceinline__ void w8_load(const W8Src& src, const W8Load& lo, int blk, char* stage, int wave) {
+// Waves 0-3 (one per SIMD) issue all of a block's copies: their own chunks and those of wave
+// w + 4 (K rows + 32 and V^T dims + 64, which keep the same lane permutation), so the other wave
+// of each SIMD runs without copy and M0 set-up instructions.  vhalf: byte distance of 64 V^T rows.
+__device__ __forceinline__ void w8_load(const W8Src& src, const W8Load& lo, int blk, char* stage, int wave, int vhalf) {
+  if (wave >= 4) return;
 #pragma unroll
-  for (int c = 0; c < 2; c++)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.k, (lds_void_t*)(stage + (2 * wave + c) * 1024), 16, lo.k[c],
-                                             blk * (W8_KB * HD * 2), 0, 0);
+  for (int h = 0; h < 2; h++) {
 #pragma unroll
-  for (int c = 0; c < 2; c++)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.v, (lds_void_t*)(stage + SWZ_KT + (2 * wave + c) * 1024), 16, lo.v[c],
-                                             blk * (W8_KB * 2), 0, 0);
+    for (int c = 0; c < 2; c++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(src.k, (lds_void_t*)(stage + (2 * wave + 8 * h + c) * 1024), 16, lo.k[c],
+                                               blk * (W8_KB * HD * 2) + h * (32 * HD * 2), 0, 0);
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(src.v, (lds_void_t*)(stage + SWZ_KT + (2 * wave + 8 * h + c) * 1024), 16,
+                                               lo.v[c], blk * (W8_KB * 2) + h * vhalf, 0, 0);
+  }
 }
 
 // Workgroup barrier without a memory fence: the LDS copies a barrier publishes are covered by
@@ -709,9 +716,10 @@ __global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
 
   // blocks 0, 1 and 2 start loading before Q is read and normalized
   const W8Load lo(a.Lkp, wave, lane);
-  w8_load(src, lo, 0, smem, wave);
-  if (nkb > 1) w8_load(src, lo, 1, smem + W8_ST, wave);
-  if (nkb > 2) w8_load(src, lo, 2, smem + 2 * W8_ST, wave);
+  const int vhalf = 64 * a.Lkp * 2;
+  w8_load(src, lo, 0, smem, wave, vhalf);
+  if (nkb > 1) w8_load(src, lo, 1, smem + W8_ST, wave, vhalf);
+  if (nkb > 2) w8_load(src, lo, 2, smem + 2 * W8_ST, wave, vhalf);
 
   bf16x8 qf[8];
   {
@@ -730,16 +738,16 @@ __global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
   f32x16 negm = {};
 
   // Block j lives in stage j % 4.  The barrier at the top of iteration j publishes block j+1 (a
-  // wave first waits for its own copies of it; the 4 of block j+2 may still be in flight), so
+  // wave first waits for its own copies of it; the 8 of block j+2 may still be in flight), so
   // block j's last MFMAs can carry the reads of block j+1's first fragments.  The barrier also
   // ends every wave's reads of block j-1, whose stage is then refilled with block j+3.  The
   // barrier before block 0 publishes blocks 0 and 1; a partial last block needs no barrier of
   // its own (published one iteration ahead, and its stage is not refilled).
   const int nfull = Lk / W8_KB;
-  if (nkb > 2) W8_WAIT_VM(4);
+  if (nkb > 2) W8_WAIT_VM(8);
   else W8_WAIT_VM(0);
   w8_barrier();
-  if (nkb > 3) w8_load(src, lo, 3, smem + 3 * W8_ST, wave);
+  if (nkb > 3) w8_load(src, lo, 3, smem + 3 * W8_ST, wave, vhalf);
   if (nfull > 0) flash_block<W8_KB, false, true>(SwzAddr(smem, of), qf, o, m, negm, l, 0, Lk, hf);
   else flash_block<W8_KB, true, true>(SwzAddr(smem, of), qf, o, m, negm, l, 0, Lk, hf);
   bf16x8 f[4];
@@ -756,10 +764,10 @@ __global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
 #define W8_ITER(ST)                                                                                    \
   {                                                                                                    \
     if (j >= nfull) break;                                                                             \
-    if (j + 2 < nkb) W8_WAIT_VM(4);                                                                    \
+    if (j + 2 < nkb) W8_WAIT_VM(8);                                                                    \
     else W8_WAIT_VM(0);                                                                                \
     w8_barrier();                                                                                      \
-    if (j + 3 < nkb) w8_load(src, lo, j + 3, smem + (((ST) + 3) & 3) * W8_ST, wave);                   \
+    if (j + 3 < nkb) w8_load(src, lo, j + 3, smem + (((ST) + 3) & 3) * W8_ST, wave, vhalf);            \
     flash_block_main<SwzAddr, true>(W8_ADDR(ST), W8_ADDR(((ST) + 1) & 3), f, qf, o, m, negm, l);        \
     j++;                                                                                               \
   }
