@@ -208,6 +208,7 @@ struct FlashArgs {
   float eps, c;  // c = scale * log2(e)
   int H, group, Hkv, Lq, Lkp, n_qt;
   int kv_len[MAXB];
+  int causal;  // keys > query index masked (the 4-wave and fp32 kernels)
 };
 
 // Loads this lane's 64 Q values (query qi, dims 16ks + 8hf + j), applies the fused
@@ -537,7 +538,12 @@ __global__ __launch_bounds__(256, KB == 32 ? 3 : 2) void attn_flash_bf16(FlashAr
   const int b = bh / a.H, h = bh - b * a.H, hk = h / a.group;
   const int qi = qt * BQ + wave * 32 + lq;
   const int Lk = a.kv_len[b];
-  const int nkb = (Lk + KB - 1) / KB;
+  // causal (app/gpu/kernels.js:49, limit = min(cols, row + 1)): this lane's keys end at lim; the
+  // workgroup's last block holds the key of its last query, and blocks before key qt * BQ (its
+  // first query) need no mask
+  const int lim = a.causal ? min(Lk, qi + 1) : Lk;
+  const int nkb = a.causal ? min((Lk + KB - 1) / KB, (qt * BQ + BQ + KB - 1) / KB) : (Lk + KB - 1) / KB;
+  const int nfull = a.causal ? min(Lk / KB, qt * BQ / KB) : Lk / KB;
 
   bf16x8 qf[8];
   {
@@ -582,12 +588,11 @@ __global__ __launch_bounds__(256, KB == 32 ? 3 : 2) void attn_flash_bf16(FlashAr
   GLOAD(0);
   LSTORE(0);
   __syncthreads();
-  // Block 0 sets the offset; the last block is the only one that can be partial and is
-  // processed after the loop with the key mask (it is already in its stage by then).
-  const int nfull = Lk / KB;
+  // Block 0 sets the offset.  Blocks from nfull on (the partial last block; with causal also
+  // the blocks on the diagonal) take the key mask with this lane's limit.
   if (nkb > 1) GLOAD(1);
   if (nfull > 0) flash_block<KB, false, true>(PadAddr<KB>(smem, smem + T::KTILE, lq, hf), qf, o, m, negm, l, 0, Lk, hf);
-  else flash_block<KB, true, true>(PadAddr<KB>(smem, smem + T::KTILE, lq, hf), qf, o, m, negm, l, 0, Lk, hf);
+  else flash_block<KB, true, true>(PadAddr<KB>(smem, smem + T::KTILE, lq, hf), qf, o, m, negm, l, 0, lim, hf);
   if (nkb > 1) LSTORE(1);
   __syncthreads();
   for (int kb = 1; kb < nfull; kb++) {
@@ -604,10 +609,16 @@ __global__ __launch_bounds__(256, KB == 32 ? 3 : 2) void attn_flash_bf16(FlashAr
     if (more) LSTORE(st ^ 1);
     __syncthreads();
   }
-  if (nfull < nkb && nfull > 0) {
-    const int st = nfull & 1;
+  // masked blocks (a separate loop: in the main loop's body the masked block raised its registers
+  // past the limit); block max(1, nfull) is already in its stage
+  for (int kb = nfull > 1 ? nfull : 1; kb < nkb; kb++) {
+    const int st = kb & 1;
+    const bool more = kb + 1 < nkb;
+    if (more) GLOAD(kb + 1);
     flash_block<KB, true, false>(PadAddr<KB>(smem + st * T::STAGE, smem + st * T::STAGE + T::KTILE, lq, hf), qf, o, m,
-                                 negm, l, nfull * KB, Lk, hf);
+                                 negm, l, kb * KB, lim, hf);
+    if (more) LSTORE(st ^ 1);
+    __syncthreads();
   }
 #undef GLOAD
 #undef LSTORE
@@ -830,7 +841,10 @@ __global__ __launch_bounds__(256) void attn_flash_fp32(FlashArgs a) {
   const int b = bh / a.H, h = bh - b * a.H, hk = h / a.group;
   const int qi = qt * BQ + wave * 32 + lq;
   const int Lk = a.kv_len[b];
-  const int nkb = (Lk + BK - 1) / BK;
+  // causal: as in attn_flash_bf16 (lim: this lane's key limit; mlim: the workgroup's smallest)
+  const int lim = a.causal ? min(Lk, qi + 1) : Lk;
+  const int mlim = a.causal ? min(Lk, qt * BQ + 1) : Lk;
+  const int nkb = a.causal ? min((Lk + BK - 1) / BK, (qt * BQ + BQ + BK - 1) / BK) : (Lk + BK - 1) / BK;
 
   // lane keeps Q[qi][2ks + hf] for ks = 0..63 (K-group g of a 32x32x2 MFMA = dim parity)
   float qv[64];
@@ -885,12 +899,12 @@ __global__ __launch_bounds__(256) void attn_flash_fp32(FlashArgs a) {
       s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(k0, qv[ks], s0, 0, 0, 0);
       s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(k1, qv[ks], s1, 0, 0, 0);
     }
-    if ((kb + 1) * BK > Lk) {
+    if ((kb + 1) * BK > mlim) {
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         const int key = kb * BK + 8 * (r >> 2) + 4 * hf + (r & 3);
-        if (key >= Lk) s0[r] = -INFINITY;
-        if (key + 32 >= Lk) s1[r] = -INFINITY;
+        if (key >= lim) s0[r] = -INFINITY;
+        if (key + 32 >= lim) s1[r] = -INFINITY;
       }
     }
     float bm = fmaxf(s0[0], s1[0]);
@@ -947,7 +961,6 @@ static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // Argument checks of anima_attention (fills kv_len[] with the valid key counts).
 static int attention_check(anima_ctx* c, const anima_attn_desc* d, int (&kv_len)[MAXB]) {
   const int group = d->group <= 0 ? 1 : d->group;
-  if (d->causal) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: causal attention is not on the DiT path (only the chunked text-encoder path of ops.js:177-207 uses it)");
   if (d->D != HD) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: head dim %d (this build implements D=128, the DiT head size)", d->D);
   if (d->B < 1 || d->B > MAXB) return fail(c, ANIMA_E_ARG, "anima_attention: B=%d outside [1,%d]", d->B, MAXB);
   if (d->Lq < 1 || d->Lk < 1 || d->H < 1) return fail(c, ANIMA_E_ARG, "anima_attention: Lq=%d Lk=%d H=%d must be >= 1", d->Lq, d->Lk, d->H);
@@ -1078,9 +1091,10 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
   f.Lq = d->Lq;
   f.Lkp = Lkp;
   // 8-wave workgroups (256 queries) when that grid still gives every CU a workgroup
-  const bool w8 = bf && (int64_t)((d->Lq + W8_BQ - 1) / W8_BQ) * d->H * d->B >= c->num_cus;
+  const bool w8 = bf && !d->causal && (int64_t)((d->Lq + W8_BQ - 1) / W8_BQ) * d->H * d->B >= c->num_cus;
   f.n_qt = w8 ? (d->Lq + W8_BQ - 1) / W8_BQ : (d->Lq + BQ - 1) / BQ;
   for (int b = 0; b < MAXB; b++) f.kv_len[b] = b < d->B ? kv_len[b] : 1;
+  f.causal = d->causal ? 1 : 0;
   double flops = 0;
   for (int b = 0; b < d->B; b++) flops += 4.0 * d->Lq * (double)kv_len[b] * HD * d->H;
   const int blocks = f.n_qt * d->H * d->B;

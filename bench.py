@@ -100,6 +100,35 @@ def dit_step(args):
             "sampling": d.get("generate")}
 
 
+def causal_attention(m, ctx, np):
+    """Causal GQA attention at the text encoder's shape (app/models/qwen3.js:60: B=1, 512 tokens,
+    16 query heads over 8 kv heads, D=128), bf16 MFMA; FLOPs over the unmasked pairs,
+    4 * H * D * L(L+1)/2."""
+    B, L, H, Hkv, D = 1, 512, 16, 8, 128
+    rng = np.random.default_rng(11)
+    q = ctx.upload(rng.standard_normal((L, H * D), dtype=np.float32))
+    k = ctx.upload(rng.standard_normal((L, Hkv * D), dtype=np.float32))
+    v = ctx.upload(rng.standard_normal((L, Hkv * D), dtype=np.float32))
+    o = ctx.empty((L, H * D))
+
+    def call():
+        ctx.attention(q=q, k=k, v=v, o=o, B=B, Lq=L, Lk=L, H=H, D=D, ldq=H * D, ldk=Hkv * D, ldv=Hkv * D,
+                      group=H // Hkv, causal=1)
+
+    for _ in range(5):
+        call()
+    ctx.sync()
+    ctx.timer_start()
+    for _ in range(50):
+        call()
+    ms = ctx.timer_stop() / 50
+    for b in (q, k, v, o):
+        b.release()
+    flops = 4.0 * H * D * L * (L + 1) / 2
+    return {"B": B, "tokens": L, "heads": H, "kv_heads": Hkv, "ms": round(ms, 5),
+            "TFLOP/s": round(flops / ms / 1e9, 1), "kernel": "attn_flash_bf16 (4 waves, causal mask)"}
+
+
 LINEAR_SHAPES = (("qkv", 6144, 2048, "store"), ("out", 2048, 2048, "gated"), ("mlp1", 8192, 2048, "gelu"),
                  ("mlp2", 2048, 8192, "gated"))
 
@@ -222,6 +251,7 @@ def main():
         prep_gbs = prep["bytes"] / prep["count"] / (prep_ms / 1e3) / 1e9 if prep else None
         for b in (d_qkv, d_qn, d_kn, d_cs, d_o):
             b.release()
+        causal = causal_attention(m, ctx, np)
         lin = None
         if not args.no_linears:
             t = time.time()
@@ -253,6 +283,7 @@ def main():
         "prep_kernel": {"ms": round(prep_ms, 5) if prep_ms else None, "GB/s": round(prep_gbs, 1) if prep_gbs else None,
                         "frac_hbm": round(prep_gbs / HBM_PEAK_GBS, 4) if prep_gbs else None},
     }
+    out["causal_attention"] = causal
     if lin is not None:
         out["linears"] = lin
     if not args.no_dit:

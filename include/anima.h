@@ -121,7 +121,9 @@ typedef struct {
   const float* rope_cs;
   int64_t rope_sin_off;
   float eps;
-  int causal; /* must be 0: the causal chunked path of the text encoder is not on this path */
+  int causal; /* 1: keys after the query's own index are masked, limit = min(Lk, query + 1)
+               * (the causal softmax of app/gpu/kernels.js:27-49, used by the text encoder's
+               * attention, app/models/qwen3.js:60); with group > 1 this is its GQA form */
   /* Optional: K and V already converted by anima_attention_prepare_kv (same B, H / group, Lk and
    * precision); then k, v, their strides, k_norm and the key side of rope_cs are not read. */
   const void* kv_prep;
