@@ -8,6 +8,8 @@
 //                     [--lora-rank R]   (seeded rank-R LoRAs on every block linear, strength 1)
 //                     [--generate N [--sampler euler_a] [--cfg 4]]  (also time an N-step sampling run:
 //                      the device loop of pipeline.mjs and the reference's host loop)
+//                     [--text-encoder N]  (also time Qwen3.encode of N tokens on a 28-layer synthetic
+//                      text encoder: causal GQA attention, bf16 linears)
 //                     [--graph [--rounds 3]]  (also the forward replayed from a HIP graph recorded
 //                      once, ForwardGraph: graph and eager blocks of --steps steps alternate,
 //                      medians; dit_step_ms stays the eager step, graph_step_ms the replay)
@@ -17,6 +19,7 @@ import { SyntheticWeights } from "./weights.mjs";
 import { AnimaDiT, ForwardGraph } from "./dit.mjs";
 import { linearRegistry, attachLoras, rotatedA } from "./lora.mjs";
 import { LatentPipeline } from "./pipeline.mjs";
+import { Qwen3 } from "./qwen3.mjs";
 
 function arg(name, def) {
   const i = process.argv.indexOf("--" + name);
@@ -161,6 +164,20 @@ async function main() {
     pipe.clearTimeCache();
     out.generate = { sampler: opts.sampler, steps: genSteps, cfg: opts.cfg,
       device_ms_per_step: Number(dev.timings.perStep.toFixed(2)), host_loop_ms_per_step: Number(host.timings.perStep.toFixed(2)) };
+  }
+  const teTokens = Number(arg("text-encoder", 0));
+  if (teTokens > 0) {
+    const te = Qwen3.synthetic(gpu, new SyntheticWeights(gpu, 99), { vocab: 4096 });
+    const ids = [];
+    for (let i = 0; i < teTokens; i++) ids.push((i * 2654435761) % 4096);
+    (await te.encode(ids)).release();
+    await gpu.sync();
+    gpu.timerStart();
+    for (let i = 0; i < 3; i++) (await te.encode(ids)).release();
+    const teMs = gpu.timerStop() / 3;
+    out.text_encoder = { tokens: teTokens, layers: te.layers.length, ms: Number(teMs.toFixed(3)),
+      note: "Qwen3.encode: embedding gather on the host, 28 layers, causal GQA 16/8 heads, bf16 linears" };
+    te.release();
   }
   console.log(JSON.stringify(out));
   if (fg) fg.release();

@@ -17,6 +17,17 @@ export function ropeTableTensor(gpu, angles, L, half) {
   return t;
 }
 
+// Standard 1D rope of the text encoder: angle(l, i) = l * fround(1 / theta^(2i / D))
+// (app/models/common.js:15-22).
+export function ropeTable(gpu, L, Dh, theta) {
+  const half = Dh / 2;
+  const a = new Float32Array(L * half);
+  for (let l = 0; l < L; l++) {
+    for (let i = 0; i < half; i++) a[l * half + i] = l * Math.fround(1 / Math.pow(theta, (2 * i) / Dh));
+  }
+  return ropeTableTensor(gpu, a, L, half);
+}
+
 // Cosmos VideoRopePosition3DEmb for one frame: 64 slots = 22 temporal (position 0), 21 height,
 // 21 width, NTK-scaled theta for h/w (app/models/common.js:238-260).
 export function ditRopeAngles(H, W) {

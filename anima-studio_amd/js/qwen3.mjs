@@ -1,0 +1,135 @@
+// The Qwen3-0.6B text encoder of Anima (app/models/qwen3.js:1-79) on this build's ops: 28 layers
+// of RMSNorm -> q/k/v linears -> per-head q/k RMSNorm -> 1D RoPE -> causal GQA attention (16 query
+// heads over 8 kv heads, on the flash kernels) -> o linear (residual) -> RMSNorm -> gate/up
+// linears -> SiLU(gate) * up -> down linear (residual); the final RMSNorm's output is the hidden
+// state the DiT's context is built from.  Node-12 syntax only.
+
+import * as ops from "./ops.mjs";
+import { ropeTable } from "./common.mjs";
+
+export const QWEN3 = { layers: 28, hidden: 1024, heads: 16, kvHeads: 8, headDim: 128, mlp: 3072, theta: 1e6, vocab: 151936 };
+
+export class Qwen3 {
+  // Weights from a safetensors file in the reference's names (qwen3.js:8-31).
+  static async load(gpu, st, onProgress) {
+    const m = new Qwen3(gpu, QWEN3);
+    m.layers = [];
+    for (let i = 0; i < QWEN3.layers; i++) {
+      const p = `model.layers.${i}.`;
+      m.layers.push({
+        ln1: st.vector(gpu, p + "input_layernorm.weight"),
+        ln2: st.vector(gpu, p + "post_attention_layernorm.weight"),
+        qn: st.vector(gpu, p + "self_attn.q_norm.weight"),
+        kn: st.vector(gpu, p + "self_attn.k_norm.weight"),
+        q: st.linear(gpu, p + "self_attn.q_proj."),
+        k: st.linear(gpu, p + "self_attn.k_proj."),
+        v: st.linear(gpu, p + "self_attn.v_proj."),
+        o: st.linear(gpu, p + "self_attn.o_proj."),
+        gate: st.linear(gpu, p + "mlp.gate_proj."),
+        up: st.linear(gpu, p + "mlp.up_proj."),
+        down: st.linear(gpu, p + "mlp.down_proj."),
+      });
+      if (onProgress) onProgress((i + 1) / QWEN3.layers);
+    }
+    m.norm = st.vector(gpu, "model.norm.weight");
+    m.embedRows = (ids) => st.rows("model.embed_tokens.weight", ids);
+    return m;
+  }
+
+  // Seeded random-init weights of the same architecture (bf16 linears, norm weights near 1, an
+  // embedding table of `vocab` rows held on the host); opts: { layers, vocab }.
+  static synthetic(gpu, src, opts) {
+    const o = opts || {};
+    const cfg = Object.assign({}, QWEN3, { layers: o.layers || QWEN3.layers, vocab: o.vocab || 4096 });
+    const m = new Qwen3(gpu, cfg);
+    const { hidden: D, heads: H, kvHeads: KH, headDim: HD, mlp: F } = cfg;
+    m.layers = [];
+    for (let i = 0; i < cfg.layers; i++) {
+      const p = `te.${i}.`;
+      m.layers.push({
+        ln1: src.vector(gpu, p + "ln1", D), ln2: src.vector(gpu, p + "ln2", D),
+        qn: src.vector(gpu, p + "qn", HD), kn: src.vector(gpu, p + "kn", HD),
+        q: src.bf16Linear(gpu, p + "q", H * HD, D, 1.0), k: src.bf16Linear(gpu, p + "k", KH * HD, D, 1.0),
+        v: src.bf16Linear(gpu, p + "v", KH * HD, D, 1.0), o: src.bf16Linear(gpu, p + "o", D, H * HD, 0.5),
+        gate: src.bf16Linear(gpu, p + "gate", F, D, 1.0), up: src.bf16Linear(gpu, p + "up", F, D, 1.0),
+        down: src.bf16Linear(gpu, p + "down", D, F, 0.5),
+      });
+    }
+    m.norm = src.vector(gpu, "te.norm", D);
+    const table = gpu.empty([cfg.vocab * D]);
+    src.fill(table, "f32", "te.embed", -1, 1);
+    m.table = table;
+    m.embedRows = async (ids) => {
+      const all = await gpu.read(table);
+      const out = new Float32Array(ids.length * D);
+      ids.forEach((id, i) => out.set(all.subarray(id * D, (id + 1) * D), i * D));
+      return out;
+    };
+    return m;
+  }
+
+  constructor(gpu, cfg) {
+    this.gpu = gpu;
+    this.cfg = cfg;
+    this.precision = "bf16"; // attention precision ("fp32": the fp32-MFMA kernel)
+  }
+
+  // ids -> Tensor [L, 1024] (qwen3.js:38-78)
+  async encode(ids) {
+    const gpu = this.gpu;
+    const { hidden: D, heads: H, kvHeads: KH, headDim: HD } = this.cfg;
+    const Lt = ids.length;
+    let x = gpu.fromArray(await this.embedRows(ids), [Lt, D]);
+    const cs = ropeTable(gpu, Lt, HD, this.cfg.theta);
+    for (const l of this.layers) {
+      const h = ops.rmsnorm(gpu, x, l.ln1, D);
+      const hr = ops.needsRotation(l.q) ? ops.rotate(gpu, h) : null;
+      const q = ops.linear(gpu, h, l.q, { xr: hr });
+      const k = ops.linear(gpu, h, l.k, { xr: hr });
+      const v = ops.linear(gpu, h, l.v, { xr: hr });
+      if (hr) hr.release();
+      h.release();
+      const qn = ops.rmsnorm(gpu, q, l.qn, HD);
+      const kn = ops.rmsnorm(gpu, k, l.kn, HD);
+      q.release();
+      k.release();
+      ops.rope(gpu, qn, cs, Lt, H, HD);
+      ops.rope(gpu, kn, cs, Lt, KH, HD);
+      const a = ops.attention(gpu, { q: qn, k: kn, v, Lq: Lt, Lk: Lt, H, D: HD, ldq: H * HD, ldk: KH * HD, ldv: KH * HD,
+        group: H / KH, causal: true, precision: this.precision });
+      qn.release();
+      kn.release();
+      v.release();
+      ops.linear(gpu, a, l.o, { out: x, resid: true });
+      a.release();
+      const h2 = ops.rmsnorm(gpu, x, l.ln2, D);
+      const h2r = ops.needsRotation(l.gate) ? ops.rotate(gpu, h2) : null;
+      const g = ops.linear(gpu, h2, l.gate, { xr: h2r });
+      const u = ops.linear(gpu, h2, l.up, { xr: h2r });
+      if (h2r) h2r.release();
+      h2.release();
+      const gu = ops.elementwise(gpu, "silu_mul", g, u);
+      g.release();
+      u.release();
+      ops.linear(gpu, gu, l.down, { out: x, resid: true });
+      gu.release();
+    }
+    cs.release();
+    const out = ops.rmsnorm(gpu, x, this.norm, D);
+    x.release();
+    return out;
+  }
+
+  release() {
+    const rel = (t) => {
+      if (!t) return;
+      if (t.buf && t.buf.release) t.buf.release();
+      else if (t.release) t.release();
+      for (const f of ["scale", "srel", "codebook", "bias"]) if (t[f] && t[f].release) t[f].release();
+    };
+    for (const l of this.layers || []) for (const key of Object.keys(l)) rel(l[key]);
+    rel(this.norm);
+    rel(this.table);
+    this.layers = [];
+  }
+}

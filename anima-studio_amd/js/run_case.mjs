@@ -18,6 +18,8 @@
 //              on a synthetic DiT, per sampler / scheduler / cfg
 //   graph      ForwardGraph replays against eager forwardDevice on a synthetic DiT: one replay per
 //              sigma, a new input latent and an eager forward before each
+//   qwen3      Qwen3.encode of a synthetic text encoder (both attention precisions) and its
+//              weights, for the oracle's restatement of qwen3.js
 
 import fs from "fs";
 import { GPU } from "./gpu.mjs";
@@ -29,6 +31,7 @@ import { SyntheticWeights } from "./weights.mjs";
 import { linearRegistry, loadLora, attachLoras, destroyLora, rotatedA } from "./lora.mjs";
 import { LatentPipeline } from "./pipeline.mjs";
 import { TorchGenerator } from "./rng.mjs";
+import { Qwen3 } from "./qwen3.mjs";
 
 const ARR = { f32: Float32Array, i8: Int8Array, u8: Uint8Array, u16: Uint16Array, i32: Int32Array };
 
@@ -200,6 +203,23 @@ async function main() {
     lat.release();
     cond.release();
     console.log(JSON.stringify({ graph: { diffs, n } }));
+  } else if (c.case === "qwen3") {
+    const te = Qwen3.synthetic(gpu, new SyntheticWeights(gpu, 17), { layers: c.layers, vocab: c.vocab });
+    for (const prec of ["fp32", "bf16"]) {
+      te.precision = prec;
+      const y = await te.encode(c.ids);
+      save(`${c.out}.${prec}`, await gpu.read(y));
+      y.release();
+    }
+    // a weight object holds its Tensor in .buf; a Tensor's .buf is its device address
+    const dump = async (name, t) => save(`${c.out}.w.${name}`, await gpu.read(typeof t.buf === "object" ? t.buf : t));
+    for (let i = 0; i < te.layers.length; i++) {
+      const l = te.layers[i];
+      for (const k of ["ln1", "ln2", "qn", "kn", "q", "k", "v", "o", "gate", "up", "down"]) await dump(`${i}.${k}`, l[k]);
+    }
+    await dump("norm", te.norm);
+    await dump("embed", te.table);
+    te.release();
   } else if (c.case === "lnmod") {
     const x = gpu.fromArray(load(c.x), [c.rows, c.cols]);
     const mod = gpu.upload(load(c.mod));

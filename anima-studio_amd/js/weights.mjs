@@ -93,6 +93,34 @@ export class SafeTensors {
     return gpu.upload(this.f32(name));
   }
 
+  // Rows `ids` of a 2D table (the token embedding) as one Float32Array [ids.length][dim],
+  // read row by row (app/weights.js:74-103): F32 / BF16 / F16, or a comfy_quant per-row int8
+  // table whose value is q * weight_scale[row].
+  async rows(name, ids) {
+    const base = name.slice(0, -"weight".length);
+    const t = this.info(name);
+    const dim = t.shape[1];
+    const out = new Float32Array(ids.length * dim);
+    const quant = this.has(base + "comfy_quant");
+    if (quant && t.dtype !== "I8") throw new Error(`unsupported quantized embedding ${base}`);
+    const scales = quant ? this.f32(base + "weight_scale") : null;
+    const rowBytes = dim * BYTES[t.dtype];
+    const buf = Buffer.alloc(rowBytes);
+    ids.forEach((id, i) => {
+      if (id < 0 || id >= t.shape[0]) throw new Error(`token id ${id} outside ${name} [${t.shape}]`);
+      const r = fs.readSync(this.fd, buf, 0, rowBytes, this.dataStart + t.data_offsets[0] + id * rowBytes);
+      if (r !== rowBytes) throw new Error(`short read of ${name} row ${id}`);
+      const u8 = new Uint8Array(buf.buffer.slice(buf.byteOffset, buf.byteOffset + rowBytes));
+      if (quant) {
+        const q = new Int8Array(u8.buffer);
+        for (let j = 0; j < dim; j++) out[i * dim + j] = q[j] * scales[id];
+      } else {
+        out.set(t.dtype === "BF16" ? bf16ToF32(u8) : t.dtype === "F16" ? f16ToF32(u8) : new Float32Array(u8.buffer), i * dim);
+      }
+    });
+    return out;
+  }
+
   linear(gpu, base) {
     const W = this.linearWeights(gpu, base);
     W.name = base.replace(/\.$/, "");

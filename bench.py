@@ -79,7 +79,8 @@ def dit_step(args):
 
     js = os.path.join(ROOT, "anima-studio_amd", "js", "bench_dit.mjs")
     r = subprocess.run(["node", js, "--steps", str(args.dit_steps), "--warmup", "1", "--graph", "--generate", "8",
-                        "--sampler", "euler_a", "--cfg", "4"], cwd=ROOT, capture_output=True, text=True, timeout=600)
+                        "--sampler", "euler_a", "--cfg", "4", "--text-encoder", "512"], cwd=ROOT, capture_output=True,
+                       text=True, timeout=600)
     if r.returncode != 0:
         raise RuntimeError("bench_dit.mjs failed: " + r.stderr[-2000:])
     d = json.loads(r.stdout.strip().splitlines()[-1])
@@ -97,7 +98,9 @@ def dit_step(args):
                       "step = timeCond + forward through node bench_dit.mjs",
             "steps": args.dit_steps,
             # an 8-step euler_a run with CFG 4: the device sampling loop vs the reference's host loop
-            "sampling": d.get("generate")}
+            "sampling": d.get("generate"),
+            # the text encoder (Qwen3, 28 layers, synthetic weights) on 512 tokens
+            "text_encoder": d.get("text_encoder")}
 
 
 def causal_attention(m, ctx, np):

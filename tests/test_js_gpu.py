@@ -283,3 +283,30 @@ def test_js_forward_graph(tmp_path):
         e, g = read(f"{out}.eager{i}"), read(f"{out}.graph{i}")
         assert np.array_equal(e, g) and np.isfinite(e).all() and np.abs(e).max() > 0
     assert not np.array_equal(read(f"{out}.eager0"), read(f"{out}.eager1"))
+
+
+def test_js_qwen3_text_encoder(tmp_path):
+    """Qwen3.encode (js/qwen3.mjs, the reference's qwen3.js forward on this build's ops: causal GQA
+    attention on the flash kernels, bf16 linears on the fp32 matrix cores, RMSNorm, 1D RoPE,
+    SiLU * up) on a seeded 2-layer synthetic encoder against the oracle's float64 restatement fed
+    the same weights: fp32 attention within 1e-5 relative L2, bf16 attention within 1e-2."""
+    from oracle import qwen3_ref
+
+    out = str(tmp_path / "te")
+    ids = [int(x) for x in np.random.default_rng(5).integers(0, 97, size=37)]
+    run_case(tmp_path, {"case": "qwen3", "layers": 2, "vocab": 97, "ids": ids, "out": out})
+    D, H, KH, Dh, F = 1024, 16, 8, 128, 3072
+    shapes = {"q": (H * Dh, D), "k": (KH * Dh, D), "v": (KH * Dh, D), "o": (D, H * Dh), "gate": (F, D), "up": (F, D),
+              "down": (D, F)}
+    W = {"norm": read(f"{out}.w.norm").astype(np.float64), "embed": read(f"{out}.w.embed").reshape(97, D).astype(np.float64)}
+    for i in range(2):
+        for n in ("ln1", "ln2", "qn", "kn"):
+            W[f"{i}.{n}"] = read(f"{out}.w.{i}.{n}").astype(np.float64)
+        for n, shp in shapes.items():
+            bits = read(f"{out}.w.{i}.{n}", np.uint16).astype(np.uint32) << 16
+            W[f"{i}.{n}"] = bits.view(np.float32).reshape(shp).astype(np.float64)
+    ref = qwen3_ref.encode(W, ids, 2)
+    got32, got16 = read(f"{out}.fp32").reshape(len(ids), D), read(f"{out}.bf16").reshape(len(ids), D)
+    assert np.isfinite(got32).all() and np.isfinite(got16).all()
+    assert report("qwen3 fp32 attention vs float64", got32, ref)[0] <= 1e-5
+    assert report("qwen3 bf16 attention vs float64", got16, ref)[0] <= 1e-2
