@@ -8,7 +8,7 @@
 
 import * as ops from "./ops.mjs";
 import { concatLinears } from "./weights.mjs";
-import { ditRopeTable, timestepEmbedding } from "./common.mjs";
+import { ditRopeTable, ropeTable, timestepEmbedding } from "./common.mjs";
 import { native } from "./gpu.mjs";
 
 const D = 2048;
@@ -421,4 +421,120 @@ export class ForwardGraph {
     if (this.tc) this.tc.release();
     this.tc = null;
   }
+}
+
+// ------------------------------------------------------------------ LLM adapter
+// Maps the text encoder's hidden states and T5 token ids to the DiT's [512, 1024] context
+// (app/models/dit.js:136-190; tools/reference.py:141-169): 6 blocks of RMSNorm -> self-attention
+// over the T5 tokens, RMSNorm -> cross-attention to the text encoder's tokens (16 heads x 64,
+// q/k RMSNorm, 1D RoPE theta 1e4 on both sides), RMSNorm -> GELU MLP (biased); then out_proj,
+// RMSNorm, the per-token prompt weights, zero rows up to 512.
+export const ADAPTER = { blocks: 6, dim: 1024, heads: 16, headDim: 64, mlp: 4096, theta: 1e4, ctxLen: 512 };
+
+// Adapter weights in the reference's names (app/models/dit.js:13-22, 84-100).
+export function loadAdapter(gpu, st) {
+  const attn = (p) => ({
+    q: st.linear(gpu, p + "q_proj."), k: st.linear(gpu, p + "k_proj."), v: st.linear(gpu, p + "v_proj."),
+    o: st.linear(gpu, p + "o_proj."), qn: st.vector(gpu, p + "q_norm.weight"), kn: st.vector(gpu, p + "k_norm.weight"),
+  });
+  const A = { blocks: [] };
+  for (let i = 0; i < ADAPTER.blocks; i++) {
+    const p = `llm_adapter.blocks.${i}.`;
+    A.blocks.push({
+      nSelf: st.vector(gpu, p + "norm_self_attn.weight"), nCross: st.vector(gpu, p + "norm_cross_attn.weight"),
+      nMlp: st.vector(gpu, p + "norm_mlp.weight"), self: attn(p + "self_attn."), cross: attn(p + "cross_attn."),
+      mlp0: st.linear(gpu, p + "mlp.0."), mlp2: st.linear(gpu, p + "mlp.2."),
+    });
+  }
+  A.outProj = st.linear(gpu, "llm_adapter.out_proj.");
+  A.norm = st.vector(gpu, "llm_adapter.norm.weight");
+  A.embedRows = (ids) => st.rows("llm_adapter.embed.weight", ids);
+  return A;
+}
+
+// Seeded random-init adapter (bf16 linears, biases on the MLP and out_proj as in the checkpoint,
+// an embedding table of `vocab` rows); opts: { blocks, vocab }.
+export function syntheticAdapter(gpu, src, opts) {
+  const o = opts || {};
+  const D = ADAPTER.dim, F = ADAPTER.mlp, HD = ADAPTER.headDim;
+  const lin = (name, N, K, gain, bias) => {
+    const W = src.bf16Linear(gpu, name, N, K, gain);
+    if (bias) W.bias = src.vector(gpu, name + ".bias", N, -0.02, 0.02);
+    return W;
+  };
+  const attn = (p) => ({
+    q: lin(p + "q", D, D, 1.0), k: lin(p + "k", D, D, 1.0), v: lin(p + "v", D, D, 1.0), o: lin(p + "o", D, D, 0.5),
+    qn: src.vector(gpu, p + "qn", HD), kn: src.vector(gpu, p + "kn", HD),
+  });
+  const A = { blocks: [] };
+  for (let i = 0; i < (o.blocks || ADAPTER.blocks); i++) {
+    const p = `ad.${i}.`;
+    A.blocks.push({
+      nSelf: src.vector(gpu, p + "ns", D), nCross: src.vector(gpu, p + "nc", D), nMlp: src.vector(gpu, p + "nm", D),
+      self: attn(p + "s."), cross: attn(p + "c."), mlp0: lin(p + "m0", F, D, 1.0, true), mlp2: lin(p + "m2", D, F, 0.5, true),
+    });
+  }
+  A.outProj = lin("ad.out", D, D, 1.0, true);
+  A.norm = src.vector(gpu, "ad.norm", D);
+  const vocab = o.vocab || 1024;
+  A.table = src.fill(gpu.empty([vocab * D]), "f32", "ad.embed", -1, 1);
+  A.embedRows = async (ids) => {
+    const all = await gpu.read(A.table);
+    const out = new Float32Array(ids.length * D);
+    ids.forEach((id, i) => out.set(all.subarray(id * D, (id + 1) * D), i * D));
+    return out;
+  };
+  return A;
+}
+
+// hidden: Tensor [Ls, 1024] from the text encoder; t5Ids / t5Weights: arrays.  Returns the context
+// Tensor [max(512, Lt), 1024] (app/models/dit.js:136-190).  precision: attention precision.
+export async function adapt(gpu, A, hidden, t5Ids, t5Weights, precision) {
+  const D = ADAPTER.dim, H = ADAPTER.heads, HD = ADAPTER.headDim;
+  const Lt = t5Ids.length, Ls = hidden.shape[0];
+  const x = gpu.fromArray(await A.embedRows(t5Ids), [Lt, D]);
+  const csT = ropeTable(gpu, Lt, HD, ADAPTER.theta);
+  const csS = ropeTable(gpu, Ls, HD, ADAPTER.theta);
+  const attn = (w, xq, ctx, Lq, Lk, csQ, csK) => {
+    const q = ops.linear(gpu, xq, w.q);
+    const k = ops.linear(gpu, ctx, w.k);
+    const v = ops.linear(gpu, ctx, w.v);
+    const qn = ops.rmsnorm(gpu, q, w.qn, HD);
+    const kn = ops.rmsnorm(gpu, k, w.kn, HD);
+    q.release();
+    k.release();
+    ops.rope(gpu, qn, csQ, Lq, H, HD);
+    ops.rope(gpu, kn, csK, Lk, H, HD);
+    const a = ops.attention(gpu, { q: qn, k: kn, v, Lq, Lk, H, D: HD, ldq: D, ldk: D, ldv: D, precision });
+    releaseAll([qn, kn, v]);
+    ops.linear(gpu, a, w.o, { out: x, resid: true });
+    a.release();
+  };
+  for (const b of A.blocks) {
+    let n = ops.rmsnorm(gpu, x, b.nSelf, D);
+    attn(b.self, n, n, Lt, Lt, csT, csT);
+    n.release();
+    n = ops.rmsnorm(gpu, x, b.nCross, D);
+    attn(b.cross, n, hidden, Lt, Ls, csT, csS);
+    n.release();
+    n = ops.rmsnorm(gpu, x, b.nMlp, D);
+    const h = ops.linear(gpu, n, b.mlp0, { act: "gelu" });
+    n.release();
+    ops.linear(gpu, h, b.mlp2, { out: x, resid: true });
+    h.release();
+  }
+  releaseAll([csT, csS]);
+  const o = ops.linear(gpu, x, A.outProj);
+  x.release();
+  const on = ops.rmsnorm(gpu, o, A.norm, D);
+  o.release();
+  // prompt weights and zero rows up to 512 (on the host, as the reference: tiny)
+  const vals = await gpu.read(on);
+  on.release();
+  const ctx = new Float32Array(Math.max(ADAPTER.ctxLen, Lt) * D);
+  for (let i = 0; i < Lt; i++) {
+    const w = t5Weights ? t5Weights[i] : 1;
+    for (let j = 0; j < D; j++) ctx[i * D + j] = vals[i * D + j] * w;
+  }
+  return gpu.fromArray(ctx, [ctx.length / D, D]);
 }

@@ -20,13 +20,15 @@
 //              sigma, a new input latent and an eager forward before each
 //   qwen3      Qwen3.encode of a synthetic text encoder (both attention precisions) and its
 //              weights, for the oracle's restatement of qwen3.js
+//   adapter    the LLM adapter (dit.mjs adapt) on a synthetic adapter, both attention precisions,
+//              and its weights
 
 import fs from "fs";
 import { GPU } from "./gpu.mjs";
 import * as ops from "./ops.mjs";
 import { ditRopeTable } from "./common.mjs";
 import { SafeTensors } from "./weights.mjs";
-import { AnimaDiT, ForwardGraph } from "./dit.mjs";
+import { AnimaDiT, ForwardGraph, syntheticAdapter, adapt } from "./dit.mjs";
 import { SyntheticWeights } from "./weights.mjs";
 import { linearRegistry, loadLora, attachLoras, destroyLora, rotatedA } from "./lora.mjs";
 import { LatentPipeline } from "./pipeline.mjs";
@@ -220,6 +222,29 @@ async function main() {
     await dump("norm", te.norm);
     await dump("embed", te.table);
     te.release();
+  } else if (c.case === "adapter") {
+    const A = syntheticAdapter(gpu, new SyntheticWeights(gpu, 23), { blocks: c.blocks, vocab: c.vocab });
+    const hidden = gpu.fromArray(new TorchGenerator(24).randn(c.Ls * 1024), [c.Ls, 1024]);
+    for (const prec of ["fp32", "bf16"]) {
+      const y = await adapt(gpu, A, hidden, c.ids, c.weights, prec);
+      save(`${c.out}.${prec}`, await gpu.read(y));
+      y.release();
+    }
+    save(`${c.out}.hidden`, await gpu.read(hidden));
+    const dump = async (name, t) => save(`${c.out}.w.${name}`, await gpu.read(typeof t.buf === "object" ? t.buf : t));
+    for (let i = 0; i < A.blocks.length; i++) {
+      const b = A.blocks[i];
+      for (const k of ["nSelf", "nCross", "nMlp"]) await dump(`${i}.${k}`, b[k]);
+      for (const a of ["self", "cross"]) for (const k of ["q", "k", "v", "o", "qn", "kn"]) await dump(`${i}.${a}.${k}`, b[a][k]);
+      for (const k of ["mlp0", "mlp2"]) {
+        await dump(`${i}.${k}`, b[k]);
+        await dump(`${i}.${k}.bias`, b[k].bias);
+      }
+    }
+    await dump("out", A.outProj);
+    await dump("out.bias", A.outProj.bias);
+    await dump("norm", A.norm);
+    await dump("embed", A.table);
   } else if (c.case === "lnmod") {
     const x = gpu.fromArray(load(c.x), [c.rows, c.cols]);
     const mod = gpu.upload(load(c.mod));

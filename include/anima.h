@@ -101,7 +101,8 @@ int anima_graph_destroy(anima_ctx* ctx, anima_graph* graph);
 #define ANIMA_PREC_FP32 1 /* fp32 MFMA (tolerance variant) */
 
 typedef struct {
-  int B, Lq, Lk, H, D; /* D == 128 */
+  int B, Lq, Lk, H, D; /* D == 128, or 64 (the LLM adapter's heads, zero-padded to 128 inside the
+                        * call: no fused norm / RoPE / prepared K/V with D == 64) */
   int group;           /* q heads per kv head (1 = MHA); 0 is read as 1 */
   const float* q;
   int64_t ldq, q_off, q_bstride;

@@ -258,6 +258,30 @@ def test_causal_gqa_attention(ctx, L, B, precision):
         assert np.allclose(got[:, 0, hh * HD:(hh + 1) * HD], v[:, 0, kvh * HD:(kvh + 1) * HD], rtol=1e-2 if precision == "bf16" else 1e-6, atol=1e-2 if precision == "bf16" else 1e-6)
 
 
+@pytest.mark.parametrize("precision", ["bf16", "fp32"])
+def test_head_dim_64_attention(ctx, precision):
+    """D = 64, the LLM adapter's attention (app/models/dit.js:147-160: 16 heads x 64 in 1024
+    columns; its cross-attention to the text encoder's tokens): heads zero-padded to 128 inside the
+    call, scale 1/8, against the oracle at D = 64 (self Lq = Lk = 77 and cross Lq = 32, Lk = 100)."""
+    case(f"attention D=64 {precision}")
+    m = amd()
+    H, D = 16, 64
+    prec = m.PREC_FP32 if precision == "fp32" else m.PREC_BF16
+    for Lq, Lk, seed in ((77, 77, 41), (32, 100, 42)):
+        q = orc.randn(seed, Lq * H * D).reshape(Lq, H * D)
+        k = orc.randn(seed + 1, Lk * H * D).reshape(Lk, H * D)
+        v = orc.randn(seed + 2, Lk * H * D).reshape(Lk, H * D)
+        dq, dk, dv, do = ctx.upload(q), ctx.upload(k), ctx.upload(v), ctx.empty((Lq, H * D))
+        ctx.attention(q=dq, k=dk, v=dv, o=do, B=1, Lq=Lq, Lk=Lk, H=H, D=D, ldq=H * D, ldk=H * D, ldv=H * D, precision=prec)
+        got = do.numpy()
+        for x in (dq, dk, dv, do):
+            x.release()
+        args = dict(B=1, Lq=Lq, Lk=Lk, H=H, D=D, ldq=H * D, ldk=H * D, ldv=H * D)
+        ref = orc.attention("f64", q, k, v, **args)[0]
+        r, mx = report(f"D=64 Lq={Lq} Lk={Lk} {precision} vs fp64", got, ref)
+        assert r <= (1e-5 if precision == "fp32" else 1e-2)
+
+
 # ------------------------------------------------------------------ ragged shapes, GQA, strides
 
 @pytest.mark.parametrize("precision", ["bf16", "fp32"])
@@ -425,7 +449,7 @@ def test_attention_rejects_bad_arguments(ctx):
     d = ctx.empty((64, 3 * 128))
     base = dict(q=d, k=d, v=d, o=d, B=1, Lq=64, Lk=64, H=1, D=128, ldq=384, ldk=384, ldv=384, ldo=384)
     with pytest.raises(m.AnimaError) as e:
-        ctx.attention(**{**base, "D": 64, "ldo": 384})
+        ctx.attention(**{**base, "D": 96, "ldo": 384})
     assert e.value.code == -5
     with pytest.raises(m.AnimaError) as e:
         ctx.attention(**{**base, "ldq": 386})

@@ -310,3 +310,40 @@ def test_js_qwen3_text_encoder(tmp_path):
     assert np.isfinite(got32).all() and np.isfinite(got16).all()
     assert report("qwen3 fp32 attention vs float64", got32, ref)[0] <= 1e-5
     assert report("qwen3 bf16 attention vs float64", got16, ref)[0] <= 1e-2
+
+
+def test_js_llm_adapter(tmp_path):
+    """The LLM adapter (js/dit.mjs adapt: self- and cross-attention with 16 x 64 heads on the
+    padded D = 64 path, q/k RMSNorm, 1D RoPE, biased GELU MLP, out_proj, norm, prompt weights,
+    zero rows to 512) on a seeded 2-block synthetic adapter against the oracle's float64
+    restatement fed the same weights and text-encoder states."""
+    from oracle import adapter_ref
+
+    out = str(tmp_path / "ad")
+    rng = np.random.default_rng(7)
+    ids = [int(x) for x in rng.integers(0, 64, size=19)]
+    weights = [float(x) for x in rng.uniform(0.5, 1.5, size=19)]
+    run_case(tmp_path, {"case": "adapter", "blocks": 2, "vocab": 64, "Ls": 23, "ids": ids, "weights": weights, "out": out})
+    D, F = 1024, 4096
+    f64 = lambda name, shp=None: read(f"{out}.w.{name}").astype(np.float64).reshape(shp if shp else -1)
+
+    def bf(name, shp):
+        return (read(f"{out}.w.{name}", np.uint16).astype(np.uint32) << 16).view(np.float32).reshape(shp).astype(np.float64)
+
+    W = {"embed": f64("embed", (64, D)), "norm": f64("norm"), "out": bf("out", (D, D)), "out.bias": f64("out.bias")}
+    for i in range(2):
+        for n in ("nSelf", "nCross", "nMlp"):
+            W[f"{i}.{n}"] = f64(f"{i}.{n}")
+        for a in ("self", "cross"):
+            for n in ("q", "k", "v", "o"):
+                W[f"{i}.{a}.{n}"] = bf(f"{i}.{a}.{n}", (D, D))
+            for n in ("qn", "kn"):
+                W[f"{i}.{a}.{n}"] = f64(f"{i}.{a}.{n}")
+        W[f"{i}.mlp0"], W[f"{i}.mlp2"] = bf(f"{i}.mlp0", (F, D)), bf(f"{i}.mlp2", (D, F))
+        W[f"{i}.mlp0.bias"], W[f"{i}.mlp2.bias"] = f64(f"{i}.mlp0.bias"), f64(f"{i}.mlp2.bias")
+    hidden = read(f"{out}.hidden").reshape(23, D).astype(np.float64)
+    ref = adapter_ref.adapt(W, hidden, ids, weights, 2)
+    for prec, tol in (("fp32", 1e-5), ("bf16", 1e-2)):
+        got = read(f"{out}.{prec}").reshape(512, D)
+        assert np.all(got[19:] == 0)
+        assert report(f"adapter {prec} attention vs float64", got[:19], ref[:19])[0] <= tol
