@@ -22,6 +22,8 @@
 //              weights, for the oracle's restatement of qwen3.js
 //   adapter    the LLM adapter (dit.mjs adapt) on a synthetic adapter, both attention precisions,
 //              and its weights
+//   chain      prompt tokens -> Qwen3.encode -> adapt -> prepareContext -> forward (synthetic
+//              weights, cond + uncond prompts), the velocities
 
 import fs from "fs";
 import { GPU } from "./gpu.mjs";
@@ -245,6 +247,25 @@ async function main() {
     await dump("out.bias", A.outProj.bias);
     await dump("norm", A.norm);
     await dump("embed", A.table);
+  } else if (c.case === "chain") {
+    const te = Qwen3.synthetic(gpu, new SyntheticWeights(gpu, 31), { layers: 2, vocab: 97 });
+    const A = syntheticAdapter(gpu, new SyntheticWeights(gpu, 32), { blocks: 2, vocab: 64 });
+    const dit = AnimaDiT.synthetic(gpu, new SyntheticWeights(gpu, 33, { mode: "int8", blocks: 1 }));
+    const ctxs = [];
+    for (const p of c.prompts) {
+      const hidden = await te.encode(p.qwen);
+      ctxs.push(await adapt(gpu, A, hidden, p.t5, p.weights));
+      hidden.release();
+    }
+    const cond = dit.prepareContext(ctxs);
+    const tc = dit.timeCond(0.7);
+    const hw = c.size / 8, per = 16 * hw * hw;
+    const lat = [0, 1].map((b) => new TorchGenerator(40 + b).randn(per));
+    const v = await dit.forward(lat, hw, hw, cond, tc);
+    v.forEach((vb, b) => save(`${c.out}.${b}`, vb));
+    tc.release();
+    cond.release();
+    te.release();
   } else if (c.case === "lnmod") {
     const x = gpu.fromArray(load(c.x), [c.rows, c.cols]);
     const mod = gpu.upload(load(c.mod));

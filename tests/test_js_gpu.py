@@ -347,3 +347,17 @@ def test_js_llm_adapter(tmp_path):
         got = read(f"{out}.{prec}").reshape(512, D)
         assert np.all(got[19:] == 0)
         assert report(f"adapter {prec} attention vs float64", got[:19], ref[:19])[0] <= tol
+
+
+def test_js_prompt_to_velocity_chain(tmp_path):
+    """The conditioning chain on the device path: prompt token ids -> Qwen3.encode -> the LLM
+    adapter -> prepareContext -> one DiT forward (synthetic 2-layer encoder, 2-block adapter,
+    1-block int8 DiT at 64x64, cond + uncond prompts of different lengths): finite velocities,
+    different for the two prompts.  Each stage's parity is checked by its own test."""
+    out = str(tmp_path / "ch")
+    prompts = [{"qwen": [3, 17, 5, 88, 41, 9, 60], "t5": [1, 5, 9, 33, 2], "weights": [1, 1, 1.2, 1, 0.8]},
+               {"qwen": [7, 7, 21], "t5": [4, 2], "weights": [1, 1]}]
+    run_case(tmp_path, {"case": "chain", "prompts": prompts, "size": 64, "out": out})
+    v0, v1 = read(f"{out}.0"), read(f"{out}.1")
+    assert v0.size == 16 * 8 * 8 and np.isfinite(v0).all() and np.isfinite(v1).all()
+    assert np.abs(v0).max() > 0 and not np.array_equal(v0, v1)
