@@ -253,7 +253,7 @@ function attnDesc(a, B, H, D, o, extra) {
   }, extra);
 }
 
-// VAE / text-encoder ops of the reference are outside the DiT attention path.
+// The VAE's ops (conv3x3, channelNorm: app/gpu/ops.js:97-109) are not built yet.
 export function conv3x3() {
   throw new Error("conv3x3 (VAE) is not part of this build");
 }
