@@ -51,6 +51,7 @@ class AttnDesc(ctypes.Structure):
         ("eps", ctypes.c_float),
         ("causal", ctypes.c_int),
         ("kv_prep", _vp),
+        ("kv_prep_bytes", _i64),
     ]
 
 
@@ -119,6 +120,7 @@ def lib():
         L.anima_linear.argtypes = [_vp, ctypes.POINTER(LinearDesc)]
         L.anima_sampler_step.argtypes = [_vp, ctypes.POINTER(SamplerDesc)]
         L.anima_split3_bf16.argtypes = [_vp, _vp, _vp, _i64]
+        L.anima_fill_random.argtypes = [_vp, _vp, _i64, ctypes.c_int, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]
         L.anima_graph_begin.argtypes = [_vp]
         L.anima_graph_end.argtypes = [_vp, P(_vp)]
         L.anima_graph_launch.argtypes = [_vp, _vp]
@@ -255,9 +257,10 @@ class Context:
     def attention(self, *, q, k, v, o, B, Lq, Lk, H, D, ldq, ldk, ldv, ldo=None, q_off=0, k_off=0, v_off=0,
                   o_off=0, q_bstride=None, k_bstride=None, v_bstride=None, o_bstride=None, group=1, scale=0.0,
                   kv_len=None, precision=PREC_BF16, q_norm=None, k_norm=None, rope_cs=None, rope_sin_off=0,
-                  eps=1e-6, causal=0, kv_prep=None, prepare_into=None):
+                  eps=1e-6, causal=0, kv_prep=None, prepare_into=None, kv_prep_bytes=None):
         """anima_attention; kv_prep: K/V converted by a call with prepare_into (which runs
-        anima_attention_prepare_kv into that buffer instead of the attention)."""
+        anima_attention_prepare_kv into that buffer instead of the attention).  kv_prep_bytes
+        defaults to the size the call's shape and precision take."""
         ldo = ldo if ldo is not None else H * D
         kl = (ctypes.c_int * B)(*[int(x) for x in kv_len]) if kv_len is not None else None
         d = AttnDesc(B=B, Lq=Lq, Lk=Lk, H=H, D=D, group=group,
@@ -267,7 +270,10 @@ class Context:
                      o=_ptr(o), ldo=ldo, o_off=o_off, o_bstride=o_bstride if o_bstride is not None else Lq * ldo,
                      scale=scale, kv_len=ctypes.cast(kl, ctypes.POINTER(ctypes.c_int)) if kl is not None else None,
                      precision=precision, q_norm=_ptr(q_norm), k_norm=_ptr(k_norm), rope_cs=_ptr(rope_cs),
-                     rope_sin_off=rope_sin_off, eps=eps, causal=causal, kv_prep=_ptr(kv_prep))
+                     rope_sin_off=rope_sin_off, eps=eps, causal=causal, kv_prep=_ptr(kv_prep),
+                     kv_prep_bytes=kv_prep_bytes if kv_prep_bytes is not None else
+                     (self.attention_kv_bytes(B, H // max(group, 1), Lk, precision)
+                      if (kv_prep is not None or prepare_into is not None) else 0))
         if prepare_into is not None:
             return self._check(lib().anima_attention_prepare_kv(self.h, ctypes.byref(d), _ptr(prepare_into)))
         return self._check(lib().anima_attention(self.h, ctypes.byref(d)))
@@ -275,6 +281,12 @@ class Context:
     @staticmethod
     def attention_kv_bytes(B, Hkv, Lk, precision=PREC_BF16):
         return lib().anima_attention_kv_bytes(B, Hkv, Lk, precision)
+
+    FILL = {"u8": 0, "i8n": 1, "f32": 2, "bf16": 3, "f32n": 4}
+
+    def fill_random(self, dst, n, kind, seed, lo, hi):
+        """anima_fill_random: the seeded synthetic fill (kind "u8" / "i8n" / "f32" / "bf16" / "f32n")."""
+        return self._check(lib().anima_fill_random(self.h, _ptr(dst), n, self.FILL[kind], seed, lo, hi))
 
     def hadamard(self, x, y, n):
         return self._check(lib().anima_hadamard(self.h, _ptr(x), _ptr(y), n))
@@ -345,7 +357,7 @@ def weight(kind, N, K, w, scale=None, srel=None, codebook=None, bias=None):
 
 
 def dit_rope_angles(Hp: int, Wp: int) -> np.ndarray:
-    """Angles [Hp*Wp][64] of the 3D Cosmos RoPE for one frame (app/models/common.js:238-260):
+    """Angles [Hp*Wp][64] of the 3D Cosmos RoPE for one frame (app/models/common.js:31-52):
     slots 0..21 temporal at t=0 (angle 0), 22..42 row * hf[j], 43..63 column * hf[j],
     hf[j] = 1 / h_theta^(2j/42) with h_theta = 1e4 * 4^(42/40) (NTK-scaled)."""
     dim_h = 42
@@ -361,7 +373,7 @@ def dit_rope_angles(Hp: int, Wp: int) -> np.ndarray:
 
 
 def rope_table(angles: np.ndarray) -> np.ndarray:
-    """cos block then sin block, flat [2*L*half]; sin offset L*half (app/models/common.js:211-220)."""
+    """cos block then sin block, flat [2*L*half]; sin offset L*half (app/models/common.js:3-12)."""
     a = np.asarray(angles, np.float64)
     return np.concatenate([np.cos(a).reshape(-1), np.sin(a).reshape(-1)]).astype(np.float32)
 

@@ -992,6 +992,10 @@ static int attention_check(anima_ctx* c, const anima_attn_desc* d, int (&kv_len)
     kv_len[b] = d->kv_len ? d->kv_len[b] : d->Lk;
     if (kv_len[b] < 1 || kv_len[b] > d->Lk) return fail(c, ANIMA_E_ARG, "anima_attention: kv_len[%d]=%d outside [1, Lk=%d]", b, kv_len[b], d->Lk);
   }
+  if (prepared && d->kv_prep_bytes != attention_kv_bytes(d->B, d->H / group, d->Lk, d->precision))
+    return fail(c, ANIMA_E_ARG, "anima_attention: kv_prep_bytes=%lld, but B=%d, %d kv heads, Lk=%d at this precision take %lld",
+                (long long)d->kv_prep_bytes, d->B, d->H / group, d->Lk,
+                (long long)attention_kv_bytes(d->B, d->H / group, d->Lk, d->precision));
   const bool rope = d->rope_cs != nullptr;
   if (rope) {
     const int64_t rows = d->rope_sin_off / (HD / 2);
@@ -1216,6 +1220,10 @@ int attention_prepare_kv_launch(anima_ctx* c, const anima_attn_desc* d, void* ds
   if (!d || !dst) return fail(c, ANIMA_E_ARG, "anima_attention_prepare_kv: null descriptor or output");
   if (d->kv_prep) return fail(c, ANIMA_E_ARG, "anima_attention_prepare_kv: desc->kv_prep must be NULL");
   if (!al16(dst)) return fail(c, ANIMA_E_ARG, "anima_attention_prepare_kv: kv_prep must be 16-byte aligned");
+  const int group = d->group <= 0 ? 1 : d->group;
+  if (d->kv_prep_bytes != attention_kv_bytes(d->B, d->H / group, d->Lk, d->precision))
+    return fail(c, ANIMA_E_ARG, "anima_attention_prepare_kv: kv_prep_bytes=%lld, the layout takes %lld",
+                (long long)d->kv_prep_bytes, (long long)attention_kv_bytes(d->B, d->H / group, d->Lk, d->precision));
   int kv_len[MAXB];
   int rc = attention_check(c, d, kv_len);  // the full call's checks (q / o included)
   if (rc) return rc;

@@ -9,6 +9,7 @@
 #include <node_api.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "../../include/anima.h"
@@ -21,6 +22,8 @@
     }                                                           \
   } while (0)
 
+static int g_bad_arg = 0; /* a RangeError is pending from num() */
+
 static napi_value throw_status(napi_env env, anima_ctx* c, int rc) {
   char msg[1200];
   snprintf(msg, sizeof msg, "anima error %d: %s", rc, anima_last_error(c));
@@ -28,9 +31,13 @@ static napi_value throw_status(napi_env env, anima_ctx* c, int rc) {
   return NULL;
 }
 
+/* Runs an ABI call; a RangeError raised while converting its arguments (or earlier in the same
+ * binding: descriptor fields) stops the binding before the call. */
 #define CHECK_RC(env, c, expr)                   \
   do {                                           \
+    if (g_bad_arg) { g_bad_arg = 0; return NULL; } \
     int rc_ = (expr);                            \
+    if (bad_arg()) return NULL;                  \
     if (rc_ != ANIMA_OK) return throw_status(env, c, rc_); \
   } while (0)
 
@@ -47,11 +54,25 @@ static int is_nullish(napi_env env, napi_value v) {
   return t == napi_undefined || t == napi_null;
 }
 
+/* Numbers crossing into the C ABI: undefined / null read as 0; anything else must be a finite
+ * Number (a NaN or an infinity cast to an integer type is undefined behaviour in C), otherwise a
+ * RangeError is raised and 0 returned; CHECK_RC then skips the call. */
 static double num(napi_env env, napi_value v) {
   double d = 0;
   if (is_nullish(env, v)) return 0;
-  napi_get_value_double(env, v, &d);
+  if (napi_get_value_double(env, v, &d) != napi_ok || !(d == d) || d > 9.3e18 || d < -9.3e18) {
+    if (!g_bad_arg) napi_throw_range_error(env, NULL, "expected a finite Number argument");
+    g_bad_arg = 1;
+    return 0;
+  }
   return d;
+}
+
+/* Pending RangeError from num(): clears the flag and reports whether the call must stop. */
+static int bad_arg(void) {
+  int b = g_bad_arg;
+  g_bad_arg = 0;
+  return b;
 }
 
 static int64_t i64(napi_env env, napi_value v) { return (int64_t)num(env, v); }
@@ -105,6 +126,17 @@ static int typed(napi_env env, napi_value v, void** data, size_t* bytes) {
 
 /* ------------------------------------------------------------------ runtime */
 
+#define MAX_CTX 64
+static anima_ctx* g_ctx[MAX_CTX]; /* contexts created by init() and not yet destroyed */
+static double g_finalized = 0;    /* buffers reclaimed by finalizers (leak guard, for tests) */
+
+static int ctx_live(anima_ctx* c) {
+  for (int i = 0; i < MAX_CTX; i++)
+    if (c && g_ctx[i] == c) return 1;
+  return 0;
+}
+
+
 static void ctx_finalize(napi_env env, void* data, void* hint) {
   (void)env;
   (void)hint;
@@ -115,7 +147,13 @@ static napi_value js_init(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   get_args(env, info, 1, argv);
   anima_ctx* c = NULL;
-  CHECK_RC(env, NULL, anima_init((int)num(env, argv[0]), &c));
+  int dev = (int)num(env, argv[0]);
+  CHECK_RC(env, NULL, anima_init(dev, &c));
+  for (int i = 0; i < MAX_CTX; i++)
+    if (!g_ctx[i]) {
+      g_ctx[i] = c;
+      break;
+    }
   napi_value ext;
   NAPI_CALL(env, napi_create_external(env, c, ctx_finalize, NULL, &ext));
   return ext;
@@ -124,7 +162,10 @@ static napi_value js_init(napi_env env, napi_callback_info info) {
 static napi_value js_destroy(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   get_args(env, info, 1, argv);
-  anima_destroy(ctx_of(env, argv[0]));
+  anima_ctx* c = ctx_of(env, argv[0]);
+  for (int i = 0; i < MAX_CTX; i++)
+    if (g_ctx[i] == c) g_ctx[i] = NULL;
+  anima_destroy(c);
   return NULL;
 }
 
@@ -141,7 +182,8 @@ static napi_value js_alloc(napi_env env, napi_callback_info info) {
   get_args(env, info, 2, argv);
   anima_ctx* c = ctx_of(env, argv[0]);
   void* p = NULL;
-  CHECK_RC(env, c, anima_alloc(c, (size_t)num(env, argv[1]), &p));
+  size_t bytes = (size_t)num(env, argv[1]);
+  CHECK_RC(env, c, anima_alloc(c, bytes, &p));
   return make_num(env, (double)(uintptr_t)p);
 }
 
@@ -151,6 +193,90 @@ static napi_value js_free(napi_env env, napi_callback_info info) {
   anima_ctx* c = ctx_of(env, argv[0]);
   CHECK_RC(env, c, anima_free(c, ptr(env, argv[1])));
   return NULL;
+}
+
+/* Device buffers owned by JS Tensors: an external whose finalizer returns the buffer to the pool
+ * when the Tensor is garbage-collected without release() (the reference's buffers are reclaimed
+ * by WebGPU the same way, app/gpu/device.js:10-24).  release() frees it at once and disarms the
+ * finalizer.  Contexts destroyed in between are skipped (their memory is already gone). */
+typedef struct dev_buf {
+  anima_ctx* c;
+  void* p;
+  int live;
+} dev_buf;
+
+static void buf_finalize(napi_env env, void* data, void* hint) {
+  (void)env;
+  (void)hint;
+  dev_buf* b = (dev_buf*)data;
+  if (b->live && ctx_live(b->c) && anima_free(b->c, b->p) == ANIMA_OK) g_finalized += 1;
+  free(b);
+}
+
+/* allocHandle(ctx, bytes) -> external (the buffer's owner) */
+static napi_value js_alloc_handle(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  size_t bytes = (size_t)num(env, argv[1]);
+  void* p = NULL;
+  CHECK_RC(env, c, anima_alloc(c, bytes, &p));
+  dev_buf* b = (dev_buf*)malloc(sizeof *b);
+  if (!b) {
+    anima_free(c, p);
+    napi_throw_error(env, NULL, "allocHandle: out of host memory");
+    return NULL;
+  }
+  b->c = c;
+  b->p = p;
+  b->live = 1;
+  napi_value ext;
+  if (napi_create_external(env, b, buf_finalize, NULL, &ext) != napi_ok) {
+    anima_free(c, p);
+    free(b);
+    napi_throw_error(env, NULL, "allocHandle: napi_create_external failed");
+    return NULL;
+  }
+  return ext;
+}
+
+static dev_buf* buf_of(napi_env env, napi_value v) {
+  void* p = NULL;
+  if (napi_get_value_external(env, v, &p) != napi_ok) return NULL;
+  return (dev_buf*)p;
+}
+
+/* handleAddr(handle) -> the device address as a Number (0 once released) */
+static napi_value js_handle_addr(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  dev_buf* b = buf_of(env, argv[0]);
+  if (!b) {
+    napi_throw_type_error(env, NULL, "handleAddr: not a buffer handle");
+    return NULL;
+  }
+  return make_num(env, b->live ? (double)(uintptr_t)b->p : 0);
+}
+
+/* release(handle): back to the pool now (stream-ordered); a second release is a no-op */
+static napi_value js_release(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  dev_buf* b = buf_of(env, argv[0]);
+  if (!b) {
+    napi_throw_type_error(env, NULL, "release: not a buffer handle");
+    return NULL;
+  }
+  if (!b->live) return NULL;
+  b->live = 0;
+  if (!ctx_live(b->c)) return NULL;
+  CHECK_RC(env, b->c, anima_free(b->c, b->p));
+  return NULL;
+}
+
+static napi_value js_finalized(napi_env env, napi_callback_info info) {
+  (void)info;
+  return make_num(env, g_finalized);
 }
 
 static napi_value js_trim(napi_env env, napi_callback_info info) {
@@ -300,6 +426,7 @@ static napi_value js_attention(napi_env env, napi_callback_info info) {
   d.eps = (float)pnum(env, o, "eps");
   d.causal = (int)pnum(env, o, "causal");
   d.kv_prep = pptr(env, o, "kvPrep");
+  d.kv_prep_bytes = (int64_t)pnum(env, o, "kvPrepBytes");
   void* prepare_into = pptr(env, o, "prepareInto"); /* run anima_attention_prepare_kv into it */
   int kv[64];
   napi_value kvl = prop(env, o, "kvLen");
@@ -307,7 +434,7 @@ static napi_value js_attention(napi_env env, napi_callback_info info) {
     uint32_t n = 0;
     napi_get_array_length(env, kvl, &n);
     if (n > 64 || (int)n < d.B) {
-      napi_throw_range_error(env, NULL, "attention: kvLen must hold B (<= 64) entries");
+      if (!bad_arg()) napi_throw_range_error(env, NULL, "attention: kvLen must hold B (<= 64) entries");
       return NULL;
     }
     for (uint32_t i = 0; i < n; i++) {
@@ -326,8 +453,9 @@ static napi_value js_attention(napi_env env, napi_callback_info info) {
 static napi_value js_attention_kv_bytes(napi_env env, napi_callback_info info) {
   napi_value a[4];
   get_args(env, info, 4, a);
-  return make_num(env, (double)anima_attention_kv_bytes((int)num(env, a[0]), (int)num(env, a[1]), (int)num(env, a[2]),
-                                                        (int)num(env, a[3])));
+  int B = (int)num(env, a[0]), Hkv = (int)num(env, a[1]), Lk = (int)num(env, a[2]), prec = (int)num(env, a[3]);
+  if (bad_arg()) return NULL;
+  return make_num(env, (double)anima_attention_kv_bytes(B, Hkv, Lk, prec));
 }
 
 /* qkNormRope(ctx, qkv, L, H, D, ld, qn, kn, cs, sinOff, eps) */
@@ -594,7 +722,8 @@ static napi_value Init(napi_env env, napi_value exports) {
 #define FN(name, f) {name, NULL, f, NULL, NULL, NULL, napi_enumerable, NULL}
   napi_property_descriptor desc[] = {
       FN("init", js_init), FN("destroy", js_destroy), FN("sync", js_sync), FN("alloc", js_alloc),
-      FN("free", js_free), FN("trim", js_trim), FN("memStats", js_mem_stats), FN("h2d", js_h2d),
+      FN("free", js_free), FN("allocHandle", js_alloc_handle), FN("handleAddr", js_handle_addr),
+      FN("release", js_release), FN("finalized", js_finalized), FN("trim", js_trim), FN("memStats", js_mem_stats), FN("h2d", js_h2d),
       FN("d2h", js_d2h), FN("d2d", js_d2d), FN("profileEnable", js_profile_enable),
       FN("profileReset", js_profile_reset), FN("profileReport", js_profile_report),
       FN("timerStart", js_timer_start), FN("timerStop", js_timer_stop), FN("attention", js_attention),

@@ -5,7 +5,7 @@
 const D = 2048;
 
 // cos block followed by sin block, each [L][half]; returned Tensor carries .sinOff
-// (app/models/common.js:211-220).
+// (app/models/common.js:3-12).
 export function ropeTableTensor(gpu, angles, L, half) {
   const cs = new Float32Array(2 * L * half);
   for (let i = 0; i < L * half; i++) {
@@ -29,7 +29,7 @@ export function ropeTable(gpu, L, Dh, theta) {
 }
 
 // Cosmos VideoRopePosition3DEmb for one frame: 64 slots = 22 temporal (position 0), 21 height,
-// 21 width, NTK-scaled theta for h/w (app/models/common.js:238-260).
+// 21 width, NTK-scaled theta for h/w (app/models/common.js:31-52).
 export function ditRopeAngles(H, W) {
   const headDim = 128;
   const dimH = Math.floor(headDim / 6) * 2; // 42

@@ -43,6 +43,29 @@ function releaseNorm(nf) {
   if (nf.n) nf.n.release();
 }
 
+// The self-attention input projection when q, k and v could not be stacked (the unstacked path of
+// app/models/dit.js:274-288): three linears on the same modulated rows, written into the column
+// slices of one [M, 3D] buffer (row stride 3D), so the attention with its fused q/k RMSNorm + RoPE
+// reads them exactly as it reads the stacked GEMM's output.  The LayerNorm runs once per input
+// form the parts need (int8 rows for quantized parts, fp32 rows for bf16 parts).
+function projectParts(gpu, x, mod, Ws, M) {
+  const quant = Ws.filter((W) => ops.needsRotation(W));
+  const xq = quant.length ? ops.layernormModQ(gpu, x, mod, 0, D, D, quant.some((W) => W.lora && W.lora.length)) : null;
+  const n = quant.length < Ws.length ? ops.layernormMod(gpu, x, mod, 0, D, D, false) : null;
+  const qkv = gpu.empty([M, 3 * D]);
+  Ws.forEach((W, j) => {
+    if (W.N !== D || W.K !== D) throw new Error(`self-attention part ${j}: [${W.N}, ${W.K}], expected [${D}, ${D}]`);
+    const o = { M, out: qkv.view(j * D, [M, D]), ldc: 3 * D };
+    if (ops.needsRotation(W)) {
+      o.xq = xq;
+      if (xq.xr) o.xr = xq.xr;
+    }
+    ops.linear(gpu, ops.needsRotation(W) ? null : n, W, o);
+  });
+  releaseAll([xq, n]);
+  return qkv;
+}
+
 // out (an M = 1 row) += scale * B (A x) for one LoRA entry of a linear whose product runs outside
 // ops.linear (the grouped modulation GEMV); x is that linear's input row.
 function loraPart(gpu, x, e, out) {
@@ -69,9 +92,12 @@ export class AnimaDiT {
       const p = `blocks.${i}.`;
       const mod = (nm) => [st.linear(gpu, p + nm + ".1."), st.linear(gpu, p + nm + ".2.")];
       const self = attn(p + "self_attn.", "output_proj");
+      // one [3D, D] GEMM instead of three; null when the formats cannot be stacked (W4 parts with
+      // different codebooks, mixed kinds): then q, k and v stay separate (dit.js:112-114)
       self.qkv = concatLinears(gpu, [self.q, self.k, self.v]);
-      if (!self.qkv) throw new Error(`block ${i}: q/k/v formats cannot be stacked`);
-      delete self.q; delete self.k; delete self.v;
+      if (self.qkv) {
+        delete self.q; delete self.k; delete self.v;
+      }
       m.blocks.push({
         modSelf: mod("adaln_modulation_self_attn"), modCross: mod("adaln_modulation_cross_attn"),
         modMlp: mod("adaln_modulation_mlp"), self, cross: attn(p + "cross_attn.", "output_proj"),
@@ -121,6 +147,9 @@ export class AnimaDiT {
     this.gpu = gpu;
     this.ropeCache = new Map(); // "HpxWp" -> device RoPE table; depends only on the token grid
     this.modFused = null;
+    // attention precision: bf16 matrix-core operands with fp32 accumulation ("fp32": the fp32-MFMA
+    // kernels, the reference's arithmetic); prepareContext records the one its K/V were made for
+    this.precision = "bf16";
   }
 
   // The 3 * blocks + 1 adaLN modulation linears all read the same SiLU(t-embedding) (dit.js:205-
@@ -257,13 +286,14 @@ export class AnimaDiT {
       const k = ops.linear(gpu, ctx, b.cross.k, xq ? { xq, M: B * Lk } : { M: B * Lk });
       ops.rmsnorm(gpu, k, b.cross.kn, HD, 1e-6, k);
       const v = ops.linear(gpu, ctx, b.cross.v, xq ? { xq, M: B * Lk } : { M: B * Lk });
-      const prep = ops.attentionPrepareKV(gpu, { q: k, k, v, B, Lq: Lk, Lk, H: HEADS, D: HD, ldq: D, ldk: D, ldv: D });
+      const prep = ops.attentionPrepareKV(gpu, { q: k, k, v, B, Lq: Lk, Lk, H: HEADS, D: HD, ldq: D, ldk: D, ldv: D,
+        precision: this.precision });
       releaseAll([k, v]);
       return { prep };
     });
     if (xq) xq.release();
     return {
-      ctx, kv, Lk, B,
+      ctx, kv, Lk, B, precision: this.precision,
       release() {
         ctx.release();
         for (const e of kv) e.prep.release();
@@ -312,11 +342,17 @@ export class AnimaDiT {
       const m = tc.blocks[i];
 
       // self-attention: stacked QKV GEMM, then attention with q/k RMSNorm + RoPE fused
-      let nf = normFor(gpu, x, m.self, b.self.qkv);
-      const qkv = project(gpu, nf, b.self.qkv, M, { name: "dit.self.qkv" });
-      releaseNorm(nf);
+      let nf;
+      let qkv;
+      if (b.self.qkv) {
+        nf = normFor(gpu, x, m.self, b.self.qkv);
+        qkv = project(gpu, nf, b.self.qkv, M, { name: "dit.self.qkv" });
+        releaseNorm(nf);
+      } else {
+        qkv = projectParts(gpu, x, m.self, [b.self.q, b.self.k, b.self.v], M);
+      }
       let a = ops.attention(gpu, { q: qkv, k: qkv, v: qkv, B, Lq: L, Lk: L, H: HEADS, D: HD, ldq: 3 * D, ldk: 3 * D,
-        ldv: 3 * D, qOff: 0, kOff: D, vOff: 2 * D, qNorm: b.self.qn, kNorm: b.self.kn, cs });
+        ldv: 3 * D, qOff: 0, kOff: D, vOff: 2 * D, qNorm: b.self.qn, kNorm: b.self.kn, cs, precision: this.precision });
       qkv.release();
       ops.linear(gpu, a, b.self.o, { M, out: x, resid: true, gate: m.self, gOff: 2 * D });
       a.release();
@@ -326,7 +362,8 @@ export class AnimaDiT {
       const q = project(gpu, nf, b.cross.q, M);
       releaseNorm(nf);
       const kv = cond.kv[i];
-      a = ops.attention(gpu, { q, kvPrep: kv.prep, B, Lq: L, Lk: cond.Lk, H: HEADS, D: HD, ldq: D, qNorm: b.cross.qn });
+      a = ops.attention(gpu, { q, kvPrep: kv.prep, B, Lq: L, Lk: cond.Lk, H: HEADS, D: HD, ldq: D, qNorm: b.cross.qn,
+        precision: cond.precision });
       q.release();
       ops.linear(gpu, a, b.cross.o, { M, out: x, resid: true, gate: m.cross, gOff: 2 * D });
       a.release();

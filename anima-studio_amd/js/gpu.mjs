@@ -20,14 +20,18 @@ function dtypeOf(arr) {
   throw new Error("unsupported typed array " + (arr && arr.constructor && arr.constructor.name));
 }
 
-// Device tensor (app/gpu/device.js:10-24).  `buf` is the device address (a Number).
+// Device tensor (app/gpu/device.js:10-24).  `buf` is the device address (a Number).  An owning
+// tensor holds `handle`, the addon's finalizer-backed owner of the buffer: release() returns the
+// buffer to the pool at once; a tensor dropped without release() returns it when the garbage
+// collector reclaims the handle (as WebGPU reclaims an unreferenced GPUBuffer).
 export class Tensor {
-  constructor(gpu, ptr, shape, bytes, dtype) {
+  constructor(gpu, ptr, shape, bytes, dtype, handle) {
     this.gpu = gpu;
     this.buf = ptr;
     this.shape = shape;
     this.bytes = bytes;
     this.dtype = dtype || "f32";
+    this.handle = handle || null;
   }
   get size() {
     return this.shape.reduce((a, b) => a * b, 1);
@@ -36,16 +40,20 @@ export class Tensor {
   at(i) {
     return this.buf + i * ESIZE[this.dtype];
   }
-  // non-owning view of elements [i, i + prod(shape)); its release() only drops the reference
+  // non-owning view of elements [i, i + prod(shape)); it keeps the owning tensor reachable (so
+  // the buffer outlives the view), and its release() only drops that reference
   view(i, shape) {
     const t = new Tensor(this.gpu, this.at(i), shape, shape.reduce((a, b) => a * b, 1) * ESIZE[this.dtype], this.dtype);
+    t.owner = this.owner || this;
     t.release = () => {
       t.buf = 0;
+      t.owner = null;
     };
     return t;
   }
   release() {
-    if (this.buf) native.free(this.gpu.ctx, this.buf);
+    if (this.handle) native.release(this.handle);
+    this.handle = null;
     this.buf = 0;
   }
   destroy() {
@@ -106,7 +114,8 @@ export class GPU {
   empty(shape, dtype) {
     const dt = dtype || "f32";
     const bytes = shape.reduce((a, b) => a * b, 1) * ESIZE[dt];
-    return new Tensor(this, native.alloc(this.ctx, bytes), shape, bytes, dt);
+    const h = native.allocHandle(this.ctx, bytes);
+    return new Tensor(this, native.handleAddr(h), shape, bytes, dt, h);
   }
 
   fromArray(arr, shape) {

@@ -216,11 +216,13 @@ export function elementwise(gpu, op, a, b, out) {
 //  q: [Lq, ldq] with head h at column qOff + h*D; k, v: [Lk, ldk]/[Lk, ldv] with kv head
 //  h/group at kOff/vOff + (h/group)*D.  Output [B*Lq, H*D].
 // a.kvPrep: K/V converted beforehand by attentionPrepareKV (then a.k / a.v are not needed).
+// a.precision: "fp32" (default, the reference's arithmetic) or "bf16" (bf16 matrix-core operands,
+// fp32 accumulation: the DiT's and the text encoder's choice).
 export function attention(gpu, a) {
   const B = a.B || 1;
   const H = a.H, D = a.D;
   const o = a.out || gpu.empty([B * a.Lq, H * D]);
-  native.attention(gpu.ctx, attnDesc(a, B, H, D, o, { kvPrep: ptr(a.kvPrep) }));
+  native.attention(gpu.ctx, attnDesc(a, B, H, D, o, { kvPrep: ptr(a.kvPrep), kvPrepBytes: a.kvPrep ? a.kvPrep.bytes : 0 }));
   return o;
 }
 
@@ -230,11 +232,17 @@ export function attention(gpu, a) {
 export function attentionPrepareKV(gpu, a) {
   const B = a.B || 1;
   const H = a.H, D = a.D;
-  const bytes = native.attentionKvBytes(B, H / (a.group || 1), a.Lk, a.precision === "fp32" ? 1 : 0);
+  const bytes = native.attentionKvBytes(B, H / (a.group || 1), a.Lk, precisionId(a));
   const prep = gpu.empty([bytes], "u8");
   const o = a.out || { buf: a.q.buf };
-  native.attention(gpu.ctx, attnDesc(a, B, H, D, o, { prepareInto: prep.buf }));
+  native.attention(gpu.ctx, attnDesc(a, B, H, D, o, { prepareInto: prep.buf, kvPrepBytes: bytes }));
   return prep;
+}
+
+function precisionId(a) {
+  const p = a.precision || "fp32";
+  if (p !== "fp32" && p !== "bf16") throw new Error(`attention: unknown precision ${p}`);
+  return p === "fp32" ? 1 : 0;
 }
 
 function attnDesc(a, B, H, D, o, extra) {
@@ -244,10 +252,11 @@ function attnDesc(a, B, H, D, o, extra) {
     ldq: a.ldq, ldk: a.ldk, ldv: a.ldv, ldo: a.ldo || H * D,
     qOff: a.qOff || 0, kOff: a.kOff || 0, vOff: a.vOff || 0, oOff: a.oOff || 0,
     qBatch: a.qBatch !== undefined ? a.qBatch : a.Lq * a.ldq,
-    kBatch: a.kBatch !== undefined ? a.kBatch : a.Lk * a.ldk,
-    vBatch: a.vBatch !== undefined ? a.vBatch : a.Lk * a.ldv,
+    // no k / v (prepared K/V): their strides are not read
+    kBatch: a.kBatch !== undefined ? a.kBatch : a.k ? a.Lk * a.ldk : 0,
+    vBatch: a.vBatch !== undefined ? a.vBatch : a.v ? a.Lk * a.ldv : 0,
     oBatch: a.oBatch !== undefined ? a.oBatch : a.Lq * (a.ldo || H * D),
-    scale: a.scale || 0, kvLen: a.kvLen || null, precision: a.precision === "fp32" ? 1 : 0,
+    scale: a.scale || 0, kvLen: a.kvLen || null, precision: precisionId(a),
     qNorm: ptr(a.qNorm), kNorm: ptr(a.kNorm), cs: ptr(a.cs), sinOff: a.cs ? a.cs.sinOff : 0, eps: 1e-6,
     causal: a.causal ? 1 : 0,
   }, extra);

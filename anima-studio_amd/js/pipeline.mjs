@@ -56,12 +56,24 @@ export class LatentPipeline {
   }
 
   // opts: { cond, cfg = 1, width, height, steps, sampler, seed = 0, shift = 3, scheduler = "simple",
-  //         onStep(i, readDenoised), graph = false }.  cond.B must be 2 when cfg != 1 (positive,
-  //         negative), else 1.
+  //         onStep(i, readDenoised), onProgress({ phase, step, steps, frac }), signal, graph = false }.
+  //         cond.B must be 2 when cfg != 1 (positive, negative), else 1.
+  // Progress and cancellation follow app/pipeline.js:226-256: onProgress after every DiT block
+  // (after every step when the forward is a graph replay), the device queue drained every 7 blocks
+  // so that both stay responsive, and `signal.aborted` checked at the same points, throwing an
+  // Error named "AbortError"; the pool is trimmed on the way out, cancelled or not.
   // Returns { latent: Float32Array [16, h, w], sigmas, timings }.
   async generate(opts) {
     const gpu = this.gpu;
-    const { cond, width, height, steps, sampler } = opts;
+    const { cond, width, height, steps, sampler, signal } = opts;
+    const onProgress = opts.onProgress || (() => {});
+    const check = () => {
+      if (signal && signal.aborted) {
+        const e = new Error("Generation cancelled");
+        e.name = "AbortError";
+        throw e;
+      }
+    };
     const cfg = opts.cfg === undefined ? 1 : opts.cfg;
     const seed = opts.seed || 0, shift = opts.shift === undefined ? 3 : opts.shift;
     const guided = cfg !== 1;
@@ -78,13 +90,25 @@ export class LatentPipeline {
     const old = gpu.empty([n]), oldD = plan.name === "er_sde" ? gpu.empty([n]) : null;
     const den = opts.onStep ? gpu.empty([n]) : null;
     const useGraph = opts.graph === true && plan.steps > 1;
+    const nBlocks = this.dit.blocks.length;
     let fg = null;
     try {
+      check();
       for (let i = 0; i < plan.steps; i++) {
         const st = plan.step(i);
         const tc = this.timeCond(st.sigma);
         for (let b = 0; b < B; b++) gpu.copy(lat.at(b * n), x, n * 4);
-        const v = fg ? fg.run(tc) : await this.dit.forwardDevice(lat, h, w, cond, tc);
+        const onBlock = async (blk) => {
+          check();
+          onProgress({ phase: "sample", step: i, steps: plan.steps, frac: (i + (blk + 1) / nBlocks) / plan.steps });
+          if (blk % 7 === 6) await gpu.sync();
+        };
+        const v = fg ? fg.run(tc) : await this.dit.forwardDevice(lat, h, w, cond, tc, onBlock);
+        if (fg) {
+          await gpu.sync();
+          check();
+          onProgress({ phase: "sample", step: i, steps: plan.steps, frac: (i + 1) / plan.steps });
+        }
         const eps = st.noise ? gpu.fromArray(gen.randn(n), [n]) : null;
         native.samplerStep(gpu.ctx, {
           kind: st.kind, n, x: x.buf, v: v.buf, vUncond: guided ? v.at(n) : 0, cfg, sigma: st.sigma,
@@ -102,6 +126,13 @@ export class LatentPipeline {
     } finally {
       if (fg) fg.release();
       for (const t of [x, lat, old, oldD, den]) if (t) t.release();
+      // free pooled activations so that idle device memory is the weights (also after a cancel)
+      try {
+        await gpu.sync();
+      } catch (e) {
+        // a device error is reported by the call that hit it
+      }
+      gpu.pool.trim();
     }
   }
 

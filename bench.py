@@ -215,7 +215,7 @@ def main():
     qkv = rng.standard_normal((B, L, 3 * H * D), dtype=np.float32)
     qn = (1 + 0.02 * rng.standard_normal(D)).astype(np.float32)
     kn = (1 + 0.02 * rng.standard_normal(D)).astype(np.float32)
-    cs = m.dit_rope_table(Hp, Wp)  # host-side table, as app/models/common.js:211-260
+    cs = m.dit_rope_table(Hp, Wp)  # host-side table, as app/models/common.js:3-12, 31-52
 
     with m.Context(0) as ctx:
         d_qkv, d_qn, d_kn, d_cs = ctx.upload(qkv), ctx.upload(qn), ctx.upload(kn), ctx.upload(cs)

@@ -128,6 +128,10 @@ typedef struct {
   /* Optional: K and V already converted by anima_attention_prepare_kv (same B, H / group, Lk and
    * precision); then k, v, their strides, k_norm and the key side of rope_cs are not read. */
   const void* kv_prep;
+  /* With kv_prep (and for anima_attention_prepare_kv): the prepared buffer's size, which must equal
+   * anima_attention_kv_bytes(B, H / group, Lk, precision) -- a buffer prepared for another shape or
+   * precision is rejected instead of being read past its end. */
+  int64_t kv_prep_bytes;
 } anima_attn_desc;
 
 /* ops.attention (app/gpu/ops.js:166-208) on the flash path (kernels.js:158-299), plus the fused
@@ -138,7 +142,8 @@ typedef struct {
 int anima_attention(anima_ctx* ctx, const anima_attn_desc* desc);
 /* The K/V half of anima_attention on its own: K rows RMS-normalized (k_norm) and rotated (rope_cs)
  * and V transposed, rounded to the MFMA operand type, written to kv_prep
- * (anima_attention_kv_bytes(B, H / group, Lk, precision) bytes, 16-byte aligned) for later
+ * (anima_attention_kv_bytes(B, H / group, Lk, precision) bytes, passed in desc->kv_prep_bytes,
+ * 16-byte aligned) for later
  * anima_attention calls with desc->kv_prep: keys and values that serve many calls (the per-prompt
  * cross-attention K/V of app/models/dit.js:232-249) are converted once. */
 int anima_attention_prepare_kv(anima_ctx* ctx, const anima_attn_desc* desc, void* kv_prep);

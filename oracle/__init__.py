@@ -58,6 +58,9 @@ def lib():
         L.orc_token_quant.argtypes = [_f32p, _i64, ctypes.c_int, _i8p, _f32p]
         L.orc_gemm_i8.argtypes = [_i8p, _i8p, _i64, ctypes.c_int, ctypes.c_int, _i32p]
         L.orc_fp8e4m3.argtypes = [ctypes.c_uint8]
+        L.orc_fill_random.argtypes = [ctypes.c_void_p, _i64, ctypes.c_int, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]
+        L.orc_splitmix64_next.argtypes = [ctypes.c_uint64]
+        L.orc_splitmix64_next.restype = ctypes.c_uint64
         L.orc_fp8e4m3.restype = ctypes.c_float
         L.orc_w4_decode.argtypes = [_u8p, _u8p, _f32p, ctypes.c_int, ctypes.c_int, _i8p]
         L.orc_linear_epilogue.argtypes = [_i32p, _i64, ctypes.c_int, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int, _f32p, _i64, _f32p, _i64,
@@ -102,7 +105,7 @@ def dit_rope_angles(Hp: int, Wp: int) -> np.ndarray:
 
 
 def rope_table(angles: np.ndarray) -> np.ndarray:
-    """cos block then sin block, flat [2*L*half]; sin_off = L*half (common.js:211-220)."""
+    """cos block then sin block, flat [2*L*half]; sin_off = L*half (common.js:3-12)."""
     a = _c(angles, np.float32)
     L, half = a.shape
     out = np.empty(2 * L * half, np.float32)
@@ -237,3 +240,19 @@ def gelu(x: float) -> float:
 
 def silu(x: float) -> float:
     return lib().orc_silu(x)
+
+
+FILL_KINDS = {"u8": (0, np.uint8), "i8n": (1, np.int8), "f32": (2, np.float32), "bf16": (3, np.uint16),
+              "f32n": (4, np.float32)}
+
+
+def fill_random(n, kind, seed, lo, hi):
+    """The seeded synthetic fill of anima_fill_random (bf16 as its uint16 bit patterns)."""
+    k, dt = FILL_KINDS[kind]
+    out = np.empty(n, dt)
+    lib().orc_fill_random(out.ctypes.data_as(ctypes.c_void_p), n, k, seed, lo, hi)
+    return out
+
+
+def splitmix64_next(state):
+    return int(lib().orc_splitmix64_next(state))

@@ -20,7 +20,10 @@ D, HEADS, HD = 2048, 16, 128
 
 
 def bf16_to_f32(u16):
-    return (np.asarray(u16, np.uint32) << 16).view(np.float32)
+    import torch
+
+    u = torch.from_numpy(np.ascontiguousarray(u16).view(np.int16)).to(torch.int32)
+    return (u << 16).view(torch.float32).numpy()
 
 
 def timestep_embedding(sigma):
@@ -83,13 +86,26 @@ def gelu_as(x):
     return 0.5 * x * (1.0 + np.sign(z) * y)
 
 
+def imatmul(q, g, chunk=1024):
+    """Exact int64 q [M,K] @ g [N,K]^T of int8 operands in |v| <= 128: float32 products over K-chunks
+    of 1024, each of whose partial sums (whatever order the BLAS adds in) is an integer below
+    128 * 127 * 1024 < 2^24, so every float32 step is exact; the chunks add in int64."""
+    import torch
+
+    qt, gt = torch.from_numpy(np.ascontiguousarray(q)), torch.from_numpy(np.ascontiguousarray(g))
+    acc = torch.zeros((q.shape[0], g.shape[0]), dtype=torch.int64)
+    for k0 in range(0, q.shape[1], chunk):
+        acc += (qt[:, k0:k0 + chunk].float() @ gt[:, k0:k0 + chunk].float().T).to(torch.int64)
+    assert int(acc.abs().max()) < 2 ** 31
+    return acc.to(torch.int32).numpy()
+
+
 def qlinear(mode, x_rot, L, epi_c=None, gate=None, g_off=0, act=0, xq=None):
     """y = x_r @ dec(W)^T with this build's W8A8 arithmetic or the reference's W8A32."""
     if mode == "w8a8":
         q, s = xq if xq is not None else orc.token_quant(x_rot)
-        acc = (q.astype(np.float64) @ L.grid.astype(np.float64).T).astype(np.int64)
-        assert np.abs(acc).max() < 2 ** 31
-        return orc.linear_epilogue(acc.astype(np.int32), s, L.scale, act=act, epi=2 if gate is not None else 0,
+        acc = imatmul(q, L.grid)
+        return orc.linear_epilogue(acc, s, L.scale, act=act, epi=2 if gate is not None else 0,
                                    gate=gate, g_off=g_off, c=epi_c)
     y = (x_rot.astype(np.float64) @ L.deq().T)
     if act == 1:
@@ -100,7 +116,9 @@ def qlinear(mode, x_rot, L, epi_c=None, gate=None, g_off=0, act=0, xq=None):
 
 
 def bf16_linear(x, L, act=None):
-    y = x.astype(np.float64) @ L.w.astype(np.float64).T
+    import torch
+
+    y = (torch.from_numpy(np.ascontiguousarray(x)).double() @ torch.from_numpy(L.w).double().T).numpy()
     if act == "silu":
         y = y / (1 + np.exp(-y))
     return y.astype(np.float32)
@@ -112,60 +130,81 @@ def attention(mode, q, k, v, B, Lq, Lk, ldq, ldk, ldv, q_off=0, k_off=0, v_off=0
                          k_off=k_off, v_off=v_off).reshape(B * Lq, HEADS * HD)
 
 
-def dit_step(W, nblocks, latents, h, w, ctxs, sigma, mode="w8a8"):
-    """Returns (velocities [B][16,h,w], x after block 0 [B*L, 2048])."""
-    B = len(latents)
-    Hp, Wp = h // 2, w // 2
-    L = Hp * Wp
-    f32 = lambda name: (bf16_to_f32(W[name]) if W[name].dtype == np.uint16 else W[name]).astype(np.float32)
-    # timeCond (dit.js:196-225)
+def _f32(W, name):
+    return (bf16_to_f32(W[name]) if W[name].dtype == np.uint16 else W[name]).astype(np.float32)
+
+
+def time_cond(W, nblocks, sigma):
+    """timeCond (app/models/dit.js:196-225; tools/reference.py:203-213, 218-220, 244): per block the
+    modulation vectors [3D] of the self-attention, cross-attention and MLP sublayers (shift, scale,
+    gate chunks), plus the final layer's [2D] (shift, scale).  mod = adaln_lora[:n] + W2 W1 silu(emb)."""
     temb = timestep_embedding(sigma)[None]
     lora = bf16_linear(bf16_linear(temb, Linear(W, "t_embedder.1.linear_1."), "silu"), Linear(W, "t_embedder.1.linear_2."))
-    emb = orc.rmsnorm(temb, f32("t_embedding_norm.weight"), D)
+    emb = orc.rmsnorm(temb, _f32(W, "t_embedding_norm.weight"), D)
     semb = (emb.astype(np.float64) / (1 + np.exp(-emb.astype(np.float64)))).astype(np.float32)
 
     def mod(p, n):
         hh = bf16_linear(semb, Linear(W, p + ".1."))
         return (lora[0, :n].astype(np.float64) + bf16_linear(hh, Linear(W, p + ".2."))[0]).astype(np.float32)
 
-    # prepareContext (dit.js:232-249): one rotation of the stacked contexts
-    Lk = ctxs[0].shape[0]
+    blocks = [tuple(mod(f"blocks.{i}.{nm}", 3 * D) for nm in
+                    ("adaln_modulation_self_attn", "adaln_modulation_cross_attn", "adaln_modulation_mlp"))
+              for i in range(nblocks)]
+    return blocks, mod("final_layer.adaln_modulation", 2 * D)
+
+
+def prepare_context(ctxs):
+    """prepareContext's shared part (dit.js:232-249): the stacked contexts, rotated once, and their
+    per-token int8 form."""
     ctx = np.concatenate(ctxs).astype(np.float32)
     ctx_r = orc.hadamard256(ctx)
-    ctx_q = orc.token_quant(ctx_r)
-    # x_embedder
+    return ctx_r, orc.token_quant(ctx_r), ctxs[0].shape[0]
+
+
+def dit_block(mode, W, i, x, mods, cs, ctx, B, L):
+    """One DiT block (dit.js:261-315; reference.py:231-242): x [B*L, D] -> x.  mods = (self, cross,
+    mlp) modulation vectors, each (shift | scale | gate) chunks of D; ctx = prepare_context(...)."""
+    p = f"blocks.{i}."
+    ms, mc, mm = mods
+    ctx_r, ctx_q, Lk = ctx
+    # self-attention
+    n = orc.layernorm_mod(x, ms, 0, D, D, rotate=True)
+    qkv_w = stack([Linear(W, p + f"self_attn.{t}_proj.") for t in "qkv"])
+    qkv = qlinear(mode, n, qkv_w)
+    qn, kn = _f32(W, p + "self_attn.q_norm.weight"), _f32(W, p + "self_attn.k_norm.weight")
+    qkv = np.concatenate([orc.qk_norm_rope(qkv[b * L:(b + 1) * L], L, HEADS, HD, 3 * D, qn, kn, cs, L * 64)
+                          for b in range(B)])
+    a = attention(mode, qkv, qkv, qkv, B, L, L, 3 * D, 3 * D, 3 * D, 0, D, 2 * D)
+    x = qlinear(mode, orc.hadamard256(a), Linear(W, p + "self_attn.output_proj."), epi_c=x, gate=ms, g_off=2 * D)
+    # cross-attention (no RoPE; q and k RMSNorm per head)
+    n = orc.layernorm_mod(x, mc, 0, D, D, rotate=True)
+    q = qlinear(mode, n, Linear(W, p + "cross_attn.q_proj."))
+    q = orc.rmsnorm(q.reshape(-1, HD), _f32(W, p + "cross_attn.q_norm.weight"), HD).reshape(B * L, D)
+    kx = qlinear(mode, ctx_r, Linear(W, p + "cross_attn.k_proj."), xq=ctx_q if mode == "w8a8" else None)
+    k = orc.rmsnorm(kx.reshape(-1, HD), _f32(W, p + "cross_attn.k_norm.weight"), HD).reshape(B * Lk, D)
+    v = qlinear(mode, ctx_r, Linear(W, p + "cross_attn.v_proj."), xq=ctx_q if mode == "w8a8" else None)
+    a = attention(mode, q, k, v, B, L, Lk, D, D, D)
+    x = qlinear(mode, orc.hadamard256(a), Linear(W, p + "cross_attn.output_proj."), epi_c=x, gate=mc, g_off=2 * D)
+    # MLP
+    n = orc.layernorm_mod(x, mm, 0, D, D, rotate=True)
+    hdn = qlinear(mode, n, Linear(W, p + "mlp.layer1."), act=1)
+    return qlinear(mode, orc.hadamard256(hdn), Linear(W, p + "mlp.layer2."), epi_c=x, gate=mm, g_off=2 * D)
+
+
+def dit_step(W, nblocks, latents, h, w, ctxs, sigma, mode="w8a8"):
+    """Returns (velocities [B][16,h,w], x after block 0 [B*L, 2048])."""
+    B = len(latents)
+    Hp, Wp = h // 2, w // 2
+    L = Hp * Wp
+    mods, mf = time_cond(W, nblocks, sigma)
+    ctx = prepare_context(ctxs)
     x = bf16_linear(np.concatenate([patchify(l, h, w) for l in latents]), Linear(W, "x_embedder.proj.1."))
     cs = orc.dit_rope_table(Hp, Wp)
     block0 = None
     for i in range(nblocks):
-        p = f"blocks.{i}."
-        ms, mc, mm = mod(p + "adaln_modulation_self_attn", 3 * D), mod(p + "adaln_modulation_cross_attn", 3 * D), \
-            mod(p + "adaln_modulation_mlp", 3 * D)
-        # self-attention
-        n = orc.layernorm_mod(x, ms, 0, D, D, rotate=True)
-        qkv_w = stack([Linear(W, p + f"self_attn.{t}_proj.") for t in "qkv"])
-        qkv = qlinear(mode, n, qkv_w)
-        qn, kn = f32(p + "self_attn.q_norm.weight"), f32(p + "self_attn.k_norm.weight")
-        qkv = np.concatenate([orc.qk_norm_rope(qkv[b * L:(b + 1) * L], L, HEADS, HD, 3 * D, qn, kn, cs, L * 64)
-                              for b in range(B)])
-        a = attention(mode, qkv, qkv, qkv, B, L, L, 3 * D, 3 * D, 3 * D, 0, D, 2 * D)
-        x = qlinear(mode, orc.hadamard256(a), Linear(W, p + "self_attn.output_proj."), epi_c=x, gate=ms, g_off=2 * D)
-        # cross-attention (no RoPE; q and k RMSNorm per head)
-        n = orc.layernorm_mod(x, mc, 0, D, D, rotate=True)
-        q = qlinear(mode, n, Linear(W, p + "cross_attn.q_proj."))
-        q = orc.rmsnorm(q.reshape(-1, HD), f32(p + "cross_attn.q_norm.weight"), HD).reshape(B * L, D)
-        kx = qlinear(mode, ctx_r, Linear(W, p + "cross_attn.k_proj."), xq=ctx_q if mode == "w8a8" else None)
-        k = orc.rmsnorm(kx.reshape(-1, HD), f32(p + "cross_attn.k_norm.weight"), HD).reshape(B * Lk, D)
-        v = qlinear(mode, ctx_r, Linear(W, p + "cross_attn.v_proj."), xq=ctx_q if mode == "w8a8" else None)
-        a = attention(mode, q, k, v, B, L, Lk, D, D, D)
-        x = qlinear(mode, orc.hadamard256(a), Linear(W, p + "cross_attn.output_proj."), epi_c=x, gate=mc, g_off=2 * D)
-        # MLP
-        n = orc.layernorm_mod(x, mm, 0, D, D, rotate=True)
-        hdn = qlinear(mode, n, Linear(W, p + "mlp.layer1."), act=1)
-        x = qlinear(mode, orc.hadamard256(hdn), Linear(W, p + "mlp.layer2."), epi_c=x, gate=mm, g_off=2 * D)
+        x = dit_block(mode, W, i, x, mods[i], cs, ctx, B, L)
         if i == 0:
             block0 = x.copy()
-    mf = mod("final_layer.adaln_modulation", 2 * D)
     n = orc.layernorm_mod(x, mf, 0, D, D, rotate=False)
     o = bf16_linear(n, Linear(W, "final_layer.linear."))
     return [unpatchify(o[b * L:(b + 1) * L], h, w) for b in range(B)], block0

@@ -85,7 +85,7 @@ void orc_randn(uint64_t seed, int64_t n, float* d) { /* app/rng.js:55-66 */
 
 /* ------------------------------------------------------------------ RoPE tables */
 
-void orc_dit_rope_angles(int Hp, int Wp, float* a) { /* app/models/common.js:239-260 */
+void orc_dit_rope_angles(int Hp, int Wp, float* a) { /* app/models/common.js:31-52 */
   const int head_dim = 128;
   const int dim_h = (head_dim / 6) * 2; /* 42 */
   const int dim_t = head_dim - 2 * dim_h; /* 44 */
@@ -107,7 +107,7 @@ void orc_dit_rope_angles(int Hp, int Wp, float* a) { /* app/models/common.js:239
     }
 }
 
-void orc_rope_table(const float* ang, int64_t L, int half, float* cs) { /* common.js:211-220 */
+void orc_rope_table(const float* ang, int64_t L, int half, float* cs) { /* common.js:3-12 */
   for (int64_t i = 0; i < L * half; i++) {
     cs[i] = (float)cos((double)ang[i]);
     cs[L * half + i] = (float)sin((double)ang[i]);
@@ -193,8 +193,9 @@ static void butterfly256(float* s) {
 }
 
 void orc_hadamard256(const float* X, float* Y, int64_t n) { /* app/gpu/kernels.js:360-388 */
-  float s[256];
+#pragma omp parallel for schedule(static)
   for (int64_t g = 0; g < n / 256; g++) {
+    float s[256];
     memcpy(s, X + g * 256, sizeof s);
     butterfly256(s);
     for (int j = 0; j < 256; j++) Y[g * 256 + j] = s[j] * 0.0625f;
@@ -203,10 +204,12 @@ void orc_hadamard256(const float* X, float* Y, int64_t n) { /* app/gpu/kernels.j
 
 void orc_layernorm_mod(const float* X, const float* MOD, float* Y, int64_t rows, int cols,
                        int64_t shift_off, int64_t scale_off, float eps, int rotate) {
-  /* app/gpu/kernels.js:108-145: 256 threads stride the row, 128..1 tree reductions */
-  float red[256];
-  float* S = (float*)malloc(sizeof(float) * (size_t)cols);
+  /* app/gpu/kernels.js:108-145: 256 threads stride the row, 128..1 tree reductions; rows are
+   * independent (one per OpenMP thread at a time) */
+#pragma omp parallel for schedule(static)
   for (int64_t row = 0; row < rows; row++) {
+    float red[256];
+    float* S = (float*)malloc(sizeof(float) * (size_t)cols);
     const float* x = X + row * cols;
     for (int t = 0; t < 256; t++) {
       float s = 0.0f;
@@ -231,8 +234,8 @@ void orc_layernorm_mod(const float* X, const float* MOD, float* Y, int64_t rows,
     } else {
       memcpy(Y + row * cols, S, sizeof(float) * (size_t)cols);
     }
+    free(S);
   }
-  free(S);
 }
 
 /* ------------------------------------------------------------------ attention */
@@ -240,10 +243,12 @@ void orc_layernorm_mod(const float* X, const float* MOD, float* Y, int64_t rows,
 static int kvlen(const orc_attn* a, int b) { return a->kv_len ? a->kv_len[b] : a->Lk; }
 
 void orc_attention_f64(const orc_attn* a) {
-  double* s = (double*)malloc(sizeof(double) * (size_t)a->Lk);
-  double* o = (double*)malloc(sizeof(double) * (size_t)a->D);
+  /* (batch, head) pairs are independent: one per thread */
+#pragma omp parallel for collapse(2) schedule(dynamic)
   for (int b = 0; b < a->B; b++)
     for (int h = 0; h < a->H; h++) {
+      double* s = (double*)malloc(sizeof(double) * (size_t)a->Lk);
+      double* o = (double*)malloc(sizeof(double) * (size_t)a->D);
       const int hk = h / a->group, n = kvlen(a, b);
       for (int i = 0; i < a->Lq; i++) {
         const float* q = a->q + b * a->q_bs + (int64_t)i * a->ldq + a->q_off + (int64_t)h * a->D;
@@ -266,18 +271,20 @@ void orc_attention_f64(const orc_attn* a) {
         float* out = a->o + b * a->o_bs + (int64_t)i * a->ldo + a->o_off + (int64_t)h * a->D;
         for (int d = 0; d < a->D; d++) out[d] = (float)(o[d] / l);
       }
+      free(s);
+      free(o);
     }
-  free(s);
-  free(o);
 }
 
 void orc_attention_wgsl(const orc_attn* a) {
   /* app/gpu/kernels.js:195-298, one query row at a time; the shader's per-row arithmetic
    * does not depend on the other rows of its workgroup. */
   const int D = a->D;
-  float s[32], e[32], o_acc[256];
+#pragma omp parallel for collapse(2) schedule(dynamic)
   for (int b = 0; b < a->B; b++)
     for (int h = 0; h < a->H; h++) {
+      float s[32], e[32];
+      float* o_acc = (float*)malloc(sizeof(float) * (size_t)D);
       const int hk = h / a->group, Lk = kvlen(a, b);
       for (int i = 0; i < a->Lq; i++) {
         const float* q = a->q + b * a->q_bs + (int64_t)i * a->ldq + a->q_off + (int64_t)h * D;
@@ -321,6 +328,7 @@ void orc_attention_wgsl(const orc_attn* a) {
         float* out = a->o + b * a->o_bs + (int64_t)i * a->ldo + a->o_off + (int64_t)h * D;
         for (int d = 0; d < D; d++) out[d] = o_acc[d] * inv;
       }
+      free(o_acc);
     }
 }
 
@@ -341,13 +349,14 @@ float orc_bf16_round(float x) {
 void orc_attention_bf16(const orc_attn* a) {
   const int D = a->D;
   const float c = a->scale * 1.4426950408889634f;
-  float* s = (float*)malloc(sizeof(float) * (size_t)a->Lk);
-  float* kb = (float*)malloc(sizeof(float) * (size_t)a->Lk * D);
-  float* vb = (float*)malloc(sizeof(float) * (size_t)a->Lk * D);
-  double o[256];
-  float qb[256];
+#pragma omp parallel for collapse(2) schedule(dynamic)
   for (int b = 0; b < a->B; b++)
     for (int h = 0; h < a->H; h++) {
+      float* s = (float*)malloc(sizeof(float) * (size_t)a->Lk);
+      float* kb = (float*)malloc(sizeof(float) * (size_t)a->Lk * D);
+      float* vb = (float*)malloc(sizeof(float) * (size_t)a->Lk * D);
+      double* o = (double*)malloc(sizeof(double) * (size_t)D);
+      float* qb = (float*)malloc(sizeof(float) * (size_t)D);
       const int hk = h / a->group, n = kvlen(a, b);
       for (int j = 0; j < n; j++) {
         const float* k = a->k + b * a->k_bs + (int64_t)j * a->ldk + a->k_off + (int64_t)hk * D;
@@ -379,15 +388,18 @@ void orc_attention_bf16(const orc_attn* a) {
         float* out = a->o + b * a->o_bs + (int64_t)i * a->ldo + a->o_off + (int64_t)h * D;
         for (int d = 0; d < D; d++) out[d] = (float)(o[d] / l);
       }
+      free(s);
+      free(kb);
+      free(vb);
+      free(o);
+      free(qb);
     }
-  free(s);
-  free(kb);
-  free(vb);
 }
 
 /* ------------------------------------------------------------------ quantized linears */
 
 void orc_token_quant(const float* X, int64_t M, int K, int8_t* Q, float* S) {
+#pragma omp parallel for schedule(static)
   for (int64_t m = 0; m < M; m++) {
     const float* x = X + m * K;
     float amax = 0.0f;
@@ -423,6 +435,7 @@ float orc_fp8e4m3(uint8_t b) { /* app/gpu/gemm.js:144-151 */
 
 void orc_w4_decode(const uint8_t* codes, const uint8_t* srel, const float* cb, int N, int K,
                    int8_t* out) { /* tools/quant.py:172-182; app/gpu/gemm.js:141-158 */
+#pragma omp parallel for schedule(static)
   for (int n = 0; n < N; n++)
     for (int k = 0; k < K; k++) {
       uint8_t byte = codes[(int64_t)n * (K / 2) + k / 2];
@@ -451,6 +464,7 @@ float orc_silu(float x) { return x / (1.0f + expf(-x)); } /* app/gpu/kernels.js:
 void orc_linear_epilogue(const int32_t* ACC, int64_t M, int N, const float* sx, const float* sw,
                          const float* bias, int act, int epi, const float* gate, int64_t g_off,
                          float* C, int64_t ldc, const float* add) { /* app/gpu/gemm.js:186-192 */
+#pragma omp parallel for schedule(static)
   for (int64_t m = 0; m < M; m++)
     for (int n = 0; n < N; n++) {
       float r = (float)ACC[m * N + n];
@@ -465,4 +479,50 @@ void orc_linear_epilogue(const int32_t* ACC, int64_t M, int N, const float* sx, 
       else if (epi == 1) *c = *c + r;
       else *c = fmaf(gate[g_off + n], r, *c);
     }
+}
+
+/* ---------------------------------------------------------------- synthetic weights
+ * The seeded fill of anima_fill_random (include/anima.h; no reference counterpart: the reference
+ * loads real checkpoints).  splitmix64 is Vigna's published generator (xoshiro/splitmix64.c);
+ * the FP kinds round every product and sum (no contraction), as the device code does. */
+static uint64_t orc_splitmix64(uint64_t x) {
+  uint64_t z = x + 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+uint64_t orc_splitmix64_next(uint64_t state) { return orc_splitmix64(state); }
+
+static uint16_t orc_bf16_bits(float v) { /* round to nearest even (finite inputs) */
+  uint32_t u;
+  memcpy(&u, &v, 4);
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+void orc_fill_random(void* dst, int64_t n, int kind, uint64_t seed, float lo, float hi) {
+  const int64_t imul = (int64_t)llrint((double)lo * 4096.0 / 147.8017);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; i++) {
+    const uint64_t h = orc_splitmix64(seed * 0xD1B54A32D192ED03ull + (uint64_t)i);
+    if (kind == 0) { /* U8 */
+      const int64_t a = (int64_t)lo, b = (int64_t)hi;
+      ((uint8_t*)dst)[i] = (uint8_t)(a + (int64_t)(h % (uint64_t)(b - a + 1)));
+    } else if (kind == 1) { /* I8N */
+      const int64_t sum = (int64_t)(h & 0xff) + (int64_t)((h >> 8) & 0xff) + (int64_t)((h >> 16) & 0xff) +
+                          (int64_t)((h >> 24) & 0xff);
+      int64_t v = ((sum - 510) * imul) >> 12;
+      v = v < -127 ? -127 : (v > 127 ? 127 : v);
+      ((int8_t*)dst)[i] = (int8_t)v;
+    } else if (kind == 4) { /* F32N */
+      const float u = (float)(h & 0xffff) * (1.0f / 65536.0f) + (float)((h >> 16) & 0xffff) * (1.0f / 65536.0f) +
+                      (float)((h >> 32) & 0xffff) * (1.0f / 65536.0f) + (float)((h >> 48) & 0xffff) * (1.0f / 65536.0f);
+      ((float*)dst)[i] = (u - 2.0f) * 1.7320508f * lo + hi;
+    } else { /* F32, BF16 */
+      const float u = (float)(h >> 40) * (1.0f / 16777216.0f);
+      const float v = lo + (hi - lo) * u;
+      if (kind == 2) ((float*)dst)[i] = v;
+      else ((uint16_t*)dst)[i] = orc_bf16_bits(v);
+    }
+  }
 }

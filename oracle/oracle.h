@@ -25,9 +25,9 @@ void orc_randn(uint64_t seed, int64_t n, float* out);
 /* One raw MT19937 draw stream (app/rng.js:5-34), for the generator's own check. */
 void orc_mt19937(uint32_t seed, int64_t n, uint32_t* out);
 
-/* 3D Cosmos RoPE angles [Hp*Wp][64] (app/models/common.js:238-260). */
+/* 3D Cosmos RoPE angles [Hp*Wp][64] (app/models/common.js:31-52). */
 void orc_dit_rope_angles(int Hp, int Wp, float* out);
-/* cos block then sin block, each [L][half] (app/models/common.js:211-220). */
+/* cos block then sin block, each [L][half] (app/models/common.js:3-12). */
 void orc_rope_table(const float* angles, int64_t L, int half, float* out);
 
 /* In-place per-head RMSNorm + split-half RoPE on q and k of X[L][ld]
@@ -97,6 +97,13 @@ void orc_linear_epilogue(const int32_t* ACC, int64_t M, int N, const float* sx, 
 /* erf-GELU with Abramowitz-Stegun 7.1.26 (app/gpu/kernels.js:9-20). */
 float orc_gelu(float x);
 float orc_silu(float x);
+
+/* The seeded synthetic-weight fill of anima_fill_random (include/anima.h; no reference
+ * counterpart): element i draws h = splitmix64(seed * 0xD1B54A32D192ED03 + i).  kind: 0 U8,
+ * 1 I8N, 2 F32, 3 BF16 (bits), 4 F32N. */
+void orc_fill_random(void* dst, int64_t n, int kind, uint64_t seed, float lo, float hi);
+/* splitmix64's output for one state (Vigna's reference generator), for its known-answer check. */
+uint64_t orc_splitmix64_next(uint64_t state);
 
 #ifdef __cplusplus
 }

@@ -8,6 +8,7 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG_DIR = os.path.join(ROOT, "anima-studio_amd")
+RUN_CASE = os.path.join(ROOT, "tests", "js", "run_case.mjs")  # the JS op-case harness of the GPU tests
 
 
 def amd():

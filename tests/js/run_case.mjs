@@ -24,18 +24,22 @@
 //              and its weights
 //   chain      prompt tokens -> Qwen3.encode -> adapt -> prepareContext -> forward (synthetic
 //              weights, cond + uncond prompts), the velocities
+//   synthdit   a seeded synthetic DiT (any depth) on given latents and contexts: velocities and the
+//              residual stream after block 0, for the oracle's restatement of the same weights
+//   fullstep   the full-size CFG step of a synthetic DiT: eager, with equal contexts, and replayed
+//              from a HIP graph
 
 import fs from "fs";
-import { GPU } from "./gpu.mjs";
-import * as ops from "./ops.mjs";
-import { ditRopeTable } from "./common.mjs";
-import { SafeTensors } from "./weights.mjs";
-import { AnimaDiT, ForwardGraph, syntheticAdapter, adapt } from "./dit.mjs";
-import { SyntheticWeights } from "./weights.mjs";
-import { linearRegistry, loadLora, attachLoras, destroyLora, rotatedA } from "./lora.mjs";
-import { LatentPipeline } from "./pipeline.mjs";
-import { TorchGenerator } from "./rng.mjs";
-import { Qwen3 } from "./qwen3.mjs";
+import { GPU, native } from "../../anima-studio_amd/js/gpu.mjs";
+import * as ops from "../../anima-studio_amd/js/ops.mjs";
+import { ditRopeTable } from "../../anima-studio_amd/js/common.mjs";
+import { SafeTensors } from "../../anima-studio_amd/js/weights.mjs";
+import { AnimaDiT, ForwardGraph, syntheticAdapter, adapt } from "../../anima-studio_amd/js/dit.mjs";
+import { SyntheticWeights } from "../../anima-studio_amd/js/weights.mjs";
+import { linearRegistry, loadLora, attachLoras, destroyLora, rotatedA } from "../../anima-studio_amd/js/lora.mjs";
+import { LatentPipeline } from "../../anima-studio_amd/js/pipeline.mjs";
+import { TorchGenerator } from "../../anima-studio_amd/js/rng.mjs";
+import { Qwen3 } from "../../anima-studio_amd/js/qwen3.mjs";
 
 const ARR = { f32: Float32Array, i8: Int8Array, u8: Uint8Array, u16: Uint16Array, i32: Int32Array };
 
@@ -207,6 +211,71 @@ async function main() {
     lat.release();
     cond.release();
     console.log(JSON.stringify({ graph: { diffs, n } }));
+  } else if (c.case === "leak") {
+    // tensors dropped without release(): their finalizers return the buffers (run with --expose-gc)
+    const bytes = c.mb * 1024 * 1024;
+    const f0 = native.finalized();
+    for (let i = 0; i < c.n; i++) {
+      const t = gpu.empty([bytes / 4]);
+      ops.zero(gpu, t);
+      global.gc();
+      await new Promise((r) => setImmediate(r));
+    }
+    global.gc();
+    await new Promise((r) => setImmediate(r));
+    const kept = gpu.empty([16]);
+    kept.release();
+    kept.release(); // a second release is a no-op
+    const peak = gpu.pool.peak;
+    console.log(JSON.stringify({ leak: { n: c.n, bytes, finalized: native.finalized() - f0, peak,
+      released_twice_ok: kept.buf === 0 } }));
+  } else if (c.case === "synthdit") {
+    // a seeded synthetic DiT (the weights the oracle restates by name) on given latents / contexts
+    const dit = AnimaDiT.synthetic(gpu, new SyntheticWeights(gpu, c.seed, { mode: c.mode, blocks: c.blocks }));
+    const tc = dit.timeCond(c.sigma);
+    const cond = dit.prepareContext(c.ctx.map((p) => gpu.fromArray(load(p), [c.Lk, 1024])));
+    const blockOut = [];
+    const v = await dit.forward(c.latents.map((p) => load(p)), c.h, c.w, cond, tc, async (i, x) => {
+      if (i === 0) blockOut.push(await gpu.read(x));
+    });
+    v.forEach((vb, b) => save(c.out + "." + b, vb));
+    save(c.out + ".block0", blockOut[0]);
+    tc.release();
+    cond.release();
+  } else if (c.case === "fullstep") {
+    // the full-size CFG step: one latent in both batch halves (as LatentPipeline.generate feeds
+    // it), the cond and uncond contexts; then the same step with the uncond context equal to the
+    // cond one, and the step replayed from a HIP graph
+    const dit = AnimaDiT.synthetic(gpu, new SyntheticWeights(gpu, c.seed, { mode: c.mode, blocks: c.blocks }));
+    const h = c.size / 8, w = c.size / 8, n = 16 * h * w;
+    const ctxA = [0, 1].map((b) => new TorchGenerator(200 + b).randn(c.Lk * 1024));
+    const lat = gpu.empty([2, 16, h, w]);
+    const x = new TorchGenerator(300).randn(n);
+    gpu.write(lat, x);
+    gpu.write(lat, x, n * 4);
+    const tc = dit.timeCond(c.sigma);
+    const run = async (ctxs) => {
+      const cond = dit.prepareContext(ctxs.map((a) => gpu.fromArray(a, [c.Lk, 1024])));
+      gpu.timerStart();
+      const v = await dit.forwardDevice(lat, h, w, cond, tc);
+      const ms = gpu.timerStop();
+      const out = await gpu.read(v);
+      v.release();
+      return { cond, out, ms };
+    };
+    const a = await run(ctxA);
+    const same = await run([ctxA[0], ctxA[0]]);
+    same.cond.release();
+    const fg = await ForwardGraph.capture(dit, lat, h, w, a.cond, tc, false);
+    const g = await gpu.read(fg.run(tc));
+    fg.release();
+    a.cond.release();
+    tc.release();
+    lat.release();
+    save(c.out + ".eager", a.out);
+    save(c.out + ".same", same.out);
+    save(c.out + ".graph", g);
+    console.log(JSON.stringify({ fullstep: { n, ms: a.ms } }));
   } else if (c.case === "qwen3") {
     const te = Qwen3.synthetic(gpu, new SyntheticWeights(gpu, 17), { layers: c.layers, vocab: c.vocab });
     for (const prec of ["fp32", "bf16"]) {
@@ -290,6 +359,8 @@ async function main() {
     });
     v.forEach((vb, b) => save(c.out + "." + b, vb));
     save(c.out + ".block0", blockOut[0]);
+    // which blocks run the stacked q/k/v GEMM (the rest run the three-linear fallback)
+    fs.writeFileSync(c.out + ".stacked.json", JSON.stringify(dit.blocks.map((b) => !!b.self.qkv)));
     st.close();
   } else {
     throw new Error("unknown case " + c.case);

@@ -66,3 +66,28 @@ def test_patchify_roundtrip():
              "const back = unpatchify(q, h, w); "
              "console.log(back.every((v, i) => v === lat[i]) && mask === 0 ? 'ok' : 'bad')")
     assert r.returncode == 0 and r.stdout.strip() == "ok", r.stderr + r.stdout
+
+
+def test_non_finite_numbers_raise_range_error():
+    # a NaN or infinity reaching the C ABI would be cast to an integer (undefined behaviour in C): the
+    # addon raises a RangeError instead and makes no call; a later valid call is unaffected
+    r = node("import { native } from './gpu.mjs'; const out = {}; "
+             "for (const [k, f] of [['nan', () => native.attentionKvBytes(NaN, 16, 512, 0)], "
+             "['inf', () => native.attentionKvBytes(2, 16, Infinity, 0)], "
+             "['ok', () => native.attentionKvBytes(2, 16, 512, 0)]]) { "
+             "try { out[k] = f(); } catch (e) { out[k] = e.name + ': ' + e.message; } } "
+             "console.log(JSON.stringify(out))")
+    assert r.returncode == 0, r.stderr
+    out = json.loads(r.stdout)
+    assert out["nan"].startswith("RangeError") and out["inf"].startswith("RangeError")
+    assert out["ok"] == 2 * 2 * 16 * 512 * 128 * 2
+
+
+def test_attention_precision_default_is_fp32():
+    # ops.attention keeps the reference's fp32 arithmetic unless the caller asks for bf16; an unknown
+    # precision is rejected before any device work
+    r = node("import * as ops from './ops.mjs'; let msg = ''; "
+             "try { ops.attention({ ctx: null, empty: () => ({ buf: 0 }) }, { q: { buf: 0 }, Lq: 1, Lk: 1, H: 1, D: 128, "
+             "ldq: 128, precision: 'fp16' }); } catch (e) { msg = e.message; } console.log(JSON.stringify({ msg }))")
+    assert r.returncode == 0, r.stderr
+    assert "unknown precision fp16" in json.loads(r.stdout)["msg"]

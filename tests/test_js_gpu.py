@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle as orc
-from helpers import PKG_DIR, report
+from helpers import PKG_DIR, RUN_CASE, report
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")]
 
@@ -18,11 +18,11 @@ JS = os.path.join(PKG_DIR, "js")
 HD = 128
 
 
-def run_case(tmp_path, spec):
+def run_case(tmp_path, spec, flags=()):
     path = tmp_path / "case.json"
     path.write_text(json.dumps(spec))
     print(f"[case] js {spec['case']}", flush=True)
-    r = subprocess.run(["node", os.path.join(JS, "run_case.mjs"), str(path)], capture_output=True, text=True, timeout=300)
+    r = subprocess.run(["node", *flags, RUN_CASE, str(path)], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stderr[-3000:]
     return r
 
@@ -57,6 +57,36 @@ def test_js_attention_fused(tmp_path):
         model = orc.attention("bf16", np.ascontiguousarray(nq[rows]), nq, nq, B=1, Lq=len(rows), Lk=L, H=H, D=HD,
                               ldq=ld, ldk=ld, ldv=ld, k_off=H * HD, v_off=2 * H * HD)[0]
         assert report(f"js attention b={b} vs bf16 model", got[b, rows], model)[0] <= 3e-4
+
+
+def test_js_attention_default_precision_is_fp32(tmp_path):
+    """ops.attention without a precision runs the reference's fp32 arithmetic (the fp32-MFMA kernel):
+    within the fp32 bar of the float64 oracle, which the bf16 kernel (~3e-3) would miss."""
+    B, Hp, Wp, H = 1, 16, 16, 4
+    L = Hp * Wp
+    qkv = orc.randn(95, B * L * 3 * H * HD).reshape(B, L, 3 * H * HD)
+    qn = (1 + 0.02 * orc.randn(96, HD)).astype(np.float32)
+    kn = (1 + 0.02 * orc.randn(97, HD)).astype(np.float32)
+    out = str(tmp_path / "o.bin")
+    run_case(tmp_path, {"case": "attention", "B": B, "Hp": Hp, "Wp": Wp, "H": H, "qkv": write(tmp_path, "qkv.bin", qkv),
+                        "qn": write(tmp_path, "qn.bin", qn), "kn": write(tmp_path, "kn.bin", kn), "out": out})
+    cs = orc.dit_rope_table(Hp, Wp)
+    ld = 3 * H * HD
+    nq = orc.qk_norm_rope(qkv[0], L, H, HD, ld, qn, kn, cs, L * 64)
+    ref = orc.attention("f64", nq, nq, nq, B=1, Lq=L, Lk=L, H=H, D=HD, ldq=ld, ldk=ld, ldv=ld, k_off=H * HD,
+                        v_off=2 * H * HD)[0]
+    assert report("js attention (default precision) vs fp64", read(out).reshape(L, H * HD), ref)[0] <= 1e-5
+
+
+def test_js_tensor_finalizer_returns_dropped_buffers(tmp_path):
+    """Device Tensors dropped without release() go back to the pool when the garbage collector
+    reclaims their handles (the leak guard of gpu.mjs / addon.c); release() disarms the finalizer."""
+    r = run_case(tmp_path, {"case": "leak", "n": 24, "mb": 64}, flags=("--expose-gc",))
+    info = json.loads(next(ln for ln in r.stdout.splitlines() if '"leak"' in ln))["leak"]
+    print(f"leak guard: {info}", flush=True)
+    assert info["finalized"] >= info["n"] - 2  # the last allocations may still be referenced
+    assert info["peak"] <= 6 * info["bytes"]  # freed buffers are reused, not accumulated
+    assert info["released_twice_ok"]
 
 
 def test_js_qk_norm_rope_bit_exact(tmp_path):
