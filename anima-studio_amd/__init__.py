@@ -120,6 +120,9 @@ def lib():
         L.anima_linear.argtypes = [_vp, ctypes.POINTER(LinearDesc)]
         L.anima_sampler_step.argtypes = [_vp, ctypes.POINTER(SamplerDesc)]
         L.anima_split3_bf16.argtypes = [_vp, _vp, _vp, _i64]
+        L.anima_attention_noalloc.argtypes = [_vp, ctypes.POINTER(AttnDesc)]
+        L.anima_attention_noalloc_scratch_bytes.argtypes = []
+        L.anima_attention_noalloc_scratch_bytes.restype = _i64
         L.anima_fill_random.argtypes = [_vp, _vp, _i64, ctypes.c_int, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]
         L.anima_graph_begin.argtypes = [_vp]
         L.anima_graph_end.argtypes = [_vp, P(_vp)]
@@ -257,10 +260,11 @@ class Context:
     def attention(self, *, q, k, v, o, B, Lq, Lk, H, D, ldq, ldk, ldv, ldo=None, q_off=0, k_off=0, v_off=0,
                   o_off=0, q_bstride=None, k_bstride=None, v_bstride=None, o_bstride=None, group=1, scale=0.0,
                   kv_len=None, precision=PREC_BF16, q_norm=None, k_norm=None, rope_cs=None, rope_sin_off=0,
-                  eps=1e-6, causal=0, kv_prep=None, prepare_into=None, kv_prep_bytes=None):
+                  eps=1e-6, causal=0, kv_prep=None, prepare_into=None, kv_prep_bytes=None, noalloc=False):
         """anima_attention; kv_prep: K/V converted by a call with prepare_into (which runs
         anima_attention_prepare_kv into that buffer instead of the attention).  kv_prep_bytes
-        defaults to the size the call's shape and precision take."""
+        defaults to the size the call's shape and precision take.  noalloc: anima_attention_noalloc
+        (the K/V conversion in the library's static scratch, no allocation)."""
         ldo = ldo if ldo is not None else H * D
         kl = (ctypes.c_int * B)(*[int(x) for x in kv_len]) if kv_len is not None else None
         d = AttnDesc(B=B, Lq=Lq, Lk=Lk, H=H, D=D, group=group,
@@ -276,7 +280,13 @@ class Context:
                       if (kv_prep is not None or prepare_into is not None) else 0))
         if prepare_into is not None:
             return self._check(lib().anima_attention_prepare_kv(self.h, ctypes.byref(d), _ptr(prepare_into)))
+        if noalloc:
+            return self._check(lib().anima_attention_noalloc(self.h, ctypes.byref(d)))
         return self._check(lib().anima_attention(self.h, ctypes.byref(d)))
+
+    @staticmethod
+    def attention_noalloc_scratch_bytes():
+        return lib().anima_attention_noalloc_scratch_bytes()
 
     @staticmethod
     def attention_kv_bytes(B, Hkv, Lk, precision=PREC_BF16):

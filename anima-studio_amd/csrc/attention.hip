@@ -26,6 +26,7 @@
 // the offset was raised (a power-of-two rescale).
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "common.h"
 #include "internal.h"
@@ -1133,7 +1134,11 @@ static int attention_d64(anima_ctx* c, const anima_attn_desc* d) {
   return rc;
 }
 
-int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
+int attention_launch(anima_ctx* c, const anima_attn_desc* d) { return attention_launch_ws(c, d, nullptr); }
+
+// scratch != nullptr: the K/V prep goes there (the caller checked its size) instead of the
+// context's workspace.
+int attention_launch_ws(anima_ctx* c, const anima_attn_desc* d, void* scratch) {
   if (d->D == 64) return attention_d64(c, d);
   int kv_len[MAXB];
   int rc = attention_check(c, d, kv_len);
@@ -1149,7 +1154,8 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
   const size_t plane = (size_t)d->B * Hkv * Lkp * HD * esz;
   void* ws = (void*)d->kv_prep;
   if (!ws) {
-    if ((rc = workspace(c, 2 * plane, &ws))) return rc;
+    if (scratch) ws = scratch;
+    else if ((rc = workspace(c, 2 * plane, &ws))) return rc;
     if ((rc = prep_kv_launch(c, d, ws))) return rc;
   }
 
@@ -1210,6 +1216,56 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) {
 }  // namespace anima
 
 namespace anima {
+
+// ---- the no-allocation entry point's scratch: the K/V prep of anima_attention_noalloc lives in
+// this file-scope device array (one per GPU, loaded with the code object, held until the process
+// ends).  Host code never passes `scratch` itself to a kernel (in host code the name is a host-side
+// stand-in): its device address is looked up once per device at context creation and kept.
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+static void* g_scratch_ptr[MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+int attention_scratch_init(anima_ctx* c) {
+  if (c->device < 0 || c->device >= MAX_DEVICES)
+    return fail(c, ANIMA_E_UNSUPPORTED, "anima_init: device %d beyond the %d devices with a scratch address slot", c->device,
+                MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[c->device]) {  // the caller made c->device current
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return hip_fail(c, e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[c->device] = ptr;
+  }
+  c->scratch = g_scratch_ptr[c->device];
+  return ANIMA_OK;
+}
+
+size_t attention_scratch_bytes() { return NOALLOC_SCRATCH_BYTES; }
+
+int attention_noalloc_launch(anima_ctx* c, const anima_attn_desc* d) {
+  if (!d) return fail(c, ANIMA_E_ARG, "anima_attention_noalloc: null descriptor");
+  if (d->D != HD)
+    return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention_noalloc: head dim %d (the allocation-free path covers D=%d)", d->D, HD);
+  if (!c->scratch) return fail(c, ANIMA_E_STATE, "anima_attention_noalloc: no scratch address for device %d", c->device);
+  if (!d->kv_prep) {
+    const int group = d->group <= 0 ? 1 : d->group;
+    const int64_t need = (d->B >= 1 && d->H >= 1 && d->H % group == 0) ? attention_kv_bytes(d->B, d->H / group, d->Lk, d->precision) : 0;
+    if (need > (int64_t)NOALLOC_SCRATCH_BYTES)
+      return fail(c, ANIMA_E_ARG,
+                  "anima_attention_noalloc: B=%d, %d kv heads, Lk=%d at this precision need %lld bytes of K/V scratch; the maximum is %zu",
+                  d->B, d->H / group, d->Lk, (long long)need, NOALLOC_SCRATCH_BYTES);
+  }
+  // the profiler's event brackets may create events: none are taken during this call
+  const bool prof = c->profiling;
+  c->profiling = false;
+  const int rc = attention_launch_ws(c, d, c->scratch);
+  c->profiling = prof;
+  return rc;
+}
+
 int64_t attention_kv_bytes(int B, int Hkv, int Lk, int precision) {
   if (B < 1 || Hkv < 1 || Lk < 1) return 0;
   const int64_t Lkp = (Lk + BK - 1) / BK * BK;

@@ -47,6 +47,8 @@ struct anima_ctx {
   // attention workspace (K in bf16/fp32, V transposed), grown on demand
   void* ws = nullptr;
   size_t ws_bytes = 0;
+  // device address of this device's static K/V scratch (anima_attention_noalloc)
+  void* scratch = nullptr;
   // stream capture (anima_graph_begin .. anima_graph_end): buffers freed while capturing are
   // parked in cap_free, reused only by later allocations of the same capture, and owned by the
   // graph at the end (its replays keep using them); cap_ws: the capture used the workspace
@@ -82,6 +84,11 @@ struct Launch {
 
 // ---- kernel launchers (attention.hip)
 int attention_launch(anima_ctx* c, const anima_attn_desc* d);
+int attention_launch_ws(anima_ctx* c, const anima_attn_desc* d, void* scratch);
+// Looks up this device's scratch address (once per device; the context's device is current).
+int attention_scratch_init(anima_ctx* c);
+size_t attention_scratch_bytes();
+int attention_noalloc_launch(anima_ctx* c, const anima_attn_desc* d);
 int attention_prepare_kv_launch(anima_ctx* c, const anima_attn_desc* d, void* dst);
 int64_t attention_kv_bytes(int B, int Hkv, int Lk, int precision);
 

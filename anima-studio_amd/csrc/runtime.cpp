@@ -184,8 +184,18 @@ int anima_init(int device, anima_ctx** out) {
   if (e == hipSuccess) e = hipEventCreate(&c->t1);
   if (e != hipSuccess) {
     fail(nullptr, ANIMA_E_HIP, "anima_init: %s", hipGetErrorString(e));
+    if (c->stream) hipStreamDestroy(c->stream);
     delete c;
     return ANIMA_E_HIP;
+  }
+  int rc = attention_scratch_init(c);
+  if (rc != ANIMA_OK) {
+    fail(nullptr, rc, "anima_init: %s", c->err.c_str());
+    hipEventDestroy(c->t0);
+    hipEventDestroy(c->t1);
+    hipStreamDestroy(c->stream);
+    delete c;
+    return rc;
   }
   *out = c;
   return ANIMA_OK;
@@ -414,6 +424,13 @@ int anima_attention(anima_ctx* c, const anima_attn_desc* d) {
   if (!d) return fail(c, ANIMA_E_ARG, "anima_attention: null descriptor");
   return attention_launch(c, d);
 }
+
+int anima_attention_noalloc(anima_ctx* c, const anima_attn_desc* d) {
+  CHECK_CTX(c);
+  return attention_noalloc_launch(c, d);
+}
+
+int64_t anima_attention_noalloc_scratch_bytes(void) { return (int64_t)attention_scratch_bytes(); }
 
 int anima_attention_prepare_kv(anima_ctx* c, const anima_attn_desc* d, void* kv_prep) {
   CHECK_CTX(c);

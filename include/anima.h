@@ -149,6 +149,19 @@ int anima_attention(anima_ctx* ctx, const anima_attn_desc* desc);
 int anima_attention_prepare_kv(anima_ctx* ctx, const anima_attn_desc* desc, void* kv_prep);
 int64_t anima_attention_kv_bytes(int B, int Hkv, int Lk, int precision);
 
+/* anima_attention without any device allocation.  No counterpart in the reference: it is for callers
+ * that cannot allocate (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  The same kernels and results as anima_attention (bit-identical); the K/V conversion
+ * goes into a static device array of anima_attention_noalloc_scratch_bytes() (64 MiB) per GPU,
+ * loaded with the library and held until the process ends, instead of the context's workspace.
+ * A call whose K/V conversion needs more (anima_attention_kv_bytes(B, H / group, Lk, precision)
+ * above the maximum; B=2, 16 heads, Lk=4096 in bf16 is exactly 64 MiB) fails with ANIMA_E_ARG;
+ * with desc->kv_prep set no scratch is used.  D must be 128 (ANIMA_E_UNSUPPORTED otherwise).  The
+ * profiler records nothing for these calls.  Every call on one GPU shares that GPU's array: calls
+ * on different contexts / streams of the same GPU that overlap in time race on it (serialize them). */
+int anima_attention_noalloc(anima_ctx* ctx, const anima_attn_desc* desc);
+int64_t anima_attention_noalloc_scratch_bytes(void);
+
 /* ---------------------------------------------------------------- row ops */
 
 /* ops.qkNormRope (app/gpu/ops.js:140-145; kernels.js:304-334): in place on the q and k parts of
