@@ -117,26 +117,33 @@ async function main() {
   for (let i = 0; i < warmup; i++) v = await step();
   await gpu.sync();
   if (gpu.profiler) gpu.profiler.reset();
+  // each step timed on its own (HIP events on the library stream around the whole step)
   const timed = async (eager) => {
-    gpu.timerStart();
-    for (let i = 0; i < steps; i++) v = await step(eager);
-    return gpu.timerStop() / steps;
+    const xs = [];
+    for (let i = 0; i < steps; i++) {
+      gpu.timerStart();
+      v = await step(eager);
+      xs.push(gpu.timerStop());
+    }
+    return xs;
   };
   const median = (xs) => xs.slice().sort((a, b) => a - b)[xs.length >> 1];
-  let ms, graphMs = null;
+  let ms, graphMs = null, stepMs;
   if (fg) {
     // graph replays and eager forwards (launched kernel by kernel) in alternating blocks of
-    // `steps` steps; medians over the rounds
+    // `steps` steps; medians over every step of the rounds
     await step(true);
-    const g = [], e = [];
+    let g = [], e = [];
     for (let r = 0; r < rounds; r++) {
-      g.push(await timed(false));
-      e.push(await timed(true));
+      g = g.concat(await timed(false));
+      e = e.concat(await timed(true));
     }
     graphMs = median(g);
     ms = median(e);
+    stepMs = e;
   } else {
-    ms = await timed(false);
+    stepMs = await timed(false);
+    ms = median(stepMs);
   }
   await gpu.sync();
   let finite = true;
@@ -147,7 +154,8 @@ async function main() {
   const perBlock = 2 * M * D_(3 * 2048, 2048) + 2 * M * D_(2048, 2048) * 3 + 2 * M * D_(8192, 2048) * 2 +
     4 * B * L * L * 128 * 16 + 4 * B * L * Lk * 128 * 16;
   const flops = nBlocks * perBlock + 2 * M * 2048 * 68 + 2 * M * 64 * 2048;
-  const out = { dit_step_ms: Number(ms.toFixed(3)), size, blocks: nBlocks, mode, B, tokens: L, steps, warmup, lora_rank: loraRank, graph: useGraph,
+  const out = { dit_step_ms: Number(ms.toFixed(3)), step_ms: stepMs.map((x) => Number(x.toFixed(3))), size, blocks: nBlocks,
+    mode, B, tokens: L, steps, warmup, lora_rank: loraRank, graph: useGraph,
     graph_step_ms: graphMs === null ? null : Number(graphMs.toFixed(3)),
     flops_per_step: flops, tflops: Number((flops / (ms / 1e3) / 1e12).toFixed(2)), finite,
     peak_gib: Number((gpu.pool.peak / 2 ** 30).toFixed(2)) };

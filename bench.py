@@ -35,19 +35,19 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-dit", action="store_true", help="skip the full DiT step leg")
-    p.add_argument("--dit-steps", type=int, default=3)
+    p.add_argument("--dit-steps", type=int, default=5)
     p.add_argument("--no-linears", action="store_true", help="skip the quantized-linear leg")
     p.add_argument("--copy-mb", type=int, default=0,
                    help="only run the elementwise copy kernel on a buffer of this many MiB (HBM counter calibration)")
     return p.parse_args()
 
 
-def cpu_baseline():
+def cpu_baseline(flag="--attention"):
     """PyTorch fp32 on the host cores (oracle/torch_ref.py), run in its own process so that
     torch's bundled HIP runtime never shares a process with libanima.so."""
     import subprocess
 
-    r = subprocess.run([sys.executable, "-m", "oracle.torch_ref", "--attention"], cwd=ROOT, capture_output=True,
+    r = subprocess.run([sys.executable, "-m", "oracle.torch_ref", flag], cwd=ROOT, capture_output=True,
                        text=True, timeout=600)
     if r.returncode != 0:
         raise RuntimeError("cpu baseline failed: " + r.stderr[-2000:])
@@ -130,6 +130,127 @@ def causal_attention(m, ctx, np):
     flops = 4.0 * H * D * L * (L + 1) / 2
     return {"B": B, "tokens": L, "heads": H, "kv_heads": Hkv, "ms": round(ms, 5),
             "TFLOP/s": round(flops / ms / 1e9, 1), "kernel": "attn_flash_bf16 (4 waves, causal mask)"}
+
+
+FP32_PEAK_TFLOPS = 157.3
+
+
+def timed_kernels(ctx, call, reps):
+    """Per-kernel average ms of `call` (HIP events around each launch on the library stream) and
+    the whole call's ms (events around the reps)."""
+    for _ in range(3):
+        call()
+    ctx.sync()
+    ctx.timer_start()
+    for _ in range(reps):
+        call()
+    total = ctx.timer_stop() / reps
+    ctx.profile(True)
+    ctx.profile_reset()
+    for _ in range(reps):
+        call()
+    rep = {r["name"]: r for r in ctx.profile_report()}
+    ctx.profile(False)
+    return total, {k: r["ms"] / r["count"] for k, r in rep.items()}, rep
+
+
+def self_attention_case(m, ctx, np, B, Hp, Wp, precision, reps):
+    """The fused self-attention op (q/k RMSNorm + 3D RoPE) at B x (Hp*Wp) tokens, 16 heads x 128:
+    whole-op ms and TFLOP/s, the flash kernel's own ms and its fraction of the precision's peak."""
+    H, D = 16, 128
+    L = Hp * Wp
+    rng = np.random.default_rng(2024 + B * L)
+    bufs = [ctx.upload(rng.standard_normal((B, L, 3 * H * D), dtype=np.float32)),
+            ctx.upload((1 + 0.02 * rng.standard_normal(D)).astype(np.float32)),
+            ctx.upload((1 + 0.02 * rng.standard_normal(D)).astype(np.float32)), ctx.upload(m.dit_rope_table(Hp, Wp)),
+            ctx.empty((B, L, H * D))]
+    qkv, qn, kn, cs, o = bufs
+    ld = 3 * H * D
+    prec = m.PREC_BF16 if precision == "bf16" else m.PREC_FP32
+
+    def call():
+        ctx.attention(q=qkv, k=qkv, v=qkv, o=o, B=B, Lq=L, Lk=L, H=H, D=D, ldq=ld, ldk=ld, ldv=ld, k_off=H * D,
+                      v_off=2 * H * D, precision=prec, q_norm=qn, k_norm=kn, rope_cs=cs, rope_sin_off=L * 64)
+
+    total, per, _ = timed_kernels(ctx, call, reps)
+    for x in bufs:
+        x.release()
+    flops = 4.0 * B * H * L * L * D
+    kname = [k for k in per if k.startswith("attn.flash")][0]
+    peak = BF16_PEAK_TFLOPS if precision == "bf16" else FP32_PEAK_TFLOPS
+    return {"B": B, "tokens": L, "heads": H, "precision": precision, "ms": round(total, 5),
+            "TFLOP/s": round(flops / total / 1e9, 1), "kernel": kname, "kernel_ms": round(per[kname], 5),
+            "kernel_TFLOP/s": round(flops / per[kname] / 1e9, 1), "peak_TFLOP/s": peak,
+            "frac": round(flops / per[kname] / 1e9 / peak, 4), "op_frac": round(flops / total / 1e9 / peak, 4)}
+
+
+def cross_attention(m, ctx, np, reps):
+    """Cross-attention at 1024x1024 (the DiT's, B=2): q [2, 4096, 2048] with q RMSNorm; K/V projected
+    from 512 context tokens of dim 1024 by int8 ConvRot linears (1024 -> 2048) with k RMSNorm,
+    converted once (anima_attention_prepare_kv); valid key lengths drawn from U{64..512} with a fixed
+    seed.  Attention FLOPs 4 * H * D * Lq * sum_b Lv_b."""
+    B, L, Lk, H, D, CTX = 2, 4096, 512, 16, 128, 1024
+    rng = np.random.default_rng(33)
+    kv_len = rng.integers(64, Lk + 1, size=B).astype(np.int32)
+    sw = lambda N, K: (rng.uniform(0.5, 1.5, N) / (127 * np.sqrt(K))).astype(np.float32)
+    grid = lambda N, K: np.clip(np.rint(40 * rng.standard_normal((N, K))), -127, 127).astype(np.int8)
+    bufs = [ctx.upload(rng.standard_normal((B, L, H * D), dtype=np.float32)),
+            ctx.upload((1 + 0.02 * rng.standard_normal(D)).astype(np.float32)),
+            ctx.upload((1 + 0.02 * rng.standard_normal(D)).astype(np.float32)),
+            ctx.upload(rng.standard_normal((B * Lk, CTX), dtype=np.float32)),
+            ctx.upload(grid(H * D, CTX)), ctx.upload(sw(H * D, CTX)), ctx.upload(grid(H * D, CTX)),
+            ctx.upload(sw(H * D, CTX)), ctx.empty((B * Lk, H * D)), ctx.empty((B * Lk, H * D)),
+            ctx.empty((B, L, H * D))]
+    q, qn, kn, cx, wk, sk, wv, sv, k, v, o = bufs
+    Wk, Wv = m.weight(m.W_I8, H * D, CTX, wk, scale=sk), m.weight(m.W_I8, H * D, CTX, wv, scale=sv)
+    kvb = m.Context.attention_kv_bytes(B, H, Lk, m.PREC_BF16)
+    prep = ctx.empty(kvb, np.uint8)
+    bufs.append(prep)
+    common = dict(B=B, Lq=L, Lk=Lk, H=H, D=D, ldq=H * D, ldk=H * D, ldv=H * D, kv_len=kv_len, q_norm=qn)
+
+    def project():  # once per prompt pair: K/V linears, k RMSNorm, conversion to the operand layout
+        ctx.linear(Wk, B * Lk, k, x=cx, x_rotated=False)
+        ctx.rmsnorm(k, kn, k, B * Lk * H, D)
+        ctx.linear(Wv, B * Lk, v, x=cx, x_rotated=False)
+        ctx.attention(q=q, k=k, v=v, o=o, prepare_into=prep, **common)
+
+    def call():
+        ctx.attention(q=q, k=None, v=None, o=o, kv_prep=prep, **common)
+
+    p_total, p_per, _ = timed_kernels(ctx, project, 10)
+    total, per, _ = timed_kernels(ctx, call, reps)
+    for x in bufs:
+        x.release()
+    flops = 4.0 * H * D * L * float(kv_len.sum())
+    kname = [kk for kk in per if kk.startswith("attn.flash")][0]
+    return {"B": B, "Lq": L, "Lk": Lk, "kv_len": kv_len.tolist(), "ms": round(total, 5),
+            "TFLOP/s": round(flops / total / 1e9, 1), "kernel": kname, "kernel_ms": round(per[kname], 5),
+            "frac": round(flops / per[kname] / 1e9 / BF16_PEAK_TFLOPS, 4),
+            "kv_projection": {"ms": round(p_total, 5), "GOP": round(2 * 2 * B * Lk * CTX * H * D / 1e9, 3),
+                              "note": "per prompt pair: int8 K and V linears (1024 -> 2048), k RMSNorm, K/V conversion"}}
+
+
+def prepasses(m, ctx, np, reps):
+    """The HBM-bound passes in front of the quantized projections at x [2*4096, 2048]: LayerNorm +
+    adaLN + ConvRot Hadamard + per-token int8 (the QKV input), and Hadamard + per-token int8 (the
+    out-projection input).  Algorithmic bytes: read 67.1 MB, write 16.8 MB int8 + 32 KB scales."""
+    M, K = 8192, 2048
+    rng = np.random.default_rng(5)
+    bufs = [ctx.upload(rng.standard_normal((M, K), dtype=np.float32)),
+            ctx.upload((0.1 * rng.standard_normal(3 * K)).astype(np.float32)), ctx.empty((M, K), np.int8),
+            ctx.empty(M)]
+    x, mod, q, sc = bufs
+    nbytes = M * K * 4 + M * K + M * 4
+    out = {}
+    for name, call in (("layernorm_mod_int8", lambda: ctx.layernorm_mod(x, mod, 0, K, M, K, rotate=True, q=q, s=sc)),
+                       ("hadamard_int8", lambda: ctx.quant_rows(x, M, K, True, q, sc))):
+        total, per, _ = timed_kernels(ctx, call, reps)
+        kname, kms = max(per.items(), key=lambda kv: kv[1])
+        out[name] = {"M": M, "K": K, "kernel": kname, "ms": round(kms, 5), "MB": round(nbytes / 1e6, 1),
+                     "GB/s": round(nbytes / kms / 1e6, 1), "frac_hbm": round(nbytes / kms / 1e6 / HBM_PEAK_GBS, 4)}
+    for b in bufs:
+        b.release()
+    return out
 
 
 LINEAR_SHAPES = (("qkv", 6144, 2048, "store"), ("out", 2048, 2048, "gated"), ("mlp1", 8192, 2048, "gelu"),
@@ -254,6 +375,15 @@ def main():
         prep_gbs = prep["bytes"] / prep["count"] / (prep_ms / 1e3) / 1e9 if prep else None
         for b in (d_qkv, d_qn, d_kn, d_cs, d_o):
             b.release()
+        t = time.time()
+        configs = {
+            "config1_n1024_bf16": self_attention_case(m, ctx, np, 1, 32, 32, "bf16", 50),
+            "config1_n1024_fp32": self_attention_case(m, ctx, np, 1, 32, 32, "fp32", 20),
+            "config2_n4096_fp32": self_attention_case(m, ctx, np, 2, 64, 64, "fp32", 5),
+            "config3_cross_lk512": cross_attention(m, ctx, np, 50),
+            "config4_prepasses": prepasses(m, ctx, np, 50),
+        }
+        print(f"bench: configs 1, 3, 4 and fp32 {time.time() - t:.1f} s", file=sys.stderr, flush=True)
         causal = causal_attention(m, ctx, np)
         lin = None
         if not args.no_linears:
@@ -286,6 +416,7 @@ def main():
         "prep_kernel": {"ms": round(prep_ms, 5) if prep_ms else None, "GB/s": round(prep_gbs, 1) if prep_gbs else None,
                         "frac_hbm": round(prep_gbs / HBM_PEAK_GBS, 4) if prep_gbs else None},
     }
+    out.update(configs)
     out["causal_attention"] = causal
     if lin is not None:
         out["linears"] = lin
@@ -296,7 +427,11 @@ def main():
     if not args.no_cpu:
         t = time.time()
         out["cpu_baseline"] = cpu_baseline()
-        print(f"bench: cpu baseline {time.time() - t:.1f} s", file=sys.stderr, flush=True)
+        # the reference-math CPU figures for the quantized projections (W8A8 and W8A32) and the
+        # full step (reported beside the GPU ones, not a target)
+        out["cpu_baselines_more"] = {"config4_linears": cpu_baseline("--linears"),
+                                     "config5_dit_step": cpu_baseline("--dit-step")}
+        print(f"bench: cpu baselines {time.time() - t:.1f} s", file=sys.stderr, flush=True)
     print(json.dumps(out), flush=True)
 
 

@@ -1,9 +1,13 @@
 """PyTorch fp32 CPU restatement of the reference's attention math -- TEST/BASELINE ONLY.
 
-Restates tools/reference.py's DiT self-attention in torch fp32 on the CPU: rms_norm
-(reference.py:93-94), rotate_half RoPE with the 3D Cosmos angles (97-99, 174-187, 214-229)
-and F.scaled_dot_product_attention (109-111).  bench.py times it on the host cores as the
-CPU baseline; tests use it as an independent formulation of the fused norm+RoPE+attention.
+Restates tools/reference.py's DiT math in torch fp32 on the CPU: rms_norm (reference.py:93-94),
+rotate_half RoPE with the 3D Cosmos angles (97-99, 174-187, 214-229),
+F.scaled_dot_product_attention (109-111), the LayerNorm + adaLN modulation and gated residuals of
+the block (231-242), and the ConvRot int8 linears in two semantics: W8A32 (the reference's own:
+dequantized weights, fp32 activations) and W8A8 (this build's: activations quantized per token
+after the rotation, emulated in fp32).  bench.py times it on the host cores as the CPU baseline
+(attention, the quantized projections, the full 28-block step); tests/test_oracle.py checks its
+attention against the C oracle.
 """
 
 from __future__ import annotations
@@ -92,9 +96,136 @@ def attention_baseline(B=2, Hp=64, Wp=64, H=16, D=128):
                       f"N={L} D={D}; median of 3 after 1 warm-up = {t * 1e3:.0f} ms/step"}
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def hadamard256(x):
+    """ConvRot rotation (tools/quant.py:30-45): x @ kron(H4, H4, H4, H4) / 16 per group of 256."""
+    h4 = torch.tensor([[1., 1., 1., -1.], [1., 1., -1., 1.], [1., -1., 1., 1.], [-1., 1., 1., 1.]])
+    h = torch.kron(torch.kron(h4, h4), torch.kron(h4, h4)) / 16
+    return (x.reshape(-1, 256) @ h).reshape(x.shape)
+
+
+def token_fake_quant(x):
+    """W8A8's per-token int8 activations (s = amax/127, q = rint(x/s) clamped), returned dequantized."""
+    s = x.abs().amax(-1, keepdim=True) / 127
+    s = torch.where(s == 0, torch.ones_like(s), s)
+    return torch.clamp(torch.round(x / s), -127, 127) * s
+
+
+def qlinear(x, w_deq, mode):
+    """ConvRot int8 linear: y = H(x) @ W^T with W the dequantized rotated-domain weight; W8A8 also
+    quantizes the rotated activations per token."""
+    xr = hadamard256(x)
+    if mode == "w8a8":
+        xr = token_fake_quant(xr)
+    return xr @ w_deq.T
+
+
+def int8_weight(g, N, K):
+    """comfy_quant int8 weight of the configs: round(40 N(0,1)) clipped to +-127, per-row scale."""
+    q = torch.clamp(torch.round(40 * torch.randn(N, K, generator=g)), -127, 127)
+    s = (0.5 + torch.rand(N, 1, generator=g)) / (127 * math.sqrt(K))
+    return q * s
+
+
+def linears_baseline(mode):
+    """The attention sublayer's quantized projections of the 1024x1024 CFG batch (x [2*4096, 2048]:
+    QKV 2048 -> 6144 and out 2048 -> 2048, 275 GOP) with the rotation and, for W8A8, the activation
+    quantization; median of 3 after 1 warm-up."""
+    import os
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2 * 4096, 2048, generator=g)
+    wq, wo = int8_weight(g, 6144, 2048), int8_weight(g, 2048, 2048)
+    with torch.no_grad():
+        t = seconds(lambda: (qlinear(x, wq, mode), qlinear(x, wo, mode)), reps=3, warmup=1)
+    ops = 2.0 * 8192 * 2048 * (6144 + 2048)
+    return {"value": round(ops / t / 1e12, 4), "unit": "TOP/s", "cores": cores, "kind": "port", "cpu": cpu_model(),
+            "ms": round(t * 1e3, 1),
+            "sample": f"QKV (2048->6144) + out (2048->2048) int8 ConvRot linears on x [2*4096, 2048], {mode.upper()} "
+                      f"semantics, torch fp32; median of 3 after 1 warm-up"}
+
+
+def dit_step_baseline(mode="w8a32", blocks=28):
+    """One full DiT step at 1024x1024, B=2 CFG (reference.py:231-242 per block, batched): self-attention
+    with q/k RMSNorm + RoPE, cross-attention to prepared 512-token K/V, GELU MLP, gated residuals,
+    quantized linears in `mode`.  One run; the weights of one block serve all 28 (the work does not
+    depend on their values), the per-prompt cross K/V are prepared outside the timed step."""
+    import os
+    import time
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    B, Hp, Wp, H, D, C = 2, 64, 64, 16, 128, 2048
+    L, Lk = Hp * Wp, 512
+    g = torch.Generator().manual_seed(4)
+    W = {n: int8_weight(g, N, K) for n, N, K in (("qkv", 3 * C, C), ("o", C, C), ("cq", C, C), ("co", C, C),
+                                                  ("m1", 4 * C, C), ("m2", C, 4 * C))}
+    norms = [1 + 0.02 * torch.randn(D, generator=g) for _ in range(3)]
+    kc = rms_norm(torch.randn(B, H, Lk, D, generator=g), norms[2])
+    vc = torch.randn(B, H, Lk, D, generator=g)
+    mods = [0.1 * torch.randn(3, 3 * C, generator=g) for _ in range(3)]
+    cos, sin = dit_rope(Hp, Wp)
+    x = torch.randn(B * L, C, generator=g)
+
+    def ln_mod(x, m):
+        return F.layer_norm(x, (C,), eps=1e-6) * (1 + m[C:2 * C]) + m[:C]
+
+    def block(x):
+        m = mods[0][0]
+        qkv = qlinear(ln_mod(x, m), W["qkv"], mode).view(B, L, 3, H, D)
+        q = rms_norm(qkv[:, :, 0], norms[0]).transpose(1, 2)
+        k = rms_norm(qkv[:, :, 1], norms[1]).transpose(1, 2)
+        v = qkv[:, :, 2].transpose(1, 2)
+        q = q * cos + rotate_half(q) * sin
+        k = k * cos + rotate_half(k) * sin
+        a = F.scaled_dot_product_attention(q, k, v).transpose(1, 2).reshape(B * L, C)
+        x = x + m[2 * C:] * qlinear(a, W["o"], mode)
+        m = mods[1][0]
+        q = rms_norm(qlinear(ln_mod(x, m), W["cq"], mode).view(B, L, H, D), norms[0]).transpose(1, 2)
+        a = F.scaled_dot_product_attention(q, kc, vc).transpose(1, 2).reshape(B * L, C)
+        x = x + m[2 * C:] * qlinear(a, W["co"], mode)
+        m = mods[2][0]
+        h = F.gelu(qlinear(ln_mod(x, m), W["m1"], mode))
+        return x + m[2 * C:] * qlinear(h, W["m2"], mode)
+
+    with torch.no_grad():
+        block(x[:512].repeat(16, 1))  # warm-up of the kernels (one block)
+        t = time.perf_counter()
+        for _ in range(blocks):
+            x = block(x)
+        t = time.perf_counter() - t
+    M = B * L
+    flops = blocks * (2 * M * C * (3 * C + C + C + C + 8 * C) + 4 * B * H * L * L * D + 4 * B * H * L * Lk * D)
+    return {"value": round(t * 1e3, 1), "unit": "ms", "tflops": round(flops / t / 1e12, 4), "cores": cores, "kind": "port",
+            "cpu": cpu_model(),
+            "sample": f"one full {blocks}-block DiT step at 1024x1024, B=2 CFG, {mode.upper()} linears, torch fp32 "
+                      f"(one run; one block's weights for all blocks, cross K/V prepared outside the step)"}
+
+
 if __name__ == "__main__":
     import json
     import sys
 
     if "--attention" in sys.argv:
-        print(json.dumps(attention_baseline()))
+        out = attention_baseline()
+        out["cpu"] = cpu_model()
+        print(json.dumps(out))
+    if "--linears" in sys.argv:
+        print(json.dumps({m: linears_baseline(m) for m in ("w8a8", "w8a32")}))
+    if "--dit-step" in sys.argv:
+        # a bounded sample: 7 of the 28 (identical-cost) blocks, scaled to the whole step
+        r = dit_step_baseline("w8a32", blocks=7)
+        r["value"] = round(r["value"] * 4, 1)
+        r["sample"] = r["sample"].replace("one full 7-block DiT step", "7 of the 28 blocks of a DiT step, scaled x4 to the step")
+        print(json.dumps(r))
