@@ -55,6 +55,12 @@ class AttnDesc(ctypes.Structure):
     ]
 
 
+class ConvDesc(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int), ("H", ctypes.c_int), ("W", ctypes.c_int), ("cin", ctypes.c_int),
+                ("cout", ctypes.c_int), ("up", ctypes.c_int), ("x", _vp), ("w", _vp), ("bias", _vp), ("out", _vp),
+                ("resid", ctypes.c_int), ("precision", ctypes.c_int)]
+
+
 class Weight(ctypes.Structure):
     _fields_ = [("kind", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int), ("w", _vp), ("scale", _vp),
                 ("srel", _vp), ("codebook", _vp), ("bias", _vp)]
@@ -123,6 +129,8 @@ def lib():
         L.anima_attention_noalloc.argtypes = [_vp, ctypes.POINTER(AttnDesc)]
         L.anima_attention_noalloc_scratch_bytes.argtypes = []
         L.anima_attention_noalloc_scratch_bytes.restype = _i64
+        L.anima_conv3x3.argtypes = [_vp, ctypes.POINTER(ConvDesc)]
+        L.anima_channel_norm.argtypes = [_vp, _vp, _vp, _vp, _i64, ctypes.c_int, ctypes.c_int]
         L.anima_fill_random.argtypes = [_vp, _vp, _i64, ctypes.c_int, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]
         L.anima_graph_begin.argtypes = [_vp]
         L.anima_graph_end.argtypes = [_vp, P(_vp)]
@@ -297,6 +305,15 @@ class Context:
     def fill_random(self, dst, n, kind, seed, lo, hi):
         """anima_fill_random: the seeded synthetic fill (kind "u8" / "i8n" / "f32" / "bf16" / "f32n")."""
         return self._check(lib().anima_fill_random(self.h, _ptr(dst), n, self.FILL[kind], seed, lo, hi))
+
+    def conv3x3(self, x, w, out, *, B, H, W, cin, cout, up=False, bias=None, resid=False, precision=PREC_FP32):
+        """anima_conv3x3 (output H x W per image; the input is half that with up)."""
+        d = ConvDesc(B=B, H=H, W=W, cin=cin, cout=cout, up=int(up), x=_ptr(x), w=_ptr(w), bias=_ptr(bias),
+                     out=_ptr(out), resid=int(resid), precision=precision)
+        return self._check(lib().anima_conv3x3(self.h, ctypes.byref(d)))
+
+    def channel_norm(self, x, gamma, y, rows, cols, silu=False):
+        return self._check(lib().anima_channel_norm(self.h, _ptr(x), _ptr(gamma), _ptr(y), rows, cols, int(silu)))
 
     def hadamard(self, x, y, n):
         return self._check(lib().anima_hadamard(self.h, _ptr(x), _ptr(y), n))

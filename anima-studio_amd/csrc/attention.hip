@@ -1140,6 +1140,18 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) { return attention_
 // context's workspace.
 int attention_launch_ws(anima_ctx* c, const anima_attn_desc* d, void* scratch) {
   if (d->D == 64) return attention_d64(c, d);
+  if (d->D != HD) {  // the chunked path (app/gpu/ops.js:177-207)
+    if (scratch) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention_noalloc: head dim %d", d->D);
+    int rc = attention_chunked_check(c, d);
+    if (rc) return rc;
+    int kvl[MAXB];
+    if (d->B > MAXB) return fail(c, ANIMA_E_ARG, "anima_attention: B=%d above %d", d->B, MAXB);
+    for (int b = 0; b < d->B; b++) {
+      kvl[b] = d->kv_len ? d->kv_len[b] : d->Lk;
+      if (kvl[b] < 1 || kvl[b] > d->Lk) return fail(c, ANIMA_E_ARG, "anima_attention: kv_len[%d]=%d outside [1, Lk=%d]", b, kvl[b], d->Lk);
+    }
+    return attention_chunked_launch(c, d, kvl);
+  }
   int kv_len[MAXB];
   int rc = attention_check(c, d, kv_len);
   if (rc) return rc;

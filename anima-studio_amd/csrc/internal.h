@@ -92,6 +92,12 @@ int attention_noalloc_launch(anima_ctx* c, const anima_attn_desc* d);
 int attention_prepare_kv_launch(anima_ctx* c, const anima_attn_desc* d, void* dst);
 int64_t attention_kv_bytes(int B, int Hkv, int Lk, int precision);
 
+// ---- kernel launchers (tgemm.hip)
+int conv3x3_launch(anima_ctx* c, const anima_conv_desc* d);
+int channel_norm_launch(anima_ctx* c, const float* x, const float* gamma, float* y, int64_t rows, int cols, int silu);
+int attention_chunked_check(anima_ctx* c, const anima_attn_desc* d);
+int attention_chunked_launch(anima_ctx* c, const anima_attn_desc* d, const int* kv_len);
+
 // ---- kernel launchers (rowops.hip)
 int qk_norm_rope_launch(anima_ctx* c, float* qkv, int64_t L, int H, int D, int64_t ld,
                         const float* qn, const float* kn, const float* cs, int64_t sin_off,

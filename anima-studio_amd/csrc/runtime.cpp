@@ -425,6 +425,16 @@ int anima_attention(anima_ctx* c, const anima_attn_desc* d) {
   return attention_launch(c, d);
 }
 
+int anima_conv3x3(anima_ctx* c, const anima_conv_desc* d) {
+  CHECK_CTX(c);
+  return conv3x3_launch(c, d);
+}
+
+int anima_channel_norm(anima_ctx* c, const float* x, const float* gamma, float* y, int64_t rows, int cols, int silu) {
+  CHECK_CTX(c);
+  return channel_norm_launch(c, x, gamma, y, rows, cols, silu);
+}
+
 int anima_attention_noalloc(anima_ctx* c, const anima_attn_desc* d) {
   CHECK_CTX(c);
   return attention_noalloc_launch(c, d);

@@ -674,6 +674,40 @@ static napi_value js_sampler_step(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* conv3x3(ctx, desc) -- desc mirrors anima_conv_desc */
+static napi_value js_conv3x3(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  napi_value o = argv[1];
+  anima_conv_desc d;
+  memset(&d, 0, sizeof d);
+  d.B = (int)pnum(env, o, "B");
+  d.H = (int)pnum(env, o, "H");
+  d.W = (int)pnum(env, o, "W");
+  d.cin = (int)pnum(env, o, "cin");
+  d.cout = (int)pnum(env, o, "cout");
+  d.up = (int)pnum(env, o, "up");
+  d.x = (const float*)pptr(env, o, "x");
+  d.w = (const uint16_t*)pptr(env, o, "w");
+  d.bias = (const float*)pptr(env, o, "bias");
+  d.out = (float*)pptr(env, o, "out");
+  d.resid = (int)pnum(env, o, "resid");
+  d.precision = (int)pnum(env, o, "precision");
+  CHECK_RC(env, c, anima_conv3x3(c, &d));
+  return NULL;
+}
+
+/* channelNorm(ctx, x, gamma, y, rows, cols, silu) */
+static napi_value js_channel_norm(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  get_args(env, info, 7, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_channel_norm(c, (const float*)ptr(env, a[1]), (const float*)ptr(env, a[2]), (float*)ptr(env, a[3]),
+                                      i64(env, a[4]), (int)num(env, a[5]), (int)num(env, a[6])));
+  return NULL;
+}
+
 /* lastError(ctx | null) */
 static napi_value js_last_error(napi_env env, napi_callback_info info) {
   napi_value a[1];
@@ -732,7 +766,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       FN("elementwise", js_elementwise), FN("zero", js_zero), FN("patchify", js_patchify), FN("linearGroupedBf16", js_linear_grouped_bf16), FN("unpatchify", js_unpatchify), FN("fillRandom", js_fill_random),
       FN("linear", js_linear), FN("samplerStep", js_sampler_step), FN("attentionKvBytes", js_attention_kv_bytes), FN("split3", js_split3), FN("lastError", js_last_error),
       FN("graphBegin", js_graph_begin), FN("graphEnd", js_graph_end), FN("graphLaunch", js_graph_launch),
-      FN("graphDestroy", js_graph_destroy),
+      FN("graphDestroy", js_graph_destroy), FN("conv3x3", js_conv3x3), FN("channelNorm", js_channel_norm),
   };
 #undef FN
   if (napi_define_properties(env, exports, sizeof desc / sizeof desc[0], desc) != napi_ok) return NULL;

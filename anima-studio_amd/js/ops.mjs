@@ -262,13 +262,32 @@ function attnDesc(a, B, H, D, o, extra) {
   }, extra);
 }
 
-// The VAE's ops (conv3x3, channelNorm: app/gpu/ops.js:97-109) are not built yet.
-export function conv3x3() {
-  throw new Error("conv3x3 (VAE) is not part of this build");
+// 3x3 conv (pad 1) on an NHWC image [h*w, cin] -> [H*W, W.N] (ops.js:95-105); up = true reads the
+// input through a 2x nearest upsample (the output is then 2h x 2w); `into`: out += conv (the residual
+// of conv3x3Into).  W: bf16 OHWI weight [N, 9*cin] (+ W.bias).  opts.precision: "fp32" (default, the
+// reference's arithmetic: activations enter the bf16 matrix cores as two bf16 terms) or "bf16";
+// opts.B: images stacked along the rows.
+export function conv3x3(gpu, x, W, h, w, up, into, opts) {
+  const o = opts || {};
+  if (W.kind !== "bf16") throw new Error(`conv3x3: ${W.name || "weight"} is ${W.kind}, expected bf16 (OHWI)`);
+  const B = o.B || 1;
+  const H = up ? 2 * h : h, Wd = up ? 2 * w : w;
+  const cin = W.K / 9;
+  const out = into || gpu.empty([B * H * Wd, W.N]);
+  native.conv3x3(gpu.ctx, { B, H, W: Wd, cin, cout: W.N, up: up ? 1 : 0, x: x.buf, w: ptr(W.buf), bias: ptr(W.bias),
+    out: out.buf, resid: into ? 1 : 0, precision: precisionId(o) });
+  return out;
 }
-export function conv3x3Into() {
-  throw new Error("conv3x3 (VAE) is not part of this build");
+
+// out += conv3x3(x) (the residual connection fused into the epilogue; ops.js:106-109)
+export function conv3x3Into(gpu, x, W, h, w, out, opts) {
+  return conv3x3(gpu, x, W, h, w, false, out, opts);
 }
-export function channelNorm() {
-  throw new Error("channelNorm (VAE) is not part of this build");
+
+// Wan VAE RMS_norm over channels (+ SiLU) (ops.js:119-126).
+export function channelNorm(gpu, x, gamma, cols, silu) {
+  const rows = x.size / cols;
+  const y = gpu.empty(x.shape);
+  native.channelNorm(gpu.ctx, x.buf, ptr(gamma), y.buf, rows, cols, silu ? 1 : 0);
+  return y;
 }

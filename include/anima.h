@@ -101,8 +101,10 @@ int anima_graph_destroy(anima_ctx* ctx, anima_graph* graph);
 #define ANIMA_PREC_FP32 1 /* fp32 MFMA (tolerance variant) */
 
 typedef struct {
-  int B, Lq, Lk, H, D; /* D == 128, or 64 (the LLM adapter's heads, zero-padded to 128 inside the
-                        * call: no fused norm / RoPE / prepared K/V with D == 64) */
+  int B, Lq, Lk, H, D; /* D == 128 (flash kernels); D == 64 (the LLM adapter's heads, zero-padded to
+                        * 128 inside the call); other D % 4 == 0 (the VAE's 384) on the chunked path
+                        * of app/gpu/ops.js:177-207.  Fused norm / RoPE, prepared K/V and the causal
+                        * mask need D == 128. */
   int group;           /* q heads per kv head (1 = MHA); 0 is read as 1 */
   const float* q;
   int64_t ldq, q_off, q_bstride;
@@ -277,6 +279,31 @@ int anima_sampler_step(anima_ctx* ctx, const anima_sampler_desc* d);
 #define ANIMA_FILL_BF16 3
 #define ANIMA_FILL_F32N 4
 int anima_fill_random(anima_ctx* ctx, void* dst, int64_t n, int kind, uint64_t seed, float lo, float hi);
+
+/* ---------------------------------------------------------------- VAE decoder ops */
+
+/* ops.conv3x3 / conv3x3Into (app/gpu/ops.js:95-109; the implicit-GEMM "conv3" loader of
+ * app/gpu/gemm.js:56-80): out[b][y][x][n] (+)= bias[n] + sum_{tap, ci} w[n][tap][ci] * in(b, y + ty - 1,
+ * x + tx - 1, ci), zero padding, NHWC fp32 activations, bf16 OHWI weights [cout][3][3][cin] (the
+ * checkpoint layout of tools/build_assets.py:160-180).  up = 1 reads the input through a 2x nearest
+ * upsample: in(b, y, x) = x_in[b][y/2][x/2], the input being H/2 x W/2.  precision: ANIMA_PREC_FP32
+ * keeps fp32-level accuracy (activations as two bf16 terms on the bf16 matrix cores), ANIMA_PREC_BF16
+ * rounds them to bf16.  cin % 16 == 0; x and w 16-byte aligned. */
+typedef struct {
+  int B, H, W;       /* images and output size */
+  int cin, cout;
+  int up;
+  const float* x;    /* [B][H or H/2][W or W/2][cin] */
+  const uint16_t* w; /* [cout][9 * cin] */
+  const float* bias; /* [cout] or NULL */
+  float* out;        /* [B][H][W][cout] */
+  int resid;         /* 1: out += conv (conv3x3Into) */
+  int precision;
+} anima_conv_desc;
+int anima_conv3x3(anima_ctx* ctx, const anima_conv_desc* desc);
+/* ops.channelNorm (app/gpu/ops.js:119-126; kernels.js:62-89 mode 1, the Wan VAE RMS_norm):
+ * y = x * sqrt(cols) / max(||x||, 1e-12) * gamma per row, then SiLU when silu != 0.  y may equal x. */
+int anima_channel_norm(anima_ctx* ctx, const float* x, const float* gamma, float* y, int64_t rows, int cols, int silu);
 
 /* ---------------------------------------------------------------- linears */
 

@@ -59,6 +59,7 @@ def lib():
         L.orc_gemm_i8.argtypes = [_i8p, _i8p, _i64, ctypes.c_int, ctypes.c_int, _i32p]
         L.orc_fp8e4m3.argtypes = [ctypes.c_uint8]
         L.orc_fill_random.argtypes = [ctypes.c_void_p, _i64, ctypes.c_int, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]
+        L.orc_channel_norm.argtypes = [_f32p, _f32p, _f32p, _i64, ctypes.c_int, ctypes.c_int]
         L.orc_splitmix64_next.argtypes = [ctypes.c_uint64]
         L.orc_splitmix64_next.restype = ctypes.c_uint64
         L.orc_fp8e4m3.restype = ctypes.c_float
@@ -256,3 +257,12 @@ def fill_random(n, kind, seed, lo, hi):
 
 def splitmix64_next(state):
     return int(lib().orc_splitmix64_next(state))
+
+
+def channel_norm(x, gamma, cols, silu=False):
+    """Wan VAE channel norm (app/gpu/kernels.js:62-89 mode 1) over rows of `cols`."""
+    x = _c(x, np.float32)
+    g = _c(gamma, np.float32)
+    y = np.empty_like(x)
+    lib().orc_channel_norm(_p(x, _f32p), _p(g, _f32p), _p(y, _f32p), x.size // cols, cols, int(silu))
+    return y

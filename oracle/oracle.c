@@ -526,3 +526,26 @@ void orc_fill_random(void* dst, int64_t n, int kind, uint64_t seed, float lo, fl
     }
   }
 }
+
+/* ---------------------------------------------------------------- VAE */
+void orc_channel_norm(const float* X, const float* G, float* Y, int64_t rows, int cols, int silu) {
+  /* app/gpu/kernels.js:65-89 mode 1: 64 threads stride the row, then the 32 .. 1 tree */
+#pragma omp parallel for schedule(static)
+  for (int64_t row = 0; row < rows; row++) {
+    const float* x = X + row * cols;
+    float red[64];
+    for (int t = 0; t < 64; t++) {
+      float ss = 0.0f;
+      for (int c = t; c < cols; c += 64) ss += x[c] * x[c];
+      red[t] = ss;
+    }
+    for (int s = 32; s > 0; s >>= 1)
+      for (int t = 0; t < s; t++) red[t] = red[t] + red[t + s];
+    const float r = sqrtf((float)cols) / fmaxf(sqrtf(red[0]), 1e-12f);
+    for (int c = 0; c < cols; c++) {
+      float y = x[c] * r * G[c];
+      if (silu) y = y / (1.0f + expf(-y));
+      Y[row * cols + c] = y;
+    }
+  }
+}

@@ -102,6 +102,9 @@ float orc_silu(float x);
  * counterpart): element i draws h = splitmix64(seed * 0xD1B54A32D192ED03 + i).  kind: 0 U8,
  * 1 I8N, 2 F32, 3 BF16 (bits), 4 F32N. */
 void orc_fill_random(void* dst, int64_t n, int kind, uint64_t seed, float lo, float hi);
+/* Wan VAE channel norm (app/gpu/kernels.js:62-89 mode 1): y = x * sqrt(cols) / max(||x||, 1e-12) * g,
+ * then SiLU when silu != 0, in the shader's reduction order. */
+void orc_channel_norm(const float* X, const float* G, float* Y, int64_t rows, int cols, int silu);
 /* splitmix64's output for one state (Vigna's reference generator), for its known-answer check. */
 uint64_t orc_splitmix64_next(uint64_t state);
 

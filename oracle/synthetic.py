@@ -115,3 +115,55 @@ def dit_weights(seed, mode="w4a8", blocks=28):
     W["final_layer.adaln_modulation.2.weight"] = src.bf16("final_layer.adaln_modulation.2", 2 * D, R, 0.1)
     W["final_layer.linear.weight"] = src.bf16("final_layer.linear", 64, D)
     return W
+
+
+# Wan 2.1 VAE decoder stages after the middle blocks (js/vae.mjs VAE_UPSAMPLES): residual blocks
+# (cin, cout) or resamples (2x upsample + conv3x3 dim -> dim / 2)
+VAE_UPSAMPLES = [(384, 384), (384, 384), (384, 384), ("up", 384),
+                 (192, 384), (384, 384), (384, 384), ("up", 384),
+                 (192, 192), (192, 192), (192, 192), ("up", 192),
+                 (96, 96), (96, 96), (96, 96)]
+
+
+def _bf16(u16):
+    return (np.asarray(u16, np.uint32) << 16).view(np.float32)
+
+
+def vae_weights(seed):
+    """The weights of VAEDecoder.synthetic(gpu, new SyntheticWeights(gpu, seed)) (js/vae.mjs): a dict
+    name -> float32 array in the checkpoint's names (OHWI convolution weights flattened to [N, 9*cin],
+    1x1 convolutions [N, cin])."""
+    src = Source(seed)
+    W = {}
+
+    def lin(name, N, K, gain):
+        W[name + ".weight"] = _bf16(src.bf16(name, N, K, gain))
+        W[name + ".bias"] = src.fill(N, "f32", name + ".bias", -0.05, 0.05)
+
+    def gamma(name, n):
+        W[name] = src.fill(n, "f32", name, 0.9, 1.1)
+
+    def res(p, cin, cout):
+        gamma(p + ".residual.0.gamma", cin)
+        lin(p + ".residual.2", cout, 9 * cin, 1.0)
+        gamma(p + ".residual.3.gamma", cout)
+        lin(p + ".residual.6", cout, 9 * cout, 0.5)
+        if cin != cout:
+            lin(p + ".shortcut", cout, cin, 1.0)
+
+    lin("conv2", 16, 16, 1.0)
+    lin("decoder.conv1", 384, 9 * 16, 1.0)
+    res("decoder.middle.0", 384, 384)
+    gamma("decoder.middle.1.norm.gamma", 384)
+    lin("decoder.middle.1.to_qkv", 3 * 384, 384, 1.0)
+    lin("decoder.middle.1.proj", 384, 384, 0.5)
+    res("decoder.middle.2", 384, 384)
+    for i, s in enumerate(VAE_UPSAMPLES):
+        p = f"decoder.upsamples.{i}"
+        if s[0] == "up":
+            lin(p + ".resample.1", s[1] // 2, 9 * s[1], 1.0)
+        else:
+            res(p, s[0], s[1])
+    gamma("decoder.head.0.gamma", 96)
+    lin("decoder.head.2", 3, 9 * 96, 1.0)
+    return W

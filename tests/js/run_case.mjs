@@ -28,6 +28,7 @@
 //              residual stream after block 0, for the oracle's restatement of the same weights
 //   fullstep   the full-size CFG step of a synthetic DiT: eager, with equal contexts, and replayed
 //              from a HIP graph
+//   vae        VAEDecoder.decode of a seeded synthetic decoder: raw output, RGBA bytes, stages
 
 import fs from "fs";
 import { GPU, native } from "../../anima-studio_amd/js/gpu.mjs";
@@ -40,6 +41,7 @@ import { linearRegistry, loadLora, attachLoras, destroyLora, rotatedA } from "..
 import { LatentPipeline } from "../../anima-studio_amd/js/pipeline.mjs";
 import { TorchGenerator } from "../../anima-studio_amd/js/rng.mjs";
 import { Qwen3 } from "../../anima-studio_amd/js/qwen3.mjs";
+import { VAEDecoder } from "../../anima-studio_amd/js/vae.mjs";
 
 const ARR = { f32: Float32Array, i8: Int8Array, u8: Uint8Array, u16: Uint16Array, i32: Int32Array };
 
@@ -229,6 +231,15 @@ async function main() {
     const peak = gpu.pool.peak;
     console.log(JSON.stringify({ leak: { n: c.n, bytes, finalized: native.finalized() - f0, peak,
       released_twice_ok: kept.buf === 0 } }));
+  } else if (c.case === "vae") {
+    // the VAE decoder on seeded synthetic weights: raw output, RGBA image, progress stages
+    const vae = VAEDecoder.synthetic(gpu, new SyntheticWeights(gpu, c.seed));
+    vae.precision = c.precision || "fp32";
+    const stages = [];
+    const r = await vae.decode(load(c.latent), c.h, c.w, (f) => stages.push(f));
+    save(c.out + ".raw", r.raw);
+    save(c.out + ".img", r.data);
+    console.log(JSON.stringify({ vae: { width: r.width, height: r.height, stages } }));
   } else if (c.case === "synthdit") {
     // a seeded synthetic DiT (the weights the oracle restates by name) on given latents / contexts
     const dit = AnimaDiT.synthetic(gpu, new SyntheticWeights(gpu, c.seed, { mode: c.mode, blocks: c.blocks }));

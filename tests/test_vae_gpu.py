@@ -1,0 +1,164 @@
+"""GPU parity of the VAE decoder's ops and of the whole decoder (the last rank-4 "next" component):
+
+  * channel norm (app/gpu/kernels.js:62-89 mode 1) bit-exact against the C oracle, and within 1e-6
+    with the SiLU (exp rounding);
+  * conv3x3 (implicit GEMM on the bf16 matrix cores, fused 2x upsample, bias, residual) against the
+    float64 convolution (oracle/vae_ref.py, pinned by a direct loop): fp32 precision (activations as
+    two bf16 terms) rel L2 <= 3e-5, bf16 <= 1e-2;
+  * attention with head dim 384 on the chunked path (app/gpu/ops.js:177-207) against float64,
+    including several score chunks, B = 2 with valid key lengths and GQA heads;
+  * VAEDecoder.decode through the JS host against the float64 decoder on the same seeded weights:
+    fp32 precision rel L2 <= 1e-3 with RGBA bytes within 1, bf16 precision reported and <= 5e-2.
+"""
+
+import json
+import math
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from helpers import RUN_CASE, amd, report
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def bf16_bits(a):
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def from_bits(u16):
+    return (np.asarray(u16, np.uint32) << 16).view(np.float32)
+
+
+@pytest.mark.parametrize("cols", [16, 96, 192, 384])
+def test_channel_norm_matches_oracle(cols):
+    m = amd()
+    rng = np.random.default_rng(cols)
+    x = (rng.standard_normal((1000, cols)) * rng.uniform(0.1, 10, (1000, 1))).astype(np.float32)
+    x[7] = 0.0
+    g = rng.uniform(0.9, 1.1, cols).astype(np.float32)
+    with m.Context() as ctx:
+        dx, dg, dy = ctx.upload(x), ctx.upload(g), ctx.empty(x.shape)
+        for silu in (False, True):
+            print(f"[case] channel_norm cols={cols} silu={silu}", flush=True)
+            ctx.channel_norm(dx, dg, dy, 1000, cols, silu)
+            got, ref = dy.numpy(), orc.channel_norm(x, g, cols, silu)
+            if silu:
+                assert report(f"channel_norm+silu cols={cols}", got, ref)[1] <= 1e-6 * np.abs(ref).max()
+            else:
+                assert np.array_equal(got, ref)
+        for b in (dx, dg, dy):
+            b.release()
+
+
+CONV_CASES = [  # B, H, W (output), cin, cout, up, resid
+    (1, 16, 16, 16, 384, False, False),
+    (2, 13, 11, 96, 3, False, True),
+    (1, 32, 24, 192, 96, True, False),
+    (1, 20, 20, 384, 192, True, True),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_conv3x3_matches_float64(case, precision):
+    from oracle import vae_ref
+
+    m = amd()
+    B, H, W, cin, cout, up, resid = case
+    rng = np.random.default_rng(hash(case) % 1000)
+    Hi, Wi = (H // 2, W // 2) if up else (H, W)
+    x = rng.standard_normal((B, Hi, Wi, cin)).astype(np.float32)
+    w = from_bits(bf16_bits(rng.uniform(-1, 1, (cout, 9 * cin)) * math.sqrt(3.0 / (9 * cin))))
+    bias = rng.uniform(-0.1, 0.1, cout).astype(np.float32)
+    c0 = rng.standard_normal((B, H, W, cout)).astype(np.float32)
+    prec = m.PREC_FP32 if precision == "fp32" else m.PREC_BF16
+    print(f"[case] conv3x3 {case} {precision}", flush=True)
+    with m.Context() as ctx:
+        dx, dw, db = ctx.upload(x), ctx.upload(bf16_bits(w)), ctx.upload(bias)
+        do = ctx.upload(c0) if resid else ctx.empty((B, H, W, cout))
+        ctx.conv3x3(dx, dw, do, B=B, H=H, W=W, cin=cin, cout=cout, up=up, bias=db, resid=resid, precision=prec)
+        got = do.numpy()
+        for b in (dx, dw, db, do):
+            b.release()
+    ref = vae_ref.conv3x3(torch.tensor(x, dtype=torch.float64), w, bias, up=up).numpy()
+    if resid:
+        ref = ref + c0
+    r, _ = report(f"conv3x3 {case} {precision} vs float64", got, ref)
+    assert r <= (3e-5 if precision == "fp32" else 1e-2)
+
+
+ATTN_CASES = [  # B, Lq, Lk, H, group, D, kv_len
+    (1, 300, 300, 1, 1, 384, None),
+    (2, 256, 200, 2, 2, 384, [200, 77]),
+    (1, 2304, 16384, 1, 1, 384, None),  # three score chunks of 1024 / 1024 / 256 rows
+    (1, 96, 150, 3, 1, 96, None),
+]
+
+
+@pytest.mark.parametrize("case", ATTN_CASES)
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_chunked_attention_matches_float64(case, precision):
+    m = amd()
+    B, Lq, Lk, H, group, D, kv_len = case
+    Hk = H // group
+    rng = np.random.default_rng(Lq + Lk)
+    q = rng.standard_normal((B, Lq, H * D)).astype(np.float32)
+    k = rng.standard_normal((B, Lk, Hk * D)).astype(np.float32)
+    v = rng.standard_normal((B, Lk, Hk * D)).astype(np.float32)
+    prec = m.PREC_FP32 if precision == "fp32" else m.PREC_BF16
+    print(f"[case] chunked attention {case} {precision}", flush=True)
+    with m.Context() as ctx:
+        dq, dk, dv, do = ctx.upload(q), ctx.upload(k), ctx.upload(v), ctx.empty((B, Lq, H * D))
+        ctx.attention(q=dq, k=dk, v=dv, o=do, B=B, Lq=Lq, Lk=Lk, H=H, D=D, ldq=H * D, ldk=Hk * D, ldv=Hk * D,
+                      group=group, kv_len=kv_len, precision=prec)
+        got = do.numpy()
+        for b in (dq, dk, dv, do):
+            b.release()
+    for b in range(B):
+        n = kv_len[b] if kv_len else Lk
+        for h in range(H):
+            hk = h // group
+            qh = torch.tensor(q[b, :, h * D:(h + 1) * D], dtype=torch.float64)
+            kh = torch.tensor(k[b, :n, hk * D:(hk + 1) * D], dtype=torch.float64)
+            vh = torch.tensor(v[b, :n, hk * D:(hk + 1) * D], dtype=torch.float64)
+            ref = (torch.softmax(qh @ kh.T / math.sqrt(D), -1) @ vh).numpy()
+            r, _ = report(f"chunked attention b={b} h={h} {precision} vs float64", got[b, :, h * D:(h + 1) * D], ref)
+            assert r <= (2e-5 if precision == "fp32" else 1e-2)
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_vae_decode_through_js_matches_float64(tmp_path, precision):
+    from oracle import synthetic, vae_ref
+
+    h = w = 16
+    seed = 21
+    lat = orc.randn(31, 16 * h * w).reshape(16, h, w)
+    lp = str(tmp_path / "lat.bin")
+    lat.tofile(lp)
+    out = str(tmp_path / "vae")
+    spec = {"case": "vae", "seed": seed, "latent": lp, "h": h, "w": w, "precision": precision, "out": out}
+    (tmp_path / "case.json").write_text(json.dumps(spec))
+    print(f"[case] js vae decode 16x16 -> 128x128 {precision}", flush=True)
+    r = subprocess.run(["node", RUN_CASE, str(tmp_path / "case.json")], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-3000:]
+    info = json.loads(next(ln for ln in r.stdout.splitlines() if '"vae"' in ln))["vae"]
+    assert info["width"] == 8 * w and info["height"] == 8 * h and len(info["stages"]) == 16
+    raw = np.fromfile(out + ".raw", np.float32).reshape(8 * h, 8 * w, 3)
+    img = np.fromfile(out + ".img", np.uint8).reshape(8 * h, 8 * w, 4)
+    ref, ref_img = vae_ref.decode(synthetic.vae_weights(seed), lat, synthetic.VAE_UPSAMPLES)
+    rr, _ = report(f"vae decode ({precision}) vs float64", raw, ref)
+    d = np.abs(img.astype(int) - ref_img.astype(int))
+    print(f"vae image bytes: max |d| {d.max()}, {np.count_nonzero(d)} of {d.size} differ", flush=True)
+    assert np.all(np.isfinite(raw))
+    if precision == "fp32":
+        assert rr <= 1e-3 and d.max() <= 1
+    else:
+        assert rr <= 5e-2
