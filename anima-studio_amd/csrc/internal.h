@@ -95,6 +95,7 @@ int64_t attention_kv_bytes(int B, int Hkv, int Lk, int precision);
 // ---- kernel launchers (tgemm.hip)
 int conv3x3_launch(anima_ctx* c, const anima_conv_desc* d);
 int channel_norm_launch(anima_ctx* c, const float* x, const float* gamma, float* y, int64_t rows, int cols, int silu);
+int to_rgba_launch(anima_ctx* c, const float* x, int64_t n, uint8_t* out);
 int attention_chunked_check(anima_ctx* c, const anima_attn_desc* d);
 int attention_chunked_launch(anima_ctx* c, const anima_attn_desc* d, const int* kv_len);
 

@@ -435,6 +435,11 @@ int anima_channel_norm(anima_ctx* c, const float* x, const float* gamma, float* 
   return channel_norm_launch(c, x, gamma, y, rows, cols, silu);
 }
 
+int anima_to_rgba(anima_ctx* c, const float* x, int64_t n, uint8_t* out) {
+  CHECK_CTX(c);
+  return to_rgba_launch(c, x, n, out);
+}
+
 int anima_attention_noalloc(anima_ctx* c, const anima_attn_desc* d) {
   CHECK_CTX(c);
   return attention_noalloc_launch(c, d);

@@ -49,24 +49,40 @@ struct TGemmArgs {
   int M, N, K;
 };
 
+// The output pixel of a conv A row, decomposed once per thread: image base pointer and (oy, ox).
+struct ConvRow {
+  const float* img;  // first element of this row's image
+  int oy, ox;
+};
+
+__device__ __forceinline__ ConvRow conv_row(const TGemmArgs& p, const float* a, int m) {
+  ConvRow r;
+  const int hw = p.H * p.W;
+  const int img = m / hw, q = m - img * hw;
+  r.oy = q / p.W;
+  r.ox = q - r.oy * p.W;
+  const int Hin = p.up ? p.H >> 1 : p.H, Win = p.up ? p.W >> 1 : p.W;
+  r.img = a + (int64_t)img * Hin * Win * p.cin;
+  return r;
+}
+
 // 16 consecutive k of A row m starting at k (k % 16 == 0), fp32; zeros outside the matrix / image.
 template <int AM>
-__device__ __forceinline__ void tg_load_a(const TGemmArgs& p, const float* a, int m, int k, float (&v)[16]) {
+__device__ __forceinline__ void tg_load_a(const TGemmArgs& p, const float* a, const ConvRow& cr, int m, int k,
+                                          float (&v)[16]) {
   bool ok = m < p.M && k < p.K;
   const float* src = nullptr;
   if (ok) {
     if constexpr (AM == TG_A_ROWS) {
       src = a + (int64_t)m * p.lda + k;
     } else {
-      const int tap = k / p.cin, ci = k - tap * p.cin;
-      const int hw = p.H * p.W;
-      const int img = m / hw, r = m - img * hw;
-      const int oy = r / p.W, ox = r - oy * p.W;
-      const int iy = oy + tap / 3 - 1, ix = ox + tap % 3 - 1;
+      const int tap = k / p.cin, ci = k - tap * p.cin;  // cin is uniform: a scalar division
+      const int ty = tap / 3, tx = tap - 3 * ty;
+      const int iy = cr.oy + ty - 1, ix = cr.ox + tx - 1;
       ok = iy >= 0 && ix >= 0 && iy < p.H && ix < p.W;
-      const int Hin = p.up ? p.H >> 1 : p.H, Win = p.up ? p.W >> 1 : p.W;
+      const int Win = p.up ? p.W >> 1 : p.W;
       const int sy = p.up ? iy >> 1 : iy, sx = p.up ? ix >> 1 : ix;
-      src = a + (((int64_t)img * Hin + sy) * Win + sx) * p.cin + ci;
+      src = cr.img + ((int64_t)sy * Win + sx) * p.cin + ci;
     }
   }
   if (ok && (AM == TG_A_CONV || k + 16 <= p.K)) {  // conv: cin % 16 == 0, a run never crosses a tap
@@ -109,11 +125,15 @@ __global__ __launch_bounds__(256) void tgemm_kernel(TGemmArgs p) {
   const int am = m0 + lr, bn = n0 + lr;
   const bool bok = bn < p.N;
 
+  ConvRow cr{};
+  if constexpr (AM == TG_A_CONV) {
+    if (am < p.M) cr = conv_row(p, a, am);
+  }
   float av[16];
   uint4 bw[2];   // bf16 B: 16 values
   float bv[16];  // fp32 B
   auto load = [&](int k0) {
-    tg_load_a<AM>(p, a, am, k0 + lk, av);
+    tg_load_a<AM>(p, a, cr, am, k0 + lk, av);
     const int k = k0 + lk;
     if constexpr (BMODE == TG_B_W16) {
       const uint16_t* src = (const uint16_t*)bb + (int64_t)bn * p.ldb + k;
@@ -325,6 +345,40 @@ int channel_norm_launch(anima_ctx* c, const float* x, const float* gamma, float*
   return lc.end();
 }
 
+// ---- the decoder's output image (app/models/vae.js:104-112): RGBA bytes of [n][3] values,
+// channel = round((clamp(v, -1, 1) + 1) / 2 * 255) in double precision with JS Math.round
+// (nearest, ties toward +inf; t - floor(t) is exact in double), NaN -> 0 as the reference's
+// Uint8ClampedArray store makes it, alpha 255.
+__global__ __launch_bounds__(256) void rgba_kernel(const float* x, int64_t n, uint8_t* out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  uchar4 o;
+  unsigned char c[3];
+#pragma unroll
+  for (int j = 0; j < 3; j++) {
+    const float xv = x[3 * i + j];
+    const double v = (fmin(1.0, fmax(-1.0, (double)xv)) + 1.0) / 2.0;
+    const double t = v * 255.0;
+    double r = floor(t);
+    if (t - r >= 0.5) r += 1.0;
+    c[j] = xv != xv ? 0 : (unsigned char)r;
+  }
+  o.x = c[0];
+  o.y = c[1];
+  o.z = c[2];
+  o.w = 255;
+  ((uchar4*)out)[i] = o;
+}
+
+int to_rgba_launch(anima_ctx* c, const float* x, int64_t n, uint8_t* out) {
+  if (!x || !out || n < 0) return fail(c, ANIMA_E_ARG, "anima_to_rgba: bad arguments");
+  if (((uintptr_t)out & 3) != 0) return fail(c, ANIMA_E_ARG, "anima_to_rgba: out must be 4-byte aligned");
+  if (n == 0) return ANIMA_OK;
+  Launch l(c, "vae.to_rgba", 0.0, (double)n * 16);
+  hipLaunchKernelGGL(rgba_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, c->stream, x, n, out);
+  return l.end();
+}
+
 // ---- attention on the chunked path (head dims other than 64 / 128)
 
 // In place on row r of S (row stride ld), columns [0, cols): e = exp(s * scale - m), m the maximum of
@@ -404,8 +458,9 @@ int attention_chunked_launch(anima_ctx* c, const anima_attn_desc* d, const int* 
   const int D = d->D, Lq = d->Lq, Lk = d->Lk;
   const float scale = d->scale != 0.0f ? d->scale : 1.0f / sqrtf((float)D);
   const bool split = d->precision == ANIMA_PREC_FP32;
-  // score rows per chunk: at most 64 MiB of scores, a multiple of the 128-row tile
-  int64_t rows = std::max<int64_t>(TG_BM, ((int64_t)(64 << 20) / 4 / Lk) / TG_BM * TG_BM);
+  // score rows per chunk: at most 1 GiB of scores (one chunk for the VAE's 16384 tokens at 1024x1024;
+  // the device has 288 GB), a multiple of the 128-row tile
+  int64_t rows = std::max<int64_t>(TG_BM, ((int64_t)(1 << 30) / 4 / Lk) / TG_BM * TG_BM);
   rows = std::min<int64_t>(rows, ((int64_t)Lq + TG_BM - 1) / TG_BM * TG_BM);
   const int64_t ldk4 = ((int64_t)Lk + 3) / 4 * 4;  // row stride of the scores and of V^T (16-byte rows)
   const size_t s_bytes = (size_t)rows * ldk4 * 4, l_bytes = ((size_t)rows * 4 + 255) / 256 * 256,

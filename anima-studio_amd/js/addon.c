@@ -708,6 +708,15 @@ static napi_value js_channel_norm(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* toRgba(ctx, x, n, out) */
+static napi_value js_to_rgba(napi_env env, napi_callback_info info) {
+  napi_value a[4];
+  get_args(env, info, 4, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_to_rgba(c, (const float*)ptr(env, a[1]), i64(env, a[2]), (uint8_t*)ptr(env, a[3])));
+  return NULL;
+}
+
 /* lastError(ctx | null) */
 static napi_value js_last_error(napi_env env, napi_callback_info info) {
   napi_value a[1];
@@ -766,7 +775,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       FN("elementwise", js_elementwise), FN("zero", js_zero), FN("patchify", js_patchify), FN("linearGroupedBf16", js_linear_grouped_bf16), FN("unpatchify", js_unpatchify), FN("fillRandom", js_fill_random),
       FN("linear", js_linear), FN("samplerStep", js_sampler_step), FN("attentionKvBytes", js_attention_kv_bytes), FN("split3", js_split3), FN("lastError", js_last_error),
       FN("graphBegin", js_graph_begin), FN("graphEnd", js_graph_end), FN("graphLaunch", js_graph_launch),
-      FN("graphDestroy", js_graph_destroy), FN("conv3x3", js_conv3x3), FN("channelNorm", js_channel_norm),
+      FN("graphDestroy", js_graph_destroy), FN("conv3x3", js_conv3x3), FN("channelNorm", js_channel_norm), FN("toRgba", js_to_rgba),
   };
 #undef FN
   if (napi_define_properties(env, exports, sizeof desc / sizeof desc[0], desc) != napi_ok) return NULL;

@@ -10,6 +10,7 @@
 //                      the device loop of pipeline.mjs and the reference's host loop)
 //                     [--text-encoder N]  (also time Qwen3.encode of N tokens on a 28-layer synthetic
 //                      text encoder: causal GQA attention, bf16 linears)
+//                     [--vae]  (also time the VAE decode of this size's latent, bf16 and fp32 precision)
 //                     [--graph [--rounds 3]]  (also the forward replayed from a HIP graph recorded
 //                      once, ForwardGraph: graph and eager blocks of --steps steps alternate,
 //                      medians; dit_step_ms stays the eager step, graph_step_ms the replay)
@@ -20,6 +21,7 @@ import { AnimaDiT, ForwardGraph } from "./dit.mjs";
 import { linearRegistry, attachLoras, rotatedA } from "./lora.mjs";
 import { LatentPipeline } from "./pipeline.mjs";
 import { Qwen3 } from "./qwen3.mjs";
+import { VAEDecoder, VAE_UPSAMPLES, VAE_DIM } from "./vae.mjs";
 
 function arg(name, def) {
   const i = process.argv.indexOf("--" + name);
@@ -187,6 +189,25 @@ async function main() {
       note: "Qwen3.encode: embedding gather on the host, 28 layers, causal GQA 16/8 heads, bf16 linears" };
     te.release();
   }
+  if (arg("vae", false)) {
+    // the VAE decoder (Wan 2.1, seeded synthetic weights) on this size's latent, both precisions:
+    // the decode of a [16, h, w] latent to a (8h x 8w) image, host conversions included
+    const vae = VAEDecoder.synthetic(gpu, new SyntheticWeights(gpu, 77));
+    const lat = normals(16 * h * w, 7);
+    out.vae = { latent: [16, h, w], image: [8 * h, 8 * w], gflop: Number((vaeFlops(h, w) / 1e9).toFixed(1)) };
+    for (const prec of ["bf16", "fp32"]) {
+      vae.precision = prec;
+      await vae.decode(lat, h, w);
+      const ts = [];
+      for (let i = 0; i < 3; i++) {
+        gpu.timerStart();
+        await vae.decode(lat, h, w);
+        ts.push(gpu.timerStop());
+      }
+      const ms = ts.sort((a, b) => a - b)[1];
+      out.vae[prec] = { ms: Number(ms.toFixed(2)), "TFLOP/s": Number((vaeFlops(h, w) / ms / 1e9).toFixed(1)) };
+    }
+  }
   console.log(JSON.stringify(out));
   if (fg) fg.release();
   if (latT) latT.release();
@@ -198,6 +219,25 @@ async function main() {
 
 function D_(n, k) {
   return n * k;
+}
+
+// algorithmic FLOPs of one VAE decode of an h x w latent (2*M*N*K per convolution / linear, 4*L*L*D
+// for the attention)
+function vaeFlops(h, w) {
+  const conv = (HW, cin, cout) => 2 * HW * cout * 9 * cin;
+  const res = (HW, cin, cout) => conv(HW, cin, cout) + conv(HW, cout, cout) + (cin !== cout ? 2 * HW * cout * cin : 0);
+  let HW = h * w;
+  let f = 2 * HW * 16 * 16 + conv(HW, 16, VAE_DIM) + 2 * res(HW, VAE_DIM, VAE_DIM);
+  f += 2 * HW * 3 * VAE_DIM * VAE_DIM + 4 * HW * HW * VAE_DIM + 2 * HW * VAE_DIM * VAE_DIM;
+  for (const s of VAE_UPSAMPLES) {
+    if (s.up) {
+      HW *= 4;
+      f += conv(HW, s.up, s.up / 2);
+    } else {
+      f += res(HW, s[0], s[1]);
+    }
+  }
+  return f + conv(HW, 96, 3);
 }
 
 main().catch((e) => {

@@ -1,9 +1,9 @@
 // The sampling half of AnimaPipeline.generate (app/pipeline.js:225-293) on the device: initial
 // noise, the sigma schedule, per step timeCond -> DiT velocities (cond and uncond batched as B=2)
 // -> CFG combine + denoised + sampler update in one kernel (anima_sampler_step), then the latent
-// comes back once at the end.  Text encoding and the VAE are outside this build: the caller
-// passes the conditioning made by AnimaDiT.prepareContext ([positive] or, with CFG,
-// [positive, negative]).
+// comes back once at the end and, when the pipeline holds a VAE decoder (vae.mjs), is decoded to
+// the image as the reference's generate does (pipeline.js:284-292).  The caller passes the
+// conditioning made by AnimaDiT.prepareContext ([positive] or, with CFG, [positive, negative]).
 //
 // Noise is drawn on the host with the reference's torch.randn port (rng.mjs), in the reference's
 // order, and uploaded; drawing it after the step's DiT work is enqueued overlaps it with that work.
@@ -21,9 +21,11 @@ import { loraGeneration } from "./lora.mjs";
 const TIME_CACHE_MAX = 64;
 
 export class LatentPipeline {
-  constructor(gpu, dit) {
+  // opts.vae: a VAEDecoder; generate then also returns the decoded image
+  constructor(gpu, dit, opts) {
     this.gpu = gpu;
     this.dit = dit;
+    this.vae = opts && opts.vae ? opts.vae : null;
     this.timeCache = new Map(); // key -> timeCond result (device tensors), in insertion (LRU) order
     this.stats = { timeCondHits: 0, timeCondMisses: 0 };
   }
@@ -56,13 +58,15 @@ export class LatentPipeline {
   }
 
   // opts: { cond, cfg = 1, width, height, steps, sampler, seed = 0, shift = 3, scheduler = "simple",
-  //         onStep(i, readDenoised), onProgress({ phase, step, steps, frac }), signal, graph = false }.
+  //         onStep(i, readDenoised), onProgress({ phase, step, steps, frac }), signal, graph = false,
+  //         decode = true (with a VAE) }.
   //         cond.B must be 2 when cfg != 1 (positive, negative), else 1.
   // Progress and cancellation follow app/pipeline.js:226-256: onProgress after every DiT block
   // (after every step when the forward is a graph replay), the device queue drained every 7 blocks
   // so that both stay responsive, and `signal.aborted` checked at the same points, throwing an
   // Error named "AbortError"; the pool is trimmed on the way out, cancelled or not.
-  // Returns { latent: Float32Array [16, h, w], sigmas, timings }.
+  // Returns { latent: Float32Array [16, h, w], image ({ data: RGBA bytes, width, height } or null),
+  // sigmas, timings }.
   async generate(opts) {
     const gpu = this.gpu;
     const { cond, width, height, steps, sampler, signal } = opts;
@@ -122,7 +126,17 @@ export class LatentPipeline {
       }
       const latent = await gpu.read(x);
       const ms = Date.now() - t0;
-      return { latent, sigmas, timings: { sample: ms, perStep: ms / plan.steps } };
+      let image = null;
+      let decodeMs = 0;
+      if (this.vae && opts.decode !== false) {
+        check();
+        const tv = Date.now();
+        onProgress({ phase: "decode", frac: 0 });
+        image = await this.vae.decode(latent, h, w, (f) => onProgress({ phase: "decode", frac: f }));
+        decodeMs = Date.now() - tv;
+      }
+      return { latent, image, sigmas, timings: { sample: ms, perStep: ms / plan.steps, decode: decodeMs,
+        total: ms + decodeMs } };
     } finally {
       if (fg) fg.release();
       for (const t of [x, lat, old, oldD, den]) if (t) t.release();

@@ -7,6 +7,7 @@
 // Node-12 syntax only.
 
 import * as ops from "./ops.mjs";
+import { native } from "./gpu.mjs";
 
 // latent denormalization constants of the Qwen-Image VAE (app/models/vae.js:6-7)
 export const LATENT_MEAN = [-0.7571, -0.7089, -0.9113, 0.1075, -0.1745, 0.9653, -0.1517, 1.5508, 0.4134, -0.0715, 0.5517,
@@ -91,6 +92,7 @@ export class VAEDecoder {
     // conv / attention arithmetic: "fp32" (the reference's: fp32-level results from the bf16 matrix
     // cores, activations as two bf16 terms) or "bf16" (activations rounded to bf16)
     this.precision = "fp32";
+    this.keepRaw = false; // decode() also returns the float output before clamping as `raw`
   }
 
   // residual block (app/models/vae.js:42-56): norm + SiLU -> conv -> norm + SiLU -> conv + shortcut
@@ -169,17 +171,16 @@ export class VAEDecoder {
       if (onStage) onStage(f);
     });
     zt.release();
-    const px = await gpu.read(rgb);
-    rgb.release();
     const H = 8 * h, W = 8 * w;
-    const img = new Uint8ClampedArray(H * W * 4);
-    for (let i = 0; i < H * W; i++) {
-      for (let c = 0; c < 3; c++) {
-        const v = (Math.min(1, Math.max(-1, px[i * 3 + c])) + 1) / 2;
-        img[i * 4 + c] = Math.round(v * 255);
-      }
-      img[i * 4 + 3] = 255;
-    }
-    return { data: img, width: W, height: H, raw: px };
+    // RGBA on the device (vae.js:104-112's loop, same arithmetic), one read of 4 bytes per pixel
+    const rgba = gpu.empty([H * W * 4], "u8");
+    native.toRgba(gpu.ctx, rgb.buf, H * W, rgba.buf);
+    const bytes = await gpu.read(rgba);
+    rgba.release();
+    const img = new Uint8ClampedArray(bytes.buffer, bytes.byteOffset, bytes.length);
+    const out = { data: img, width: W, height: H };
+    if (this.keepRaw) out.raw = await gpu.read(rgb);
+    rgb.release();
+    return out;
   }
 }

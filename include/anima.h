@@ -304,6 +304,10 @@ int anima_conv3x3(anima_ctx* ctx, const anima_conv_desc* desc);
 /* ops.channelNorm (app/gpu/ops.js:119-126; kernels.js:62-89 mode 1, the Wan VAE RMS_norm):
  * y = x * sqrt(cols) / max(||x||, 1e-12) * gamma per row, then SiLU when silu != 0.  y may equal x. */
 int anima_channel_norm(anima_ctx* ctx, const float* x, const float* gamma, float* y, int64_t rows, int cols, int silu);
+/* The decoder's image conversion (app/models/vae.js:104-112, a host loop in the reference) on the
+ * device: out[i] = RGBA bytes of x[i][0..2], each round((clamp(v, -1, 1) + 1) / 2 * 255) with the
+ * reference's double-precision arithmetic and Math.round ties; alpha 255.  out 4-byte aligned. */
+int anima_to_rgba(anima_ctx* ctx, const float* x, int64_t n, uint8_t* out);
 
 /* ---------------------------------------------------------------- linears */
 

@@ -122,6 +122,18 @@ def decode(W, latent, upsamples):
         x = channel_norm(x, W["decoder.head.0.gamma"], True)
         x = conv3x3(x, W["decoder.head.2.weight"], W["decoder.head.2.bias"])
     out = x[0].numpy()
+    return out, to_rgba(out)
+
+
+def to_rgba(out):
+    """RGBA bytes of the decoder output [H, W, 3] (app/models/vae.js:104-112): float32 values promoted
+    to double, clamp to [-1, 1], (v + 1) / 2 * 255, JS Math.round (nearest, ties toward +inf), a NaN
+    stored as 0 by Uint8ClampedArray; alpha 255."""
+    out = np.asarray(out, np.float32)
+    t = (np.clip(out.astype(np.float64), -1.0, 1.0) + 1.0) / 2.0 * 255.0
+    r = np.floor(t)
+    r = np.where(t - r >= 0.5, r + 1.0, r)
+    r = np.where(np.isnan(t), 0.0, r)
     img = np.full(out.shape[:2] + (4,), 255, np.uint8)
-    img[..., :3] = np.round((np.clip(out, -1, 1) + 1) / 2 * 255).astype(np.uint8)
-    return out, img
+    img[..., :3] = r.astype(np.uint8)
+    return img

@@ -29,6 +29,7 @@
 //   fullstep   the full-size CFG step of a synthetic DiT: eager, with equal contexts, and replayed
 //              from a HIP graph
 //   vae        VAEDecoder.decode of a seeded synthetic decoder: raw output, RGBA bytes, stages
+//   pipeline   LatentPipeline.generate with a VAE: progress events, the image, a cancelled run
 
 import fs from "fs";
 import { GPU, native } from "../../anima-studio_amd/js/gpu.mjs";
@@ -186,6 +187,31 @@ async function main() {
     }
     console.log(JSON.stringify({ runs, stats: pipe.stats }));
     pipe.clearTimeCache();
+  } else if (c.case === "pipeline") {
+    // LatentPipeline.generate with a VAE: progress events, the decoded image, and cancellation
+    const dit = AnimaDiT.synthetic(gpu, new SyntheticWeights(gpu, 5, { mode: "int8", blocks: c.blocks }));
+    const vae = VAEDecoder.synthetic(gpu, new SyntheticWeights(gpu, 21));
+    const pipe = new LatentPipeline(gpu, dit, { vae });
+    const ctxs = [0, 1].map((b) => gpu.fromArray(new TorchGenerator(100 + b).randn(c.Lk * 1024), [c.Lk, 1024]));
+    const cond = dit.prepareContext(ctxs);
+    const events = [];
+    const opts = { cond, width: c.size, height: c.size, steps: c.steps, sampler: "euler", cfg: 3,
+      onProgress: (e) => events.push(e) };
+    const r = await pipe.generate(opts);
+    save(c.out + ".latent", r.latent);
+    save(c.out + ".img", r.image.data);
+    // cancelled after the first progress event: the generation throws an AbortError
+    const signal = { aborted: false };
+    let cancel = null;
+    try {
+      await pipe.generate(Object.assign({}, opts, { signal, onProgress: () => { signal.aborted = true; } }));
+    } catch (e) {
+      cancel = { name: e.name, message: e.message };
+    }
+    console.log(JSON.stringify({ pipeline: { events, image: [r.image.width, r.image.height], cancel,
+      timings: r.timings, pool: gpu.pool.allocated } }));
+    cond.release();
+    pipe.clearTimeCache();
   } else if (c.case === "graph") {
     const dit = AnimaDiT.synthetic(gpu, new SyntheticWeights(gpu, 9, { mode: c.mode, blocks: c.blocks }));
     const ctxs = [0, 1].map((b) => gpu.fromArray(new TorchGenerator(200 + b).randn(c.Lk * 1024), [c.Lk, 1024]));
@@ -235,6 +261,7 @@ async function main() {
     // the VAE decoder on seeded synthetic weights: raw output, RGBA image, progress stages
     const vae = VAEDecoder.synthetic(gpu, new SyntheticWeights(gpu, c.seed));
     vae.precision = c.precision || "fp32";
+    vae.keepRaw = true;
     const stages = [];
     const r = await vae.decode(load(c.latent), c.h, c.w, (f) => stages.push(f));
     save(c.out + ".raw", r.raw);

@@ -84,3 +84,23 @@ def test_vae_oracle_decode_runs():
     out, img = vae_ref.decode(W, lat, synthetic.VAE_UPSAMPLES)
     assert out.shape == (32, 32, 3) and img.shape == (32, 32, 4) and np.all(np.isfinite(out))
     assert np.all(img[..., 3] == 255)
+
+
+def test_to_rgba_matches_js_semantics():
+    # Math.round: nearest, ties toward +inf (x = 0 -> 127.5 -> 128; np.round would agree there, so
+    # ties are also pinned directly below); clamp to [-1, 1]; NaN -> 0 (Uint8ClampedArray); alpha 255
+    x = np.array([[[0.0, -1.0, 1.0], [5.0, -7.0, np.nan], [-0.5, 0.5, 0.999]]], np.float32)
+    img = vae_ref.to_rgba(x)
+    assert img.tolist() == [[[128, 0, 255, 255], [255, 0, 0, 255], [64, 191, 255, 255]]]
+
+    def js_round(t):  # the spec's definition, one value at a time
+        f = math.floor(t)
+        return f + 1 if t - f >= 0.5 else f
+
+    rng = np.random.default_rng(5)
+    v = rng.uniform(-1.2, 1.2, (1, 4000, 3)).astype(np.float32)
+    got = vae_ref.to_rgba(v)[0, :, :3]
+    ref = [[js_round((min(1.0, max(-1.0, float(a))) + 1.0) / 2.0 * 255.0) for a in row] for row in v[0]]
+    assert got.tolist() == ref
+    # ties: the helper rounds 2.5 -> 3 and 3.5 -> 4 (banker's rounding would give 2 and 4)
+    assert js_round(2.5) == 3 and js_round(3.5) == 4

@@ -158,7 +158,37 @@ def test_vae_decode_through_js_matches_float64(tmp_path, precision):
     d = np.abs(img.astype(int) - ref_img.astype(int))
     print(f"vae image bytes: max |d| {d.max()}, {np.count_nonzero(d)} of {d.size} differ", flush=True)
     assert np.all(np.isfinite(raw))
+    # the device's RGBA conversion is the reference loop's arithmetic: exact on the device's own output
+    assert np.array_equal(img, vae_ref.to_rgba(raw))
     if precision == "fp32":
         assert rr <= 1e-3 and d.max() <= 1
     else:
         assert rr <= 5e-2
+
+
+@pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")
+@pytest.mark.timeout(600)
+def test_pipeline_generate_decodes_reports_progress_and_cancels(tmp_path):
+    """LatentPipeline.generate with a VAE (app/pipeline.js:225-292): per-block sampling progress
+    with increasing fractions, decode progress, the image of the final latent (equal to a separate
+    decode of it), and an AbortError when the signal is raised mid-generation."""
+    from oracle import synthetic, vae_ref
+
+    out = str(tmp_path / "p")
+    spec = {"case": "pipeline", "blocks": 2, "size": 128, "steps": 3, "Lk": 64, "out": out}
+    (tmp_path / "case.json").write_text(json.dumps(spec))
+    print("[case] js pipeline generate + decode 128x128, 2 blocks, 3 steps", flush=True)
+    r = subprocess.run(["node", RUN_CASE, str(tmp_path / "case.json")], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-3000:]
+    info = json.loads(next(ln for ln in r.stdout.splitlines() if '"pipeline"' in ln))["pipeline"]
+    ev = info["events"]
+    sample = [e for e in ev if e["phase"] == "sample"]
+    decode = [e for e in ev if e["phase"] == "decode"]
+    assert len(sample) == 3 * 2 and [e["frac"] for e in sample] == sorted(e["frac"] for e in sample)
+    assert abs(sample[-1]["frac"] - 1.0) < 1e-9 and decode[0]["frac"] == 0 and decode[-1]["frac"] == 1
+    assert info["image"] == [128, 128]
+    assert info["cancel"] is not None and info["cancel"]["name"] == "AbortError"
+    lat = np.fromfile(out + ".latent", np.float32).reshape(16, 16, 16)
+    img = np.fromfile(out + ".img", np.uint8).reshape(128, 128, 4)
+    _, ref_img = vae_ref.decode(synthetic.vae_weights(21), lat, synthetic.VAE_UPSAMPLES)
+    assert np.abs(img.astype(int) - ref_img.astype(int)).max() <= 1
