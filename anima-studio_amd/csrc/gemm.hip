@@ -62,19 +62,28 @@ __device__ __forceinline__ float fp8e4m3(uint32_t b) {  // app/gpu/gemm.js:144-1
   return (b & 128u) ? -v : v;
 }
 
-// 4 nibbles (one per byte, values 0..15) -> 4 table bytes, table = 16 bytes in t0..t3.
-__device__ __forceinline__ uint32_t lut4(uint32_t nib, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
-  const uint32_t sel = nib & 0x07070707u;
+// 4 nibbles -> 4 table bytes (table = 16 bytes in t0..t3).  x holds the nibbles' bit 3 as the
+// sign bit of each byte (bits 0..2 of the selector bytes in sel).  Entries 0..7 and 8..15 come
+// from two byte permutes; the choice between them is a byte mask made from the four sign bits
+// by a third permute (selectors 8..11 replicate the sign of bytes 1, 3, 5, 7 of {x << 8, x}).
+__device__ __forceinline__ uint32_t lut4(uint32_t sel, uint32_t x, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
   const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);  // entries 0..7
   const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);  // entries 8..15
-  const uint32_t mask = ((nib >> 3) & 0x01010101u) * 0xffu;
+  const uint32_t mask = __builtin_amdgcn_perm(x << 8, x, 0x090b080au);
   return (hi & mask) | (lo & ~mask);
+}
+// even nibbles (low, k = 0, 2, 4, 6) and odd nibbles (high, k = 1, 3, 5, 7) of a code word
+__device__ __forceinline__ uint32_t lut4_even(uint32_t w, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+  return lut4(w & 0x07070707u, w << 4, t0, t1, t2, t3);
+}
+__device__ __forceinline__ uint32_t lut4_odd(uint32_t w, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+  return lut4((w >> 4) & 0x07070707u, w, t0, t1, t2, t3);
 }
 
 // 8 consecutive 4-bit codes (low nibble = even k) -> 8 int8 values in k order.
 __device__ __forceinline__ uint2 decode8(uint32_t w, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
-  const uint32_t ev = lut4(w & 0x0f0f0f0fu, t0, t1, t2, t3);          // k = 0, 2, 4, 6
-  const uint32_t od = lut4((w >> 4) & 0x0f0f0f0fu, t0, t1, t2, t3);   // k = 1, 3, 5, 7
+  const uint32_t ev = lut4_even(w, t0, t1, t2, t3);  // k = 0, 2, 4, 6
+  const uint32_t od = lut4_odd(w, t0, t1, t2, t3);   // k = 1, 3, 5, 7
   return make_uint2(__builtin_amdgcn_perm(od, ev, 0x05010400u), __builtin_amdgcn_perm(od, ev, 0x07030602u));
 }
 
@@ -224,8 +233,8 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
 // n + 8(r/4) + r%4 with n = (tile column) + 4g.  Four consecutive columns of one row sit in four
 // consecutive registers and move as one 16-byte access; the row scale is one value per lane.
 // Arithmetic order is that of epilogue_store.
-struct EpiCols {  // per-column operands of one 32-column tile for this lane: columns n + 8q + e
-  f32x4 sw[4], gate[4];  // (a bias, rare, is read where it is added)
+struct EpiCols {  // per-column scales of one 32-column tile for this lane: columns n + 8q + e
+  f32x4 sw[4];    // (a bias, rare, and the gate are read where they are used)
 };
 
 __device__ __forceinline__ void epi_cols(const GemmArgs& a, int n, EpiCols& c) {
@@ -234,7 +243,6 @@ __device__ __forceinline__ void epi_cols(const GemmArgs& a, int n, EpiCols& c) {
     const bool ok = n + 8 * q < a.N;  // N % 4 == 0: a 4-column group is all in or all out
     const int nq = ok ? n + 8 * q : 0;
     c.sw[q] = *(const f32x4*)(a.sw + nq);
-    c.gate[q] = a.epi == ANIMA_EPI_GATED ? *(const f32x4*)(a.gate + a.gate_off + nq) : (f32x4){};
   }
 }
 
@@ -282,8 +290,9 @@ __device__ __forceinline__ void epi_store_t(const GemmArgs& a, const i32x16& v, 
     } else if constexpr (EPI == ANIMA_EPI_RESID) {
       o = cv[q] + y;
     } else {
+      const f32x4 gt = *(const f32x4*)(a.gate + a.gate_off + nq);
 #pragma unroll
-      for (int e = 0; e < 4; e++) o[e] = __builtin_fmaf(c.gate[q][e], y[e], cv[q][e]);
+      for (int e = 0; e < 4; e++) o[e] = __builtin_fmaf(gt[e], y[e], cv[q][e]);
     }
     *(f32x4*)(orow + nq) = o;
   }
@@ -301,10 +310,20 @@ __device__ __forceinline__ void epi_store_t(const GemmArgs& a, const i32x16& v, 
 // LDS tile layout: row r (an M row of A or an N row of B) holds four 16-byte k units; unit u is
 // stored at slot u ^ ((r / 4) % 4), which spreads one unit index of 16 consecutive rows over
 // 16 distinct bank groups (rows 4 apart would otherwise share banks in 64-byte rows).
+//
+// W4 weights are unpacked in registers on their way into the B tile (gemm.js:141-158 semantics):
+// a 16-byte k unit of a B row is one 16-weight group = 8 code bytes + 1 s_rel byte.  Every lane
+// of all 8 waves owns two (row, unit) slots of the tile; it loads their codes and s_rel bytes
+// into VGPRs one stage before the stage is published, reads the group's 16-entry int8 table
+// (built in LDS at kernel start for all 256 s_rel values, T[s][c] = clamp(rint(codebook[c] *
+// fp8(s)), -127, 127)), turns the 16 nibbles into 16 grid bytes with byte permutes, and writes
+// them to the slot the direct copy of an int8 weight would have filled.  The MFMA stream and
+// the fragment reads are the int8 kernel's.
 constexpr int G2_BK = 64;               // k bytes per stage
 constexpr int G2_TILE = 256 * G2_BK;    // bytes of one operand tile
 constexpr int G2_ST = 2 * G2_TILE;      // stage: A tile, then B tile
 constexpr int G2_NST = 4;
+constexpr int G2_GM = 4;                // row tiles per group of the tile order
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -319,13 +338,25 @@ __device__ __forceinline__ void g2_barrier() {
 // vmcnt(n) only (expcnt and lgkmcnt at their no-wait maxima), gfx9 s_waitcnt encoding.
 #define G2_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
 
-template <int EPI>
+constexpr int G2_LUT = G2_NST * G2_ST;  // W4 table offset in LDS (256 x 16 bytes)
+
+template <int EPI, bool W4>
 __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
-  __shared__ __attribute__((aligned(1024))) char smem[G2_NST * G2_ST];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  __shared__ __attribute__((aligned(1024))) char smem[G2_NST * G2_ST + (W4 ? 4096 : 0)];
+  // the wave index is uniform: in a scalar register, so copy offsets derived from it stay scalar
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lq = lane & 31, hf = lane >> 5;
-  const int ntn = (a.N + 255) / 256;
-  const int ntiles = ntn * ((a.M + 255) / 256);
+  const int ntn = (a.N + 255) / 256, ntm = (a.M + 255) / 256;
+  const int ntiles = ntn * ntm;
+  // Tile order: groups of G2_GM row tiles, column-major inside a group, so the tiles that one
+  // XCD's 32 CUs run at the same time form a G2_GM x 8 block whose A rows and B columns stay in
+  // that XCD's L2 (row-major order would put ~2 row tiles and ~24 column tiles in flight).
+  auto tile_mn = [&](int t, int& tm, int& tn) {
+    const int grp = t / (G2_GM * ntn), row0 = grp * G2_GM;
+    const int gm = min(G2_GM, ntm - row0), local = t - grp * (G2_GM * ntn);
+    tn = local / gm;
+    tm = row0 + (local - tn * gm);
+  };
   const int wm = (wave & 1) * 128, wn = (wave >> 1) * 64;
   const int K = a.K;
   const int nk = K / G2_BK;
@@ -346,29 +377,76 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
   // the other wave of each SIMD runs an MFMA stream free of copy and M0 set-up instructions
   // (3-4% faster than eight issuing waves).  Wave w < 4 moves the 1 KiB chunks of rows
   // 16*(2*w + c) + lane/4 and the same rows + 128 of each tile (unit permuted); rows r and r + 128
-  // share the permutation.
-  const int row0 = 32 * wave + (lane >> 2), row1 = row0 + 16;
+  // share the permutation.  With W4 weights every wave unpacks B bytes, and every wave also
+  // copies its two A chunks (those of rows 32*(w%4) + 128*(w/4) + 16*c + lane/4).
+  const int row0 = 32 * (wave & 3) + (lane >> 2), row1 = row0 + 16;
   const int loff0 = row0 * K + 16 * ((lane & 3) ^ ((row0 >> 2) & 3));
   const int loff1 = row1 * K + 16 * ((lane & 3) ^ ((row1 >> 2) & 3));
   // The copy stream runs three stages ahead of the compute: ig = next stage to copy (LDS stage
   // ig % 4), is = its k-stage within tile it; ra / rb are tile it's buffer resources, which
   // cover the tile's rows only, so rows past M (N) read as zero.  Advanced incrementally (no
-  // division per stage).
+  // division per stage).  Past this workgroup's last stage the resources stay those of its
+  // last tile, so the copies issued there (unconditionally, to keep the wait counts the same
+  // on every path) re-read that tile in bounds into LDS stages no wave reads any more.
   int ig = 0, is = 0, it = 0;
-  __amdgpu_buffer_rsrc_t ra, rb;
+  __amdgpu_buffer_rsrc_t ra, rb, rc, rs;  // A, int8 B | W4 codes, W4 s_rel
+  // W4 slots of this lane: tile rows wrow + 16 c (c = 0, 1), k unit wunit of the stage (the unit
+  // whose copy lands in this lane's LDS slot; rows 16 apart share it), LDS chunk
+  // (wchunk + c) * 1024 + 16 * lane.  Row c = 1 is a constant byte step away (scalar offset).
+  const int wrow = 32 * (wave & 3) + 128 * (wave >> 2) + (lane >> 2), wchunk = 2 * (wave & 3) + 8 * (wave >> 2);
+  const int wunit = (lane & 3) ^ ((wrow >> 2) & 3);
+  const int coff = wrow * (K / 2) + 8 * wunit, soff = wrow * (K / 16) + wunit;
+  // W4 codes are a second stream (stage cs of tile ct next, resources rc / rs), issued between
+  // the two k-steps of each iteration into one of two register sets (stage parity): stage X's
+  // codes are loaded into set X % 2 during iteration X-3 and unpacked during iteration X-2.
+  int cs = 0, ct = 0;
+  uint2 wcode[2][2] = {};
+  uint32_t wsrel[2][2] = {};
 #define G2_RSRC()                                                                                             \
   {                                                                                                           \
-    const int t_ = first + it * stride, tm_ = t_ / ntn;                                                       \
-    const int bm_ = tm_ * 256, bn_ = (t_ - tm_ * ntn) * 256;                                                  \
+    int tm_, tn_;                                                                                             \
+    tile_mn(first + it * stride, tm_, tn_);                                                                   \
+    const int bm_ = tm_ * 256, bn_ = tn_ * 256;                                                               \
     ra = __builtin_amdgcn_make_buffer_rsrc((void*)(a.qx + (int64_t)bm_ * K), (short)0, min(256, a.M - bm_) * K, \
                                            0x00020000);                                                       \
-    rb = __builtin_amdgcn_make_buffer_rsrc((void*)((const int8_t*)a.w + (int64_t)bn_ * K), (short)0,           \
-                                           min(256, a.N - bn_) * K, 0x00020000);                              \
+    if constexpr (!W4) {                                                                                      \
+      rb = __builtin_amdgcn_make_buffer_rsrc((void*)((const int8_t*)a.w + (int64_t)bn_ * K), (short)0,         \
+                                             min(256, a.N - bn_) * K, 0x00020000);                            \
+    }                                                                                                         \
+  }
+#define G2_RSRC_C()                                                                                           \
+  {                                                                                                           \
+    int tm_, tn_;                                                                                             \
+    tile_mn(first + ct * stride, tm_, tn_);                                                                   \
+    const int bn_ = tn_ * 256;                                                                                \
+    rc = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint8_t*)a.w + (int64_t)bn_ * (K / 2)), (short)0,    \
+                                           min(256, a.N - bn_) * (K / 2), 0x00020000);                        \
+    rs = __builtin_amdgcn_make_buffer_rsrc((void*)(a.srel + (int64_t)bn_ * (K / 16)), (short)0,                \
+                                           min(256, a.N - bn_) * (K / 16), 0x00020000);                       \
+  }
+  // W4: this lane's codes and s_rel bytes of the next codes stage into register set SET
+#define G2_ISSUE_C(SET)                                                                                       \
+  {                                                                                                           \
+    _Pragma("unroll") for (int c_ = 0; c_ < 2; c_++) {                                                        \
+      const auto v_ = __builtin_amdgcn_raw_buffer_load_b64(rc, coff, cs * (G2_BK / 2) + c_ * 8 * K, 0);       \
+      wcode[SET][c_] = make_uint2(v_[0], v_[1]);                                                              \
+      wsrel[SET][c_] = __builtin_amdgcn_raw_buffer_load_b8(rs, soff, cs * (G2_BK / 16) + c_ * K, 0);         \
+    }                                                                                                         \
+    if (++cs == nk) {                                                                                         \
+      cs = 0;                                                                                                 \
+      if (++ct < mine) G2_RSRC_C();                                                                           \
+    }                                                                                                         \
   }
 #define G2_ISSUE()                                                                                            \
   {                                                                                                           \
     char* st_ = smem + (ig & (G2_NST - 1)) * G2_ST;                                                           \
-    if (wave < 4) {                                                                                           \
+    if constexpr (W4) {                                                                                       \
+      /* every wave: its two A chunks (the same chunks as its W4 slots) */                                    \
+      const int so_ = is * G2_BK + (wave >> 2) * 128 * K;                                                     \
+      char* sw_ = st_ + wchunk * 1024;                                                                        \
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sw_), 16, loff0, so_, 0, 0);                 \
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(sw_ + 1024), 16, loff1, so_, 0, 0);          \
+    } else if (wave < 4) {                                                                                    \
       _Pragma("unroll") for (int h_ = 0; h_ < 2; h_++) {                                                      \
         const int so_ = is * G2_BK + h_ * 128 * K;                                                            \
         char* sw_ = st_ + (2 * wave + 8 * h_) * 1024;                                                         \
@@ -384,6 +462,52 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
       if (++it < mine) G2_RSRC();                                                                             \
     }                                                                                                         \
   }
+  // W4 unpack of one stage's codes (register set SET) into the B tile of LDS stage st, in three
+  // steps so the loop can spread them over its MFMAs: the two group tables (w4_tables), the
+  // nibble lookups (w4_lookup, part q = slot q/4, code word (q/2)%2, even / odd nibbles q%2),
+  // and the byte interleave + tile write of a slot (w4_store).  The table read and the tile
+  // write are explicit LDS instructions: the compiler cannot tell them apart from the in-flight
+  // direct copies into other stages and would otherwise wait for all of those first.  Ordering
+  // is the barrier protocol's: the slot is free after the barrier of the iteration that writes
+  // it, the tables were written before the first barrier, and every wave waits lgkmcnt(0)
+  // before the barrier that publishes the slot.
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)smem;
+  i32x4 wt[2];         // group tables of the two slots
+  uint32_t wl[2][4];   // nibble lookups: [slot][2 * word + odd]
+  auto w4_tables = [&](int set) {
+    if constexpr (W4) {
+      asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                   : "=&v"(wt[0]), "=&v"(wt[1])
+                   : "v"(lds0 + G2_LUT + 16 * (wsrel[set][0] & 0xffu)), "v"(lds0 + G2_LUT + 16 * (wsrel[set][1] & 0xffu))
+                   : "memory");
+    }
+  };
+  auto w4_lookup = [&](int set, int q) {
+    if constexpr (W4) {
+      const int c_ = q >> 2, word = (q >> 1) & 1, odd = q & 1;
+      const uint32_t w = word ? wcode[set][c_].y : wcode[set][c_].x;
+      wl[c_][q & 3] = odd ? lut4_odd(w, wt[c_][0], wt[c_][1], wt[c_][2], wt[c_][3])
+                          : lut4_even(w, wt[c_][0], wt[c_][1], wt[c_][2], wt[c_][3]);
+    }
+  };
+  auto w4_store = [&](int st, int c_) {
+    if constexpr (W4) {
+      // even / odd k bytes -> k order (decode8's interleave)
+      const i32x4 o = {(int)__builtin_amdgcn_perm(wl[c_][1], wl[c_][0], 0x05010400u),
+                       (int)__builtin_amdgcn_perm(wl[c_][1], wl[c_][0], 0x07030602u),
+                       (int)__builtin_amdgcn_perm(wl[c_][3], wl[c_][2], 0x05010400u),
+                       (int)__builtin_amdgcn_perm(wl[c_][3], wl[c_][2], 0x07030602u)};
+      const uint32_t dst = lds0 + (st & (G2_NST - 1)) * G2_ST + G2_TILE + (wchunk + c_) * 1024 + 16 * lane;
+      asm volatile("ds_write_b128 %0, %1" ::"v"(dst), "v"(o) : "memory");
+    }
+  };
+  auto w4_unpack = [&](int set, int st) {  // all three steps at once (prologue)
+    w4_tables(set);
+#pragma unroll
+    for (int q = 0; q < 8; q++) w4_lookup(set, q);
+    w4_store(st, 0);
+    w4_store(st, 1);
+  };
   // fragment lane offsets: row lq of a 32-row tile, unit 2*ks + hf (k-step ks of 32 bytes)
   int fofs[2];
 #pragma unroll
@@ -397,14 +521,51 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
 
   // Stage g is published (barrier) one iteration before it is computed, so the fragment reads
   // of its first k-step run under the MFMAs of stage g-1's second k-step.
+  // W4: stage g's codes are issued with its A copies (iteration g-3) and unpacked into LDS at
+  // iteration g-2, after the barrier that ends all reads of the LDS stage it reuses, so the
+  // barrier of iteration g-1 publishes them with the A tile.
   i32x4 af0[4], bf0[2], af1[4], bf1[2];
-  if (total > 0) G2_RSRC();
-  if (total > 0) G2_ISSUE();
-  if (total > 1) G2_ISSUE();
-  if (total > 2) G2_ISSUE();
-  if (total > 2) G2_WAIT_VM(16);
-  else if (total > 1) G2_WAIT_VM(8);
-  else G2_WAIT_VM(0);
+  if constexpr (W4) {
+    // the 256 tables, 4 dwords each: table s, bytes c = clamp(rint(codebook[c] * fp8(s)), -127, 127)
+    for (int i = tid; i < 256 * 4; i += 512) {
+      const float sv = fp8e4m3((uint32_t)(i >> 2));
+      uint32_t packed = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        float v = rintf(a.cb[4 * (i & 3) + j] * sv);
+        v = fminf(fmaxf(v, -127.0f), 127.0f);
+        packed |= ((uint32_t)(int32_t)v & 0xffu) << (8 * j);
+      }
+      *(uint32_t*)(smem + G2_LUT + 4 * i) = packed;
+    }
+    __syncthreads();
+  }
+  if (total == 0) return;
+  G2_RSRC();
+  if constexpr (W4) {
+    // stages 0 and 1 unpacked here (their copies waited for outright), stage 2 during
+    // iteration 0.  From here on, per wave and iteration: 2 A copies (stage g+3, at the start),
+    // then 4 code / s_rel loads (stage g+3, between the k-steps or after a tile's epilogue).
+    G2_RSRC_C();
+    G2_ISSUE();
+    G2_ISSUE_C(0);
+    G2_WAIT_VM(0);
+    w4_unpack(0, 0);
+    G2_ISSUE();
+    G2_ISSUE_C(1);
+    G2_WAIT_VM(0);
+    w4_unpack(1, 1);
+    G2_ISSUE();
+    G2_ISSUE_C(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's unpacked B bytes are in LDS
+  } else {
+    if (total > 0) G2_ISSUE();
+    if (total > 1) G2_ISSUE();
+    if (total > 2) G2_ISSUE();
+    if (total > 2) G2_WAIT_VM(16);
+    else if (total > 1) G2_WAIT_VM(8);
+    else G2_WAIT_VM(0);
+  }
   g2_barrier();
   if (total > 0) {
 #pragma unroll
@@ -413,18 +574,42 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
     for (int j = 0; j < 2; j++) bf0[j] = *(const i32x4*)(smem + G2_TILE + (wn + 32 * j) * G2_BK + fofs[0]);
   }
   int s = 0, k = 0;  // stage within the tile, tile index within this workgroup's list
-  for (int g = 0; g < total; g++) {
+  // One iteration per stage g; written as a lambda over the stage parity P (a compile-time W4
+  // register set), called for even and odd stages in turn.
+  auto iteration = [&](const int g, auto par) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
     // publish stage g+1: this wave's copies of it are done once at most those of g+2 are
     // pending; the barrier also ends every wave's reads of stage g-1, which is refilled with g+3
-    if (g + 2 < total) G2_WAIT_VM(8);
-    else G2_WAIT_VM(0);
+    if constexpr (W4) {
+      // stage g+1's A copies landed (stage g+2's A copies and codes may pend: 6); this wave's
+      // unpacked bytes of stage g+1 (written during iteration g-1) are in LDS
+      G2_WAIT_VM(6);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+    } else {
+      if (g + 2 < total) G2_WAIT_VM(8);
+      else G2_WAIT_VM(0);
+    }
     g2_barrier();
-    if (g + 3 < total) G2_ISSUE();
+    // W4: stage g+2 is unpacked from set P during the second k-step of this iteration: its
+    // tables are read between the k-steps (the only loads issued after its codes are stage
+    // g+3's A copies, which stay in flight), then stage g+3's codes are issued into set 1-P.
+    // Past the last stage the unpack runs on stale registers into the LDS stage of g-2, which no
+    // wave reads any more (harmless, and branch-free inside the MFMA stream).  On the
+    // iteration that ends a tile, stage g+3's codes are issued after the epilogue, so no code
+    // registers are live across it (register pressure; one wait per tile).
+    const bool late = W4 && s + 1 == nk;
+    if constexpr (W4) {
+      G2_ISSUE();
+    } else {
+      if (g + 3 < total) G2_ISSUE();
+    }
     // Hand-ordered (sched_barrier fences keep the written order): each MFMA of one k-step is
     // followed by one fragment read for the next k-step, B fragments first, so a fragment is
     // read at least three MFMAs (~100 cycles) before its first use.  The second k-step reads
     // stage g+1 (unconditionally: after the last stage this reads a stale stage whose values
-    // are unused; a branch here would make the compiler drain all LDS reads first).
+    // are unused; a branch here would make the compiler drain all LDS reads first).  W4, in the
+    // second k-step: two nibble lookups after each of its MFMAs 1-4, one tile write after each
+    // of MFMAs 5 and 6.
     const char* st = smem + (g & (G2_NST - 1)) * G2_ST;
     const char* sn = smem + ((g + 1) & (G2_NST - 1)) * G2_ST;
 #pragma unroll
@@ -434,11 +619,20 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
       else if (q < 6) af1[q - 2] = *(const i32x4*)(st + (wm + 32 * (q - 2)) * G2_BK + fofs[1]);
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (W4) {
+      w4_tables(P);
+      if (!late) G2_ISSUE_C(1 - P);
+    }
 #pragma unroll
     for (int q = 0; q < 8; q++) {
       acc[q >> 1][q & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf1[q & 1], af1[q >> 1], acc[q >> 1][q & 1], 0, 0, 0);
       if (q < 2) bf0[q] = *(const i32x4*)(sn + G2_TILE + (wn + 32 * q) * G2_BK + fofs[0]);
       else if (q < 6) af0[q - 2] = *(const i32x4*)(sn + (wm + 32 * (q - 2)) * G2_BK + fofs[0]);
+      if (q >= 1 && q <= 4) {
+        w4_lookup(P, 2 * (q - 1));
+        w4_lookup(P, 2 * (q - 1) + 1);
+      }
+      if (q == 5 || q == 6) w4_store(g + 2, q - 5);
       __builtin_amdgcn_sched_barrier(0);
     }
     if (++s == nk) {
@@ -447,8 +641,9 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
       // and a run-time tile index would put the accumulators in scratch memory)
       // The residual loads of the next 32x32 tile are issued before the current tile's
       // stores, so each tile's wait overlaps the previous tile's arithmetic.
-      const int t = first + k * stride, tm = t / ntn;
-      const int m0 = tm * 256 + wm + lq, n0 = (t - tm * ntn) * 256 + wn + 4 * hf;
+      int tm, tn;
+      tile_mn(first + k * stride, tm, tn);
+      const int m0 = tm * 256 + wm + lq, n0 = tn * 256 + wn + 4 * hf;
       float sxv[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) sxv[i] = m0 + 32 * i < a.M ? a.sx[m0 + 32 * i] : 0.0f;
@@ -476,50 +671,22 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
         for (int j = 0; j < 2; j++) acc[i][j] = (i32x16){};
       s = 0;
       k++;
+      if constexpr (W4) {
+        if (late) G2_ISSUE_C(1 - P);
+      }
     }
+  };
+  for (int g = 0; g < total; g += 2) {
+    iteration(g, std::integral_constant<int, 0>{});
+    if (g + 1 < total) iteration(g + 1, std::integral_constant<int, 1>{});
   }
+  G2_WAIT_VM(0);  // no copy into LDS outlives the workgroup
 }
 #undef G2_WAIT_VM
 #undef G2_ISSUE
+#undef G2_ISSUE_C
 #undef G2_RSRC
-
-// ------------------------------------------------------------------ W4 -> int8 decode pass
-//
-// For the 256x256 kernel a W4 weight is decoded once per call into an int8 workspace (the
-// in-GEMM decode repeats it for every 256-row band of M).  Thread = 32 weights: 16 bytes of
-// codes (low nibble = even k) and their two fp8 s_rel bytes; the 16-entry tables of all 256
-// s_rel values are built in LDS per workgroup exactly as in gemm_i8_kernel<true>.
-__global__ __launch_bounds__(256) void w4_decode_kernel(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ srel,
-                                                        const float* __restrict__ cb, int8_t* __restrict__ out, int64_t nchunk,
-                                                        int K) {
-  __shared__ __attribute__((aligned(16))) uint32_t lut[256 * 4];
-  for (int i = threadIdx.x; i < 256 * 4; i += 256) {
-    const float s = fp8e4m3((uint32_t)(i >> 2));
-    uint32_t packed = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      float v = rintf(cb[4 * (i & 3) + j] * s);
-      v = fminf(fmaxf(v, -127.0f), 127.0f);
-      packed |= ((uint32_t)(int32_t)v & 0xffu) << (8 * j);
-    }
-    lut[i] = packed;
-  }
-  __syncthreads();
-  const int cpr = K / 32;  // chunks of 32 weights per row
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nchunk; i += (int64_t)gridDim.x * 256) {
-    const int64_t row = i / cpr;
-    const int c = (int)(i - row * cpr);
-    const uint4 w = *(const uint4*)(codes + row * (K / 2) + 16 * c);
-    const uint8_t* sp = srel + row * (K / 16) + 2 * c;
-    const uint4 t0 = *(const uint4*)&lut[4 * sp[0]];
-    const uint4 t1 = *(const uint4*)&lut[4 * sp[1]];
-    const uint2 d0 = decode8(w.x, t0.x, t0.y, t0.z, t0.w), d1 = decode8(w.y, t0.x, t0.y, t0.z, t0.w);
-    const uint2 d2 = decode8(w.z, t1.x, t1.y, t1.z, t1.w), d3 = decode8(w.w, t1.x, t1.y, t1.z, t1.w);
-    uint4* o = (uint4*)(out + row * K + 32 * c);
-    o[0] = make_uint4(d0.x, d0.y, d1.x, d1.y);
-    o[1] = make_uint4(d2.x, d2.y, d3.x, d3.y);
-  }
-}
+#undef G2_RSRC_C
 
 // ------------------------------------------------------------------ bf16 weights, fp32 math
 
@@ -1268,38 +1435,30 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
   GemmArgs g{qx, sx, W->w, W->scale, W->srel, W->codebook, W->bias, d->out, ldc, alpha, d->act, d->epilogue,
              d->gate, d->gate_off, d->acc_out, (int)M, N, K, d->add, ld_add};
   int rc = ANIMA_OK;
-  // Grids that give every CU a 256x256 tile run the persistent 256 kernel; a W4 weight is then
-  // decoded once into an int8 workspace first.  Smaller grids run the 128x128 kernel, which
-  // decodes W4 inside the GEMM.
+  // Grids that give every CU a 256x256 tile run the persistent 256 kernel, smaller grids the
+  // 128x128 kernel; both unpack W4 codes inside the GEMM.
   // The 256 kernel's epilogue moves 16-byte column groups: it needs N % 4 == 0 and 16-byte
   // aligned output rows, scales, bias and gate.
   const int64_t tiles256 = (int64_t)((N + 255) / 256) * ((M + 255) / 256);
   const bool vec = N % 4 == 0 && g.ldc % 4 == 0 && al(g.out, 16) && al(g.sw, 16) && (!g.bias || al(g.bias, 16)) &&
                    (g.epi != ANIMA_EPI_GATED || al(g.gate + g.gate_off, 16)) && (!g.add || (al(g.add, 16) && g.ld_add % 4 == 0));
   const bool big = vec && tiles256 >= c->num_cus && tiles256 <= 0x7fffffff;
-  void* wdec = nullptr;
-  if (big && w4) {
-    if ((rc = anima_alloc(c, (size_t)N * K, &wdec))) {
-      if (tmp) anima_free(c, tmp);
-      return rc;
-    }
-    const int64_t nchunk = (int64_t)N * (K / 32);
-    Launch L(c, "w4.decode", 0.0, (double)N * K * 1.5 + (double)N * K / 16);
-    const int64_t blocks = (nchunk + 255) / 256;
-    hipLaunchKernelGGL(w4_decode_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, c->stream,
-                       (const uint8_t*)W->w, W->srel, W->codebook, (int8_t*)wdec, nchunk, K);
-    rc = L.end();
-    g.w = wdec;
-  }
-  if (rc == ANIMA_OK) {
+  {
     Launch L(c, w4 ? "gemm.w4a8" : "gemm.i8", 2.0 * M * N * K, 0.0);
     if (big) {
-      if (g.epi == ANIMA_EPI_STORE)
-        hipLaunchKernelGGL(gemm_i8_256<ANIMA_EPI_STORE>, dim3((unsigned)c->num_cus), dim3(512), 0, c->stream, g);
-      else if (g.epi == ANIMA_EPI_RESID)
-        hipLaunchKernelGGL(gemm_i8_256<ANIMA_EPI_RESID>, dim3((unsigned)c->num_cus), dim3(512), 0, c->stream, g);
-      else
-        hipLaunchKernelGGL(gemm_i8_256<ANIMA_EPI_GATED>, dim3((unsigned)c->num_cus), dim3(512), 0, c->stream, g);
+      const dim3 grid((unsigned)c->num_cus), block(512);
+#define G2L(E, W) hipLaunchKernelGGL((gemm_i8_256<E, W>), grid, block, 0, c->stream, g)
+      if (g.epi == ANIMA_EPI_STORE) {
+        if (w4) G2L(ANIMA_EPI_STORE, true);
+        else G2L(ANIMA_EPI_STORE, false);
+      } else if (g.epi == ANIMA_EPI_RESID) {
+        if (w4) G2L(ANIMA_EPI_RESID, true);
+        else G2L(ANIMA_EPI_RESID, false);
+      } else {
+        if (w4) G2L(ANIMA_EPI_GATED, true);
+        else G2L(ANIMA_EPI_GATED, false);
+      }
+#undef G2L
     } else {
       dim3 grid((N + GBN - 1) / GBN, (unsigned)((M + GBM - 1) / GBM));
       if (w4) hipLaunchKernelGGL(gemm_i8_kernel<true>, grid, dim3(256), 0, c->stream, g);
@@ -1307,7 +1466,6 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
     }
     rc = L.end();
   }
-  if (wdec) anima_free(c, wdec);  // stream-ordered reuse
   if (tmp) anima_free(c, tmp);
   return rc;
 }

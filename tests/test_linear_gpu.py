@@ -257,14 +257,15 @@ def test_out_projection_gated_epilogue(ctx, kind):
 
 @pytest.mark.parametrize("kind", ["i8", "w4"])
 def test_256_tile_kernel_ragged_edges(ctx, kind):
-    """M=4000, N=4100: 16 x 17 tiles of 256 (the 256x256 persistent kernel), partial last row
+    """M=4500, N=4100: 18 x 17 tiles of 256 (the 256x256 persistent kernel), partial last row
     and column tiles (rows / columns past the edge read as zero through the buffer bounds; W4
-    rows past N decode to zero); gated residual + bias epilogue and the int32 accumulators
-    bit-exact on sampled rows, including the last ones, and the accumulator checksums over the
-    whole product."""
-    case(f"256x256-tile kernel M=4000 N=4100 K=1024 gated + bias {kind}")
+    rows past N decode to zero), and a last group of 2 row tiles in the kernel's tile order
+    (groups of 4); gated residual + bias epilogue and the int32 accumulators bit-exact on
+    sampled rows, including the last ones, and the accumulator checksums over the whole
+    product."""
+    case(f"256x256-tile kernel M=4500 N=4100 K=1024 gated + bias {kind}")
     m = amd()
-    M, K, N = 4000, 1024, 4100
+    M, K, N = 4500, 1024, 4100
     x = orc.randn(91, M * K).reshape(M, K)
     qx, sx = orc.token_quant(orc.hadamard256(x))
     bias = (0.1 * orc.randn(93, N)).astype(np.float32)
@@ -289,6 +290,37 @@ def test_256_tile_kernel_ragged_edges(ctx, kind):
     assert np.array_equal(acc[rows], ref_acc)
     ref = orc.linear_epilogue(ref_acc, sx[rows], sw, bias=bias, epi=2, gate=mod, g_off=N, c=resid[rows])
     assert np.array_equal(got[rows], ref), report("gated", got[rows], ref)
+
+
+@pytest.mark.parametrize("K", [64, 192, 1024])
+def test_256_tile_kernel_w4_every_srel(ctx, K):
+    """W4 unpacked inside the 256x256 kernel over all 256 s_rel bytes (fp8 e4m3 0 .. 480, so the
+    grid clamps at +-127) with a non-uniform codebook reaching +-2 (a fitted one, quant.py:116-124),
+    at M = N = 4096 (one tile per CU).  K = 64 ends a tile at every stage, K = 192 alternates the
+    stage parity across tiles, K = 1024 runs long tiles.  int32 accumulators: checksums over the
+    whole product and exact sampled rows; the store epilogue bit-exact."""
+    case(f"256x256-tile kernel W4 every s_rel M=N=4096 K={K}")
+    m = amd()
+    M = N = 4096
+    rng = np.random.default_rng(K)
+    codes = rng.integers(0, 256, size=(N, K // 2), dtype=np.uint8)
+    srel = rng.integers(0, 256, size=(N, K // 16), dtype=np.uint8)
+    srel[:, 0] = np.arange(N) % 256  # every byte value in use
+    cb = np.sort(rng.uniform(-2.0, 2.0, 16)).astype(np.float32)
+    sw = (rng.uniform(0.5, 1.5, N) / (127 * np.sqrt(K))).astype(np.float32)
+    qx = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    sx = rng.uniform(0.001, 0.01, M).astype(np.float32)
+    W = m.weight(m.W_W4, N, K, ctx.upload(codes), scale=ctx.upload(sw), srel=ctx.upload(srel), codebook=ctx.upload(cb))
+    grid = orc.w4_decode(codes, srel, cb, N, K)
+    assert grid.min() == -127 or grid.max() == 127  # the clamp is exercised
+    dout, dacc = ctx.empty((M, N)), ctx.empty((M, N), np.int32)
+    ctx.linear(W, M, dout, xq=ctx.upload(qx), xs=ctx.upload(sx), acc_out=dacc)
+    acc, got = dacc.numpy(), dout.numpy()
+    assert checksums_ok(qx, grid, acc), "int32 accumulator checksums"
+    rows = np.unique(np.concatenate([np.arange(0, 4), rng.choice(M, 16, replace=False), np.arange(M - 4, M)]))
+    ref_acc = orc.gemm_i8(qx[rows], grid)
+    assert np.array_equal(acc[rows], ref_acc)
+    assert np.array_equal(got[rows], orc.linear_epilogue(ref_acc, sx[rows], sw))
 
 
 @pytest.mark.parametrize("act,epi", [("gelu", 0), ("silu", 1)])
