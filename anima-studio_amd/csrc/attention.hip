@@ -60,29 +60,61 @@ __device__ __forceinline__ bf16 cvt<bf16>(float x) { return (bf16)x; }
 template <>
 __device__ __forceinline__ float cvt<float>(float x) { return x; }
 
-// grid (Lkp/64, Hkv, B), 256 threads.
+// grid (Hkv, Lkp/64, B), 256 threads.  Every thread issues all of its K and V loads first (one
+// memory round trip per workgroup instead of one for K and then one for V).
 template <typename T, bool NORM, bool ROPE>
 __global__ __launch_bounds__(256) void attn_prep_kv(PrepArgs a) {
   constexpr int VSP = BK + (sizeof(T) == 2 ? 2 : 4);  // padded LDS row (keys) of the V transpose
   __shared__ T vs[HD * VSP];
   const int t = threadIdx.x;
-  const int kb0 = blockIdx.x * BK, hk = blockIdx.y, b = blockIdx.z;
+  const int kb0 = blockIdx.y * BK, hk = blockIdx.x, b = blockIdx.z;
   const int64_t head_row0 = ((int64_t)b * a.Hkv + hk) * a.Lkp;
 
-  // ---- K: thread = (row t/4, quarter t%4); quarter p owns dims [16p,16p+16) and +64
+  // V rows of this thread: dim group g -> dims 8g..8g+7, token group tg -> tokens 4tg..4tg+3
+  const int g = (t & 7) | (((t >> 5) & 1) << 3), tg = ((t >> 3) & 3) | ((t >> 6) << 2);
+  // Loads are unconditional (rows past Lk read row Lk-1, then count as zero), so they issue
+  // back to back instead of one branch (and one wait) per row.
+  float e[4][8];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int l = kb0 + 4 * tg + j;
+    const float* src = a.v + (int64_t)b * a.v_bs + (int64_t)min(l, a.Lk - 1) * a.ldv + hk * HD + 8 * g;
+    const float4 lo = *(const float4*)src, hi = *(const float4*)(src + 4);
+    e[j][0] = lo.x; e[j][1] = lo.y; e[j][2] = lo.z; e[j][3] = lo.w;
+    e[j][4] = hi.x; e[j][5] = hi.y; e[j][6] = hi.z; e[j][7] = hi.w;
+  }
+
+  // ---- K: thread = (row t/4, quarter t%4); quarter p owns dims [16p,16p+16) and +64.  The row,
+  // its norm weights and its RoPE table entries are loaded here too, then a scheduling fence
+  // keeps every load of the thread ahead of the first wait.
   {
     const int r = t >> 2, p = t & 3, l = kb0 + r;
-    float x[32];
-    if (l < a.Lk) {
-      const float* src = a.k + (int64_t)b * a.k_bs + (int64_t)l * a.ldk + hk * HD;
+    float x[32], w[32], cv[16], sv[16];
+    {
+      const float* src = a.k + (int64_t)b * a.k_bs + (int64_t)min(l, a.Lk - 1) * a.ldk + hk * HD;
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        float4 lo = *(const float4*)(src + 16 * p + 4 * j);
-        float4 hi = *(const float4*)(src + 64 + 16 * p + 4 * j);
-        x[4 * j] = lo.x; x[4 * j + 1] = lo.y; x[4 * j + 2] = lo.z; x[4 * j + 3] = lo.w;
-        x[16 + 4 * j] = hi.x; x[16 + 4 * j + 1] = hi.y; x[16 + 4 * j + 2] = hi.z; x[16 + 4 * j + 3] = hi.w;
+        *(float4*)(x + 4 * j) = *(const float4*)(src + 16 * p + 4 * j);
+        *(float4*)(x + 16 + 4 * j) = *(const float4*)(src + 64 + 16 * p + 4 * j);
       }
-    } else {
+    }
+    if (NORM) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        *(float4*)(w + 4 * j) = *(const float4*)(a.kn + 16 * p + 4 * j);
+        *(float4*)(w + 16 + 4 * j) = *(const float4*)(a.kn + 64 + 16 * p + 4 * j);
+      }
+    }
+    if (ROPE) {
+      const float* cr = a.cs + (int64_t)min(l, a.Lk - 1) * (HD / 2) + 16 * p;  // rows of 64, 16-byte aligned
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        *(float4*)(cv + 4 * j) = *(const float4*)(cr + 4 * j);
+        *(float4*)(sv + 4 * j) = *(const float4*)(cr + a.sin_off + 4 * j);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (l >= a.Lk) {
 #pragma unroll
       for (int i = 0; i < 32; i++) x[i] = 0.0f;
     }
@@ -93,12 +125,6 @@ __global__ __launch_bounds__(256) void attn_prep_kv(PrepArgs a) {
       ss += __shfl_xor(ss, 1);
       ss += __shfl_xor(ss, 2);
       const float rn = 1.0f / sqrtf(ss / (float)HD + a.eps);
-      float w[32];  // norm weights of dims 16p.. and 64+16p.., as 16-byte loads
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        *(float4*)(w + 4 * j) = *(const float4*)(a.kn + 16 * p + 4 * j);
-        *(float4*)(w + 16 + 4 * j) = *(const float4*)(a.kn + 64 + 16 * p + 4 * j);
-      }
 #pragma unroll
       for (int i = 0; i < 16; i++) {
         x[i] = x[i] * rn * w[i];
@@ -106,13 +132,6 @@ __global__ __launch_bounds__(256) void attn_prep_kv(PrepArgs a) {
       }
     }
     if (ROPE && l < a.Lk) {
-      const float* cr = a.cs + (int64_t)l * (HD / 2) + 16 * p;
-      float cv[16], sv[16];  // 16-byte loads (the table is 16-byte aligned, rows of 64)
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        *(float4*)(cv + 4 * j) = *(const float4*)(cr + 4 * j);
-        *(float4*)(sv + 4 * j) = *(const float4*)(cr + a.sin_off + 4 * j);
-      }
 #pragma unroll
       for (int i = 0; i < 16; i++) {
         const float c = cv[i], s = sv[i];
@@ -145,23 +164,16 @@ __global__ __launch_bounds__(256) void attn_prep_kv(PrepArgs a) {
     }
   }
 
-  // ---- V: thread = (dim group g -> dims 8g..8g+7, token group tg -> tokens 4tg..4tg+3); each
-  // half-wave holds dim groups 0-7 or 8-15 and four token groups, so with the 66-element LDS rows
-  // its 8-byte writes (four tokens of one dim) cover all 64 banks once.
+  // ---- V (loaded above): each half-wave holds dim groups 0-7 or 8-15 and four token groups, so
+  // with the 66-element LDS rows its 8-byte writes (four tokens of one dim) cover all 64 banks
+  // once.
   {
-    const int g = (t & 7) | (((t >> 5) & 1) << 3), tg = ((t >> 3) & 3) | ((t >> 6) << 2);
-    float e[4][8];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const int l = kb0 + 4 * tg + j;
-      float4 lo = make_float4(0, 0, 0, 0), hi = lo;
-      if (l < a.Lk) {
-        const float* src = a.v + (int64_t)b * a.v_bs + (int64_t)l * a.ldv + hk * HD + 8 * g;
-        lo = *(const float4*)src;
-        hi = *(const float4*)(src + 4);
+      if (kb0 + 4 * tg + j >= a.Lk) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) e[j][i] = 0.0f;
       }
-      e[j][0] = lo.x; e[j][1] = lo.y; e[j][2] = lo.z; e[j][3] = lo.w;
-      e[j][4] = hi.x; e[j][5] = hi.y; e[j][6] = hi.z; e[j][7] = hi.w;
     }
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -966,6 +978,7 @@ static int attention_check(anima_ctx* c, const anima_attn_desc* d, int (&kv_len)
   if (d->D != HD) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: head dim %d (this build implements D=128, the DiT head size, and D=64 by padding)", d->D);
   if (d->B < 1 || d->B > MAXB) return fail(c, ANIMA_E_ARG, "anima_attention: B=%d outside [1,%d]", d->B, MAXB);
   if (d->Lq < 1 || d->Lk < 1 || d->H < 1) return fail(c, ANIMA_E_ARG, "anima_attention: Lq=%d Lk=%d H=%d must be >= 1", d->Lq, d->Lk, d->H);
+  if (d->Lk > (1 << 22)) return fail(c, ANIMA_E_ARG, "anima_attention: Lk=%d (at most %d keys)", d->Lk, 1 << 22);
   if (d->H % group) return fail(c, ANIMA_E_ARG, "anima_attention: H=%d not a multiple of group=%d", d->H, group);
   const bool prepared = d->kv_prep != nullptr;
   if (!d->q || !d->o || (!prepared && (!d->k || !d->v))) return fail(c, ANIMA_E_ARG, "anima_attention: null q/k/v/o");
@@ -1037,7 +1050,7 @@ static int prep_kv_launch(anima_ctx* c, const anima_attn_desc* d, void* dst) {
   {
     const double bytes = (double)d->B * Hkv * d->Lk * HD * 4 * 2 + 2.0 * plane;
     Launch L(c, bf ? "attn.prep_kv_bf16" : "attn.prep_kv_fp32", 0.0, bytes);
-    dim3 grid(Lkp / BK, Hkv, d->B);
+    dim3 grid(Hkv, Lkp / BK, d->B);  // heads fastest: concurrent workgroups read whole K / V rows
     const bool kn = d->k_norm != nullptr;
 #define PREP(T, N, R) hipLaunchKernelGGL((attn_prep_kv<T, N, R>), grid, dim3(256), 0, c->stream, p)
     if (bf) {

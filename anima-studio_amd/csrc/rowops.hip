@@ -689,7 +689,9 @@ __global__ __launch_bounds__(256) void copy4_kernel(const float4* A, float4* Y, 
     Y[i] = A ? A[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
-static unsigned grid_for(int64_t n) { return (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, 8192)); }
+// Grid of the grid-stride element kernels: at most 1024 workgroups (4 per CU), where a 16-byte
+// copy moved the most bytes per second (fewer, longer-lived waves than one per 256 elements).
+static unsigned grid_for(int64_t n) { return (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, 1024)); }
 
 int hadamard_launch(anima_ctx* c, const float* x, float* y, int64_t n) {
   if (!x || !y) return fail(c, ANIMA_E_ARG, "anima_hadamard: null pointer");

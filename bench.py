@@ -178,10 +178,18 @@ def self_attention_case(m, ctx, np, B, Hp, Wp, precision, reps):
     flops = 4.0 * B * H * L * L * D
     kname = [k for k in per if k.startswith("attn.flash")][0]
     peak = BF16_PEAK_TFLOPS if precision == "bf16" else FP32_PEAK_TFLOPS
-    return {"B": B, "tokens": L, "heads": H, "precision": precision, "ms": round(total, 5),
-            "TFLOP/s": round(flops / total / 1e9, 1), "kernel": kname, "kernel_ms": round(per[kname], 5),
-            "kernel_TFLOP/s": round(flops / per[kname] / 1e9, 1), "peak_TFLOP/s": peak,
-            "frac": round(flops / per[kname] / 1e9 / peak, 4), "op_frac": round(flops / total / 1e9 / peak, 4)}
+    res = {"B": B, "tokens": L, "heads": H, "precision": precision, "ms": round(total, 5),
+           "TFLOP/s": round(flops / total / 1e9, 1), "kernel": kname, "kernel_ms": round(per[kname], 5),
+           "kernel_TFLOP/s": round(flops / per[kname] / 1e9, 1), "peak_TFLOP/s": peak,
+           "frac": round(flops / per[kname] / 1e9 / peak, 4), "op_frac": round(flops / total / 1e9 / peak, 4)}
+    pname = [k for k in per if k.startswith("attn.prep_kv")]
+    if pname:
+        # K/V prep: reads K and V (fp32), writes normed + rotated K and V^T in the MFMA type
+        pbytes = B * L * H * D * (4 + 4 + 2 * (2 if precision == "bf16" else 4))
+        res.update({"prep_kernel": pname[0], "prep_ms": round(per[pname[0]], 5), "prep_MB": round(pbytes / 1e6, 1),
+                    "prep_GB/s": round(pbytes / per[pname[0]] / 1e6, 1),
+                    "prep_frac_hbm": round(pbytes / per[pname[0]] / 1e6 / HBM_PEAK_GBS, 4)})
+    return res
 
 
 def cross_attention(m, ctx, np, reps):
@@ -250,7 +258,23 @@ def prepasses(m, ctx, np, reps):
                      "GB/s": round(nbytes / kms / 1e6, 1), "frac_hbm": round(nbytes / kms / 1e6 / HBM_PEAK_GBS, 4)}
     for b in bufs:
         b.release()
+    out["hbm_copy"] = hbm_copy(ctx, reps)
     return out
+
+
+def hbm_copy(ctx, reps, mib=512):
+    """What a plain 16-byte copy kernel moves on this device (the library's elementwise copy, 512 MiB
+    read + 512 MiB written): the practical HBM ceiling the passes above are read against."""
+    n = mib * (1 << 20) // 4
+    a, b = ctx.empty(n), ctx.empty(n)
+    ctx.zero(a, n)
+    _, per, _ = timed_kernels(ctx, lambda: ctx.elementwise("copy", a, None, b, n), reps)
+    a.release()
+    b.release()
+    ms = per["elementwise.copy"]
+    nbytes = 2 * n * 4
+    return {"MB": round(nbytes / 1e6, 1), "ms": round(ms, 5), "GB/s": round(nbytes / ms / 1e6, 1),
+            "frac_hbm": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
 
 
 LINEAR_SHAPES = (("qkv", 6144, 2048, "store"), ("out", 2048, 2048, "gated"), ("mlp1", 8192, 2048, "gelu"),

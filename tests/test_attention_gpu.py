@@ -448,8 +448,13 @@ def test_attention_rejects_bad_arguments(ctx):
     m = amd()
     d = ctx.empty((64, 3 * 128))
     base = dict(q=d, k=d, v=d, o=d, B=1, Lq=64, Lk=64, H=1, D=128, ldq=384, ldk=384, ldv=384, ldo=384)
+    # head dims outside {64, 128} run on the chunked path, which takes D % 4 == 0 and no fused
+    # norm / RoPE
     with pytest.raises(m.AnimaError) as e:
-        ctx.attention(**{**base, "D": 96, "ldo": 384})
+        ctx.attention(**{**base, "D": 90, "ldo": 384})
+    assert e.value.code == -5
+    with pytest.raises(m.AnimaError) as e:
+        ctx.attention(**{**base, "D": 96, "q_norm": d})
     assert e.value.code == -5
     with pytest.raises(m.AnimaError) as e:
         ctx.attention(**{**base, "ldq": 386})
