@@ -975,7 +975,7 @@ static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // Argument checks of anima_attention (fills kv_len[] with the valid key counts).
 static int attention_check(anima_ctx* c, const anima_attn_desc* d, int (&kv_len)[MAXB]) {
   const int group = d->group <= 0 ? 1 : d->group;
-  if (d->D != HD) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: head dim %d (this build implements D=128, the DiT head size, and D=64 by padding)", d->D);
+  if (d->D != HD) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: head dim %d on the flash kernels (D=128 only)", d->D);
   if (d->B < 1 || d->B > MAXB) return fail(c, ANIMA_E_ARG, "anima_attention: B=%d outside [1,%d]", d->B, MAXB);
   if (d->Lq < 1 || d->Lk < 1 || d->H < 1) return fail(c, ANIMA_E_ARG, "anima_attention: Lq=%d Lk=%d H=%d must be >= 1", d->Lq, d->Lk, d->H);
   if (d->Lk > (1 << 22)) return fail(c, ANIMA_E_ARG, "anima_attention: Lk=%d (at most %d keys)", d->Lk, 1 << 22);
@@ -1071,89 +1071,12 @@ static int prep_kv_launch(anima_ctx* c, const anima_attn_desc* d, void* dst) {
   return ANIMA_OK;
 }
 
-// Head dim 64 (the LLM adapter's attention, app/models/dit.js:147-160) on the 128-dim kernels:
-// heads zero-padded to 128 dims.  Zero dims add nothing to q . k, and the padded V dims only
-// produce output dims that are dropped; the scale stays that of D = 64.
-__global__ __launch_bounds__(256) void pad_heads_kernel(const float* src, int64_t ld, int64_t off, int64_t bs, int L, int H,
-                                                        float* dst, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    const int d = (int)(i & 127);
-    const int64_t r = i >> 7;  // (b, row, h)
-    const int h = (int)(r % H);
-    const int64_t br = r / H, b = br / L, row = br - b * L;
-    dst[i] = d < 64 ? src[b * bs + row * ld + off + h * 64 + d] : 0.0f;
-  }
-}
-
-__global__ __launch_bounds__(256) void unpad_heads_kernel(const float* src, int L, int H, float* dst, int64_t ld, int64_t off,
-                                                          int64_t bs, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    const int d = (int)(i & 63);
-    const int64_t r = i >> 6;
-    const int h = (int)(r % H);
-    const int64_t br = r / H, b = br / L, row = br - b * L;
-    dst[b * bs + row * ld + off + h * 64 + d] = src[r * 128 + d];
-  }
-}
-
-static int attention_d64(anima_ctx* c, const anima_attn_desc* d) {
-  if (d->q_norm || d->k_norm || d->rope_cs || d->kv_prep)
-    return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: D=64 takes no fused norm / RoPE / prepared K/V");
-  if (d->B < 1 || d->B > MAXB || d->Lq < 1 || d->Lk < 1 || d->H < 1 || !d->q || !d->k || !d->v || !d->o)
-    return fail(c, ANIMA_E_ARG, "anima_attention: bad D=64 descriptor");
-  const int group = d->group <= 0 ? 1 : d->group;
-  if (d->H % group) return fail(c, ANIMA_E_ARG, "anima_attention: H=%d not a multiple of group=%d", d->H, group);
-  const int Hkv = d->H / group;
-  const int64_t ldo = d->ldo ? d->ldo : (int64_t)d->H * 64;
-  if (d->ldq < (int64_t)d->H * 64 || d->ldk < (int64_t)Hkv * 64 || d->ldv < (int64_t)Hkv * 64 || ldo < (int64_t)d->H * 64)
-    return fail(c, ANIMA_E_ARG, "anima_attention: D=64 leading dimensions below the heads' width");
-  const int64_t nq = (int64_t)d->B * d->Lq * d->H * 128, nk = (int64_t)d->B * d->Lk * Hkv * 128;
-  void* buf = nullptr;
-  int rc = anima_alloc(c, (size_t)(2 * nq + 2 * nk) * 4, &buf);
-  if (rc) return rc;
-  float* qp = (float*)buf;
-  float* kp = qp + nq;
-  float* vp = kp + nk;
-  float* op = vp + nk;
-  auto grid = [](int64_t n) { return dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)); };
-  {
-    Launch L(c, "attn.pad_d64", 0.0, (double)(nq + 2 * nk) * 6);
-    hipLaunchKernelGGL(pad_heads_kernel, grid(nq), dim3(256), 0, c->stream, d->q, d->ldq, d->q_off, d->q_bstride, d->Lq,
-                       d->H, qp, nq);
-    hipLaunchKernelGGL(pad_heads_kernel, grid(nk), dim3(256), 0, c->stream, d->k, d->ldk, d->k_off, d->k_bstride, d->Lk,
-                       Hkv, kp, nk);
-    hipLaunchKernelGGL(pad_heads_kernel, grid(nk), dim3(256), 0, c->stream, d->v, d->ldv, d->v_off, d->v_bstride, d->Lk,
-                       Hkv, vp, nk);
-    rc = L.end();
-  }
-  if (!rc) {
-    anima_attn_desc p = *d;
-    p.D = 128;
-    p.q = qp, p.ldq = (int64_t)d->H * 128, p.q_off = 0, p.q_bstride = (int64_t)d->Lq * d->H * 128;
-    p.k = kp, p.ldk = (int64_t)Hkv * 128, p.k_off = 0, p.k_bstride = (int64_t)d->Lk * Hkv * 128;
-    p.v = vp, p.ldv = (int64_t)Hkv * 128, p.v_off = 0, p.v_bstride = (int64_t)d->Lk * Hkv * 128;
-    p.o = op, p.ldo = (int64_t)d->H * 128, p.o_off = 0, p.o_bstride = (int64_t)d->Lq * d->H * 128;
-    p.scale = d->scale != 0.0f ? d->scale : 0.125f;  // 1 / sqrt(64)
-    rc = attention_launch(c, &p);
-  }
-  if (!rc) {
-    Launch L(c, "attn.unpad_d64", 0.0, (double)nq * 3);
-    const int64_t no = nq / 2;
-    hipLaunchKernelGGL(unpad_heads_kernel, grid(no), dim3(256), 0, c->stream, op, d->Lq, d->H, d->o, ldo, d->o_off,
-                       d->o_bstride ? d->o_bstride : (int64_t)d->Lq * ldo, no);
-    rc = L.end();
-  }
-  anima_free(c, buf);  // stream-ordered reuse
-  return rc;
-}
-
 int attention_launch(anima_ctx* c, const anima_attn_desc* d) { return attention_launch_ws(c, d, nullptr); }
 
 // scratch != nullptr: the K/V prep goes there (the caller checked its size) instead of the
 // context's workspace.
 int attention_launch_ws(anima_ctx* c, const anima_attn_desc* d, void* scratch) {
-  if (d->D == 64) return attention_d64(c, d);
-  if (d->D != HD) {  // the chunked path (app/gpu/ops.js:177-207)
+  if (d->D != HD) {  // the chunked path (app/gpu/ops.js:177-207), e.g. the adapter's D = 64
     if (scratch) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention_noalloc: head dim %d", d->D);
     int rc = attention_chunked_check(c, d);
     if (rc) return rc;

@@ -4,9 +4,9 @@
 //     of app/gpu/gemm.js:56-80, dispatched by ops.conv3x3 / conv3x3Into, app/gpu/ops.js:95-109);
 //   * the Wan channel norm y = x / max(||x||, 1e-12) * sqrt(C) * gamma (+ SiLU) of
 //     app/gpu/kernels.js:62-89 (mode 1), in the shader's reduction order;
-//   * attention for head dims other than 64 and 128 (the VAE's single 384-dim head), on the
-//     reference's chunked path (app/gpu/ops.js:177-207): scores for a chunk of query rows, a row
-//     softmax, then P.V.
+//   * attention for head dims other than 128 (the LLM adapter's 64, the VAE's single 384-dim head),
+//     on the reference's chunked path (app/gpu/ops.js:177-207): scores for a chunk of query rows, a
+//     row softmax (optionally causal), then P.V.
 //
 // The GEMM: C[m][n] = alpha * sum_k A[m][k] B[n][k] (* rs[m]) (+ bias[n]) (act), stored or added
 // to C.  One workgroup = 4 waves = a 128 x 128 output tile, each wave 64 x 64 (2 x 2 tiles of
@@ -382,15 +382,18 @@ int to_rgba_launch(anima_ctx* c, const float* x, int64_t n, uint8_t* out) {
 // ---- attention on the chunked path (head dims other than 64 / 128)
 
 // In place on row r of S (row stride ld), columns [0, cols): e = exp(s * scale - m), m the maximum of
-// s * scale over the first `valid` columns, 0 past them; rl[r] = 1 / sum of e (the P.V product's row
-// scale).  One workgroup per row.
+// s * scale over the row's first `lim` columns, 0 past them; rl[r] = 1 / sum of e (the P.V
+// product's row scale).  lim = valid, or with the causal mask (app/gpu/kernels.js:49,
+// limit = min(cols, row + 1)) min(valid, q + 1) for the row's query index q = row0 + r.  One
+// workgroup per row.
 __global__ __launch_bounds__(256) void chunk_softmax_kernel(float* S, int64_t ld, float* rl, int cols, int valid,
-                                                            float scale) {
+                                                            float scale, int row0, int causal) {
   __shared__ float red[4];
   float* s = S + (int64_t)blockIdx.x * ld;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int lim = causal ? min(valid, row0 + (int)blockIdx.x + 1) : valid;
   float mx = -INFINITY;
-  for (int c = t; c < valid; c += 256) mx = fmaxf(mx, s[c] * scale);
+  for (int c = t; c < lim; c += 256) mx = fmaxf(mx, s[c] * scale);
   mx = wave_max(mx);
   if (lane == 0) red[wave] = mx;
   __syncthreads();
@@ -398,7 +401,7 @@ __global__ __launch_bounds__(256) void chunk_softmax_kernel(float* S, int64_t ld
   __syncthreads();
   float sum = 0.0f;
   for (int c = t; c < cols; c += 256) {
-    const float e = c < valid ? expf(s[c] * scale - mx) : 0.0f;
+    const float e = c < lim ? expf(s[c] * scale - mx) : 0.0f;
     s[c] = e;
     sum += e;
   }
@@ -424,13 +427,13 @@ __global__ __launch_bounds__(256) void transpose_kernel(const float* src, int64_
   }
 }
 
-// Checks of the chunked path: plain attention (no fused norm / RoPE, no prepared K/V, not causal)
-// with 16-byte aligned rows, D % 4 == 0.
+// Checks of the chunked path: plain attention (no fused norm / RoPE, no prepared K/V; causal mask
+// allowed) with 16-byte aligned rows, D % 4 == 0.
 int attention_chunked_check(anima_ctx* c, const anima_attn_desc* d) {
   if (d->D < 4 || d->D % 4 || d->D > 4096)
     return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: head dim %d (the chunked path takes D %% 4 == 0, D <= 4096)", d->D);
-  if (d->q_norm || d->k_norm || d->rope_cs || d->kv_prep || d->causal)
-    return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: head dim %d takes no fused norm / RoPE, prepared K/V or causal mask", d->D);
+  if (d->q_norm || d->k_norm || d->rope_cs || d->kv_prep)
+    return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: head dim %d takes no fused norm / RoPE or prepared K/V", d->D);
   if (d->precision != ANIMA_PREC_BF16 && d->precision != ANIMA_PREC_FP32)
     return fail(c, ANIMA_E_ARG, "anima_attention: unknown precision %d", d->precision);
   const int group = d->group <= 0 ? 1 : d->group;
@@ -498,7 +501,8 @@ int attention_chunked_launch(anima_ctx* c, const anima_attn_desc* d, const int* 
         if ((rc = tgemm_launch(c, qk, TG_A_ROWS, TG_B_F32, split, 1, "attn.chunk.qk", 2.0 * nr * Lk * D))) return rc;
         {
           Launch ls(c, "attn.chunk.softmax", 0.0, 8.0 * nr * Lk);
-          hipLaunchKernelGGL(chunk_softmax_kernel, dim3(nr), dim3(256), 0, c->stream, S, ldk4, L, Lk, valid, scale);
+          hipLaunchKernelGGL(chunk_softmax_kernel, dim3(nr), dim3(256), 0, c->stream, S, ldk4, L, Lk, valid, scale, r0,
+                             d->causal ? 1 : 0);
           if ((rc = ls.end())) return rc;
         }
         TGemmArgs pv{};

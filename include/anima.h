@@ -101,10 +101,9 @@ int anima_graph_destroy(anima_ctx* ctx, anima_graph* graph);
 #define ANIMA_PREC_FP32 1 /* fp32 MFMA (tolerance variant) */
 
 typedef struct {
-  int B, Lq, Lk, H, D; /* D == 128 (flash kernels); D == 64 (the LLM adapter's heads, zero-padded to
-                        * 128 inside the call); other D % 4 == 0 (the VAE's 384) on the chunked path
-                        * of app/gpu/ops.js:177-207.  Fused norm / RoPE, prepared K/V and the causal
-                        * mask need D == 128. */
+  int B, Lq, Lk, H, D; /* D == 128 (flash kernels); other D % 4 == 0 (the LLM adapter's 64, the VAE's
+                        * 384) on the chunked path of app/gpu/ops.js:177-207, causal mask included.
+                        * Fused norm / RoPE and prepared K/V need D == 128. */
   int group;           /* q heads per kv head (1 = MHA); 0 is read as 1 */
   const float* q;
   int64_t ldq, q_off, q_bstride;

@@ -261,8 +261,8 @@ def test_causal_gqa_attention(ctx, L, B, precision):
 @pytest.mark.parametrize("precision", ["bf16", "fp32"])
 def test_head_dim_64_attention(ctx, precision):
     """D = 64, the LLM adapter's attention (app/models/dit.js:147-160: 16 heads x 64 in 1024
-    columns; its cross-attention to the text encoder's tokens): heads zero-padded to 128 inside the
-    call, scale 1/8, against the oracle at D = 64 (self Lq = Lk = 77 and cross Lq = 32, Lk = 100)."""
+    columns; its cross-attention to the text encoder's tokens) on the chunked path at D = 64 (no
+    padding), scale 1/8, against the oracle (self Lq = Lk = 77 and cross Lq = 32, Lk = 100)."""
     case(f"attention D=64 {precision}")
     m = amd()
     H, D = 16, 64

@@ -96,7 +96,7 @@ def test_conv3x3_matches_float64(case, precision):
 ATTN_CASES = [  # B, Lq, Lk, H, group, D, kv_len
     (1, 300, 300, 1, 1, 384, None),
     (2, 256, 200, 2, 2, 384, [200, 77]),
-    (1, 2304, 16384, 1, 1, 384, None),  # three score chunks of 1024 / 1024 / 256 rows
+    (1, 2304, 16384, 1, 1, 384, None),  # one 2304 x 16384 score chunk
     (1, 96, 150, 3, 1, 96, None),
 ]
 
@@ -130,6 +130,80 @@ def test_chunked_attention_matches_float64(case, precision):
             ref = (torch.softmax(qh @ kh.T / math.sqrt(D), -1) @ vh).numpy()
             r, _ = report(f"chunked attention b={b} h={h} {precision} vs float64", got[b, :, h * D:(h + 1) * D], ref)
             assert r <= (2e-5 if precision == "fp32" else 1e-2)
+
+
+def _attn_rows_f64(q, k, v, rows, D, causal, n=None):
+    """float64 softmax(q k^T / sqrt(D)) v for the given query rows of one head (keys < n; with
+    causal, keys <= row as well)."""
+    n = k.shape[0] if n is None else n
+    out = []
+    for i in rows:
+        lim = min(n, i + 1) if causal else n
+        s = (k[:lim].astype(np.float64) @ q[i].astype(np.float64)) / math.sqrt(D)
+        p = np.exp(s - s.max())
+        out.append(p @ v[:lim].astype(np.float64) / p.sum())
+    return np.array(out)
+
+
+@pytest.mark.parametrize("D", [64, 96])
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_chunked_attention_causal_gqa(D, precision):
+    """The causal mask on the chunked path (app/gpu/ops.js:196, kernels.js:49: limit =
+    min(cols, row + 1)), with GQA (4 query heads over 2 kv heads), B = 2 with a ragged valid key
+    length, and Lq != Lk: every query row against a float64 restatement."""
+    m = amd()
+    B, Lq, Lk, H, group = 2, 150, 190, 4, 2
+    Hk = H // group
+    kv_len = [190, 120]
+    rng = np.random.default_rng(D)
+    q = rng.standard_normal((B, Lq, H * D)).astype(np.float32)
+    k = rng.standard_normal((B, Lk, Hk * D)).astype(np.float32)
+    v = rng.standard_normal((B, Lk, Hk * D)).astype(np.float32)
+    prec = m.PREC_FP32 if precision == "fp32" else m.PREC_BF16
+    print(f"[case] chunked causal GQA attention D={D} {precision}", flush=True)
+    with m.Context() as ctx:
+        dq, dk, dv, do = ctx.upload(q), ctx.upload(k), ctx.upload(v), ctx.empty((B, Lq, H * D))
+        ctx.attention(q=dq, k=dk, v=dv, o=do, B=B, Lq=Lq, Lk=Lk, H=H, D=D, ldq=H * D, ldk=Hk * D, ldv=Hk * D,
+                      group=group, kv_len=kv_len, precision=prec, causal=1)
+        got = do.numpy()
+        for b_ in (dq, dk, dv, do):
+            b_.release()
+    for b in range(B):
+        for h in range(H):
+            hk = h // group
+            sl, kl = slice(h * D, (h + 1) * D), slice(hk * D, (hk + 1) * D)
+            ref = _attn_rows_f64(q[b, :, sl], k[b, :, kl], v[b, :, kl], range(Lq), D, True, kv_len[b])
+            r, _ = report(f"causal b={b} h={h} D={D} {precision} vs float64", got[b, :, sl], ref)
+            assert r <= (2e-5 if precision == "fp32" else 1e-2)
+    # query 0 sees key 0 only
+    for h in range(H):
+        hk = h // group
+        assert np.allclose(got[:, 0, h * D:(h + 1) * D], v[:, 0, hk * D:(hk + 1) * D], rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_chunked_attention_two_score_chunks(causal):
+    """Lq = 4500 queries over Lk = 65536 keys: 4096 score rows fit the 1 GiB chunk, so the product
+    runs in two chunks (4096 + 404 rows).  Rows on both sides of the boundary and the last ones
+    against float64, plain and causal (the causal limit follows the absolute query index)."""
+    m = amd()
+    B, Lq, Lk, H, D = 1, 4500, 65536, 1, 8
+    rng = np.random.default_rng(7 + causal)
+    q = rng.standard_normal((Lq, D)).astype(np.float32)
+    k = rng.standard_normal((Lk, D)).astype(np.float32)
+    v = rng.standard_normal((Lk, D)).astype(np.float32)
+    print(f"[case] chunked attention two score chunks causal={causal}", flush=True)
+    with m.Context() as ctx:
+        dq, dk, dv, do = ctx.upload(q), ctx.upload(k), ctx.upload(v), ctx.empty((Lq, D))
+        ctx.attention(q=dq, k=dk, v=dv, o=do, B=B, Lq=Lq, Lk=Lk, H=H, D=D, ldq=D, ldk=D, ldv=D,
+                      precision=m.PREC_FP32, causal=causal)
+        got = do.numpy()
+        for b_ in (dq, dk, dv, do):
+            b_.release()
+    rows = [0, 1, 2, 4094, 4095, 4096, 4097, Lq - 2, Lq - 1]
+    ref = _attn_rows_f64(q, k, v, rows, D, bool(causal))
+    r, _ = report(f"two chunks causal={causal} vs float64", got[rows], ref)
+    assert r <= 2e-5
 
 
 @pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")
