@@ -124,6 +124,7 @@ def lib():
         L.anima_patchify.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]
         L.anima_unpatchify.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]
         L.anima_linear.argtypes = [_vp, ctypes.POINTER(LinearDesc)]
+        L.anima_weight_unpack_w4.argtypes = [_vp, ctypes.POINTER(Weight), _vp]
         L.anima_sampler_step.argtypes = [_vp, ctypes.POINTER(SamplerDesc)]
         L.anima_split3_bf16.argtypes = [_vp, _vp, _vp, _i64]
         L.anima_attention_noalloc.argtypes = [_vp, ctypes.POINTER(AttnDesc)]
@@ -354,6 +355,10 @@ class Context:
                        epilogue=epilogue, gate=_ptr(gate), gate_off=gate_off, acc_out=_ptr(acc_out), add=_ptr(add),
                        ld_add=ld_add)
         return self._check(lib().anima_linear(self.h, ctypes.byref(d)))
+
+    def weight_unpack_w4(self, W, grid):
+        """The int8 grid [N][K] of a W4 weight (anima_weight_unpack_w4)."""
+        return self._check(lib().anima_weight_unpack_w4(self.h, ctypes.byref(W), _ptr(grid)))
 
     def split3_bf16(self, src, dst, n):
         return self._check(lib().anima_split3_bf16(self.h, _ptr(src), _ptr(dst), n))

@@ -688,6 +688,57 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
 #undef G2_RSRC
 #undef G2_RSRC_C
 
+// ------------------------------------------------------------------ W4 -> int8 grid (load time)
+//
+// Thread = 32 weights of a row: 16 code bytes (low nibble = even k) and their two s_rel bytes;
+// the 16-entry tables of all 256 s_rel values are built in LDS per workgroup as in the GEMMs.
+__global__ __launch_bounds__(256) void w4_unpack_kernel(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ srel,
+                                                        const float* __restrict__ cb, int8_t* __restrict__ out, int64_t nchunk,
+                                                        int K) {
+  __shared__ __attribute__((aligned(16))) uint32_t lut[256 * 4];
+  for (int i = threadIdx.x; i < 256 * 4; i += 256) {
+    const float s = fp8e4m3((uint32_t)(i >> 2));
+    uint32_t packed = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float v = rintf(cb[4 * (i & 3) + j] * s);
+      v = fminf(fmaxf(v, -127.0f), 127.0f);
+      packed |= ((uint32_t)(int32_t)v & 0xffu) << (8 * j);
+    }
+    lut[i] = packed;
+  }
+  __syncthreads();
+  const int cpr = K / 32;  // chunks of 32 weights per row
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nchunk; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = i / cpr;
+    const int c = (int)(i - row * cpr);
+    const uint4 w = *(const uint4*)(codes + row * (K / 2) + 16 * c);
+    const uint8_t* sp = srel + row * (K / 16) + 2 * c;
+    const uint4 t0 = *(const uint4*)&lut[4 * sp[0]];
+    const uint4 t1 = *(const uint4*)&lut[4 * sp[1]];
+    const uint2 d0 = decode8(w.x, t0.x, t0.y, t0.z, t0.w), d1 = decode8(w.y, t0.x, t0.y, t0.z, t0.w);
+    const uint2 d2 = decode8(w.z, t1.x, t1.y, t1.z, t1.w), d3 = decode8(w.w, t1.x, t1.y, t1.z, t1.w);
+    uint4* o = (uint4*)(out + row * K + 32 * c);
+    o[0] = make_uint4(d0.x, d0.y, d1.x, d1.y);
+    o[1] = make_uint4(d2.x, d2.y, d3.x, d3.y);
+  }
+}
+
+int weight_unpack_w4_launch(anima_ctx* c, const anima_weight* W, int8_t* grid) {
+  if (!W || !grid) return fail(c, ANIMA_E_ARG, "anima_weight_unpack_w4: null weight or grid");
+  if (W->kind != ANIMA_W_W4) return fail(c, ANIMA_E_ARG, "anima_weight_unpack_w4: weight kind %d is not W4", W->kind);
+  if (!W->w || !W->srel || !W->codebook) return fail(c, ANIMA_E_ARG, "anima_weight_unpack_w4: missing codes / s_rel / codebook");
+  if (W->N < 1 || W->K < 32 || W->K % 32) return fail(c, ANIMA_E_ARG, "anima_weight_unpack_w4: N=%d K=%d (K %% 32 == 0)", W->N, W->K);
+  if (((uintptr_t)W->w & 15) || ((uintptr_t)grid & 15))
+    return fail(c, ANIMA_E_ARG, "anima_weight_unpack_w4: codes and grid must be 16-byte aligned");
+  const int64_t nchunk = (int64_t)W->N * (W->K / 32);
+  Launch L(c, "w4.unpack", 0.0, (double)W->N * W->K * 1.5 + (double)W->N * W->K / 16);
+  const int64_t blocks = (nchunk + 255) / 256;
+  hipLaunchKernelGGL(w4_unpack_kernel, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(256), 0, c->stream,
+                     (const uint8_t*)W->w, W->srel, W->codebook, grid, nchunk, W->K);
+  return L.end();
+}
+
 // ------------------------------------------------------------------ bf16 weights, fp32 math
 
 struct F32WArgs {

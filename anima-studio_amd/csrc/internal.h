@@ -96,6 +96,7 @@ int64_t attention_kv_bytes(int B, int Hkv, int Lk, int precision);
 int conv3x3_launch(anima_ctx* c, const anima_conv_desc* d);
 int channel_norm_launch(anima_ctx* c, const float* x, const float* gamma, float* y, int64_t rows, int cols, int silu);
 int to_rgba_launch(anima_ctx* c, const float* x, int64_t n, uint8_t* out);
+int weight_unpack_w4_launch(anima_ctx* c, const anima_weight* W, int8_t* grid);
 int attention_chunked_check(anima_ctx* c, const anima_attn_desc* d);
 int attention_chunked_launch(anima_ctx* c, const anima_attn_desc* d, const int* kv_len);
 

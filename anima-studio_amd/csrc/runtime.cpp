@@ -435,6 +435,12 @@ int anima_channel_norm(anima_ctx* c, const float* x, const float* gamma, float* 
   return channel_norm_launch(c, x, gamma, y, rows, cols, silu);
 }
 
+int anima_weight_unpack_w4(anima_ctx* c, const anima_weight* w4, int8_t* grid) {
+  CHECK_CTX(c);
+  NOT_CAPTURING(c, "anima_weight_unpack_w4");
+  return weight_unpack_w4_launch(c, w4, grid);
+}
+
 int anima_to_rgba(anima_ctx* c, const float* x, int64_t n, uint8_t* out) {
   CHECK_CTX(c);
   return to_rgba_launch(c, x, n, out);

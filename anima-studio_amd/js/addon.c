@@ -589,21 +589,37 @@ static napi_value js_fill_random(napi_env env, napi_callback_info info) {
 
 /* linear(ctx, W, desc): W = {kind, N, K, w, scale, srel, codebook, bias}, desc mirrors
  * anima_linear_desc (x, ldx, xRotated, xq, xs, out, ldc, alpha, act, epilogue, gate, gOff, accOut) */
+/* the weight object {kindId, N, K, buf, scale, srel, codebook, bias} of ops.mjs weightArg */
+static void read_weight(napi_env env, napi_value wo, anima_weight* w) {
+  memset(w, 0, sizeof *w);
+  w->kind = (int)pnum(env, wo, "kindId");
+  w->N = (int)pnum(env, wo, "N");
+  w->K = (int)pnum(env, wo, "K");
+  w->w = pptr(env, wo, "buf");
+  w->scale = (const float*)pptr(env, wo, "scale");
+  w->srel = (const uint8_t*)pptr(env, wo, "srel");
+  w->codebook = (const float*)pptr(env, wo, "codebook");
+  w->bias = (const float*)pptr(env, wo, "bias");
+}
+
+/* weightUnpackW4(ctx, weight, grid) */
+static napi_value js_weight_unpack_w4(napi_env env, napi_callback_info info) {
+  napi_value a[3];
+  get_args(env, info, 3, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  anima_weight w;
+  read_weight(env, a[1], &w);
+  CHECK_RC(env, c, anima_weight_unpack_w4(c, &w, (int8_t*)ptr(env, a[2])));
+  return NULL;
+}
+
 static napi_value js_linear(napi_env env, napi_callback_info info) {
   napi_value a[3];
   get_args(env, info, 3, a);
   anima_ctx* c = ctx_of(env, a[0]);
   napi_value wo = a[1], o = a[2];
   anima_weight w;
-  memset(&w, 0, sizeof w);
-  w.kind = (int)pnum(env, wo, "kindId");
-  w.N = (int)pnum(env, wo, "N");
-  w.K = (int)pnum(env, wo, "K");
-  w.w = pptr(env, wo, "buf");
-  w.scale = (const float*)pptr(env, wo, "scale");
-  w.srel = (const uint8_t*)pptr(env, wo, "srel");
-  w.codebook = (const float*)pptr(env, wo, "codebook");
-  w.bias = (const float*)pptr(env, wo, "bias");
+  read_weight(env, wo, &w);
   anima_linear_desc d;
   memset(&d, 0, sizeof d);
   d.M = (int64_t)pnum(env, o, "M");
@@ -776,6 +792,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       FN("linear", js_linear), FN("samplerStep", js_sampler_step), FN("attentionKvBytes", js_attention_kv_bytes), FN("split3", js_split3), FN("lastError", js_last_error),
       FN("graphBegin", js_graph_begin), FN("graphEnd", js_graph_end), FN("graphLaunch", js_graph_launch),
       FN("graphDestroy", js_graph_destroy), FN("conv3x3", js_conv3x3), FN("channelNorm", js_channel_norm), FN("toRgba", js_to_rgba),
+      FN("weightUnpackW4", js_weight_unpack_w4),
   };
 #undef FN
   if (napi_define_properties(env, exports, sizeof desc / sizeof desc[0], desc) != napi_ok) return NULL;

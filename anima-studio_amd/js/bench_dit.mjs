@@ -11,6 +11,8 @@
 //                     [--text-encoder N]  (also time Qwen3.encode of N tokens on a 28-layer synthetic
 //                      text encoder: causal GQA attention, bf16 linears)
 //                     [--vae]  (also time the VAE decode of this size's latent, bf16 and fp32 precision)
+//                     [--w4 packed|int8]  (W4 weights unpacked inside each GEMM, or converted to their
+//                      int8 grid once at load: bit-identical products)
 //                     [--graph [--rounds 3]]  (also the forward replayed from a HIP graph recorded
 //                      once, ForwardGraph: graph and eager blocks of --steps steps alternate,
 //                      medians; dit_step_ms stays the eager step, graph_step_ms the replay)
@@ -60,6 +62,10 @@ async function main() {
   const gpu = await GPU.create({ profile });
   const src = new SyntheticWeights(gpu, 1234, { mode, blocks: nBlocks });
   const dit = AnimaDiT.synthetic(gpu, src);
+  // --w4 int8: W4 weights converted to their int8 grid at load (bit-identical products, no
+  // nibble unpack per GEMM; one byte per weight)
+  const w4mode = arg("w4", "packed");
+  const unpacked = w4mode === "int8" ? dit.unpackW4() : 0;
   const ctxs = [0, 1].map((b) => {
     const t = gpu.empty([Lk, 1024]);
     native.fillRandom(gpu.ctx, t.buf, t.size, 4, 77 + b, 1.0, 0.0); // ~N(0,1)
@@ -88,7 +94,7 @@ async function main() {
   }
   const latents = [normals(16 * h * w, 1), normals(16 * h * w, 2)];
   await gpu.sync();
-  process.stderr.write(`bench_dit: model ready (${nBlocks} blocks, ${mode}), ${(gpu.pool.allocated / 2 ** 30).toFixed(2)} GiB\n`);
+  process.stderr.write(`bench_dit: model ready (${nBlocks} blocks, ${mode}, W4 ${w4mode}${unpacked ? `: ${unpacked} linears` : ""}), ${(gpu.pool.allocated / 2 ** 30).toFixed(2)} GiB\n`);
 
   const useGraph = !!arg("graph", false);
   const rounds = Number(arg("rounds", 3));
@@ -156,7 +162,7 @@ async function main() {
   const perBlock = 2 * M * D_(3 * 2048, 2048) + 2 * M * D_(2048, 2048) * 3 + 2 * M * D_(8192, 2048) * 2 +
     4 * B * L * L * 128 * 16 + 4 * B * L * Lk * 128 * 16;
   const flops = nBlocks * perBlock + 2 * M * 2048 * 68 + 2 * M * 64 * 2048;
-  const out = { dit_step_ms: Number(ms.toFixed(3)), step_ms: stepMs.map((x) => Number(x.toFixed(3))), size, blocks: nBlocks,
+  const out = { dit_step_ms: Number(ms.toFixed(3)), step_ms: stepMs.map((x) => Number(x.toFixed(3))), size, blocks: nBlocks, w4: w4mode,
     mode, B, tokens: L, steps, warmup, lora_rank: loraRank, graph: useGraph,
     graph_step_ms: graphMs === null ? null : Number(graphMs.toFixed(3)),
     flops_per_step: flops, tflops: Number((flops / (ms / 1e3) / 1e12).toFixed(2)), finite,

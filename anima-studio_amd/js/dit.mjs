@@ -152,6 +152,24 @@ export class AnimaDiT {
     this.precision = "bf16";
   }
 
+  // Converts every W4 block linear to its int8 grid once (ops.unpackW4): the GEMMs then run on the
+  // int8 path with bit-identical results and no nibble unpack per call, at one byte per weight
+  // (a load-time option for a device with the memory to spare; the packed form is the default).
+  // Returns the number of linears converted.
+  unpackW4() {
+    let n = 0;
+    for (const b of this.blocks) {
+      const Ws = [b.self.qkv, b.self.q, b.self.k, b.self.v, b.self.o, b.cross.q, b.cross.k, b.cross.v, b.cross.o, b.l1, b.l2];
+      for (const W of Ws) {
+        if (W && W.kind === "w4") {
+          ops.unpackW4(this.gpu, W);
+          n++;
+        }
+      }
+    }
+    return n;
+  }
+
   // The 3 * blocks + 1 adaLN modulation linears all read the same SiLU(t-embedding) (dit.js:205-
   // 222): their first stages are stacked into one [(3B+1)*256, 2048] weight (one GEMV) and the
   // blocks' second stages into one [3B*6144, 256] weight run as one grouped GEMV, with adaln_lora

@@ -33,6 +33,23 @@ export function quantRows(gpu, x, K, rotateFirst, act) {
   return { q, s, release() { q.release(); s.release(); } };
 }
 
+// A W4 weight turned into the int8 weight with the same products, in place (the object keeps its
+// identity, so LoRA attachments and stacked views stay valid): the int8 grid replaces the codes
+// (one byte per weight instead of half), s_channel stays the per-row scale.  Bit-identical
+// linear results; the GEMM then skips the nibble unpack.
+export function unpackW4(gpu, W) {
+  if (W.kind !== "w4") return W;
+  const grid = gpu.empty([W.N * W.K], "i8");
+  native.weightUnpackW4(gpu.ctx, weightArg(W), grid.buf);
+  for (const t of [W.buf, W.srel, W.codebook]) if (t && t.release) t.release();
+  W.kind = "i8";
+  W.buf = grid;
+  W.srel = null;
+  W.codebook = null;
+  W.unpackedW4 = true;
+  return W;
+}
+
 function weightArg(W) {
   if (!(W.kind in KIND)) throw new Error(`unsupported weight kind ${W.kind}`);
   return { kindId: KIND[W.kind], N: W.N, K: W.K, buf: ptr(W.buf), scale: ptr(W.scale), srel: ptr(W.srel),

@@ -371,6 +371,14 @@ typedef struct {
  * i8/w4 need K % 64 == 0 (and K <= 8192 when x is quantized here). */
 int anima_linear(anima_ctx* ctx, const anima_linear_desc* desc);
 
+/* The int8 grid of a W4 weight, grid[n][k] = clamp(rint(codebook[code] * fp8(s_rel)), -127, 127)
+ * for the 4-bit code of (n, k): the values gemm.js:141-158's W4 B-loader multiplies
+ * (tools/quant.py:127-129).  An i8 weight {grid, scale = the W4 weight's s_channel, bias} then
+ * gives bit-identical anima_linear results on the int8 path; a loader that can spend the memory
+ * (one byte per weight instead of half a byte) converts W4 weights once at load time this way.
+ * grid: [N][K] int8, 16-byte aligned; K % 32 == 0. */
+int anima_weight_unpack_w4(anima_ctx* ctx, const anima_weight* w4, int8_t* grid);
+
 /* G independent small-M bf16-weight products in one launch, for the adaLN modulation linears of
  * timeCond (app/models/dit.js:196-225 runs one per block and kind, all on the same sigma):
  *   out[g*out_gstride + m*ldc + n] = sum_k x[g*x_gstride + m*ldx + k] * w[g*w_gstride + n*K + k]

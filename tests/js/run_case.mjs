@@ -270,6 +270,8 @@ async function main() {
   } else if (c.case === "synthdit") {
     // a seeded synthetic DiT (the weights the oracle restates by name) on given latents / contexts
     const dit = AnimaDiT.synthetic(gpu, new SyntheticWeights(gpu, c.seed, { mode: c.mode, blocks: c.blocks }));
+    // unpackW4: W4 weights converted to their int8 grids at load first
+    if (c.unpackW4) console.log(JSON.stringify({ unpacked: dit.unpackW4() }));
     const tc = dit.timeCond(c.sigma);
     const cond = dit.prepareContext(c.ctx.map((p) => gpu.fromArray(load(p), [c.Lk, 1024])));
     const blockOut = [];

@@ -99,3 +99,28 @@ def test_dit_full_size_step(tmp_path):
     assert np.array_equal(same[:n], same[n:])
     assert np.array_equal(same[:n], e[:n])
     assert np.array_equal(g, e)
+
+
+@pytest.mark.timeout(600)
+def test_dit_w4_unpacked_at_load_is_bit_identical(tmp_path):
+    """AnimaDiT.unpackW4 (W4 block linears converted to their int8 grids at load) gives the same
+    velocity, bit for bit, as the in-GEMM nibble unpack: a 4-block W4A8-mixed step at 256x256."""
+    nblocks, h, w, Lk, sigma, seed = 4, 32, 32, 64, 0.7, 11
+    files = {}
+    for b in range(2):
+        files[f"lat{b}"] = str(tmp_path / f"lat{b}.bin")
+        orc.randn(301 + b, 16 * h * w).tofile(files[f"lat{b}"])
+        files[f"ctx{b}"] = str(tmp_path / f"ctx{b}.bin")
+        orc.randn(311 + b, Lk * 1024).tofile(files[f"ctx{b}"])
+    outs = []
+    for unpack in (False, True):
+        out = str(tmp_path / f"v{int(unpack)}")
+        r = run_case(tmp_path, {"case": "synthdit", "seed": seed, "mode": "w4a8", "blocks": nblocks, "sigma": sigma,
+                                "Lk": Lk, "h": h, "w": w, "ctx": [files["ctx0"], files["ctx1"]],
+                                "latents": [files["lat0"], files["lat1"]], "out": out, "unpackW4": unpack})
+        if unpack:
+            info = json.loads(next(ln for ln in r.stdout.splitlines() if '"unpacked"' in ln))
+            # blocks 1 and 2 are W4 (0 and 3 int8): stacked qkv, self out, cross q / k / v / out, mlp 1 / 2
+            assert info["unpacked"] == 2 * 8
+        outs.append(np.concatenate([np.fromfile(out + f".{b}", np.float32) for b in range(2)]))
+    assert np.all(np.isfinite(outs[0])) and np.array_equal(outs[0], outs[1])

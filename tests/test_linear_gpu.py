@@ -580,3 +580,37 @@ def test_linear_rejects_bad_arguments(ctx):
     W = m.weight(m.W_I8, 64, 128, buf, scale=buf)
     with pytest.raises(m.AnimaError):
         ctx.linear(W, 4, buf, xq=buf, xs=buf, epilogue=m.EPI_GATED)  # no gate
+
+
+@pytest.mark.parametrize("K", [64, 2048])
+def test_weight_unpack_w4_grid_and_linear(ctx, K):
+    """anima_weight_unpack_w4: the int8 grid of a W4 weight equals the oracle's decode
+    (quant.py:127-129 / gemm.js:141-158) for every s_rel byte and a clamping codebook, and the i8
+    weight {grid, s_channel} gives the same linear output and accumulators as the W4 weight."""
+    case(f"W4 -> int8 grid unpack N=512 K={K}")
+    m = amd()
+    N, M = 512, 300
+    rng = np.random.default_rng(K + 5)
+    codes = rng.integers(0, 256, size=(N, K // 2), dtype=np.uint8)
+    srel = rng.integers(0, 256, size=(N, K // 16), dtype=np.uint8)
+    srel[:, 0] = np.arange(N) % 256
+    cb = np.sort(rng.uniform(-2.0, 2.0, 16)).astype(np.float32)
+    sw = (rng.uniform(0.5, 1.5, N) / (127 * np.sqrt(K))).astype(np.float32)
+    dsw = ctx.upload(sw)
+    W4 = m.weight(m.W_W4, N, K, ctx.upload(codes), scale=dsw, srel=ctx.upload(srel), codebook=ctx.upload(cb))
+    dgrid = ctx.empty((N, K), np.int8)
+    ctx.weight_unpack_w4(W4, dgrid)
+    grid = dgrid.numpy()
+    assert np.array_equal(grid, orc.w4_decode(codes, srel, cb, N, K))
+    W8 = m.weight(m.W_I8, N, K, dgrid, scale=dsw)
+    qx = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    sx = rng.uniform(0.001, 0.01, M).astype(np.float32)
+    dq, ds = ctx.upload(qx), ctx.upload(sx)
+    outs = []
+    for W in (W4, W8):
+        do, da = ctx.empty((M, N)), ctx.empty((M, N), np.int32)
+        ctx.linear(W, M, do, xq=dq, xs=ds, acc_out=da)
+        outs.append((do.numpy(), da.numpy()))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    with pytest.raises(m.AnimaError):
+        ctx.weight_unpack_w4(W8, dgrid)  # not a W4 weight
