@@ -31,8 +31,10 @@ INT8_PEAK_TOPS = 5033.2
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    # the device raises its clocks over ~25 ms of sustained load: 100 warmup steps (~30 ms) time
+    # the steady state
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=100)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-dit", action="store_true", help="skip the full DiT step leg")
     p.add_argument("--dit-steps", type=int, default=5)
@@ -79,8 +81,8 @@ def dit_step(args):
 
     js = os.path.join(ROOT, "anima-studio_amd", "js", "bench_dit.mjs")
     r = subprocess.run(["node", js, "--steps", str(args.dit_steps), "--warmup", "1", "--graph", "--generate", "8",
-                        "--sampler", "euler_a", "--cfg", "4", "--text-encoder", "512"], cwd=ROOT, capture_output=True,
-                       text=True, timeout=600)
+                        "--sampler", "euler_a", "--cfg", "4", "--text-encoder", "512", "--vae"], cwd=ROOT,
+                       capture_output=True, text=True, timeout=600)
     if r.returncode != 0:
         raise RuntimeError("bench_dit.mjs failed: " + r.stderr[-2000:])
     d = json.loads(r.stdout.strip().splitlines()[-1])
@@ -100,7 +102,10 @@ def dit_step(args):
             # an 8-step euler_a run with CFG 4: the device sampling loop vs the reference's host loop
             "sampling": d.get("generate"),
             # the text encoder (Qwen3, 28 layers, synthetic weights) on 512 tokens
-            "text_encoder": d.get("text_encoder")}
+            "text_encoder": d.get("text_encoder"),
+            # the VAE decode of this size's latent [16, 128, 128] -> 1024x1024 RGBA (Wan 2.1 decoder,
+            # synthetic weights), bf16 and fp32 precision, host conversions included
+            "vae_decode": d.get("vae")}
 
 
 def causal_attention(m, ctx, np):
@@ -118,9 +123,7 @@ def causal_attention(m, ctx, np):
         ctx.attention(q=q, k=k, v=v, o=o, B=B, Lq=L, Lk=L, H=H, D=D, ldq=H * D, ldk=Hkv * D, ldv=Hkv * D,
                       group=H // Hkv, causal=1)
 
-    for _ in range(5):
-        call()
-    ctx.sync()
+    settle(ctx, call)
     ctx.timer_start()
     for _ in range(50):
         call()
@@ -135,12 +138,26 @@ def causal_attention(m, ctx, np):
 FP32_PEAK_TFLOPS = 157.3
 
 
-def timed_kernels(ctx, call, reps):
-    """Per-kernel average ms of `call` (HIP events around each launch on the library stream) and
-    the whole call's ms (events around the reps)."""
+def settle(ctx, call, device_ms=30.0):
+    """Runs `call` back to back until about `device_ms` of device time has passed (at least 3
+    calls): the device raises its clocks over ~25 ms of sustained load, so the timings that
+    follow see the steady state."""
     for _ in range(3):
         call()
     ctx.sync()
+    ctx.timer_start()
+    for _ in range(3):
+        call()
+    per = max(ctx.timer_stop() / 3, 1e-3)
+    for _ in range(min(5000, int(device_ms / per) + 1)):
+        call()
+    ctx.sync()
+
+
+def timed_kernels(ctx, call, reps):
+    """Per-kernel average ms of `call` (HIP events around each launch on the library stream) and
+    the whole call's ms (events around the reps), after `settle`."""
+    settle(ctx, call)
     ctx.timer_start()
     for _ in range(reps):
         call()
@@ -313,9 +330,7 @@ def linears(m, ctx, reps):
                 kw.update(epilogue=m.EPI_GATED, gate=gate, gate_off=N)
             elif epi == "gelu":
                 kw.update(act="gelu")
-            for _ in range(2):
-                ctx.linear(W, M, out, **kw)
-            ctx.sync()
+            settle(ctx, lambda: ctx.linear(W, M, out, **kw))
             ctx.profile(True)
             ctx.profile_reset()
             for _ in range(reps):
@@ -413,7 +428,7 @@ def main():
         lin = None
         if not args.no_linears:
             t = time.time()
-            lin = linears(m, ctx, 10)
+            lin = linears(m, ctx, 20)
             print(f"bench: linears {time.time() - t:.1f} s", file=sys.stderr, flush=True)
 
     value = flops / (ms / 1e3) / 1e12
