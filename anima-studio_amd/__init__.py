@@ -102,6 +102,8 @@ def lib():
         L.anima_free.argtypes = [_vp, _vp]
         for n in ("anima_h2d", "anima_d2h", "anima_d2d"):
             getattr(L, n).argtypes = [_vp, _vp, _vp, ctypes.c_size_t]
+        L.anima_mark.argtypes = [_vp, P(ctypes.c_uint64)]
+        L.anima_wait_mark.argtypes = [_vp, ctypes.c_uint64]
         L.anima_profile_enable.argtypes = [_vp, ctypes.c_int]
         L.anima_profile_report.argtypes = [_vp, ctypes.c_char_p, ctypes.c_size_t]
         L.anima_timer_stop.argtypes = [_vp, P(ctypes.c_float)]
@@ -219,6 +221,15 @@ class Context:
 
     def sync(self):
         self._check(lib().anima_sync(self.h))
+
+    def mark(self):
+        """A point in the stream; wait_mark(t) returns once the work enqueued before it is done."""
+        t = ctypes.c_uint64()
+        self._check(lib().anima_mark(self.h, ctypes.byref(t)))
+        return t.value
+
+    def wait_mark(self, ticket):
+        self._check(lib().anima_wait_mark(self.h, ticket))
 
     def mem_stats(self):
         a, p, q = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()

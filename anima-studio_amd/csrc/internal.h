@@ -44,6 +44,19 @@ struct anima_ctx {
   std::unordered_map<std::string, anima::Stat> stats;
   // timer
   hipEvent_t t0 = nullptr, t1 = nullptr;
+  // host -> device staging: a ring of pinned slots, so that anima_h2d of a pageable source
+  // returns without waiting for the stream; slot i is reusable once stage_ev[i] has completed
+  static constexpr int kStageSlots = 4;
+  static constexpr size_t kStageBytes = (size_t)4 << 20;
+  void* stage[kStageSlots] = {};
+  hipEvent_t stage_ev[kStageSlots] = {};
+  bool stage_pending[kStageSlots] = {};
+  int stage_next = 0;
+  bool stage_failed = false;  // pinned allocation refused once: plain pageable copies from then on
+  // queue marks (anima_mark / anima_wait_mark): a ring of events, ticket t in slot t % kMarks
+  static constexpr int kMarks = 16;
+  hipEvent_t marks[kMarks] = {};
+  uint64_t mark_count = 0;
   // attention workspace (K in bf16/fp32, V transposed), grown on demand
   void* ws = nullptr;
   size_t ws_bytes = 0;

@@ -160,6 +160,28 @@ static void drop_capture(anima_ctx* c) {
   c->cap_ws = false;
 }
 
+// The pinned staging ring of anima_h2d, allocated on first use (4 x 4 MiB of page-locked host
+// memory per context).  If the host refuses it, copies stay on the pageable path.
+static bool stage_ready(anima_ctx* c) {
+  if (c->stage[0]) return true;
+  if (c->stage_failed) return false;
+  for (int i = 0; i < anima_ctx::kStageSlots; i++) {
+    if (hipHostMalloc(&c->stage[i], anima_ctx::kStageBytes, hipHostMallocDefault) != hipSuccess ||
+        hipEventCreateWithFlags(&c->stage_ev[i], hipEventDisableTiming) != hipSuccess) {
+      for (int j = 0; j <= i; j++) {
+        if (c->stage[j]) hipHostFree(c->stage[j]);
+        if (c->stage_ev[j]) hipEventDestroy(c->stage_ev[j]);
+        c->stage[j] = nullptr;
+        c->stage_ev[j] = nullptr;
+      }
+      hipGetLastError();  // the refusal is not an error of the copy that asked
+      c->stage_failed = true;
+      return false;
+    }
+  }
+  return true;
+}
+
 extern "C" {
 
 int anima_init(int device, anima_ctx** out) {
@@ -222,6 +244,12 @@ int anima_destroy(anima_ctx* c) {
     hipEventDestroy(r.b);
   }
   for (hipEvent_t e : c->spare_events) hipEventDestroy(e);
+  for (int i = 0; i < anima_ctx::kStageSlots; i++) {
+    if (c->stage[i]) hipHostFree(c->stage[i]);
+    if (c->stage_ev[i]) hipEventDestroy(c->stage_ev[i]);
+  }
+  for (int i = 0; i < anima_ctx::kMarks; i++)
+    if (c->marks[i]) hipEventDestroy(c->marks[i]);
   if (c->t0) hipEventDestroy(c->t0);
   if (c->t1) hipEventDestroy(c->t1);
   hipStreamDestroy(c->stream);
@@ -335,9 +363,56 @@ int anima_h2d(anima_ctx* c, void* dst, const void* src, size_t bytes) {
   NOT_CAPTURING(c, "anima_h2d");
   if (bytes == 0) return ANIMA_OK;
   if (!dst || !src) return fail(c, ANIMA_E_ARG, "anima_h2d: null pointer");
-  // pageable source: hipMemcpyAsync stages it before returning, so `src` may be reused
-  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream);
+  hipError_t e;
+  if (bytes <= anima_ctx::kStageBytes && stage_ready(c)) {
+    // copy into a pinned slot and enqueue the DMA from there: the call returns without waiting
+    // for the work already on the stream, and `src` may be reused at once
+    const int s = c->stage_next;
+    c->stage_next = (s + 1) % anima_ctx::kStageSlots;
+    if (c->stage_pending[s]) {
+      e = hipEventSynchronize(c->stage_ev[s]);
+      if (e != hipSuccess) return hip_fail(c, e, "anima_h2d (staging slot)");
+      c->stage_pending[s] = false;
+    }
+    std::memcpy(c->stage[s], src, bytes);
+    e = hipMemcpyAsync(dst, c->stage[s], bytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipEventRecord(c->stage_ev[s], c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "anima_h2d");
+    c->stage_pending[s] = true;
+    return ANIMA_OK;
+  }
+  // larger copies: hipMemcpyAsync from pageable memory stages the source before it returns (and
+  // waits for the stream to reach the copy), so `src` may be reused
+  e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "anima_h2d");
+  return ANIMA_OK;
+}
+
+int anima_mark(anima_ctx* c, uint64_t* ticket) {
+  CHECK_CTX(c);
+  NOT_CAPTURING(c, "anima_mark");
+  if (!ticket) return fail(c, ANIMA_E_ARG, "anima_mark: ticket is NULL");
+  const int s = (int)(c->mark_count % anima_ctx::kMarks);
+  hipError_t e = hipSuccess;
+  if (!c->marks[s]) e = hipEventCreateWithFlags(&c->marks[s], hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventRecord(c->marks[s], c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "anima_mark");
+  *ticket = c->mark_count++;
+  return ANIMA_OK;
+}
+
+int anima_wait_mark(anima_ctx* c, uint64_t ticket) {
+  CHECK_CTX(c);
+  NOT_CAPTURING(c, "anima_wait_mark");
+  if (ticket >= c->mark_count)
+    return fail(c, ANIMA_E_ARG, "anima_wait_mark: ticket %llu was not issued (next is %llu)", (unsigned long long)ticket,
+                (unsigned long long)c->mark_count);
+  // a ticket older than the last kMarks marks shares its slot with a later mark: waiting for that
+  // later point also covers the work before the older one
+  hipError_t e = hipEventSynchronize(c->marks[ticket % anima_ctx::kMarks]);
+  if (e != hipSuccess) return hip_fail(c, e, "anima_wait_mark");
+  e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(c, e, "anima_wait_mark (deferred)");
   return ANIMA_OK;
 }
 

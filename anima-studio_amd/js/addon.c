@@ -279,6 +279,24 @@ static napi_value js_finalized(napi_env env, napi_callback_info info) {
   return make_num(env, g_finalized);
 }
 
+/* anima_mark / anima_wait_mark: tickets travel as JS numbers (exact below 2^53) */
+static napi_value js_mark(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  uint64_t t = 0;
+  CHECK_RC(env, c, anima_mark(c, &t));
+  return make_num(env, (double)t);
+}
+
+static napi_value js_wait_mark(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  CHECK_RC(env, c, anima_wait_mark(c, (uint64_t)i64(env, argv[1])));
+  return NULL;
+}
+
 static napi_value js_trim(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   get_args(env, info, 1, argv);
@@ -780,7 +798,7 @@ static napi_value js_graph_destroy(napi_env env, napi_callback_info info) {
 static napi_value Init(napi_env env, napi_value exports) {
 #define FN(name, f) {name, NULL, f, NULL, NULL, NULL, napi_enumerable, NULL}
   napi_property_descriptor desc[] = {
-      FN("init", js_init), FN("destroy", js_destroy), FN("sync", js_sync), FN("alloc", js_alloc),
+      FN("init", js_init), FN("destroy", js_destroy), FN("sync", js_sync), FN("mark", js_mark), FN("waitMark", js_wait_mark), FN("alloc", js_alloc),
       FN("free", js_free), FN("allocHandle", js_alloc_handle), FN("handleAddr", js_handle_addr),
       FN("release", js_release), FN("finalized", js_finalized), FN("trim", js_trim), FN("memStats", js_mem_stats), FN("h2d", js_h2d),
       FN("d2h", js_d2h), FN("d2d", js_d2d), FN("profileEnable", js_profile_enable),

@@ -151,6 +151,16 @@ export class GPU {
     native.sync(this.ctx);
   }
 
+  // A point in the queue (its ticket) and the wait for it: `await gpu.waitMark(t)` returns when
+  // the work enqueued before mark t has finished, with device errors surfaced as by sync().
+  mark() {
+    return native.mark(this.ctx);
+  }
+
+  async waitMark(t) {
+    native.waitMark(this.ctx, t);
+  }
+
   timerStart() {
     native.timerStart(this.ctx);
   }

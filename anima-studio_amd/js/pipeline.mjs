@@ -96,24 +96,40 @@ export class LatentPipeline {
     const useGraph = opts.graph === true && plan.steps > 1;
     const nBlocks = this.dit.blocks.length;
     let fg = null;
+    // The reference drains the queue every 7 blocks (pipeline.js:255) to keep progress and
+    // cancellation responsive.  Here each such point waits for the previous point's mark instead,
+    // so the device keeps the last 7 blocks queued while the host enqueues the next ones (a full
+    // drain would idle it for the host's share of every chunk).
+    let lastMark = null;
+    const pace = async () => {
+      const m = gpu.mark();
+      if (lastMark !== null) await gpu.waitMark(lastMark);
+      lastMark = m;
+    };
     try {
       check();
       for (let i = 0; i < plan.steps; i++) {
         const st = plan.step(i);
         const tc = this.timeCond(st.sigma);
         for (let b = 0; b < B; b++) gpu.copy(lat.at(b * n), x, n * 4);
+        // the step's noise (samplers.js:105-106: one draw per noisy step, in step order) is drawn on the
+        // host once the whole forward is enqueued, before the wait, so that it overlaps the
+        // device's work on the queued blocks
+        let noise = null;
         const onBlock = async (blk) => {
           check();
           onProgress({ phase: "sample", step: i, steps: plan.steps, frac: (i + (blk + 1) / nBlocks) / plan.steps });
-          if (blk % 7 === 6) await gpu.sync();
+          if (blk === nBlocks - 1 && st.noise) noise = gen.randn(n);
+          if (blk % 7 === 6) await pace();
         };
         const v = fg ? fg.run(tc) : await this.dit.forwardDevice(lat, h, w, cond, tc, onBlock);
         if (fg) {
-          await gpu.sync();
+          if (st.noise) noise = gen.randn(n);
+          await pace();
           check();
           onProgress({ phase: "sample", step: i, steps: plan.steps, frac: (i + 1) / plan.steps });
         }
-        const eps = st.noise ? gpu.fromArray(gen.randn(n), [n]) : null;
+        const eps = st.noise ? gpu.fromArray(noise || gen.randn(n), [n]) : null;
         native.samplerStep(gpu.ctx, {
           kind: st.kind, n, x: x.buf, v: v.buf, vUncond: guided ? v.at(n) : 0, cfg, sigma: st.sigma,
           final: st.final, stage: st.stage, den: den ? den.buf : 0, old: plan.kind >= 2 ? old.buf : 0,

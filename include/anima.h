@@ -57,8 +57,18 @@ int anima_free(anima_ctx* ctx, void* ptr);
 /* BufferPool.trim (app/gpu/device.js:53-56): synchronize and release every parked buffer. */
 int anima_pool_trim(anima_ctx* ctx);
 /* GPU.write / fromArray (app/gpu/device.js:113-131): host -> device, stream-ordered; the host
- * buffer may be reused when the call returns. */
+ * buffer may be reused when the call returns.  Copies up to 4 MiB go through a ring of pinned
+ * staging slots and return without waiting for the work already on the stream (as
+ * queue.writeBuffer does); larger ones wait for the stream to reach the copy. */
 int anima_h2d(anima_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Queue marks, for the reference's periodic `await gpu.sync()` in long encodes
+ * (app/pipeline.js:255, every 7 DiT blocks): anima_mark records the current end of the
+ * stream and returns its ticket; anima_wait_mark(t) blocks until the work enqueued before mark t
+ * has finished and surfaces deferred device errors like anima_sync.  Waiting for the mark before
+ * the last one keeps work queued on the device while the host catches up.  Tickets older than
+ * the 16 most recent marks wait for a later mark (a superset of their work). */
+int anima_mark(anima_ctx* ctx, uint64_t* ticket);
+int anima_wait_mark(anima_ctx* ctx, uint64_t ticket);
 /* GPU.read (app/gpu/device.js:141-154): device -> host, waits for the stream. */
 int anima_d2h(anima_ctx* ctx, void* dst, const void* src, size_t bytes);
 /* Device-to-device copy (the copyBufferToBuffer of concatLinears, app/weights.js:168-184). */

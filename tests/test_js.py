@@ -38,7 +38,7 @@ def test_addon_exports_and_error_path():
              "console.log(JSON.stringify({ ks, msg }))")
     assert r.returncode == 0, r.stderr
     out = json.loads(r.stdout)
-    for k in ("init", "attention", "linear", "layernormMod", "qkNormRope", "h2d", "d2h", "alloc", "free"):
+    for k in ("init", "attention", "linear", "layernormMod", "qkNormRope", "h2d", "d2h", "alloc", "free", "mark", "waitMark"):
         assert k in out["ks"], k
     if out["msg"]:  # no GPU here: the C ABI status becomes a JS Error with the library's message
         assert "anima error" in out["msg"]
