@@ -45,19 +45,20 @@ export class Qwen3 {
     const { hidden: D, heads: H, kvHeads: KH, headDim: HD, mlp: F } = cfg;
     m.layers = [];
     for (let i = 0; i < cfg.layers; i++) {
-      const p = `te.${i}.`;
+      // the checkpoint's module names (qwen3.js:8-31), so that LoRA files address these linears
+      const p = `model.layers.${i}.`;
       m.layers.push({
-        ln1: src.vector(gpu, p + "ln1", D), ln2: src.vector(gpu, p + "ln2", D),
-        qn: src.vector(gpu, p + "qn", HD), kn: src.vector(gpu, p + "kn", HD),
-        q: src.bf16Linear(gpu, p + "q", H * HD, D, 1.0), k: src.bf16Linear(gpu, p + "k", KH * HD, D, 1.0),
-        v: src.bf16Linear(gpu, p + "v", KH * HD, D, 1.0), o: src.bf16Linear(gpu, p + "o", D, H * HD, 0.5),
-        gate: src.bf16Linear(gpu, p + "gate", F, D, 1.0), up: src.bf16Linear(gpu, p + "up", F, D, 1.0),
-        down: src.bf16Linear(gpu, p + "down", D, F, 0.5),
+        ln1: src.vector(gpu, p + "input_layernorm.weight", D), ln2: src.vector(gpu, p + "post_attention_layernorm.weight", D),
+        qn: src.vector(gpu, p + "self_attn.q_norm.weight", HD), kn: src.vector(gpu, p + "self_attn.k_norm.weight", HD),
+        q: src.bf16Linear(gpu, p + "self_attn.q_proj", H * HD, D, 1.0), k: src.bf16Linear(gpu, p + "self_attn.k_proj", KH * HD, D, 1.0),
+        v: src.bf16Linear(gpu, p + "self_attn.v_proj", KH * HD, D, 1.0), o: src.bf16Linear(gpu, p + "self_attn.o_proj", D, H * HD, 0.5),
+        gate: src.bf16Linear(gpu, p + "mlp.gate_proj", F, D, 1.0), up: src.bf16Linear(gpu, p + "mlp.up_proj", F, D, 1.0),
+        down: src.bf16Linear(gpu, p + "mlp.down_proj", D, F, 0.5),
       });
     }
-    m.norm = src.vector(gpu, "te.norm", D);
+    m.norm = src.vector(gpu, "model.norm.weight", D);
     const table = gpu.empty([cfg.vocab * D]);
-    src.fill(table, "f32", "te.embed", -1, 1);
+    src.fill(table, "f32", "model.embed_tokens.weight", -1, 1);
     m.table = table;
     m.embedRows = async (ids) => {
       const all = await gpu.read(table);

@@ -6,8 +6,8 @@ F.scaled_dot_product_attention (109-111), the LayerNorm + adaLN modulation and g
 the block (231-242), and the ConvRot int8 linears in two semantics: W8A32 (the reference's own:
 dequantized weights, fp32 activations) and W8A8 (this build's: activations quantized per token
 after the rotation, emulated in fp32).  bench.py times it on the host cores as the CPU baseline
-(attention, the quantized projections, the full 28-block step); tests/test_oracle.py checks its
-attention against the C oracle.
+(attention, the quantized projections, the full 28-block step); tests/test_oracle_torchref.py
+checks its RoPE table and attention against the C oracle.
 """
 
 from __future__ import annotations

@@ -12,6 +12,8 @@
 //              stacked A matrices and a rotated-only input
 //   lorafile   loadLora(safetensors) onto a 1-block synthetic DiT, then the block's stacked qkv
 //              and mlp.layer2 linears with and without the attached LoRA
+//   lorate     loadLora(safetensors) onto a 2-layer synthetic text encoder (text-encoder names):
+//              layer 1's q_proj and mlp.down_proj with and without the LoRA, and the encoding
 //   loramod    timeCond of a 1-block synthetic DiT with LoRAs on the adaLN modulation linears,
 //              on the fused (grouped GEMV) and the per-linear modulation paths
 //   generate   LatentPipeline.generate (device loop) and generateHost (the reference's host loop)
@@ -140,6 +142,30 @@ async function main() {
     console.log(JSON.stringify({ matched: L.matched, total: L.total, unsupported: L.unsupported, skipped: L.skipped, entries }));
     attachLoras(regs, []);
     destroyLora(L);
+  } else if (c.case === "lorate") {
+    const te = Qwen3.synthetic(gpu, new SyntheticWeights(gpu, 17), { layers: 2, vocab: 97 });
+    const regs = { dit: null, te: linearRegistry(te) };
+    const L = loadLora(gpu, c.lora, regs);
+    const x = gpu.fromArray(load(c.x), [c.M, 1024]);
+    const h = gpu.fromArray(load(c.h), [c.M, 3072]);
+    const l = te.layers[1];
+    const ids = [3, 14, 15, 92, 65, 35];
+    const e0 = await te.encode(ids);
+    save(c.out + ".enc.base", await gpu.read(e0));
+    e0.release();
+    save(c.out + ".q.base", await gpu.read(ops.linear(gpu, x, l.q, {})));
+    save(c.out + ".down.base", await gpu.read(ops.linear(gpu, h, l.down, {})));
+    attachLoras(regs, [{ lora: L, strength: c.strength }]);
+    save(c.out + ".q", await gpu.read(ops.linear(gpu, x, l.q, {})));
+    save(c.out + ".down", await gpu.read(ops.linear(gpu, h, l.down, {})));
+    const e1 = await te.encode(ids);
+    save(c.out + ".enc", await gpu.read(e1));
+    e1.release();
+    const entries = [l.q, l.down].map((W) => W.lora.map((e) => ({ r: e.r, scale: e.scale, off: e.off, n: e.n })));
+    console.log(JSON.stringify({ matched: L.matched, total: L.total, unsupported: L.unsupported, skipped: L.skipped, entries }));
+    attachLoras(regs, []);
+    destroyLora(L);
+    te.release();
   } else if (c.case === "loramod") {
     const mods = async (tc) => {
       const parts = [tc.blocks[0].self, tc.blocks[0].cross, tc.blocks[0].mlp, tc.final];

@@ -264,6 +264,48 @@ def test_js_lora_file(tmp_path):
     assert report("mlp.layer2 LoRA delta", l.astype(np.float64) - lb, dl)[0] < 1e-4
 
 
+def test_js_lora_text_encoder(tmp_path):
+    """loadLora with text-encoder names (PEFT `text_encoder.` and kohya `lora_te_`, app/lora.js:21,
+    89) onto the Qwen3 encoder's registry: layer 1's q_proj and mlp.down_proj (bf16 weights, no
+    rotation) get scale * B (A x) within 1e-4 of float64, a DiT-named module finds no target (no
+    DiT registry), and the encoding changes once the LoRA is attached."""
+    from safetensors.numpy import save_file
+
+    M = 48
+    rq, rd = 8, 4
+    Aq = (0.05 * orc.randn(141, rq * 1024)).reshape(rq, 1024).astype(np.float32)
+    Bq = (0.05 * orc.randn(142, 2048 * rq)).reshape(2048, rq).astype(np.float32)
+    Ad = (0.05 * orc.randn(143, rd * 3072)).reshape(rd, 3072).astype(np.float32)
+    Bd = (0.05 * orc.randn(144, 1024 * rd)).reshape(1024, rd).astype(np.float32)
+    tensors = {
+        "text_encoder.model.layers.1.self_attn.q_proj.lora_A.weight": Aq,
+        "text_encoder.model.layers.1.self_attn.q_proj.lora_B.weight": Bq,
+        "lora_te_model_layers_1_mlp_down_proj.lora_down.weight": Ad,
+        "lora_te_model_layers_1_mlp_down_proj.lora_up.weight": Bd,
+        "lora_te_model_layers_1_mlp_down_proj.alpha": np.array(2.0, np.float32),
+        "diffusion_model.blocks.0.mlp.layer1.lora_A.weight": np.zeros((2, 2048), np.float32),
+        "diffusion_model.blocks.0.mlp.layer1.lora_B.weight": np.zeros((8192, 2), np.float32),
+    }
+    path = str(tmp_path / "lora_te.safetensors")
+    save_file(tensors, path)
+    x = orc.randn(145, M * 1024).reshape(M, 1024)
+    h = orc.randn(146, M * 3072).reshape(M, 3072)
+    out = str(tmp_path / "t")
+    r = run_case(tmp_path, {"case": "lorate", "lora": path, "strength": 0.8, "M": M,
+                            "x": write(tmp_path, "x.bin", x), "h": write(tmp_path, "h.bin", h), "out": out})
+    info = json.loads(next(ln for ln in r.stdout.splitlines() if '"matched"' in ln))
+    assert (info["matched"], info["total"], info["unsupported"], info["skipped"]) == (2, 3, 0, 1), info
+    assert info["entries"] == [[{"r": rq, "scale": 0.8, "off": 0, "n": 2048}], [{"r": rd, "scale": 0.4, "off": 0, "n": 1024}]]
+    q, qb = read(out + ".q").reshape(M, 2048), read(out + ".q.base").reshape(M, 2048)
+    dq = lora_delta(x, [dict(A=Aq, B=Bq, scale=0.8, off=0, n=2048)], 2048)
+    assert report("text encoder q_proj LoRA delta", q.astype(np.float64) - qb, dq)[0] < 1e-4
+    d, db = read(out + ".down").reshape(M, 1024), read(out + ".down.base").reshape(M, 1024)
+    dd = lora_delta(h, [dict(A=Ad, B=Bd, scale=0.4, off=0, n=1024)], 1024)
+    assert report("text encoder down_proj LoRA delta", d.astype(np.float64) - db, dd)[0] < 1e-4
+    e, eb = read(out + ".enc"), read(out + ".enc.base")
+    assert np.all(np.isfinite(e)) and np.abs(e - eb).max() > 1e-3 * np.abs(eb).max()
+
+
 def test_js_lora_modulation(tmp_path):
     """LoRAs on adaLN modulation linears (a first stage, a second stage and the final layer's
     second stage): timeCond on the fused path (one stacked first-stage GEMV + one grouped
