@@ -13,6 +13,8 @@
 //                     [--vae]  (also time the VAE decode of this size's latent, bf16 and fp32 precision)
 //                     [--w4 packed|int8]  (W4 weights unpacked inside each GEMM, or converted to their
 //                      int8 grid once at load: bit-identical products)
+//                     [--unpacked-too]  (with packed W4: also time the step after converting the W4
+//                      linears to their int8 grid in place, reported as w4_unpacked)
 //                     [--graph [--rounds 3]]  (also the forward replayed from a HIP graph recorded
 //                      once, ForwardGraph: graph and eager blocks of --steps steps alternate,
 //                      medians; dit_step_ms stays the eager step, graph_step_ms the replay)
@@ -213,6 +215,19 @@ async function main() {
       const ms = ts.sort((a, b) => a - b)[1];
       out.vae[prec] = { ms: Number(ms.toFixed(2)), "TFLOP/s": Number((vaeFlops(h, w) / ms / 1e9).toFixed(1)) };
     }
+  }
+  if (arg("unpacked-too", false) && w4mode === "packed" && mode === "w4a8") {
+    // the same step once the W4 linears are converted to their int8 grid in place (after the
+    // graph, which holds the packed buffers, is released): bit-identical velocities
+    if (fg) {
+      fg.release();
+      fg = null;
+    }
+    const n = dit.unpackW4();
+    for (let i = 0; i < warmup; i++) await step(true);
+    await gpu.sync();
+    const xs = await timed(true);
+    out.w4_unpacked = { linears: n, step_ms: Number(median(xs).toFixed(3)) };
   }
   console.log(JSON.stringify(out));
   if (fg) fg.release();

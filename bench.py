@@ -86,14 +86,15 @@ def dit_step(args):
     import subprocess
 
     js = os.path.join(ROOT, "anima-studio_amd", "js", "bench_dit.mjs")
-    r = subprocess.run(["node", js, "--steps", str(args.dit_steps), "--warmup", "1", "--graph", "--generate", "8",
-                        "--sampler", "euler_a", "--cfg", "4", "--text-encoder", "512", "--vae"], cwd=ROOT,
+    r = subprocess.run(["node", js, "--steps", str(args.dit_steps), "--warmup", "3", "--graph", "--generate", "8",
+                        "--sampler", "euler_a", "--cfg", "4", "--text-encoder", "512", "--vae", "--unpacked-too"],
+                       cwd=ROOT,
                        capture_output=True, text=True, timeout=600)
     if r.returncode != 0:
         raise RuntimeError("bench_dit.mjs failed: " + r.stderr[-2000:])
     d = json.loads(r.stdout.strip().splitlines()[-1])
     # the same step with rank-32 LoRAs on every block linear (strength 1)
-    rl = subprocess.run(["node", js, "--steps", str(args.dit_steps), "--warmup", "1", "--lora-rank", "32"], cwd=ROOT,
+    rl = subprocess.run(["node", js, "--steps", str(args.dit_steps), "--warmup", "3", "--lora-rank", "32"], cwd=ROOT,
                         capture_output=True, text=True, timeout=600)
     lora = json.loads(rl.stdout.strip().splitlines()[-1]) if rl.returncode == 0 else None
     return {"ms": d["dit_step_ms"], "tflops": d["tflops"], "finite": d["finite"],
@@ -101,6 +102,9 @@ def dit_step(args):
             # blocks alternating with the eager steps (medians)
             "graph_ms": d.get("graph_step_ms"),
             "lora_rank32_ms": lora["dit_step_ms"] if lora else None,
+            # the same eager step with the W4 linears converted to their int8 grid at load
+            # (anima_weight_unpack_w4; bit-identical velocities, 2x the W4 weight bytes)
+            "w4_unpacked_ms": (d.get("w4_unpacked") or {}).get("step_ms"),
             "config": "Anima DiT 28 blocks, 1024x1024 (4096 tokens), B=2 CFG, hidden 2048, 16x128 heads, MLP 8192, "
                       "self + cross attention to 512x1024 contexts, W4A8 mixed (blocks 0/27 int8), seeded random weights; "
                       "step = timeCond + forward through node bench_dit.mjs",
