@@ -203,9 +203,16 @@ async function main() {
     const vae = VAEDecoder.synthetic(gpu, new SyntheticWeights(gpu, 77));
     const lat = normals(16 * h * w, 7);
     out.vae = { latent: [16, h, w], image: [8 * h, 8 * w], gflop: Number((vaeFlops(h, w) / 1e9).toFixed(1)) };
+    // both precisions warmed up first: the first decodes of a process run their middle stage
+    // (the 16384-token attention over a fresh 1 GiB score buffer) several times slower
+    for (let i = 0; i < 3; i++) {
+      for (const prec of ["bf16", "fp32"]) {
+        vae.precision = prec;
+        await vae.decode(lat, h, w);
+      }
+    }
     for (const prec of ["bf16", "fp32"]) {
       vae.precision = prec;
-      await vae.decode(lat, h, w);
       const ts = [];
       for (let i = 0; i < 3; i++) {
         gpu.timerStart();
