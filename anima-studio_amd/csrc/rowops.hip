@@ -595,7 +595,11 @@ template <int LR>
 __global__ __launch_bounds__(256) void layernorm_mod_reg_kernel(const float* X, const float* MOD, int64_t shift_off,
                                                                 int64_t scale_off, int64_t rows, float eps, int rotate,
                                                                 float* Y, int8_t* Q, float* S_out) {
-  constexpr int COLS = 64 * LR, VT = 256 / LR, NB = COLS / 256, RPW = 256 / LR, RS = COLS + 4 * LR;
+  // The modulated row crosses LDS in two halves of COLS / 2 columns through one half-row buffer
+  // (4 floats of padding per 64): 34 KiB per workgroup instead of 68, so four workgroups (four
+  // waves per SIMD) fit on a CU instead of two.
+  constexpr int COLS = 64 * LR, VT = 256 / LR, NB = COLS / 256, RPW = 256 / LR, HB = NB / 2;
+  constexpr int RS = COLS / 2 + 2 * LR;  // half-row stride in floats
   __shared__ __attribute__((aligned(16))) float SH[RPW * RS];
   const int l = threadIdx.x % LR, rl = threadIdx.x / LR;
   const int64_t row = (int64_t)blockIdx.x * RPW + rl;
@@ -631,27 +635,36 @@ __global__ __launch_bounds__(256) void layernorm_mod_reg_kernel(const float* X, 
     }
   const float r = 1.0f / sqrtf(seg_tree_sum<LR>(p) / (float)COLS + eps);
   float* S = SH + rl * RS;
-#pragma unroll
-  for (int i = 0; i < NB; i++)
-#pragma unroll
-    for (int q = 0; q < VT / 4; q++) {
-      const int c = 256 * i + VT * l + 4 * q;
-      const float4 sc = *(const float4*)(MOD + scale_off + c);
-      const float4 sh = *(const float4*)(MOD + shift_off + c);
-      const float* t = v + VT * i + 4 * q;
-      *(float4*)(S + c + 4 * (c >> 6)) =
-          make_float4((t[0] - mean) * r * (1.0f + sc.x) + sh.x, (t[1] - mean) * r * (1.0f + sc.y) + sh.y,
-                      (t[2] - mean) * r * (1.0f + sc.z) + sh.z, (t[3] - mean) * r * (1.0f + sc.w) + sh.w);
-    }
-  // (LDS operations of one wave complete in order: the row's lanes all belong to this wave)
+  // Half hh: every lane writes its elements of columns [hh * COLS / 2, (hh + 1) * COLS / 2)
+  // (blocks hh * HB .. + HB), then the LR / 2 lanes whose 64 Hadamard columns lie in that half
+  // read them.  (LDS operations of one wave complete in order, and the row's lanes all belong to
+  // this wave: the second half's writes follow the first half's reads.)
   float w[64];
 #pragma unroll
-  for (int q = 0; q < 16; q++) {
-    const float4 t = *(const float4*)(S + 68 * l + 4 * q);
-    w[4 * q] = t.x;
-    w[4 * q + 1] = t.y;
-    w[4 * q + 2] = t.z;
-    w[4 * q + 3] = t.w;
+  for (int hh = 0; hh < 2; hh++) {
+#pragma unroll
+    for (int i = hh * HB; i < (hh + 1) * HB; i++)
+#pragma unroll
+      for (int q = 0; q < VT / 4; q++) {
+        const int c = 256 * i + VT * l + 4 * q, ch = c - hh * (COLS / 2);
+        const float4 sc = *(const float4*)(MOD + scale_off + c);
+        const float4 sh = *(const float4*)(MOD + shift_off + c);
+        const float* t = v + VT * i + 4 * q;
+        *(float4*)(S + ch + 4 * (ch >> 6)) =
+            make_float4((t[0] - mean) * r * (1.0f + sc.x) + sh.x, (t[1] - mean) * r * (1.0f + sc.y) + sh.y,
+                        (t[2] - mean) * r * (1.0f + sc.z) + sh.z, (t[3] - mean) * r * (1.0f + sc.w) + sh.w);
+      }
+    if (l / (LR / 2) == hh) {
+      const int lh = l - hh * (LR / 2);
+#pragma unroll
+      for (int q = 0; q < 16; q++) {
+        const float4 t = *(const float4*)(S + 68 * lh + 4 * q);
+        w[4 * q] = t.x;
+        w[4 * q + 1] = t.y;
+        w[4 * q + 2] = t.z;
+        w[4 * q + 3] = t.w;
+      }
+    }
   }
   if (rotate) hadamard64_quad(w, l & 3);
   if (Y) {
