@@ -6,6 +6,19 @@
 
 import * as ops from "./ops.mjs";
 import { ropeTable } from "./common.mjs";
+import { concatLinears } from "./weights.mjs";
+
+// q, k and v of a layer stacked into one [(H + 2 KH) HD, D] linear (one GEMM per layer instead
+// of three; the q/k RMSNorm and RoPE then run inside the attention's loads).  Formats that
+// cannot be stacked (W4 parts with different codebooks) keep the three linears.
+function stackQKV(gpu, l) {
+  const qkv = concatLinears(gpu, [l.q, l.k, l.v]);
+  if (!qkv) return;
+  l.qkv = qkv;
+  delete l.q;
+  delete l.k;
+  delete l.v;
+}
 
 export const QWEN3 = { layers: 28, hidden: 1024, heads: 16, kvHeads: 8, headDim: 128, mlp: 3072, theta: 1e6, vocab: 151936 };
 
@@ -29,6 +42,7 @@ export class Qwen3 {
         up: st.linear(gpu, p + "mlp.up_proj."),
         down: st.linear(gpu, p + "mlp.down_proj."),
       });
+      stackQKV(gpu, m.layers[i]);
       if (onProgress) onProgress((i + 1) / QWEN3.layers);
     }
     m.norm = st.vector(gpu, "model.norm.weight");
@@ -55,6 +69,7 @@ export class Qwen3 {
         gate: src.bf16Linear(gpu, p + "mlp.gate_proj", F, D, 1.0), up: src.bf16Linear(gpu, p + "mlp.up_proj", F, D, 1.0),
         down: src.bf16Linear(gpu, p + "mlp.down_proj", D, F, 0.5),
       });
+      stackQKV(gpu, m.layers[i]);
     }
     m.norm = src.vector(gpu, "model.norm.weight", D);
     const table = gpu.empty([cfg.vocab * D]);
@@ -84,23 +99,34 @@ export class Qwen3 {
     const cs = ropeTable(gpu, Lt, HD, this.cfg.theta);
     for (const l of this.layers) {
       const h = ops.rmsnorm(gpu, x, l.ln1, D);
-      const hr = ops.needsRotation(l.q) ? ops.rotate(gpu, h) : null;
-      const q = ops.linear(gpu, h, l.q, { xr: hr });
-      const k = ops.linear(gpu, h, l.k, { xr: hr });
-      const v = ops.linear(gpu, h, l.v, { xr: hr });
+      const hr = ops.needsRotation(l.qkv || l.q) ? ops.rotate(gpu, h) : null;
+      let a;
+      if (l.qkv) {
+        // one GEMM for q, k and v; their per-head RMSNorm and RoPE run in the attention's loads
+        const qkv = ops.linear(gpu, h, l.qkv, { xr: hr });
+        const ld = (H + 2 * KH) * HD;
+        a = ops.attention(gpu, { q: qkv, k: qkv, v: qkv, Lq: Lt, Lk: Lt, H, D: HD, ldq: ld, ldk: ld, ldv: ld, qOff: 0,
+          kOff: H * HD, vOff: (H + KH) * HD, group: H / KH, causal: true, qNorm: l.qn, kNorm: l.kn, cs,
+          precision: this.precision });
+        qkv.release();
+      } else {
+        const q = ops.linear(gpu, h, l.q, { xr: hr });
+        const k = ops.linear(gpu, h, l.k, { xr: hr });
+        const v = ops.linear(gpu, h, l.v, { xr: hr });
+        const qn = ops.rmsnorm(gpu, q, l.qn, HD);
+        const kn = ops.rmsnorm(gpu, k, l.kn, HD);
+        q.release();
+        k.release();
+        ops.rope(gpu, qn, cs, Lt, H, HD);
+        ops.rope(gpu, kn, cs, Lt, KH, HD);
+        a = ops.attention(gpu, { q: qn, k: kn, v, Lq: Lt, Lk: Lt, H, D: HD, ldq: H * HD, ldk: KH * HD, ldv: KH * HD,
+          group: H / KH, causal: true, precision: this.precision });
+        qn.release();
+        kn.release();
+        v.release();
+      }
       if (hr) hr.release();
       h.release();
-      const qn = ops.rmsnorm(gpu, q, l.qn, HD);
-      const kn = ops.rmsnorm(gpu, k, l.kn, HD);
-      q.release();
-      k.release();
-      ops.rope(gpu, qn, cs, Lt, H, HD);
-      ops.rope(gpu, kn, cs, Lt, KH, HD);
-      const a = ops.attention(gpu, { q: qn, k: kn, v, Lq: Lt, Lk: Lt, H, D: HD, ldq: H * HD, ldk: KH * HD, ldv: KH * HD,
-        group: H / KH, causal: true, precision: this.precision });
-      qn.release();
-      kn.release();
-      v.release();
       ops.linear(gpu, a, l.o, { out: x, resid: true });
       a.release();
       const h2 = ops.rmsnorm(gpu, x, l.ln2, D);

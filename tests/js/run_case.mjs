@@ -153,15 +153,24 @@ async function main() {
     const e0 = await te.encode(ids);
     save(c.out + ".enc.base", await gpu.read(e0));
     e0.release();
-    save(c.out + ".q.base", await gpu.read(ops.linear(gpu, x, l.q, {})));
+    // q_proj: its own linear, or the first H*HD columns of the stacked q/k/v linear
+    const Wq = l.qkv || l.q;
+    const nq = te.cfg.heads * te.cfg.headDim;
+    const qCols = async (y) => {
+      const all = await gpu.read(y);
+      const out = new Float32Array(c.M * nq);
+      for (let r = 0; r < c.M; r++) out.set(all.subarray(r * Wq.N, r * Wq.N + nq), r * nq);
+      return out;
+    };
+    save(c.out + ".q.base", await qCols(ops.linear(gpu, x, Wq, {})));
     save(c.out + ".down.base", await gpu.read(ops.linear(gpu, h, l.down, {})));
     attachLoras(regs, [{ lora: L, strength: c.strength }]);
-    save(c.out + ".q", await gpu.read(ops.linear(gpu, x, l.q, {})));
+    save(c.out + ".q", await qCols(ops.linear(gpu, x, Wq, {})));
     save(c.out + ".down", await gpu.read(ops.linear(gpu, h, l.down, {})));
     const e1 = await te.encode(ids);
     save(c.out + ".enc", await gpu.read(e1));
     e1.release();
-    const entries = [l.q, l.down].map((W) => W.lora.map((e) => ({ r: e.r, scale: e.scale, off: e.off, n: e.n })));
+    const entries = [Wq, l.down].map((W) => W.lora.map((e) => ({ r: e.r, scale: e.scale, off: e.off, n: e.n })));
     console.log(JSON.stringify({ matched: L.matched, total: L.total, unsupported: L.unsupported, skipped: L.skipped, entries }));
     attachLoras(regs, []);
     destroyLora(L);
@@ -354,7 +363,17 @@ async function main() {
     const dump = async (name, t) => save(`${c.out}.w.${name}`, await gpu.read(typeof t.buf === "object" ? t.buf : t));
     for (let i = 0; i < te.layers.length; i++) {
       const l = te.layers[i];
-      for (const k of ["ln1", "ln2", "qn", "kn", "q", "k", "v", "o", "gate", "up", "down"]) await dump(`${i}.${k}`, l[k]);
+      for (const k of ["ln1", "ln2", "qn", "kn", "o", "gate", "up", "down"]) await dump(`${i}.${k}`, l[k]);
+      if (l.qkv) {
+        // q, k and v are row blocks of the stacked [(H + 2 KH) HD, D] weight
+        const all = await gpu.read(l.qkv.buf);
+        const K = l.qkv.K, nq = te.cfg.heads * te.cfg.headDim, nk = te.cfg.kvHeads * te.cfg.headDim;
+        save(`${c.out}.w.${i}.q`, all.subarray(0, nq * K));
+        save(`${c.out}.w.${i}.k`, all.subarray(nq * K, (nq + nk) * K));
+        save(`${c.out}.w.${i}.v`, all.subarray((nq + nk) * K, (nq + 2 * nk) * K));
+      } else {
+        for (const k of ["q", "k", "v"]) await dump(`${i}.${k}`, l[k]);
+      }
     }
     await dump("norm", te.norm);
     await dump("embed", te.table);
