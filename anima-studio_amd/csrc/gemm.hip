@@ -1309,6 +1309,129 @@ __global__ __launch_bounds__(256) void gemm_s3_t_kernel(F32WArgs a) {
   }
 }
 
+// fp32 activations x bf16 weights on the bf16 matrix cores (the text encoder's and the LLM
+// adapter's linears, app/gpu/gemm.js:17-55 semantics: fp32 products and sums of the bf16 weights).
+// x enters as its three bf16 terms (x = h + m + l exactly), the weight as it is, so every product
+// term is exact in fp32 and the MFMA sums are fp32: three bf16 MFMAs per 32x32x16 step in place of
+// eight fp32 ones (v_mfma_f32_32x32x2_f32).  W rows are the MFMA A operand (the C^T layout and
+// 16-byte epilogue of gemm_f32m_t_kernel).  A wave owns 32 rows x 64 columns (two MFMA tiles that
+// share one split of x); a workgroup is 2 column waves x KG k-groups over a 32 x 128 tile, k-group g
+// takes the 32-k chunks g, g + KG, ... (the next chunk's loads issued before this chunk's MFMAs),
+// and the k-groups' partial sums are added in a fixed tree order through LDS (deterministic).
+// Needs K % 32 == 0, N % 4 == 0 and 16-byte aligned x / W / out / bias / add / gate rows.
+template <int KG>
+__global__ __launch_bounds__(128 * KG) void gemm_bf16_s3_kernel(F32WArgs a) {
+  __shared__ float part[(KG > 1 ? KG / 2 : 1) * 2 * 32 * 64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lq = lane & 31, hf = lane >> 5;
+  const int wn = wave & 1, kg = wave >> 1;
+  const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 128 + wn * 64;
+  const int m = m0 + lq;
+  const bool mok = m < a.M;
+  const float* xr = a.x + (int64_t)(mok ? m : 0) * a.ldx + 8 * hf;
+  const uint16_t* W = (const uint16_t*)a.w;
+  int64_t wr[2];
+  bool nok[2];
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    const int n = n0 + 32 * t + lq;
+    nok[t] = n < a.N;
+    wr[t] = (int64_t)(nok[t] ? n : 0) * a.K + 8 * hf;
+  }
+  f32x16 acc[2] = {f32x16{}, f32x16{}};
+  const int nch = a.K / 32;
+  // chunk J: lane (l, h) loads x[m][32J + 16s + 8h .. +7] and W[n_t][same] for s = 0, 1.  Rows
+  // past M or N are clamped to row 0 and used as they are: such an x row only reaches output row
+  // m, such a W row only output column n, and neither is stored.
+#define B3_LOAD(J, X, WV)                                                        \
+  {                                                                              \
+    const int k_ = 32 * (J);                                                     \
+    _Pragma("unroll") for (int s = 0; s < 2; s++) {                              \
+      X[2 * s] = *(const float4*)(xr + k_ + 16 * s);                             \
+      X[2 * s + 1] = *(const float4*)(xr + k_ + 16 * s + 4);                     \
+      _Pragma("unroll") for (int t = 0; t < 2; t++) WV[t][s] = ld_bf8(W + wr[t] + k_ + 16 * s); \
+    }                                                                            \
+  }
+  // smallest terms first: l, m, h
+#define B3_MMA(X, WV)                                                                          \
+  {                                                                                            \
+    _Pragma("unroll") for (int s = 0; s < 2; s++) {                                            \
+      bf16x8 xs_[3];                                                                           \
+      split3(X[2 * s], X[2 * s + 1], xs_);                                                     \
+      _Pragma("unroll") for (int p = 2; p >= 0; p--)                                           \
+      _Pragma("unroll") for (int t = 0; t < 2; t++)                                            \
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(WV[t][s], xs_[p], acc[t], 0, 0, 0);   \
+    }                                                                                          \
+  }
+  int j = kg;
+  if (j < nch) {
+    float4 xa[4], xb[4];
+    bf16x8 wa[2][2], wb[2][2];
+    B3_LOAD(j, xa, wa)
+    for (;;) {
+      B3_LOAD(min(j + KG, nch - 1), xb, wb)
+      B3_MMA(xa, wa)
+      j += KG;
+      if (j >= nch) break;
+      B3_LOAD(min(j + KG, nch - 1), xa, wa)
+      B3_MMA(xb, wb)
+      j += KG;
+      if (j >= nch) break;
+    }
+  }
+#undef B3_LOAD
+#undef B3_MMA
+  if constexpr (KG > 1) {
+    // k-groups [h, 2h) hand their sums to k-groups [0, h); consecutive lanes on consecutive words
+#pragma unroll
+    for (int h = KG / 2; h >= 1; h >>= 1) {
+      if (kg >= h && kg < 2 * h) {
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) part[((((kg - h) * 2 + wn) * 2 + t) * 16 + r) * 64 + lane] = acc[t][r];
+      }
+      __syncthreads();
+      if (kg < h) {
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) acc[t][r] = acc[t][r] + part[(((kg * 2 + wn) * 2 + t) * 16 + r) * 64 + lane];
+      }
+      __syncthreads();
+    }
+  }
+  if (kg > 0 || !mok) return;
+  float* crow = a.out + (int64_t)m * a.ldc;
+#pragma unroll
+  for (int t = 0; t < 2; t++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const int nb = n0 + 32 * t + 8 * g + 4 * hf;
+      if (nb >= a.N) continue;
+      f32x4 v = {acc[t][4 * g] * a.alpha, acc[t][4 * g + 1] * a.alpha, acc[t][4 * g + 2] * a.alpha,
+                 acc[t][4 * g + 3] * a.alpha};
+      if (a.bias) v = v + *(const f32x4*)(a.bias + nb);
+      if (a.add) v = v + *(const f32x4*)(a.add + (int64_t)m * a.ld_add + nb);
+      if (a.act != ANIMA_ACT_NONE) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = apply_act(v[i], a.act);
+      }
+      f32x4* c = (f32x4*)(crow + nb);
+      if (a.epi == ANIMA_EPI_STORE) {
+        *c = v;
+      } else if (a.epi == ANIMA_EPI_RESID) {
+        *c = *c + v;
+      } else {
+        const f32x4 gt = *(const f32x4*)(a.gate + a.gate_off + nb);
+        const f32x4 o = *c;
+        f32x4 r;
+#pragma unroll
+        for (int i = 0; i < 4; i++) r[i] = __builtin_fmaf(gt[i], v[i], o[i]);
+        *c = r;
+      }
+    }
+}
+
 __global__ __launch_bounds__(256) void split3_kernel(const float* src, uint16_t* dst, int64_t n8, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (int64_t)gridDim.x * 256) {
     bf16x8 o[3];
@@ -1425,6 +1548,23 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
     if (!f32 && M <= GEMV_MAXM && K % 8 == 0 && ldx % 4 == 0 && al(d->x, 16) && al(W->w, 16)) {
       Launch L(c, "gemv.bf16", 2.0 * M * N * K, 2.0 * N * K);
       hipLaunchKernelGGL(gemv_f32w_kernel, dim3((N + 3) / 4), dim3(256), 0, c->stream, f);
+      return L.end();
+    }
+    const bool vec_out = N % 4 == 0 && ldc % 4 == 0 && al(d->out, 16) && (!W->bias || al(W->bias, 16)) &&
+                         (!d->add || (al(d->add, 16) && ld_add % 4 == 0)) &&
+                         (d->epilogue != ANIMA_EPI_GATED || al(d->gate + d->gate_off, 16));
+    if (!f32 && N > 256 && K % 32 == 0 && M <= 65535LL * 32 && ldx % 4 == 0 && al(d->x, 16) && al(W->w, 16) && vec_out) {
+      // bf16 matrix cores with x in three bf16 terms; k-groups per workgroup so that the grid
+      // holds about 2048 waves while every k-group keeps at least 4 chunks
+      Launch L(c, "gemm.bf16s3", 2.0 * M * N * K, 0.0);
+      const int64_t tiles = (int64_t)((N + 127) / 128) * ((M + 31) / 32);
+      const int nch = K / 32;
+      int kgs = 1;
+      while (kgs < 4 && tiles * 2 * kgs < 2048 && nch / (2 * kgs) >= 4) kgs *= 2;
+      const dim3 grid((unsigned)((N + 127) / 128), (unsigned)((M + 31) / 32));
+      if (kgs == 1) hipLaunchKernelGGL(gemm_bf16_s3_kernel<1>, grid, dim3(128), 0, c->stream, f);
+      else if (kgs == 2) hipLaunchKernelGGL(gemm_bf16_s3_kernel<2>, grid, dim3(256), 0, c->stream, f);
+      else hipLaunchKernelGGL(gemm_bf16_s3_kernel<4>, grid, dim3(512), 0, c->stream, f);
       return L.end();
     }
     Launch L(c, f32 ? "gemm.f32" : "gemm.bf16", 2.0 * M * N * K, 0.0);

@@ -396,6 +396,32 @@ def test_bf16_weight_linears(ctx):
         assert r < 1e-6
 
 
+@pytest.mark.parametrize("M,K,N,epi", [(2048, 256, 2048, "store"), (512, 1024, 4096, "store"),
+                                       (512, 2048, 1024, "resid"), (100, 3072, 1024, "gated"),
+                                       (33, 1024, 388, "store")])
+def test_bf16_weight_split_kernel(ctx, M, K, N, epi):
+    """bf16 weights with N > 256 and K % 32 == 0 (the text encoder's q/k/v, o, gate / up and down
+    shapes at 512 tokens, a 1 and a 2 k-group grid, ragged M and N): x enters the bf16 matrix cores
+    as three bf16 terms, so every product is exact and the sums are fp32; within 1e-6 of float64
+    for each epilogue."""
+    case(f"bf16 split kernel M={M} K={K} N={N} epilogue {epi}")
+    m = amd()
+    x = orc.randn(151 + K, M * K).reshape(M, K)
+    w32 = orc.bf16_round(0.05 * orc.randn(152 + N, N * K)).reshape(N, K)
+    wb = (w32.view(np.uint32) >> 16).astype(np.uint16)
+    bias = orc.randn(153, N).astype(np.float32)
+    y0 = orc.randn(154, M * N).reshape(M, N)
+    gate = orc.randn(155, N).astype(np.float32)
+    W = m.weight(m.W_BF16, N, K, ctx.upload(wb), bias=ctx.upload(bias))
+    dy = ctx.upload(y0)
+    e = {"store": m.EPI_STORE, "resid": m.EPI_RESID, "gated": m.EPI_GATED}[epi]
+    ctx.linear(W, M, dy, x=ctx.upload(x), epilogue=e, gate=ctx.upload(gate) if epi == "gated" else None)
+    r64 = x.astype(np.float64) @ w32.astype(np.float64).T + bias
+    ref = {"store": r64, "resid": y0 + r64, "gated": y0 + gate * r64}[epi]
+    r, _ = report(f"bf16 split M={M} K={K} N={N} {epi}", dy.numpy(), ref)
+    assert r < 1e-6
+
+
 @pytest.mark.parametrize("M", [4000, 200])
 def test_linear_add_term(ctx, M):
     """The optional fp32 add term (the LoRA delta input of gemm.js:189) after the bias: M=4000
