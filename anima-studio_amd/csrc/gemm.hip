@@ -1244,67 +1244,84 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_s3_skinny_kernel(F32WArgs 
 }
 
 // Split product with the operands swapped (the LoRA B side, K = rank): the C^T layout and 16-byte
-// epilogue of gemm_f32m_t_kernel.
+// epilogue of gemm_f32m_t_kernel.  A wave owns 32 rows x 32 NT columns (NT MFMA tiles sharing one
+// split of x, so a wave reads each x row once for NT tiles); workgroup = 2 x 2 waves.
+template <int NT>
 __global__ __launch_bounds__(256) void gemm_s3_t_kernel(F32WArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lq = lane & 31, hf = lane >> 5;
   const int m0 = blockIdx.y * 64 + (wave & 1) * 32;
-  const int n0 = blockIdx.x * 64 + (wave >> 1) * 32;
-  const int m = m0 + lq, n = n0 + lq;
-  const bool mok = m < a.M, nok = n < a.N;
+  const int n0 = blockIdx.x * 64 * NT + (wave >> 1) * 32 * NT;
+  const int m = m0 + lq;
+  const bool mok = m < a.M;
   const float* xr = a.x + (int64_t)(mok ? m : 0) * a.ldx + 8 * hf;
   const uint16_t* W = (const uint16_t*)a.w;
-  const int64_t plane = (int64_t)a.N * a.K, wr = (int64_t)(nok ? n : 0) * a.K + 8 * hf;
+  const int64_t plane = (int64_t)a.N * a.K;
+  int64_t wr[NT];
+  bool nok[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int n = n0 + 32 * t + lq;
+    nok[t] = n < a.N;
+    wr[t] = (int64_t)(nok[t] ? n : 0) * a.K + 8 * hf;
+  }
   const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  const bf16x8 z8 = {};
-  f32x16 acc = {};
+  f32x16 acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) acc[t] = f32x16{};
   for (int k0 = 0; k0 < a.K; k0 += 32) {  // two 16-k slices per load round trip
     float4 x[2][2];
-    bf16x8 wv[2][3], xs[3];
+    bf16x8 wv[NT][2][3], xs[3];
+    // unconditional loads at clamped in-bounds offsets, taken as loaded: rows past M or N only
+    // reach outputs that are not stored; a slice past K (K % 8 == 0: a lane's 8 values are all
+    // in or all out) loads k = 0 and its x values are zeroed where they are split
 #pragma unroll
-    for (int h = 0; h < 2; h++) {  // unconditional in-bounds loads (clamped offsets), then selects
+    for (int h = 0; h < 2; h++) {
       const int k = k0 + 16 * h;
-      const bool kok = k + 8 * hf < a.K;
-      const int kc = kok ? k : 0;
-      const float4 t0 = *(const float4*)(xr + kc), t1 = *(const float4*)(xr + kc + 4);
-      x[h][0] = mok && kok ? t0 : z4;
-      x[h][1] = mok && kok ? t1 : z4;
+      const int kc = k + 8 * hf < a.K ? k : 0;
+      x[h][0] = *(const float4*)(xr + kc);
+      x[h][1] = *(const float4*)(xr + kc + 4);
 #pragma unroll
-      for (int p = 0; p < 3; p++) {
-        const bf16x8 u = ld_bf8(W + p * plane + wr + kc);
-        wv[h][p] = nok && kok ? u : z8;
-      }
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int p = 0; p < 3; p++) wv[t][h][p] = ld_bf8(W + p * plane + wr[t] + kc);
     }
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      split3(x[h][0], x[h][1], xs);
-      acc = mfma_s3(wv[h], xs, acc);
+      const bool kok = k0 + 16 * h + 8 * hf < a.K;
+      split3(kok ? x[h][0] : z4, kok ? x[h][1] : z4, xs);
+#pragma unroll
+      for (int t = 0; t < NT; t++) acc[t] = mfma_s3(wv[t][h], xs, acc[t]);
     }
   }
   if (!mok) return;
   float* crow = a.out + (int64_t)m * a.ldc;
 #pragma unroll
-  for (int g = 0; g < 4; g++) {
-    const int nbk = n0 + 8 * g + 4 * hf;
-    if (nbk >= a.N) continue;
-    f32x4 v = {acc[4 * g] * a.alpha, acc[4 * g + 1] * a.alpha, acc[4 * g + 2] * a.alpha, acc[4 * g + 3] * a.alpha};
-    if (a.bias) v = v + *(const f32x4*)(a.bias + nbk);
-    if (a.add) v = v + *(const f32x4*)(a.add + (int64_t)m * a.ld_add + nbk);
-    if (a.act != ANIMA_ACT_NONE) {
+  for (int t = 0; t < NT; t++) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) v[i] = apply_act(v[i], a.act);
-    }
-    f32x4* c = (f32x4*)(crow + nbk);
-    if (a.epi == ANIMA_EPI_STORE) {
-      *c = v;
-    } else if (a.epi == ANIMA_EPI_RESID) {
-      *c = *c + v;
-    } else {
-      const f32x4 gt = *(const f32x4*)(a.gate + a.gate_off + nbk);
-      const f32x4 o = *c;
-      f32x4 r;
+    for (int g = 0; g < 4; g++) {
+      const int nbk = n0 + 32 * t + 8 * g + 4 * hf;
+      if (nbk >= a.N) continue;
+      f32x4 v = {acc[t][4 * g] * a.alpha, acc[t][4 * g + 1] * a.alpha, acc[t][4 * g + 2] * a.alpha,
+                 acc[t][4 * g + 3] * a.alpha};
+      if (a.bias) v = v + *(const f32x4*)(a.bias + nbk);
+      if (a.add) v = v + *(const f32x4*)(a.add + (int64_t)m * a.ld_add + nbk);
+      if (a.act != ANIMA_ACT_NONE) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) r[i] = __builtin_fmaf(gt[i], v[i], o[i]);
-      *c = r;
+        for (int i = 0; i < 4; i++) v[i] = apply_act(v[i], a.act);
+      }
+      f32x4* c = (f32x4*)(crow + nbk);
+      if (a.epi == ANIMA_EPI_STORE) {
+        *c = v;
+      } else if (a.epi == ANIMA_EPI_RESID) {
+        *c = *c + v;
+      } else {
+        const f32x4 gt = *(const f32x4*)(a.gate + a.gate_off + nbk);
+        const f32x4 o = *c;
+        f32x4 r;
+#pragma unroll
+        for (int i = 0; i < 4; i++) r[i] = __builtin_fmaf(gt[i], v[i], o[i]);
+        *c = r;
+      }
     }
   }
 }
@@ -1532,7 +1549,14 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
     else if (N % 4 == 0 && ldc % 4 == 0 && al(d->out, 16) && (!W->bias || al(W->bias, 16)) &&
              (!d->add || (al(d->add, 16) && ld_add % 4 == 0)) &&
              (d->epilogue != ANIMA_EPI_GATED || al(d->gate + d->gate_off, 16)))
-      hipLaunchKernelGGL(gemm_s3_t_kernel, dim3((N + 63) / 64, (unsigned)((M + 63) / 64)), dim3(256), 0, c->stream, f);
+    {
+      // four column tiles per wave where the grid stays large, one otherwise
+      const int64_t big = (int64_t)((N + 255) / 256) * ((M + 63) / 64);
+      if (big >= 1024)
+        hipLaunchKernelGGL(gemm_s3_t_kernel<4>, dim3((N + 255) / 256, (unsigned)((M + 63) / 64)), dim3(256), 0, c->stream, f);
+      else
+        hipLaunchKernelGGL(gemm_s3_t_kernel<1>, dim3((N + 63) / 64, (unsigned)((M + 63) / 64)), dim3(256), 0, c->stream, f);
+    }
     else
       return fail(c, ANIMA_E_ARG, "anima_linear: split weights with N > 256 need N %% 4 == 0 and 16-byte aligned out / bias / add / gate rows");
     return L.end();
