@@ -335,13 +335,61 @@ __global__ __launch_bounds__(256) void channel_norm_kernel(const float* X, const
   }
 }
 
+// The same per-row arithmetic for rows of at most 64 NV channels, CN_RPW rows per wave with every
+// load of the wave issued first: one row per wave kept too few bytes in flight (a row of 96
+// channels is 384 bytes) and left the pass at a third of the HBM rate.  Channels past cols read as
+// zero, which adds nothing to a lane's sum (0 + x^2 and x^2 + 0 are exact).
+constexpr int CN_RPW = 8;
+template <int NV>
+__global__ __launch_bounds__(256) void channel_norm_rows_kernel(const float* X, const float* G, float* Y, int64_t rows,
+                                                                int cols, int silu) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * CN_RPW;
+  float xv[CN_RPW][NV], g[NV];
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    const int c = lane + 64 * v;
+    g[v] = c < cols ? G[c] : 0.0f;
+  }
+#pragma unroll
+  for (int r = 0; r < CN_RPW; r++)
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+      const int c = lane + 64 * v;
+      xv[r][v] = row0 + r < rows && c < cols ? X[(row0 + r) * cols + c] : 0.0f;
+    }
+#pragma unroll
+  for (int r = 0; r < CN_RPW; r++) {
+    if (row0 + r >= rows) break;  // uniform across the wave
+    float ss = 0.0f;
+#pragma unroll
+    for (int v = 0; v < NV; v++) ss += xv[r][v] * xv[r][v];
+    ss = tree_sum_down(ss, 64);
+    const float rn = sqrtf((float)cols) / fmaxf(sqrtf(__shfl(ss, 0)), 1e-12f);
+    float* y = Y + (row0 + r) * cols;
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+      const int c = lane + 64 * v;
+      float o = xv[r][v] * rn * g[v];
+      if (silu) o = silu_f(o);
+      if (c < cols) y[c] = o;
+    }
+  }
+}
+
 int channel_norm_launch(anima_ctx* c, const float* x, const float* gamma, float* y, int64_t rows, int cols, int silu) {
   if (!x || !gamma || !y) return fail(c, ANIMA_E_ARG, "anima_channel_norm: null pointer");
   if (rows < 0 || cols < 1) return fail(c, ANIMA_E_ARG, "anima_channel_norm: rows=%lld cols=%d", (long long)rows, cols);
   if (rows == 0) return ANIMA_OK;
   Launch lc(c, "vae.channel_norm", 0.0, (double)rows * cols * 8);
-  hipLaunchKernelGGL(channel_norm_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, c->stream, x, gamma, y, rows,
-                     cols, silu ? 1 : 0);
+  const unsigned gr = (unsigned)((rows + 4 * CN_RPW - 1) / (4 * CN_RPW));
+  const int sl = silu ? 1 : 0;
+  if (cols <= 128) hipLaunchKernelGGL(channel_norm_rows_kernel<2>, dim3(gr), dim3(256), 0, c->stream, x, gamma, y, rows, cols, sl);
+  else if (cols <= 192) hipLaunchKernelGGL(channel_norm_rows_kernel<3>, dim3(gr), dim3(256), 0, c->stream, x, gamma, y, rows, cols, sl);
+  else if (cols <= 384) hipLaunchKernelGGL(channel_norm_rows_kernel<6>, dim3(gr), dim3(256), 0, c->stream, x, gamma, y, rows, cols, sl);
+  else
+    hipLaunchKernelGGL(channel_norm_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, c->stream, x, gamma, y, rows,
+                       cols, sl);
   return lc.end();
 }
 

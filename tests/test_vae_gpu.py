@@ -35,7 +35,7 @@ def from_bits(u16):
     return (np.asarray(u16, np.uint32) << 16).view(np.float32)
 
 
-@pytest.mark.parametrize("cols", [16, 96, 192, 384])
+@pytest.mark.parametrize("cols", [16, 96, 192, 384, 500])
 def test_channel_norm_matches_oracle(cols):
     m = amd()
     rng = np.random.default_rng(cols)
