@@ -280,6 +280,153 @@ static int tgemm_launch(anima_ctx* c, const TGemmArgs& p, int amode, int bmode, 
   return L.end();
 }
 
+// ---- conv3x3 on spatial tiles: a workgroup (8 waves) computes a 16 x 32 block of output pixels
+// for 96 output channels.  Per step of 32 input channels the input halo it needs (18 x 34 pixels in
+// output coordinates, sampled through the 2x nearest upsample when up; zero outside the image) and
+// the 9 x 96 x 32 weights are copied once into LDS, so every input value is read from memory once
+// per step instead of once per tap (the row-tiled implicit GEMM reads each pixel nine times).  The
+// next step's halo and weights are loaded into registers before this step's MFMAs.  Wave w owns
+// output rows 2w, 2w+1 (two 32-pixel MFMA row tiles) x three 32-channel column tiles; for tap
+// (ty, tx) the A row of output pixel (r, c) is halo pixel (r + ty, c + tx).  LDS rows are 64 bytes
+// (32 channels) with the 16-byte unit u of row q stored at slot u ^ ((q / 4) % 4), so the fragment
+// reads of 16 consecutive rows fall in distinct bank groups.  Products and sums are those of
+// tgemm_kernel (activation rounded to bf16, or split hi + lo with SPLIT; bf16 weights exact); only
+// the order of the k-terms differs (input-channel chunk outer, tap inner).
+constexpr int CT_TH = 16, CT_TW = 32, CT_HH = CT_TH + 2, CT_HW = CT_TW + 2, CT_HP = CT_HH * CT_HW;
+constexpr int CT_BN = 96, CT_CC = 32;
+constexpr int CT_HU = CT_HP * 4;          // 16-byte units of one halo plane (8 channels each)
+constexpr int CT_WU = 9 * CT_BN * 4;      // 16-byte units of the step's weights
+constexpr int CT_HJ = (CT_HU + 511) / 512, CT_WJ = (CT_WU + 511) / 512;
+
+__device__ __forceinline__ int ct_off(int row, int u) { return row * 64 + ((u ^ ((row >> 2) & 3)) << 4); }
+
+template <bool SPLIT>
+__global__ __launch_bounds__(512) void conv3x3_tile_kernel(TGemmArgs p) {
+  constexpr int NA = SPLIT ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) char lds[NA * CT_HP * 64 + 9 * CT_BN * 64];
+  char* const wl = lds + NA * CT_HP * 64;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, lq = lane & 31, hf = lane >> 5;
+  const int tx_n = p.W / CT_TW, ty_n = p.H / CT_TH;
+  const int tile = blockIdx.x, img = tile / (tx_n * ty_n), trem = tile - img * tx_n * ty_n;
+  const int oy0 = (trem / tx_n) * CT_TH, ox0 = (trem % tx_n) * CT_TW;
+  const int n0 = blockIdx.y * CT_BN;
+  const int Hin = p.up ? p.H >> 1 : p.H, Win = p.up ? p.W >> 1 : p.W;
+  const float* imgp = p.a + (int64_t)img * Hin * Win * p.cin;
+  const uint16_t* W = (const uint16_t*)p.b;
+
+  // staged loads of one step (input channels c0 .. c0 + 31); addresses past the image or the
+  // unit count are clamped to valid memory and their units stored as zeros / skipped
+  float4 hv[CT_HJ][2];
+  uint4 wv[CT_WJ];
+  unsigned hok = 0;
+  auto stage = [&](int c0) {
+    hok = 0;
+#pragma unroll
+    for (int j = 0; j < CT_HJ; j++) {
+      const int U = t + 512 * j, px = min(U, CT_HU - 1) >> 2, u = U & 3;
+      const int hy = px / CT_HW, hx = px - hy * CT_HW;
+      const int y = oy0 - 1 + hy, x = ox0 - 1 + hx;
+      const bool ok = U < CT_HU && y >= 0 && x >= 0 && y < p.H && x < p.W;
+      const int sy = ok ? (p.up ? y >> 1 : y) : 0, sx = ok ? (p.up ? x >> 1 : x) : 0;
+      const float* src = imgp + ((int64_t)sy * Win + sx) * p.cin + c0 + 8 * u;
+      hv[j][0] = *(const float4*)src;
+      hv[j][1] = *(const float4*)(src + 4);
+      hok |= (ok ? 1u : 0u) << j;
+    }
+#pragma unroll
+    for (int j = 0; j < CT_WJ; j++) {
+      const int V = min(t + 512 * j, CT_WU - 1), tap = V / (CT_BN * 4), rem = V - tap * CT_BN * 4;
+      const int n = rem >> 2, u = rem & 3;
+      wv[j] = *(const uint4*)(W + (int64_t)(n0 + n) * p.ldb + tap * p.cin + c0 + 8 * u);
+    }
+  };
+  auto publish = [&]() {
+#pragma unroll
+    for (int j = 0; j < CT_HJ; j++) {
+      const int U = t + 512 * j;
+      if (U >= CT_HU) break;
+      const int px = U >> 2, u = U & 3;
+      const bool ok = (hok >> j) & 1;
+      const float v[8] = {hv[j][0].x, hv[j][0].y, hv[j][0].z, hv[j][0].w, hv[j][1].x, hv[j][1].y, hv[j][1].z, hv[j][1].w};
+      bf16x8 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float f = ok ? v[e] : 0.0f;
+        hi[e] = to_bf16(f);
+        if (SPLIT) lo[e] = to_bf16(f - (float)hi[e]);
+      }
+      *(bf16x8*)(lds + ct_off(px, u)) = hi;
+      if constexpr (SPLIT) *(bf16x8*)(lds + CT_HP * 64 + ct_off(px, u)) = lo;
+    }
+#pragma unroll
+    for (int j = 0; j < CT_WJ; j++) {
+      const int V = t + 512 * j;
+      if (V >= CT_WU) break;
+      const int tap = V / (CT_BN * 4), rem = V - tap * CT_BN * 4;
+      *(uint4*)(wl + ct_off(tap * CT_BN + (rem >> 2), rem & 3)) = wv[j];
+    }
+  };
+
+  f32x16 acc[2][3];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 3; j++) acc[i][j] = f32x16{};
+
+  stage(0);
+  for (int c0 = 0; c0 < p.cin; c0 += CT_CC) {
+    if (c0 > 0) __syncthreads();  // every wave is done with the previous step's tiles
+    publish();
+    __syncthreads();
+    stage(min(c0 + CT_CC, p.cin - CT_CC));  // the next step's loads fly during these MFMAs
+#pragma unroll
+    for (int tap = 0; tap < 9; tap++) {
+      const int ty = tap / 3, tx = tap - 3 * ty;
+#pragma unroll
+      for (int s = 0; s < 2; s++) {
+        const int u = 2 * s + hf;
+        bf16x8 fa[2][NA], fb[3];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+          const int px = (2 * wave + i + ty) * CT_HW + lq + tx;
+#pragma unroll
+          for (int a = 0; a < NA; a++) fa[i][a] = *(const bf16x8*)(lds + a * CT_HP * 64 + ct_off(px, u));
+        }
+#pragma unroll
+        for (int j = 0; j < 3; j++) fb[j] = *(const bf16x8*)(wl + ct_off(tap * CT_BN + 32 * j + lq, u));
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+          for (int j = 0; j < 3; j++) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][0], fb[j], acc[i][j], 0, 0, 0);
+            if constexpr (SPLIT) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][1], fb[j], acc[i][j], 0, 0, 0);
+          }
+      }
+    }
+  }
+
+  // epilogue: register r of tile (i, j) holds pixel 8(r/4) + 4hf + r%4 of output row oy0 + 2w + i
+  // and channel n0 + 32j + lq
+#pragma unroll
+  for (int j = 0; j < 3; j++) {
+    const int n = n0 + 32 * j + lq;
+    const float bias = p.bias ? p.bias[n] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int y = oy0 + 2 * wave + i;
+      float* orow = p.c + (((int64_t)img * p.H + y) * p.W + ox0) * p.ldc + n;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int x = 8 * (r >> 2) + 4 * hf + (r & 3);
+        float v = acc[i][j][r] * p.alpha;
+        v = v + bias;
+        float* dst = orow + (int64_t)x * p.ldc;
+        *dst = p.resid ? *dst + v : v;
+      }
+    }
+  }
+}
+
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 int conv3x3_launch(anima_ctx* c, const anima_conv_desc* d) {
@@ -311,8 +458,18 @@ int conv3x3_launch(anima_ctx* c, const anima_conv_desc* d) {
   p.M = (int)M;
   p.N = d->cout;
   p.K = 9 * d->cin;
-  return tgemm_launch(c, p, TG_A_CONV, TG_B_W16, d->precision == ANIMA_PREC_FP32, 1,
-                      d->up ? "conv3x3.up" : "conv3x3", 2.0 * M * d->cout * 9.0 * d->cin);
+  const bool split = d->precision == ANIMA_PREC_FP32;
+  if (d->cin % CT_CC == 0 && d->cout % CT_BN == 0 && d->H % CT_TH == 0 && d->W % CT_TW == 0 &&
+      (int64_t)d->B * (d->H / CT_TH) * (d->W / CT_TW) <= 0x7fffffff && d->cout / CT_BN <= 65535) {
+    // spatial tiles with the input halo in LDS
+    const dim3 grid((unsigned)((int64_t)d->B * (d->H / CT_TH) * (d->W / CT_TW)), (unsigned)(d->cout / CT_BN));
+    Launch L(c, d->up ? "conv3x3.up" : "conv3x3", 2.0 * M * d->cout * 9.0 * d->cin, 0.0);
+    if (split) hipLaunchKernelGGL(conv3x3_tile_kernel<true>, grid, dim3(512), 0, c->stream, p);
+    else hipLaunchKernelGGL(conv3x3_tile_kernel<false>, grid, dim3(512), 0, c->stream, p);
+    return L.end();
+  }
+  return tgemm_launch(c, p, TG_A_CONV, TG_B_W16, split, 1, d->up ? "conv3x3.up" : "conv3x3",
+                      2.0 * M * d->cout * 9.0 * d->cin);
 }
 
 // ---- channel norm: one wave per row; lane t sums x[c]^2 over c = t, t + 64, ... in order, then the

@@ -455,7 +455,10 @@ async function main() {
   console.log(JSON.stringify({ ok: true, case: c.case }));
 }
 
-main().catch((e) => {
+// Exit explicitly once done: Node 12 runs the N-API finalizers still queued at teardown (device
+// buffers dropped without release()) from its environment cleanup, where creating their handle
+// scope can crash the process after all output is written.
+main().then(() => process.exit(0), (e) => {
   process.stderr.write(String(e && e.stack ? e.stack : e) + "\n");
   process.exit(1);
 });

@@ -61,6 +61,11 @@ CONV_CASES = [  # B, H, W (output), cin, cout, up, resid
     (2, 13, 11, 96, 3, False, True),
     (1, 32, 24, 192, 96, True, False),
     (1, 20, 20, 384, 192, True, True),
+    # spatial tiles (16 x 32 pixels x 96 channels, input halo in LDS): borders, several tiles and
+    # images, residual, upsample, several channel steps and column tiles
+    (2, 32, 64, 96, 96, False, True),
+    (1, 32, 32, 192, 192, True, False),
+    (1, 16, 32, 384, 384, False, False),
 ]
 
 
