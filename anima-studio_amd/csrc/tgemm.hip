@@ -281,7 +281,7 @@ static int tgemm_launch(anima_ctx* c, const TGemmArgs& p, int amode, int bmode, 
 }
 
 // ---- conv3x3 on spatial tiles: a workgroup (8 waves) computes a 16 x 32 block of output pixels
-// for 96 output channels.  Per step of 32 input channels the input halo it needs (18 x 34 pixels in
+// for BN = 96 output channels (or one 32-wide column tile when cout <= 32: the 3-channel head).  Per step of 32 input channels the input halo it needs (18 x 34 pixels in
 // output coordinates, sampled through the 2x nearest upsample when up; zero outside the image) and
 // the 9 x 96 x 32 weights are copied once into LDS, so every input value is read from memory once
 // per step instead of once per tap (the row-tiled implicit GEMM reads each pixel nine times).  The
@@ -294,24 +294,25 @@ static int tgemm_launch(anima_ctx* c, const TGemmArgs& p, int amode, int bmode, 
 // tgemm_kernel (activation rounded to bf16, or split hi + lo with SPLIT; bf16 weights exact); only
 // the order of the k-terms differs (input-channel chunk outer, tap inner).
 constexpr int CT_TH = 16, CT_TW = 32, CT_HH = CT_TH + 2, CT_HW = CT_TW + 2, CT_HP = CT_HH * CT_HW;
-constexpr int CT_BN = 96, CT_CC = 32, CT_NW = 8;
+constexpr int CT_CC = 32, CT_NW = 8;
 constexpr int CT_HU = CT_HP * 4;          // 16-byte units of one halo plane (8 channels each)
-constexpr int CT_WU = 9 * CT_BN * 4;      // 16-byte units of the step's weights
 
 __device__ __forceinline__ int ct_off(int row, int u) { return row * 64 + ((u ^ ((row >> 2) & 3)) << 4); }
 
-template <bool SPLIT, int NW>
+template <bool SPLIT, int NW, int BN>
 __global__ __launch_bounds__(64 * NW) void conv3x3_tile_kernel(TGemmArgs p) {
   constexpr int NA = SPLIT ? 2 : 1;
+  constexpr int NJ = BN / 32;              // 32-channel MFMA column tiles per wave
+  constexpr int CT_WU = 9 * BN * 4;        // 16-byte units of the step's weights
   constexpr int NT = 64 * NW, MT = CT_TH / NW;  // threads; output rows (32-pixel MFMA tiles) per wave
   constexpr int CT_HJ = (CT_HU + NT - 1) / NT, CT_WJ = (CT_WU + NT - 1) / NT;
-  __shared__ __attribute__((aligned(16))) char lds[NA * CT_HP * 64 + 9 * CT_BN * 64];
+  __shared__ __attribute__((aligned(16))) char lds[NA * CT_HP * 64 + 9 * BN * 64];
   char* const wl = lds + NA * CT_HP * 64;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63, lq = lane & 31, hf = lane >> 5;
   const int tx_n = p.W / CT_TW, ty_n = p.H / CT_TH;
   const int tile = blockIdx.x, img = tile / (tx_n * ty_n), trem = tile - img * tx_n * ty_n;
   const int oy0 = (trem / tx_n) * CT_TH, ox0 = (trem % tx_n) * CT_TW;
-  const int n0 = blockIdx.y * CT_BN;
+  const int n0 = blockIdx.y * BN;
   const int Hin = p.up ? p.H >> 1 : p.H, Win = p.up ? p.W >> 1 : p.W;
   const float* imgp = p.a + (int64_t)img * Hin * Win * p.cin;
   const uint16_t* W = (const uint16_t*)p.b;
@@ -337,9 +338,9 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_tile_kernel(TGemmArgs p) {
     }
 #pragma unroll
     for (int j = 0; j < CT_WJ; j++) {
-      const int V = min(t + NT * j, CT_WU - 1), tap = V / (CT_BN * 4), rem = V - tap * CT_BN * 4;
-      const int n = rem >> 2, u = rem & 3;
-      wv[j] = *(const uint4*)(W + (int64_t)(n0 + n) * p.ldb + tap * p.cin + c0 + 8 * u);
+      const int V = min(t + NT * j, CT_WU - 1), tap = V / (BN * 4), rem = V - tap * BN * 4;
+      const int n = min(n0 + (rem >> 2), p.N - 1), u = rem & 3;  // channels past cout: never stored
+      wv[j] = *(const uint4*)(W + (int64_t)n * p.ldb + tap * p.cin + c0 + 8 * u);
     }
   };
   auto publish = [&]() {
@@ -364,16 +365,16 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_tile_kernel(TGemmArgs p) {
     for (int j = 0; j < CT_WJ; j++) {
       const int V = t + NT * j;
       if (V >= CT_WU) break;
-      const int tap = V / (CT_BN * 4), rem = V - tap * CT_BN * 4;
-      *(uint4*)(wl + ct_off(tap * CT_BN + (rem >> 2), rem & 3)) = wv[j];
+      const int tap = V / (BN * 4), rem = V - tap * BN * 4;
+      *(uint4*)(wl + ct_off(tap * BN + (rem >> 2), rem & 3)) = wv[j];
     }
   };
 
-  f32x16 acc[MT][3];
+  f32x16 acc[MT][NJ];
 #pragma unroll
   for (int i = 0; i < MT; i++)
 #pragma unroll
-    for (int j = 0; j < 3; j++) acc[i][j] = f32x16{};
+    for (int j = 0; j < NJ; j++) acc[i][j] = f32x16{};
 
   stage(0);
   for (int c0 = 0; c0 < p.cin; c0 += CT_CC) {
@@ -387,7 +388,7 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_tile_kernel(TGemmArgs p) {
 #pragma unroll
       for (int s = 0; s < 2; s++) {
         const int u = 2 * s + hf;
-        bf16x8 fa[MT][NA], fb[3];
+        bf16x8 fa[MT][NA], fb[NJ];
 #pragma unroll
         for (int i = 0; i < MT; i++) {
           const int px = (MT * wave + i + ty) * CT_HW + lq + tx;
@@ -395,11 +396,11 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_tile_kernel(TGemmArgs p) {
           for (int a = 0; a < NA; a++) fa[i][a] = *(const bf16x8*)(lds + a * CT_HP * 64 + ct_off(px, u));
         }
 #pragma unroll
-        for (int j = 0; j < 3; j++) fb[j] = *(const bf16x8*)(wl + ct_off(tap * CT_BN + 32 * j + lq, u));
+        for (int j = 0; j < NJ; j++) fb[j] = *(const bf16x8*)(wl + ct_off(tap * BN + 32 * j + lq, u));
 #pragma unroll
         for (int i = 0; i < MT; i++)
 #pragma unroll
-          for (int j = 0; j < 3; j++) {
+          for (int j = 0; j < NJ; j++) {
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][0], fb[j], acc[i][j], 0, 0, 0);
             if constexpr (SPLIT) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][1], fb[j], acc[i][j], 0, 0, 0);
           }
@@ -410,8 +411,9 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_tile_kernel(TGemmArgs p) {
   // epilogue: register r of tile (i, j) holds pixel 8(r/4) + 4hf + r%4 of output row oy0 + 2w + i
   // and channel n0 + 32j + lq
 #pragma unroll
-  for (int j = 0; j < 3; j++) {
+  for (int j = 0; j < NJ; j++) {
     const int n = n0 + 32 * j + lq;
+    if (n >= p.N) continue;
     const float bias = p.bias ? p.bias[n] : 0.0f;
 #pragma unroll
     for (int i = 0; i < MT; i++) {
@@ -461,13 +463,21 @@ int conv3x3_launch(anima_ctx* c, const anima_conv_desc* d) {
   p.N = d->cout;
   p.K = 9 * d->cin;
   const bool split = d->precision == ANIMA_PREC_FP32;
-  if (d->cin % CT_CC == 0 && d->cout % CT_BN == 0 && d->H % CT_TH == 0 && d->W % CT_TW == 0 &&
-      (int64_t)d->B * (d->H / CT_TH) * (d->W / CT_TW) <= 0x7fffffff && d->cout / CT_BN <= 65535) {
+  const int bn = d->cout % 96 == 0 ? 96 : d->cout <= 32 ? 32 : 0;  // 96-channel tiles, or one 32-wide tile
+  if (bn && d->cin % CT_CC == 0 && d->H % CT_TH == 0 && d->W % CT_TW == 0 &&
+      (int64_t)d->B * (d->H / CT_TH) * (d->W / CT_TW) <= 0x7fffffff && (d->cout + bn - 1) / bn <= 65535) {
     // spatial tiles with the input halo in LDS
-    const dim3 grid((unsigned)((int64_t)d->B * (d->H / CT_TH) * (d->W / CT_TW)), (unsigned)(d->cout / CT_BN));
+    const dim3 grid((unsigned)((int64_t)d->B * (d->H / CT_TH) * (d->W / CT_TW)), (unsigned)((d->cout + bn - 1) / bn));
     Launch L(c, d->up ? "conv3x3.up" : "conv3x3", 2.0 * M * d->cout * 9.0 * d->cin, 0.0);
-    if (split) hipLaunchKernelGGL((conv3x3_tile_kernel<true, CT_NW>), grid, dim3(64 * CT_NW), 0, c->stream, p);
-    else hipLaunchKernelGGL((conv3x3_tile_kernel<false, CT_NW>), grid, dim3(64 * CT_NW), 0, c->stream, p);
+#define CTL(S, BN) hipLaunchKernelGGL((conv3x3_tile_kernel<S, CT_NW, BN>), grid, dim3(64 * CT_NW), 0, c->stream, p)
+    if (bn == 96) {
+      if (split) CTL(true, 96);
+      else CTL(false, 96);
+    } else {
+      if (split) CTL(true, 32);
+      else CTL(false, 32);
+    }
+#undef CTL
     return L.end();
   }
   return tgemm_launch(c, p, TG_A_CONV, TG_B_W16, split, 1, d->up ? "conv3x3.up" : "conv3x3",

@@ -66,6 +66,8 @@ CONV_CASES = [  # B, H, W (output), cin, cout, up, resid
     (2, 32, 64, 96, 96, False, True),
     (1, 32, 32, 192, 192, True, False),
     (1, 16, 32, 384, 384, False, False),
+    (1, 16, 32, 96, 3, False, True),  # one 32-wide column tile for 3 channels (the head)
+    (1, 32, 64, 64, 32, True, False),
 ]
 
 
