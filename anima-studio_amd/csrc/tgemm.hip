@@ -628,6 +628,47 @@ __global__ __launch_bounds__(256) void chunk_softmax_kernel(float* S, int64_t ld
   if (t == 0) rl[blockIdx.x] = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
 }
 
+// The same row softmax with the row held in registers (NPT values per thread, columns t + 256 i):
+// one read and one write of the score row instead of two reads and a write; the maximum, the
+// exponentials and the sums are taken in the same order as chunk_softmax_kernel (bit-identical).
+template <int NPT>
+__global__ __launch_bounds__(256) void chunk_softmax_reg_kernel(float* S, int64_t ld, float* rl, int cols, int valid,
+                                                                float scale, int row0, int causal) {
+  __shared__ float red[4];
+  float* s = S + (int64_t)blockIdx.x * ld;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int lim = causal ? min(valid, row0 + (int)blockIdx.x + 1) : valid;
+  float v[NPT];
+#pragma unroll
+  for (int i = 0; i < NPT; i++) {
+    const int c = t + 256 * i;
+    v[i] = c < cols ? s[c] : 0.0f;
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NPT; i++)
+    if (t + 256 * i < lim) mx = fmaxf(mx, v[i] * scale);
+  mx = wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NPT; i++) {
+    const int c = t + 256 * i;
+    if (c < cols) {
+      const float e = c < lim ? expf(v[i] * scale - mx) : 0.0f;
+      s[c] = e;
+      sum += e;
+    }
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) red[wave] = sum;
+  __syncthreads();
+  if (t == 0) rl[blockIdx.x] = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
+}
+
 // dst[d * ldd + j] = src[j * ld + d] for j < L, d < D (V -> V^T for the P.V product's B operand).
 __global__ __launch_bounds__(256) void transpose_kernel(const float* src, int64_t ld, int L, int D, float* dst, int64_t ldd) {
   __shared__ float tile[32][33];
@@ -718,8 +759,15 @@ int attention_chunked_launch(anima_ctx* c, const anima_attn_desc* d, const int* 
         if ((rc = tgemm_launch(c, qk, TG_A_ROWS, TG_B_F32, split, 1, "attn.chunk.qk", 2.0 * nr * Lk * D))) return rc;
         {
           Launch ls(c, "attn.chunk.softmax", 0.0, 8.0 * nr * Lk);
-          hipLaunchKernelGGL(chunk_softmax_kernel, dim3(nr), dim3(256), 0, c->stream, S, ldk4, L, Lk, valid, scale, r0,
-                             d->causal ? 1 : 0);
+          const int cz = d->causal ? 1 : 0;
+          if (Lk <= 256 * 16)
+            hipLaunchKernelGGL(chunk_softmax_reg_kernel<16>, dim3(nr), dim3(256), 0, c->stream, S, ldk4, L, Lk, valid, scale, r0, cz);
+          else if (Lk <= 256 * 32)
+            hipLaunchKernelGGL(chunk_softmax_reg_kernel<32>, dim3(nr), dim3(256), 0, c->stream, S, ldk4, L, Lk, valid, scale, r0, cz);
+          else if (Lk <= 256 * 64)
+            hipLaunchKernelGGL(chunk_softmax_reg_kernel<64>, dim3(nr), dim3(256), 0, c->stream, S, ldk4, L, Lk, valid, scale, r0, cz);
+          else
+            hipLaunchKernelGGL(chunk_softmax_kernel, dim3(nr), dim3(256), 0, c->stream, S, ldk4, L, Lk, valid, scale, r0, cz);
           if ((rc = ls.end())) return rc;
         }
         TGemmArgs pv{};
