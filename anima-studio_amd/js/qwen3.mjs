@@ -7,6 +7,12 @@
 import * as ops from "./ops.mjs";
 import { ropeTable } from "./common.mjs";
 import { concatLinears } from "./weights.mjs";
+import { native } from "./gpu.mjs";
+
+function releaseGraph(gpu, g) {
+  native.graphDestroy(gpu.ctx, g.graph);
+  for (const t of [g.out, g.x, g.cs]) t.release();
+}
 
 // q, k and v of a layer stacked into one [(H + 2 KH) HD, D] linear (one GEMM per layer instead
 // of three; the q/k RMSNorm and RoPE then run inside the attention's loads).  Formats that
@@ -88,15 +94,81 @@ export class Qwen3 {
     this.gpu = gpu;
     this.cfg = cfg;
     this.precision = "bf16"; // attention precision ("fp32": the fp32-MFMA kernel)
+    this.graphs = true; // replay the layers from a recorded HIP graph (per token count and precision)
+    this.graphCache = new Map();
   }
 
-  // ids -> Tensor [L, 1024] (qwen3.js:38-78)
+  // ids -> Tensor [L, 1024] (qwen3.js:38-78).  With this.graphs (the default) the 28 layers run as a
+  // HIP graph recorded once per (token count, attention precision): the host only uploads the
+  // embedding rows and replays it (the same kernels and arguments as the eager pass, so the same
+  // result), which removes the per-kernel launch cost of ~280 short kernels.
   async encode(ids) {
     const gpu = this.gpu;
-    const { hidden: D, heads: H, kvHeads: KH, headDim: HD } = this.cfg;
+    const { hidden: D, headDim: HD } = this.cfg;
     const Lt = ids.length;
-    let x = gpu.fromArray(await this.embedRows(ids), [Lt, D]);
+    const rows = await this.embedRows(ids);
+    // LoRA side paths (attachLoras) run eagerly: a graph recorded before an attach would not hold them
+    const lora = this.layers.some((l) => ["qkv", "q", "k", "v", "o", "gate", "up", "down"].some((k) => l[k] && l[k].lora && l[k].lora.length));
+    if (!this.graphs || lora) {
+      const x = gpu.fromArray(rows, [Lt, D]);
+      const cs = ropeTable(gpu, Lt, HD, this.cfg.theta);
+      const out = this.layersDevice(x, cs, Lt);
+      cs.release();
+      x.release();
+      return out;
+    }
+    const key = `${Lt}:${this.precision}`;
+    let g = this.graphCache.get(key);
+    if (!g) {
+      g = this.recordGraph(rows, Lt);
+      if (this.graphCache.size >= 4) {
+        const [k0, g0] = this.graphCache.entries().next().value;
+        this.graphCache.delete(k0);
+        releaseGraph(gpu, g0);
+      }
+    } else {
+      this.graphCache.delete(key);  // most recently used last
+    }
+    this.graphCache.set(key, g);
+    gpu.write(g.x, rows);
+    native.graphLaunch(gpu.ctx, g.graph);
+    const out = gpu.empty([Lt, D]);
+    gpu.copy(out, g.out, Lt * D * 4);
+    return out;
+  }
+
+  // The fixed residual-stream buffer, RoPE table and output of one token count, and the graph of
+  // the layers over them (recorded after one eager pass, so the pool already holds its buffers).
+  recordGraph(rows, Lt) {
+    const gpu = this.gpu;
+    const { hidden: D, headDim: HD } = this.cfg;
+    const x = gpu.fromArray(rows, [Lt, D]);
     const cs = ropeTable(gpu, Lt, HD, this.cfg.theta);
+    this.layersDevice(x, cs, Lt).release();
+    native.graphBegin(gpu.ctx);
+    let out = null, graph = 0;
+    try {
+      out = this.layersDevice(x, cs, Lt);
+    } finally {
+      if (out) graph = native.graphEnd(gpu.ctx);
+      else {
+        try {
+          native.graphDestroy(gpu.ctx, native.graphEnd(gpu.ctx));
+        } catch (e) {
+          // the capture was already invalid: graphEnd discarded it
+        }
+        x.release();
+        cs.release();
+      }
+    }
+    return { x, cs, out, graph };
+  }
+
+  // The decoder layers and the final RMSNorm on the residual stream x [Lt, D] (updated in place);
+  // returns the normed hidden states (a new tensor).
+  layersDevice(x, cs, Lt) {
+    const gpu = this.gpu;
+    const { hidden: D, heads: H, kvHeads: KH, headDim: HD } = this.cfg;
     for (const l of this.layers) {
       const h = ops.rmsnorm(gpu, x, l.ln1, D);
       const hr = ops.needsRotation(l.qkv || l.q) ? ops.rotate(gpu, h) : null;
@@ -141,10 +213,7 @@ export class Qwen3 {
       ops.linear(gpu, gu, l.down, { out: x, resid: true });
       gu.release();
     }
-    cs.release();
-    const out = ops.rmsnorm(gpu, x, this.norm, D);
-    x.release();
-    return out;
+    return ops.rmsnorm(gpu, x, this.norm, D);
   }
 
   release() {
@@ -154,6 +223,8 @@ export class Qwen3 {
       else if (t.release) t.release();
       for (const f of ["scale", "srel", "codebook", "bias"]) if (t[f] && t[f].release) t[f].release();
     };
+    for (const g of this.graphCache.values()) releaseGraph(this.gpu, g);
+    this.graphCache.clear();
     for (const l of this.layers || []) for (const key of Object.keys(l)) rel(l[key]);
     rel(this.norm);
     rel(this.table);

@@ -355,9 +355,18 @@ async function main() {
     const te = Qwen3.synthetic(gpu, new SyntheticWeights(gpu, 17), { layers: c.layers, vocab: c.vocab });
     for (const prec of ["fp32", "bf16"]) {
       te.precision = prec;
-      const y = await te.encode(c.ids);
-      save(`${c.out}.${prec}`, await gpu.read(y));
-      y.release();
+      // graph replays (recorded on the first call, replayed on the second) and the eager pass
+      te.graphs = true;
+      for (const tag of ["", ".replay"]) {
+        const y = await te.encode(c.ids);
+        save(`${c.out}.${prec}${tag}`, await gpu.read(y));
+        y.release();
+      }
+      te.graphs = false;
+      const ye = await te.encode(c.ids);
+      save(`${c.out}.${prec}.eager`, await gpu.read(ye));
+      ye.release();
+      te.graphs = true;
     }
     // a weight object holds its Tensor in .buf; a Tensor's .buf is its device address
     const dump = async (name, t) => save(`${c.out}.w.${name}`, await gpu.read(typeof t.buf === "object" ? t.buf : t));

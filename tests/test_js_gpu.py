@@ -359,9 +359,11 @@ def test_js_forward_graph(tmp_path):
 
 def test_js_qwen3_text_encoder(tmp_path):
     """Qwen3.encode (js/qwen3.mjs, the reference's qwen3.js forward on this build's ops: causal GQA
-    attention on the flash kernels, bf16 linears on the fp32 matrix cores, RMSNorm, 1D RoPE,
-    SiLU * up) on a seeded 2-layer synthetic encoder against the oracle's float64 restatement fed
-    the same weights: fp32 attention within 1e-5 relative L2, bf16 attention within 1e-2."""
+    attention on the flash kernels, bf16 linears on the split-bf16 matrix-core kernel, RMSNorm, 1D
+    RoPE, SiLU * up) on a seeded 2-layer synthetic encoder against the oracle's float64 restatement
+    fed the same weights: fp32 attention within 1e-5 relative L2, bf16 attention within 1e-2.  The
+    encodings come from the recorded HIP graph; its first call, a second replay and the eager pass
+    are bit-identical."""
     from oracle import qwen3_ref
 
     out = str(tmp_path / "te")
@@ -382,6 +384,10 @@ def test_js_qwen3_text_encoder(tmp_path):
     assert np.isfinite(got32).all() and np.isfinite(got16).all()
     assert report("qwen3 fp32 attention vs float64", got32, ref)[0] <= 1e-5
     assert report("qwen3 bf16 attention vs float64", got16, ref)[0] <= 1e-2
+    for prec in ("fp32", "bf16"):
+        g = read(f"{out}.{prec}")
+        assert np.array_equal(g, read(f"{out}.{prec}.replay")), f"{prec}: graph replay differs"
+        assert np.array_equal(g, read(f"{out}.{prec}.eager")), f"{prec}: graph vs eager"
 
 
 def test_js_llm_adapter(tmp_path):
