@@ -714,6 +714,28 @@ int attention_chunked_check(anima_ctx* c, const anima_attn_desc* d) {
   return ANIMA_OK;
 }
 
+// Key ranges of the chunked P.V product: 1 unless its grid has fewer than 1024 tiles; then up to
+// 8 ranges of at least 1024 keys, each a multiple of the 32-key k-tile (so a range never reads past
+// the valid keys).
+static int pv_splits(int rows, int D, int valid) {
+  const int64_t tiles = (int64_t)((rows + TG_BM - 1) / TG_BM) * ((D + TG_BN - 1) / TG_BN);
+  int ks = 1;
+  while (ks < 8 && tiles * ks < 1024 && valid % (2 * ks * TG_BK) == 0 && valid / (2 * ks) >= 1024) ks *= 2;
+  return ks;
+}
+
+// o[m][d] = (sum over the key ranges of part[z][m][d]) * rl[m]
+__global__ __launch_bounds__(256) void pv_sum_kernel(const float* part, int ks, int rows, int D, const float* rl, float* o,
+                                                     int64_t ldo) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t n = (int64_t)rows * D;
+  if (i >= n) return;
+  float acc = part[i];
+  for (int z = 1; z < ks; z++) acc = acc + part[(int64_t)z * n + i];
+  const int64_t m = i / D;
+  o[m * ldo + (i - m * D)] = acc * rl[m];
+}
+
 int attention_chunked_launch(anima_ctx* c, const anima_attn_desc* d, const int* kv_len) {
   const int group = d->group <= 0 ? 1 : d->group;
   const int D = d->D, Lq = d->Lq, Lk = d->Lk;
@@ -725,13 +747,17 @@ int attention_chunked_launch(anima_ctx* c, const anima_attn_desc* d, const int* 
   rows = std::min<int64_t>(rows, ((int64_t)Lq + TG_BM - 1) / TG_BM * TG_BM);
   const int64_t ldk4 = ((int64_t)Lk + 3) / 4 * 4;  // row stride of the scores and of V^T (16-byte rows)
   const size_t s_bytes = (size_t)rows * ldk4 * 4, l_bytes = ((size_t)rows * 4 + 255) / 256 * 256,
-               vt_bytes = (size_t)D * ldk4 * 4;
+               vt_bytes = ((size_t)D * ldk4 * 4 + 255) / 256 * 256;
+  int max_ks = 1;
+  for (int b = 0; b < d->B; b++) max_ks = std::max(max_ks, pv_splits((int)rows, D, kv_len[b]));
+  const size_t p_bytes = max_ks > 1 ? (size_t)max_ks * rows * D * 4 : 0;
   void* ws = nullptr;
-  int rc = workspace(c, s_bytes + l_bytes + vt_bytes, &ws);
+  int rc = workspace(c, s_bytes + l_bytes + vt_bytes + p_bytes, &ws);
   if (rc) return rc;
   float* S = (float*)ws;
   float* L = (float*)((char*)ws + s_bytes);
   float* VT = (float*)((char*)ws + s_bytes + l_bytes);
+  float* P = (float*)((char*)ws + s_bytes + l_bytes + vt_bytes);
   for (int b = 0; b < d->B; b++) {
     const int valid = kv_len[b];
     for (int h = 0; h < d->H; h++) {
@@ -775,14 +801,34 @@ int attention_chunked_launch(anima_ctx* c, const anima_attn_desc* d, const int* 
         pv.lda = ldk4;
         pv.b = VT;
         pv.ldb = ldk4;
-        pv.c = d->o + (int64_t)b * d->o_bstride + (int64_t)r0 * d->ldo + d->o_off + (int64_t)h * D;
-        pv.ldc = d->ldo;
-        pv.rs = L;
         pv.alpha = 1.0f;
         pv.M = nr;
         pv.N = D;
-        pv.K = valid;  // columns past the valid keys hold zero weights
-        if ((rc = tgemm_launch(c, pv, TG_A_ROWS, TG_B_F32, split, 1, "attn.chunk.pv", 2.0 * nr * valid * D))) return rc;
+        float* o = d->o + (int64_t)b * d->o_bstride + (int64_t)r0 * d->ldo + d->o_off + (int64_t)h * D;
+        // A grid of few tiles over a long key range (the VAE's 16384 keys x 384 dims: 384 tiles)
+        // splits the keys into ks ranges, products into ks partial outputs, summed and scaled by
+        // 1 / rowsum afterwards
+        const int ks = pv_splits(nr, D, valid);
+        if (ks > 1) {
+          pv.c = P;
+          pv.ldc = D;
+          pv.c_bs = (int64_t)nr * D;
+          pv.a_bs = valid / ks;
+          pv.b_bs = valid / ks;
+          pv.K = valid / ks;
+          if ((rc = tgemm_launch(c, pv, TG_A_ROWS, TG_B_F32, split, ks, "attn.chunk.pv", 2.0 * nr * valid * D))) return rc;
+          Launch lsum(c, "attn.chunk.pv_sum", 0.0, 4.0 * nr * D * (ks + 1));
+          const int64_t n = (int64_t)nr * D;
+          hipLaunchKernelGGL(pv_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, c->stream, P, ks, nr, D, L, o,
+                             d->ldo);
+          if ((rc = lsum.end())) return rc;
+        } else {
+          pv.c = o;
+          pv.ldc = d->ldo;
+          pv.rs = L;
+          pv.K = valid;  // columns past the valid keys hold zero weights
+          if ((rc = tgemm_launch(c, pv, TG_A_ROWS, TG_B_F32, split, 1, "attn.chunk.pv", 2.0 * nr * valid * D))) return rc;
+        }
       }
     }
   }
