@@ -1449,6 +1449,99 @@ __global__ __launch_bounds__(128 * KG) void gemm_bf16_s3_kernel(F32WArgs a) {
     }
 }
 
+// The same product (x in three bf16 terms x bf16 weights) for grids of at least 128 workgroups: a
+// workgroup (2 x 2 waves, each 32 rows x 64 columns) computes a 64 x 128 tile with both operand
+// tiles staged through double-buffered LDS, 32 k per step (x split once per workgroup as it is
+// stored; each x row read from memory once per 128 columns and each weight row once per 64 rows,
+// where the register-operand kernel reads them once per wave).  LDS rows of 40 bf16 (80 bytes)
+// give conflict-free 16-byte fragment reads.  Epilogue and C^T layout of gemm_bf16_s3_kernel.
+constexpr int B3L_ROW = 40;
+__global__ __launch_bounds__(256) void gemm_bf16_s3_lds_kernel(F32WArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16 xs[2][3][64 * B3L_ROW];
+  __shared__ __attribute__((aligned(16))) bf16 wsm[2][128 * B3L_ROW];
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, lq = lane & 31, hf = lane >> 5;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int mb = blockIdx.y * 64, nb = blockIdx.x * 128;
+  // loader roles: x row t/4, k (t%4)*8 .. +7; weight row t/2, k (t%2)*16 .. +15 (rows past M / N
+  // clamped to row 0: they only reach outputs that are not stored)
+  const int xr_row = t >> 2, xk = (t & 3) * 8, wr_row = t >> 1, wk = (t & 1) * 16;
+  const float* xsrc = a.x + (int64_t)(mb + xr_row < a.M ? mb + xr_row : 0) * a.ldx + xk;
+  const uint16_t* wsrc = (const uint16_t*)a.w + (int64_t)(nb + wr_row < a.N ? nb + wr_row : 0) * a.K + wk;
+  float4 xv0, xv1;
+  uint4 wv0, wv1;
+  auto load = [&](int k0) {
+    xv0 = *(const float4*)(xsrc + k0);
+    xv1 = *(const float4*)(xsrc + k0 + 4);
+    wv0 = *(const uint4*)(wsrc + k0);
+    wv1 = *(const uint4*)(wsrc + k0 + 8);
+  };
+  auto store = [&](int st) {
+    bf16x8 sp[3];
+    split3(xv0, xv1, sp);
+#pragma unroll
+    for (int p = 0; p < 3; p++) *(bf16x8*)(&xs[st][p][xr_row * B3L_ROW + xk]) = sp[p];
+    *(uint4*)(&wsm[st][wr_row * B3L_ROW + wk]) = wv0;
+    *(uint4*)(&wsm[st][wr_row * B3L_ROW + wk + 8]) = wv1;
+  };
+  f32x16 acc[2] = {f32x16{}, f32x16{}};
+  const int nch = a.K / 32;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int kc = 0; kc < nch; kc++) {
+    const int st = kc & 1;
+    if (kc + 1 < nch) load(32 * (kc + 1));
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      const int ko = 16 * s + 8 * hf;
+      bf16x8 fw[2], fx[3];
+#pragma unroll
+      for (int u = 0; u < 2; u++) fw[u] = *(const bf16x8*)(&wsm[st][(wn * 64 + 32 * u + lq) * B3L_ROW + ko]);
+#pragma unroll
+      for (int p = 0; p < 3; p++) fx[p] = *(const bf16x8*)(&xs[st][p][(wm * 32 + lq) * B3L_ROW + ko]);
+      // smallest terms first: l, m, h
+#pragma unroll
+      for (int p = 2; p >= 0; p--)
+#pragma unroll
+        for (int u = 0; u < 2; u++) acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[u], fx[p], acc[u], 0, 0, 0);
+    }
+    if (kc + 1 < nch) store(st ^ 1);
+    __syncthreads();
+  }
+  const int m = mb + wm * 32 + lq;
+  if (m >= a.M) return;
+  float* crow = a.out + (int64_t)m * a.ldc;
+  const int n0 = nb + wn * 64;
+#pragma unroll
+  for (int u = 0; u < 2; u++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const int nbk = n0 + 32 * u + 8 * g + 4 * hf;
+      if (nbk >= a.N) continue;
+      f32x4 v = {acc[u][4 * g] * a.alpha, acc[u][4 * g + 1] * a.alpha, acc[u][4 * g + 2] * a.alpha,
+                 acc[u][4 * g + 3] * a.alpha};
+      if (a.bias) v = v + *(const f32x4*)(a.bias + nbk);
+      if (a.add) v = v + *(const f32x4*)(a.add + (int64_t)m * a.ld_add + nbk);
+      if (a.act != ANIMA_ACT_NONE) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = apply_act(v[i], a.act);
+      }
+      f32x4* c = (f32x4*)(crow + nbk);
+      if (a.epi == ANIMA_EPI_STORE) {
+        *c = v;
+      } else if (a.epi == ANIMA_EPI_RESID) {
+        *c = *c + v;
+      } else {
+        const f32x4 gt = *(const f32x4*)(a.gate + a.gate_off + nbk);
+        const f32x4 o = *c;
+        f32x4 r;
+#pragma unroll
+        for (int i = 0; i < 4; i++) r[i] = __builtin_fmaf(gt[i], v[i], o[i]);
+        *c = r;
+      }
+    }
+}
+
 __global__ __launch_bounds__(256) void split3_kernel(const float* src, uint16_t* dst, int64_t n8, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (int64_t)gridDim.x * 256) {
     bf16x8 o[3];
@@ -1581,6 +1674,11 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
       // bf16 matrix cores with x in three bf16 terms; k-groups per workgroup so that the grid
       // holds about 2048 waves while every k-group keeps at least 4 chunks
       Launch L(c, "gemm.bf16s3", 2.0 * M * N * K, 0.0);
+      const int64_t ltiles = (int64_t)((N + 127) / 128) * ((M + 63) / 64);
+      if (ltiles >= 128 && (M + 63) / 64 <= 65535) {  // wide grids: LDS-staged tiles
+        hipLaunchKernelGGL(gemm_bf16_s3_lds_kernel, dim3((N + 127) / 128, (unsigned)((M + 63) / 64)), dim3(256), 0, c->stream, f);
+        return L.end();
+      }
       const int64_t tiles = (int64_t)((N + 127) / 128) * ((M + 31) / 32);
       const int nch = K / 32;
       int kgs = 1;
