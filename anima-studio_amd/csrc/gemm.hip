@@ -759,6 +759,7 @@ struct F32WArgs {
   const float* add;  // optional [M][ld_add] term after the bias
   int64_t ld_add;
   int wf32;  // fp32 weights (tile kernel only)
+  int64_t ldw = 0;  // weight row stride (0: K); the split-k LDS kernel reads k-slices of longer rows
 };
 
 // 64x64 tile, 256 threads x (4x4) outputs, k-tile 16 (the small-tile layout of gemm.js:17).
@@ -1465,8 +1466,11 @@ __global__ __launch_bounds__(256) void gemm_bf16_s3_lds_kernel(F32WArgs a) {
   // loader roles: x row t/4, k (t%4)*8 .. +7; weight row t/2, k (t%2)*16 .. +15 (rows past M / N
   // clamped to row 0: they only reach outputs that are not stored)
   const int xr_row = t >> 2, xk = (t & 3) * 8, wr_row = t >> 1, wk = (t & 1) * 16;
-  const float* xsrc = a.x + (int64_t)(mb + xr_row < a.M ? mb + xr_row : 0) * a.ldx + xk;
-  const uint16_t* wsrc = (const uint16_t*)a.w + (int64_t)(nb + wr_row < a.N ? nb + wr_row : 0) * a.K + wk;
+  // blockIdx.z: k-slice z of a split product (x + z x_gs, w + z w_gs, partial output out + z out_gs)
+  const int z = blockIdx.z;
+  const int64_t ldw = a.ldw ? a.ldw : a.K;
+  const float* xsrc = a.x + z * a.x_gs + (int64_t)(mb + xr_row < a.M ? mb + xr_row : 0) * a.ldx + xk;
+  const uint16_t* wsrc = (const uint16_t*)a.w + z * a.w_gs + (int64_t)(nb + wr_row < a.N ? nb + wr_row : 0) * ldw + wk;
   float4 xv0, xv1;
   uint4 wv0, wv1;
   auto load = [&](int k0) {
@@ -1510,7 +1514,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_s3_lds_kernel(F32WArgs a) {
   }
   const int m = mb + wm * 32 + lq;
   if (m >= a.M) return;
-  float* crow = a.out + (int64_t)m * a.ldc;
+  float* crow = a.out + z * a.out_gs + (int64_t)m * a.ldc;
   const int n0 = nb + wn * 64;
 #pragma unroll
   for (int u = 0; u < 2; u++)
@@ -1540,6 +1544,25 @@ __global__ __launch_bounds__(256) void gemm_bf16_s3_lds_kernel(F32WArgs a) {
         *c = r;
       }
     }
+}
+
+// The epilogue of a split-k product: out = epilogue(alpha * sum_z P[z] + bias + add) with the act
+// and store / residual / gated forms of the linear epilogues, one element per thread.
+__global__ __launch_bounds__(256) void splitk_epilogue_kernel(const float* P, int ks, F32WArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x, n_el = (int64_t)a.M * a.N;
+  if (i >= n_el) return;
+  const int64_t m = i / a.N;
+  const int n = (int)(i - m * a.N);
+  float acc = P[i];
+  for (int z = 1; z < ks; z++) acc = acc + P[z * n_el + i];
+  float v = acc * a.alpha;
+  if (a.bias) v = v + a.bias[n];
+  if (a.add) v = v + a.add[m * a.ld_add + n];
+  v = apply_act(v, a.act);
+  float* c = a.out + m * a.ldc + n;
+  if (a.epi == ANIMA_EPI_STORE) *c = v;
+  else if (a.epi == ANIMA_EPI_RESID) *c = *c + v;
+  else *c = __builtin_fmaf(a.gate[a.gate_off + n], v, *c);
 }
 
 __global__ __launch_bounds__(256) void split3_kernel(const float* src, uint16_t* dst, int64_t n8, int64_t n) {
@@ -1677,6 +1700,35 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
       const int64_t ltiles = (int64_t)((N + 127) / 128) * ((M + 63) / 64);
       if (ltiles >= 128 && (M + 63) / 64 <= 65535) {  // wide grids: LDS-staged tiles
         hipLaunchKernelGGL(gemm_bf16_s3_lds_kernel, dim3((N + 127) / 128, (unsigned)((M + 63) / 64)), dim3(256), 0, c->stream, f);
+        return L.end();
+      }
+      // small grids over long rows: k-slices of the LDS kernel into partial outputs, then one pass
+      // that sums them and applies the epilogue
+      int ks = 1;
+      while (ks < 8 && ltiles * ks < 256 && (K / (2 * ks)) % 32 == 0 && K / (2 * ks) >= 256) ks *= 2;
+      if (ks > 1 && (M + 63) / 64 <= 65535) {
+        void* tmp = nullptr;
+        int rc = anima_alloc(c, (size_t)ks * M * N * 4, &tmp);
+        if (rc) return rc;
+        F32WArgs g = f;
+        g.out = (float*)tmp;
+        g.ldc = N;
+        g.alpha = 1.0f;
+        g.bias = nullptr;
+        g.add = nullptr;
+        g.act = ANIMA_ACT_NONE;
+        g.epi = ANIMA_EPI_STORE;
+        g.K = K / ks;
+        g.ldw = K;
+        g.x_gs = K / ks;
+        g.w_gs = K / ks;
+        g.out_gs = (int64_t)M * N;
+        hipLaunchKernelGGL(gemm_bf16_s3_lds_kernel, dim3((N + 127) / 128, (unsigned)((M + 63) / 64), ks), dim3(256), 0,
+                           c->stream, g);
+        const int64_t n_el = (int64_t)M * N;
+        hipLaunchKernelGGL(splitk_epilogue_kernel, dim3((unsigned)((n_el + 255) / 256)), dim3(256), 0, c->stream,
+                           (const float*)tmp, ks, f);
+        anima_free(c, tmp);
         return L.end();
       }
       const int64_t tiles = (int64_t)((N + 127) / 128) * ((M + 31) / 32);
