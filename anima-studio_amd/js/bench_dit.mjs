@@ -178,10 +178,14 @@ async function main() {
       cfg: Number(arg("cfg", 4)), seed: 1, scheduler: "simple" };
     await pipe.generate(Object.assign({}, opts, { steps: 1 })); // first-use allocations
     const dev = await pipe.generate(opts);
+    // the same run with steps 1.. replayed from a HIP graph of the forward (opts.graph)
+    const devg = await pipe.generate(Object.assign({}, opts, { graph: true }));
     const host = await pipe.generateHost(opts);
     pipe.clearTimeCache();
     out.generate = { sampler: opts.sampler, steps: genSteps, cfg: opts.cfg,
-      device_ms_per_step: Number(dev.timings.perStep.toFixed(2)), host_loop_ms_per_step: Number(host.timings.perStep.toFixed(2)) };
+      device_ms_per_step: Number(dev.timings.perStep.toFixed(2)),
+      device_graph_ms_per_step: Number(devg.timings.perStep.toFixed(2)),
+      host_loop_ms_per_step: Number(host.timings.perStep.toFixed(2)) };
   }
   const teTokens = Number(arg("text-encoder", 0));
   if (teTokens > 0) {
