@@ -83,14 +83,51 @@ class SamplerDesc(ctypes.Structure):
                 ("c", ctypes.c_double * 10)]
 
 
+class Limits(ctypes.Structure):
+    _fields_ = [("max_buffer_size", _i64), ("max_binding_size", _i64), ("total_memory", _i64),
+                ("free_memory", _i64), ("workgroup_storage_size", ctypes.c_int32),
+                ("max_workgroup_size", ctypes.c_int32), ("max_workgroups_per_dimension", ctypes.c_int32),
+                ("compute_units", ctypes.c_int32), ("wavefront_size", ctypes.c_int32), ("clock_khz", ctypes.c_int32),
+                ("arch", ctypes.c_char * 64)]
+
+
+ABI_STRUCTS = {"anima_attn_desc": AttnDesc, "anima_linear_desc": LinearDesc, "anima_weight": Weight,
+               "anima_sampler_desc": SamplerDesc, "anima_conv_desc": ConvDesc, "anima_limits": Limits}
+
+
+def abi_mismatches(L):
+    """Differences between the ctypes restatement of the descriptor structs above and the
+    library's own layout (anima_abi_offset): sizes and the offset of every field."""
+    bad = []
+    for cname, S in ABI_STRUCTS.items():
+        size = L.anima_abi_offset(cname.encode(), None)
+        if size != ctypes.sizeof(S):
+            bad.append(f"sizeof({cname}) = {size}, binding {ctypes.sizeof(S)}")
+        for fname, _ in S._fields_:
+            off = L.anima_abi_offset(cname.encode(), fname.encode())
+            if off != getattr(S, fname).offset:
+                bad.append(f"{cname}.{fname} at {off}, binding {getattr(S, fname).offset}")
+    return bad
+
+
+def check_abi(L):
+    bad = abi_mismatches(L)
+    if bad:
+        raise RuntimeError("the ctypes binding does not match libanima.so's structs: " + "; ".join(bad))
+
+
 def lib():
-    """Loads libanima.so (raises if it is not built)."""
+    """Loads libanima.so (raises if it is not built, or if its descriptor layouts differ from the
+    structs restated here)."""
     global _LIB
     if _LIB is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
         L = ctypes.CDLL(LIB_PATH)
         P = ctypes.POINTER
+        L.anima_abi_offset.argtypes = [ctypes.c_char_p, ctypes.c_char_p]
+        L.anima_abi_offset.restype = _i64
+        check_abi(L)
         L.anima_init.argtypes = [ctypes.c_int, P(_vp)]
         L.anima_destroy.argtypes = [_vp]
         L.anima_last_error.argtypes = [_vp]
@@ -98,6 +135,7 @@ def lib():
         for n in ("anima_sync", "anima_flush", "anima_pool_trim", "anima_profile_reset", "anima_timer_start"):
             getattr(L, n).argtypes = [_vp]
         L.anima_mem_stats.argtypes = [_vp, P(ctypes.c_uint64), P(ctypes.c_uint64), P(ctypes.c_uint64)]
+        L.anima_device_limits.argtypes = [_vp, P(Limits)]
         L.anima_alloc.argtypes = [_vp, ctypes.c_size_t, P(_vp)]
         L.anima_free.argtypes = [_vp, _vp]
         for n in ("anima_h2d", "anima_d2h", "anima_d2d"):
@@ -235,6 +273,14 @@ class Context:
         a, p, q = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
         self._check(lib().anima_mem_stats(self.h, ctypes.byref(a), ctypes.byref(p), ctypes.byref(q)))
         return {"allocated": a.value, "peak": p.value, "pooled": q.value}
+
+    def limits(self):
+        """The device limits (anima_device_limits), as a dict."""
+        d = Limits()
+        self._check(lib().anima_device_limits(self.h, ctypes.byref(d)))
+        out = {f: getattr(d, f) for f, _ in Limits._fields_}
+        out["arch"] = d.arch.decode()
+        return out
 
     def trim(self):
         self._check(lib().anima_pool_trim(self.h))

@@ -64,9 +64,9 @@ struct anima_ctx {
   void* scratch = nullptr;
   // stream capture (anima_graph_begin .. anima_graph_end): buffers freed while capturing are
   // parked in cap_free, reused only by later allocations of the same capture, and owned by the
-  // graph at the end (its replays keep using them); cap_ws: the capture used the workspace
+  // graph at the end (its replays keep using them); a workspace requested while capturing is such
+  // a parked buffer of the requested size
   bool capturing = false;
-  bool cap_ws = false;
   std::unordered_map<size_t, std::vector<void*>> cap_free;
   std::unordered_set<anima_graph*> graphs;
 };

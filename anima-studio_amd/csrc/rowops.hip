@@ -637,8 +637,9 @@ __global__ __launch_bounds__(256) void layernorm_mod_reg_kernel(const float* X, 
   float* S = SH + rl * RS;
   // Half hh: every lane writes its elements of columns [hh * COLS / 2, (hh + 1) * COLS / 2)
   // (blocks hh * HB .. + HB), then the LR / 2 lanes whose 64 Hadamard columns lie in that half
-  // read them.  (LDS operations of one wave complete in order, and the row's lanes all belong to
-  // this wave: the second half's writes follow the first half's reads.)
+  // read them.  The row's lanes all belong to this wave and LDS operations of one wave complete
+  // in order; the wavefront-scope fences keep the compiler from moving a half's reads above its
+  // writes, or the second half's writes above the first half's reads.
   float w[64];
 #pragma unroll
   for (int hh = 0; hh < 2; hh++) {
@@ -654,6 +655,7 @@ __global__ __launch_bounds__(256) void layernorm_mod_reg_kernel(const float* X, 
             make_float4((t[0] - mean) * r * (1.0f + sc.x) + sh.x, (t[1] - mean) * r * (1.0f + sc.y) + sh.y,
                         (t[2] - mean) * r * (1.0f + sc.z) + sh.z, (t[3] - mean) * r * (1.0f + sc.w) + sh.w);
       }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     if (l / (LR / 2) == hh) {
       const int lh = l - hh * (LR / 2);
 #pragma unroll
@@ -665,6 +667,7 @@ __global__ __launch_bounds__(256) void layernorm_mod_reg_kernel(const float* X, 
         w[4 * q + 3] = t.w;
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   }
   if (rotate) hadamard64_quad(w, l & 3);
   if (Y) {

@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdarg>
+#include <cstddef>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -43,10 +44,17 @@ int hip_fail(anima_ctx* c, hipError_t e, const char* what) {
 
 int workspace(anima_ctx* c, size_t bytes, void** out) {
   if (c->capturing) {
-    if (bytes > c->ws_bytes)
-      return fail(c, ANIMA_E_STATE, "workspace of %zu bytes needed while capturing a graph (%zu available): run the work once before capturing",
-                  bytes, c->ws_bytes);
-    c->cap_ws = true;
+    // A graph's replays keep using the scratch its capture was handed, so the capture gets a pool
+    // buffer of the requested size, parked for the graph at once (the graph owns it from
+    // anima_graph_end on), and never the context's own workspace, which may have grown far
+    // larger for some earlier call.  Later requests of the same capture reuse parked buffers:
+    // the stream runs them in order.
+    void* p = nullptr;
+    int rc = anima_alloc(c, bytes, &p);
+    if (rc != ANIMA_OK) return rc;
+    anima_free(c, p);
+    *out = p;
+    return ANIMA_OK;
   }
   if (bytes > c->ws_bytes) {
     if (c->ws) {
@@ -157,7 +165,6 @@ static void drop_capture(anima_ctx* c) {
     }
   c->cap_free.clear();
   c->capturing = false;
-  c->cap_ws = false;
 }
 
 // The pinned staging ring of anima_h2d, allocated on first use (4 x 4 MiB of page-locked host
@@ -279,6 +286,30 @@ int anima_mem_stats(anima_ctx* c, uint64_t* allocated, uint64_t* peak, uint64_t*
   if (allocated) *allocated = c->allocated;
   if (peak) *peak = c->peak;
   if (pooled) *pooled = c->pooled;
+  return ANIMA_OK;
+}
+
+int anima_device_limits(anima_ctx* c, anima_limits* out) {
+  CHECK_CTX(c);
+  if (!out) return fail(c, ANIMA_E_ARG, "anima_device_limits: out is NULL");
+  hipDeviceProp_t p;
+  hipError_t e = hipGetDeviceProperties(&p, c->device);
+  if (e != hipSuccess) return hip_fail(c, e, "anima_device_limits (properties)");
+  size_t fr = 0, tot = 0;
+  e = hipMemGetInfo(&fr, &tot);
+  if (e != hipSuccess) return hip_fail(c, e, "anima_device_limits (memory)");
+  memset(out, 0, sizeof *out);
+  out->max_buffer_size = (int64_t)p.totalGlobalMem;
+  out->max_binding_size = (int64_t)p.totalGlobalMem;
+  out->total_memory = (int64_t)tot;
+  out->free_memory = (int64_t)fr;
+  out->workgroup_storage_size = (int32_t)p.sharedMemPerBlock;
+  out->max_workgroup_size = p.maxThreadsPerBlock;
+  out->max_workgroups_per_dimension = p.maxGridSize[0];
+  out->compute_units = p.multiProcessorCount;
+  out->wavefront_size = p.warpSize;
+  out->clock_khz = p.clockRate;
+  snprintf(out->arch, sizeof out->arch, "%s", p.gcnArchName);
   return ANIMA_OK;
 }
 
@@ -622,13 +653,66 @@ int anima_linear_grouped_bf16(anima_ctx* c, int G, int64_t M, int N, int K, cons
                                     out_gstride);
 }
 
+#define ABI_FIELD(T, f) {#T, #f, (int64_t)offsetof(T, f)}
+#define ABI_SIZE(T) {#T, nullptr, (int64_t)sizeof(T)}
+static const struct {
+  const char* type;
+  const char* field;
+  int64_t value;
+} k_abi[] = {
+    ABI_SIZE(anima_attn_desc), ABI_FIELD(anima_attn_desc, B), ABI_FIELD(anima_attn_desc, Lq),
+    ABI_FIELD(anima_attn_desc, Lk), ABI_FIELD(anima_attn_desc, H), ABI_FIELD(anima_attn_desc, D),
+    ABI_FIELD(anima_attn_desc, group), ABI_FIELD(anima_attn_desc, q), ABI_FIELD(anima_attn_desc, ldq),
+    ABI_FIELD(anima_attn_desc, q_off), ABI_FIELD(anima_attn_desc, q_bstride), ABI_FIELD(anima_attn_desc, k),
+    ABI_FIELD(anima_attn_desc, ldk), ABI_FIELD(anima_attn_desc, k_off), ABI_FIELD(anima_attn_desc, k_bstride),
+    ABI_FIELD(anima_attn_desc, v), ABI_FIELD(anima_attn_desc, ldv), ABI_FIELD(anima_attn_desc, v_off),
+    ABI_FIELD(anima_attn_desc, v_bstride), ABI_FIELD(anima_attn_desc, o), ABI_FIELD(anima_attn_desc, ldo),
+    ABI_FIELD(anima_attn_desc, o_off), ABI_FIELD(anima_attn_desc, o_bstride), ABI_FIELD(anima_attn_desc, scale),
+    ABI_FIELD(anima_attn_desc, kv_len), ABI_FIELD(anima_attn_desc, precision), ABI_FIELD(anima_attn_desc, q_norm),
+    ABI_FIELD(anima_attn_desc, k_norm), ABI_FIELD(anima_attn_desc, rope_cs), ABI_FIELD(anima_attn_desc, rope_sin_off),
+    ABI_FIELD(anima_attn_desc, eps), ABI_FIELD(anima_attn_desc, causal), ABI_FIELD(anima_attn_desc, kv_prep),
+    ABI_FIELD(anima_attn_desc, kv_prep_bytes),
+    ABI_SIZE(anima_weight), ABI_FIELD(anima_weight, kind), ABI_FIELD(anima_weight, N), ABI_FIELD(anima_weight, K),
+    ABI_FIELD(anima_weight, w), ABI_FIELD(anima_weight, scale), ABI_FIELD(anima_weight, srel),
+    ABI_FIELD(anima_weight, codebook), ABI_FIELD(anima_weight, bias),
+    ABI_SIZE(anima_linear_desc), ABI_FIELD(anima_linear_desc, M), ABI_FIELD(anima_linear_desc, W),
+    ABI_FIELD(anima_linear_desc, x), ABI_FIELD(anima_linear_desc, ldx), ABI_FIELD(anima_linear_desc, x_rotated),
+    ABI_FIELD(anima_linear_desc, xq), ABI_FIELD(anima_linear_desc, xs), ABI_FIELD(anima_linear_desc, out),
+    ABI_FIELD(anima_linear_desc, ldc), ABI_FIELD(anima_linear_desc, alpha), ABI_FIELD(anima_linear_desc, act),
+    ABI_FIELD(anima_linear_desc, epilogue), ABI_FIELD(anima_linear_desc, gate), ABI_FIELD(anima_linear_desc, gate_off),
+    ABI_FIELD(anima_linear_desc, acc_out), ABI_FIELD(anima_linear_desc, add), ABI_FIELD(anima_linear_desc, ld_add),
+    ABI_SIZE(anima_sampler_desc), ABI_FIELD(anima_sampler_desc, kind), ABI_FIELD(anima_sampler_desc, n),
+    ABI_FIELD(anima_sampler_desc, x), ABI_FIELD(anima_sampler_desc, v), ABI_FIELD(anima_sampler_desc, v_uncond),
+    ABI_FIELD(anima_sampler_desc, cfg), ABI_FIELD(anima_sampler_desc, sigma), ABI_FIELD(anima_sampler_desc, final_step),
+    ABI_FIELD(anima_sampler_desc, stage), ABI_FIELD(anima_sampler_desc, den_out), ABI_FIELD(anima_sampler_desc, old),
+    ABI_FIELD(anima_sampler_desc, old_d), ABI_FIELD(anima_sampler_desc, eps), ABI_FIELD(anima_sampler_desc, c),
+    ABI_SIZE(anima_conv_desc), ABI_FIELD(anima_conv_desc, B), ABI_FIELD(anima_conv_desc, H), ABI_FIELD(anima_conv_desc, W),
+    ABI_FIELD(anima_conv_desc, cin), ABI_FIELD(anima_conv_desc, cout), ABI_FIELD(anima_conv_desc, up),
+    ABI_FIELD(anima_conv_desc, x), ABI_FIELD(anima_conv_desc, w), ABI_FIELD(anima_conv_desc, bias),
+    ABI_FIELD(anima_conv_desc, out), ABI_FIELD(anima_conv_desc, resid), ABI_FIELD(anima_conv_desc, precision),
+    ABI_SIZE(anima_limits), ABI_FIELD(anima_limits, max_buffer_size), ABI_FIELD(anima_limits, max_binding_size),
+    ABI_FIELD(anima_limits, total_memory), ABI_FIELD(anima_limits, free_memory),
+    ABI_FIELD(anima_limits, workgroup_storage_size), ABI_FIELD(anima_limits, max_workgroup_size),
+    ABI_FIELD(anima_limits, max_workgroups_per_dimension), ABI_FIELD(anima_limits, compute_units),
+    ABI_FIELD(anima_limits, wavefront_size), ABI_FIELD(anima_limits, clock_khz), ABI_FIELD(anima_limits, arch),
+};
+#undef ABI_FIELD
+#undef ABI_SIZE
+
+int64_t anima_abi_offset(const char* type, const char* field) {
+  if (!type) return -1;
+  for (const auto& e : k_abi)
+    if (!strcmp(e.type, type) && ((!field && !e.field) || (field && e.field && !strcmp(field, e.field))))
+      return e.value;
+  return -1;
+}
+
 int anima_graph_begin(anima_ctx* c) {
   CHECK_CTX(c);
   NOT_CAPTURING(c, "anima_graph_begin");
   hipError_t e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed);
   if (e != hipSuccess) return hip_fail(c, e, "anima_graph_begin");
   c->capturing = true;
-  c->cap_ws = false;
   c->cap_free.clear();
   return ANIMA_OK;
 }
@@ -658,13 +742,7 @@ int anima_graph_end(anima_ctx* c, anima_graph** out) {
   for (auto& kv : c->cap_free)
     for (void* p : kv.second) g->owned.emplace_back(p, kv.first);
   c->cap_free.clear();
-  if (c->cap_ws && c->ws) {  // the replays use this workspace: the context takes a new one
-    g->owned.emplace_back(c->ws, c->ws_bytes);
-    c->ws = nullptr;
-    c->ws_bytes = 0;
-  }
   c->capturing = false;
-  c->cap_ws = false;
   c->graphs.insert(g);
   *out = g;
   return ANIMA_OK;

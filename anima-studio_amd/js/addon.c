@@ -126,36 +126,59 @@ static int typed(napi_env env, napi_value v, void** data, size_t* bytes) {
 
 /* ------------------------------------------------------------------ runtime */
 
-#define MAX_CTX 64
-static anima_ctx* g_ctx[MAX_CTX]; /* contexts created by init() and not yet destroyed */
-static double g_finalized = 0;    /* buffers reclaimed by finalizers (leak guard, for tests) */
+/* Contexts created by init() and not yet destroyed: a growable registry, so release() and the
+ * finalizers can tell whether a buffer's context still exists. */
+static anima_ctx** g_ctx = NULL;
+static size_t g_nctx = 0, g_capctx = 0;
+static double g_finalized = 0; /* buffers reclaimed by finalizers (leak guard, for tests) */
 
 static int ctx_live(anima_ctx* c) {
-  for (int i = 0; i < MAX_CTX; i++)
+  for (size_t i = 0; i < g_nctx; i++)
     if (c && g_ctx[i] == c) return 1;
   return 0;
 }
 
-
-static void ctx_finalize(napi_env env, void* data, void* hint) {
-  (void)env;
-  (void)hint;
-  (void)data; /* destroyed explicitly by destroy(); a leaked context is reclaimed at exit */
+static int ctx_register(anima_ctx* c) {
+  if (g_nctx == g_capctx) {
+    size_t cap = g_capctx ? 2 * g_capctx : 16;
+    anima_ctx** n = (anima_ctx**)realloc(g_ctx, cap * sizeof *n);
+    if (!n) return -1;
+    g_ctx = n;
+    g_capctx = cap;
+  }
+  g_ctx[g_nctx++] = c;
+  return 0;
 }
 
+static void ctx_unregister(anima_ctx* c) {
+  for (size_t i = 0; i < g_nctx; i++)
+    if (g_ctx[i] == c) {
+      g_ctx[i] = g_ctx[--g_nctx];
+      return;
+    }
+}
+
+/* The context travels as an external without a finalizer: a context is destroyed by destroy(),
+ * and one still open at exit goes with the process.  (A finalizer here would be queued by Node's
+ * environment teardown and run after the N-API environment is gone.) */
 static napi_value js_init(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   get_args(env, info, 1, argv);
   anima_ctx* c = NULL;
   int dev = (int)num(env, argv[0]);
   CHECK_RC(env, NULL, anima_init(dev, &c));
-  for (int i = 0; i < MAX_CTX; i++)
-    if (!g_ctx[i]) {
-      g_ctx[i] = c;
-      break;
-    }
+  if (ctx_register(c)) {
+    anima_destroy(c);
+    napi_throw_error(env, NULL, "init: out of host memory for the context registry");
+    return NULL;
+  }
   napi_value ext;
-  NAPI_CALL(env, napi_create_external(env, c, ctx_finalize, NULL, &ext));
+  if (napi_create_external(env, c, NULL, NULL, &ext) != napi_ok) {
+    ctx_unregister(c);
+    anima_destroy(c);
+    napi_throw_error(env, NULL, "init: napi_create_external failed");
+    return NULL;
+  }
   return ext;
 }
 
@@ -163,8 +186,7 @@ static napi_value js_destroy(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   get_args(env, info, 1, argv);
   anima_ctx* c = ctx_of(env, argv[0]);
-  for (int i = 0; i < MAX_CTX; i++)
-    if (g_ctx[i] == c) g_ctx[i] = NULL;
+  ctx_unregister(c);
   anima_destroy(c);
   return NULL;
 }
@@ -195,25 +217,56 @@ static napi_value js_free(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
-/* Device buffers owned by JS Tensors: an external whose finalizer returns the buffer to the pool
- * when the Tensor is garbage-collected without release() (the reference's buffers are reclaimed
- * by WebGPU the same way, app/gpu/device.js:10-24).  release() frees it at once and disarms the
- * finalizer.  Contexts destroyed in between are skipped (their memory is already gone). */
+/* Device buffers owned by JS Tensors.  A handle is a plain JS object wrapping a dev_buf; the
+ * wrap's finalizer returns the buffer to the pool when the Tensor is garbage-collected without
+ * release() (the reference's buffers are reclaimed by WebGPU the same way,
+ * app/gpu/device.js:10-24).  release() frees the buffer at once and leaves the finalizer only the
+ * host record to drop.  Contexts destroyed in between are skipped (their memory is already gone).
+ *
+ * Every dev_buf sits on a list together with the reference its wrap returned.  At environment
+ * teardown the cleanup hook below deletes those references before Node finalizes what is left:
+ * a finalizer queued by the teardown itself would run after the N-API environment has been freed
+ * (a crash at exit in Node 12), while a deleted reference is never finalized. */
 typedef struct dev_buf {
   anima_ctx* c;
   void* p;
   int live;
+  napi_ref ref;
+  struct dev_buf *prev, *next;
 } dev_buf;
 
+static dev_buf* g_bufs = NULL; /* every handle not yet finalized */
+
+static void buf_unlink(dev_buf* b) {
+  if (b->prev) b->prev->next = b->next;
+  else g_bufs = b->next;
+  if (b->next) b->next->prev = b->prev;
+  b->prev = b->next = NULL;
+}
+
 static void buf_finalize(napi_env env, void* data, void* hint) {
-  (void)env;
   (void)hint;
   dev_buf* b = (dev_buf*)data;
   if (b->live && ctx_live(b->c) && anima_free(b->c, b->p) == ANIMA_OK) g_finalized += 1;
+  buf_unlink(b);
+  if (b->ref) napi_delete_reference(env, b->ref);
   free(b);
 }
 
-/* allocHandle(ctx, bytes) -> external (the buffer's owner) */
+/* Environment cleanup: runs before N-API tears its environment down (hooks run newest first and
+ * this one is added after the environment exists). */
+static void bufs_cleanup(void* arg) {
+  napi_env env = (napi_env)arg;
+  while (g_bufs) {
+    dev_buf* b = g_bufs;
+    buf_unlink(b);
+    if (b->live && ctx_live(b->c)) anima_free(b->c, b->p);
+    if (b->ref) napi_delete_reference(env, b->ref);
+    free(b);
+  }
+}
+
+/* allocHandle(ctx, bytes) -> handle object (the buffer's owner) */
 static napi_value js_alloc_handle(napi_env env, napi_callback_info info) {
   napi_value argv[2];
   get_args(env, info, 2, argv);
@@ -221,7 +274,7 @@ static napi_value js_alloc_handle(napi_env env, napi_callback_info info) {
   size_t bytes = (size_t)num(env, argv[1]);
   void* p = NULL;
   CHECK_RC(env, c, anima_alloc(c, bytes, &p));
-  dev_buf* b = (dev_buf*)malloc(sizeof *b);
+  dev_buf* b = (dev_buf*)calloc(1, sizeof *b);
   if (!b) {
     anima_free(c, p);
     napi_throw_error(env, NULL, "allocHandle: out of host memory");
@@ -230,19 +283,24 @@ static napi_value js_alloc_handle(napi_env env, napi_callback_info info) {
   b->c = c;
   b->p = p;
   b->live = 1;
-  napi_value ext;
-  if (napi_create_external(env, b, buf_finalize, NULL, &ext) != napi_ok) {
+  napi_value obj;
+  if (napi_create_object(env, &obj) != napi_ok || napi_wrap(env, obj, b, buf_finalize, NULL, &b->ref) != napi_ok) {
     anima_free(c, p);
     free(b);
-    napi_throw_error(env, NULL, "allocHandle: napi_create_external failed");
+    napi_throw_error(env, NULL, "allocHandle: napi_wrap failed");
     return NULL;
   }
-  return ext;
+  b->next = g_bufs;
+  if (g_bufs) g_bufs->prev = b;
+  g_bufs = b;
+  return obj;
 }
 
 static dev_buf* buf_of(napi_env env, napi_value v) {
   void* p = NULL;
-  if (napi_get_value_external(env, v, &p) != napi_ok) return NULL;
+  napi_valuetype t;
+  if (napi_typeof(env, v, &t) != napi_ok || t != napi_object) return NULL;
+  if (napi_unwrap(env, v, &p) != napi_ok) return NULL;
   return (dev_buf*)p;
 }
 
@@ -303,6 +361,30 @@ static napi_value js_trim(napi_env env, napi_callback_info info) {
   anima_ctx* c = ctx_of(env, argv[0]);
   CHECK_RC(env, c, anima_pool_trim(c));
   return NULL;
+}
+
+/* deviceLimits(ctx) -> the adapter limits in WebGPU's names (app/gpu/device.js:63-88) */
+static napi_value js_device_limits(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  anima_limits L;
+  CHECK_RC(env, c, anima_device_limits(c, &L));
+  napi_value o, s;
+  NAPI_CALL(env, napi_create_object(env, &o));
+  napi_set_named_property(env, o, "maxBufferSize", make_num(env, (double)L.max_buffer_size));
+  napi_set_named_property(env, o, "maxStorageBufferBindingSize", make_num(env, (double)L.max_binding_size));
+  napi_set_named_property(env, o, "maxComputeWorkgroupStorageSize", make_num(env, (double)L.workgroup_storage_size));
+  napi_set_named_property(env, o, "maxComputeInvocationsPerWorkgroup", make_num(env, (double)L.max_workgroup_size));
+  napi_set_named_property(env, o, "maxComputeWorkgroupsPerDimension", make_num(env, (double)L.max_workgroups_per_dimension));
+  napi_set_named_property(env, o, "totalMemory", make_num(env, (double)L.total_memory));
+  napi_set_named_property(env, o, "freeMemory", make_num(env, (double)L.free_memory));
+  napi_set_named_property(env, o, "computeUnits", make_num(env, (double)L.compute_units));
+  napi_set_named_property(env, o, "subgroupSize", make_num(env, (double)L.wavefront_size));
+  napi_set_named_property(env, o, "clockKHz", make_num(env, (double)L.clock_khz));
+  NAPI_CALL(env, napi_create_string_utf8(env, L.arch, NAPI_AUTO_LENGTH, &s));
+  napi_set_named_property(env, o, "architecture", s);
+  return o;
 }
 
 static napi_value js_mem_stats(napi_env env, napi_callback_info info) {
@@ -800,7 +882,7 @@ static napi_value Init(napi_env env, napi_value exports) {
   napi_property_descriptor desc[] = {
       FN("init", js_init), FN("destroy", js_destroy), FN("sync", js_sync), FN("mark", js_mark), FN("waitMark", js_wait_mark), FN("alloc", js_alloc),
       FN("free", js_free), FN("allocHandle", js_alloc_handle), FN("handleAddr", js_handle_addr),
-      FN("release", js_release), FN("finalized", js_finalized), FN("trim", js_trim), FN("memStats", js_mem_stats), FN("h2d", js_h2d),
+      FN("release", js_release), FN("finalized", js_finalized), FN("trim", js_trim), FN("memStats", js_mem_stats), FN("deviceLimits", js_device_limits), FN("h2d", js_h2d),
       FN("d2h", js_d2h), FN("d2d", js_d2d), FN("profileEnable", js_profile_enable),
       FN("profileReset", js_profile_reset), FN("profileReport", js_profile_report),
       FN("timerStart", js_timer_start), FN("timerStop", js_timer_stop), FN("attention", js_attention),
@@ -814,6 +896,7 @@ static napi_value Init(napi_env env, napi_value exports) {
   };
 #undef FN
   if (napi_define_properties(env, exports, sizeof desc / sizeof desc[0], desc) != napi_ok) return NULL;
+  if (napi_add_env_cleanup_hook(env, bufs_cleanup, env) != napi_ok) return NULL;
   return exports;
 }
 

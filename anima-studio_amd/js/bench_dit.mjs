@@ -273,10 +273,7 @@ function vaeFlops(h, w) {
   return f + conv(HW, 96, 3);
 }
 
-// Exit explicitly once done: Node 12 runs the N-API finalizers still queued at teardown (device
-// buffers dropped without release()) from its environment cleanup, where creating their handle
-// scope can crash the process after all output is written.
-main().then(() => process.exit(0), (e) => {
+main().catch((e) => {
   process.stderr.write(String(e && e.stack ? e.stack : e) + "\n");
-  process.exit(1);
+  process.exitCode = 1;
 });

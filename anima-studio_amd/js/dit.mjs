@@ -319,6 +319,36 @@ export class AnimaDiT {
     };
   }
 
+  // Several prepared conditionings (prepareContext results, e.g. one per prompt from a cache) as
+  // one batched conditioning, in the given order: per block, each part's prepared K plane and V^T
+  // plane ([B][heads][Lkp][128] each) are copied side by side on the device.  The parts stay the
+  // caller's; release() of the result frees only the copies.
+  stackConds(conds) {
+    const gpu = this.gpu;
+    const Lk = conds[0].Lk, precision = conds[0].precision;
+    for (const c of conds)
+      if (c.Lk !== Lk || c.precision !== precision) throw new Error("stackConds: contexts must share Lk and precision");
+    const B = conds.reduce((a, c) => a + c.B, 0);
+    const kv = this.blocks.map((_, i) => {
+      const prep = gpu.empty([conds.reduce((a, c) => a + c.kv[i].prep.bytes, 0)], "u8");
+      const plane = prep.bytes / 2;
+      let off = 0;
+      for (const c of conds) {
+        const src = c.kv[i].prep, half = src.bytes / 2;
+        gpu.copy(prep.at(off), src.at(0), half);
+        gpu.copy(prep.at(plane + off), src.at(half), half);
+        off += half;
+      }
+      return { prep };
+    });
+    return {
+      kv, Lk, B, precision,
+      release() {
+        for (const e of kv) e.prep.release();
+      },
+    };
+  }
+
   // latents: B Float32Arrays [16, h, w]; cond: prepareContext(...) with the same B; tc: timeCond.
   // Returns B flow velocities [16, h, w] (app/models/dit.js:253-325).
   async forward(latents, h, w, cond, tc, onBlock) {
@@ -422,9 +452,10 @@ export class AnimaDiT {
 // forwardDevice recorded once into a HIP graph (anima_graph_*) and replayed: the same ~600
 // kernels with the same arguments, submitted as one graph launch instead of one launch each.
 // A replay reads `lat` and the graph's timeCond slot as they are when it runs and overwrites
-// `v`.  Capture needs the pool and the workspace to hold every buffer the forward uses and the
-// RoPE table to be cached: with `warm` it runs the forward once eagerly first; without, the
-// caller has just run forwardDevice for the same shapes.  Recording itself executes nothing.
+// `v`.  Capture needs the RoPE table to be cached (and is cheapest when the pool already holds
+// the forward's buffers): with `warm` it runs the forward once eagerly first; without, the caller
+// has just run forwardDevice for the same shapes.  The attention scratch of the captured calls is
+// the graph's own (sized for them), not the context's workspace.  Recording itself executes nothing.
 export class ForwardGraph {
   constructor(dit, graph, lat, v, tc) {
     this.dit = dit;

@@ -105,9 +105,11 @@ export class GPU {
   constructor(ctx) {
     this.ctx = ctx;
     this.profiler = null;
-    this.info = { vendor: "AMD", architecture: "gfx950", description: "MI355X (HIP)" };
-    this.limits = {};
-    this.maxBinding = Number.MAX_SAFE_INTEGER;
+    // adapter limits in WebGPU's names (app/gpu/device.js:83-88): HIP caps neither one buffer nor
+    // one binding below the device memory, so maxBinding is the device's global memory
+    this.limits = native.deviceLimits(ctx);
+    this.info = { vendor: "AMD", architecture: this.limits.architecture.split(":")[0], description: "MI355X (HIP)" };
+    this.maxBinding = Math.min(this.limits.maxStorageBufferBindingSize, this.limits.maxBufferSize);
     this.pool = new Pool(this);
   }
 

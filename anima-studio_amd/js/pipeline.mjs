@@ -3,7 +3,8 @@
 // -> CFG combine + denoised + sampler update in one kernel (anima_sampler_step), then the latent
 // comes back once at the end and, when the pipeline holds a VAE decoder (vae.mjs), is decoded to
 // the image as the reference's generate does (pipeline.js:284-292).  The caller passes the
-// conditioning made by AnimaDiT.prepareContext ([positive] or, with CFG, [positive, negative]).
+// conditioning made by AnimaDiT.prepareContext ([positive] or, with CFG, [positive, negative]), or
+// the per-prompt conditionings of encode() (cached per prompt, as pipeline.js:192-211 caches them).
 //
 // Noise is drawn on the host with the reference's torch.randn port (rng.mjs), in the reference's
 // order, and uploaded; drawing it after the step's DiT work is enqueued overlaps it with that work.
@@ -14,20 +15,65 @@
 
 import { native } from "./gpu.mjs";
 import { TorchGenerator } from "./rng.mjs";
-import { ForwardGraph } from "./dit.mjs";
+import { ForwardGraph, adapt } from "./dit.mjs";
 import { SCHEDULERS, SamplerPlan, sample } from "./samplers.mjs";
 import { loraGeneration } from "./lora.mjs";
 
 const TIME_CACHE_MAX = 64;
 
 export class LatentPipeline {
-  // opts.vae: a VAEDecoder; generate then also returns the decoded image
+  // opts.vae: a VAEDecoder; generate then also returns the decoded image.  opts.te (a Qwen3 text
+  // encoder, qwen3.mjs) and opts.adapter (the LLM adapter, dit.mjs) enable encode().
   constructor(gpu, dit, opts) {
+    const o = opts || {};
     this.gpu = gpu;
     this.dit = dit;
-    this.vae = opts && opts.vae ? opts.vae : null;
+    this.vae = o.vae || null;
+    this.te = o.te || null;
+    this.adapter = o.adapter || null;
     this.timeCache = new Map(); // key -> timeCond result (device tensors), in insertion (LRU) order
-    this.stats = { timeCondHits: 0, timeCondMisses: 0 };
+    this.ctxCache = new Map(); // prompt key -> prepared conditioning (B = 1)
+    this.ctxGeneration = loraGeneration();
+    this.stats = { timeCondHits: 0, timeCondMisses: 0, encodeHits: 0, encodeMisses: 0 };
+  }
+
+  // Prompt -> conditioning ready for the DiT (AnimaPipeline.encode, app/pipeline.js:192-211): token
+  // ids -> te.encode -> the LLM adapter -> prepareContext (per-block cross-attention K/V, converted
+  // once to the attention's operand layout).  The tokenizer is not part of this build: `prompt` is
+  // what the reference's tokenizer.encode returns, { qwenIds, t5Ids, t5Weights }, plus an optional
+  // `key` (the prompt text; default: the ids).  Only the prompts in `keep` (keys or prompts; default
+  // this one) stay cached -- the reference keeps the positive and negative prompt of the current
+  // image, each entry holding every block's K/V -- and attaching LoRAs (a new LoRA generation)
+  // clears the cache, as applyLoras -> clearContexts does.  The result belongs to the cache.
+  async encode(prompt, keep) {
+    if (!this.te || !this.adapter) throw new Error("encode: the pipeline was built without opts.te / opts.adapter");
+    const key = promptKey(prompt);
+    const keys = (keep || [prompt]).map((k) => (typeof k === "string" ? k : promptKey(k)));
+    if (this.ctxGeneration !== loraGeneration()) {
+      this.clearContexts();
+      this.ctxGeneration = loraGeneration();
+    }
+    for (const [k, t] of this.ctxCache)
+      if (!keys.includes(k)) {
+        t.release();
+        this.ctxCache.delete(k);
+      }
+    if (this.ctxCache.has(key)) {
+      this.stats.encodeHits++;
+      return this.ctxCache.get(key);
+    }
+    this.stats.encodeMisses++;
+    const hidden = await this.te.encode(prompt.qwenIds);
+    const ctx = await adapt(this.gpu, this.adapter, hidden, prompt.t5Ids, prompt.t5Weights);
+    hidden.release();
+    const cond = this.dit.prepareContext([ctx]);
+    this.ctxCache.set(key, cond);
+    return cond;
+  }
+
+  clearContexts() {
+    for (const t of this.ctxCache.values()) t.release();
+    this.ctxCache.clear();
   }
 
   // dit.timeCond(sigma), cached.  The key includes the LoRA generation, so attaching LoRAs
@@ -58,6 +104,7 @@ export class LatentPipeline {
   }
 
   // opts: { cond, cfg = 1, width, height, steps, sampler, seed = 0, shift = 3, scheduler = "simple",
+  //         (cond: one batched conditioning, or an array of them such as [encode(pos), encode(neg)])
   //         onStep(i, readDenoised), onProgress({ phase, step, steps, frac }), signal, graph = false,
   //         decode = true (with a VAE) }.
   //         cond.B must be 2 when cfg != 1 (positive, negative), else 1.
@@ -68,6 +115,15 @@ export class LatentPipeline {
   // Returns { latent: Float32Array [16, h, w], image ({ data: RGBA bytes, width, height } or null),
   // sigmas, timings }.
   async generate(opts) {
+    // an array of conditionings (e.g. [encode(positive), encode(negative)]) runs as one batch
+    if (Array.isArray(opts.cond)) {
+      const cond = this.dit.stackConds(opts.cond);
+      try {
+        return await this.generate(Object.assign({}, opts, { cond }));
+      } finally {
+        cond.release();
+      }
+    }
     const gpu = this.gpu;
     const { cond, width, height, steps, sampler, signal } = opts;
     const onProgress = opts.onProgress || (() => {});
@@ -196,4 +252,9 @@ export class LatentPipeline {
     const ms = Date.now() - t0;
     return { latent, sigmas, timings: { sample: ms, perStep: ms / (sigmas.length - 1) } };
   }
+}
+
+function promptKey(p) {
+  if (p.key !== undefined) return String(p.key);
+  return JSON.stringify([p.qwenIds, p.t5Ids, p.t5Weights]);
 }

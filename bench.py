@@ -31,10 +31,10 @@ INT8_PEAK_TOPS = 5033.2
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    # the device raises its clocks over ~25 ms of sustained load: 100 warmup steps (~30 ms) time
-    # the steady state
+    # the device raises its clocks over ~25 ms of sustained load; every leg settles for ~30 ms of
+    # device time after its warmup steps, so the timed steps see the steady state
     p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-dit", action="store_true", help="skip the full DiT step leg")
     p.add_argument("--dit-steps", type=int, default=5)
@@ -148,7 +148,10 @@ def causal_attention(m, ctx, np):
 FP32_PEAK_TFLOPS = 157.3
 
 
-def settle(ctx, call, device_ms=30.0):
+SETTLE_MS = 30.0
+
+
+def settle(ctx, call, device_ms=SETTLE_MS):
     """Runs `call` back to back until about `device_ms` of device time has passed (at least 3
     calls): the device raises its clocks over ~25 ms of sustained load, so the timings that
     follow see the steady state."""
@@ -402,7 +405,11 @@ def main():
         for _ in range(args.warmup):
             step()
         ctx.sync()
-        print(f"bench: warmup {args.warmup} done", file=sys.stderr, flush=True)
+        # the clock ramp takes ~25 ms of sustained load: whatever --warmup says, the timed steps
+        # follow at least ~30 ms of back-to-back steps, like every other leg below
+        settle(ctx, step)
+        print(f"bench: warmup {args.warmup} done (+ {SETTLE_MS:.0f} ms of device time settled)", file=sys.stderr,
+              flush=True)
         ctx.timer_start()
         for _ in range(args.steps):
             step()
@@ -450,6 +457,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        # after the warmup steps, the same step back to back for this much device time (clock ramp)
+        "settle_device_ms": SETTLE_MS,
         "ms_per_step": round(ms, 5),
         "higher_is_better": True,
         "scaling": "weak",

@@ -49,6 +49,24 @@ int anima_sync(anima_ctx* ctx);
 int anima_flush(anima_ctx* ctx);
 /* BufferPool.allocated / peak (app/gpu/device.js:26-57) plus bytes parked in free lists. */
 int anima_mem_stats(anima_ctx* ctx, uint64_t* allocated, uint64_t* peak, uint64_t* pooled);
+/* The adapter limits of app/gpu/device.js:63-88 (GPU.limits, GPU.maxBinding) for this context's
+ * device.  WebGPU caps one buffer and one binding; HIP caps neither below the device memory, so
+ * both report the device's global memory, and a caller sizing chunks from them (the score chunks
+ * of app/gpu/ops.js:177-181) gets the same bound the library's own chunked path respects
+ * (anima_attention: score chunks of at most 1 GiB). */
+typedef struct {
+  int64_t max_buffer_size;             /* maxBufferSize: the device's global memory */
+  int64_t max_binding_size;            /* maxStorageBufferBindingSize: the same */
+  int64_t total_memory, free_memory;   /* hipMemGetInfo at the call */
+  int32_t workgroup_storage_size;      /* maxComputeWorkgroupStorageSize: LDS bytes per workgroup */
+  int32_t max_workgroup_size;          /* maxComputeInvocationsPerWorkgroup */
+  int32_t max_workgroups_per_dimension; /* maxComputeWorkgroupsPerDimension (grid x) */
+  int32_t compute_units;
+  int32_t wavefront_size;
+  int32_t clock_khz;                   /* peak shader clock */
+  char arch[64];                       /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+} anima_limits;
+int anima_device_limits(anima_ctx* ctx, anima_limits* out);
 /* BufferPool.get (app/gpu/device.js:40-48): device memory from 1/8-power-of-two size buckets. */
 int anima_alloc(anima_ctx* ctx, size_t bytes, void** out);
 /* Tensor.release / BufferPool.put (app/gpu/device.js:20-23, 49-52): back to its bucket.
@@ -85,15 +103,22 @@ int anima_profile_report(anima_ctx* ctx, char* buf, size_t len);
 int anima_timer_start(anima_ctx* ctx);
 int anima_timer_stop(anima_ctx* ctx, float* ms);
 
+/* ABI self-description, for bindings that restate the descriptor structs below (ctypes, FFI):
+ * the byte offset of `field` in the struct named `type` -- "anima_attn_desc", "anima_linear_desc",
+ * "anima_weight", "anima_sampler_desc", "anima_conv_desc", "anima_limits" -- or the struct's size when `field` is
+ * NULL; -1 for a name this library does not know.  No counterpart in the reference (its op layer
+ * has no C ABI); it lets a binding refuse to load when its layout differs from the library's. */
+int64_t anima_abi_offset(const char* type, const char* field);
+
 /* Recorded submission.  The reference records its dispatches into command encoders and submits
  * them in batches (app/gpu/device.js:1-5, 183-216), re-recording every forward.  Here the
  * context stream's work between anima_graph_begin and anima_graph_end is captured once into a
  * HIP graph and anima_graph_launch replays it (same kernels, same arguments, same device
  * addresses; inputs are read as they are when the replay runs).
- * While capturing, host copies (anima_h2d, anima_d2h), synchronization (anima_sync,
- * anima_pool_trim, the profiler report, the timer) and workspace growth fail with
- * ANIMA_E_STATE: run the work once eagerly first, so the pool and the workspace already hold
- * what it needs.  Buffers freed during the capture stay reserved for the graph until
+ * While capturing, host copies (anima_h2d, anima_d2h) and synchronization (anima_sync,
+ * anima_pool_trim, the profiler report, the timer) fail with ANIMA_E_STATE.  Buffers freed during
+ * the capture, and the scratch the captured calls are handed (a pool buffer of the size each call
+ * asks for, never the context's own workspace), stay reserved for the graph until
  * anima_graph_destroy; buffers still allocated at the end (outputs) and those allocated before
  * the capture (inputs, weights) remain the caller's and must stay allocated while the graph is
  * replayed.  Profiling is suspended during the capture. */

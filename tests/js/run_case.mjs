@@ -274,6 +274,8 @@ async function main() {
     lat.release();
     cond.release();
     console.log(JSON.stringify({ graph: { diffs, n } }));
+  } else if (c.case === "limits") {
+    console.log(JSON.stringify({ limits: gpu.limits, maxBinding: gpu.maxBinding, info: gpu.info }));
   } else if (c.case === "leak") {
     // tensors dropped without release(): their finalizers return the buffers (run with --expose-gc)
     const bytes = c.mb * 1024 * 1024;
@@ -292,6 +294,24 @@ async function main() {
     const peak = gpu.pool.peak;
     console.log(JSON.stringify({ leak: { n: c.n, bytes, finalized: native.finalized() - f0, peak,
       released_twice_ok: kept.buf === 0 } }));
+  } else if (c.case === "teardown") {
+    // the process returns normally with tensors that were never released: some already collected
+    // (their finalizers ran), some unreachable but not yet collected, some still referenced, and
+    // the context left open; Node's environment teardown must not crash on them
+    const kept = [];
+    for (let i = 0; i < c.n; i++) {
+      const t = gpu.empty([1024 * (i + 1)]);
+      ops.zero(gpu, t);
+      if (i % 3 === 0) kept.push(t);
+      if (i === c.n >> 1 && global.gc) {
+        global.gc();
+        await new Promise((r) => setImmediate(r));
+      }
+    }
+    globalThis.__kept = kept;
+    await gpu.sync();
+    console.log(JSON.stringify({ teardown: { n: c.n, kept: kept.length, finalized: native.finalized() } }));
+    return; // no destroy(), no release(), no process.exit()
   } else if (c.case === "vae") {
     // the VAE decoder on seeded synthetic weights: raw output, RGBA image, progress stages
     const vae = VAEDecoder.synthetic(gpu, new SyntheticWeights(gpu, c.seed));
@@ -429,6 +449,46 @@ async function main() {
     tc.release();
     cond.release();
     te.release();
+  } else if (c.case === "encode") {
+    // LatentPipeline.encode: per-prompt conditioning cache with keep-list eviction; stacked cached
+    // conditionings give the same velocities as prepareContext over both contexts at once
+    const te = Qwen3.synthetic(gpu, new SyntheticWeights(gpu, 31), { layers: 2, vocab: 97 });
+    const A = syntheticAdapter(gpu, new SyntheticWeights(gpu, 32), { blocks: 2, vocab: 64 });
+    const dit = AnimaDiT.synthetic(gpu, new SyntheticWeights(gpu, 33, { mode: "int8", blocks: 2 }));
+    const pipe = new LatentPipeline(gpu, dit, { te, adapter: A });
+    const P = c.prompts.map((p) => ({ qwenIds: p.qwen, t5Ids: p.t5, t5Weights: p.weights }));
+    const keep = [P[0], P[1]];
+    const c0 = await pipe.encode(P[0], keep);
+    const c1 = await pipe.encode(P[1], keep);
+    const c0again = await pipe.encode({ qwenIds: P[0].qwenIds.slice(), t5Ids: P[0].t5Ids.slice(), t5Weights: P[0].t5Weights.slice() }, keep);
+    const reused = c0again === c0;
+    const stats1 = Object.assign({}, pipe.stats);
+    // reference batch: both contexts through prepareContext at once
+    const ctxs = [];
+    for (const p of P.slice(0, 2)) {
+      const hidden = await te.encode(p.qwenIds);
+      ctxs.push(await adapt(gpu, A, hidden, p.t5Ids, p.t5Weights));
+      hidden.release();
+    }
+    const both = dit.prepareContext(ctxs);
+    const stacked = dit.stackConds([c0, c1]);
+    const tc = dit.timeCond(0.6);
+    const hw = c.size / 8, per = 16 * hw * hw;
+    const lat = [0, 1].map((b) => new TorchGenerator(50 + b).randn(per));
+    const vA = await dit.forward(lat, hw, hw, both, tc);
+    const vB = await dit.forward(lat, hw, hw, stacked, tc);
+    let diffs = 0;
+    vA.forEach((va, b) => va.forEach((x, i) => { if (x !== vB[b][i]) diffs++; }));
+    stacked.release();
+    both.release();
+    // a third prompt with the default keep list evicts the other two
+    await pipe.encode(P[2]);
+    const after = { size: pipe.ctxCache.size, hasP0: pipe.ctxCache.has(JSON.stringify([P[0].qwenIds, P[0].t5Ids, P[0].t5Weights])) };
+    tc.release();
+    pipe.clearContexts();
+    te.release();
+    console.log(JSON.stringify({ encode: { reused, stats1, stats: pipe.stats, diffs, n: vA[0].length, after,
+      finite: vA.every((v) => v.every((x) => Number.isFinite(x))) } }));
   } else if (c.case === "lnmod") {
     const x = gpu.fromArray(load(c.x), [c.rows, c.cols]);
     const mod = gpu.upload(load(c.mod));
@@ -464,10 +524,7 @@ async function main() {
   console.log(JSON.stringify({ ok: true, case: c.case }));
 }
 
-// Exit explicitly once done: Node 12 runs the N-API finalizers still queued at teardown (device
-// buffers dropped without release()) from its environment cleanup, where creating their handle
-// scope can crash the process after all output is written.
-main().then(() => process.exit(0), (e) => {
+main().catch((e) => {
   process.stderr.write(String(e && e.stack ? e.stack : e) + "\n");
-  process.exit(1);
+  process.exitCode = 1;
 });

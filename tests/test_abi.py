@@ -37,3 +37,23 @@ def test_null_context_is_rejected():
     m = amd()
     assert m.lib().anima_sync(None) == -1
     assert m.lib().anima_attention(None, None) == -1
+
+
+def test_binding_struct_layouts_match_the_library():
+    """Every descriptor struct the ctypes binding restates has the library's size and field
+    offsets (anima_abi_offset); a planted layout change is detected."""
+    m = amd()
+    assert m.abi_mismatches(m.lib()) == []
+    L = m.lib()
+    assert L.anima_abi_offset(b"anima_attn_desc", b"no_such_field") == -1
+    assert L.anima_abi_offset(b"no_such_struct", None) == -1
+
+    class Shifted(ctypes.Structure):  # kv_prep_bytes dropped: the size differs
+        _fields_ = m.AttnDesc._fields_[:-1]
+
+    saved = m.ABI_STRUCTS["anima_attn_desc"]
+    m.ABI_STRUCTS["anima_attn_desc"] = Shifted
+    try:
+        assert any("sizeof(anima_attn_desc)" in b for b in m.abi_mismatches(L))
+    finally:
+        m.ABI_STRUCTS["anima_attn_desc"] = saved

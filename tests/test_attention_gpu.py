@@ -168,6 +168,36 @@ def test_attention_constant_v_full_size(ctx):
 
 # ------------------------------------------------------------------ cross-attention 4096 x 512
 
+def test_prepared_kv_size_is_checked(ctx):
+    """A prepared K/V buffer is only accepted with the byte count of its layout: K/V prepared in
+    bf16 and passed to an fp32 call, or to a call with a shorter Lk, and a prepare_into whose
+    kv_prep_bytes does not match, are refused on the host with ANIMA_E_ARG before any launch."""
+    case("prepared K/V size checks (host-side refusals)")
+    m = amd()
+    B, Lq, Lk, H = 1, 256, 256, 2
+    q = ctx.upload(orc.randn(41, B * Lq * H * HD))
+    k = ctx.upload(orc.randn(42, B * Lk * H * HD))
+    o = ctx.empty((B, Lq, H * HD))
+    nb16 = m.Context.attention_kv_bytes(B, H, Lk, m.PREC_BF16)
+    assert m.Context.attention_kv_bytes(B, H, Lk, m.PREC_FP32) != nb16
+    prep = ctx.empty(m.Context.attention_kv_bytes(B, H, Lk, m.PREC_FP32), np.uint8)
+    common = dict(B=B, Lq=Lq, H=H, D=HD, ldq=H * HD, ldk=H * HD, ldv=H * HD)
+    ctx.attention(q=q, k=k, v=k, o=o, Lk=Lk, prepare_into=prep, precision=m.PREC_BF16, **common)
+    for kw in (dict(Lk=Lk, precision=m.PREC_FP32), dict(Lk=Lk - 64, precision=m.PREC_BF16)):
+        with pytest.raises(m.AnimaError) as e:
+            ctx.attention(q=q, k=None, v=None, o=o, kv_prep=prep, kv_prep_bytes=nb16, **common, **kw)
+        assert e.value.code == -1, kw
+    with pytest.raises(m.AnimaError) as e:
+        ctx.attention(q=q, k=k, v=k, o=o, Lk=Lk, prepare_into=prep, kv_prep_bytes=nb16 - 256,
+                      precision=m.PREC_BF16, **common)
+    assert e.value.code == -1
+    # the right size is accepted
+    ctx.attention(q=q, k=None, v=None, o=o, Lk=Lk, kv_prep=prep, kv_prep_bytes=nb16, precision=m.PREC_BF16, **common)
+    ctx.sync()
+    for x in (q, k, o, prep):
+        x.release()
+
+
 @pytest.mark.parametrize("precision", ["bf16", "fp32"])
 def test_cross_attention_masked(ctx, precision):
     """Masked cross-attention against fp64 / the bf16 model; the same call on K/V prepared once

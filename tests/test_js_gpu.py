@@ -89,6 +89,29 @@ def test_js_tensor_finalizer_returns_dropped_buffers(tmp_path):
     assert info["released_twice_ok"]
 
 
+def test_js_device_limits(tmp_path):
+    """GPU.limits / GPU.maxBinding carry the device's limits under WebGPU's names
+    (app/gpu/device.js:83-88): the buffer and binding bounds are the device memory."""
+    r = run_case(tmp_path, {"case": "limits"})
+    d = json.loads(next(ln for ln in r.stdout.splitlines() if '"limits"' in ln))
+    L = d["limits"]
+    print(f"js limits: {d}", flush=True)
+    assert d["maxBinding"] == min(L["maxStorageBufferBindingSize"], L["maxBufferSize"]) >= 250 * 10**9
+    assert L["maxComputeWorkgroupStorageSize"] >= 64 * 1024 and L["subgroupSize"] == 64
+    assert d["info"]["architecture"] == "gfx950"
+
+
+def test_js_exit_with_unreleased_tensors(tmp_path):
+    """A script that ends normally -- no release(), no destroy(), no process.exit() -- with device
+    Tensors outstanding (collected, unreachable and still referenced) exits with status 0: the
+    addon's environment cleanup hook retires the buffer handles before Node's N-API teardown."""
+    r = run_case(tmp_path, {"case": "teardown", "n": 24}, flags=("--expose-gc",))
+    info = json.loads(next(ln for ln in r.stdout.splitlines() if '"teardown"' in ln))["teardown"]
+    print(f"teardown: {info}, rc {r.returncode}", flush=True)
+    assert r.returncode == 0 and info["kept"] == 8
+    assert "Segmentation" not in r.stderr and "FATAL" not in r.stderr
+
+
 def test_js_qk_norm_rope_bit_exact(tmp_path):
     Hp, Wp, H = 16, 16, 16
     L = Hp * Wp
@@ -439,3 +462,21 @@ def test_js_prompt_to_velocity_chain(tmp_path):
     v0, v1 = read(f"{out}.0"), read(f"{out}.1")
     assert v0.size == 16 * 8 * 8 and np.isfinite(v0).all() and np.isfinite(v1).all()
     assert np.abs(v0).max() > 0 and not np.array_equal(v0, v1)
+
+
+def test_js_pipeline_encode_cache(tmp_path):
+    """LatentPipeline.encode (app/pipeline.js:192-211): token ids -> Qwen3 -> the LLM adapter ->
+    prepareContext, cached per prompt.  A repeated prompt (equal ids, new arrays) returns the
+    cached conditioning without encoding again; the cached conditionings of two prompts, stacked,
+    give bit-identical velocities to prepareContext over both contexts at once; a new prompt with
+    the default keep list evicts the others."""
+    prompts = [{"qwen": [3, 17, 5, 88, 41, 9, 60], "t5": [1, 5, 9, 33, 2], "weights": [1, 1, 1.2, 1, 0.8]},
+               {"qwen": [7, 7, 21], "t5": [4, 2], "weights": [1, 1]},
+               {"qwen": [11, 2], "t5": [8], "weights": [1]}]
+    r = run_case(tmp_path, {"case": "encode", "prompts": prompts, "size": 64})
+    info = json.loads(next(ln for ln in r.stdout.splitlines() if '"encode"' in ln))["encode"]
+    print(f"encode cache: {info}", flush=True)
+    assert info["reused"]
+    assert info["stats1"]["encodeMisses"] == 2 and info["stats1"]["encodeHits"] == 1
+    assert info["diffs"] == 0 and info["n"] == 16 * 8 * 8 and info["finite"]
+    assert info["after"] == {"size": 1, "hasP0": False}

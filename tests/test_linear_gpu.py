@@ -398,12 +398,17 @@ def test_bf16_weight_linears(ctx):
 
 @pytest.mark.parametrize("M,K,N,epi", [(2048, 256, 2048, "store"), (512, 1024, 4096, "store"),
                                        (512, 2048, 1024, "resid"), (100, 3072, 1024, "gated"),
-                                       (33, 1024, 388, "store")])
+                                       (33, 1024, 388, "store"), (40, 224, 388, "gated"),
+                                       (256, 384, 1152, "resid"), (32, 1056, 512, "store")])
 def test_bf16_weight_split_kernel(ctx, M, K, N, epi):
-    """bf16 weights with N > 256 and K % 32 == 0 (the text encoder's q/k/v, o, gate / up and down
-    shapes at 512 tokens, a 1 and a 2 k-group grid, ragged M and N): x enters the bf16 matrix cores
-    as three bf16 terms, so every product is exact and the sums are fp32; within 1e-6 of float64
-    for each epilogue."""
+    """bf16 weights with N > 256 and K % 32 == 0: x enters the bf16 matrix cores as three bf16
+    terms, so every product is exact and the sums are fp32; within 1e-6 of float64 for each
+    epilogue.  The shapes reach every kernel of the dispatch: the LDS-staged tiles (2048 x 256 x
+    2048, 512 x 1024 x 4096: the text encoder's q/k/v and gate / up at 512 tokens), the k-sliced LDS
+    kernel with its summing epilogue pass (512 x 2048 x 1024, 100 x 3072 x 1024, 33 x 1024 x 388:
+    the o and down products, ragged M and N), and the register kernel with one, two and four
+    k-groups per workgroup (40 x 224 x 388, 256 x 384 x 1152, 32 x 1056 x 512: too short a K
+    for k-slices)."""
     case(f"bf16 split kernel M={M} K={K} N={N} epilogue {epi}")
     m = amd()
     x = orc.randn(151 + K, M * K).reshape(M, K)

@@ -1,6 +1,7 @@
 """Runtime behaviour at the C ABI: host -> device copies through the pinned staging ring keep
 stream order and let the caller reuse its buffer at once, behind queued device work; queue marks
-(anima_mark / anima_wait_mark) order correctly and reject tickets never issued."""
+(anima_mark / anima_wait_mark) order correctly and reject tickets never issued; the device limits
+(anima_device_limits) describe the MI355X."""
 
 import ctypes
 
@@ -94,3 +95,18 @@ def test_marks_order_and_errors(ctx):
     ctx.sync()
     for t in [x] + list(keep):
         t.release()
+
+
+def test_device_limits(ctx):
+    """anima_device_limits reports the device the context runs on: gfx950, 256 compute units,
+    64-wide wavefronts, 288 GB of HBM as the buffer / binding bound, 160 KiB of LDS per workgroup
+    at most, and a free-memory figure within the total."""
+    case("device limits")
+    L = ctx.limits()
+    print(f"limits: {L}", flush=True)
+    assert L["arch"].startswith("gfx950")
+    assert L["compute_units"] == 256 and L["wavefront_size"] == 64
+    assert L["max_buffer_size"] == L["max_binding_size"] >= 250 * 10**9
+    assert 0 < L["free_memory"] <= L["total_memory"]
+    assert 64 * 1024 <= L["workgroup_storage_size"] <= 160 * 1024
+    assert L["max_workgroup_size"] >= 1024 and L["max_workgroups_per_dimension"] >= 65535
