@@ -6,7 +6,9 @@
 //                 out [B][Hkv][Lkp][128]; V transposed to [B][Hkv][128][Lkp] so the P.V MFMA
 //                 reads 4 consecutive keys per 8-byte LDS load.  Rows Lk..Lkp are zero.
 //                 One pass over K and V (HBM-bound) instead of re-normalizing K in every
-//                 query tile (32x redundant VALU work at N=4096).
+//                 query tile (32x redundant VALU work at N=4096).  bf16 operands take
+//                 attn_prep_kv_lines (whole-line loads and stores, no LDS); fp32 operands the
+//                 LDS-transpose kernel attn_prep_kv.
 //   attn_flash_*  One workgroup = 4 waves x 32 queries.  Q is loaded from the fp32 input with
 //                 RMSNorm + RoPE fused into the load and kept in registers; K/V tiles of 64
 //                 keys stream through double-buffered LDS.  Scores are computed transposed,
@@ -206,6 +208,108 @@ __global__ __launch_bounds__(256) void attn_prep_kv(PrepArgs a) {
         *(float4*)((float*)dst + 4 * i) = make_float4(s4[0], s4[1], s4[2], s4[3]);
       }
     }
+  }
+}
+
+// Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15); every lane of the row receives the
+// same bits (each step adds a lane's value to a partner's, and fp addition is commutative).
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));  // row_ror:8
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));  // row_ror:4
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));   // quad [1,0,3,2]
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));   // quad [2,3,0,1]
+  return v;
+}
+
+// bf16 K / V prep with whole-line accesses: every load and store instruction of a wave moves
+// complete 128-byte lines, and no LDS is used.  grid (Hkv, Lkp/64, B), 256 threads; one
+// workgroup = one kv head x 64 keys of one batch element.
+//   K: 16 lanes per key row, lane q holding dims 4q..4q+3 and 64+4q..64+4q+3 (so each RoPE pair is
+//      in one lane); wave w takes rows 16w .. 16w+15, four per load instruction.  The row's sum of
+//      squares crosses its 16 lanes by DPP.
+//   V: wave w takes dims 32w .. 32w+31 of all 64 keys; lane (q = lane % 8, c = lane / 8) loads the
+//      8 keys of V^T chunk c (the MFMA key order: each 16-key group stored as keys 0-3, 8-11, 4-7,
+//      12-15) at dims 32w+4q .. +3 and stores four 16-byte chunks, one per dim; the 8 lanes of one
+//      dim cover its 64 keys (128 bytes).
+template <bool NORM, bool ROPE>
+__global__ __launch_bounds__(256) void attn_prep_kv_lines(PrepArgs a) {
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int kb0 = blockIdx.y * BK, hk = blockIdx.x, b = blockIdx.z;
+  const int64_t bh = (int64_t)b * a.Hkv + hk;
+  // ---- all loads first
+  const int q16 = lane & 15, rsub = lane >> 4;
+  float4 klo[4], khi[4], cv[4], sv[4], wl = {}, wh = {};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int l = min(kb0 + 16 * w + 4 * i + rsub, a.Lk - 1);
+    const float* src = a.k + (int64_t)b * a.k_bs + (int64_t)l * a.ldk + hk * HD + 4 * q16;
+    klo[i] = *(const float4*)src;
+    khi[i] = *(const float4*)(src + 64);
+    if (ROPE) {
+      const float* cr = a.cs + (int64_t)l * (HD / 2) + 4 * q16;
+      cv[i] = *(const float4*)cr;
+      sv[i] = *(const float4*)(cr + a.sin_off);
+    }
+  }
+  if (NORM) {
+    wl = *(const float4*)(a.kn + 4 * q16);
+    wh = *(const float4*)(a.kn + 64 + 4 * q16);
+  }
+  const int vq = lane & 7, vc = lane >> 3;
+  float4 ve[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const int key = kb0 + 16 * (vc >> 1) + 4 * (vc & 1) + (e & 3) + 8 * (e >> 2);
+    ve[e] = *(const float4*)(a.v + (int64_t)b * a.v_bs + (int64_t)min(key, a.Lk - 1) * a.ldv + hk * HD + 32 * w + 4 * vq);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // ---- K rows
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int l = kb0 + 16 * w + 4 * i + rsub;
+    float x[8] = {klo[i].x, klo[i].y, klo[i].z, klo[i].w, khi[i].x, khi[i].y, khi[i].z, khi[i].w};
+    if (NORM) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; j++) ss += x[j] * x[j];
+      ss = row16_sum(ss);
+      const float rn = 1.0f / sqrtf(ss / (float)HD + a.eps);
+      const float wv[8] = {wl.x, wl.y, wl.z, wl.w, wh.x, wh.y, wh.z, wh.w};
+#pragma unroll
+      for (int j = 0; j < 8; j++) x[j] = x[j] * rn * wv[j];
+    }
+    if (ROPE) {
+      const float c4[4] = {cv[i].x, cv[i].y, cv[i].z, cv[i].w}, s4[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float x1 = x[j], x2 = x[4 + j];
+        x[j] = x1 * c4[j] - x2 * s4[j];
+        x[4 + j] = x2 * c4[j] + x1 * s4[j];
+      }
+    }
+    bf16x4 lo, hi;
+    const bool live = l < a.Lk;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      lo[j] = to_bf16(live ? x[j] : 0.0f);
+      hi[j] = to_bf16(live ? x[4 + j] : 0.0f);
+    }
+    bf16* dst = (bf16*)a.kb + (bh * a.Lkp + l) * HD + 4 * q16;
+    *(bf16x4*)dst = lo;
+    *(bf16x4*)(dst + 64) = hi;
+  }
+  // ---- V^T chunks
+  bf16* vdst = (bf16*)a.vt + (bh * HD + 32 * w + 4 * vq) * a.Lkp + kb0 + 8 * vc;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const int key = kb0 + 16 * (vc >> 1) + 4 * (vc & 1) + (e & 3) + 8 * (e >> 2);
+      const float v = j == 0 ? ve[e].x : j == 1 ? ve[e].y : j == 2 ? ve[e].z : ve[e].w;
+      o[e] = to_bf16(key < a.Lk ? v : 0.0f);
+    }
+    *(bf16x8*)(vdst + (int64_t)j * a.Lkp) = o;
   }
 }
 
@@ -1053,11 +1157,12 @@ static int prep_kv_launch(anima_ctx* c, const anima_attn_desc* d, void* dst) {
     dim3 grid(Hkv, Lkp / BK, d->B);  // heads fastest: concurrent workgroups read whole K / V rows
     const bool kn = d->k_norm != nullptr;
 #define PREP(T, N, R) hipLaunchKernelGGL((attn_prep_kv<T, N, R>), grid, dim3(256), 0, c->stream, p)
+#define PREP_LINES(N, R) hipLaunchKernelGGL((attn_prep_kv_lines<N, R>), grid, dim3(256), 0, c->stream, p)
     if (bf) {
-      if (kn && rope) PREP(bf16, true, true);
-      else if (kn) PREP(bf16, true, false);
-      else if (rope) PREP(bf16, false, true);
-      else PREP(bf16, false, false);
+      if (kn && rope) PREP_LINES(true, true);
+      else if (kn) PREP_LINES(true, false);
+      else if (rope) PREP_LINES(false, true);
+      else PREP_LINES(false, false);
     } else {
       if (kn && rope) PREP(float, true, true);
       else if (kn) PREP(float, true, false);
@@ -1065,6 +1170,7 @@ static int prep_kv_launch(anima_ctx* c, const anima_attn_desc* d, void* dst) {
       else PREP(float, false, false);
     }
 #undef PREP
+#undef PREP_LINES
     if ((rc = L.end())) return rc;
   }
 
