@@ -91,8 +91,14 @@ class Limits(ctypes.Structure):
                 ("arch", ctypes.c_char * 64)]
 
 
+class QkvDesc(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int), ("L", ctypes.c_int), ("H", ctypes.c_int), ("k_norm", _vp), ("rope_cs", _vp),
+                ("rope_sin_off", _i64), ("eps", ctypes.c_float), ("kv_prep", _vp), ("kv_prep_bytes", _i64)]
+
+
 ABI_STRUCTS = {"anima_attn_desc": AttnDesc, "anima_linear_desc": LinearDesc, "anima_weight": Weight,
-               "anima_sampler_desc": SamplerDesc, "anima_conv_desc": ConvDesc, "anima_limits": Limits}
+               "anima_sampler_desc": SamplerDesc, "anima_conv_desc": ConvDesc, "anima_limits": Limits,
+               "anima_qkv_desc": QkvDesc}
 
 
 def abi_mismatches(L):
@@ -146,6 +152,7 @@ def lib():
         L.anima_profile_report.argtypes = [_vp, ctypes.c_char_p, ctypes.c_size_t]
         L.anima_timer_stop.argtypes = [_vp, P(ctypes.c_float)]
         L.anima_attention.argtypes = [_vp, P(AttnDesc)]
+        L.anima_linear_qkv.argtypes = [_vp, P(LinearDesc), P(QkvDesc)]
         L.anima_attention_prepare_kv.argtypes = [_vp, P(AttnDesc), _vp]
         L.anima_attention_kv_bytes.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.anima_attention_kv_bytes.restype = _i64
@@ -412,6 +419,16 @@ class Context:
                        epilogue=epilogue, gate=_ptr(gate), gate_off=gate_off, acc_out=_ptr(acc_out), add=_ptr(add),
                        ld_add=ld_add)
         return self._check(lib().anima_linear(self.h, ctypes.byref(d)))
+
+    def linear_qkv(self, W, M, out, *, B, L, H, k_norm, rope_cs, rope_sin_off, kv_prep, eps=1e-6, x=None, ldx=0,
+                   x_rotated=True, xq=None, xs=None, ldc=0, alpha=0.0):
+        """anima_linear_qkv: the stacked QKV projection writing Q (fp32) to out and K / V in the
+        attention's bf16 operand layout to kv_prep (sized by attention_kv_bytes(B, H, L, bf16))."""
+        d = LinearDesc(M=M, W=ctypes.pointer(W), x=_ptr(x), ldx=ldx, x_rotated=int(x_rotated), xq=_ptr(xq),
+                       xs=_ptr(xs), out=_ptr(out), ldc=ldc, alpha=alpha, act=0, epilogue=EPI_STORE)
+        p = QkvDesc(B=B, L=L, H=H, k_norm=_ptr(k_norm), rope_cs=_ptr(rope_cs), rope_sin_off=rope_sin_off, eps=eps,
+                    kv_prep=_ptr(kv_prep), kv_prep_bytes=self.attention_kv_bytes(B, H, L, PREC_BF16))
+        return self._check(lib().anima_linear_qkv(self.h, ctypes.byref(d), ctypes.byref(p)))
 
     def weight_unpack_w4(self, W, grid):
         """The int8 grid [N][K] of a W4 weight (anima_weight_unpack_w4)."""

@@ -211,22 +211,12 @@ __global__ __launch_bounds__(256) void attn_prep_kv(PrepArgs a) {
   }
 }
 
-// Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15); every lane of the row receives the
-// same bits (each step adds a lane's value to a partner's, and fp addition is commutative).
-__device__ __forceinline__ float row16_sum(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));  // row_ror:8
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));  // row_ror:4
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));   // quad [1,0,3,2]
-  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));   // quad [2,3,0,1]
-  return v;
-}
-
 // bf16 K / V prep with whole-line accesses: every load and store instruction of a wave moves
 // complete 128-byte lines, and no LDS is used.  grid (Hkv, Lkp/64, B), 256 threads; one
 // workgroup = one kv head x 64 keys of one batch element.
 //   K: 16 lanes per key row, lane q holding dims 4q..4q+3 and 64+4q..64+4q+3 (so each RoPE pair is
 //      in one lane); wave w takes rows 16w .. 16w+15, four per load instruction.  The row's sum of
-//      squares crosses its 16 lanes by DPP.
+//      squares crosses its 16 lanes by lane shuffles in a fixed tree.
 //   V: wave w takes dims 32w .. 32w+31 of all 64 keys; lane (q = lane % 8, c = lane / 8) loads the
 //      8 keys of V^T chunk c (the MFMA key order: each 16-key group stored as keys 0-3, 8-11, 4-7,
 //      12-15) at dims 32w+4q .. +3 and stores four 16-byte chunks, one per dim; the 8 lanes of one
@@ -269,22 +259,29 @@ __global__ __launch_bounds__(256) void attn_prep_kv_lines(PrepArgs a) {
     const int l = kb0 + 16 * w + 4 * i + rsub;
     float x[8] = {klo[i].x, klo[i].y, klo[i].z, klo[i].w, khi[i].x, khi[i].y, khi[i].z, khi[i].w};
     if (NORM) {
+      // The sum of squares over the row's 128 dims in a fixed tree (the QKV GEMM's attention
+      // operand epilogue, anima_linear_qkv, forms the same one): this lane's 8 squares chained
+      // by fma, then its partners across lane bits 1 and 2 (pairs of 8-dim leaves), bit 0 (the
+      // two 4-dim halves of each 8) and bit 3 (the two 32-dim groups of each 64).
       float ss = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 8; j++) ss += x[j] * x[j];
-      ss = row16_sum(ss);
-      const float rn = 1.0f / sqrtf(ss / (float)HD + a.eps);
+      for (int j = 0; j < 8; j++) ss = __builtin_fmaf(x[j], x[j], ss);
+      ss = ss + __shfl_xor(ss, 2);
+      ss = ss + __shfl_xor(ss, 4);
+      ss = ss + __shfl_xor(ss, 1);
+      ss = ss + __shfl_xor(ss, 8);
+      const float rn = 1.0f / sqrtf(__builtin_fmaf(ss, 1.0f / (float)HD, a.eps));
       const float wv[8] = {wl.x, wl.y, wl.z, wl.w, wh.x, wh.y, wh.z, wh.w};
 #pragma unroll
-      for (int j = 0; j < 8; j++) x[j] = x[j] * rn * wv[j];
+      for (int j = 0; j < 8; j++) x[j] = (x[j] * rn) * wv[j];
     }
     if (ROPE) {
       const float c4[4] = {cv[i].x, cv[i].y, cv[i].z, cv[i].w}, s4[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         const float x1 = x[j], x2 = x[4 + j];
-        x[j] = x1 * c4[j] - x2 * s4[j];
-        x[4 + j] = x2 * c4[j] + x1 * s4[j];
+        x[j] = __builtin_fmaf(x1, c4[j], -(x2 * s4[j]));
+        x[4 + j] = __builtin_fmaf(x2, c4[j], x1 * s4[j]);
       }
     }
     bf16x4 lo, hi;

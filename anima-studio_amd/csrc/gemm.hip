@@ -36,6 +36,18 @@ struct GemmArgs {
   int M, N, K;
   const float* add;  // optional [M][ld_add] term after the bias
   int64_t ld_add;
+  // Attention operand epilogue of the stacked QKV projection (gemm_i8_256<STORE, W4, true>):
+  // columns [kcol, vcol) are K and [vcol, N) V, H heads of 128 each; they leave as the attention's
+  // bf16 K rows [B][H][Lkp][128] (RMSNorm + RoPE applied) and V^T rows [B][H][128][Lkp] (keys in
+  // the MFMA order) in kv instead of out, which receives only the Q columns [0, kcol).
+  void* kv;
+  int64_t kv_plane;  // bytes of the K plane (the V^T plane follows)
+  const float* kn;   // [128] k RMSNorm weight
+  const float* cs;   // RoPE table: cos [rows][64], sin at + sin_off
+  int64_t sin_off;
+  float eps;
+  int L, Lkp, H;     // tokens per batch element (M = B * L, L % 64 == 0 so Lkp = L), heads
+  int kcol, vcol;
 };
 
 
@@ -298,6 +310,135 @@ __device__ __forceinline__ void epi_store_t(const GemmArgs& a, const i32x16& v, 
   }
 }
 
+// ------------------------------------------------------------------ attention operand epilogue
+constexpr int HD_K = 128;  // head dim of the attention operands
+//
+// The stacked QKV projection of a DiT block can hand its K and V columns to the attention in the
+// operand layout that anima_attention_prepare_kv writes (what attn_prep_kv_lines computes from the
+// fp32 output), bit for bit: y is the store epilogue's fp32 value; K rows get
+// x = (y * rn) * w, rn = 1 / sqrt(fma(ss, 1/128, eps)), then the split-half RoPE
+// lo' = fma(lo, c, -(hi * s)), hi' = fma(hi, c, lo * s), rounded to bf16; V goes to V^T rows
+// rounded to bf16.  The row sum of squares ss of a head's 128 columns uses one fixed tree:
+// leaves of 8 values (columns 8q' + e and 64 + 8q' + e, e = 0..3: fmaf of the squares in that
+// order), pairs of leaves q' = 2t, 2t + 1 (t = 0, 1 within a 32-column group and half), then the
+// two 4-column halves, then the two 32-column groups of each 64 (the prep kernel's lane
+// butterfly reaches the same sums: fp addition is commutative).
+
+// K tile: lane (lq, hf) of wave w holds rows m0 + 32i and columns n0 + 8q + e (j = 0) and
+// n0 + 64 + 8q + e (j = 1) of head (col0 - kcol) / 128 + w / 4; waves w and w ^ 2 hold the other
+// 64 columns of the same rows and exchange one partial sum per row through LDS.
+__device__ __forceinline__ f32x4 kv_epi_y(const GemmArgs& a, const i32x16& v, int q, float sx, int n) {
+  // the store epilogue's fp32 value of columns n + 8q .. n + 8q + 3 (epi_store_t's order; the
+  // QKV tiles are whole, so every column group is in range)
+  const f32x4 sw = *(const f32x4*)(a.sw + n + 8 * q);
+  f32x4 y;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const float t = (float)v[4 * q + e] * sx;
+    y[e] = t * sw[e];
+  }
+  if (a.alpha != 1.0f) y = y * a.alpha;
+  if (a.bias) y = y + *(const f32x4*)(a.bias + n + 8 * q);
+  return y;
+}
+
+__device__ __forceinline__ void kv_epi_k(const GemmArgs& a, const i32x16 (&acc)[4][2], int m0, int n0, int col0,
+                                         int wave, int hf, int lq, const float (&sxv)[4], float* xch) {
+  const int grp = (wave >> 1) & 1;
+  const int c0 = 32 * grp + 4 * hf;  // this lane's first column within the head (< 64)
+  const int head = (col0 - a.kcol) / HD_K + (wave >> 2);
+  // One 32-row block at a time: the partial sum of squares over this lane pair's 64 columns goes
+  // to LDS, a barrier, the partner wave's partial completes the row, and the block's values are
+  // recomputed (the same fp32 bits), normalized, rotated, rounded and stored.
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float lf[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const f32x4 y = kv_epi_y(a, acc[i][j], q, sxv[i], n0 + 64 * j);
+#pragma unroll
+        for (int e = 0; e < 4; e++) lf[q] = __builtin_fmaf(y[e], y[e], lf[q]);
+      }
+    float part = (lf[0] + lf[1]) + (lf[2] + lf[3]);
+    part = part + __shfl_xor(part, 32);
+    if (hf == 0) xch[wave * 128 + 32 * i + lq] = part;
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the partial sums are in LDS
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const float other = xch[(wave ^ 2) * 128 + 32 * i + lq];
+    const int m = m0 + 32 * i;
+    if (m >= a.M) continue;
+    const float ss = grp == 0 ? part + other : other + part;
+    const float rn = 1.0f / sqrtf(__builtin_fmaf(ss, 1.0f / 128.0f, a.eps));
+    const int b = m / a.L, l = m - b * a.L;
+    const float* crow = a.cs + (int64_t)l * (HD_K / 2) + c0;
+    bf16* dst = (bf16*)a.kv + (((int64_t)b * a.H + head) * a.Lkp + l) * HD_K + c0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const f32x4 cv = *(const f32x4*)(crow + 8 * q), sv = *(const f32x4*)(crow + a.sin_off + 8 * q);
+      const f32x4 w0 = *(const f32x4*)(a.kn + c0 + 8 * q), w1 = *(const f32x4*)(a.kn + c0 + 64 + 8 * q);
+      const f32x4 y0 = kv_epi_y(a, acc[i][0], q, sxv[i], n0), y1 = kv_epi_y(a, acc[i][1], q, sxv[i], n0 + 64);
+      bf16x4 lo, hi;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float x1 = (y0[e] * rn) * w0[e];
+        const float x2 = (y1[e] * rn) * w1[e];
+        lo[e] = (bf16)__builtin_fmaf(x1, cv[e], -(x2 * sv[e]));
+        hi[e] = (bf16)__builtin_fmaf(x2, cv[e], x1 * sv[e]);
+      }
+      *(bf16x4*)(dst + 8 * q) = lo;
+      *(bf16x4*)(dst + 64 + 8 * q) = hi;
+    }
+  }
+}
+
+// V tile: the lane's values are one token (row) x 16 columns; V^T rows are token-contiguous, so
+// each pair of lanes lq, lq ^ 1 (tokens 2t, 2t + 1: adjacent in the key order too) trades
+// columns and stores 4-byte token pairs, the even lane those of columns e = 0, 1, the odd lane
+// e = 2, 3.  Key order of V^T within each 16-key group: keys 0-3, 8-11, 4-7, 12-15.
+__device__ __forceinline__ void kv_epi_v(const GemmArgs& a, const i32x16 (&acc)[4][2], int m0, int n0, int col0, int wave,
+                                         int hf, int lq, const float (&sxv)[4]) {
+  const int c0 = 32 * ((wave >> 1) & 1) + 4 * hf;
+  const int head = (col0 - a.vcol) / HD_K + (wave >> 2);
+  const bool odd = lq & 1;
+  bf16* vt = (bf16*)((char*)a.kv + a.kv_plane);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int m = m0 + 32 * i;
+    const int mp = m - (odd ? 1 : 0);  // the pair's even token
+    const int b = mp / a.L, l = mp - b * a.L;
+    const int g16 = l & 15, pos = (l & ~15) + 4 * (((g16 >> 2) & 1) << 1 | (g16 >> 3)) + (g16 & 3);
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const f32x4 y = kv_epi_y(a, acc[i][j], q, sxv[i], n0 + 64 * j);
+        // own bf16 pairs: columns (e0, e1) and (e2, e3)
+        const uint32_t p01 = (uint32_t)__builtin_bit_cast(uint16_t, (bf16)y[0]) |
+                             ((uint32_t)__builtin_bit_cast(uint16_t, (bf16)y[1]) << 16);
+        const uint32_t p23 = (uint32_t)__builtin_bit_cast(uint16_t, (bf16)y[2]) |
+                             ((uint32_t)__builtin_bit_cast(uint16_t, (bf16)y[3]) << 16);
+        // the even lane sends (e2, e3) and keeps (e0, e1); the odd lane the other way round
+        const uint32_t send = odd ? p01 : p23, keep = odd ? p23 : p01;
+        const uint32_t got = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xb1, 0xf, 0xf, false);  // lane ^ 1
+        // token pair words (even token in the low half) for the lane's two columns
+        const uint32_t lo_t = odd ? got : keep, hi_t = odd ? keep : got;
+        const uint32_t w0 = __builtin_amdgcn_perm(hi_t, lo_t, 0x05040100u);  // column ea: tokens (2t, 2t+1)
+        const uint32_t w1 = __builtin_amdgcn_perm(hi_t, lo_t, 0x07060302u);  // column eb
+        if (m < a.M) {
+          const int d = c0 + 64 * j + 8 * q + (odd ? 2 : 0);
+          bf16* r0 = vt + (((int64_t)b * a.H + head) * HD_K + d) * a.Lkp + pos;
+          *(uint32_t*)r0 = w0;
+          *(uint32_t*)(r0 + a.Lkp) = w1;
+        }
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ 256x256 int8 kernel
 //
 // gemm_i8_256: persistent workgroups (one per CU), each walking a list of 256 x 256 output
@@ -340,9 +481,10 @@ __device__ __forceinline__ void g2_barrier() {
 
 constexpr int G2_LUT = G2_NST * G2_ST;  // W4 table offset in LDS (256 x 16 bytes)
 
-template <int EPI, bool W4>
+template <int EPI, bool W4, bool KV = false>
 __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
-  __shared__ __attribute__((aligned(1024))) char smem[G2_NST * G2_ST + (W4 ? 4096 : 0)];
+  static_assert(!KV || EPI == ANIMA_EPI_STORE, "the attention operand epilogue stores");
+  __shared__ __attribute__((aligned(1024))) char smem[G2_NST * G2_ST + (W4 ? 4096 : 0) + (KV ? 4096 : 0)];
   // the wave index is uniform: in a scalar register, so copy offsets derived from it stay scalar
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lq = lane & 31, hf = lane >> 5;
@@ -358,6 +500,11 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
     tm = row0 + (local - tn * gm);
   };
   const int wm = (wave & 1) * 128, wn = (wave >> 1) * 64;
+  // B column tiles of this wave: bc0 and bc0 + BSTEP.  KV: columns 128 (w / 4) + 32 ((w / 2) % 2)
+  // and 64 further, so that one lane holds both columns of every RoPE pair (d, d + 64) of a head,
+  // and waves w, w ^ 2 (same rows) hold the head's 128 columns between them.
+  const int bc0 = KV ? 128 * (wave >> 2) + 32 * ((wave >> 1) & 1) : wn;
+  constexpr int BSTEP = KV ? 64 : 32;
   const int K = a.K;
   const int nk = K / G2_BK;
 
@@ -571,7 +718,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) af0[i] = *(const i32x4*)(smem + (wm + 32 * i) * G2_BK + fofs[0]);
 #pragma unroll
-    for (int j = 0; j < 2; j++) bf0[j] = *(const i32x4*)(smem + G2_TILE + (wn + 32 * j) * G2_BK + fofs[0]);
+    for (int j = 0; j < 2; j++) bf0[j] = *(const i32x4*)(smem + G2_TILE + (bc0 + BSTEP * j) * G2_BK + fofs[0]);
   }
   int s = 0, k = 0;  // stage within the tile, tile index within this workgroup's list
   // One iteration per stage g; written as a lambda over the stage parity P (a compile-time W4
@@ -615,7 +762,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
 #pragma unroll
     for (int q = 0; q < 8; q++) {
       acc[q >> 1][q & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf0[q & 1], af0[q >> 1], acc[q >> 1][q & 1], 0, 0, 0);
-      if (q < 2) bf1[q] = *(const i32x4*)(st + G2_TILE + (wn + 32 * q) * G2_BK + fofs[1]);
+      if (q < 2) bf1[q] = *(const i32x4*)(st + G2_TILE + (bc0 + BSTEP * q) * G2_BK + fofs[1]);
       else if (q < 6) af1[q - 2] = *(const i32x4*)(st + (wm + 32 * (q - 2)) * G2_BK + fofs[1]);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -626,7 +773,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
 #pragma unroll
     for (int q = 0; q < 8; q++) {
       acc[q >> 1][q & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf1[q & 1], af1[q >> 1], acc[q >> 1][q & 1], 0, 0, 0);
-      if (q < 2) bf0[q] = *(const i32x4*)(sn + G2_TILE + (wn + 32 * q) * G2_BK + fofs[0]);
+      if (q < 2) bf0[q] = *(const i32x4*)(sn + G2_TILE + (bc0 + BSTEP * q) * G2_BK + fofs[0]);
       else if (q < 6) af0[q - 2] = *(const i32x4*)(sn + (wm + 32 * (q - 2)) * G2_BK + fofs[0]);
       if (q >= 1 && q <= 4) {
         w4_lookup(P, 2 * (q - 1));
@@ -635,7 +782,39 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
       if (q == 5 || q == 6) w4_store(g + 2, q - 5);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (++s == nk) {
+    if (++s == nk && KV) {
+      // tile done, attention operand epilogue: Q columns stored as fp32, K and V columns
+      // converted to the attention's bf16 operand layout
+      int tm, tn;
+      tile_mn(first + k * stride, tm, tn);
+      const int col0 = tn * 256, m0 = tm * 256 + wm + lq, n0 = col0 + bc0 + 4 * hf;
+      float sxv[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) sxv[i] = m0 + 32 * i < a.M ? a.sx[m0 + 32 * i] : 0.0f;
+      if (col0 < a.kcol) {
+        EpiCols cc;
+        const f32x4 none[4] = {};
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          epi_cols(a, n0 + 64 * j, cc);
+#pragma unroll
+          for (int i = 0; i < 4; i++) epi_store_t<ANIMA_EPI_STORE>(a, acc[i][j], m0 + 32 * i, n0 + 64 * j, sxv[i], cc, none);
+        }
+      } else if (col0 < a.vcol) {
+        kv_epi_k(a, acc, m0, n0, col0, wave, hf, lq, sxv, (float*)(smem + G2_NST * G2_ST + (W4 ? 4096 : 0)));
+      } else {
+        kv_epi_v(a, acc, m0, n0, col0, wave, hf, lq, sxv);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = (i32x16){};
+      s = 0;
+      k++;
+      if constexpr (W4) {
+        if (late) G2_ISSUE_C(1 - P);
+      }
+    } else if (s == nk) {
       // tile done: epilogue (the next tile's first stages are already in flight), one 32x32
       // tile at a time, written out (a loop over the tiles is not fully unrolled at this size,
       // and a run-time tile index would put the accumulators in scratch memory)
@@ -1829,6 +2008,89 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
       if (w4) hipLaunchKernelGGL(gemm_i8_kernel<true>, grid, dim3(256), 0, c->stream, g);
       else hipLaunchKernelGGL(gemm_i8_kernel<false>, grid, dim3(256), 0, c->stream, g);
     }
+    rc = L.end();
+  }
+  if (tmp) anima_free(c, tmp);
+  return rc;
+}
+
+// The stacked QKV projection with the attention operand epilogue (anima_linear_qkv).
+int linear_qkv_launch(anima_ctx* c, const anima_linear_desc* d, const anima_qkv_desc* p) {
+  if (!d || !p) return fail(c, ANIMA_E_ARG, "anima_linear_qkv: null descriptor");
+  const anima_weight* W = d->W;
+  if (!W) return fail(c, ANIMA_E_ARG, "anima_linear_qkv: null weight");
+  if (W->kind != ANIMA_W_I8 && W->kind != ANIMA_W_W4)
+    return fail(c, ANIMA_E_UNSUPPORTED, "anima_linear_qkv: int8 or W4 weights only (kind %d)", W->kind);
+  const int64_t M = d->M;
+  const int N = W->N, K = W->K, H = p->H;
+  if (p->B < 1 || p->L < 1 || H < 2 || H % 2 || (int64_t)p->B * p->L != M || M > 0x7fffffff)
+    return fail(c, ANIMA_E_ARG, "anima_linear_qkv: B=%d L=%d H=%d M=%lld (M = B * L, H even)", p->B, p->L, H, (long long)M);
+  if (p->L % 64) return fail(c, ANIMA_E_UNSUPPORTED, "anima_linear_qkv: L=%d must be a multiple of 64", p->L);
+  if (N != 3 * H * HD_K || K % GBK)
+    return fail(c, ANIMA_E_ARG, "anima_linear_qkv: N=%d must be 3 * H * 128 = %d, K %% %d == 0", N, 3 * H * HD_K, GBK);
+  if (d->epilogue != ANIMA_EPI_STORE || d->act != ANIMA_ACT_NONE || d->add || d->acc_out)
+    return fail(c, ANIMA_E_UNSUPPORTED, "anima_linear_qkv: plain store only (no activation, residual, gate, add term or acc_out)");
+  if (!p->k_norm || !p->rope_cs || !p->kv_prep)
+    return fail(c, ANIMA_E_ARG, "anima_linear_qkv: k_norm, rope_cs and kv_prep are required");
+  if (p->kv_prep_bytes != attention_kv_bytes(p->B, H, p->L, ANIMA_PREC_BF16))
+    return fail(c, ANIMA_E_ARG, "anima_linear_qkv: kv_prep_bytes=%lld, the layout takes %lld", (long long)p->kv_prep_bytes,
+                (long long)attention_kv_bytes(p->B, H, p->L, ANIMA_PREC_BF16));
+  const int64_t rows = p->rope_sin_off / (HD_K / 2);
+  if (p->rope_sin_off <= 0 || p->rope_sin_off % (HD_K / 2) || rows < p->L)
+    return fail(c, ANIMA_E_ARG, "anima_linear_qkv: rope_sin_off=%lld must be rows*64 with rows >= L=%d", (long long)p->rope_sin_off, p->L);
+  const int64_t ldc = d->ldc ? d->ldc : N;
+  if (!d->out || ldc < H * HD_K) return fail(c, ANIMA_E_ARG, "anima_linear_qkv: out with ldc >= %d (the Q columns) required", H * HD_K);
+  if (!W->w || !W->scale || (W->kind == ANIMA_W_W4 && (!W->srel || !W->codebook)))
+    return fail(c, ANIMA_E_ARG, "anima_linear_qkv: missing weight data, scale, s_rel or codebook");
+  if (!al(W->w, 16) || !al(d->out, 16) || ldc % 4 || !al(W->scale, 16) || (W->bias && !al(W->bias, 16)) ||
+      !al(p->kv_prep, 16) || !al(p->k_norm, 16) || !al(p->rope_cs, 16))
+    return fail(c, ANIMA_E_ARG, "anima_linear_qkv: weight, out (ldc %% 4), scale, bias, kv_prep, k_norm and rope_cs must be 16-byte aligned");
+  const int8_t* qx = d->xq;
+  const float* sx = d->xs;
+  void* tmp = nullptr;
+  if (!qx) {
+    if (!d->x) return fail(c, ANIMA_E_ARG, "anima_linear_qkv: no input (x or xq)");
+    const int64_t ldx = d->ldx ? d->ldx : K;
+    if (ldx != K) return fail(c, ANIMA_E_ARG, "anima_linear_qkv: contiguous x (ldx == K) required");
+    if (K > 8192 || (!d->x_rotated && K % 256)) return fail(c, ANIMA_E_ARG, "anima_linear_qkv: K=%d (<= 8192, %% 256 == 0 to rotate)", K);
+    int rc = anima_alloc(c, (size_t)M * K + (size_t)M * 4 + 256, &tmp);
+    if (rc) return rc;
+    int8_t* q = (int8_t*)tmp;
+    float* s = (float*)((char*)tmp + ((size_t)M * K + 255) / 256 * 256);
+    rc = quant_rows_launch(c, d->x, M, K, d->x_rotated ? 0 : 1, ANIMA_ACT_NONE, q, s);
+    if (rc) {
+      anima_free(c, tmp);
+      return rc;
+    }
+    qx = q;
+    sx = s;
+  } else {
+    if (!sx) return fail(c, ANIMA_E_ARG, "anima_linear_qkv: xq without xs");
+    if (!al(qx, 16)) return fail(c, ANIMA_E_ARG, "anima_linear_qkv: xq must be 16-byte aligned");
+  }
+  const float alpha = d->alpha != 0.0f ? d->alpha : 1.0f;
+  GemmArgs g{qx, sx, W->w, W->scale, W->srel, W->codebook, W->bias, d->out, ldc, alpha, ANIMA_ACT_NONE, ANIMA_EPI_STORE,
+             nullptr, 0, nullptr, (int)M, N, K, nullptr, 0};
+  g.kv = p->kv_prep;
+  g.kv_plane = p->kv_prep_bytes / 2;
+  g.kn = p->k_norm;
+  g.cs = p->rope_cs;
+  g.sin_off = p->rope_sin_off;
+  g.eps = p->eps;
+  g.L = p->L;
+  g.Lkp = p->L;
+  g.H = H;
+  g.kcol = H * HD_K;
+  g.vcol = 2 * H * HD_K;
+  const bool w4 = W->kind == ANIMA_W_W4;
+  int rc;
+  {
+    Launch L(c, w4 ? "gemm.w4a8_qkv" : "gemm.i8_qkv", 2.0 * M * N * K, 0.0);
+    // persistent 256 x 256 tiles (a tile holds two whole heads); one workgroup per CU at most
+    const int64_t tiles = (int64_t)(N / 256) * ((M + 255) / 256);
+    const dim3 grid((unsigned)(tiles < c->num_cus ? tiles : c->num_cus)), block(512);
+    if (w4) hipLaunchKernelGGL((gemm_i8_256<ANIMA_EPI_STORE, true, true>), grid, block, 0, c->stream, g);
+    else hipLaunchKernelGGL((gemm_i8_256<ANIMA_EPI_STORE, false, true>), grid, block, 0, c->stream, g);
     rc = L.end();
   }
   if (tmp) anima_free(c, tmp);

@@ -138,6 +138,7 @@ int fill_random_launch(anima_ctx* c, void* dst, int64_t n, int kind, uint64_t se
 
 // ---- kernel launchers (gemm.hip)
 int linear_launch(anima_ctx* c, const anima_linear_desc* d);
+int linear_qkv_launch(anima_ctx* c, const anima_linear_desc* d, const anima_qkv_desc* p);
 int linear_grouped_bf16_launch(anima_ctx* c, int G, int64_t M, int N, int K, const float* x, int64_t ldx,
                                int64_t x_gs, const uint16_t* w, int64_t w_gs, const float* bias, int64_t bias_gs,
                                float* out, int64_t ldc, int64_t out_gs);

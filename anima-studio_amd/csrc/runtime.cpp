@@ -645,6 +645,11 @@ int anima_linear(anima_ctx* c, const anima_linear_desc* d) {
   return linear_launch(c, d);
 }
 
+int anima_linear_qkv(anima_ctx* c, const anima_linear_desc* d, const anima_qkv_desc* p) {
+  CHECK_CTX(c);
+  return linear_qkv_launch(c, d, p);
+}
+
 int anima_linear_grouped_bf16(anima_ctx* c, int G, int64_t M, int N, int K, const float* x, int64_t ldx,
                               int64_t x_gstride, const uint16_t* w, int64_t w_gstride, const float* bias,
                               int64_t bias_gstride, float* out, int64_t ldc, int64_t out_gstride) {
@@ -695,6 +700,9 @@ static const struct {
     ABI_FIELD(anima_limits, workgroup_storage_size), ABI_FIELD(anima_limits, max_workgroup_size),
     ABI_FIELD(anima_limits, max_workgroups_per_dimension), ABI_FIELD(anima_limits, compute_units),
     ABI_FIELD(anima_limits, wavefront_size), ABI_FIELD(anima_limits, clock_khz), ABI_FIELD(anima_limits, arch),
+    ABI_SIZE(anima_qkv_desc), ABI_FIELD(anima_qkv_desc, B), ABI_FIELD(anima_qkv_desc, L), ABI_FIELD(anima_qkv_desc, H),
+    ABI_FIELD(anima_qkv_desc, k_norm), ABI_FIELD(anima_qkv_desc, rope_cs), ABI_FIELD(anima_qkv_desc, rope_sin_off),
+    ABI_FIELD(anima_qkv_desc, eps), ABI_FIELD(anima_qkv_desc, kv_prep), ABI_FIELD(anima_qkv_desc, kv_prep_bytes),
 };
 #undef ABI_FIELD
 #undef ABI_SIZE

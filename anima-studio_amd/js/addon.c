@@ -743,6 +743,40 @@ static napi_value js_linear(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* linearQkv(ctx, weight, desc, qkv) -- desc as for linear(); qkv mirrors anima_qkv_desc */
+static napi_value js_linear_qkv(napi_env env, napi_callback_info info) {
+  napi_value a[4];
+  get_args(env, info, 4, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  napi_value wo = a[1], o = a[2], k = a[3];
+  anima_weight w;
+  read_weight(env, wo, &w);
+  anima_linear_desc d;
+  memset(&d, 0, sizeof d);
+  d.M = (int64_t)pnum(env, o, "M");
+  d.W = &w;
+  d.x = (const float*)pptr(env, o, "x");
+  d.x_rotated = (int)pnum(env, o, "xRotated");
+  d.xq = (const int8_t*)pptr(env, o, "xq");
+  d.xs = (const float*)pptr(env, o, "xs");
+  d.out = (float*)pptr(env, o, "out");
+  d.ldc = (int64_t)pnum(env, o, "ldc");
+  d.alpha = (float)pnum(env, o, "alpha");
+  anima_qkv_desc q;
+  memset(&q, 0, sizeof q);
+  q.B = (int)pnum(env, k, "B");
+  q.L = (int)pnum(env, k, "L");
+  q.H = (int)pnum(env, k, "H");
+  q.k_norm = (const float*)pptr(env, k, "kNorm");
+  q.rope_cs = (const float*)pptr(env, k, "cs");
+  q.rope_sin_off = (int64_t)pnum(env, k, "sinOff");
+  q.eps = (float)pnum(env, k, "eps");
+  q.kv_prep = pptr(env, k, "kvPrep");
+  q.kv_prep_bytes = (int64_t)pnum(env, k, "kvPrepBytes");
+  CHECK_RC(env, c, anima_linear_qkv(c, &d, &q));
+  return NULL;
+}
+
 /* split3(ctx, src, dst, n) */
 static napi_value js_split3(napi_env env, napi_callback_info info) {
   napi_value a[4];
@@ -889,7 +923,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       FN("qkNormRope", js_qk_norm_rope), FN("rmsnorm", js_rmsnorm), FN("rope", js_rope),
       FN("hadamard", js_hadamard), FN("quantRows", js_quant_rows), FN("layernormMod", js_layernorm_mod),
       FN("elementwise", js_elementwise), FN("zero", js_zero), FN("patchify", js_patchify), FN("linearGroupedBf16", js_linear_grouped_bf16), FN("unpatchify", js_unpatchify), FN("fillRandom", js_fill_random),
-      FN("linear", js_linear), FN("samplerStep", js_sampler_step), FN("attentionKvBytes", js_attention_kv_bytes), FN("split3", js_split3), FN("lastError", js_last_error),
+      FN("linear", js_linear), FN("linearQkv", js_linear_qkv), FN("samplerStep", js_sampler_step), FN("attentionKvBytes", js_attention_kv_bytes), FN("split3", js_split3), FN("lastError", js_last_error),
       FN("graphBegin", js_graph_begin), FN("graphEnd", js_graph_end), FN("graphLaunch", js_graph_launch),
       FN("graphDestroy", js_graph_destroy), FN("conv3x3", js_conv3x3), FN("channelNorm", js_channel_norm), FN("toRgba", js_to_rgba),
       FN("weightUnpackW4", js_weight_unpack_w4),

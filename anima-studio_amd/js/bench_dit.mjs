@@ -13,6 +13,8 @@
 //                     [--vae]  (also time the VAE decode of this size's latent, bf16 and fp32 precision)
 //                     [--w4 packed|int8]  (W4 weights unpacked inside each GEMM, or converted to their
 //                      int8 grid once at load: bit-identical products)
+//                     [--no-fuse-qkv]  (the self-attention K / V converted by the attention's own prep
+//                      kernel instead of in the QKV GEMM epilogue)
 //                     [--unpacked-too]  (with packed W4: also time the step after converting the W4
 //                      linears to their int8 grid in place, reported as w4_unpacked)
 //                     [--graph [--rounds 3]]  (also the forward replayed from a HIP graph recorded
@@ -68,6 +70,7 @@ async function main() {
   // nibble unpack per GEMM; one byte per weight)
   const w4mode = arg("w4", "packed");
   const unpacked = w4mode === "int8" ? dit.unpackW4() : 0;
+  if (arg("no-fuse-qkv", false)) dit.fuseQkv = false;
   const ctxs = [0, 1].map((b) => {
     const t = gpu.empty([Lk, 1024]);
     native.fillRandom(gpu.ctx, t.buf, t.size, 4, 77 + b, 1.0, 0.0); // ~N(0,1)

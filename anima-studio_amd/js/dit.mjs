@@ -150,6 +150,9 @@ export class AnimaDiT {
     // attention precision: bf16 matrix-core operands with fp32 accumulation ("fp32": the fp32-MFMA
     // kernels, the reference's arithmetic); prepareContext records the one its K/V were made for
     this.precision = "bf16";
+    // self-attention K / V prepared in the QKV GEMM's epilogue where the weight allows
+    // (ops.qkvFusable); false runs the linear and the attention's own K / V conversion
+    this.fuseQkv = true;
   }
 
   // Converts every W4 block linear to its int8 grid once (ops.unpackW4): the GEMMs then run on the
@@ -389,19 +392,32 @@ export class AnimaDiT {
       const b = this.blocks[i];
       const m = tc.blocks[i];
 
-      // self-attention: stacked QKV GEMM, then attention with q/k RMSNorm + RoPE fused
+      // self-attention: stacked QKV GEMM, then attention with q/k RMSNorm + RoPE fused.  With an
+      // int8 / W4 stacked weight (no LoRA) and bf16 attention, the GEMM's epilogue writes K
+      // (normed, rotated) and V^T straight into the attention's operand layout.
       let nf;
-      let qkv;
-      if (b.self.qkv) {
+      let a;
+      if (b.self.qkv && this.fuseQkv && this.precision === "bf16" && ops.qkvFusable(b.self.qkv, L, HEADS)) {
         nf = normFor(gpu, x, m.self, b.self.qkv);
-        qkv = project(gpu, nf, b.self.qkv, M, { name: "dit.self.qkv" });
+        const f = ops.linearQkv(gpu, null, b.self.qkv, { B, L, H: HEADS, xq: nf.xq, kNorm: b.self.kn, cs });
         releaseNorm(nf);
+        a = ops.attention(gpu, { q: f.q, kvPrep: f.kvPrep, B, Lq: L, Lk: L, H: HEADS, D: HD, ldq: D, qNorm: b.self.qn,
+          cs, precision: "bf16" });
+        f.q.release();
+        f.kvPrep.release();
       } else {
-        qkv = projectParts(gpu, x, m.self, [b.self.q, b.self.k, b.self.v], M);
+        let qkv;
+        if (b.self.qkv) {
+          nf = normFor(gpu, x, m.self, b.self.qkv);
+          qkv = project(gpu, nf, b.self.qkv, M, { name: "dit.self.qkv" });
+          releaseNorm(nf);
+        } else {
+          qkv = projectParts(gpu, x, m.self, [b.self.q, b.self.k, b.self.v], M);
+        }
+        a = ops.attention(gpu, { q: qkv, k: qkv, v: qkv, B, Lq: L, Lk: L, H: HEADS, D: HD, ldq: 3 * D, ldk: 3 * D,
+          ldv: 3 * D, qOff: 0, kOff: D, vOff: 2 * D, qNorm: b.self.qn, kNorm: b.self.kn, cs, precision: this.precision });
+        qkv.release();
       }
-      let a = ops.attention(gpu, { q: qkv, k: qkv, v: qkv, B, Lq: L, Lk: L, H: HEADS, D: HD, ldq: 3 * D, ldk: 3 * D,
-        ldv: 3 * D, qOff: 0, kOff: D, vOff: 2 * D, qNorm: b.self.qn, kNorm: b.self.kn, cs, precision: this.precision });
-      qkv.release();
       ops.linear(gpu, a, b.self.o, { M, out: x, resid: true, gate: m.self, gOff: 2 * D });
       a.release();
 

@@ -96,6 +96,37 @@ export function linear(gpu, x, W, opts) {
   return out;
 }
 
+// The stacked QKV projection of a DiT self-attention with the attention's K / V operand
+// preparation in the GEMM epilogue (anima_linear_qkv; app/models/dit.js:266-304 runs the linear,
+// then qkNormRope, then the attention).  Returns { q: [M, H*128] fp32, kvPrep } for
+// attention(gpu, { q, kvPrep, qNorm, cs, ... }); K is RMS-normed (kNorm) and rotated (cs) and the
+// prepared bytes equal attentionPrepareKV of the plain linear's output.  Callers check
+// qkvFusable first (int8 / W4 weights without LoRA, tokens per image a multiple of 64).
+export function qkvFusable(W, L, H) {
+  return needsRotation(W) && !(W.lora && W.lora.length) && L % 64 === 0 && H % 2 === 0 && W.N === 3 * H * 128;
+}
+
+export function linearQkv(gpu, x, W, opts) {
+  const o = opts || {};
+  const { B, L, H } = o;
+  const M = B * L;
+  const q = gpu.empty([M, H * 128]);
+  const bytes = native.attentionKvBytes(B, H, L, 0);
+  const kvPrep = gpu.empty([bytes], "u8");
+  const d = { M, out: q.buf, ldc: H * 128, alpha: o.alpha || 0 };
+  if (o.xq) {
+    d.xq = o.xq.q.buf;
+    d.xs = o.xq.s.buf;
+  } else {
+    d.x = x.buf;
+    d.xRotated = o.xRotated ? 1 : 0;
+  }
+  const w = weightArg(W);
+  native.linearQkv(gpu.ctx, w, d, { B, L, H, kNorm: o.kNorm.buf, cs: o.cs.buf, sinOff: o.cs.sinOff, eps: o.eps || 1e-6,
+    kvPrep: kvPrep.buf, kvPrepBytes: bytes });
+  return { q, kvPrep };
+}
+
 // Adds (or, storeFirst, stores where it comes first over a column range) every LoRA entry's
 // scale * B (A x_in) into columns [off, off + n) of out (row stride ldc) (ops.js:70-87).
 // Entries { A: [r, K] f32, Ar: A H (ConvRot targets), B: [n, r] f32, r, scale, off, n }: the

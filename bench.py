@@ -357,6 +357,62 @@ def linears(m, ctx, reps):
                                      "TOPS": round(ops / ms / 1e9, 1), "frac_int8_peak": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4)}
             for b in bufs:
                 b.release()
+    res.update(qkv_operands(m, ctx, rng, M, reps))
+    return res
+
+
+def qkv_operands(m, ctx, rng, M, reps):
+    """The self-attention QKV projection at M = 8192 (B=2, 4096 tokens, 16 heads) with the
+    attention's K / V operand preparation: fused into the GEMM epilogue (anima_linear_qkv) and
+    as the plain linear followed by the attention's K / V conversion; kernel times summed."""
+    import numpy as np
+
+    B, L, H, K = 2, 4096, 16, 2048
+    N = 3 * H * 128
+    res = {}
+    kn = ctx.upload((1 + 0.02 * rng.standard_normal(128)).astype(np.float32))
+    cs = ctx.upload(m.dit_rope_table(64, 64))
+    nbytes = m.Context.attention_kv_bytes(B, H, L, m.PREC_BF16)
+    for kind in ("i8", "w4"):
+        bufs = [ctx.upload(rng.integers(-127, 128, size=(M, K), dtype=np.int8)),
+                ctx.upload(rng.uniform(0.001, 0.01, M).astype(np.float32)),
+                ctx.upload(rng.uniform(0.001, 0.01, N).astype(np.float32))]
+        xq, xs, sw = bufs
+        if kind == "i8":
+            bufs.append(ctx.upload(rng.integers(-127, 128, size=(N, K), dtype=np.int8)))
+            W = m.weight(m.W_I8, N, K, bufs[-1], scale=sw)
+        else:
+            bufs += [ctx.upload(rng.integers(0, 256, size=(N, K // 2), dtype=np.uint8)),
+                     ctx.upload(rng.integers(0x40, 0x7f, size=(N, K // 16), dtype=np.uint8)),
+                     ctx.upload(np.linspace(-1, 1, 16).astype(np.float32))]
+            W = m.weight(m.W_W4, N, K, bufs[-3], scale=sw, srel=bufs[-2], codebook=bufs[-1])
+        out, q, prep = ctx.empty((M, N)), ctx.empty((M, H * 128)), ctx.empty(nbytes, np.uint8)
+        bufs += [out, q, prep]
+
+        def fused():
+            ctx.linear_qkv(W, M, q, B=B, L=L, H=H, k_norm=kn, rope_cs=cs, rope_sin_off=L * 64, kv_prep=prep, xq=xq,
+                           xs=xs, ldc=H * 128)
+
+        def plain():
+            ctx.linear(W, M, out, xq=xq, xs=xs)
+            ctx.attention(q=out, k=out, v=out, o=out, prepare_into=prep, B=B, Lq=L, Lk=L, H=H, D=128, ldq=N, ldk=N,
+                          ldv=N, k_off=H * 128, v_off=2 * H * 128, k_norm=kn, rope_cs=cs, rope_sin_off=L * 64)
+
+        for name, call in (("fused", fused), ("plain", plain)):
+            settle(ctx, call)
+            ctx.profile(True)
+            ctx.profile_reset()
+            for _ in range(reps):
+                call()
+            rep = ctx.profile_report()
+            ctx.profile(False)
+            res[f"{kind}.qkv_attn_operands_{name}"] = {
+                "ms": round(sum(r["ms"] for r in rep) / reps, 4),
+                "kernels": {r["name"]: round(r["ms"] / r["count"], 4) for r in rep}}
+        for b in bufs:
+            b.release()
+    kn.release()
+    cs.release()
     return res
 
 

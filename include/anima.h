@@ -105,7 +105,8 @@ int anima_timer_stop(anima_ctx* ctx, float* ms);
 
 /* ABI self-description, for bindings that restate the descriptor structs below (ctypes, FFI):
  * the byte offset of `field` in the struct named `type` -- "anima_attn_desc", "anima_linear_desc",
- * "anima_weight", "anima_sampler_desc", "anima_conv_desc", "anima_limits" -- or the struct's size when `field` is
+ * "anima_weight", "anima_sampler_desc", "anima_conv_desc", "anima_limits", "anima_qkv_desc" -- or the
+ * struct's size when `field` is
  * NULL; -1 for a name this library does not know.  No counterpart in the reference (its op layer
  * has no C ABI); it lets a binding refuse to load when its layout differs from the library's. */
 int64_t anima_abi_offset(const char* type, const char* field);
@@ -405,6 +406,30 @@ typedef struct {
  * and the store / residual / gated-residual epilogue of gemm.js:186-192.
  * i8/w4 need K % 64 == 0 (and K <= 8192 when x is quantized here). */
 int anima_linear(anima_ctx* ctx, const anima_linear_desc* desc);
+
+/* The stacked QKV projection of a DiT block with the attention's operand preparation in its
+ * epilogue: app/models/dit.js:266-304 runs ops.linear (qkv), ops.qkNormRope (q and k in place) and
+ * the flash attention, whose operands this library converts first (anima_attention_prepare_kv).
+ * Here the GEMM that produces qkv writes, per token,
+ *   Q  columns [0, 128 H)        fp32 into d->out (row stride d->ldc >= 128 H), as anima_linear;
+ *   K  columns [128 H, 256 H)    RMSNorm(k_norm, eps) + RoPE (rope_cs, as anima_attn_desc), bf16,
+ *   V  columns [256 H, 384 H)    bf16, transposed,
+ * K and V into kv_prep in the layout of anima_attention_prepare_kv(B, Lq = Lk = L, H heads,
+ * bf16) -- the same bytes, bit for bit, as preparing this linear's fp32 output -- for
+ * anima_attention(desc->kv_prep = kv_prep) with q = d->out, q_norm and the same RoPE table.
+ * Requirements: int8 or W4 weights with N = 3 * 128 * H (H even), the store epilogue (bias and
+ * alpha allowed; no activation, add term or acc_out), M = B * L with L % 64 == 0, 16-byte aligned
+ * buffers; ANIMA_E_UNSUPPORTED otherwise (the caller then runs anima_linear + anima_attention). */
+typedef struct {
+  int B, L, H;          /* batch elements, tokens each (M = B * L), heads of 128 */
+  const float* k_norm;  /* [128] */
+  const float* rope_cs; /* cos block [rows][64] then sin block at rope_sin_off, rows >= L */
+  int64_t rope_sin_off;
+  float eps;
+  void* kv_prep;        /* anima_attention_kv_bytes(B, H, L, ANIMA_PREC_BF16) bytes */
+  int64_t kv_prep_bytes;
+} anima_qkv_desc;
+int anima_linear_qkv(anima_ctx* ctx, const anima_linear_desc* desc, const anima_qkv_desc* qkv);
 
 /* The int8 grid of a W4 weight, grid[n][k] = clamp(rint(codebook[code] * fp8(s_rel)), -127, 127)
  * for the 4-bit code of (n, k): the values gemm.js:141-158's W4 B-loader multiplies

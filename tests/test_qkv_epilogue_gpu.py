@@ -1,0 +1,138 @@
+"""The stacked QKV projection with the attention's operand preparation in its epilogue
+(anima_linear_qkv): Q columns as fp32, K rows RMS-normed + roped in bf16 and V^T in bf16, in the
+layout of anima_attention_prepare_kv.
+
+Bars: the K / V operand bytes equal those of anima_linear followed by
+anima_attention_prepare_kv on its fp32 output, byte for byte (both form the row norm in the same
+reduction tree), and the Q columns equal anima_linear's, bit for bit; the K rows are checked
+against a float64 RMSNorm + RoPE of the linear's fp32 K columns (within bf16 rounding); the
+attention on the fused operands equals the plain attention call bit for bit."""
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from helpers import amd, report
+from test_linear_gpu import FIXED_LUT, int8_weight, w4_weight
+
+pytestmark = pytest.mark.gpu
+
+HD = 128
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = amd().Context(0)
+    yield c
+    c.close()
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def bf16_to_f32(u16):
+    return (u16.astype(np.uint32) << 16).view(np.float32)
+
+
+def make_weight(ctx, m, kind, seed, N, K, bias):
+    bufs = []
+    b = ctx.upload((0.05 * orc.randn(seed + 7, N)).astype(np.float32)) if bias else None
+    if b is not None:
+        bufs.append(b)
+    if kind == "i8":
+        qw, sw = int8_weight(seed, N, K)
+        bufs += [ctx.upload(qw), ctx.upload(sw)]
+        return m.weight(m.W_I8, N, K, bufs[-2], scale=bufs[-1], bias=b), bufs
+    codes, srel, sw = w4_weight(seed, N, K)
+    bufs += [ctx.upload(codes), ctx.upload(srel), ctx.upload(sw), ctx.upload(FIXED_LUT)]
+    return m.weight(m.W_W4, N, K, bufs[-4], scale=bufs[-2], srel=bufs[-3], codebook=bufs[-1], bias=b), bufs
+
+
+@pytest.mark.parametrize("kind,B,Hp,Wp,H,K,bias", [("i8", 2, 16, 16, 2, 512, False), ("w4", 3, 8, 24, 4, 1024, True),
+                                                   ("i8", 2, 64, 64, 16, 2048, True), ("w4", 2, 64, 64, 16, 2048, False)])
+def test_linear_qkv_operands_bit_exact(ctx, kind, B, Hp, Wp, H, K, bias):
+    L = Hp * Wp
+    M, N = B * L, 3 * H * HD
+    case(f"linear_qkv {kind} B={B} L={L} H={H} K={K} bias={bias}")
+    m = amd()
+    W, wbufs = make_weight(ctx, m, kind, 300 + K + H, N, K, bias)
+    rng = np.random.default_rng(400 + L)
+    xq = ctx.upload(rng.integers(-127, 128, size=(M, K), dtype=np.int8))
+    xs = ctx.upload(rng.uniform(0.002, 0.02, M).astype(np.float32))
+    kn = (1 + 0.02 * orc.randn(401, HD)).astype(np.float32)
+    qn = (1 + 0.02 * orc.randn(402, HD)).astype(np.float32)
+    cs_np = orc.dit_rope_table(Hp, Wp)
+    dkn, dqn, dcs = ctx.upload(kn), ctx.upload(qn), ctx.upload(cs_np)
+    sin_off = L * 64
+    nbytes = m.Context.attention_kv_bytes(B, H, L, m.PREC_BF16)
+    # reference: the plain linear, then the K / V conversion of its fp32 output
+    ref = ctx.empty((M, N))
+    ctx.linear(W, M, ref, xq=xq, xs=xs)
+    prep_ref = ctx.empty(nbytes, np.uint8)
+    common = dict(B=B, Lq=L, Lk=L, H=H, D=HD, ldq=N, ldk=N, ldv=N, k_off=H * HD, v_off=2 * H * HD, precision=m.PREC_BF16)
+    ctx.attention(q=ref, k=ref, v=ref, o=ref, prepare_into=prep_ref, k_norm=dkn, rope_cs=dcs, rope_sin_off=sin_off,
+                  **common)
+    # fused: Q into a [M, H*128] buffer, K / V straight into the operand layout
+    q = ctx.empty((M, H * HD))
+    prep = ctx.empty(nbytes, np.uint8)
+    ctx.linear_qkv(W, M, q, B=B, L=L, H=H, k_norm=dkn, rope_cs=dcs, rope_sin_off=sin_off, kv_prep=prep, xq=xq, xs=xs,
+                   ldc=H * HD)
+    r = ref.numpy()
+    got_prep, want_prep = prep.numpy(), prep_ref.numpy()
+    kbytes = nbytes // 2
+    print(f"K bytes differing: {int((got_prep[:kbytes] != want_prep[:kbytes]).sum())}, "
+          f"V^T bytes differing: {int((got_prep[kbytes:] != want_prep[kbytes:]).sum())}", flush=True)
+    assert np.array_equal(q.numpy(), r[:, :H * HD])
+    assert np.array_equal(got_prep, want_prep)
+    # K rows against float64 RMSNorm + RoPE of the fp32 K columns (the bf16 rounding bound)
+    kplane = bf16_to_f32(got_prep[:kbytes].view(np.uint16)).reshape(B, H, L, HD)
+    rows = np.unique(np.concatenate([np.arange(0, 8), rng.choice(L, 24, replace=False), np.arange(L - 8, L)]))
+    cos = cs_np[:L * 64].reshape(L, 64).astype(np.float64)
+    sin = cs_np[sin_off:sin_off + L * 64].reshape(L, 64).astype(np.float64)
+    for b in (0, B - 1):
+        k = r[b * L + rows, H * HD:2 * H * HD].astype(np.float64).reshape(len(rows), H, HD)
+        kn64 = k / np.sqrt((k * k).mean(-1, keepdims=True) + 1e-6) * kn.astype(np.float64)
+        lo, hi = kn64[..., :64], kn64[..., 64:]
+        c, s = cos[rows][:, None, :], sin[rows][:, None, :]
+        want = np.concatenate([lo * c - hi * s, hi * c + lo * s], -1)
+        got = kplane[b][:, rows].transpose(1, 0, 2)
+        err = np.abs(got - want) / np.maximum(np.abs(want), 1e-3)
+        assert err.max() <= 2.0 ** -8 + 1e-5, err.max()
+    # attention on the fused operands = the plain call
+    if L <= 1024:
+        o1, o2 = ctx.empty((M, H * HD)), ctx.empty((M, H * HD))
+        ctx.attention(q=ref, k=ref, v=ref, o=o1, q_norm=dqn, k_norm=dkn, rope_cs=dcs, rope_sin_off=sin_off, **common)
+        ctx.attention(q=q, k=None, v=None, o=o2, kv_prep=prep, q_norm=dqn, rope_cs=dcs, rope_sin_off=sin_off,
+                      **dict(common, ldq=H * HD))
+        assert np.array_equal(o1.numpy(), o2.numpy())
+        o1.release()
+        o2.release()
+    for x in wbufs + [xq, xs, dkn, dqn, dcs, ref, prep_ref, q, prep]:
+        x.release()
+
+
+def test_linear_qkv_refusals(ctx):
+    """Shapes the fused epilogue does not cover are refused on the host before any launch:
+    L % 64 != 0 (ANIMA_E_UNSUPPORTED), a wrong operand buffer size and N != 3 * 128 * H
+    (ANIMA_E_ARG)."""
+    case("linear_qkv host refusals")
+    m = amd()
+    H, K = 2, 256
+    N = 3 * H * HD
+    qw, sw = int8_weight(501, N, K)
+    dq, ds = ctx.upload(qw), ctx.upload(sw)
+    W = m.weight(m.W_I8, N, K, dq, scale=ds)
+    kn, cs = ctx.upload(np.ones(HD, np.float32)), ctx.upload(orc.dit_rope_table(8, 12))
+    for L, Hh, exp in ((96, H, -5), (128, 3, -1)):
+        M = 2 * L
+        xq, xs, out = ctx.empty((M, K), np.int8), ctx.empty(M), ctx.empty((M, N))
+        prep = ctx.empty(m.Context.attention_kv_bytes(2, Hh, L, m.PREC_BF16), np.uint8)
+        with pytest.raises(m.AnimaError) as e:
+            ctx.linear_qkv(W, M, out, B=2, L=L, H=Hh, k_norm=kn, rope_cs=cs, rope_sin_off=96 * 64, kv_prep=prep,
+                           xq=xq, xs=xs)
+        assert e.value.code == exp, (L, Hh, e.value)
+        for x in (xq, xs, out, prep):
+            x.release()
+    for x in (dq, ds, kn, cs):
+        x.release()
