@@ -21,6 +21,7 @@ ANIMA_OK = 0
 PREC_BF16 = 0
 PREC_FP32 = 1
 W_BF16, W_I8, W_W4, W_F32, W_F32S3 = 0, 1, 2, 3, 4
+W4_GRID_SCRATCH, W4_IN_GEMM = 0, 1
 ACT = {"none": 0, "gelu": 1, "silu": 2}
 EPI_STORE, EPI_RESID, EPI_GATED = 0, 1, 2
 EW = {"silu_mul": 0, "add": 1, "silu": 2, "copy": 3}
@@ -142,6 +143,7 @@ def lib():
             getattr(L, n).argtypes = [_vp]
         L.anima_mem_stats.argtypes = [_vp, P(ctypes.c_uint64), P(ctypes.c_uint64), P(ctypes.c_uint64)]
         L.anima_device_limits.argtypes = [_vp, P(Limits)]
+        L.anima_set_w4_path.argtypes = [_vp, ctypes.c_int]
         L.anima_alloc.argtypes = [_vp, ctypes.c_size_t, P(_vp)]
         L.anima_free.argtypes = [_vp, _vp]
         for n in ("anima_h2d", "anima_d2h", "anima_d2d"):
@@ -280,6 +282,10 @@ class Context:
         a, p, q = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
         self._check(lib().anima_mem_stats(self.h, ctypes.byref(a), ctypes.byref(p), ctypes.byref(q)))
         return {"allocated": a.value, "peak": p.value, "pooled": q.value}
+
+    def set_w4_path(self, path):
+        """W4_GRID_SCRATCH (default) or W4_IN_GEMM for the large W4 products (anima_set_w4_path)."""
+        self._check(lib().anima_set_w4_path(self.h, path))
 
     def limits(self):
         """The device limits (anima_device_limits), as a dict."""

@@ -869,12 +869,31 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
 
 // ------------------------------------------------------------------ W4 -> int8 grid (load time)
 //
-// Thread = 32 weights of a row: 16 code bytes (low nibble = even k) and their two s_rel bytes;
-// the 16-entry tables of all 256 s_rel values are built in LDS per workgroup as in the GEMMs.
-__global__ __launch_bounds__(256) void w4_unpack_kernel(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ srel,
-                                                        const float* __restrict__ cb, int8_t* __restrict__ out, int64_t nchunk,
-                                                        int K) {
+// A W4 weight is a row-major stream of 16-weight groups: group g has code bytes [8g, 8g + 8)
+// (low nibble = even k), s_rel byte g and grid bytes [16g, 16g + 16), whatever the row length
+// (K % 16 == 0).  Thread = W4_UNPACK_U groups, 256 groups apart, whose loads are all issued
+// before the first lookup; a wave reads 512 contiguous code bytes and 64 s_rel bytes and writes
+// 1 KiB per instruction.  The 16-entry tables of all 256 s_rel values are built in LDS per
+// workgroup as in the GEMMs, while the first groups' loads are in flight.
+constexpr int W4_UNPACK_U = 4;
+__global__ __launch_bounds__(256) void w4_unpack_kernel(const uint2* __restrict__ codes, const uint8_t* __restrict__ srel,
+                                                        const float* __restrict__ cb, uint4* __restrict__ out, int64_t ngroups) {
   __shared__ __attribute__((aligned(16))) uint32_t lut[256 * 4];
+  const int64_t stride = (int64_t)gridDim.x * (256 * W4_UNPACK_U);
+  int64_t g0 = (int64_t)blockIdx.x * (256 * W4_UNPACK_U) + threadIdx.x;
+  uint2 w[W4_UNPACK_U];
+  uint32_t sr[W4_UNPACK_U];
+  auto load = [&]() {
+#pragma unroll
+    for (int u = 0; u < W4_UNPACK_U; u++) {
+      const int64_t g = g0 + 256 * u;
+      if (g < ngroups) {
+        w[u] = codes[g];
+        sr[u] = srel[g];
+      }
+    }
+  };
+  load();
   for (int i = threadIdx.x; i < 256 * 4; i += 256) {
     const float s = fp8e4m3((uint32_t)(i >> 2));
     uint32_t packed = 0;
@@ -887,20 +906,40 @@ __global__ __launch_bounds__(256) void w4_unpack_kernel(const uint8_t* __restric
     lut[i] = packed;
   }
   __syncthreads();
-  const int cpr = K / 32;  // chunks of 32 weights per row
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nchunk; i += (int64_t)gridDim.x * 256) {
-    const int64_t row = i / cpr;
-    const int c = (int)(i - row * cpr);
-    const uint4 w = *(const uint4*)(codes + row * (K / 2) + 16 * c);
-    const uint8_t* sp = srel + row * (K / 16) + 2 * c;
-    const uint4 t0 = *(const uint4*)&lut[4 * sp[0]];
-    const uint4 t1 = *(const uint4*)&lut[4 * sp[1]];
-    const uint2 d0 = decode8(w.x, t0.x, t0.y, t0.z, t0.w), d1 = decode8(w.y, t0.x, t0.y, t0.z, t0.w);
-    const uint2 d2 = decode8(w.z, t1.x, t1.y, t1.z, t1.w), d3 = decode8(w.w, t1.x, t1.y, t1.z, t1.w);
-    uint4* o = (uint4*)(out + row * K + 32 * c);
-    o[0] = make_uint4(d0.x, d0.y, d1.x, d1.y);
-    o[1] = make_uint4(d2.x, d2.y, d3.x, d3.y);
+  while (g0 < ngroups) {
+#pragma unroll
+    for (int u = 0; u < W4_UNPACK_U; u++) {
+      const int64_t g = g0 + 256 * u;
+      if (g < ngroups) {
+        const uint4 t = *(const uint4*)&lut[4 * sr[u]];
+        const uint2 lo = decode8(w[u].x, t.x, t.y, t.z, t.w), hi = decode8(w[u].y, t.x, t.y, t.z, t.w);
+        out[g] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      }
+    }
+    g0 += stride;
+    load();
   }
+}
+
+int weight_unpack_w4_launch(anima_ctx* c, const anima_weight* W, int8_t* grid);
+
+// ANIMA_W4_GRID_SCRATCH: the int8 grid of W in a pooled buffer of N * K bytes (the caller frees
+// it after the GEMM that reads it; the pool is stream-ordered), and g pointed at it as an int8
+// weight.  The scale (s_channel) and bias stay the W4 weight's.
+static int w4_grid_scratch(anima_ctx* c, const anima_weight* W, GemmArgs& g, void** grid) {
+  *grid = nullptr;
+  int rc = anima_alloc(c, (size_t)W->N * W->K, grid);
+  if (rc) return rc;
+  rc = weight_unpack_w4_launch(c, W, (int8_t*)*grid);
+  if (rc) {
+    anima_free(c, *grid);
+    *grid = nullptr;
+    return rc;
+  }
+  g.w = *grid;
+  g.srel = nullptr;
+  g.cb = nullptr;
+  return ANIMA_OK;
 }
 
 int weight_unpack_w4_launch(anima_ctx* c, const anima_weight* W, int8_t* grid) {
@@ -910,11 +949,11 @@ int weight_unpack_w4_launch(anima_ctx* c, const anima_weight* W, int8_t* grid) {
   if (W->N < 1 || W->K < 32 || W->K % 32) return fail(c, ANIMA_E_ARG, "anima_weight_unpack_w4: N=%d K=%d (K %% 32 == 0)", W->N, W->K);
   if (((uintptr_t)W->w & 15) || ((uintptr_t)grid & 15))
     return fail(c, ANIMA_E_ARG, "anima_weight_unpack_w4: codes and grid must be 16-byte aligned");
-  const int64_t nchunk = (int64_t)W->N * (W->K / 32);
+  const int64_t ngroups = (int64_t)W->N * (W->K / 16);
   Launch L(c, "w4.unpack", 0.0, (double)W->N * W->K * 1.5 + (double)W->N * W->K / 16);
-  const int64_t blocks = (nchunk + 255) / 256;
-  hipLaunchKernelGGL(w4_unpack_kernel, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(256), 0, c->stream,
-                     (const uint8_t*)W->w, W->srel, W->codebook, grid, nchunk, W->K);
+  const int64_t blocks = (ngroups + 256 * W4_UNPACK_U - 1) / (256 * W4_UNPACK_U), cap = 8LL * c->num_cus;
+  hipLaunchKernelGGL(w4_unpack_kernel, dim3((unsigned)(blocks < cap ? blocks : cap)), dim3(256), 0, c->stream,
+                     (const uint2*)W->w, W->srel, W->codebook, (uint4*)grid, ngroups);
   return L.end();
 }
 
@@ -1987,19 +2026,29 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
   const bool vec = N % 4 == 0 && g.ldc % 4 == 0 && al(g.out, 16) && al(g.sw, 16) && (!g.bias || al(g.bias, 16)) &&
                    (g.epi != ANIMA_EPI_GATED || al(g.gate + g.gate_off, 16)) && (!g.add || (al(g.add, 16) && g.ld_add % 4 == 0));
   const bool big = vec && tiles256 >= c->num_cus && tiles256 <= 0x7fffffff;
+  void* grid8 = nullptr;
+  bool w4k = w4;  // the GEMM unpacks W4 codes itself
+  if (big && w4 && c->w4_path == ANIMA_W4_GRID_SCRATCH) {
+    rc = w4_grid_scratch(c, W, g, &grid8);
+    if (rc) {
+      if (tmp) anima_free(c, tmp);
+      return rc;
+    }
+    w4k = false;
+  }
   {
-    Launch L(c, w4 ? "gemm.w4a8" : "gemm.i8", 2.0 * M * N * K, 0.0);
+    Launch L(c, w4k ? "gemm.w4a8" : "gemm.i8", 2.0 * M * N * K, 0.0);
     if (big) {
       const dim3 grid((unsigned)c->num_cus), block(512);
 #define G2L(E, W) hipLaunchKernelGGL((gemm_i8_256<E, W>), grid, block, 0, c->stream, g)
       if (g.epi == ANIMA_EPI_STORE) {
-        if (w4) G2L(ANIMA_EPI_STORE, true);
+        if (w4k) G2L(ANIMA_EPI_STORE, true);
         else G2L(ANIMA_EPI_STORE, false);
       } else if (g.epi == ANIMA_EPI_RESID) {
-        if (w4) G2L(ANIMA_EPI_RESID, true);
+        if (w4k) G2L(ANIMA_EPI_RESID, true);
         else G2L(ANIMA_EPI_RESID, false);
       } else {
-        if (w4) G2L(ANIMA_EPI_GATED, true);
+        if (w4k) G2L(ANIMA_EPI_GATED, true);
         else G2L(ANIMA_EPI_GATED, false);
       }
 #undef G2L
@@ -2010,6 +2059,7 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
     }
     rc = L.end();
   }
+  if (grid8) anima_free(c, grid8);
   if (tmp) anima_free(c, tmp);
   return rc;
 }
@@ -2082,8 +2132,17 @@ int linear_qkv_launch(anima_ctx* c, const anima_linear_desc* d, const anima_qkv_
   g.H = H;
   g.kcol = H * HD_K;
   g.vcol = 2 * H * HD_K;
-  const bool w4 = W->kind == ANIMA_W_W4;
+  bool w4 = W->kind == ANIMA_W_W4;
+  void* grid8 = nullptr;
   int rc;
+  if (w4 && c->w4_path == ANIMA_W4_GRID_SCRATCH) {
+    rc = w4_grid_scratch(c, W, g, &grid8);
+    if (rc) {
+      if (tmp) anima_free(c, tmp);
+      return rc;
+    }
+    w4 = false;
+  }
   {
     Launch L(c, w4 ? "gemm.w4a8_qkv" : "gemm.i8_qkv", 2.0 * M * N * K, 0.0);
     // persistent 256 x 256 tiles (a tile holds two whole heads); one workgroup per CU at most
@@ -2093,6 +2152,7 @@ int linear_qkv_launch(anima_ctx* c, const anima_linear_desc* d, const anima_qkv_
     else hipLaunchKernelGGL((gemm_i8_256<ANIMA_EPI_STORE, false, true>), grid, block, 0, c->stream, g);
     rc = L.end();
   }
+  if (grid8) anima_free(c, grid8);
   if (tmp) anima_free(c, tmp);
   return rc;
 }

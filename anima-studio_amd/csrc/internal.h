@@ -62,6 +62,8 @@ struct anima_ctx {
   size_t ws_bytes = 0;
   // device address of this device's static K/V scratch (anima_attention_noalloc)
   void* scratch = nullptr;
+  // ANIMA_W4_GRID_SCRATCH / ANIMA_W4_IN_GEMM (anima_set_w4_path)
+  int w4_path = 0;
   // stream capture (anima_graph_begin .. anima_graph_end): buffers freed while capturing are
   // parked in cap_free, reused only by later allocations of the same capture, and owned by the
   // graph at the end (its replays keep using them); a workspace requested while capturing is such

@@ -547,6 +547,13 @@ int anima_weight_unpack_w4(anima_ctx* c, const anima_weight* w4, int8_t* grid) {
   return weight_unpack_w4_launch(c, w4, grid);
 }
 
+int anima_set_w4_path(anima_ctx* c, int path) {
+  CHECK_CTX(c);
+  if (path != ANIMA_W4_GRID_SCRATCH && path != ANIMA_W4_IN_GEMM) return fail(c, ANIMA_E_ARG, "anima_set_w4_path: unknown path %d", path);
+  c->w4_path = path;
+  return ANIMA_OK;
+}
+
 int anima_to_rgba(anima_ctx* c, const float* x, int64_t n, uint8_t* out) {
   CHECK_CTX(c);
   return to_rgba_launch(c, x, n, out);

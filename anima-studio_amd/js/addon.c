@@ -363,6 +363,17 @@ static napi_value js_trim(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* setW4Path(ctx, path): ANIMA_W4_GRID_SCRATCH (0) or ANIMA_W4_IN_GEMM (1), anima_set_w4_path */
+static napi_value js_set_w4_path(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  anima_ctx* c = ctx_of(env, argv[0]);
+  int32_t path = 0;
+  NAPI_CALL(env, napi_get_value_int32(env, argv[1], &path));
+  CHECK_RC(env, c, anima_set_w4_path(c, path));
+  return NULL;
+}
+
 /* deviceLimits(ctx) -> the adapter limits in WebGPU's names (app/gpu/device.js:63-88) */
 static napi_value js_device_limits(napi_env env, napi_callback_info info) {
   napi_value argv[1];
@@ -916,7 +927,7 @@ static napi_value Init(napi_env env, napi_value exports) {
   napi_property_descriptor desc[] = {
       FN("init", js_init), FN("destroy", js_destroy), FN("sync", js_sync), FN("mark", js_mark), FN("waitMark", js_wait_mark), FN("alloc", js_alloc),
       FN("free", js_free), FN("allocHandle", js_alloc_handle), FN("handleAddr", js_handle_addr),
-      FN("release", js_release), FN("finalized", js_finalized), FN("trim", js_trim), FN("memStats", js_mem_stats), FN("deviceLimits", js_device_limits), FN("h2d", js_h2d),
+      FN("release", js_release), FN("finalized", js_finalized), FN("trim", js_trim), FN("memStats", js_mem_stats), FN("deviceLimits", js_device_limits), FN("setW4Path", js_set_w4_path), FN("h2d", js_h2d),
       FN("d2h", js_d2h), FN("d2d", js_d2d), FN("profileEnable", js_profile_enable),
       FN("profileReset", js_profile_reset), FN("profileReport", js_profile_report),
       FN("timerStart", js_timer_start), FN("timerStop", js_timer_stop), FN("attention", js_attention),

@@ -11,12 +11,18 @@
 //                     [--text-encoder N]  (also time Qwen3.encode of N tokens on a 28-layer synthetic
 //                      text encoder: causal GQA attention, bf16 linears)
 //                     [--vae]  (also time the VAE decode of this size's latent, bf16 and fp32 precision)
-//                     [--w4 packed|int8]  (W4 weights unpacked inside each GEMM, or converted to their
-//                      int8 grid once at load: bit-identical products)
+//                     [--w4 packed|in-gemm|int8]  (W4 weights kept packed: the large products unpack
+//                      them per call into a pooled int8 scratch grid (packed) or inside the GEMM main
+//                      loop (in-gemm); int8: converted to their int8 grid once at load.  Bit-identical
+//                      products.)
+//                     [--in-gemm-too]  (with packed W4: also time the step with the in-GEMM unpack,
+//                      reported as w4_in_gemm)
 //                     [--no-fuse-qkv]  (the self-attention K / V converted by the attention's own prep
 //                      kernel instead of in the QKV GEMM epilogue)
 //                     [--unpacked-too]  (with packed W4: also time the step after converting the W4
 //                      linears to their int8 grid in place, reported as w4_unpacked)
+//                     [--settle-ms 1500]  (after the warmup steps, steps until this much device time
+//                      has passed, before anything is timed)
 //                     [--graph [--rounds 3]]  (also the forward replayed from a HIP graph recorded
 //                      once, ForwardGraph: graph and eager blocks of --steps steps alternate,
 //                      medians; dit_step_ms stays the eager step, graph_step_ms the replay)
@@ -70,6 +76,7 @@ async function main() {
   // nibble unpack per GEMM; one byte per weight)
   const w4mode = arg("w4", "packed");
   const unpacked = w4mode === "int8" ? dit.unpackW4() : 0;
+  if (w4mode === "in-gemm") native.setW4Path(gpu.ctx, 1);
   if (arg("no-fuse-qkv", false)) dit.fuseQkv = false;
   const ctxs = [0, 1].map((b) => {
     const t = gpu.empty([Lk, 1024]);
@@ -129,6 +136,14 @@ async function main() {
   let v = null;
   for (let i = 0; i < warmup; i++) v = await step();
   await gpu.sync();
+  // settle: keep stepping until the device has run ~settleMs of steps, so that the timed steps
+  // see the sustained clocks rather than the ramp after load
+  const settleMs = Number(arg("settle-ms", 1500));
+  for (let t = 0; t < settleMs; ) {
+    gpu.timerStart();
+    v = await step();
+    t += gpu.timerStop();
+  }
   if (gpu.profiler) gpu.profiler.reset();
   // each step timed on its own (HIP events on the library stream around the whole step)
   const timed = async (eager) => {
@@ -230,6 +245,16 @@ async function main() {
       const ms = ts.sort((a, b) => a - b)[1];
       out.vae[prec] = { ms: Number(ms.toFixed(2)), "TFLOP/s": Number((vaeFlops(h, w) / ms / 1e9).toFixed(1)) };
     }
+  }
+  if (arg("in-gemm-too", false) && w4mode === "packed" && mode === "w4a8") {
+    // the same packed weights with the nibbles unpacked inside every GEMM's main loop (eager
+    // steps; bit-identical velocities)
+    native.setW4Path(gpu.ctx, 1);
+    for (let i = 0; i < warmup; i++) await step(true);
+    await gpu.sync();
+    const xs = await timed(true);
+    out.w4_in_gemm = { step_ms: Number(median(xs).toFixed(3)) };
+    native.setW4Path(gpu.ctx, 0);
   }
   if (arg("unpacked-too", false) && w4mode === "packed" && mode === "w4a8") {
     // the same step once the W4 linears are converted to their int8 grid in place (after the

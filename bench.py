@@ -87,7 +87,8 @@ def dit_step(args):
 
     js = os.path.join(ROOT, "anima-studio_amd", "js", "bench_dit.mjs")
     r = subprocess.run(["node", js, "--steps", str(args.dit_steps), "--warmup", "3", "--graph", "--generate", "8",
-                        "--sampler", "euler_a", "--cfg", "4", "--text-encoder", "512", "--vae", "--unpacked-too"],
+                        "--sampler", "euler_a", "--cfg", "4", "--text-encoder", "512", "--vae", "--in-gemm-too",
+                        "--unpacked-too"],
                        cwd=ROOT,
                        capture_output=True, text=True, timeout=600)
     if r.returncode != 0:
@@ -105,6 +106,9 @@ def dit_step(args):
             # the same eager step with the W4 linears converted to their int8 grid at load
             # (anima_weight_unpack_w4; bit-identical velocities, 2x the W4 weight bytes)
             "w4_unpacked_ms": (d.get("w4_unpacked") or {}).get("step_ms"),
+            # the same eager step with the W4 nibbles unpacked inside every GEMM's main loop
+            # (anima_set_w4_path(ANIMA_W4_IN_GEMM)) instead of into a per-call int8 scratch grid
+            "w4_in_gemm_ms": (d.get("w4_in_gemm") or {}).get("step_ms"),
             "config": "Anima DiT 28 blocks, 1024x1024 (4096 tokens), B=2 CFG, hidden 2048, 16x128 heads, MLP 8192, "
                       "self + cross attention to 512x1024 contexts, W4A8 mixed (blocks 0/27 int8), seeded random weights; "
                       "step = timeCond + forward through node bench_dit.mjs",
@@ -315,14 +319,17 @@ LINEAR_SHAPES = (("qkv", 6144, 2048, "store"), ("out", 2048, 2048, "gated"), ("m
 def linears(m, ctx, reps):
     """The DiT block's quantized linears at M = B*N = 8192 tokens (int8 and W4 weights, per-token
     int8 activations, the block's epilogues): kernel time from HIP events around each launch,
-    summed over the launch's kernels.  W4 codes are unpacked inside the GEMM; their s_rel bytes
-    span 63 fp8 values (0.125 .. 448), so the group tables are read from all over the table."""
+    summed over the launch's kernels.  W4 ("w4") is the default path: the codes are unpacked per
+    call into a pooled int8 scratch grid that the int8 GEMM reads; "w4_in_gemm" unpacks them inside
+    the GEMM main loop.  The s_rel bytes span 63 fp8 values (0.125 .. 448), so the group tables are
+    read from all over the table."""
     import numpy as np
 
     M = 8192
     rng = np.random.default_rng(7)
     res = {}
-    for kind in ("i8", "w4"):
+    for kind in ("i8", "w4", "w4_in_gemm"):
+        ctx.set_w4_path(m.W4_IN_GEMM if kind == "w4_in_gemm" else m.W4_GRID_SCRATCH)
         for name, N, K, epi in LINEAR_SHAPES:
             bufs = [ctx.upload(rng.integers(-127, 128, size=(M, K), dtype=np.int8)),
                     ctx.upload(rng.uniform(0.001, 0.01, M).astype(np.float32)),
@@ -354,9 +361,11 @@ def linears(m, ctx, reps):
             ms = sum(r["ms"] for r in rep) / reps
             ops = 2.0 * M * N * K
             res[f"{kind}.{name}"] = {"M": M, "N": N, "K": K, "epilogue": epi, "ms": round(ms, 4),
-                                     "TOPS": round(ops / ms / 1e9, 1), "frac_int8_peak": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4)}
+                                     "TOPS": round(ops / ms / 1e9, 1), "frac_int8_peak": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4),
+                                     "kernels": {r["name"]: round(r["ms"] / r["count"], 4) for r in rep}}
             for b in bufs:
                 b.release()
+    ctx.set_w4_path(m.W4_GRID_SCRATCH)
     res.update(qkv_operands(m, ctx, rng, M, reps))
     return res
 
@@ -373,7 +382,8 @@ def qkv_operands(m, ctx, rng, M, reps):
     kn = ctx.upload((1 + 0.02 * rng.standard_normal(128)).astype(np.float32))
     cs = ctx.upload(m.dit_rope_table(64, 64))
     nbytes = m.Context.attention_kv_bytes(B, H, L, m.PREC_BF16)
-    for kind in ("i8", "w4"):
+    for kind in ("i8", "w4", "w4_in_gemm"):
+        ctx.set_w4_path(m.W4_IN_GEMM if kind == "w4_in_gemm" else m.W4_GRID_SCRATCH)
         bufs = [ctx.upload(rng.integers(-127, 128, size=(M, K), dtype=np.int8)),
                 ctx.upload(rng.uniform(0.001, 0.01, M).astype(np.float32)),
                 ctx.upload(rng.uniform(0.001, 0.01, N).astype(np.float32))]
@@ -411,6 +421,7 @@ def qkv_operands(m, ctx, rng, M, reps):
                 "kernels": {r["name"]: round(r["ms"] / r["count"], 4) for r in rep}}
         for b in bufs:
             b.release()
+    ctx.set_w4_path(m.W4_GRID_SCRATCH)
     kn.release()
     cs.release()
     return res

@@ -439,6 +439,19 @@ int anima_linear_qkv(anima_ctx* ctx, const anima_linear_desc* desc, const anima_
  * grid: [N][K] int8, 16-byte aligned; K % 32 == 0. */
 int anima_weight_unpack_w4(anima_ctx* ctx, const anima_weight* w4, int8_t* grid);
 
+/* Where anima_linear / anima_linear_qkv turn a W4 weight's nibbles into int8 grid values on the
+ * persistent 256 x 256 GEMM (products with at least one 256 x 256 tile per compute unit; smaller
+ * products always unpack inside their GEMM).  No counterpart in the reference, whose W4 B-loader
+ * decodes inside the matmul (gemm.js:141-158); both paths give bit-identical results.
+ *   ANIMA_W4_GRID_SCRATCH (default): one pass writes the weight's int8 grid (anima_weight_unpack_w4
+ *     semantics) into a pooled scratch buffer of N * K bytes, released after the call; the int8
+ *     GEMM reads it.  The weight stays packed in memory; the nibble work runs once per call
+ *     instead of once per row tile.
+ *   ANIMA_W4_IN_GEMM: every workgroup unpacks its B tiles inside the GEMM main loop (no scratch). */
+#define ANIMA_W4_GRID_SCRATCH 0
+#define ANIMA_W4_IN_GEMM 1
+int anima_set_w4_path(anima_ctx* ctx, int path);
+
 /* G independent small-M bf16-weight products in one launch, for the adaLN modulation linears of
  * timeCond (app/models/dit.js:196-225 runs one per block and kind, all on the same sigma):
  *   out[g*out_gstride + m*ldc + n] = sum_k x[g*x_gstride + m*ldx + k] * w[g*w_gstride + n*K + k]

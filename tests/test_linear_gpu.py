@@ -255,15 +255,26 @@ def test_out_projection_gated_epilogue(ctx, kind):
     assert np.array_equal(dout.numpy(), orc.linear_epilogue(orc.gemm_i8(qx, grid), sx, sw, bias=bias, epi=1, c=resid))
 
 
-@pytest.mark.parametrize("kind", ["i8", "w4"])
-def test_256_tile_kernel_ragged_edges(ctx, kind):
+@pytest.fixture
+def w4_path(ctx):
+    """Sets the context's W4 path for one test (default afterwards)."""
+    def set_path(name):
+        m = amd()
+        ctx.set_w4_path(m.W4_IN_GEMM if name == "in_gemm" else m.W4_GRID_SCRATCH)
+    yield set_path
+    ctx.set_w4_path(amd().W4_GRID_SCRATCH)
+
+
+@pytest.mark.parametrize("kind,path", [("i8", "-"), ("w4", "scratch"), ("w4", "in_gemm")])
+def test_256_tile_kernel_ragged_edges(ctx, w4_path, kind, path):
     """M=4500, N=4100: 18 x 17 tiles of 256 (the 256x256 persistent kernel), partial last row
     and column tiles (rows / columns past the edge read as zero through the buffer bounds; W4
     rows past N decode to zero), and a last group of 2 row tiles in the kernel's tile order
     (groups of 4); gated residual + bias epilogue and the int32 accumulators bit-exact on
     sampled rows, including the last ones, and the accumulator checksums over the whole
-    product."""
-    case(f"256x256-tile kernel M=4500 N=4100 K=1024 gated + bias {kind}")
+    product.  W4 both ways: unpacked into the scratch grid and inside the GEMM."""
+    case(f"256x256-tile kernel M=4500 N=4100 K=1024 gated + bias {kind} {path}")
+    w4_path(path)
     m = amd()
     M, K, N = 4500, 1024, 4100
     x = orc.randn(91, M * K).reshape(M, K)
@@ -292,14 +303,17 @@ def test_256_tile_kernel_ragged_edges(ctx, kind):
     assert np.array_equal(got[rows], ref), report("gated", got[rows], ref)
 
 
-@pytest.mark.parametrize("K", [64, 192, 1024])
-def test_256_tile_kernel_w4_every_srel(ctx, K):
-    """W4 unpacked inside the 256x256 kernel over all 256 s_rel bytes (fp8 e4m3 0 .. 480, so the
-    grid clamps at +-127) with a non-uniform codebook reaching +-2 (a fitted one, quant.py:116-124),
-    at M = N = 4096 (one tile per CU).  K = 64 ends a tile at every stage, K = 192 alternates the
-    stage parity across tiles, K = 1024 runs long tiles.  int32 accumulators: checksums over the
-    whole product and exact sampled rows; the store epilogue bit-exact."""
-    case(f"256x256-tile kernel W4 every s_rel M=N=4096 K={K}")
+@pytest.mark.parametrize("K,path", [(64, "in_gemm"), (192, "in_gemm"), (1024, "in_gemm"), (64, "scratch"),
+                                    (1024, "scratch")])
+def test_256_tile_kernel_w4_every_srel(ctx, w4_path, K, path):
+    """W4 on the 256x256 kernel over all 256 s_rel bytes (fp8 e4m3 0 .. 480, so the grid clamps at
+    +-127) with a non-uniform codebook reaching +-2 (a fitted one, quant.py:116-124), at
+    M = N = 4096 (one tile per CU), unpacked inside the GEMM (K = 64 ends a tile at every stage,
+    K = 192 alternates the stage parity across tiles, K = 1024 runs long tiles) and into the
+    scratch grid.  int32 accumulators: checksums over the whole product and exact sampled rows;
+    the store epilogue bit-exact."""
+    case(f"256x256-tile kernel W4 every s_rel M=N=4096 K={K} {path}")
+    w4_path(path)
     m = amd()
     M = N = 4096
     rng = np.random.default_rng(K)
@@ -613,6 +627,9 @@ def test_linear_rejects_bad_arguments(ctx):
     W = m.weight(m.W_I8, 64, 128, buf, scale=buf)
     with pytest.raises(m.AnimaError):
         ctx.linear(W, 4, buf, xq=buf, xs=buf, epilogue=m.EPI_GATED)  # no gate
+    with pytest.raises(m.AnimaError) as e:
+        ctx.set_w4_path(2)  # neither ANIMA_W4_GRID_SCRATCH nor ANIMA_W4_IN_GEMM
+    assert e.value.code == -1
 
 
 @pytest.mark.parametrize("K", [64, 2048])

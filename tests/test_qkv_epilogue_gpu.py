@@ -50,12 +50,26 @@ def make_weight(ctx, m, kind, seed, N, K, bias):
 
 
 @pytest.mark.parametrize("kind,B,Hp,Wp,H,K,bias", [("i8", 2, 16, 16, 2, 512, False), ("w4", 3, 8, 24, 4, 1024, True),
-                                                   ("i8", 2, 64, 64, 16, 2048, True), ("w4", 2, 64, 64, 16, 2048, False)])
+                                                   ("w4_in_gemm", 3, 8, 24, 4, 1024, True),
+                                                   ("i8", 2, 64, 64, 16, 2048, True), ("w4", 2, 64, 64, 16, 2048, False),
+                                                   ("w4_in_gemm", 2, 64, 64, 16, 2048, False)])
 def test_linear_qkv_operands_bit_exact(ctx, kind, B, Hp, Wp, H, K, bias):
+    """W4 runs both ways: unpacked per call into the int8 scratch grid ("w4", the default) and
+    inside the GEMM main loop ("w4_in_gemm")."""
     L = Hp * Wp
     M, N = B * L, 3 * H * HD
     case(f"linear_qkv {kind} B={B} L={L} H={H} K={K} bias={bias}")
     m = amd()
+    ctx.set_w4_path(m.W4_IN_GEMM if kind == "w4_in_gemm" else m.W4_GRID_SCRATCH)
+    try:
+        run_linear_qkv_case(ctx, m, kind.split("_")[0], B, Hp, Wp, H, K, bias)
+    finally:
+        ctx.set_w4_path(m.W4_GRID_SCRATCH)
+
+
+def run_linear_qkv_case(ctx, m, kind, B, Hp, Wp, H, K, bias):
+    L = Hp * Wp
+    M, N = B * L, 3 * H * HD
     W, wbufs = make_weight(ctx, m, kind, 300 + K + H, N, K, bias)
     rng = np.random.default_rng(400 + L)
     xq = ctx.upload(rng.integers(-127, 128, size=(M, K), dtype=np.int8))
