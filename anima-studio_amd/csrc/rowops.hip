@@ -595,16 +595,23 @@ template <int LR>
 __global__ __launch_bounds__(256) void layernorm_mod_reg_kernel(const float* X, const float* MOD, int64_t shift_off,
                                                                 int64_t scale_off, int64_t rows, float eps, int rotate,
                                                                 float* Y, int8_t* Q, float* S_out) {
-  // The modulated row crosses LDS in two halves of COLS / 2 columns through one half-row buffer
-  // (4 floats of padding per 64): 34 KiB per workgroup instead of 68, so four workgroups (four
-  // waves per SIMD) fit on a CU instead of two.
+  // The modulated row crosses LDS in two halves of COLS / 2 columns through one half-row buffer:
+  // 34-38 KiB per workgroup instead of 68-76, so four workgroups (four waves per SIMD) fit on a CU
+  // instead of two.  A 16-byte LDS access is served eight lanes at a time over 32 banks, so the
+  // 16-byte slots of any eight consecutive lanes must differ modulo 8.  LR = 32: the writers
+  // (lane x, slot 2x + q of a 256-column block) and the readers (lane lh, slots 16 lh + q') both
+  // meet that with 4 floats of padding after every 32 columns and 4 more after every 64 (slot n
+  // at n + n/8 + n/16); LR = 16 keeps 4 floats per 64.
   constexpr int COLS = 64 * LR, VT = 256 / LR, NB = COLS / 256, RPW = 256 / LR, HB = NB / 2;
-  constexpr int RS = COLS / 2 + 2 * LR;  // half-row stride in floats
+  constexpr int RS = LR == 32 ? COLS / 2 + COLS / 16 + COLS / 32 : COLS / 2 + 2 * LR;  // half-row stride in floats
   __shared__ __attribute__((aligned(16))) float SH[RPW * RS];
   const int l = threadIdx.x % LR, rl = threadIdx.x / LR;
   const int64_t row = (int64_t)blockIdx.x * RPW + rl;
   if (row >= rows) return;  // (a row's lanes leave together; nothing below spans rows)
   const float* x = X + row * COLS + VT * l;
+  // padded LDS offsets of this lane's writes (column 256 i' + VT l + 4 q of the half: wb + the
+  // compile-time 304 i' + 4 q for LR = 32, whose q < 2) and reads (columns 64 lh + 4 q)
+  const int wb = LR == 32 ? 8 * l + 4 * (l >> 2) + 4 * (l >> 3) : VT * l + 4 * ((VT * l) >> 6);
   float v[64];  // v[VT i + j] = x[256 i + VT l + j]
 #pragma unroll
   for (int i = 0; i < NB; i++)
@@ -647,11 +654,11 @@ __global__ __launch_bounds__(256) void layernorm_mod_reg_kernel(const float* X, 
     for (int i = hh * HB; i < (hh + 1) * HB; i++)
 #pragma unroll
       for (int q = 0; q < VT / 4; q++) {
-        const int c = 256 * i + VT * l + 4 * q, ch = c - hh * (COLS / 2);
+        const int c = 256 * i + VT * l + 4 * q, ih = i - hh * HB;
         const float4 sc = *(const float4*)(MOD + scale_off + c);
         const float4 sh = *(const float4*)(MOD + shift_off + c);
         const float* t = v + VT * i + 4 * q;
-        *(float4*)(S + ch + 4 * (ch >> 6)) =
+        *(float4*)(S + wb + (LR == 32 ? 304 * ih : (256 + 16) * ih) + 4 * q) =
             make_float4((t[0] - mean) * r * (1.0f + sc.x) + sh.x, (t[1] - mean) * r * (1.0f + sc.y) + sh.y,
                         (t[2] - mean) * r * (1.0f + sc.z) + sh.z, (t[3] - mean) * r * (1.0f + sc.w) + sh.w);
       }
@@ -660,7 +667,7 @@ __global__ __launch_bounds__(256) void layernorm_mod_reg_kernel(const float* X, 
       const int lh = l - hh * (LR / 2);
 #pragma unroll
       for (int q = 0; q < 16; q++) {
-        const float4 t = *(const float4*)(S + 68 * lh + 4 * q);
+        const float4 t = *(const float4*)(S + (LR == 32 ? 76 * lh + 4 * q + 4 * (q >> 3) : 68 * lh + 4 * q));
         w[4 * q] = t.x;
         w[4 * q + 1] = t.y;
         w[4 * q + 2] = t.z;
