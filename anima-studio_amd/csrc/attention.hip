@@ -53,6 +53,7 @@ struct PrepArgs {
   int64_t sin_off;
   float eps;
   int Hkv, Lk, Lkp;
+  int D;  // the caller's head dim, 128 or 64 (dims D..127 of the operands are zero)
 };
 
 template <typename T>
@@ -80,8 +81,10 @@ __global__ __launch_bounds__(256) void attn_prep_kv(PrepArgs a) {
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const int l = kb0 + 4 * tg + j;
-    const float* src = a.v + (int64_t)b * a.v_bs + (int64_t)min(l, a.Lk - 1) * a.ldv + hk * HD + 8 * g;
-    const float4 lo = *(const float4*)src, hi = *(const float4*)(src + 4);
+    const float* src = a.v + (int64_t)b * a.v_bs + (int64_t)min(l, a.Lk - 1) * a.ldv + hk * a.D + 8 * g;
+    const bool in = 8 * g < a.D;  // D = 64: dim groups 8..15 are padding
+    const float4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float4 lo = in ? *(const float4*)src : z, hi = in ? *(const float4*)(src + 4) : z;
     e[j][0] = lo.x; e[j][1] = lo.y; e[j][2] = lo.z; e[j][3] = lo.w;
     e[j][4] = hi.x; e[j][5] = hi.y; e[j][6] = hi.z; e[j][7] = hi.w;
   }
@@ -93,11 +96,12 @@ __global__ __launch_bounds__(256) void attn_prep_kv(PrepArgs a) {
     const int r = t >> 2, p = t & 3, l = kb0 + r;
     float x[32], w[32], cv[16], sv[16];
     {
-      const float* src = a.k + (int64_t)b * a.k_bs + (int64_t)min(l, a.Lk - 1) * a.ldk + hk * HD;
+      const float* src = a.k + (int64_t)b * a.k_bs + (int64_t)min(l, a.Lk - 1) * a.ldk + hk * a.D;
+      const bool hi = a.D == HD;  // D = 64: dims 64..127 are padding
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         *(float4*)(x + 4 * j) = *(const float4*)(src + 16 * p + 4 * j);
-        *(float4*)(x + 16 + 4 * j) = *(const float4*)(src + 64 + 16 * p + 4 * j);
+        *(float4*)(x + 16 + 4 * j) = hi ? *(const float4*)(src + 64 + 16 * p + 4 * j) : (float4){0.0f, 0.0f, 0.0f, 0.0f};
       }
     }
     if (NORM) {
@@ -232,9 +236,9 @@ __global__ __launch_bounds__(256) void attn_prep_kv_lines(PrepArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int l = min(kb0 + 16 * w + 4 * i + rsub, a.Lk - 1);
-    const float* src = a.k + (int64_t)b * a.k_bs + (int64_t)l * a.ldk + hk * HD + 4 * q16;
+    const float* src = a.k + (int64_t)b * a.k_bs + (int64_t)l * a.ldk + hk * a.D + 4 * q16;
     klo[i] = *(const float4*)src;
-    khi[i] = *(const float4*)(src + 64);
+    khi[i] = a.D == HD ? *(const float4*)(src + 64) : (float4){0.0f, 0.0f, 0.0f, 0.0f};  // D = 64: padding
     if (ROPE) {
       const float* cr = a.cs + (int64_t)l * (HD / 2) + 4 * q16;
       cv[i] = *(const float4*)cr;
@@ -250,7 +254,8 @@ __global__ __launch_bounds__(256) void attn_prep_kv_lines(PrepArgs a) {
 #pragma unroll
   for (int e = 0; e < 8; e++) {
     const int key = kb0 + 16 * (vc >> 1) + 4 * (vc & 1) + (e & 3) + 8 * (e >> 2);
-    ve[e] = *(const float4*)(a.v + (int64_t)b * a.v_bs + (int64_t)min(key, a.Lk - 1) * a.ldv + hk * HD + 32 * w + 4 * vq);
+    ve[e] = 32 * w < a.D ? *(const float4*)(a.v + (int64_t)b * a.v_bs + (int64_t)min(key, a.Lk - 1) * a.ldv + hk * a.D + 32 * w + 4 * vq)
+                         : (float4){0.0f, 0.0f, 0.0f, 0.0f};  // D = 64: waves 2, 3 write the zero dims
   }
   __builtin_amdgcn_sched_barrier(0);
   // ---- K rows
@@ -324,6 +329,7 @@ struct FlashArgs {
   int H, group, Hkv, Lq, Lkp, n_qt;
   int kv_len[MAXB];
   int causal;  // keys > query index masked (the 4-wave and fp32 kernels)
+  int D;       // the caller's head dim, 128 or 64 (the operands are zero-padded to 128)
 };
 
 // Loads this lane's 64 Q values (query qi, dims 16ks + 8hf + j), applies the fused
@@ -331,11 +337,13 @@ struct FlashArgs {
 template <bool NORM, bool ROPE>
 __device__ __forceinline__ void load_q(const FlashArgs& a, int b, int h, int qi, int hf, float* x) {
   if (qi < a.Lq) {
-    const float* src = a.q + (int64_t)b * a.q_bs + (int64_t)qi * a.ldq + h * HD + 8 * hf;
+    const float* src = a.q + (int64_t)b * a.q_bs + (int64_t)qi * a.ldq + h * a.D + 8 * hf;
+    const float4 z = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int ks = 0; ks < 8; ks++) {
-      float4 lo = *(const float4*)(src + 16 * ks);
-      float4 hi = *(const float4*)(src + 16 * ks + 4);
+      const bool in = 16 * ks < a.D;  // D = 64: k-steps 4..7 are padding
+      float4 lo = in ? *(const float4*)(src + 16 * ks) : z;
+      float4 hi = in ? *(const float4*)(src + 16 * ks + 4) : z;
       x[8 * ks] = lo.x; x[8 * ks + 1] = lo.y; x[8 * ks + 2] = lo.z; x[8 * ks + 3] = lo.w;
       x[8 * ks + 4] = hi.x; x[8 * ks + 5] = hi.y; x[8 * ks + 6] = hi.z; x[8 * ks + 7] = hi.w;
     }
@@ -741,13 +749,14 @@ __global__ __launch_bounds__(256, KB == 32 ? 3 : 2) void attn_flash_bf16(FlashAr
   l = pair_sum(l);
   if (qi < a.Lq) {
     const float inv = 1.0f / l;
-    float* dst = a.o + (int64_t)b * a.o_bs + (int64_t)qi * a.ldo + h * HD + 4 * hf;
+    float* dst = a.o + (int64_t)b * a.o_bs + (int64_t)qi * a.ldo + h * a.D + 4 * hf;
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
+      if (32 * dt < a.D)  // D = 64: dim tiles 2, 3 are padding
 #pragma unroll
-      for (int g = 0; g < 4; g++)
-        *(float4*)(dst + 32 * dt + 8 * g) =
-            make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+        for (int g = 0; g < 4; g++)
+          *(float4*)(dst + 32 * dt + 8 * g) =
+              make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
   }
 }
 constexpr int FLASH_KB = 64;  // keys per block of the bf16 kernel
@@ -1059,13 +1068,14 @@ __global__ __launch_bounds__(256) void attn_flash_fp32(FlashArgs a) {
   l += __shfl_xor(l, 32);
   if (qi < a.Lq) {
     const float inv = 1.0f / l;
-    float* dst = a.o + (int64_t)b * a.o_bs + (int64_t)qi * a.ldo + h * HD + 4 * hf;
+    float* dst = a.o + (int64_t)b * a.o_bs + (int64_t)qi * a.ldo + h * a.D + 4 * hf;
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
+      if (32 * dt < a.D)  // D = 64: dim tiles 2, 3 are padding
 #pragma unroll
-      for (int g = 0; g < 4; g++)
-        *(float4*)(dst + 32 * dt + 8 * g) =
-            make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+        for (int g = 0; g < 4; g++)
+          *(float4*)(dst + 32 * dt + 8 * g) =
+              make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
   }
 }
 
@@ -1076,7 +1086,10 @@ static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // Argument checks of anima_attention (fills kv_len[] with the valid key counts).
 static int attention_check(anima_ctx* c, const anima_attn_desc* d, int (&kv_len)[MAXB]) {
   const int group = d->group <= 0 ? 1 : d->group;
-  if (d->D != HD) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: head dim %d on the flash kernels (D=128 only)", d->D);
+  if (d->D != HD && d->D != HD / 2)
+    return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: head dim %d on the flash kernels (D = 128 or 64)", d->D);
+  if (d->D != HD && (d->q_norm || d->k_norm || d->rope_cs || d->kv_prep))
+    return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: fused q/k norm, RoPE and prepared K/V need D = 128 (D = %d)", d->D);
   if (d->B < 1 || d->B > MAXB) return fail(c, ANIMA_E_ARG, "anima_attention: B=%d outside [1,%d]", d->B, MAXB);
   if (d->Lq < 1 || d->Lk < 1 || d->H < 1) return fail(c, ANIMA_E_ARG, "anima_attention: Lq=%d Lk=%d H=%d must be >= 1", d->Lq, d->Lk, d->H);
   if (d->Lk > (1 << 22)) return fail(c, ANIMA_E_ARG, "anima_attention: Lk=%d (at most %d keys)", d->Lk, 1 << 22);
@@ -1095,9 +1108,9 @@ static int attention_check(anima_ctx* c, const anima_attn_desc* d, int (&kv_len)
     if (lds[i] % 4 || offs[i] % 4 || bss[i] % 4 || lds[i] < 0 || offs[i] < 0 || bss[i] < 0)
       return fail(c, ANIMA_E_ARG, "anima_attention: %s ld/off/bstride (%lld/%lld/%lld) must be non-negative multiples of 4 (vec4 rows, as ops.js:169)",
                   nm[i], (long long)lds[i], (long long)offs[i], (long long)bss[i]);
-    if (lds[i] < offs[i] + (int64_t)heads[i] * HD)
+    if (lds[i] < offs[i] + (int64_t)heads[i] * d->D)
       return fail(c, ANIMA_E_ARG, "anima_attention: %s rows of %lld elements cannot hold off %lld + %d heads x %d", nm[i],
-                  (long long)lds[i], (long long)offs[i], heads[i], HD);
+                  (long long)lds[i], (long long)offs[i], heads[i], d->D);
   }
   if (!al16(d->q) || !al16(d->o) || (!prepared && (!al16(d->k) || !al16(d->v))) || (prepared && !al16(d->kv_prep)))
     return fail(c, ANIMA_E_ARG, "anima_attention: q/k/v/o (or kv_prep) must be 16-byte aligned");
@@ -1148,8 +1161,9 @@ static int prep_kv_launch(anima_ctx* c, const anima_attn_desc* d, void* dst) {
   p.Hkv = Hkv;
   p.Lk = d->Lk;
   p.Lkp = Lkp;
+  p.D = d->D;
   {
-    const double bytes = (double)d->B * Hkv * d->Lk * HD * 4 * 2 + 2.0 * plane;
+    const double bytes = (double)d->B * Hkv * d->Lk * d->D * 4 * 2 + 2.0 * plane;
     Launch L(c, bf ? "attn.prep_kv_bf16" : "attn.prep_kv_fp32", 0.0, bytes);
     dim3 grid(Hkv, Lkp / BK, d->B);  // heads fastest: concurrent workgroups read whole K / V rows
     const bool kn = d->k_norm != nullptr;
@@ -1179,8 +1193,12 @@ int attention_launch(anima_ctx* c, const anima_attn_desc* d) { return attention_
 // scratch != nullptr: the K/V prep goes there (the caller checked its size) instead of the
 // context's workspace.
 int attention_launch_ws(anima_ctx* c, const anima_attn_desc* d, void* scratch) {
-  if (d->D != HD) {  // the chunked path (app/gpu/ops.js:177-207), e.g. the adapter's D = 64
-    if (scratch) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention_noalloc: head dim %d", d->D);
+  if (scratch && d->D != HD) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention_noalloc: head dim %d", d->D);
+  // D = 64 without fused norm / RoPE / prepared K/V (the LLM adapter's heads, dit.js:147-160):
+  // the flash kernels with the operands zero-padded to 128 dims (flashAttentionShader(64) of
+  // ops.js:170); any other head dim: the chunked path (app/gpu/ops.js:177-207)
+  const bool flash64 = d->D == HD / 2 && !d->q_norm && !d->k_norm && !d->rope_cs && !d->kv_prep;
+  if (d->D != HD && !flash64) {
     int rc = attention_chunked_check(c, d);
     if (rc) return rc;
     int kvl[MAXB];
@@ -1196,7 +1214,7 @@ int attention_launch_ws(anima_ctx* c, const anima_attn_desc* d, void* scratch) {
   if (rc) return rc;
   const int group = d->group <= 0 ? 1 : d->group;
   const bool rope = d->rope_cs != nullptr;
-  const float scale = d->scale != 0.0f ? d->scale : 1.0f / sqrtf((float)HD);
+  const float scale = d->scale != 0.0f ? d->scale : 1.0f / sqrtf((float)d->D);
   const float eps = d->eps;
   const int Hkv = d->H / group;
   const int Lkp = (d->Lk + BK - 1) / BK * BK;
@@ -1230,12 +1248,13 @@ int attention_launch_ws(anima_ctx* c, const anima_attn_desc* d, void* scratch) {
   f.Lq = d->Lq;
   f.Lkp = Lkp;
   // 8-wave workgroups (256 queries) when that grid still gives every CU a workgroup
-  const bool w8 = bf && !d->causal && (int64_t)((d->Lq + W8_BQ - 1) / W8_BQ) * d->H * d->B >= c->num_cus;
+  const bool w8 = bf && !d->causal && d->D == HD && (int64_t)((d->Lq + W8_BQ - 1) / W8_BQ) * d->H * d->B >= c->num_cus;
   f.n_qt = w8 ? (d->Lq + W8_BQ - 1) / W8_BQ : (d->Lq + BQ - 1) / BQ;
   for (int b = 0; b < MAXB; b++) f.kv_len[b] = b < d->B ? kv_len[b] : 1;
   f.causal = d->causal ? 1 : 0;
+  f.D = d->D;
   double flops = 0;
-  for (int b = 0; b < d->B; b++) flops += 4.0 * d->Lq * (double)kv_len[b] * HD * d->H;
+  for (int b = 0; b < d->B; b++) flops += 4.0 * d->Lq * (double)kv_len[b] * d->D * d->H;
   const int blocks = f.n_qt * d->H * d->B;
   Launch L(c, w8 ? "attn.flash_bf16" : bf ? "attn.flash_bf16_4w" : "attn.flash_fp32", flops, 0.0);
   const bool qn = d->q_norm != nullptr;
@@ -1328,6 +1347,7 @@ int attention_prepare_kv_launch(anima_ctx* c, const anima_attn_desc* d, void* ds
   if (d->kv_prep) return fail(c, ANIMA_E_ARG, "anima_attention_prepare_kv: desc->kv_prep must be NULL");
   if (!al16(dst)) return fail(c, ANIMA_E_ARG, "anima_attention_prepare_kv: kv_prep must be 16-byte aligned");
   const int group = d->group <= 0 ? 1 : d->group;
+  if (d->D != HD) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention_prepare_kv: head dim %d (prepared K/V need D = 128)", d->D);
   if (d->kv_prep_bytes != attention_kv_bytes(d->B, d->H / group, d->Lk, d->precision))
     return fail(c, ANIMA_E_ARG, "anima_attention_prepare_kv: kv_prep_bytes=%lld, the layout takes %lld",
                 (long long)d->kv_prep_bytes, (long long)attention_kv_bytes(d->B, d->H / group, d->Lk, d->precision));

@@ -137,9 +137,11 @@ int anima_graph_destroy(anima_ctx* ctx, anima_graph* graph);
 #define ANIMA_PREC_FP32 1 /* fp32 MFMA (tolerance variant) */
 
 typedef struct {
-  int B, Lq, Lk, H, D; /* D == 128 (flash kernels); other D % 4 == 0 (the LLM adapter's 64, the VAE's
-                        * 384) on the chunked path of app/gpu/ops.js:177-207, causal mask included.
-                        * Fused norm / RoPE and prepared K/V need D == 128. */
+  int B, Lq, Lk, H, D; /* D == 128 and D == 64 (the LLM adapter's heads; operands zero-padded to 128
+                        * dims) on the flash kernels, as ops.js:170 sends D in {64, 128} to
+                        * flashAttentionShader; other D % 4 == 0 (the VAE's 384) on the chunked path of
+                        * app/gpu/ops.js:177-207, causal mask included.  Fused norm / RoPE and
+                        * prepared K/V need D == 128 (D == 64 with them takes the chunked path). */
   int group;           /* q heads per kv head (1 = MHA); 0 is read as 1 */
   const float* q;
   int64_t ldq, q_off, q_bstride;

@@ -291,8 +291,9 @@ def test_causal_gqa_attention(ctx, L, B, precision):
 @pytest.mark.parametrize("precision", ["bf16", "fp32"])
 def test_head_dim_64_attention(ctx, precision):
     """D = 64, the LLM adapter's attention (app/models/dit.js:147-160: 16 heads x 64 in 1024
-    columns; its cross-attention to the text encoder's tokens) on the chunked path at D = 64 (no
-    padding), scale 1/8, against the oracle (self Lq = Lk = 77 and cross Lq = 32, Lk = 100)."""
+    columns; its cross-attention to the text encoder's tokens) on the flash kernels with the
+    operands zero-padded to 128 dims (ops.js:170 sends D = 64 to flashAttentionShader), scale 1/8,
+    against the oracle (self Lq = Lk = 77 and cross Lq = 32, Lk = 100)."""
     case(f"attention D=64 {precision}")
     m = amd()
     H, D = 16, 64
@@ -310,6 +311,54 @@ def test_head_dim_64_attention(ctx, precision):
         ref = orc.attention("f64", q, k, v, **args)[0]
         r, mx = report(f"D=64 Lq={Lq} Lk={Lk} {precision} vs fp64", got, ref)
         assert r <= (1e-5 if precision == "fp32" else 1e-2)
+
+
+@pytest.mark.parametrize("precision", ["bf16", "fp32"])
+def test_head_dim_64_flash_path(ctx, precision):
+    """D = 64 runs the flash kernels (the profiler names the flash launch, no chunked-path kernel)
+    with the operands zero-padded to 128 dims: B = 2 with ragged valid key lengths, GQA (8 query
+    heads over 4 kv heads), causal and not, strided rows (the heads of a fused [q | k | v] row),
+    every query row against float64 restated on the host, and the padding columns of the output
+    rows (other heads' slices) left untouched."""
+    m = amd()
+    B, Lq, Lk, H, group, D = 2, 200, 333, 8, 2, 64
+    Hk = H // group
+    kv_len = [333, 90]
+    prec = m.PREC_FP32 if precision == "fp32" else m.PREC_BF16
+    rng = np.random.default_rng(640)
+    ld = (H + 2 * Hk) * D + 64  # q | k | v heads, then 64 spare columns
+    for causal in (0, 1):
+        case(f"attention D=64 flash path {precision} causal={causal}")
+        x = rng.standard_normal((B, max(Lq, Lk), ld)).astype(np.float32)
+        dx = ctx.upload(x)
+        o0 = np.full((B, Lq, H * D + 64), 7.0, np.float32)
+        do = ctx.upload(o0)
+        ctx.profile(True)
+        ctx.profile_reset()
+        ctx.attention(q=dx, k=dx, v=dx, o=do, B=B, Lq=Lq, Lk=Lk, H=H, D=D, group=group, ldq=ld, ldk=ld, ldv=ld,
+                      ldo=H * D + 64, k_off=H * D, v_off=(H + Hk) * D, q_bstride=max(Lq, Lk) * ld,
+                      k_bstride=max(Lq, Lk) * ld, v_bstride=max(Lq, Lk) * ld, o_bstride=Lq * (H * D + 64),
+                      kv_len=kv_len, precision=prec, causal=causal)
+        names = [r["name"] for r in ctx.profile_report()]
+        ctx.profile(False)
+        assert any(n.startswith("attn.flash") for n in names) and not any("chunk" in n for n in names), names
+        got = do.numpy()
+        for x_ in (dx, do):
+            x_.release()
+        assert np.all(got[:, :, H * D:] == 7.0)  # spare columns untouched
+        for b in range(B):
+            for h in range(H):
+                hk = h // group
+                q = x[b, :Lq, h * D:(h + 1) * D].astype(np.float64)
+                k = x[b, :kv_len[b], H * D + hk * D:H * D + (hk + 1) * D].astype(np.float64)
+                v = x[b, :kv_len[b], (H + Hk) * D + hk * D:(H + Hk) * D + (hk + 1) * D].astype(np.float64)
+                s = q @ k.T / 8.0
+                if causal:
+                    s = np.where(np.arange(kv_len[b])[None, :] <= np.arange(Lq)[:, None], s, -np.inf)
+                p = np.exp(s - s.max(-1, keepdims=True))
+                ref = (p @ v) / p.sum(-1, keepdims=True)
+                r, _ = report(f"D=64 flash b={b} h={h} causal={causal} {precision}", got[b, :, h * D:(h + 1) * D], ref)
+                assert r <= (1e-5 if precision == "fp32" else 1e-2)
 
 
 # ------------------------------------------------------------------ ragged shapes, GQA, strides

@@ -155,9 +155,10 @@ def _attn_rows_f64(q, k, v, rows, D, causal, n=None):
 @pytest.mark.parametrize("D", [64, 96])
 @pytest.mark.parametrize("precision", ["fp32", "bf16"])
 def test_chunked_attention_causal_gqa(D, precision):
-    """The causal mask on the chunked path (app/gpu/ops.js:196, kernels.js:49: limit =
-    min(cols, row + 1)), with GQA (4 query heads over 2 kv heads), B = 2 with a ragged valid key
-    length, and Lq != Lk: every query row against a float64 restatement."""
+    """The causal mask (app/gpu/ops.js:196, kernels.js:49: limit = min(cols, row + 1)) on the
+    chunked path (D = 96) and on the flash kernels with zero-padded operands (D = 64), with GQA (4
+    query heads over 2 kv heads), B = 2 with a ragged valid key length, and Lq != Lk: every query
+    row against a float64 restatement."""
     m = amd()
     B, Lq, Lk, H, group = 2, 150, 190, 4, 2
     Hk = H // group
