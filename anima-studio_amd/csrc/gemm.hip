@@ -48,8 +48,52 @@ struct GemmArgs {
   float eps;
   int L, Lkp, H;     // tokens per batch element (M = B * L, L % 64 == 0 so Lkp = L), heads
   int kcol, vcol;
+  // LoRA B product in the epilogue (gemm_i8_256<..., LORA>): y += sum_k lx[m][k] * B[n][k], k < lr,
+  // with B as three bf16 planes lb [3][N][lr] (the scales folded in); lr % 16 == 0
+  const float* lx = nullptr;
+  int64_t ld_lx = 0;
+  const uint16_t* lb = nullptr;
+  int lr = 0;
 };
 
+
+// three bf16 pieces of 8 fp32 values, two at a time (packed round-to-nearest-even conversions;
+// bf16 -> fp32 is exact, so each remainder is exact)
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split3_pair(f32x2_t v, bf16x2_t& h, bf16x2_t& m, bf16x2_t& l) {
+  h = __builtin_convertvector(v, bf16x2_t);
+  const f32x2_t r = v - __builtin_convertvector(h, f32x2_t);
+  m = __builtin_convertvector(r, bf16x2_t);
+  l = __builtin_convertvector(r - __builtin_convertvector(m, f32x2_t), bf16x2_t);
+}
+__device__ __forceinline__ void split3(float4 a, float4 b, bf16x8 (&o)[3]) {
+  bf16x2_t h0, m0, l0, h1, m1, l1, h2, m2, l2, h3, m3, l3;
+  split3_pair(f32x2_t{a.x, a.y}, h0, m0, l0);
+  split3_pair(f32x2_t{a.z, a.w}, h1, m1, l1);
+  split3_pair(f32x2_t{b.x, b.y}, h2, m2, l2);
+  split3_pair(f32x2_t{b.z, b.w}, h3, m3, l3);
+  o[0] = bf16x8{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+  o[1] = bf16x8{m0[0], m0[1], m1[0], m1[1], m2[0], m2[1], m3[0], m3[1]};
+  o[2] = bf16x8{l0[0], l0[1], l1[0], l1[1], l2[0], l2[1], l3[0], l3[1]};
+}
+
+// acc += sum_{i+j<=2} a_i b_j, smallest terms first
+__device__ __forceinline__ f32x16 mfma_s3(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f32x16 acc) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 ld_bf8(const uint16_t* p) {
+  const uint4 u = *(const uint4*)p;
+  bf16x8 r;
+  __builtin_memcpy(&r, &u, 16);
+  return r;
+}
 
 __device__ __forceinline__ float apply_act(float r, int act) {
   if (act == ANIMA_ACT_GELU) return gelu_erf(r);
@@ -267,6 +311,124 @@ __device__ __forceinline__ void epi_load_c(const GemmArgs& a, int m, int n, f32x
   }
 }
 
+// The plain epilogues with the LoRA B product (gemm_i8_256<..., LORA>), for the wave's 4 x 2
+// tiles of 32 x 32 in the C^T layout, in three phases: (1) every accumulator becomes its fp32
+// y = (acc * s_x) * s_w (* alpha) (+ bias) in place; (2) per 16-k slice of the rank, the slice's
+// operands of all eight tiles are loaded at once -- the B planes of the two column groups (A
+// operand: lane lq holds row n + lq) and the activations of the four row groups (B operand: lane
+// lq holds row m, split into three bf16 terms in registers) -- and six v_mfma_f32_32x32x16_bf16
+// per tile (mfma_s3) add sum_k lx[m][k] * B[n][k] onto y, so that one load latency per slice is
+// exposed, not one per tile; (3) activation and store / residual / gate as in epi_store_t.
+// Every lane takes part in the MFMAs (rows past M and columns past N read zeros).
+template <int EPI>
+__device__ __forceinline__ void lora_epilogue(const GemmArgs& a, const i32x16 (&acc)[4][2], int m0, int n0, int hf,
+                                              int lq, const float (&sxv)[4]) {
+  f32x16 y[4][2];
+  if (a.acc_out) {  // the raw accumulators first: acc is dead once y is formed
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int m = m0 + 32 * i, nq = n0 + 32 * j + 8 * q;
+          if (m < a.M && nq < a.N)
+#pragma unroll
+            for (int e = 0; e < 4; e++) a.acc_out[(int64_t)m * a.N + nq + e] = acc[i][j][4 * q + e];
+        }
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    EpiCols c;
+    epi_cols(a, n0 + 32 * j, c);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int nq = n0 + 32 * j + 8 * q;
+      const bool ok = nq < a.N;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float b = a.bias && ok ? a.bias[nq + e] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          float t = (float)acc[i][j][4 * q + e] * sxv[i];
+          t = t * c.sw[q][e];
+          if (a.alpha != 1.0f) t = t * a.alpha;
+          if (a.bias) t = t + b;
+          y[i][j][4 * q + e] = t;
+        }
+      }
+    }
+  }
+  const int64_t plane = (int64_t)a.N * a.lr;
+  const bf16x8 z8 = {};
+  const float4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k0 = 0; k0 < a.lr; k0 += 16) {
+    bf16x8 bv[2][3];
+    float4 xr[4][2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int nr = n0 - 4 * hf + 32 * j + lq;
+      const bool nok = nr < a.N;
+      const uint16_t* bp = a.lb + (int64_t)(nok ? nr : 0) * a.lr + 8 * hf + k0;
+#pragma unroll
+      for (int p = 0; p < 3; p++) bv[j][p] = nok ? ld_bf8(bp + p * plane) : z8;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int m = m0 + 32 * i;
+      const bool mok = m < a.M;
+      const float* xp = a.lx + (int64_t)(mok ? m : 0) * a.ld_lx + 8 * hf + k0;
+      xr[i][0] = mok ? *(const float4*)xp : z4;
+      xr[i][1] = mok ? *(const float4*)(xp + 4) : z4;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      bf16x8 xv[3];
+      split3(xr[i][0], xr[i][1], xv);
+#pragma unroll
+      for (int j = 0; j < 2; j++) y[i][j] = mfma_s3(bv[j], xv, y[i][j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      // one tile at a time: keeps the residual loads from being hoisted above the earlier tiles'
+      // stores (32 residual quads in flight would not fit beside the 128 registers of y)
+      __builtin_amdgcn_sched_barrier(0);
+      const int m = m0 + 32 * i;
+      if (m >= a.M) continue;
+      float* orow = a.out + (int64_t)m * a.ldc;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int nq = n0 + 32 * j + 8 * q;
+        if (nq >= a.N) continue;
+        f32x4 yq = {y[i][j][4 * q], y[i][j][4 * q + 1], y[i][j][4 * q + 2], y[i][j][4 * q + 3]};
+        if (a.act == ANIMA_ACT_GELU) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) yq[e] = gelu_erf(yq[e]);
+        } else if (a.act == ANIMA_ACT_SILU) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) yq[e] = silu_f(yq[e]);
+        }
+        f32x4 o;
+        if constexpr (EPI == ANIMA_EPI_STORE) {
+          o = yq;
+        } else {
+          const f32x4 cq = *(const f32x4*)(orow + nq);
+          if constexpr (EPI == ANIMA_EPI_RESID) {
+            o = cq + yq;
+          } else {
+            const f32x4 gt = *(const f32x4*)(a.gate + a.gate_off + nq);
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = __builtin_fmaf(gt[e], yq[e], cq[e]);
+          }
+        }
+        *(f32x4*)(orow + nq) = o;
+      }
+    }
+}
+
 template <int EPI>
 __device__ __forceinline__ void epi_store_t(const GemmArgs& a, const i32x16& v, int m, int n, float sx,
                                             const EpiCols& c, const f32x4 (&cv)[4]) {
@@ -481,9 +643,10 @@ __device__ __forceinline__ void g2_barrier() {
 
 constexpr int G2_LUT = G2_NST * G2_ST;  // W4 table offset in LDS (256 x 16 bytes)
 
-template <int EPI, bool W4, bool KV = false>
+template <int EPI, bool W4, bool KV = false, bool LORA = false>
 __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
   static_assert(!KV || EPI == ANIMA_EPI_STORE, "the attention operand epilogue stores");
+  static_assert(!(KV && LORA), "the LoRA term goes through the plain epilogues");
   __shared__ __attribute__((aligned(1024))) char smem[G2_NST * G2_ST + (W4 ? 4096 : 0) + (KV ? 4096 : 0)];
   // the wave index is uniform: in a scalar register, so copy offsets derived from it stay scalar
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -832,16 +995,20 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
 #define G2_C(buf, i, j) \
   if constexpr (EPI != ANIMA_EPI_STORE) epi_load_c(a, m0 + 32 * (i), n0 + 32 * (j), buf);
 #define G2_T(buf, i, j, cc) epi_store_t<EPI>(a, acc[i][j], m0 + 32 * (i), n0 + 32 * (j), sxv[i], cc, buf);
-      G2_C(cA, 0, 0)
-      G2_C(cB, 1, 0) G2_T(cA, 0, 0, cc)
-      G2_C(cA, 2, 0) G2_T(cB, 1, 0, cc)
-      G2_C(cB, 3, 0) G2_T(cA, 2, 0, cc)
-      G2_C(cA, 0, 1) G2_T(cB, 3, 0, cc)
-      epi_cols(a, n0 + 32, cc);
-      G2_C(cB, 1, 1) G2_T(cA, 0, 1, cc)
-      G2_C(cA, 2, 1) G2_T(cB, 1, 1, cc)
-      G2_C(cB, 3, 1) G2_T(cA, 2, 1, cc)
-      G2_T(cB, 3, 1, cc)
+      if constexpr (LORA) {
+        lora_epilogue<EPI>(a, acc, m0, n0, hf, lq, sxv);
+      } else {
+        G2_C(cA, 0, 0)
+        G2_C(cB, 1, 0) G2_T(cA, 0, 0, cc)
+        G2_C(cA, 2, 0) G2_T(cB, 1, 0, cc)
+        G2_C(cB, 3, 0) G2_T(cA, 2, 0, cc)
+        G2_C(cA, 0, 1) G2_T(cB, 3, 0, cc)
+        epi_cols(a, n0 + 32, cc);
+        G2_C(cB, 1, 1) G2_T(cA, 0, 1, cc)
+        G2_C(cA, 2, 1) G2_T(cB, 1, 1, cc)
+        G2_C(cB, 3, 1) G2_T(cA, 2, 1, cc)
+        G2_T(cB, 3, 1, cc)
+      }
 #undef G2_C
 #undef G2_T
 #pragma unroll
@@ -1319,43 +1486,6 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_f32m_skinny_kernel(F32WArg
 // time.  Both operands of one MFMA hold k = 8h .. 8h + 7 in lane half h, so the k order is the same
 // on both sides.  Output layouts and epilogues are those of the fp32 kernels.
 
-// three bf16 pieces of 8 fp32 values, two at a time (packed round-to-nearest-even conversions;
-// bf16 -> fp32 is exact, so each remainder is exact)
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ void split3_pair(f32x2_t v, bf16x2_t& h, bf16x2_t& m, bf16x2_t& l) {
-  h = __builtin_convertvector(v, bf16x2_t);
-  const f32x2_t r = v - __builtin_convertvector(h, f32x2_t);
-  m = __builtin_convertvector(r, bf16x2_t);
-  l = __builtin_convertvector(r - __builtin_convertvector(m, f32x2_t), bf16x2_t);
-}
-__device__ __forceinline__ void split3(float4 a, float4 b, bf16x8 (&o)[3]) {
-  bf16x2_t h0, m0, l0, h1, m1, l1, h2, m2, l2, h3, m3, l3;
-  split3_pair(f32x2_t{a.x, a.y}, h0, m0, l0);
-  split3_pair(f32x2_t{a.z, a.w}, h1, m1, l1);
-  split3_pair(f32x2_t{b.x, b.y}, h2, m2, l2);
-  split3_pair(f32x2_t{b.z, b.w}, h3, m3, l3);
-  o[0] = bf16x8{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
-  o[1] = bf16x8{m0[0], m0[1], m1[0], m1[1], m2[0], m2[1], m3[0], m3[1]};
-  o[2] = bf16x8{l0[0], l0[1], l1[0], l1[1], l2[0], l2[1], l3[0], l3[1]};
-}
-
-// acc += sum_{i+j<=2} a_i b_j, smallest terms first
-__device__ __forceinline__ f32x16 mfma_s3(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f32x16 acc) {
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
-}
-
-__device__ __forceinline__ bf16x8 ld_bf8(const uint16_t* p) {
-  const uint4 u = *(const uint4*)p;
-  bf16x8 r;
-  __builtin_memcpy(&r, &u, 16);
-  return r;
-}
 
 // Tall-skinny split product (the stacked LoRA A side, N <= 256, long K): the structure of
 // gemm_f32m_skinny_kernel (32 rows x 32 RT columns, eight waves over the k-slices, fixed-order
@@ -1863,6 +1993,16 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
   const float alpha = d->alpha != 0.0f ? d->alpha : 1.0f;
   const int64_t ld_add = d->ld_add ? d->ld_add : N;
   if (d->add && ld_add < N) return fail(c, ANIMA_E_ARG, "anima_linear: ld_add=%lld < N=%d", (long long)ld_add, N);
+  const bool lora = d->lora_xa || d->lora_b || d->lora_r;
+  if (lora) {
+    if (W->kind != ANIMA_W_I8 && W->kind != ANIMA_W_W4)
+      return fail(c, ANIMA_E_UNSUPPORTED, "anima_linear: the LoRA epilogue takes i8 / w4 weights (kind %d)", W->kind);
+    if (!d->lora_xa || !d->lora_b || d->lora_r < 16 || d->lora_r % 16 || d->ld_lora_xa < d->lora_r || d->ld_lora_xa % 4 ||
+        !al(d->lora_xa, 16) || !al(d->lora_b, 16))
+      return fail(c, ANIMA_E_ARG, "anima_linear: LoRA factors need lora_r %% 16 == 0 (%d), ld_lora_xa >= lora_r and %% 4 == 0 (%lld), 16-byte aligned",
+                  d->lora_r, (long long)d->ld_lora_xa);
+    if (d->add) return fail(c, ANIMA_E_UNSUPPORTED, "anima_linear: the LoRA epilogue and an add term together");
+  }
   if (M == 0) return ANIMA_OK;
 
   if (W->kind == ANIMA_W_F32S3) {
@@ -2017,6 +2157,12 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
   }
   GemmArgs g{qx, sx, W->w, W->scale, W->srel, W->codebook, W->bias, d->out, ldc, alpha, d->act, d->epilogue,
              d->gate, d->gate_off, d->acc_out, (int)M, N, K, d->add, ld_add};
+  if (lora) {
+    g.lx = d->lora_xa;
+    g.ld_lx = d->ld_lora_xa;
+    g.lb = d->lora_b;
+    g.lr = d->lora_r;
+  }
   int rc = ANIMA_OK;
   // Grids that give every CU a 256x256 tile run the persistent 256 kernel, smaller grids the
   // 128x128 kernel; both unpack W4 codes inside the GEMM.
@@ -2028,7 +2174,8 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
   const bool big = vec && tiles256 >= c->num_cus && tiles256 <= 0x7fffffff;
   void* grid8 = nullptr;
   bool w4k = w4;  // the GEMM unpacks W4 codes itself
-  if (big && w4 && c->w4_path == ANIMA_W4_GRID_SCRATCH) {
+  // (a LoRA epilogue always runs on the int8 grid: the in-GEMM unpack leaves it no registers)
+  if (big && w4 && (c->w4_path == ANIMA_W4_GRID_SCRATCH || lora)) {
     rc = w4_grid_scratch(c, W, g, &grid8);
     if (rc) {
       if (tmp) anima_free(c, tmp);
@@ -2036,20 +2183,44 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
     }
     w4k = false;
   }
-  {
+  void* ldelta = nullptr;  // small grids: the LoRA product as an add term (the split-bf16 kernel)
+  if (lora && !big) {
+    rc = anima_alloc(c, (size_t)M * N * 4, &ldelta);
+    if (rc) {
+      if (grid8) anima_free(c, grid8);
+      if (tmp) anima_free(c, tmp);
+      return rc;
+    }
+    const anima_weight bw{ANIMA_W_F32S3, N, d->lora_r, d->lora_b, nullptr, nullptr, nullptr, nullptr};
+    anima_linear_desc dd{};
+    dd.M = M;
+    dd.W = &bw;
+    dd.x = d->lora_xa;
+    dd.ldx = d->ld_lora_xa;
+    dd.out = (float*)ldelta;
+    rc = linear_launch(c, &dd);
+    g.add = (const float*)ldelta;
+    g.ld_add = N;
+    g.lr = 0;
+  }
+  if (!rc) {
     Launch L(c, w4k ? "gemm.w4a8" : "gemm.i8", 2.0 * M * N * K, 0.0);
     if (big) {
       const dim3 grid((unsigned)c->num_cus), block(512);
-#define G2L(E, W) hipLaunchKernelGGL((gemm_i8_256<E, W>), grid, block, 0, c->stream, g)
+#define G2L(E, W)                                                                                    \
+  {                                                                                                  \
+    if (lora) hipLaunchKernelGGL((gemm_i8_256<E, false, false, true>), grid, block, 0, c->stream, g); \
+    else hipLaunchKernelGGL((gemm_i8_256<E, W>), grid, block, 0, c->stream, g);                       \
+  }
       if (g.epi == ANIMA_EPI_STORE) {
-        if (w4k) G2L(ANIMA_EPI_STORE, true);
-        else G2L(ANIMA_EPI_STORE, false);
+        if (w4k) G2L(ANIMA_EPI_STORE, true)
+        else G2L(ANIMA_EPI_STORE, false)
       } else if (g.epi == ANIMA_EPI_RESID) {
-        if (w4k) G2L(ANIMA_EPI_RESID, true);
-        else G2L(ANIMA_EPI_RESID, false);
+        if (w4k) G2L(ANIMA_EPI_RESID, true)
+        else G2L(ANIMA_EPI_RESID, false)
       } else {
-        if (w4k) G2L(ANIMA_EPI_GATED, true);
-        else G2L(ANIMA_EPI_GATED, false);
+        if (w4k) G2L(ANIMA_EPI_GATED, true)
+        else G2L(ANIMA_EPI_GATED, false)
       }
 #undef G2L
     } else {
@@ -2059,6 +2230,7 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
     }
     rc = L.end();
   }
+  if (ldelta) anima_free(c, ldelta);
   if (grid8) anima_free(c, grid8);
   if (tmp) anima_free(c, tmp);
   return rc;
@@ -2078,8 +2250,8 @@ int linear_qkv_launch(anima_ctx* c, const anima_linear_desc* d, const anima_qkv_
   if (p->L % 64) return fail(c, ANIMA_E_UNSUPPORTED, "anima_linear_qkv: L=%d must be a multiple of 64", p->L);
   if (N != 3 * H * HD_K || K % GBK)
     return fail(c, ANIMA_E_ARG, "anima_linear_qkv: N=%d must be 3 * H * 128 = %d, K %% %d == 0", N, 3 * H * HD_K, GBK);
-  if (d->epilogue != ANIMA_EPI_STORE || d->act != ANIMA_ACT_NONE || d->add || d->acc_out)
-    return fail(c, ANIMA_E_UNSUPPORTED, "anima_linear_qkv: plain store only (no activation, residual, gate, add term or acc_out)");
+  if (d->epilogue != ANIMA_EPI_STORE || d->act != ANIMA_ACT_NONE || d->add || d->acc_out || d->lora_xa || d->lora_b || d->lora_r)
+    return fail(c, ANIMA_E_UNSUPPORTED, "anima_linear_qkv: plain store only (no activation, residual, gate, add term, LoRA or acc_out)");
   if (!p->k_norm || !p->rope_cs || !p->kv_prep)
     return fail(c, ANIMA_E_ARG, "anima_linear_qkv: k_norm, rope_cs and kv_prep are required");
   if (p->kv_prep_bytes != attention_kv_bytes(p->B, H, p->L, ANIMA_PREC_BF16))

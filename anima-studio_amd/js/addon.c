@@ -750,6 +750,10 @@ static napi_value js_linear(napi_env env, napi_callback_info info) {
   d.acc_out = (int32_t*)pptr(env, o, "accOut");
   d.add = (const float*)pptr(env, o, "add");
   d.ld_add = (int64_t)pnum(env, o, "ldAdd");
+  d.lora_xa = (const float*)pptr(env, o, "loraXa");
+  d.ld_lora_xa = (int64_t)pnum(env, o, "ldLoraXa");
+  d.lora_b = (const uint16_t*)pptr(env, o, "loraB");
+  d.lora_r = (int)pnum(env, o, "loraR");
   CHECK_RC(env, c, anima_linear(c, &d));
   return NULL;
 }

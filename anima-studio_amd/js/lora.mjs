@@ -12,7 +12,7 @@
 
 import { SafeTensors } from "./weights.mjs";
 import { native } from "./gpu.mjs";
-import { stackLora, releaseLoraStack, splitPlanes } from "./ops.mjs";
+import { stackLora, releaseLoraStack, splitPlanes, fuseLora, releaseLoraFused } from "./ops.mjs";
 
 const needsRotation = (W) => W.kind === "i8" || W.kind === "w4";
 const norm = (name) => name.replace(/\./g, "_");
@@ -161,6 +161,7 @@ export function attachLoras(regs, active) {
   for (const reg of [regs.dit, regs.te]) if (reg) for (const { W } of reg.values()) ws.add(W);
   for (const W of ws) {
     releaseLoraStack(W);
+    releaseLoraFused(W);
     if (W.lora) for (const e of W.lora) if (e.owned) for (const t of e.owned) t.release();
     W.lora = [];
   }
@@ -175,5 +176,11 @@ export function attachLoras(regs, active) {
         scale: strength * m.alphaScale, off: m.target.off, n: m.target.n });
     }
   }
-  for (const W of ws) if (W.lora.length > 1) stackLora(W.lora[0].A.gpu, W);
+  for (const W of ws) {
+    if (!W.lora.length) continue;
+    // quantized weights: the A stack and the B factor for the GEMM epilogue (fuseLora); others:
+    // the A stack of the separate products
+    if (needsRotation(W)) fuseLora(W.lora[0].A.gpu, W);
+    else if (W.lora.length > 1) stackLora(W.lora[0].A.gpu, W);
+  }
 }

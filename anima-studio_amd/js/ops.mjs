@@ -70,14 +70,20 @@ export function linear(gpu, x, W, opts) {
   const rot = !!(lora && needsRotation(W) && o.xr);
   const xin = rot ? o.xr : x;
   if (lora && !xin) throw new Error(`${W.name || "linear"}: a LoRA on a quantized weight needs the fp32 input (x or opts.xr)`);
-  // A plain store (no activation, no residual) takes the LoRA products afterwards, accumulated
-  // straight into the output; otherwise they form a delta that the epilogue adds.
-  const late = lora && !o.resid && ACT[o.act || "none"] === 0;
-  const delta = lora && !late ? loraDelta(gpu, xin, W, M, rot) : null;
+  // Quantized weights with fused LoRA factors (fuseLora): one A product over the stacked A, and
+  // the B product inside the GEMM's epilogue (no [M, N] delta).  Otherwise a plain store (no
+  // activation, no residual) takes the LoRA products afterwards, accumulated straight into the
+  // output, and other epilogues get them as a delta that the epilogue adds.
+  const F = lora && W.loraFused && W.loraFused.lora === W.lora ? W.loraFused : null;
+  if (F && rot && !F.Ar) throw new Error(`${W.name || "linear"}: LoRA entries without the rotated A for a rotated input`);
+  const down = F ? linear(gpu, xin, rot ? { kind: "f32s3", N: F.R, K: W.K, buf: F.Ars } : { kind: "f32s3", N: F.R, K: W.K, buf: F.As }, { M }) : null;
+  const late = lora && !F && !o.resid && ACT[o.act || "none"] === 0;
+  const delta = lora && !F && !late ? loraDelta(gpu, xin, W, M, rot) : null;
   const out = o.out || gpu.empty([M, W.N]);
   const d = { M, out: out.buf, ldc: o.ldc || 0, alpha: o.alpha || 0, act: ACT[o.act || "none"],
     epilogue: o.resid ? (o.gate ? 2 : 1) : 0, gate: ptr(o.gate), gOff: o.gOff || 0, accOut: ptr(o.accOut),
-    add: delta ? delta.buf : 0, ldAdd: delta ? W.N : 0 };
+    add: delta ? delta.buf : 0, ldAdd: delta ? W.N : 0,
+    loraXa: down ? down.buf : 0, ldLoraXa: down ? F.R : 0, loraB: F ? F.Bs.buf : 0, loraR: F ? F.R : 0 };
   if (needsRotation(W) && o.xq) {
     d.xq = o.xq.q.buf;
     d.xs = o.xq.s.buf;
@@ -93,7 +99,51 @@ export function linear(gpu, x, W, opts) {
   native.linear(gpu.ctx, w, d);
   if (late) loraInto(gpu, xin, W, M, out, o.ldc || W.N, false, rot);
   if (delta) delta.release();
+  if (down) down.release();
   return out;
+}
+
+// The LoRA factors of a quantized weight for the GEMM epilogue (anima_linear_desc.lora_*): every
+// entry's A (and A H) stacked into [R, K] with R the summed ranks rounded up to 16 (zero rows
+// pad), and B as one [N, R] matrix whose rows n of entry e hold scale_e * B_e[n - off_e] in the
+// columns of e's ranks (zeros elsewhere), so that y += (A x_in)^T-row times B-row sums
+// sum_e scale_e B_e (A_e x_in) over the entries covering column n (ops.js:55-87).  Built at
+// attach time (B composed on the host from the device copies); owned by W, freed with its stack.
+export function fuseLora(gpu, W) {
+  releaseLoraFused(W);
+  if (!W.lora || !W.lora.length || !needsRotation(W)) return null;
+  const R0 = W.lora.reduce((s, e) => s + e.r, 0), R = Math.ceil(R0 / 16) * 16, K = W.K, N = W.N;
+  const stack = (key) => {
+    const A = gpu.empty([R, K]);
+    if (R > R0) zero(gpu, A);
+    let r0 = 0;
+    for (const e of W.lora) {
+      gpu.copy(A.at(r0 * K), e[key], e.r * K * 4);
+      r0 += e.r;
+    }
+    return A;
+  };
+  const A = stack("A"), Ar = W.lora.every((e) => e.Ar) ? stack("Ar") : null;
+  const Bh = new Float32Array(N * R);
+  let r0 = 0;
+  for (const e of W.lora) {
+    const b = new Float32Array(e.n * e.r);
+    native.d2h(gpu.ctx, e.B.buf, b);
+    for (let i = 0; i < e.n; i++)
+      for (let j = 0; j < e.r; j++) Bh[(e.off + i) * R + r0 + j] = Math.fround(e.scale * b[i * e.r + j]);
+    r0 += e.r;
+  }
+  const Bf = gpu.fromArray(Bh, [N, R]);
+  W.loraFused = { A, Ar, As: splitPlanes(gpu, A, R * K), Ars: Ar ? splitPlanes(gpu, Ar, R * K) : null,
+    Bs: splitPlanes(gpu, Bf, N * R), R, lora: W.lora };
+  Bf.release();
+  return W.loraFused;
+}
+
+export function releaseLoraFused(W) {
+  const F = W.loraFused;
+  if (F) for (const t of [F.A, F.Ar, F.As, F.Ars, F.Bs]) if (t) t.release();
+  W.loraFused = null;
 }
 
 // The stacked QKV projection of a DiT self-attention with the attention's K / V operand

@@ -400,6 +400,16 @@ typedef struct {
    * input of gemm.js:189 that carries the LoRA delta of ops.js:55-62 (ld_add 0 -> N) */
   const float* add;
   int64_t ld_add;
+  /* i8/w4 only, optional: the LoRA delta of ops.js:55-62 (sum over entries of scale * B (A x_in))
+   * computed inside the epilogue from its two factors instead of passed as `add`:
+   * y += sum_k lora_xa[m*ld_lora_xa + k] * B[n][k] for k < lora_r, after the bias and before the
+   * activation / gate, with lora_xa the A products (fp32 [M][ld_lora_xa]) and lora_b the three
+   * bf16 planes [3][N][lora_r] (anima_split3_bf16) of B, every entry's scale folded into its
+   * columns.  lora_r % 16 == 0, ld_lora_xa % 4 == 0, both 16-byte aligned; not with `add`. */
+  const float* lora_xa;
+  int64_t ld_lora_xa;
+  const uint16_t* lora_b;
+  int lora_r;
 } anima_linear_desc;
 
 /* ops.linear (app/gpu/ops.js:48-66) -> matmulShader (gemm.js:166-280):

@@ -472,6 +472,66 @@ def test_linear_add_term(ctx, M):
     assert np.array_equal(got[rows], ref), report("add term", got[rows], ref)
 
 
+@pytest.mark.parametrize("M,epi,act", [(4000, "gated", "none"), (4000, "store", "gelu"), (4000, "resid", "none"),
+                                       (200, "gated", "none")])
+def test_linear_lora_epilogue(ctx, M, epi, act):
+    """The LoRA delta computed from its two factors in the quantized GEMM (anima_linear_desc
+    lora_xa / lora_b / lora_r): y += xa[m] . B[n] after the bias, before the activation / gate
+    (ops.js:55-87 with the scale folded into B).  xa [M, R] fp32 with ld > R, B [N, R] as three
+    bf16 planes (anima_split3_bf16), R = 48 (three 16-k slices); N = 4100 leaves a partial column
+    tile.  M = 4000 runs the 256-tile kernel with the product inside its epilogue, M = 200 the
+    128-tile kernel with the product as an add term.  Against the oracle epilogue fed the float64
+    delta (rounded to fp32): rel-L2 <= 2e-6; the int32 accumulators bit-exact."""
+    case(f"linear LoRA epilogue M={M} {epi} act={act}")
+    m = amd()
+    K, N, R, ld = 1024, 4100, 48, 52
+    x = orc.randn(141, M * K).reshape(M, K)
+    qx, sx = orc.token_quant(orc.hadamard256(x))
+    qw, sw = int8_weight(142, N, K)
+    bias = (0.1 * orc.randn(143, N)).astype(np.float32)
+    gate = orc.randn(144, 3 * N).astype(np.float32)
+    resid = orc.randn(145, M * N).reshape(M, N)
+    xa = (0.5 * orc.randn(146, M * ld)).reshape(M, ld).astype(np.float32)
+    Bm = (0.05 * orc.randn(147, N * R)).reshape(N, R).astype(np.float32)
+    dB = ctx.upload(Bm)
+    planes = ctx.empty(3 * N * R, np.uint16)
+    ctx.split3_bf16(dB, planes, N * R)
+    W = m.weight(m.W_I8, N, K, ctx.upload(qw), scale=ctx.upload(sw), bias=ctx.upload(bias))
+    dout, dacc = ctx.upload(resid), ctx.empty((M, N), np.int32)
+    e = {"store": m.EPI_STORE, "resid": m.EPI_RESID, "gated": m.EPI_GATED}[epi]
+    ctx.linear(W, M, dout, xq=ctx.upload(qx), xs=ctx.upload(sx), epilogue=e, gate=ctx.upload(gate), gate_off=N,
+               act=act, acc_out=dacc, lora_xa=ctx.upload(xa), ld_lora_xa=ld, lora_b=planes, lora_r=R)
+    acc, got = dacc.numpy(), dout.numpy()
+    assert checksums_ok(qx, qw, acc)
+    rows = np.unique(np.concatenate([np.arange(0, 4), np.random.default_rng(5).choice(M, 12, replace=False),
+                                     np.arange(M - 8, M)]))
+    ref_acc = orc.gemm_i8(qx[rows], qw)
+    assert np.array_equal(acc[rows], ref_acc)
+    delta = (xa[rows, :R].astype(np.float64) @ Bm.astype(np.float64).T).astype(np.float32)
+    ref = orc.linear_epilogue(ref_acc, sx[rows], sw, bias=bias, act={"none": 0, "gelu": 1}[act], epi=e, gate=gate,
+                              g_off=N, c=resid[rows] if epi != "store" else None, add=delta)
+    r, _ = report(f"LoRA epilogue {epi} {act} M={M}", got[rows], ref)
+    assert r <= 2e-6
+
+
+def test_linear_lora_epilogue_refusals(ctx):
+    """The LoRA factors are refused on the host: a rank that is not a multiple of 16 or an ld below
+    it (ANIMA_E_ARG), together with an add term or on a bf16 weight (ANIMA_E_UNSUPPORTED)."""
+    case("linear LoRA epilogue refusals")
+    m = amd()
+    buf = ctx.empty(1 << 20)
+    W = m.weight(m.W_I8, 64, 128, buf, scale=buf)
+    for kw, code in ((dict(lora_r=40, ld_lora_xa=40), -1), (dict(lora_r=32, ld_lora_xa=16), -1),
+                     (dict(lora_r=32, ld_lora_xa=32, add=buf, ld_add=64), -5)):
+        with pytest.raises(m.AnimaError) as e:
+            ctx.linear(W, 4, buf, xq=buf, xs=buf, lora_xa=buf, lora_b=buf, **kw)
+        assert e.value.code == code, (kw, e.value)
+    Wb = m.weight(m.W_BF16, 64, 128, buf)
+    with pytest.raises(m.AnimaError) as e:
+        ctx.linear(Wb, 4, buf, x=buf, lora_xa=buf, lora_b=buf, lora_r=32, ld_lora_xa=32)
+    assert e.value.code == -5
+
+
 def test_f32_weight_linears(ctx):
     """fp32 weights (the LoRA A / B matrices): tall-skinny and short-K shapes against float64,
     with alpha, column offset into a wider output (ldc) and residual accumulation."""
