@@ -1487,108 +1487,146 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_f32m_skinny_kernel(F32WArg
 // on both sides.  Output layouts and epilogues are those of the fp32 kernels.
 
 
-// Tall-skinny split product (the stacked LoRA A side, N <= 256, long K): the structure of
-// gemm_f32m_skinny_kernel (32 rows x 32 RT columns, eight waves over the k-slices, fixed-order
-// LDS tree), one 16-k slice per step.
+// Tall-skinny split product (the stacked LoRA A side, N <= 96, long K): 32 rows x 32 RT columns per
+// workgroup, eight waves over k with the fixed-order LDS tree of gemm_f32m_skinny_kernel.  The
+// 16x16x32 matrix-core shape: a wave's 32-k step is 2 row tiles x 2 RT column tiles, lane (r, g)
+// holding row (or column) r's k = 8 g .. 8 g + 7 on both operands.  One load instruction then
+// covers 16 rows x 64 contiguous bytes (x) or 16 rows x 64 bytes (a W plane): half the cache
+// lines per byte of the 32x32x16 layout (32 rows x 32 bytes), whose address path bounds the
+// kernel well below HBM rate (the product itself is a small share of the matrix-core time).
+__device__ __forceinline__ f32x4 mfma16_s3(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f32x4 acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[0], acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], acc, 0, 0, 0);
+}
+
 template <int RT>
 __global__ __launch_bounds__(64 * SK_WAVES) void gemm_s3_skinny_kernel(F32WArgs a) {
+  constexpr int CT = 2 * RT;  // 16-column tiles
   __shared__ float part[SK_WAVES / 2 * 64 * 16 * RT];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lq = lane & 31, hf = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int r16 = lane & 15, g = lane >> 4;
   const int m0 = blockIdx.y * 32, nb = blockIdx.x * 32 * RT;
-  const int m = m0 + lq;
-  const bool mok = m < a.M;
-  const float* xr = a.x + (int64_t)(mok ? m : 0) * a.ldx + 8 * hf;
-  const uint16_t* W = (const uint16_t*)a.w;
-  const int64_t plane = (int64_t)a.N * a.K;
-  int64_t wr[RT];
-  bool nok[RT];
+  // Raw buffer loads: an offset at or past the buffer's end reads zeros, which masks the k tail
+  // (and x's rows past M) without a select, and the loads are not plain LLVM loads, which the
+  // compiler would fold across the loop's back edge into the header (undoing the prefetch).  A
+  // row of W past N reads the next plane's data and feeds only columns that are never stored.
+  const int rows = a.M - m0 < 32 ? a.M - m0 : 32;
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.x + (int64_t)m0 * a.ldx), (short)0, rows * (int)a.ldx * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, 3 * a.N * a.K * 2, 0x00020000);
+  const uint32_t plane2 = 2u * (uint32_t)a.N * (uint32_t)a.K;  // bytes per plane
+  uint32_t xoff[2], woff[CT];
 #pragma unroll
-  for (int t = 0; t < RT; t++) {
-    const int n = nb + 32 * t + lq;
-    nok[t] = n < a.N;
-    wr[t] = (int64_t)(nok[t] ? n : 0) * a.K + 8 * hf;
-  }
-  f32x16 acc[RT];
+  for (int t = 0; t < 2; t++) xoff[t] = 4u * ((uint32_t)(16 * t + r16) * (uint32_t)a.ldx + 8u * g);
 #pragma unroll
-  for (int t = 0; t < RT; t++) acc[t] = f32x16{};
-  const int nsl = (a.K + 15) / 16;
-  const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  const bf16x8 z8 = {};
-  // one 16-k slice per step, the next slice's loads issued before this slice's MFMAs
-#define S3_LOAD(SL, X0, X1, WV)                                                                  \
+  for (int t = 0; t < CT; t++) woff[t] = 2u * ((uint32_t)(nb + 16 * t + r16) * (uint32_t)a.K + 8u * g);
+  f32x4 acc[2][CT];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int t = 0; t < CT; t++) acc[i][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int nst = (a.K + 31) / 32;
+  // one 32-k step; the next step's loads are issued before this step's MFMAs
+#define S3_LOAD(ST, VALID, XV, WV)                                                               \
   {                                                                                              \
-    const int k0_ = 16 * (SL);                                                                   \
-    const bool kok_ = k0_ + 8 * hf < a.K; /* K % 8 == 0: a lane's 8 values are all in or out */ \
-    const int kc_ = kok_ ? k0_ : 0;       /* unconditional in-bounds loads, then selects */     \
-    const float4 t0_ = *(const float4*)(xr + kc_), t1_ = *(const float4*)(xr + kc_ + 4);        \
-    X0 = mok && kok_ ? t0_ : z4;                                                                 \
-    X1 = mok && kok_ ? t1_ : z4;                                                                 \
-    _Pragma("unroll") for (int t = 0; t < RT; t++)                                               \
-    _Pragma("unroll") for (int p = 0; p < 3; p++) {                                              \
-      const bf16x8 u_ = ld_bf8(W + p * plane + wr[t] + kc_);                                     \
-      WV[t][p] = nok[t] && kok_ ? u_ : z8;                                                       \
+    const int kb_ = 32 * (ST);                                                                   \
+    const bool ok_ = (VALID) && kb_ + 8 * g < a.K; /* K % 8 == 0: 8 values all in or out */      \
+    _Pragma("unroll") for (int i = 0; i < 2; i++) {                                              \
+      const uint32_t xo_ = ok_ ? xoff[i] + 4u * kb_ : 0x80000000u;                               \
+      XV[i][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo_, 0, 0)); \
+      XV[i][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo_ + 16u, 0, 0)); \
+    }                                                                                            \
+    _Pragma("unroll") for (int t = 0; t < CT; t++)                                               \
+    _Pragma("unroll") for (int p = 0; p < 3; p++) WV[t][p] = __builtin_bit_cast(bf16x8,          \
+        __builtin_amdgcn_raw_buffer_load_b128(rw, ok_ ? woff[t] + p * plane2 + 2u * kb_ : 0x80000000u, 0, 0)); \
+  }
+#define S3_MMA(XV, WV)                                                                           \
+  {                                                                                              \
+    _Pragma("unroll") for (int i = 0; i < 2; i++) {                                              \
+      bf16x8 xs_[3];                                                                             \
+      split3(XV[i][0], XV[i][1], xs_);                                                           \
+      _Pragma("unroll") for (int t = 0; t < CT; t++) acc[i][t] = mfma16_s3(xs_, WV[t], acc[i][t]); \
     }                                                                                            \
   }
-#define S3_MMA(X0, X1, WV)                                                   \
-  {                                                                          \
-    bf16x8 xs_[3];                                                           \
-    split3(X0, X1, xs_);                                                     \
-    _Pragma("unroll") for (int t = 0; t < RT; t++) acc[t] = mfma_s3(xs_, WV[t], acc[t]); \
-  }
-  if (wave < nsl) {
-    float4 xa0, xa1, xb0, xb1;
-    bf16x8 wa[RT][3], wb[RT][3];
-    S3_LOAD(wave, xa0, xa1, wa)
-    for (int sl = wave;;) {
-      const bool more = sl + SK_WAVES < nsl;
-      if (more) S3_LOAD(sl + SK_WAVES, xb0, xb1, wb)
-      S3_MMA(xa0, xa1, wa)
-      if (!more) break;
-      sl += SK_WAVES;
-      const bool more2 = sl + SK_WAVES < nsl;
-      if (more2) S3_LOAD(sl + SK_WAVES, xa0, xa1, wa)
-      S3_MMA(xb0, xb1, wb)
-      if (!more2) break;
-      sl += SK_WAVES;
+  // Wave w takes the contiguous steps [w * per, w * per + cnt), starting at a per-block rotation:
+  // concurrent loads spread over the row length instead of every wave of the grid reading the
+  // same window of every row.
+  const int per = (nst + SK_WAVES - 1) / SK_WAVES, s0 = wave * per;
+  const int cnt = nst - s0 < per ? nst - s0 : per;
+  if (cnt > 0) {
+    const int rot = (int)(blockIdx.y % (unsigned)cnt);
+#define S3_STEP(I) (s0 + ((I) + rot < cnt ? (I) + rot : (I) + rot - cnt))
+    float4 xa[2][2], xb[2][2];
+    bf16x8 wa[CT][3], wb[CT][3];
+    // Steps in pairs, one basic block per pair: each half issues the other buffer's loads before
+    // its own MFMAs, and no branch separates a load from its use (which would let the compiler
+    // sink the load next to that use).  An odd count ends on a zero-read repeat of the last step;
+    // the final prefetch is never used.  The scheduling barriers keep each load group above the
+    // other buffer's MFMAs (left alone, the scheduler moves loads down next to their uses).
+    S3_LOAD(S3_STEP(0), true, xa, wa)
+    for (int i = 0; i < cnt; i += 2) {
+      S3_LOAD(S3_STEP(i + 1 < cnt ? i + 1 : i), i + 1 < cnt, xb, wb)
+      __builtin_amdgcn_sched_barrier(0);
+      S3_MMA(xa, wa)
+      __builtin_amdgcn_sched_barrier(0);
+      S3_LOAD(S3_STEP(i + 2 < cnt ? i + 2 : cnt - 1), i + 2 < cnt, xa, wa)
+      __builtin_amdgcn_sched_barrier(0);
+      S3_MMA(xb, wb)
+      __builtin_amdgcn_sched_barrier(0);
     }
+#undef S3_STEP
   }
 #undef S3_LOAD
 #undef S3_MMA
+  // fixed-order tree: waves [h, 2h) hand their sums to waves [0, h), h = 4, 2, 1
 #pragma unroll
   for (int h = SK_WAVES / 2; h >= 1; h >>= 1) {
     if (wave >= h && wave < 2 * h) {
 #pragma unroll
-      for (int t = 0; t < RT; t++)
+      for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) part[(((wave - h) * RT + t) * 64 + lane) * 16 + r] = acc[t][r];
+        for (int t = 0; t < CT; t++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) part[((((wave - h) * 2 + i) * CT + t) * 4 + r) * 64 + lane] = acc[i][t][r];
     }
     __syncthreads();
     if (wave < h) {
 #pragma unroll
-      for (int t = 0; t < RT; t++)
+      for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) acc[t][r] = acc[t][r] + part[((wave * RT + t) * 64 + lane) * 16 + r];
+        for (int t = 0; t < CT; t++)
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            acc[i][t][r] = acc[i][t][r] + part[(((wave * 2 + i) * CT + t) * 4 + r) * 64 + lane];
     }
     __syncthreads();
   }
   if (wave > 0) return;
+  // lane (r16, g) holds rows 16 i + 4 g + r of column tile t's column r16
 #pragma unroll
-  for (int t = 0; t < RT; t++) {
-    if (!nok[t]) continue;
-    const int n = nb + 32 * t + lq;
+  for (int t = 0; t < CT; t++) {
+    const int n = nb + 16 * t + r16;
+    if (n >= a.N) continue;
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int mm = m0 + 8 * (r >> 2) + 4 * hf + (r & 3);
-      if (mm >= a.M) continue;
-      float v = acc[t][r] * a.alpha;
-      if (a.bias) v = v + a.bias[n];
-      if (a.add) v = v + a.add[(int64_t)mm * a.ld_add + n];
-      v = apply_act(v, a.act);
-      float* c = a.out + (int64_t)mm * a.ldc + n;
-      if (a.epi == ANIMA_EPI_STORE) *c = v;
-      else if (a.epi == ANIMA_EPI_RESID) *c = *c + v;
-      else *c = __builtin_fmaf(a.gate[a.gate_off + n], v, *c);
-    }
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int mm = m0 + 16 * i + 4 * g + r;
+        if (mm >= a.M) continue;
+        float v = acc[i][t][r] * a.alpha;
+        if (a.bias) v = v + a.bias[n];
+        if (a.add) v = v + a.add[(int64_t)mm * a.ld_add + n];
+        v = apply_act(v, a.act);
+        float* c = a.out + (int64_t)mm * a.ldc + n;
+        if (a.epi == ANIMA_EPI_STORE) *c = v;
+        else if (a.epi == ANIMA_EPI_RESID) *c = *c + v;
+        else *c = __builtin_fmaf(a.gate[a.gate_off + n], v, *c);
+      }
   }
 }
 
@@ -1621,12 +1659,13 @@ __global__ __launch_bounds__(256) void gemm_s3_t_kernel(F32WArgs a) {
     float4 x[2][2];
     bf16x8 wv[NT][2][3], xs[3];
     // unconditional loads at clamped in-bounds offsets, taken as loaded: rows past M or N only
-    // reach outputs that are not stored; a slice past K (K % 8 == 0: a lane's 8 values are all
-    // in or all out) loads k = 0 and its x values are zeroed where they are split
+    // reach outputs that are not stored; a lane whose 8 values of a slice lie past K (K % 8 == 0:
+    // all in or all out) loads its row's first 8 (xr and wr already hold the lane's 8 hf, so the
+    // offset is -8 hf) and its x values are zeroed where they are split
 #pragma unroll
     for (int h = 0; h < 2; h++) {
       const int k = k0 + 16 * h;
-      const int kc = k + 8 * hf < a.K ? k : 0;
+      const int kc = k + 8 * hf < a.K ? k : -8 * hf;
       x[h][0] = *(const float4*)(xr + kc);
       x[h][1] = *(const float4*)(xr + kc + 4);
 #pragma unroll
@@ -2015,11 +2054,14 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
     F32WArgs f{d->x, ldx, W->w, W->bias, d->out, ldc, alpha, d->act, d->epilogue, d->gate, d->gate_off,
                (int)M, N, K, 0, 0, 0, 0, d->add, ld_add, 0};
     Launch L(c, "gemm.f32s3", 2.0 * M * N * K, 0.0);
-    const dim3 sk((unsigned)((N + 127) / 128), (unsigned)((M + 31) / 32)), blk(64 * SK_WAVES);
-    if (N <= 32 && K >= 512) hipLaunchKernelGGL(gemm_s3_skinny_kernel<1>, sk, blk, 0, c->stream, f);
-    else if (N <= 64 && K >= 512) hipLaunchKernelGGL(gemm_s3_skinny_kernel<2>, sk, blk, 0, c->stream, f);
-    else if (N <= 96 && K >= 512) hipLaunchKernelGGL(gemm_s3_skinny_kernel<3>, sk, blk, 0, c->stream, f);
-    else if (N <= 256 && K >= 512) hipLaunchKernelGGL(gemm_s3_skinny_kernel<4>, sk, blk, 0, c->stream, f);
+    // the skinny kernel's buffer offsets are 32-bit: 32 rows of x and the three planes of W;
+    // N in (96, 256] runs as 64-column workgroups
+    const bool skf = K >= 512 && ldx < (1 << 23) && 6LL * N * K < (1LL << 31) && N <= 256;
+    const int srt = N <= 32 ? 1 : N <= 64 || N > 96 ? 2 : 3;
+    const dim3 sk((unsigned)((N + 32 * srt - 1) / (32 * srt)), (unsigned)((M + 31) / 32)), blk(64 * SK_WAVES);
+    if (skf && srt == 1) hipLaunchKernelGGL(gemm_s3_skinny_kernel<1>, sk, blk, 0, c->stream, f);
+    else if (skf && srt == 2) hipLaunchKernelGGL(gemm_s3_skinny_kernel<2>, sk, blk, 0, c->stream, f);
+    else if (skf) hipLaunchKernelGGL(gemm_s3_skinny_kernel<3>, sk, blk, 0, c->stream, f);
     else if (N % 4 == 0 && ldc % 4 == 0 && al(d->out, 16) && (!W->bias || al(W->bias, 16)) &&
              (!d->add || (al(d->add, 16) && ld_add % 4 == 0)) &&
              (d->epilogue != ANIMA_EPI_GATED || al(d->gate + d->gate_off, 16)))
