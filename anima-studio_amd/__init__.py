@@ -72,7 +72,7 @@ class LinearDesc(ctypes.Structure):
                 ("xq", _vp), ("xs", _vp), ("out", _vp), ("ldc", _i64), ("alpha", ctypes.c_float),
                 ("act", ctypes.c_int), ("epilogue", ctypes.c_int), ("gate", _vp), ("gate_off", _i64),
                 ("acc_out", _vp), ("add", _vp), ("ld_add", _i64), ("lora_xa", _vp), ("ld_lora_xa", _i64),
-                ("lora_b", _vp), ("lora_r", ctypes.c_int)]
+                ("lora_b", _vp), ("lora_r", ctypes.c_int), ("lora_cols", ctypes.c_int)]
 
 
 SAMPLER = {"euler": 0, "euler_a": 1, "dpmpp_2m": 2, "er_sde": 3}
@@ -421,14 +421,16 @@ class Context:
 
     def linear(self, W, M, out, *, x=None, ldx=0, x_rotated=True, xq=None, xs=None, ldc=0, alpha=0.0, act="none",
                epilogue=EPI_STORE, gate=None, gate_off=0, acc_out=None, add=None, ld_add=0, lora_xa=None,
-               ld_lora_xa=0, lora_b=None, lora_r=0):
+               ld_lora_xa=0, lora_b=None, lora_r=0, lora_cols=0):
         """anima_linear; lora_xa / lora_b / lora_r: the LoRA delta's factors for the quantized
-        GEMM's epilogue (A products [M][ld_lora_xa] fp32, B as three bf16 planes [3][N][lora_r])."""
+        GEMM's epilogue (A products [M][ld_lora_xa] fp32, B as three bf16 planes [3][N][lora_r]);
+        lora_cols > 0: block-diagonal ranks, column n reading xa columns (n // lora_cols) * lora_r
+        + k."""
         d = LinearDesc(M=M, W=ctypes.pointer(W), x=_ptr(x), ldx=ldx, x_rotated=int(x_rotated), xq=_ptr(xq),
                        xs=_ptr(xs), out=_ptr(out), ldc=ldc, alpha=alpha, act=ACT[act] if isinstance(act, str) else act,
                        epilogue=epilogue, gate=_ptr(gate), gate_off=gate_off, acc_out=_ptr(acc_out), add=_ptr(add),
                        ld_add=ld_add, lora_xa=_ptr(lora_xa), ld_lora_xa=ld_lora_xa, lora_b=_ptr(lora_b),
-                       lora_r=lora_r)
+                       lora_r=lora_r, lora_cols=lora_cols)
         return self._check(lib().anima_linear(self.h, ctypes.byref(d)))
 
     def linear_qkv(self, W, M, out, *, B, L, H, k_norm, rope_cs, rope_sin_off, kv_prep, eps=1e-6, x=None, ldx=0,

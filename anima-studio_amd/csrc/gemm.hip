@@ -49,11 +49,14 @@ struct GemmArgs {
   int L, Lkp, H;     // tokens per batch element (M = B * L, L % 64 == 0 so Lkp = L), heads
   int kcol, vcol;
   // LoRA B product in the epilogue (gemm_i8_256<..., LORA>): y += sum_k lx[m][k] * B[n][k], k < lr,
-  // with B as three bf16 planes lb [3][N][lr] (the scales folded in); lr % 16 == 0
+  // with B as three bf16 planes lb [3][N][lr] (the scales folded in); lr % 16 == 0.  lcols > 0
+  // (a multiple of 256, so a tile lies in one block): columns of block n / lcols read lx columns
+  // (n / lcols) * lr + k
   const float* lx = nullptr;
   int64_t ld_lx = 0;
   const uint16_t* lb = nullptr;
   int lr = 0;
+  int lcols = 0;
 };
 
 
@@ -362,6 +365,9 @@ __device__ __forceinline__ void lora_epilogue(const GemmArgs& a, const i32x16 (&
   const int64_t plane = (int64_t)a.N * a.lr;
   const bf16x8 z8 = {};
   const float4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  // the tile's rank block (wave-uniform; taken to a scalar register, which keeps the division's
+  // vector temporaries from raising the kernel's register pressure into main-loop spills)
+  const float* lx = a.lx + (int64_t)__builtin_amdgcn_readfirstlane(a.lcols ? (n0 / a.lcols) * a.lr : 0);
   for (int k0 = 0; k0 < a.lr; k0 += 16) {
     bf16x8 bv[2][3];
     float4 xr[4][2];
@@ -377,7 +383,7 @@ __device__ __forceinline__ void lora_epilogue(const GemmArgs& a, const i32x16 (&
     for (int i = 0; i < 4; i++) {
       const int m = m0 + 32 * i;
       const bool mok = m < a.M;
-      const float* xp = a.lx + (int64_t)(mok ? m : 0) * a.ld_lx + 8 * hf + k0;
+      const float* xp = lx + (int64_t)(mok ? m : 0) * a.ld_lx + 8 * hf + k0;
       xr[i][0] = mok ? *(const float4*)xp : z4;
       xr[i][1] = mok ? *(const float4*)(xp + 4) : z4;
     }
@@ -1145,6 +1151,7 @@ struct F32WArgs {
   int64_t ld_add;
   int wf32;  // fp32 weights (tile kernel only)
   int64_t ldw = 0;  // weight row stride (0: K); the split-k LDS kernel reads k-slices of longer rows
+  int64_t wplane = 0;  // split weights: plane stride in elements (set by the host, N * K unless a row block)
 };
 
 // 64x64 tile, 256 threads x (4x4) outputs, k-tile 16 (the small-tile layout of gemm.js:17).
@@ -1517,9 +1524,9 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_s3_skinny_kernel(F32WArgs 
   const int rows = a.M - m0 < 32 ? a.M - m0 : 32;
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.x + (int64_t)m0 * a.ldx), (short)0, rows * (int)a.ldx * 4, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rw =
-      __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, 3 * a.N * a.K * 2, 0x00020000);
-  const uint32_t plane2 = 2u * (uint32_t)a.N * (uint32_t)a.K;  // bytes per plane
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.w, (short)0, (int)(2 * (2 * a.wplane + (int64_t)a.N * a.K)), 0x00020000);
+  const uint32_t plane2 = 2u * (uint32_t)a.wplane;  // bytes per plane
   uint32_t xoff[2], woff[CT];
 #pragma unroll
   for (int t = 0; t < 2; t++) xoff[t] = 4u * ((uint32_t)(16 * t + r16) * (uint32_t)a.ldx + 8u * g);
@@ -1642,7 +1649,7 @@ __global__ __launch_bounds__(256) void gemm_s3_t_kernel(F32WArgs a) {
   const bool mok = m < a.M;
   const float* xr = a.x + (int64_t)(mok ? m : 0) * a.ldx + 8 * hf;
   const uint16_t* W = (const uint16_t*)a.w;
-  const int64_t plane = (int64_t)a.N * a.K;
+  const int64_t plane = a.wplane;
   int64_t wr[NT];
   bool nok[NT];
 #pragma unroll
@@ -2017,7 +2024,7 @@ __global__ __launch_bounds__(256) void gemv_f32w_kernel(F32WArgs a) {
 
 static bool al(const void* p, int b) { return ((uintptr_t)p & (b - 1)) == 0; }
 
-int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
+int linear_launch(anima_ctx* c, const anima_linear_desc* d, int64_t s3_plane) {
   const anima_weight* W = d->W;
   if (!W) return fail(c, ANIMA_E_ARG, "anima_linear: null weight");
   const int64_t M = d->M;
@@ -2040,6 +2047,10 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
         !al(d->lora_xa, 16) || !al(d->lora_b, 16))
       return fail(c, ANIMA_E_ARG, "anima_linear: LoRA factors need lora_r %% 16 == 0 (%d), ld_lora_xa >= lora_r and %% 4 == 0 (%lld), 16-byte aligned",
                   d->lora_r, (long long)d->ld_lora_xa);
+    if (d->lora_cols < 0 || (d->lora_cols && (N % d->lora_cols || d->lora_cols % 16)) ||
+        d->ld_lora_xa < (int64_t)d->lora_r * (d->lora_cols ? N / d->lora_cols : 1))
+      return fail(c, ANIMA_E_ARG, "anima_linear: lora_cols=%d must divide N=%d, be a multiple of 16 and fit ld_lora_xa=%lld",
+                  d->lora_cols, N, (long long)d->ld_lora_xa);
     if (d->add) return fail(c, ANIMA_E_UNSUPPORTED, "anima_linear: the LoRA epilogue and an add term together");
   }
   if (M == 0) return ANIMA_OK;
@@ -2051,12 +2062,14 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
     if (ldx < K) return fail(c, ANIMA_E_ARG, "anima_linear: ldx < K");
     if (K % 8 || ldx % 4 || !al(d->x, 16) || !al(W->w, 16))
       return fail(c, ANIMA_E_ARG, "anima_linear: split weights need K %% 8 == 0, ldx %% 4 == 0, 16-byte aligned x and w");
+    if (s3_plane && s3_plane < (int64_t)N * K) return fail(c, ANIMA_E_ARG, "anima_linear: split-weight plane stride below N * K");
     F32WArgs f{d->x, ldx, W->w, W->bias, d->out, ldc, alpha, d->act, d->epilogue, d->gate, d->gate_off,
                (int)M, N, K, 0, 0, 0, 0, d->add, ld_add, 0};
+    f.wplane = s3_plane ? s3_plane : (int64_t)N * K;
     Launch L(c, "gemm.f32s3", 2.0 * M * N * K, 0.0);
     // the skinny kernel's buffer offsets are 32-bit: 32 rows of x and the three planes of W;
     // N in (96, 256] runs as 64-column workgroups
-    const bool skf = K >= 512 && ldx < (1 << 23) && 6LL * N * K < (1LL << 31) && N <= 256;
+    const bool skf = K >= 512 && ldx < (1 << 23) && 2 * (2 * f.wplane + (int64_t)N * K) < (1LL << 31) && N <= 256;
     const int srt = N <= 32 ? 1 : N <= 64 || N > 96 ? 2 : 3;
     const dim3 sk((unsigned)((N + 32 * srt - 1) / (32 * srt)), (unsigned)((M + 31) / 32)), blk(64 * SK_WAVES);
     if (skf && srt == 1) hipLaunchKernelGGL(gemm_s3_skinny_kernel<1>, sk, blk, 0, c->stream, f);
@@ -2204,6 +2217,7 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
     g.ld_lx = d->ld_lora_xa;
     g.lb = d->lora_b;
     g.lr = d->lora_r;
+    g.lcols = d->lora_cols;
   }
   int rc = ANIMA_OK;
   // Grids that give every CU a 256x256 tile run the persistent 256 kernel, smaller grids the
@@ -2225,22 +2239,29 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d) {
     }
     w4k = false;
   }
-  void* ldelta = nullptr;  // small grids: the LoRA product as an add term (the split-bf16 kernel)
-  if (lora && !big) {
+  // small grids, and rank blocks that split a 256-column tile: the LoRA product as an add term
+  // (the split-bf16 kernel, one product per rank block over its columns' rows of the B planes)
+  void* ldelta = nullptr;
+  if (lora && (!big || d->lora_cols % 256)) {
     rc = anima_alloc(c, (size_t)M * N * 4, &ldelta);
     if (rc) {
       if (grid8) anima_free(c, grid8);
       if (tmp) anima_free(c, tmp);
       return rc;
     }
-    const anima_weight bw{ANIMA_W_F32S3, N, d->lora_r, d->lora_b, nullptr, nullptr, nullptr, nullptr};
-    anima_linear_desc dd{};
-    dd.M = M;
-    dd.W = &bw;
-    dd.x = d->lora_xa;
-    dd.ldx = d->ld_lora_xa;
-    dd.out = (float*)ldelta;
-    rc = linear_launch(c, &dd);
+    const int bc = d->lora_cols ? d->lora_cols : N;
+    for (int b = 0; b * bc < N && !rc; b++) {
+      const anima_weight bw{ANIMA_W_F32S3, bc, d->lora_r, d->lora_b + (int64_t)b * bc * d->lora_r, nullptr, nullptr,
+                            nullptr, nullptr};
+      anima_linear_desc dd{};
+      dd.M = M;
+      dd.W = &bw;
+      dd.x = d->lora_xa + (int64_t)b * d->lora_r;
+      dd.ldx = d->ld_lora_xa;
+      dd.out = (float*)ldelta + (int64_t)b * bc;
+      dd.ldc = N;
+      rc = linear_launch(c, &dd, (int64_t)N * d->lora_r);
+    }
     g.add = (const float*)ldelta;
     g.ld_add = N;
     g.lr = 0;

@@ -139,7 +139,9 @@ int sampler_step_launch(anima_ctx* c, const anima_sampler_desc* d);
 int fill_random_launch(anima_ctx* c, void* dst, int64_t n, int kind, uint64_t seed, float lo, float hi);
 
 // ---- kernel launchers (gemm.hip)
-int linear_launch(anima_ctx* c, const anima_linear_desc* d);
+// s3_plane: split-weight (ANIMA_W_F32S3) plane stride in elements, 0 = N * K (a row block of
+// larger planes passes the full planes' stride)
+int linear_launch(anima_ctx* c, const anima_linear_desc* d, int64_t s3_plane = 0);
 int linear_qkv_launch(anima_ctx* c, const anima_linear_desc* d, const anima_qkv_desc* p);
 int linear_grouped_bf16_launch(anima_ctx* c, int G, int64_t M, int N, int K, const float* x, int64_t ldx,
                                int64_t x_gs, const uint16_t* w, int64_t w_gs, const float* bias, int64_t bias_gs,

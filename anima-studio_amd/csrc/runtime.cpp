@@ -694,7 +694,7 @@ static const struct {
     ABI_FIELD(anima_linear_desc, epilogue), ABI_FIELD(anima_linear_desc, gate), ABI_FIELD(anima_linear_desc, gate_off),
     ABI_FIELD(anima_linear_desc, acc_out), ABI_FIELD(anima_linear_desc, add), ABI_FIELD(anima_linear_desc, ld_add),
     ABI_FIELD(anima_linear_desc, lora_xa), ABI_FIELD(anima_linear_desc, ld_lora_xa), ABI_FIELD(anima_linear_desc, lora_b),
-    ABI_FIELD(anima_linear_desc, lora_r),
+    ABI_FIELD(anima_linear_desc, lora_r), ABI_FIELD(anima_linear_desc, lora_cols),
     ABI_SIZE(anima_sampler_desc), ABI_FIELD(anima_sampler_desc, kind), ABI_FIELD(anima_sampler_desc, n),
     ABI_FIELD(anima_sampler_desc, x), ABI_FIELD(anima_sampler_desc, v), ABI_FIELD(anima_sampler_desc, v_uncond),
     ABI_FIELD(anima_sampler_desc, cfg), ABI_FIELD(anima_sampler_desc, sigma), ABI_FIELD(anima_sampler_desc, final_step),

@@ -754,6 +754,7 @@ static napi_value js_linear(napi_env env, napi_callback_info info) {
   d.ld_lora_xa = (int64_t)pnum(env, o, "ldLoraXa");
   d.lora_b = (const uint16_t*)pptr(env, o, "loraB");
   d.lora_r = (int)pnum(env, o, "loraR");
+  d.lora_cols = (int)pnum(env, o, "loraCols");
   CHECK_RC(env, c, anima_linear(c, &d));
   return NULL;
 }

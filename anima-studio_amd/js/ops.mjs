@@ -83,7 +83,8 @@ export function linear(gpu, x, W, opts) {
   const d = { M, out: out.buf, ldc: o.ldc || 0, alpha: o.alpha || 0, act: ACT[o.act || "none"],
     epilogue: o.resid ? (o.gate ? 2 : 1) : 0, gate: ptr(o.gate), gOff: o.gOff || 0, accOut: ptr(o.accOut),
     add: delta ? delta.buf : 0, ldAdd: delta ? W.N : 0,
-    loraXa: down ? down.buf : 0, ldLoraXa: down ? F.R : 0, loraB: F ? F.Bs.buf : 0, loraR: F ? F.R : 0 };
+    loraXa: down ? down.buf : 0, ldLoraXa: down ? F.R : 0, loraB: F ? F.Bs.buf : 0, loraR: F ? F.Rb : 0,
+    loraCols: F ? F.cols : 0 };
   if (needsRotation(W) && o.xq) {
     d.xq = o.xq.q.buf;
     d.xs = o.xq.s.buf;
@@ -104,38 +105,44 @@ export function linear(gpu, x, W, opts) {
 }
 
 // The LoRA factors of a quantized weight for the GEMM epilogue (anima_linear_desc.lora_*): every
-// entry's A (and A H) stacked into [R, K] with R the summed ranks rounded up to 16 (zero rows
-// pad), and B as one [N, R] matrix whose rows n of entry e hold scale_e * B_e[n - off_e] in the
-// columns of e's ranks (zeros elsewhere), so that y += (A x_in)^T-row times B-row sums
-// sum_e scale_e B_e (A_e x_in) over the entries covering column n (ops.js:55-87).  Built at
-// attach time (B composed on the host from the device copies); owned by W, freed with its stack.
+// entry's A (and A H) stacked into [R, K], and B as one matrix whose row n holds scale_e *
+// B_e[n - off_e] in the columns of the ranks of the entries e covering column n (zeros elsewhere),
+// so that y += (A x_in)^T-row times B-row sums sum_e scale_e B_e (A_e x_in) over those entries
+// (ops.js:55-87).  When every entry covers one of the equal column blocks of a stacked weight
+// (q / k / v with their own LoRAs), the ranks are kept per block (lora_cols): block b's entries
+// fill ranks [b Rb, (b + 1) Rb) of the A stack, Rb their largest per-block sum rounded up to 16,
+// and B is [N, Rb] with each row holding only its block's ranks; otherwise one block of R = the
+// summed ranks rounded up to 16 (zero rows pad).  Built at attach time (B composed on the host
+// from the device copies); owned by W, freed with its stack.
 export function fuseLora(gpu, W) {
   releaseLoraFused(W);
   if (!W.lora || !W.lora.length || !needsRotation(W)) return null;
-  const R0 = W.lora.reduce((s, e) => s + e.r, 0), R = Math.ceil(R0 / 16) * 16, K = W.K, N = W.N;
+  const K = W.K, N = W.N, cols = W.lora[0].n;
+  const blocked = N > cols && N % cols === 0 && cols % 16 === 0 && W.lora.every((e) => e.n === cols && e.off % cols === 0);
+  const nb = blocked ? N / cols : 1, blk = (e) => (blocked ? e.off / cols : 0);
+  const used = new Array(nb).fill(0), start = new Map();
+  for (const e of W.lora) {
+    start.set(e, used[blk(e)]);
+    used[blk(e)] += e.r;
+  }
+  const Rb = Math.ceil(Math.max(...used) / 16) * 16, R = nb * Rb;
   const stack = (key) => {
     const A = gpu.empty([R, K]);
-    if (R > R0) zero(gpu, A);
-    let r0 = 0;
-    for (const e of W.lora) {
-      gpu.copy(A.at(r0 * K), e[key], e.r * K * 4);
-      r0 += e.r;
-    }
+    if (used.some((u) => u < Rb)) zero(gpu, A);
+    for (const e of W.lora) gpu.copy(A.at((blk(e) * Rb + start.get(e)) * K), e[key], e.r * K * 4);
     return A;
   };
   const A = stack("A"), Ar = W.lora.every((e) => e.Ar) ? stack("Ar") : null;
-  const Bh = new Float32Array(N * R);
-  let r0 = 0;
+  const Bh = new Float32Array(N * Rb);
   for (const e of W.lora) {
-    const b = new Float32Array(e.n * e.r);
+    const b = new Float32Array(e.n * e.r), c0 = start.get(e);
     native.d2h(gpu.ctx, e.B.buf, b);
     for (let i = 0; i < e.n; i++)
-      for (let j = 0; j < e.r; j++) Bh[(e.off + i) * R + r0 + j] = Math.fround(e.scale * b[i * e.r + j]);
-    r0 += e.r;
+      for (let j = 0; j < e.r; j++) Bh[(e.off + i) * Rb + c0 + j] = Math.fround(e.scale * b[i * e.r + j]);
   }
-  const Bf = gpu.fromArray(Bh, [N, R]);
+  const Bf = gpu.fromArray(Bh, [N, Rb]);
   W.loraFused = { A, Ar, As: splitPlanes(gpu, A, R * K), Ars: Ar ? splitPlanes(gpu, Ar, R * K) : null,
-    Bs: splitPlanes(gpu, Bf, N * R), R, lora: W.lora };
+    Bs: splitPlanes(gpu, Bf, N * Rb), R, Rb, cols: blocked ? cols : 0, lora: W.lora };
   Bf.release();
   return W.loraFused;
 }

@@ -405,11 +405,16 @@ typedef struct {
    * y += sum_k lora_xa[m*ld_lora_xa + k] * B[n][k] for k < lora_r, after the bias and before the
    * activation / gate, with lora_xa the A products (fp32 [M][ld_lora_xa]) and lora_b the three
    * bf16 planes [3][N][lora_r] (anima_split3_bf16) of B, every entry's scale folded into its
-   * columns.  lora_r % 16 == 0, ld_lora_xa % 4 == 0, both 16-byte aligned; not with `add`. */
+   * columns.  lora_r % 16 == 0, ld_lora_xa % 4 == 0, both 16-byte aligned; not with `add`.
+   * lora_cols > 0: block-diagonal ranks (a stacked q/k/v projection whose parts carry their own
+   * LoRAs): column n takes the lora_r ranks of its block, lora_xa columns (n / lora_cols) *
+   * lora_r + k, so lora_b is [3][N][lora_r] with only the block's own ranks; N % lora_cols == 0,
+   * lora_cols % 16 == 0, ld_lora_xa >= (N / lora_cols) * lora_r.  0: one block over all N. */
   const float* lora_xa;
   int64_t ld_lora_xa;
   const uint16_t* lora_b;
   int lora_r;
+  int lora_cols;
 } anima_linear_desc;
 
 /* ops.linear (app/gpu/ops.js:48-66) -> matmulShader (gemm.js:166-280):

@@ -514,14 +514,55 @@ def test_linear_lora_epilogue(ctx, M, epi, act):
     assert r <= 2e-6
 
 
+@pytest.mark.parametrize("M,N,cols", [(4000, 3072, 1024), (4000, 1152, 384), (200, 3072, 1024)])
+def test_linear_lora_block_diagonal(ctx, M, N, cols):
+    """Block-diagonal LoRA ranks (lora_cols: a stacked projection whose column blocks carry their
+    own ranks, e.g. q / k / v): column n adds xa[m, (n // cols) * R + k] * B[n, k], B holding only
+    each block's R = 32 ranks.  cols = 1024 runs the product inside the 256-tile kernel's
+    epilogue (a tile lies in one block); cols = 384 splits tiles and M = 200 runs the 128-tile
+    kernel, both taking the product as an add term, one split-bf16 product per block over its
+    rows of the B planes.  Against the oracle epilogue fed the float64 delta: rel-L2 <= 2e-6."""
+    case(f"linear LoRA block-diagonal M={M} N={N} cols={cols}")
+    m = amd()
+    K, R = 1024, 32
+    nb = N // cols
+    ld = nb * R + 4
+    x = orc.randn(241, M * K).reshape(M, K)
+    qx, sx = orc.token_quant(orc.hadamard256(x))
+    qw, sw = int8_weight(242, N, K)
+    gate = orc.randn(244, N).astype(np.float32)
+    resid = orc.randn(245, M * N).reshape(M, N)
+    xa = (0.5 * orc.randn(246, M * ld)).reshape(M, ld).astype(np.float32)
+    Bm = (0.05 * orc.randn(247, N * R)).reshape(N, R).astype(np.float32)
+    planes = ctx.empty(3 * N * R, np.uint16)
+    ctx.split3_bf16(ctx.upload(Bm), planes, N * R)
+    W = m.weight(m.W_I8, N, K, ctx.upload(qw), scale=ctx.upload(sw))
+    dout = ctx.upload(resid)
+    ctx.linear(W, M, dout, xq=ctx.upload(qx), xs=ctx.upload(sx), epilogue=m.EPI_GATED, gate=ctx.upload(gate),
+               lora_xa=ctx.upload(xa), ld_lora_xa=ld, lora_b=planes, lora_r=R, lora_cols=cols)
+    got = dout.numpy()
+    rows = np.unique(np.concatenate([np.arange(0, 4), np.random.default_rng(6).choice(M, 12, replace=False),
+                                     np.arange(M - 8, M)]))
+    delta = np.zeros((len(rows), N))
+    for b in range(nb):
+        c = slice(b * cols, (b + 1) * cols)
+        delta[:, c] = xa[rows, b * R:(b + 1) * R].astype(np.float64) @ Bm[c].astype(np.float64).T
+    ref = orc.linear_epilogue(orc.gemm_i8(qx[rows], qw), sx[rows], sw, epi=m.EPI_GATED, gate=gate, g_off=0,
+                              c=resid[rows], add=delta.astype(np.float32))
+    r, _ = report(f"LoRA block-diagonal M={M} cols={cols}", got[rows], ref)
+    assert r <= 2e-6
+
+
 def test_linear_lora_epilogue_refusals(ctx):
     """The LoRA factors are refused on the host: a rank that is not a multiple of 16 or an ld below
-    it (ANIMA_E_ARG), together with an add term or on a bf16 weight (ANIMA_E_UNSUPPORTED)."""
+    it, rank blocks that do not divide N or whose ranks do not fit the ld (ANIMA_E_ARG), together
+    with an add term or on a bf16 weight (ANIMA_E_UNSUPPORTED)."""
     case("linear LoRA epilogue refusals")
     m = amd()
     buf = ctx.empty(1 << 20)
     W = m.weight(m.W_I8, 64, 128, buf, scale=buf)
     for kw, code in ((dict(lora_r=40, ld_lora_xa=40), -1), (dict(lora_r=32, ld_lora_xa=16), -1),
+                     (dict(lora_r=32, ld_lora_xa=64, lora_cols=24), -1), (dict(lora_r=32, ld_lora_xa=32, lora_cols=32), -1),
                      (dict(lora_r=32, ld_lora_xa=32, add=buf, ld_add=64), -5)):
         with pytest.raises(m.AnimaError) as e:
             ctx.linear(W, 4, buf, xq=buf, xs=buf, lora_xa=buf, lora_b=buf, **kw)
