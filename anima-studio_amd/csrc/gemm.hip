@@ -1494,13 +1494,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_f32m_skinny_kernel(F32WArg
 // on both sides.  Output layouts and epilogues are those of the fp32 kernels.
 
 
-// Tall-skinny split product (the stacked LoRA A side, N <= 96, long K): 32 rows x 32 RT columns per
-// workgroup, eight waves over k with the fixed-order LDS tree of gemm_f32m_skinny_kernel.  The
-// 16x16x32 matrix-core shape: a wave's 32-k step is 2 row tiles x 2 RT column tiles, lane (r, g)
-// holding row (or column) r's k = 8 g .. 8 g + 7 on both operands.  One load instruction then
-// covers 16 rows x 64 contiguous bytes (x) or 16 rows x 64 bytes (a W plane): half the cache
-// lines per byte of the 32x32x16 layout (32 rows x 32 bytes), whose address path bounds the
-// kernel well below HBM rate (the product itself is a small share of the matrix-core time).
+// acc += sum_{i+j<=2} a_i b_j on the 16x16x32 bf16 shape, smallest terms first
 __device__ __forceinline__ f32x4 mfma16_s3(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f32x4 acc) {
   acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[1], acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[2], acc, 0, 0, 0);
@@ -1510,111 +1504,145 @@ __device__ __forceinline__ f32x4 mfma16_s3(const bf16x8 (&a)[3], const bf16x8 (&
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], acc, 0, 0, 0);
 }
 
+constexpr int TK_WAVES = 8;
+constexpr int TK_XB = 32 * 128;  // one wave's x step tile: 32 rows x 32 fp32
+
+// Per-lane DMA state of gemm_s3_tall_kernel: x instruction i covers rows 8 i .. 8 i + 7 of the wave
+// (lane -> row 8 i + lane / 8, piece slot lane % 8 holding k-piece (slot ^ row) % 8 of 4 fp32); W
+// instruction t covers plane t / CT, rows 16 (t % CT) .. + 15 (lane -> row + lane / 4, slot
+// lane % 4 holding k-piece slot ^ ((row / 2) % 4) of 8 bf16), issued by wave t % TK_WAVES.
 template <int RT>
-__global__ __launch_bounds__(64 * SK_WAVES) void gemm_s3_skinny_kernel(F32WArgs a) {
-  constexpr int CT = 2 * RT;  // 16-column tiles
-  __shared__ float part[SK_WAVES / 2 * 64 * 16 * RT];
+struct TallDma {
+  static constexpr int CT = 2 * RT, WI = (6 * RT + TK_WAVES - 1) / TK_WAVES;
+  __amdgpu_buffer_rsrc_t rx, rw;
+  int xo[4], xk[4], wo[WI], wk[WI];
+};
+
+// One step's copies into `buf` (restrict: the compiler then tells them apart from the operand
+// reads of the other buffer and does not make those reads wait for them).
+template <int RT>
+__device__ __forceinline__ void tall_issue(const TallDma<RT>& d, char* __restrict__ buf, int k0, int K, int wave) {
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rx, (lds_void_t*)(buf + wave * TK_XB + i * 1024), 16,
+                                             k0 + d.xk[i] < K ? d.xo[i] + 4 * k0 : 0x7ffffff0, 0, 0, 0);
+#pragma unroll
+  for (int j = 0; j < TallDma<RT>::WI; j++) {
+    const int t = wave + TK_WAVES * j;
+    if (t < 6 * RT)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rw, (lds_void_t*)(buf + TK_WAVES * TK_XB + t * 1024), 16,
+                                               k0 + d.wk[j] < K ? d.wo[j] + 2 * k0 : 0x7ffffff0, 0, 0, 0);
+  }
+}
+
+// One step's operand reads from `buf` and its products (lane (r16, g): x row 16 i + r16, W row
+// 16 t + r16, k = 8 g .. 8 g + 7 of the step on both operands).
+template <int RT>
+__device__ __forceinline__ void tall_step(const char* __restrict__ buf, int wave, int r16, int g, f32x4 (&acc)[2][2 * RT]) {
+  constexpr int CT = 2 * RT;
+  bf16x8 wv[CT][3];
+#pragma unroll
+  for (int t = 0; t < CT; t++) {
+    const int row = 16 * t + r16;
+#pragma unroll
+    for (int p = 0; p < 3; p++)
+      wv[t][p] = *(const bf16x8*)(buf + TK_WAVES * TK_XB + p * CT * 1024 + row * 64 + 16 * (g ^ ((row >> 1) & 3)));
+  }
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int row = 16 * i + r16;
+    const char* xr = buf + wave * TK_XB + row * 128;
+    // whole 16-byte reads: split into scalar loads and merged again, the reads lose the alias
+    // information that keeps them from waiting on the other buffer's copies
+    f32x4 v0 = *(const f32x4*)(xr + 16 * ((2 * g) ^ (row & 7)));
+    f32x4 v1 = *(const f32x4*)(xr + 16 * ((2 * g + 1) ^ (row & 7)));
+    asm volatile("" : "+v"(v0), "+v"(v1));
+    const float4 x0 = make_float4(v0[0], v0[1], v0[2], v0[3]), x1 = make_float4(v1[0], v1[1], v1[2], v1[3]);
+    bf16x8 xs[3];
+    split3(x0, x1, xs);
+#pragma unroll
+    for (int t = 0; t < CT; t++) acc[i][t] = mfma16_s3(xs, wv[t], acc[i][t]);
+  }
+}
+
+// k-sliced tall-skinny split product (the stacked LoRA A side over many rows): a workgroup is 8
+// waves x 32 rows (256 rows) over one slice of k, 32 k per step.  Both operands move HBM/L2 ->
+// LDS with `buffer_load ... lds`, lane-contiguous 16-byte pieces (whole cache lines per
+// instruction): x as each wave's 32 rows x 128 bytes, W as the step's 32 RT rows x 64 bytes of
+// each plane, loaded once per workgroup and read by all eight waves.  (Register loads straight
+// into the 16x16x32 operand layout touch 16-32 rows per instruction, one 16-byte access each,
+// which bounds that form by the vector memory address path at half the HBM rate.)  Pieces are
+// XOR-swizzled within their row so that the operand reads (8 lanes = 8 rows per 16-byte access)
+// hit distinct bank groups.  Up to four step buffers, one barrier per step.  Each slice writes its
+// partial sums [slice][M][N]; s3_ksum_kernel adds them in slice order (deterministic) and applies
+// the epilogue.  Offsets past a buffer's end read zeros: the k tail and rows past M.  A row of W
+// past N reads other rows' data (or zeros) and feeds only columns that are never stored.
+template <int RT>
+__global__ __launch_bounds__(64 * TK_WAVES) void gemm_s3_tall_kernel(F32WArgs a, float* part, int spb) {
+  constexpr int CT = 2 * RT;
+  constexpr int BUF = TK_WAVES * TK_XB + 3 * CT * 1024;
+  // step buffers: as many as fit in LDS (up to 4), so that up to TD - 1 steps' copies are in
+  // flight behind the one being computed
+  constexpr int TD = 160 * 1024 / BUF < 4 ? 160 * 1024 / BUF : 4;
+  __shared__ __attribute__((aligned(1024))) char smem[TD * BUF];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int r16 = lane & 15, g = lane >> 4;
-  const int m0 = blockIdx.y * 32, nb = blockIdx.x * 32 * RT;
-  // Raw buffer loads: an offset at or past the buffer's end reads zeros, which masks the k tail
-  // (and x's rows past M) without a select, and the loads are not plain LLVM loads, which the
-  // compiler would fold across the loop's back edge into the header (undoing the prefetch).  A
-  // row of W past N reads the next plane's data and feeds only columns that are never stored.
-  const int rows = a.M - m0 < 32 ? a.M - m0 : 32;
-  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.x + (int64_t)m0 * a.ldx), (short)0, rows * (int)a.ldx * 4, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)a.w, (short)0, (int)(2 * (2 * a.wplane + (int64_t)a.N * a.K)), 0x00020000);
-  const uint32_t plane2 = 2u * (uint32_t)a.wplane;  // bytes per plane
-  uint32_t xoff[2], woff[CT];
+  const int nb = blockIdx.x * 32 * RT, m0 = blockIdx.y * (32 * TK_WAVES) + wave * 32;
+  const int nst = (a.K + 31) / 32, s0 = blockIdx.z * spb, s1 = nst < s0 + spb ? nst : s0 + spb;
+  // (wave-uniform values taken to scalar registers: a buffer resource in vector registers would
+  // turn every load into a loop over the lanes' distinct values)
+  const int rows = __builtin_amdgcn_readfirstlane(a.M - m0 < 0 ? 0 : a.M - m0 < 32 ? a.M - m0 : 32);
+  const int mb = __builtin_amdgcn_readfirstlane(rows ? m0 : 0);
+  TallDma<RT> d;
+  d.rx = __builtin_amdgcn_make_buffer_rsrc((void*)(a.x + (int64_t)mb * a.ldx), (short)0, rows * (int)a.ldx * 4, 0x00020000);
+  d.rw = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)(2 * (2 * a.wplane + (int64_t)a.N * a.K)), 0x00020000);
 #pragma unroll
-  for (int t = 0; t < 2; t++) xoff[t] = 4u * ((uint32_t)(16 * t + r16) * (uint32_t)a.ldx + 8u * g);
+  for (int i = 0; i < 4; i++) {
+    const int row = 8 * i + (lane >> 3), c = (lane & 7) ^ (row & 7);
+    d.xk[i] = 4 * c;
+    d.xo[i] = (row * (int)a.ldx + 4 * c) * 4;
+  }
 #pragma unroll
-  for (int t = 0; t < CT; t++) woff[t] = 2u * ((uint32_t)(nb + 16 * t + r16) * (uint32_t)a.K + 8u * g);
+  for (int j = 0; j < TallDma<RT>::WI; j++) {
+    const int t = wave + TK_WAVES * j, tt = t < 6 * RT ? t : 0;
+    const int p = tt / CT, row = 16 * (tt % CT) + (lane >> 2), c = (lane & 3) ^ ((row >> 1) & 3);
+    d.wk[j] = 8 * c;
+    const int64_t o = p * 2 * a.wplane + ((int64_t)(nb + row) * a.K + 8 * c) * 2;
+    d.wo[j] = o < 0x7ffffff0 ? (int)o : 0x7ffffff0;  // (past the end: reads zeros)
+  }
   f32x4 acc[2][CT];
 #pragma unroll
   for (int i = 0; i < 2; i++)
 #pragma unroll
     for (int t = 0; t < CT; t++) acc[i][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  const int nst = (a.K + 31) / 32;
-  // one 32-k step; the next step's loads are issued before this step's MFMAs
-#define S3_LOAD(ST, VALID, XV, WV)                                                               \
-  {                                                                                              \
-    const int kb_ = 32 * (ST);                                                                   \
-    const bool ok_ = (VALID) && kb_ + 8 * g < a.K; /* K % 8 == 0: 8 values all in or out */      \
-    _Pragma("unroll") for (int i = 0; i < 2; i++) {                                              \
-      const uint32_t xo_ = ok_ ? xoff[i] + 4u * kb_ : 0x80000000u;                               \
-      XV[i][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo_, 0, 0)); \
-      XV[i][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo_ + 16u, 0, 0)); \
-    }                                                                                            \
-    _Pragma("unroll") for (int t = 0; t < CT; t++)                                               \
-    _Pragma("unroll") for (int p = 0; p < 3; p++) WV[t][p] = __builtin_bit_cast(bf16x8,          \
-        __builtin_amdgcn_raw_buffer_load_b128(rw, ok_ ? woff[t] + p * plane2 + 2u * kb_ : 0x80000000u, 0, 0)); \
-  }
-#define S3_MMA(XV, WV)                                                                           \
-  {                                                                                              \
-    _Pragma("unroll") for (int i = 0; i < 2; i++) {                                              \
-      bf16x8 xs_[3];                                                                             \
-      split3(XV[i][0], XV[i][1], xs_);                                                           \
-      _Pragma("unroll") for (int t = 0; t < CT; t++) acc[i][t] = mfma16_s3(xs_, WV[t], acc[i][t]); \
-    }                                                                                            \
-  }
-  // Wave w takes the contiguous steps [w * per, w * per + cnt), starting at a per-block rotation:
-  // concurrent loads spread over the row length instead of every wave of the grid reading the
-  // same window of every row.
-  const int per = (nst + SK_WAVES - 1) / SK_WAVES, s0 = wave * per;
-  const int cnt = nst - s0 < per ? nst - s0 : per;
-  if (cnt > 0) {
-    const int rot = (int)(blockIdx.y % (unsigned)cnt);
-#define S3_STEP(I) (s0 + ((I) + rot < cnt ? (I) + rot : (I) + rot - cnt))
-    float4 xa[2][2], xb[2][2];
-    bf16x8 wa[CT][3], wb[CT][3];
-    // Steps in pairs, one basic block per pair: each half issues the other buffer's loads before
-    // its own MFMAs, and no branch separates a load from its use (which would let the compiler
-    // sink the load next to that use).  An odd count ends on a zero-read repeat of the last step;
-    // the final prefetch is never used.  The scheduling barriers keep each load group above the
-    // other buffer's MFMAs (left alone, the scheduler moves loads down next to their uses).
-    S3_LOAD(S3_STEP(0), true, xa, wa)
-    for (int i = 0; i < cnt; i += 2) {
-      S3_LOAD(S3_STEP(i + 1 < cnt ? i + 1 : i), i + 1 < cnt, xb, wb)
-      __builtin_amdgcn_sched_barrier(0);
-      S3_MMA(xa, wa)
-      __builtin_amdgcn_sched_barrier(0);
-      S3_LOAD(S3_STEP(i + 2 < cnt ? i + 2 : cnt - 1), i + 2 < cnt, xa, wa)
-      __builtin_amdgcn_sched_barrier(0);
-      S3_MMA(xb, wb)
-      __builtin_amdgcn_sched_barrier(0);
+  // Copies issued by this wave per step: 4 of x and its share of the 6 RT of W (waves below
+  // (6 RT) % 8, or all when it is 0, take one more).  Steps s0 .. s0 + TD - 2 are issued up front
+  // and step st + TD - 1 after the barrier of step st, so before step st the TD - 2 steps after it
+  // are in flight (once they exist) and may stay so: vmcnt((TD - 2) * per-step count), vmcnt(0)
+  // in the last steps of the slice.
+  constexpr int WHI = (6 * RT) % TK_WAVES ? (6 * RT) % TK_WAVES : TK_WAVES;
+  constexpr int CHI = 4 + TallDma<RT>::WI, NHI = (TD - 2) * CHI, NLO = (TD - 2) * (CHI - 1);
+  static_assert(TD >= 2, "two step buffers at least");
+  static_assert(NHI < 64, "vmcnt field");
+  for (int i = 0; i < TD - 1; i++)
+    if (s0 + i < s1) tall_issue<RT>(d, smem + i * BUF, 32 * (s0 + i), a.K, wave);
+  for (int st = s0; st < s1; st++) {
+    if (st + TD - 1 <= s1) {  // steps st + 1 .. st + TD - 2 all exist (and are issued)
+      if (wave < WHI) __builtin_amdgcn_s_waitcnt((NHI & 15) | (7 << 4) | (15 << 8) | ((NHI >> 4) << 14));
+      else __builtin_amdgcn_s_waitcnt((NLO & 15) | (7 << 4) | (15 << 8) | ((NLO >> 4) << 14));
+    } else {
+      __builtin_amdgcn_s_waitcnt((15 << 8) | (7 << 4));  // vmcnt(0)
     }
-#undef S3_STEP
+    // every wave's copies of step st have landed, and every wave is done reading step st - 1's
+    // buffer, which step st + TD - 1 then refills
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const int nx = st + TD - 1;
+    if (nx < s1) tall_issue<RT>(d, smem + ((nx - s0) % TD) * BUF, 32 * nx, a.K, wave);
+    tall_step<RT>(smem + ((st - s0) % TD) * BUF, wave, r16, g, acc);
   }
-#undef S3_LOAD
-#undef S3_MMA
-  // fixed-order tree: waves [h, 2h) hand their sums to waves [0, h), h = 4, 2, 1
-#pragma unroll
-  for (int h = SK_WAVES / 2; h >= 1; h >>= 1) {
-    if (wave >= h && wave < 2 * h) {
-#pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int t = 0; t < CT; t++)
-#pragma unroll
-          for (int r = 0; r < 4; r++) part[((((wave - h) * 2 + i) * CT + t) * 4 + r) * 64 + lane] = acc[i][t][r];
-    }
-    __syncthreads();
-    if (wave < h) {
-#pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int t = 0; t < CT; t++)
-#pragma unroll
-          for (int r = 0; r < 4; r++)
-            acc[i][t][r] = acc[i][t][r] + part[(((wave * 2 + i) * CT + t) * 4 + r) * 64 + lane];
-    }
-    __syncthreads();
-  }
-  if (wave > 0) return;
   // lane (r16, g) holds rows 16 i + 4 g + r of column tile t's column r16
+  float* pp = part + (int64_t)blockIdx.z * a.M * a.N;
 #pragma unroll
   for (int t = 0; t < CT; t++) {
     const int n = nb + 16 * t + r16;
@@ -1623,18 +1651,28 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_s3_skinny_kernel(F32WArgs 
     for (int i = 0; i < 2; i++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const int mm = m0 + 16 * i + 4 * g + r;
-        if (mm >= a.M) continue;
-        float v = acc[i][t][r] * a.alpha;
-        if (a.bias) v = v + a.bias[n];
-        if (a.add) v = v + a.add[(int64_t)mm * a.ld_add + n];
-        v = apply_act(v, a.act);
-        float* c = a.out + (int64_t)mm * a.ldc + n;
-        if (a.epi == ANIMA_EPI_STORE) *c = v;
-        else if (a.epi == ANIMA_EPI_RESID) *c = *c + v;
-        else *c = __builtin_fmaf(a.gate[a.gate_off + n], v, *c);
+        const int m = m0 + 16 * i + 4 * g + r;
+        if (m < a.M) pp[(int64_t)m * a.N + n] = acc[i][t][r];
       }
   }
+}
+
+// The slices' partial sums added in slice order, then alpha, bias, add, activation and the store /
+// residual / gated epilogue of the split-weight kernels.
+__global__ __launch_bounds__(256) void s3_ksum_kernel(F32WArgs a, const float* part, int ks) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x, mn = (int64_t)a.M * a.N;
+  if (i >= mn) return;
+  const int m = (int)(i / a.N), n = (int)(i - (int64_t)m * a.N);
+  float v = part[i];
+  for (int s = 1; s < ks; s++) v = v + part[s * mn + i];
+  v = v * a.alpha;
+  if (a.bias) v = v + a.bias[n];
+  if (a.add) v = v + a.add[(int64_t)m * a.ld_add + n];
+  v = apply_act(v, a.act);
+  float* c = a.out + (int64_t)m * a.ldc + n;
+  if (a.epi == ANIMA_EPI_STORE) *c = v;
+  else if (a.epi == ANIMA_EPI_RESID) *c = *c + v;
+  else *c = __builtin_fmaf(a.gate[a.gate_off + n], v, *c);
 }
 
 // Split product with the operands swapped (the LoRA B side, K = rank): the C^T layout and 16-byte
@@ -2067,14 +2105,29 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d, int64_t s3_plane) {
                (int)M, N, K, 0, 0, 0, 0, d->add, ld_add, 0};
     f.wplane = s3_plane ? s3_plane : (int64_t)N * K;
     Launch L(c, "gemm.f32s3", 2.0 * M * N * K, 0.0);
-    // the skinny kernel's buffer offsets are 32-bit: 32 rows of x and the three planes of W;
+    // the tall kernel's buffer offsets are 32-bit: 32 rows of x and the three planes of W;
     // N in (96, 256] runs as 64-column workgroups
-    const bool skf = K >= 512 && ldx < (1 << 23) && 2 * (2 * f.wplane + (int64_t)N * K) < (1LL << 31) && N <= 256;
-    const int srt = N <= 32 ? 1 : N <= 64 || N > 96 ? 2 : 3;
-    const dim3 sk((unsigned)((N + 32 * srt - 1) / (32 * srt)), (unsigned)((M + 31) / 32)), blk(64 * SK_WAVES);
-    if (skf && srt == 1) hipLaunchKernelGGL(gemm_s3_skinny_kernel<1>, sk, blk, 0, c->stream, f);
-    else if (skf && srt == 2) hipLaunchKernelGGL(gemm_s3_skinny_kernel<2>, sk, blk, 0, c->stream, f);
-    else if (skf) hipLaunchKernelGGL(gemm_s3_skinny_kernel<3>, sk, blk, 0, c->stream, f);
+    const bool skf = K >= 512 && ldx < (1 << 23) && 2 * (2 * f.wplane + (int64_t)N * K) < (1LL << 31) - 64 && N <= 256;
+    if (skf) {
+      // k-slices so that the grid gives every CU about one workgroup, each slice at least 4 steps
+      const int srt = N <= 32 ? 1 : N <= 64 || N > 96 ? 2 : 3;
+      const int cb = (N + 32 * srt - 1) / (32 * srt), rb = (int)((M + 32 * TK_WAVES - 1) / (32 * TK_WAVES));
+      const int nst = (K + 31) / 32;
+      int ks = (c->num_cus + cb * rb - 1) / (cb * rb);
+      ks = ks < nst / 4 ? ks : nst / 4;
+      ks = ks < 1 ? 1 : ks;
+      const int spb = (nst + ks - 1) / ks;
+      ks = (nst + spb - 1) / spb;
+      void* pt = nullptr;
+      if (int rc = anima_alloc(c, (size_t)ks * M * N * 4, &pt)) return rc;
+      const dim3 tg((unsigned)cb, (unsigned)rb, (unsigned)ks), blk(64 * TK_WAVES);
+      if (srt == 1) hipLaunchKernelGGL(gemm_s3_tall_kernel<1>, tg, blk, 0, c->stream, f, (float*)pt, spb);
+      else if (srt == 2) hipLaunchKernelGGL(gemm_s3_tall_kernel<2>, tg, blk, 0, c->stream, f, (float*)pt, spb);
+      else hipLaunchKernelGGL(gemm_s3_tall_kernel<3>, tg, blk, 0, c->stream, f, (float*)pt, spb);
+      hipLaunchKernelGGL(s3_ksum_kernel, dim3((unsigned)((M * N + 255) / 256)), dim3(256), 0, c->stream, f,
+                         (const float*)pt, ks);
+      anima_free(c, pt);
+    }
     else if (N % 4 == 0 && ldc % 4 == 0 && al(d->out, 16) && (!W->bias || al(W->bias, 16)) &&
              (!d->add || (al(d->add, 16) && ld_add % 4 == 0)) &&
              (d->epilogue != ANIMA_EPI_GATED || al(d->gate + d->gate_off, 16)))
