@@ -434,11 +434,15 @@ class Context:
         return self._check(lib().anima_linear(self.h, ctypes.byref(d)))
 
     def linear_qkv(self, W, M, out, *, B, L, H, k_norm, rope_cs, rope_sin_off, kv_prep, eps=1e-6, x=None, ldx=0,
-                   x_rotated=True, xq=None, xs=None, ldc=0, alpha=0.0):
+                   x_rotated=True, xq=None, xs=None, ldc=0, alpha=0.0, lora_xa=None, ld_lora_xa=0, lora_b=None,
+                   lora_r=0, lora_cols=0):
         """anima_linear_qkv: the stacked QKV projection writing Q (fp32) to out and K / V in the
-        attention's bf16 operand layout to kv_prep (sized by attention_kv_bytes(B, H, L, bf16))."""
+        attention's bf16 operand layout to kv_prep (sized by attention_kv_bytes(B, H, L, bf16));
+        lora_*: the LoRA factors as for linear(), added before the K / V conversion."""
         d = LinearDesc(M=M, W=ctypes.pointer(W), x=_ptr(x), ldx=ldx, x_rotated=int(x_rotated), xq=_ptr(xq),
-                       xs=_ptr(xs), out=_ptr(out), ldc=ldc, alpha=alpha, act=0, epilogue=EPI_STORE)
+                       xs=_ptr(xs), out=_ptr(out), ldc=ldc, alpha=alpha, act=0, epilogue=EPI_STORE,
+                       lora_xa=_ptr(lora_xa), ld_lora_xa=ld_lora_xa, lora_b=_ptr(lora_b), lora_r=lora_r,
+                       lora_cols=lora_cols)
         p = QkvDesc(B=B, L=L, H=H, k_norm=_ptr(k_norm), rope_cs=_ptr(rope_cs), rope_sin_off=rope_sin_off, eps=eps,
                     kv_prep=_ptr(kv_prep), kv_prep_bytes=self.attention_kv_bytes(B, H, L, PREC_BF16))
         return self._check(lib().anima_linear_qkv(self.h, ctypes.byref(d), ctypes.byref(p)))

@@ -323,10 +323,9 @@ __device__ __forceinline__ void epi_load_c(const GemmArgs& a, int m, int n, f32x
 // per tile (mfma_s3) add sum_k lx[m][k] * B[n][k] onto y, so that one load latency per slice is
 // exposed, not one per tile; (3) activation and store / residual / gate as in epi_store_t.
 // Every lane takes part in the MFMAs (rows past M and columns past N read zeros).
-template <int EPI>
-__device__ __forceinline__ void lora_epilogue(const GemmArgs& a, const i32x16 (&acc)[4][2], int m0, int n0, int hf,
-                                              int lq, const float (&sxv)[4]) {
-  f32x16 y[4][2];
+template <int BSTEP>
+__device__ __forceinline__ void lora_y(const GemmArgs& a, const i32x16 (&acc)[4][2], int m0, int n0, int hf, int lq,
+                                       const float (&sxv)[4], f32x16 (&y)[4][2]) {
   if (a.acc_out) {  // the raw accumulators first: acc is dead once y is formed
 #pragma unroll
     for (int j = 0; j < 2; j++)
@@ -334,7 +333,7 @@ __device__ __forceinline__ void lora_epilogue(const GemmArgs& a, const i32x16 (&
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-          const int m = m0 + 32 * i, nq = n0 + 32 * j + 8 * q;
+          const int m = m0 + 32 * i, nq = n0 + BSTEP * j + 8 * q;
           if (m < a.M && nq < a.N)
 #pragma unroll
             for (int e = 0; e < 4; e++) a.acc_out[(int64_t)m * a.N + nq + e] = acc[i][j][4 * q + e];
@@ -343,10 +342,10 @@ __device__ __forceinline__ void lora_epilogue(const GemmArgs& a, const i32x16 (&
 #pragma unroll
   for (int j = 0; j < 2; j++) {
     EpiCols c;
-    epi_cols(a, n0 + 32 * j, c);
+    epi_cols(a, n0 + BSTEP * j, c);
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      const int nq = n0 + 32 * j + 8 * q;
+      const int nq = n0 + BSTEP * j + 8 * q;
       const bool ok = nq < a.N;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -373,7 +372,7 @@ __device__ __forceinline__ void lora_epilogue(const GemmArgs& a, const i32x16 (&
     float4 xr[4][2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-      const int nr = n0 - 4 * hf + 32 * j + lq;
+      const int nr = n0 - 4 * hf + BSTEP * j + lq;
       const bool nok = nr < a.N;
       const uint16_t* bp = a.lb + (int64_t)(nok ? nr : 0) * a.lr + 8 * hf + k0;
 #pragma unroll
@@ -395,6 +394,11 @@ __device__ __forceinline__ void lora_epilogue(const GemmArgs& a, const i32x16 (&
       for (int j = 0; j < 2; j++) y[i][j] = mfma_s3(bv[j], xv, y[i][j]);
     }
   }
+}
+
+// Phase (3) of the LoRA epilogue: activation and store / residual / gate of y.
+template <int EPI, int BSTEP>
+__device__ __forceinline__ void lora_store(const GemmArgs& a, const f32x16 (&y)[4][2], int m0, int n0) {
 #pragma unroll
   for (int j = 0; j < 2; j++)
 #pragma unroll
@@ -407,7 +411,7 @@ __device__ __forceinline__ void lora_epilogue(const GemmArgs& a, const i32x16 (&
       float* orow = a.out + (int64_t)m * a.ldc;
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const int nq = n0 + 32 * j + 8 * q;
+        const int nq = n0 + BSTEP * j + 8 * q;
         if (nq >= a.N) continue;
         f32x4 yq = {y[i][j][4 * q], y[i][j][4 * q + 1], y[i][j][4 * q + 2], y[i][j][4 * q + 3]};
         if (a.act == ANIMA_ACT_GELU) {
@@ -433,6 +437,14 @@ __device__ __forceinline__ void lora_epilogue(const GemmArgs& a, const i32x16 (&
         *(f32x4*)(orow + nq) = o;
       }
     }
+}
+
+template <int EPI>
+__device__ __forceinline__ void lora_epilogue(const GemmArgs& a, const i32x16 (&acc)[4][2], int m0, int n0, int hf,
+                                              int lq, const float (&sxv)[4]) {
+  f32x16 y[4][2];
+  lora_y<32>(a, acc, m0, n0, hf, lq, sxv, y);
+  lora_store<EPI, 32>(a, y, m0, n0);
 }
 
 template <int EPI>
@@ -510,8 +522,10 @@ __device__ __forceinline__ f32x4 kv_epi_y(const GemmArgs& a, const i32x16& v, in
   return y;
 }
 
-__device__ __forceinline__ void kv_epi_k(const GemmArgs& a, const i32x16 (&acc)[4][2], int m0, int n0, int col0,
-                                         int wave, int hf, int lq, const float (&sxv)[4], float* xch) {
+// yf(i, j, q): the fp32 store values of row group i, column group j (+ 64 j), quad q.
+template <class YF>
+__device__ __forceinline__ void kv_epi_k(const GemmArgs& a, const YF& yf, int m0, int n0, int col0, int wave, int hf,
+                                         int lq, float* xch) {
   const int grp = (wave >> 1) & 1;
   const int c0 = 32 * grp + 4 * hf;  // this lane's first column within the head (< 64)
   const int head = (col0 - a.kcol) / HD_K + (wave >> 2);
@@ -525,7 +539,7 @@ __device__ __forceinline__ void kv_epi_k(const GemmArgs& a, const i32x16 (&acc)[
     for (int j = 0; j < 2; j++)
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const f32x4 y = kv_epi_y(a, acc[i][j], q, sxv[i], n0 + 64 * j);
+        const f32x4 y = yf(i, j, q);
 #pragma unroll
         for (int e = 0; e < 4; e++) lf[q] = __builtin_fmaf(y[e], y[e], lf[q]);
       }
@@ -548,7 +562,7 @@ __device__ __forceinline__ void kv_epi_k(const GemmArgs& a, const i32x16 (&acc)[
     for (int q = 0; q < 4; q++) {
       const f32x4 cv = *(const f32x4*)(crow + 8 * q), sv = *(const f32x4*)(crow + a.sin_off + 8 * q);
       const f32x4 w0 = *(const f32x4*)(a.kn + c0 + 8 * q), w1 = *(const f32x4*)(a.kn + c0 + 64 + 8 * q);
-      const f32x4 y0 = kv_epi_y(a, acc[i][0], q, sxv[i], n0), y1 = kv_epi_y(a, acc[i][1], q, sxv[i], n0 + 64);
+      const f32x4 y0 = yf(i, 0, q), y1 = yf(i, 1, q);
       bf16x4 lo, hi;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -567,8 +581,9 @@ __device__ __forceinline__ void kv_epi_k(const GemmArgs& a, const i32x16 (&acc)[
 // each pair of lanes lq, lq ^ 1 (tokens 2t, 2t + 1: adjacent in the key order too) trades
 // columns and stores 4-byte token pairs, the even lane those of columns e = 0, 1, the odd lane
 // e = 2, 3.  Key order of V^T within each 16-key group: keys 0-3, 8-11, 4-7, 12-15.
-__device__ __forceinline__ void kv_epi_v(const GemmArgs& a, const i32x16 (&acc)[4][2], int m0, int n0, int col0, int wave,
-                                         int hf, int lq, const float (&sxv)[4]) {
+template <class YF>
+__device__ __forceinline__ void kv_epi_v(const GemmArgs& a, const YF& yf, int m0, int n0, int col0, int wave, int hf,
+                                         int lq) {
   const int c0 = 32 * ((wave >> 1) & 1) + 4 * hf;
   const int head = (col0 - a.vcol) / HD_K + (wave >> 2);
   const bool odd = lq & 1;
@@ -583,7 +598,7 @@ __device__ __forceinline__ void kv_epi_v(const GemmArgs& a, const i32x16 (&acc)[
     for (int j = 0; j < 2; j++) {
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const f32x4 y = kv_epi_y(a, acc[i][j], q, sxv[i], n0 + 64 * j);
+        const f32x4 y = yf(i, j, q);
         // own bf16 pairs: columns (e0, e1) and (e2, e3)
         const uint32_t p01 = (uint32_t)__builtin_bit_cast(uint16_t, (bf16)y[0]) |
                              ((uint32_t)__builtin_bit_cast(uint16_t, (bf16)y[1]) << 16);
@@ -652,7 +667,6 @@ constexpr int G2_LUT = G2_NST * G2_ST;  // W4 table offset in LDS (256 x 16 byte
 template <int EPI, bool W4, bool KV = false, bool LORA = false>
 __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
   static_assert(!KV || EPI == ANIMA_EPI_STORE, "the attention operand epilogue stores");
-  static_assert(!(KV && LORA), "the LoRA term goes through the plain epilogues");
   __shared__ __attribute__((aligned(1024))) char smem[G2_NST * G2_ST + (W4 ? 4096 : 0) + (KV ? 4096 : 0)];
   // the wave index is uniform: in a scalar register, so copy offsets derived from it stay scalar
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -960,19 +974,33 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
       float sxv[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) sxv[i] = m0 + 32 * i < a.M ? a.sx[m0 + 32 * i] : 0.0f;
-      if (col0 < a.kcol) {
-        EpiCols cc;
-        const f32x4 none[4] = {};
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-          epi_cols(a, n0 + 64 * j, cc);
-#pragma unroll
-          for (int i = 0; i < 4; i++) epi_store_t<ANIMA_EPI_STORE>(a, acc[i][j], m0 + 32 * i, n0 + 64 * j, sxv[i], cc, none);
-        }
-      } else if (col0 < a.vcol) {
-        kv_epi_k(a, acc, m0, n0, col0, wave, hf, lq, sxv, (float*)(smem + G2_NST * G2_ST + (W4 ? 4096 : 0)));
+      if constexpr (LORA) {
+        // y with the LoRA term (the column groups are 64 apart in this layout), then the same
+        // Q store / K / V conversions on y
+        f32x16 y[4][2];
+        lora_y<64>(a, acc, m0, n0, hf, lq, sxv, y);
+        const auto yf = [&](int i, int j, int q) {
+          return f32x4{y[i][j][4 * q], y[i][j][4 * q + 1], y[i][j][4 * q + 2], y[i][j][4 * q + 3]};
+        };
+        if (col0 < a.kcol) lora_store<ANIMA_EPI_STORE, 64>(a, y, m0, n0);
+        else if (col0 < a.vcol) kv_epi_k(a, yf, m0, n0, col0, wave, hf, lq, (float*)(smem + G2_NST * G2_ST + (W4 ? 4096 : 0)));
+        else kv_epi_v(a, yf, m0, n0, col0, wave, hf, lq);
       } else {
-        kv_epi_v(a, acc, m0, n0, col0, wave, hf, lq, sxv);
+        const auto yf = [&](int i, int j, int q) { return kv_epi_y(a, acc[i][j], q, sxv[i], n0 + 64 * j); };
+        if (col0 < a.kcol) {
+          EpiCols cc;
+          const f32x4 none[4] = {};
+#pragma unroll
+          for (int j = 0; j < 2; j++) {
+            epi_cols(a, n0 + 64 * j, cc);
+#pragma unroll
+            for (int i = 0; i < 4; i++) epi_store_t<ANIMA_EPI_STORE>(a, acc[i][j], m0 + 32 * i, n0 + 64 * j, sxv[i], cc, none);
+          }
+        } else if (col0 < a.vcol) {
+          kv_epi_k(a, yf, m0, n0, col0, wave, hf, lq, (float*)(smem + G2_NST * G2_ST + (W4 ? 4096 : 0)));
+        } else {
+          kv_epi_v(a, yf, m0, n0, col0, wave, hf, lq);
+        }
       }
 #pragma unroll
       for (int i = 0; i < 4; i++)
@@ -1658,21 +1686,48 @@ __global__ __launch_bounds__(64 * TK_WAVES) void gemm_s3_tall_kernel(F32WArgs a,
 }
 
 // The slices' partial sums added in slice order, then alpha, bias, add, activation and the store /
-// residual / gated epilogue of the split-weight kernels.
+// residual / gated epilogue of the split-weight kernels; four consecutive (flat [M][N]) outputs
+// per thread with 16-byte partial reads, every slice's read issued before the sums (element by
+// element when M * N % 4 != 0).
 __global__ __launch_bounds__(256) void s3_ksum_kernel(F32WArgs a, const float* part, int ks) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x, mn = (int64_t)a.M * a.N;
-  if (i >= mn) return;
-  const int m = (int)(i / a.N), n = (int)(i - (int64_t)m * a.N);
-  float v = part[i];
-  for (int s = 1; s < ks; s++) v = v + part[s * mn + i];
-  v = v * a.alpha;
-  if (a.bias) v = v + a.bias[n];
-  if (a.add) v = v + a.add[(int64_t)m * a.ld_add + n];
-  v = apply_act(v, a.act);
-  float* c = a.out + (int64_t)m * a.ldc + n;
-  if (a.epi == ANIMA_EPI_STORE) *c = v;
-  else if (a.epi == ANIMA_EPI_RESID) *c = *c + v;
-  else *c = __builtin_fmaf(a.gate[a.gate_off + n], v, *c);
+  const int64_t i4 = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x), mn = (int64_t)a.M * a.N;
+  if (i4 >= mn) return;
+  constexpr int KSM = 16;
+  f32x4 v;
+  if (mn % 4 == 0) {  // (every slice's plane then starts 16-byte aligned)
+    f32x4 pv[KSM];
+#pragma unroll
+    for (int s = 0; s < KSM; s++)
+      if (s < ks) pv[s] = *(const f32x4*)(part + s * mn + i4);
+    v = pv[0];
+#pragma unroll
+    for (int s = 1; s < KSM; s++)
+      if (s < ks) v = v + pv[s];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      float t = 0.0f;
+      if (i4 + e < mn) {
+        t = part[i4 + e];
+        for (int s = 1; s < ks; s++) t = t + part[s * mn + i4 + e];
+      }
+      v[e] = t;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const int64_t idx = i4 + e;
+    if (idx >= mn) break;
+    const int m = (int)(idx / a.N), n = (int)(idx - (int64_t)m * a.N);
+    float r = v[e] * a.alpha;
+    if (a.bias) r = r + a.bias[n];
+    if (a.add) r = r + a.add[(int64_t)m * a.ld_add + n];
+    r = apply_act(r, a.act);
+    float* c = a.out + (int64_t)m * a.ldc + n;
+    if (a.epi == ANIMA_EPI_STORE) *c = r;
+    else if (a.epi == ANIMA_EPI_RESID) *c = *c + r;
+    else *c = __builtin_fmaf(a.gate[a.gate_off + n], r, *c);
+  }
 }
 
 // Split product with the operands swapped (the LoRA B side, K = rank): the C^T layout and 16-byte
@@ -2115,7 +2170,7 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d, int64_t s3_plane) {
       const int nst = (K + 31) / 32;
       int ks = (c->num_cus + cb * rb - 1) / (cb * rb);
       ks = ks < nst / 4 ? ks : nst / 4;
-      ks = ks < 1 ? 1 : ks;
+      ks = ks < 1 ? 1 : ks > 16 ? 16 : ks;  // (the sum pass holds up to 16 slices)
       const int spb = (nst + ks - 1) / ks;
       ks = (nst + spb - 1) / spb;
       void* pt = nullptr;
@@ -2124,7 +2179,7 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d, int64_t s3_plane) {
       if (srt == 1) hipLaunchKernelGGL(gemm_s3_tall_kernel<1>, tg, blk, 0, c->stream, f, (float*)pt, spb);
       else if (srt == 2) hipLaunchKernelGGL(gemm_s3_tall_kernel<2>, tg, blk, 0, c->stream, f, (float*)pt, spb);
       else hipLaunchKernelGGL(gemm_s3_tall_kernel<3>, tg, blk, 0, c->stream, f, (float*)pt, spb);
-      hipLaunchKernelGGL(s3_ksum_kernel, dim3((unsigned)((M * N + 255) / 256)), dim3(256), 0, c->stream, f,
+      hipLaunchKernelGGL(s3_ksum_kernel, dim3((unsigned)(((M * N + 3) / 4 + 255) / 256)), dim3(256), 0, c->stream, f,
                          (const float*)pt, ks);
       anima_free(c, pt);
     }
@@ -2366,8 +2421,17 @@ int linear_qkv_launch(anima_ctx* c, const anima_linear_desc* d, const anima_qkv_
   if (p->L % 64) return fail(c, ANIMA_E_UNSUPPORTED, "anima_linear_qkv: L=%d must be a multiple of 64", p->L);
   if (N != 3 * H * HD_K || K % GBK)
     return fail(c, ANIMA_E_ARG, "anima_linear_qkv: N=%d must be 3 * H * 128 = %d, K %% %d == 0", N, 3 * H * HD_K, GBK);
-  if (d->epilogue != ANIMA_EPI_STORE || d->act != ANIMA_ACT_NONE || d->add || d->acc_out || d->lora_xa || d->lora_b || d->lora_r)
-    return fail(c, ANIMA_E_UNSUPPORTED, "anima_linear_qkv: plain store only (no activation, residual, gate, add term, LoRA or acc_out)");
+  if (d->epilogue != ANIMA_EPI_STORE || d->act != ANIMA_ACT_NONE || d->add || d->acc_out)
+    return fail(c, ANIMA_E_UNSUPPORTED, "anima_linear_qkv: plain store only (no activation, residual, gate, add term or acc_out)");
+  const bool lora = d->lora_xa || d->lora_b || d->lora_r;
+  if (lora) {
+    if (!d->lora_xa || !d->lora_b || d->lora_r < 16 || d->lora_r % 16 || d->ld_lora_xa % 4 || !al(d->lora_xa, 16) ||
+        !al(d->lora_b, 16) || d->lora_cols < 0 || (d->lora_cols && (N % d->lora_cols || d->lora_cols % 256)) ||
+        d->ld_lora_xa < (int64_t)d->lora_r * (d->lora_cols ? N / d->lora_cols : 1))
+      return fail(c, ANIMA_E_ARG, "anima_linear_qkv: LoRA factors need lora_r %% 16 == 0 (%d), lora_cols 0 or a divisor of N "
+                  "that is a multiple of 256 (%d), ld_lora_xa %% 4 == 0 covering the ranks (%lld), 16-byte aligned",
+                  d->lora_r, d->lora_cols, (long long)d->ld_lora_xa);
+  }
   if (!p->k_norm || !p->rope_cs || !p->kv_prep)
     return fail(c, ANIMA_E_ARG, "anima_linear_qkv: k_norm, rope_cs and kv_prep are required");
   if (p->kv_prep_bytes != attention_kv_bytes(p->B, H, p->L, ANIMA_PREC_BF16))
@@ -2420,10 +2484,18 @@ int linear_qkv_launch(anima_ctx* c, const anima_linear_desc* d, const anima_qkv_
   g.H = H;
   g.kcol = H * HD_K;
   g.vcol = 2 * H * HD_K;
+  if (lora) {
+    g.lx = d->lora_xa;
+    g.ld_lx = d->ld_lora_xa;
+    g.lb = d->lora_b;
+    g.lr = d->lora_r;
+    g.lcols = d->lora_cols;
+  }
   bool w4 = W->kind == ANIMA_W_W4;
   void* grid8 = nullptr;
   int rc;
-  if (w4 && c->w4_path == ANIMA_W4_GRID_SCRATCH) {
+  // (the LoRA epilogue always runs on the int8 grid: the in-GEMM unpack leaves it no registers)
+  if (w4 && (c->w4_path == ANIMA_W4_GRID_SCRATCH || lora)) {
     rc = w4_grid_scratch(c, W, g, &grid8);
     if (rc) {
       if (tmp) anima_free(c, tmp);
@@ -2436,7 +2508,8 @@ int linear_qkv_launch(anima_ctx* c, const anima_linear_desc* d, const anima_qkv_
     // persistent 256 x 256 tiles (a tile holds two whole heads); one workgroup per CU at most
     const int64_t tiles = (int64_t)(N / 256) * ((M + 255) / 256);
     const dim3 grid((unsigned)(tiles < c->num_cus ? tiles : c->num_cus)), block(512);
-    if (w4) hipLaunchKernelGGL((gemm_i8_256<ANIMA_EPI_STORE, true, true>), grid, block, 0, c->stream, g);
+    if (lora) hipLaunchKernelGGL((gemm_i8_256<ANIMA_EPI_STORE, false, true, true>), grid, block, 0, c->stream, g);
+    else if (w4) hipLaunchKernelGGL((gemm_i8_256<ANIMA_EPI_STORE, true, true>), grid, block, 0, c->stream, g);
     else hipLaunchKernelGGL((gemm_i8_256<ANIMA_EPI_STORE, false, true>), grid, block, 0, c->stream, g);
     rc = L.end();
   }

@@ -778,6 +778,11 @@ static napi_value js_linear_qkv(napi_env env, napi_callback_info info) {
   d.out = (float*)pptr(env, o, "out");
   d.ldc = (int64_t)pnum(env, o, "ldc");
   d.alpha = (float)pnum(env, o, "alpha");
+  d.lora_xa = (const float*)pptr(env, o, "loraXa");
+  d.ld_lora_xa = (int64_t)pnum(env, o, "ldLoraXa");
+  d.lora_b = (const uint16_t*)pptr(env, o, "loraB");
+  d.lora_r = (int)pnum(env, o, "loraR");
+  d.lora_cols = (int)pnum(env, o, "loraCols");
   anima_qkv_desc q;
   memset(&q, 0, sizeof q);
   q.B = (int)pnum(env, k, "B");

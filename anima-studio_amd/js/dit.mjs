@@ -393,13 +393,13 @@ export class AnimaDiT {
       const m = tc.blocks[i];
 
       // self-attention: stacked QKV GEMM, then attention with q/k RMSNorm + RoPE fused.  With an
-      // int8 / W4 stacked weight (no LoRA) and bf16 attention, the GEMM's epilogue writes K
-      // (normed, rotated) and V^T straight into the attention's operand layout.
+      // int8 / W4 stacked weight (LoRAs through its fused factors) and bf16 attention, the GEMM's
+      // epilogue writes K (normed, rotated) and V^T straight into the attention's operand layout.
       let nf;
       let a;
       if (b.self.qkv && this.fuseQkv && this.precision === "bf16" && ops.qkvFusable(b.self.qkv, L, HEADS)) {
         nf = normFor(gpu, x, m.self, b.self.qkv);
-        const f = ops.linearQkv(gpu, null, b.self.qkv, { B, L, H: HEADS, xq: nf.xq, kNorm: b.self.kn, cs });
+        const f = ops.linearQkv(gpu, null, b.self.qkv, { B, L, H: HEADS, xq: nf.xq, xr: nf.xq.xr, kNorm: b.self.kn, cs });
         releaseNorm(nf);
         a = ops.attention(gpu, { q: f.q, kvPrep: f.kvPrep, B, Lq: L, Lk: L, H: HEADS, D: HD, ldq: D, qNorm: b.self.qn,
           cs, precision: "bf16" });

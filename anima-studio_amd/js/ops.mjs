@@ -158,9 +158,17 @@ export function releaseLoraFused(W) {
 // then qkNormRope, then the attention).  Returns { q: [M, H*128] fp32, kvPrep } for
 // attention(gpu, { q, kvPrep, qNorm, cs, ... }); K is RMS-normed (kNorm) and rotated (cs) and the
 // prepared bytes equal attentionPrepareKV of the plain linear's output.  Callers check
-// qkvFusable first (int8 / W4 weights without LoRA, tokens per image a multiple of 64).
-export function qkvFusable(W, L, H) {
-  return needsRotation(W) && !(W.lora && W.lora.length) && L % 64 === 0 && H % 2 === 0 && W.N === 3 * H * 128;
+// qkvFusable first (int8 / W4 weights, tokens per image a multiple of 64).  linearQkv takes LoRAs
+// too (their fused factors, fuseLora, with rank blocks of whole 256-column tiles, and the rotated
+// fp32 input in opts.xr for the A product), but qkvFusable declines them unless withLora: the
+// GEMM instance with both epilogues runs at the register limit and measured no faster than the
+// LoRA linear plus the attention's own K / V conversion (51.7 vs 51.5 ms per DiT step at rank 32).
+export function qkvFusable(W, L, H, withLora) {
+  if (W.lora && W.lora.length) {
+    const F = W.loraFused;
+    if (!withLora || !(F && F.lora === W.lora && F.Ars && F.cols % 256 === 0)) return false;
+  }
+  return needsRotation(W) && L % 64 === 0 && H % 2 === 0 && W.N === 3 * H * 128;
 }
 
 export function linearQkv(gpu, x, W, opts) {
@@ -178,9 +186,15 @@ export function linearQkv(gpu, x, W, opts) {
     d.x = x.buf;
     d.xRotated = o.xRotated ? 1 : 0;
   }
+  // LoRAs: the A product of the rotated input (x H)(A H)^T = x A^T, the B product in the epilogue
+  const F = W.lora && W.lora.length ? W.loraFused : null;
+  if (F && !o.xr) throw new Error(`${W.name || "linearQkv"}: a LoRA needs the rotated fp32 input (opts.xr)`);
+  const down = F ? linear(gpu, o.xr, { kind: "f32s3", N: F.R, K: W.K, buf: F.Ars }, { M }) : null;
+  if (F) Object.assign(d, { loraXa: down.buf, ldLoraXa: F.R, loraB: F.Bs.buf, loraR: F.Rb, loraCols: F.cols });
   const w = weightArg(W);
   native.linearQkv(gpu.ctx, w, d, { B, L, H, kNorm: o.kNorm.buf, cs: o.cs.buf, sinOff: o.cs.sinOff, eps: o.eps || 1e-6,
     kvPrep: kvPrep.buf, kvPrepBytes: bytes });
+  if (down) down.release();
   return { q, kvPrep };
 }
 

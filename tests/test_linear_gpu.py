@@ -650,12 +650,13 @@ def test_split3_planes(ctx):
 
 @pytest.mark.parametrize("N,K,M,epi", [(32, 2048, 257, "store"), (96, 2048, 300, "store"), (200, 1040, 45, "store"),
                                       (32, 1032, 70, "store"), (64, 520, 33, "resid"), (96, 1544, 64, "gated"),
+                                      (30, 1040, 33, "resid"),
                                       (2048, 32, 300, "resid"), (2048, 8, 97, "gated"), (516, 24, 64, "store"),
                                       (2052, 40, 8200, "resid")])
 def test_split3_linears(ctx, N, K, M, epi):
     """ANIMA_W_F32S3 (fp32 matrices as three bf16 planes, products split the same way on the
     bf16 matrix cores): the tall-skinny LoRA-A shapes (ragged N and M; K = 1032, 520, 1544 end
-    inside a step of 4, 2 and 2 slices, two of them inside a 16-k slice) and the
+    inside a 32-k step; N = 30 at M = 33 makes M * N odd, summed element by element) and the
     swapped-operand LoRA-B shapes (K = rank 32 / 8 / 24, store / residual into a wider output /
     gated; at M = 8200, N = 2052, K = 40 the four-tiles-per-wave grid with ragged rows, columns and
     a partial k-chunk) within 1e-6 of float64, as the fp32 kernels."""

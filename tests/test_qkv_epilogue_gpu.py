@@ -126,10 +126,55 @@ def run_linear_qkv_case(ctx, m, kind, B, Hp, Wp, H, K, bias):
         x.release()
 
 
+@pytest.mark.parametrize("kind,cols", [("i8", 2048), ("w4", 2048), ("i8", 0)])
+def test_linear_qkv_lora(ctx, kind, cols):
+    """The fused QKV epilogue with the LoRA term (anima_linear_desc lora_*): Q and the K / V operands
+    bit-identical to the LoRA linear's fp32 output converted by anima_attention_prepare_kv.
+    B = 2, 48 x 48 tokens (M = 4608: the plain linear also runs the product inside its epilogue,
+    as it does from one 256 x 256 tile per CU up), H = 16, K = 2048; rank 32 per q / k / v block
+    (lora_cols = 2048), or one rank-48 block over all columns (lora_cols = 0)."""
+    case(f"linear_qkv LoRA {kind} cols={cols}")
+    m = amd()
+    B, Hp, Wp, H, K = 2, 48, 48, 16, 2048
+    L = Hp * Wp
+    M, N = B * L, 3 * H * HD
+    R = 32 if cols else 48
+    nb = N // cols if cols else 1
+    W, wbufs = make_weight(ctx, m, kind, 777, N, K, True)
+    rng = np.random.default_rng(778)
+    xq = ctx.upload(rng.integers(-127, 128, size=(M, K), dtype=np.int8))
+    xs = ctx.upload(rng.uniform(0.002, 0.02, M).astype(np.float32))
+    xa = ctx.upload((0.5 * rng.standard_normal((M, nb * R))).astype(np.float32))
+    Bm = ctx.upload((0.05 * rng.standard_normal((N, R))).astype(np.float32))
+    planes = ctx.empty(3 * N * R, np.uint16)
+    ctx.split3_bf16(Bm, planes, N * R)
+    lk = dict(lora_xa=xa, ld_lora_xa=nb * R, lora_b=planes, lora_r=R, lora_cols=cols)
+    kn = ctx.upload((1 + 0.02 * orc.randn(779, HD)).astype(np.float32))
+    cs = ctx.upload(orc.dit_rope_table(Hp, Wp))
+    sin_off = L * 64
+    nbytes = m.Context.attention_kv_bytes(B, H, L, m.PREC_BF16)
+    ref = ctx.empty((M, N))
+    ctx.linear(W, M, ref, xq=xq, xs=xs, **lk)
+    prep_ref = ctx.empty(nbytes, np.uint8)
+    ctx.attention(q=ref, k=ref, v=ref, o=ref, prepare_into=prep_ref, k_norm=kn, rope_cs=cs, rope_sin_off=sin_off,
+                  B=B, Lq=L, Lk=L, H=H, D=HD, ldq=N, ldk=N, ldv=N, k_off=H * HD, v_off=2 * H * HD,
+                  precision=m.PREC_BF16)
+    q = ctx.empty((M, H * HD))
+    prep = ctx.empty(nbytes, np.uint8)
+    ctx.linear_qkv(W, M, q, B=B, L=L, H=H, k_norm=kn, rope_cs=cs, rope_sin_off=sin_off, kv_prep=prep, xq=xq, xs=xs,
+                   ldc=H * HD, **lk)
+    got_prep, want_prep = prep.numpy(), prep_ref.numpy()
+    print(f"differing prep bytes: {int((got_prep != want_prep).sum())}", flush=True)
+    assert np.array_equal(q.numpy(), ref.numpy()[:, :H * HD])
+    assert np.array_equal(got_prep, want_prep)
+    for x in wbufs + [xq, xs, xa, Bm, planes, kn, cs, ref, prep_ref, q, prep]:
+        x.release()
+
+
 def test_linear_qkv_refusals(ctx):
     """Shapes the fused epilogue does not cover are refused on the host before any launch:
-    L % 64 != 0 (ANIMA_E_UNSUPPORTED), a wrong operand buffer size and N != 3 * 128 * H
-    (ANIMA_E_ARG)."""
+    L % 64 != 0 (ANIMA_E_UNSUPPORTED), a wrong operand buffer size, N != 3 * 128 * H and LoRA
+    rank blocks that split a 256-column tile (ANIMA_E_ARG)."""
     case("linear_qkv host refusals")
     m = amd()
     H, K = 2, 256
@@ -148,5 +193,14 @@ def test_linear_qkv_refusals(ctx):
         assert e.value.code == exp, (L, Hh, e.value)
         for x in (xq, xs, out, prep):
             x.release()
-    for x in (dq, ds, kn, cs):
+    # LoRA rank blocks that split a 256-column tile (lora_cols = 384): ANIMA_E_ARG
+    L, M = 128, 256
+    xq, xs, out = ctx.empty((M, K), np.int8), ctx.empty(M), ctx.empty((M, N))
+    prep = ctx.empty(m.Context.attention_kv_bytes(2, H, L, m.PREC_BF16), np.uint8)
+    xa, planes = ctx.empty((M, 64)), ctx.empty(3 * N * 32, np.uint16)
+    with pytest.raises(m.AnimaError) as e:
+        ctx.linear_qkv(W, M, out, B=2, L=L, H=H, k_norm=kn, rope_cs=cs, rope_sin_off=96 * 64, kv_prep=prep, xq=xq,
+                       xs=xs, lora_xa=xa, ld_lora_xa=64, lora_b=planes, lora_r=32, lora_cols=384)
+    assert e.value.code == -1, e.value
+    for x in (xq, xs, out, prep, xa, planes, dq, ds, kn, cs):
         x.release()
