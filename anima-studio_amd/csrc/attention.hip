@@ -335,6 +335,12 @@ struct FlashArgs {
 // Loads this lane's 64 Q values (query qi, dims 16ks + 8hf + j), applies the fused
 // RMSNorm + RoPE, and returns them in x[ks*8 + j].
 template <bool NORM, bool ROPE>
+__device__ __forceinline__ void q_post(const FlashArgs& a, int qi, int hf, float* x);
+template <bool NORM>
+__device__ __forceinline__ void q_norm(const FlashArgs& a, int hf, float* x);
+__device__ __forceinline__ void q_rope(float* x, const float* c, const float* sn);
+
+template <bool NORM, bool ROPE>
 __device__ __forceinline__ void load_q(const FlashArgs& a, int b, int h, int qi, int hf, float* x) {
   if (qi < a.Lq) {
     const float* src = a.q + (int64_t)b * a.q_bs + (int64_t)qi * a.ldq + h * a.D + 8 * hf;
@@ -351,6 +357,44 @@ __device__ __forceinline__ void load_q(const FlashArgs& a, int b, int h, int qi,
 #pragma unroll
     for (int i = 0; i < 64; i++) x[i] = 0.0f;
   }
+  q_post<NORM, ROPE>(a, qi, hf, x);
+}
+
+// The q RMSNorm and RoPE of load_q on the lane's 64 values x[8 ks + j] (dims 16 ks + 8 hf + j):
+// the sum of squares over the lane pair, then weights, then the split-half rotation.
+template <bool NORM, bool ROPE>
+__device__ __forceinline__ void q_post(const FlashArgs& a, int qi, int hf, float* x) {
+  q_norm<NORM>(a, hf, x);
+  if (ROPE && qi < a.Lq) {
+    const float* cr = a.cs + (int64_t)qi * (HD / 2) + 8 * hf;
+    const float* sr = a.cs + a.sin_off + (int64_t)qi * (HD / 2) + 8 * hf;
+    float c[32], sn[32];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        c[8 * ks + j] = cr[16 * ks + j];
+        sn[8 * ks + j] = sr[16 * ks + j];
+      }
+    q_rope(x, c, sn);
+  }
+}
+
+// The lane's split-half rotation with its cos / sin values c[8 ks + j], s[8 ks + j] (dims
+// 16 ks + 8 hf + j of the table row).
+__device__ __forceinline__ void q_rope(float* x, const float* c, const float* sn) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float x1 = x[8 * ks + j], x2 = x[8 * (ks + 4) + j];
+      x[8 * ks + j] = x1 * c[8 * ks + j] - x2 * sn[8 * ks + j];
+      x[8 * (ks + 4) + j] = x2 * c[8 * ks + j] + x1 * sn[8 * ks + j];
+    }
+}
+
+template <bool NORM>
+__device__ __forceinline__ void q_norm(const FlashArgs& a, int hf, float* x) {
   if (NORM) {
     float ss = 0.0f;
 #pragma unroll
@@ -361,19 +405,6 @@ __device__ __forceinline__ void load_q(const FlashArgs& a, int b, int h, int qi,
     for (int ks = 0; ks < 8; ks++)
 #pragma unroll
       for (int j = 0; j < 8; j++) x[8 * ks + j] = x[8 * ks + j] * rn * a.qn[16 * ks + 8 * hf + j];
-  }
-  if (ROPE && qi < a.Lq) {
-    const float* cr = a.cs + (int64_t)qi * (HD / 2) + 8 * hf;
-    const float* sr = a.cs + a.sin_off + (int64_t)qi * (HD / 2) + 8 * hf;
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const float c = cr[16 * ks + j], s = sr[16 * ks + j];
-        const float x1 = x[8 * ks + j], x2 = x[8 * (ks + 4) + j];
-        x[8 * ks + j] = x1 * c - x2 * s;
-        x[8 * (ks + 4) + j] = x2 * c + x1 * s;
-      }
   }
 }
 
@@ -831,9 +862,35 @@ __device__ __forceinline__ void w8_barrier() {
 // vmcnt(n) only (expcnt and lgkmcnt at their no-wait maxima), gfx9 s_waitcnt encoding.
 #define W8_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
 
+// Q rows of one wave (32 queries x 128 fp32) reach the MFMA layout through LDS: per round of 64
+// dims, eight lane-contiguous copies of 4 rows x 256 bytes each (whole lines per instruction;
+// lane l -> row 4 i + l / 16, 16-byte slot l % 16 holding piece (slot ^ row) % 16 of the row), then
+// each lane reads its row's pieces 4 ks + 2 hf, + 1.  Loaded straight into the MFMA layout, one
+// instruction would touch 32 rows with one 16-byte access each, which the vector memory address
+// path serves at about one access per clock.
+constexpr int W8_QB = 8192;  // one wave's staging bytes: 32 rows x 64 fp32
+__device__ __forceinline__ void w8_q_issue(__amdgpu_buffer_rsrc_t rq, char* qs, const int (&qo)[8], int round) {
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void_t*)(qs + i * 1024), 16, qo[i] + 256 * round, 0, 0, 0);
+}
+// (restrict: the reads carry alias scopes, so the compiler does not make them wait for the K / V
+// copies in flight; whole 16-byte vectors, which keep them)
+__device__ __forceinline__ void w8_q_read(const char* __restrict__ qs, int lq, int hf, float* x) {
+  f32x4 v[8];
+#pragma unroll
+  for (int p = 0; p < 8; p++) v[p] = *(const f32x4*)(qs + lq * 256 + 16 * ((4 * (p >> 1) + 2 * hf + (p & 1)) ^ (lq & 7)));
+  asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
+#pragma unroll
+  for (int p = 0; p < 8; p++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) x[4 * p + e] = v[p][e];
+}
+
 template <bool NORM, bool ROPE>
 __global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
-  __shared__ __attribute__((aligned(1024))) char smem[W8_NST * W8_ST];
+  // the K / V stages, then 32 KiB that with stage 3 stage Q in the prologue
+  __shared__ __attribute__((aligned(1024))) char smem[W8_NST * W8_ST + 32768];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 31, hf = lane >> 5;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
@@ -849,7 +906,19 @@ __global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
   src.v = __builtin_amdgcn_make_buffer_rsrc((void*)((const bf16*)a.vt + ((int64_t)b * a.Hkv + hk) * HD * a.Lkp), (short)0,
                                             head_bytes, 0x00020000);
 
-  // blocks 0, 1 and 2 start loading before Q is read and normalized
+  // Q's first 64 dims are copied first, then K / V blocks 0, 1 and 2, so the wait for Q leaves
+  // those in flight (rows past Lq read zeros)
+  const int qrow0 = qt * W8_BQ, nrow = a.Lq - qrow0 < W8_BQ ? a.Lq - qrow0 : W8_BQ;
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.q + (int64_t)b * a.q_bs + (int64_t)qrow0 * a.ldq + h * a.D), (short)0, nrow * (int)a.ldq * 4, 0x00020000);
+  char* qs = smem + 3 * W8_ST + wave * W8_QB;
+  int qo[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int row = 4 * i + (lane >> 4);
+    qo[i] = ((wave * 32 + row) * (int)a.ldq + 4 * ((lane & 15) ^ (row & 7))) * 4;
+  }
+  w8_q_issue(rq, qs, qo, 0);
   const W8Load lo(a.Lkp, wave, lane);
   const int vhalf = 64 * a.Lkp * 2;
   w8_load(src, lo, 0, smem, wave, vhalf);
@@ -859,7 +928,41 @@ __global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
   bf16x8 qf[8];
   {
     float x[64];
-    load_q<NORM, ROPE>(a, b, h, qi, hf, x);
+    // waves 0-3 issued 8 K / V copies per block after Q's
+    if (wave >= 4) W8_WAIT_VM(0);
+    else if (nkb > 2) W8_WAIT_VM(24);
+    else if (nkb > 1) W8_WAIT_VM(16);
+    else W8_WAIT_VM(8);
+    w8_q_read(qs, lq, hf, x);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the reads are done before the refill
+    w8_q_issue(rq, qs, qo, 1);
+    W8_WAIT_VM(0);
+    w8_q_read(qs, lq, hf, x + 32);
+    q_norm<NORM>(a, hf, x);
+    if constexpr (ROPE) {
+      // the rows' cos and sin (64 fp32 each) through the same staging, rows past Lq reading zeros
+      // (their Q is zero)
+      const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(a.cs + (int64_t)qrow0 * (HD / 2)), (short)0, nrow * (HD / 2) * 4, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(a.cs + a.sin_off + (int64_t)qrow0 * (HD / 2)), (short)0, nrow * (HD / 2) * 4, 0x00020000);
+      int co[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int row = 4 * i + (lane >> 4);
+        co[i] = ((wave * 32 + row) * (HD / 2) + 4 * ((lane & 15) ^ (row & 7))) * 4;
+      }
+      float c[32], sn[32];
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      w8_q_issue(rc, qs, co, 0);
+      W8_WAIT_VM(0);
+      w8_q_read(qs, lq, hf, c);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      w8_q_issue(rs, qs, co, 0);
+      W8_WAIT_VM(0);
+      w8_q_read(qs, lq, hf, sn);
+      q_rope(x, c, sn);
+    }
 #pragma unroll
     for (int ks = 0; ks < 8; ks++)
 #pragma unroll
@@ -1248,7 +1351,9 @@ int attention_launch_ws(anima_ctx* c, const anima_attn_desc* d, void* scratch) {
   f.Lq = d->Lq;
   f.Lkp = Lkp;
   // 8-wave workgroups (256 queries) when that grid still gives every CU a workgroup
-  const bool w8 = bf && !d->causal && d->D == HD && (int64_t)((d->Lq + W8_BQ - 1) / W8_BQ) * d->H * d->B >= c->num_cus;
+  // (the Q copies of a workgroup use 32-bit offsets: 256 rows of ldq fp32)
+  const bool w8 = bf && !d->causal && d->D == HD && (int64_t)((d->Lq + W8_BQ - 1) / W8_BQ) * d->H * d->B >= c->num_cus &&
+                  (int64_t)W8_BQ * d->ldq * 4 < (1LL << 31);
   f.n_qt = w8 ? (d->Lq + W8_BQ - 1) / W8_BQ : (d->Lq + BQ - 1) / BQ;
   for (int b = 0; b < MAXB; b++) f.kv_len[b] = b < d->B ? kv_len[b] : 1;
   f.causal = d->causal ? 1 : 0;
