@@ -53,6 +53,7 @@ class AttnDesc(ctypes.Structure):
         ("causal", ctypes.c_int),
         ("kv_prep", _vp),
         ("kv_prep_bytes", _i64),
+        ("q_prep", _vp),
     ]
 
 
@@ -95,7 +96,8 @@ class Limits(ctypes.Structure):
 
 class QkvDesc(ctypes.Structure):
     _fields_ = [("B", ctypes.c_int), ("L", ctypes.c_int), ("H", ctypes.c_int), ("k_norm", _vp), ("rope_cs", _vp),
-                ("rope_sin_off", _i64), ("eps", ctypes.c_float), ("kv_prep", _vp), ("kv_prep_bytes", _i64)]
+                ("rope_sin_off", _i64), ("eps", ctypes.c_float), ("kv_prep", _vp), ("kv_prep_bytes", _i64),
+                ("q_norm", _vp), ("q_prep", _vp), ("q_scale", ctypes.c_float)]
 
 
 ABI_STRUCTS = {"anima_attn_desc": AttnDesc, "anima_linear_desc": LinearDesc, "anima_weight": Weight,
@@ -340,11 +342,13 @@ class Context:
     def attention(self, *, q, k, v, o, B, Lq, Lk, H, D, ldq, ldk, ldv, ldo=None, q_off=0, k_off=0, v_off=0,
                   o_off=0, q_bstride=None, k_bstride=None, v_bstride=None, o_bstride=None, group=1, scale=0.0,
                   kv_len=None, precision=PREC_BF16, q_norm=None, k_norm=None, rope_cs=None, rope_sin_off=0,
-                  eps=1e-6, causal=0, kv_prep=None, prepare_into=None, kv_prep_bytes=None, noalloc=False):
+                  eps=1e-6, causal=0, kv_prep=None, prepare_into=None, kv_prep_bytes=None, noalloc=False,
+                  q_prep=None):
         """anima_attention; kv_prep: K/V converted by a call with prepare_into (which runs
         anima_attention_prepare_kv into that buffer instead of the attention).  kv_prep_bytes
         defaults to the size the call's shape and precision take.  noalloc: anima_attention_noalloc
-        (the K/V conversion in the library's static scratch, no allocation)."""
+        (the K/V conversion in the library's static scratch, no allocation).  q_prep: Q as
+        linear_qkv(q_prep=...) prepared it (then q may be None)."""
         ldo = ldo if ldo is not None else H * D
         kl = (ctypes.c_int * B)(*[int(x) for x in kv_len]) if kv_len is not None else None
         d = AttnDesc(B=B, Lq=Lq, Lk=Lk, H=H, D=D, group=group,
@@ -354,7 +358,7 @@ class Context:
                      o=_ptr(o), ldo=ldo, o_off=o_off, o_bstride=o_bstride if o_bstride is not None else Lq * ldo,
                      scale=scale, kv_len=ctypes.cast(kl, ctypes.POINTER(ctypes.c_int)) if kl is not None else None,
                      precision=precision, q_norm=_ptr(q_norm), k_norm=_ptr(k_norm), rope_cs=_ptr(rope_cs),
-                     rope_sin_off=rope_sin_off, eps=eps, causal=causal, kv_prep=_ptr(kv_prep),
+                     rope_sin_off=rope_sin_off, eps=eps, causal=causal, kv_prep=_ptr(kv_prep), q_prep=_ptr(q_prep),
                      kv_prep_bytes=kv_prep_bytes if kv_prep_bytes is not None else
                      (self.attention_kv_bytes(B, H // max(group, 1), Lk, precision)
                       if (kv_prep is not None or prepare_into is not None) else 0))
@@ -433,18 +437,21 @@ class Context:
                        lora_r=lora_r, lora_cols=lora_cols)
         return self._check(lib().anima_linear(self.h, ctypes.byref(d)))
 
-    def linear_qkv(self, W, M, out, *, B, L, H, k_norm, rope_cs, rope_sin_off, kv_prep, eps=1e-6, x=None, ldx=0,
-                   x_rotated=True, xq=None, xs=None, ldc=0, alpha=0.0, lora_xa=None, ld_lora_xa=0, lora_b=None,
-                   lora_r=0, lora_cols=0):
+    def linear_qkv(self, W, M, out, *, B, L, H, k_norm=None, rope_cs=None, rope_sin_off=0, kv_prep=None, eps=1e-6,
+                   x=None, ldx=0, x_rotated=True, xq=None, xs=None, ldc=0, alpha=0.0, lora_xa=None, ld_lora_xa=0,
+                   lora_b=None, lora_r=0, lora_cols=0, q_norm=None, q_prep=None, q_scale=0.0):
         """anima_linear_qkv: the stacked QKV projection writing Q (fp32) to out and K / V in the
         attention's bf16 operand layout to kv_prep (sized by attention_kv_bytes(B, H, L, bf16));
-        lora_*: the LoRA factors as for linear(), added before the K / V conversion."""
+        lora_*: the LoRA factors as for linear(), added before the K / V conversion; q_prep: Q in the
+        attention's prepared bf16 form (q_norm, RoPE, q_scale) instead of fp32 into out (out may then
+        be None; with W of H * 128 columns, a Q-only projection)."""
         d = LinearDesc(M=M, W=ctypes.pointer(W), x=_ptr(x), ldx=ldx, x_rotated=int(x_rotated), xq=_ptr(xq),
                        xs=_ptr(xs), out=_ptr(out), ldc=ldc, alpha=alpha, act=0, epilogue=EPI_STORE,
                        lora_xa=_ptr(lora_xa), ld_lora_xa=ld_lora_xa, lora_b=_ptr(lora_b), lora_r=lora_r,
                        lora_cols=lora_cols)
         p = QkvDesc(B=B, L=L, H=H, k_norm=_ptr(k_norm), rope_cs=_ptr(rope_cs), rope_sin_off=rope_sin_off, eps=eps,
-                    kv_prep=_ptr(kv_prep), kv_prep_bytes=self.attention_kv_bytes(B, H, L, PREC_BF16))
+                    kv_prep=_ptr(kv_prep), kv_prep_bytes=self.attention_kv_bytes(B, H, L, PREC_BF16) if kv_prep else 0,
+                    q_norm=_ptr(q_norm), q_prep=_ptr(q_prep), q_scale=q_scale)
         return self._check(lib().anima_linear_qkv(self.h, ctypes.byref(d), ctypes.byref(p)))
 
     def weight_unpack_w4(self, W, grid):

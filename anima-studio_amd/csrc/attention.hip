@@ -330,6 +330,9 @@ struct FlashArgs {
   int kv_len[MAXB];
   int causal;  // keys > query index masked (the 4-wave and fp32 kernels)
   int D;       // the caller's head dim, 128 or 64 (the operands are zero-padded to 128)
+  // prepared Q (the bf16 kernels' QP form): [B][Lq][H][128] bf16, each value the kernel's own
+  // to_bf16(c * q') of the normed, rotated query q'; then q, qn and cs are not read
+  const uint16_t* qp;
 };
 
 // Loads this lane's 64 Q values (query qi, dims 16ks + 8hf + j), applies the fused
@@ -388,19 +391,42 @@ __device__ __forceinline__ void q_rope(float* x, const float* c, const float* sn
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       const float x1 = x[8 * ks + j], x2 = x[8 * (ks + 4) + j];
-      x[8 * ks + j] = x1 * c[8 * ks + j] - x2 * sn[8 * ks + j];
-      x[8 * (ks + 4) + j] = x2 * c[8 * ks + j] + x1 * sn[8 * ks + j];
+      // the rotation in the fused form of the K operand epilogue
+      x[8 * ks + j] = __builtin_fmaf(x1, c[8 * ks + j], -(x2 * sn[8 * ks + j]));
+      x[8 * (ks + 4) + j] = __builtin_fmaf(x2, c[8 * ks + j], x1 * sn[8 * ks + j]);
     }
 }
 
 template <bool NORM>
 __device__ __forceinline__ void q_norm(const FlashArgs& a, int hf, float* x) {
   if (NORM) {
-    float ss = 0.0f;
+    // The row's sum of squares in one fixed tree, that of the K operand epilogue of the stacked
+    // QKV projection (so a Q prepared there is bit-identical): leaves of 8 values, dims
+    // 32 g + 8 q + 4 h + e then 64 + the same (e = 0..3, fused multiply-adds in that order); per
+    // (g, h): (L0 + L1) + (L2 + L3) over q; then the two h; then the two g.  This lane holds the
+    // leaves q = 2 qq + hf (dims 16 ks + 8 hf + j with ks = 2 g + qq, j = 4 h + e), its pair lane
+    // the others.  (fp addition is commutative, so both lanes reach the same bits.)
+    float part[2][2];
 #pragma unroll
-    for (int i = 0; i < 64; i++) ss += x[i] * x[i];
-    ss += __shfl_xor(ss, 32);
-    const float rn = 1.0f / sqrtf(ss / (float)HD + a.eps);
+    for (int g = 0; g < 2; g++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        float lf[2];
+#pragma unroll
+        for (int qq = 0; qq < 2; qq++) {
+          const int ks = 2 * g + qq;
+          float acc = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 4; e++) acc = __builtin_fmaf(x[8 * ks + 4 * h + e], x[8 * ks + 4 * h + e], acc);
+#pragma unroll
+          for (int e = 0; e < 4; e++) acc = __builtin_fmaf(x[8 * (ks + 4) + 4 * h + e], x[8 * (ks + 4) + 4 * h + e], acc);
+          lf[qq] = acc;
+        }
+        const float o0 = __shfl_xor(lf[0], 32), o1 = __shfl_xor(lf[1], 32);
+        part[g][h] = (lf[0] + o0) + (lf[1] + o1);
+      }
+    const float ss = (part[0][0] + part[0][1]) + (part[1][0] + part[1][1]);
+    const float rn = 1.0f / sqrtf(__builtin_fmaf(ss, 1.0f / 128.0f, a.eps));
 #pragma unroll
     for (int ks = 0; ks < 8; ks++)
 #pragma unroll
@@ -679,7 +705,7 @@ __device__ __forceinline__ void flash_block_main(const Addr& A, const Addr& N, b
 
 // 4 waves x 32 queries per workgroup; K/V blocks of KB keys double-buffered in LDS, the next
 // block prefetched into registers while the current one is consumed (one barrier per block).
-template <int KB, bool NORM, bool ROPE>
+template <int KB, bool NORM, bool ROPE, bool QP = false>
 __global__ __launch_bounds__(256, KB == 32 ? 3 : 2) void attn_flash_bf16(FlashArgs a) {
   using T = Tiles<KB>;
   constexpr int UK = KB / 16;  // uint4 per thread for each of the K and V^T block copies
@@ -700,7 +726,12 @@ __global__ __launch_bounds__(256, KB == 32 ? 3 : 2) void attn_flash_bf16(FlashAr
   const int nfull = a.causal ? min(Lk / KB, qt * BQ / KB) : Lk / KB;
 
   bf16x8 qf[8];
-  {
+  if constexpr (QP) {
+    const bf16x8 z8 = {};
+    const uint16_t* src = a.qp + (((int64_t)b * a.Lq + (qi < a.Lq ? qi : 0)) * a.H + h) * HD + 8 * hf;
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) qf[ks] = qi < a.Lq ? *(const bf16x8*)(src + 16 * ks) : z8;
+  } else {
     float x[64];
     load_q<NORM, ROPE>(a, b, h, qi, hf, x);
 #pragma unroll
@@ -874,6 +905,12 @@ __device__ __forceinline__ void w8_q_issue(__amdgpu_buffer_rsrc_t rq, char* qs, 
   for (int i = 0; i < 8; i++)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void_t*)(qs + i * 1024), 16, qo[i] + 256 * round, 0, 0, 0);
 }
+// The prepared bf16 Q fragments (piece 2 ks + hf of the row for k-step ks) from the staging.
+__device__ __forceinline__ void w8_qp_read(const char* __restrict__ qs, int lq, int hf, bf16x8 (&qf)[8]) {
+#pragma unroll
+  for (int ks = 0; ks < 8; ks++) qf[ks] = *(const bf16x8*)(qs + lq * 256 + 16 * ((2 * ks + hf) ^ (lq & 7)));
+  asm volatile("" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]), "+v"(qf[4]), "+v"(qf[5]), "+v"(qf[6]), "+v"(qf[7]));
+}
 // (restrict: the reads carry alias scopes, so the compiler does not make them wait for the K / V
 // copies in flight; whole 16-byte vectors, which keep them)
 __device__ __forceinline__ void w8_q_read(const char* __restrict__ qs, int lq, int hf, float* x) {
@@ -887,7 +924,7 @@ __device__ __forceinline__ void w8_q_read(const char* __restrict__ qs, int lq, i
     for (int e = 0; e < 4; e++) x[4 * p + e] = v[p][e];
 }
 
-template <bool NORM, bool ROPE>
+template <bool NORM, bool ROPE, bool QP = false>
 __global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
   // the K / V stages, then 32 KiB that with stage 3 stage Q in the prologue
   __shared__ __attribute__((aligned(1024))) char smem[W8_NST * W8_ST + 32768];
@@ -909,14 +946,27 @@ __global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
   // Q's first 64 dims are copied first, then K / V blocks 0, 1 and 2, so the wait for Q leaves
   // those in flight (rows past Lq read zeros)
   const int qrow0 = qt * W8_BQ, nrow = a.Lq - qrow0 < W8_BQ ? a.Lq - qrow0 : W8_BQ;
-  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.q + (int64_t)b * a.q_bs + (int64_t)qrow0 * a.ldq + h * a.D), (short)0, nrow * (int)a.ldq * 4, 0x00020000);
   char* qs = smem + 3 * W8_ST + wave * W8_QB;
   int qo[8];
+  __amdgpu_buffer_rsrc_t rq;
+  if constexpr (QP) {
+    // prepared Q: one copy round of the wave's 32 rows x 256 bytes (16-byte pieces swizzled as
+    // for fp32 Q, 16 per row)
+    rq = __builtin_amdgcn_make_buffer_rsrc((void*)(a.qp + (((int64_t)b * a.Lq + qrow0) * a.H + h) * HD), (short)0,
+                                           nrow * a.H * HD * 2, 0x00020000);
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const int row = 4 * i + (lane >> 4);
-    qo[i] = ((wave * 32 + row) * (int)a.ldq + 4 * ((lane & 15) ^ (row & 7))) * 4;
+    for (int i = 0; i < 8; i++) {
+      const int row = 4 * i + (lane >> 4);
+      qo[i] = (wave * 32 + row) * a.H * HD * 2 + 16 * ((lane & 15) ^ (row & 7));
+    }
+  } else {
+    rq = __builtin_amdgcn_make_buffer_rsrc((void*)(a.q + (int64_t)b * a.q_bs + (int64_t)qrow0 * a.ldq + h * a.D),
+                                           (short)0, nrow * (int)a.ldq * 4, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int row = 4 * i + (lane >> 4);
+      qo[i] = ((wave * 32 + row) * (int)a.ldq + 4 * ((lane & 15) ^ (row & 7))) * 4;
+    }
   }
   w8_q_issue(rq, qs, qo, 0);
   const W8Load lo(a.Lkp, wave, lane);
@@ -926,13 +976,15 @@ __global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
   if (nkb > 2) w8_load(src, lo, 2, smem + 2 * W8_ST, wave, vhalf);
 
   bf16x8 qf[8];
-  {
+  // waves 0-3 issued 8 K / V copies per block after Q's
+  if (wave >= 4) W8_WAIT_VM(0);
+  else if (nkb > 2) W8_WAIT_VM(24);
+  else if (nkb > 1) W8_WAIT_VM(16);
+  else W8_WAIT_VM(8);
+  if constexpr (QP) {
+    w8_qp_read(qs, lq, hf, qf);
+  } else {
     float x[64];
-    // waves 0-3 issued 8 K / V copies per block after Q's
-    if (wave >= 4) W8_WAIT_VM(0);
-    else if (nkb > 2) W8_WAIT_VM(24);
-    else if (nkb > 1) W8_WAIT_VM(16);
-    else W8_WAIT_VM(8);
     w8_q_read(qs, lq, hf, x);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the reads are done before the refill
     w8_q_issue(rq, qs, qo, 1);
@@ -1197,8 +1249,10 @@ static int attention_check(anima_ctx* c, const anima_attn_desc* d, int (&kv_len)
   if (d->Lq < 1 || d->Lk < 1 || d->H < 1) return fail(c, ANIMA_E_ARG, "anima_attention: Lq=%d Lk=%d H=%d must be >= 1", d->Lq, d->Lk, d->H);
   if (d->Lk > (1 << 22)) return fail(c, ANIMA_E_ARG, "anima_attention: Lk=%d (at most %d keys)", d->Lk, 1 << 22);
   if (d->H % group) return fail(c, ANIMA_E_ARG, "anima_attention: H=%d not a multiple of group=%d", d->H, group);
-  const bool prepared = d->kv_prep != nullptr;
-  if (!d->q || !d->o || (!prepared && (!d->k || !d->v))) return fail(c, ANIMA_E_ARG, "anima_attention: null q/k/v/o");
+  const bool prepared = d->kv_prep != nullptr, qprep = d->q_prep != nullptr;
+  if ((!d->q && !qprep) || !d->o || (!prepared && (!d->k || !d->v))) return fail(c, ANIMA_E_ARG, "anima_attention: null q/k/v/o");
+  if (qprep && (d->precision != ANIMA_PREC_BF16 || d->D != HD || !al16(d->q_prep)))
+    return fail(c, ANIMA_E_ARG, "anima_attention: a prepared Q needs bf16 precision, D = 128 and 16-byte alignment");
   if (d->precision != ANIMA_PREC_BF16 && d->precision != ANIMA_PREC_FP32)
     return fail(c, ANIMA_E_ARG, "anima_attention: unknown precision %d", d->precision);
   const int64_t lds[4] = {d->ldq, d->ldk, d->ldv, d->ldo};
@@ -1208,6 +1262,7 @@ static int attention_check(anima_ctx* c, const anima_attn_desc* d, int (&kv_len)
   const int heads[4] = {d->H, d->H / group, d->H / group, d->H};
   for (int i = 0; i < 4; i++) {
     if (prepared && (i == 1 || i == 2)) continue;  // K / V come converted
+    if (qprep && i == 0) continue;                 // Q comes prepared
     if (lds[i] % 4 || offs[i] % 4 || bss[i] % 4 || lds[i] < 0 || offs[i] < 0 || bss[i] < 0)
       return fail(c, ANIMA_E_ARG, "anima_attention: %s ld/off/bstride (%lld/%lld/%lld) must be non-negative multiples of 4 (vec4 rows, as ops.js:169)",
                   nm[i], (long long)lds[i], (long long)offs[i], (long long)bss[i]);
@@ -1215,7 +1270,7 @@ static int attention_check(anima_ctx* c, const anima_attn_desc* d, int (&kv_len)
       return fail(c, ANIMA_E_ARG, "anima_attention: %s rows of %lld elements cannot hold off %lld + %d heads x %d", nm[i],
                   (long long)lds[i], (long long)offs[i], heads[i], d->D);
   }
-  if (!al16(d->q) || !al16(d->o) || (!prepared && (!al16(d->k) || !al16(d->v))) || (prepared && !al16(d->kv_prep)))
+  if ((!qprep && !al16(d->q)) || !al16(d->o) || (!prepared && (!al16(d->k) || !al16(d->v))) || (prepared && !al16(d->kv_prep)))
     return fail(c, ANIMA_E_ARG, "anima_attention: q/k/v/o (or kv_prep) must be 16-byte aligned");
   if ((d->q_norm && !al16(d->q_norm)) || (d->k_norm && !al16(d->k_norm)))
     return fail(c, ANIMA_E_ARG, "anima_attention: q_norm/k_norm must be 16-byte aligned");
@@ -1332,7 +1387,7 @@ int attention_launch_ws(anima_ctx* c, const anima_attn_desc* d, void* scratch) {
   }
 
   FlashArgs f;
-  f.q = d->q + d->q_off;
+  f.q = d->q ? d->q + d->q_off : nullptr;
   f.ldq = d->ldq;
   f.q_bs = d->q_bstride;
   f.kb = ws;
@@ -1353,11 +1408,12 @@ int attention_launch_ws(anima_ctx* c, const anima_attn_desc* d, void* scratch) {
   // 8-wave workgroups (256 queries) when that grid still gives every CU a workgroup
   // (the Q copies of a workgroup use 32-bit offsets: 256 rows of ldq fp32)
   const bool w8 = bf && !d->causal && d->D == HD && (int64_t)((d->Lq + W8_BQ - 1) / W8_BQ) * d->H * d->B >= c->num_cus &&
-                  (int64_t)W8_BQ * d->ldq * 4 < (1LL << 31);
+                  (int64_t)W8_BQ * (d->q_prep ? d->H * HD / 2 : d->ldq) * 4 < (1LL << 31);
   f.n_qt = w8 ? (d->Lq + W8_BQ - 1) / W8_BQ : (d->Lq + BQ - 1) / BQ;
   for (int b = 0; b < MAXB; b++) f.kv_len[b] = b < d->B ? kv_len[b] : 1;
   f.causal = d->causal ? 1 : 0;
   f.D = d->D;
+  f.qp = (const uint16_t*)d->q_prep;
   double flops = 0;
   for (int b = 0; b < d->B; b++) flops += 4.0 * d->Lq * (double)kv_len[b] * d->D * d->H;
   const int blocks = f.n_qt * d->H * d->B;
@@ -1365,7 +1421,11 @@ int attention_launch_ws(anima_ctx* c, const anima_attn_desc* d, void* scratch) {
   const bool qn = d->q_norm != nullptr;
 #define FLASH(K, N, R) hipLaunchKernelGGL((K<N, R>), dim3(blocks), dim3(256), 0, c->stream, f)
 #define FLASHB(T, N, R) hipLaunchKernelGGL((attn_flash_bf16<T, N, R>), dim3(blocks), dim3(256), 0, c->stream, f)
-  if (w8) {
+  if (f.qp && w8) {
+    hipLaunchKernelGGL((attn_flash_w8<false, false, true>), dim3(blocks), dim3(512), 0, c->stream, f);
+  } else if (f.qp) {
+    hipLaunchKernelGGL((attn_flash_bf16<FLASH_KB, false, false, true>), dim3(blocks), dim3(256), 0, c->stream, f);
+  } else if (w8) {
 #define FLASH8(N, R) hipLaunchKernelGGL((attn_flash_w8<N, R>), dim3(blocks), dim3(512), 0, c->stream, f)
     if (qn && rope) FLASH8(true, true);
     else if (qn) FLASH8(true, false);

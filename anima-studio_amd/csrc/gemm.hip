@@ -57,6 +57,12 @@ struct GemmArgs {
   const uint16_t* lb = nullptr;
   int lr = 0;
   int lcols = 0;
+  // prepared Q of the QKV / Q-only projection (kv_epi_k<true>): q_norm weights (or null), the
+  // bf16 [M][H][128] destination, the attention's scale * log2(e), RoPE on Q or not
+  const float* qn = nullptr;
+  uint16_t* qp = nullptr;
+  float qc = 0.0f;
+  int qrope = 0;
 };
 
 
@@ -523,53 +529,80 @@ __device__ __forceinline__ f32x4 kv_epi_y(const GemmArgs& a, const i32x16& v, in
 }
 
 // yf(i, j, q): the fp32 store values of row group i, column group j (+ 64 j), quad q.
-template <class YF>
+// Q (the prepared-Q form of the attention) goes through the same steps: its own weights (none:
+// no RMSNorm), RoPE when a.qrope, then times a.qc (the attention's scale * log2(e)) before the
+// bf16 rounding, into row-major [M][H][128].
+template <bool Q, class YF>
 __device__ __forceinline__ void kv_epi_k(const GemmArgs& a, const YF& yf, int m0, int n0, int col0, int wave, int hf,
                                          int lq, float* xch) {
   const int grp = (wave >> 1) & 1;
   const int c0 = 32 * grp + 4 * hf;  // this lane's first column within the head (< 64)
-  const int head = (col0 - a.kcol) / HD_K + (wave >> 2);
+  const int head = (col0 - (Q ? 0 : a.kcol)) / HD_K + (wave >> 2);
+  const float* wn = Q ? a.qn : a.kn;
+  const bool norm = !Q || wn, rope = !Q || a.qrope;  // (uniform over the workgroup)
   // One 32-row block at a time: the partial sum of squares over this lane pair's 64 columns goes
   // to LDS, a barrier, the partner wave's partial completes the row, and the block's values are
   // recomputed (the same fp32 bits), normalized, rotated, rounded and stored.
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    float lf[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float rn = 1.0f;
+    if (norm) {
+      float lf[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+      for (int j = 0; j < 2; j++)
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const f32x4 y = yf(i, j, q);
+        for (int q = 0; q < 4; q++) {
+          const f32x4 y = yf(i, j, q);
 #pragma unroll
-        for (int e = 0; e < 4; e++) lf[q] = __builtin_fmaf(y[e], y[e], lf[q]);
-      }
-    float part = (lf[0] + lf[1]) + (lf[2] + lf[3]);
-    part = part + __shfl_xor(part, 32);
-    if (hf == 0) xch[wave * 128 + 32 * i + lq] = part;
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the partial sums are in LDS
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    const float other = xch[(wave ^ 2) * 128 + 32 * i + lq];
+          for (int e = 0; e < 4; e++) lf[q] = __builtin_fmaf(y[e], y[e], lf[q]);
+        }
+      float part = (lf[0] + lf[1]) + (lf[2] + lf[3]);
+      part = part + __shfl_xor(part, 32);
+      if (hf == 0) xch[wave * 128 + 32 * i + lq] = part;
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the partial sums are in LDS
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      const float other = xch[(wave ^ 2) * 128 + 32 * i + lq];
+      const float ss = grp == 0 ? part + other : other + part;
+      rn = 1.0f / sqrtf(__builtin_fmaf(ss, 1.0f / 128.0f, a.eps));
+    }
     const int m = m0 + 32 * i;
     if (m >= a.M) continue;
-    const float ss = grp == 0 ? part + other : other + part;
-    const float rn = 1.0f / sqrtf(__builtin_fmaf(ss, 1.0f / 128.0f, a.eps));
     const int b = m / a.L, l = m - b * a.L;
     const float* crow = a.cs + (int64_t)l * (HD_K / 2) + c0;
-    bf16* dst = (bf16*)a.kv + (((int64_t)b * a.H + head) * a.Lkp + l) * HD_K + c0;
+    bf16* dst = Q ? (bf16*)a.qp + ((int64_t)m * a.H + head) * HD_K + c0
+                  : (bf16*)a.kv + (((int64_t)b * a.H + head) * a.Lkp + l) * HD_K + c0;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      const f32x4 cv = *(const f32x4*)(crow + 8 * q), sv = *(const f32x4*)(crow + a.sin_off + 8 * q);
-      const f32x4 w0 = *(const f32x4*)(a.kn + c0 + 8 * q), w1 = *(const f32x4*)(a.kn + c0 + 64 + 8 * q);
       const f32x4 y0 = yf(i, 0, q), y1 = yf(i, 1, q);
+      f32x4 x1 = y0, x2 = y1;
+      if (norm) {
+        const f32x4 w0 = *(const f32x4*)(wn + c0 + 8 * q), w1 = *(const f32x4*)(wn + c0 + 64 + 8 * q);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          x1[e] = (y0[e] * rn) * w0[e];
+          x2[e] = (y1[e] * rn) * w1[e];
+        }
+      }
+      f32x4 r1 = x1, r2 = x2;
+      if (rope) {
+        const f32x4 cv = *(const f32x4*)(crow + 8 * q), sv = *(const f32x4*)(crow + a.sin_off + 8 * q);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          r1[e] = __builtin_fmaf(x1[e], cv[e], -(x2[e] * sv[e]));
+          r2[e] = __builtin_fmaf(x2[e], cv[e], x1[e] * sv[e]);
+        }
+      }
+      if (Q) {
+        r1 = r1 * a.qc;
+        r2 = r2 * a.qc;
+      }
       bf16x4 lo, hi;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        const float x1 = (y0[e] * rn) * w0[e];
-        const float x2 = (y1[e] * rn) * w1[e];
-        lo[e] = (bf16)__builtin_fmaf(x1, cv[e], -(x2 * sv[e]));
-        hi[e] = (bf16)__builtin_fmaf(x2, cv[e], x1 * sv[e]);
+        lo[e] = (bf16)r1[e];
+        hi[e] = (bf16)r2[e];
       }
       *(bf16x4*)(dst + 8 * q) = lo;
       *(bf16x4*)(dst + 64 + 8 * q) = hi;
@@ -664,7 +697,7 @@ __device__ __forceinline__ void g2_barrier() {
 
 constexpr int G2_LUT = G2_NST * G2_ST;  // W4 table offset in LDS (256 x 16 bytes)
 
-template <int EPI, bool W4, bool KV = false, bool LORA = false>
+template <int EPI, bool W4, bool KV = false, bool LORA = false, bool QP = false>
 __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
   static_assert(!KV || EPI == ANIMA_EPI_STORE, "the attention operand epilogue stores");
   __shared__ __attribute__((aligned(1024))) char smem[G2_NST * G2_ST + (W4 ? 4096 : 0) + (KV ? 4096 : 0)];
@@ -982,12 +1015,17 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
         const auto yf = [&](int i, int j, int q) {
           return f32x4{y[i][j][4 * q], y[i][j][4 * q + 1], y[i][j][4 * q + 2], y[i][j][4 * q + 3]};
         };
-        if (col0 < a.kcol) lora_store<ANIMA_EPI_STORE, 64>(a, y, m0, n0);
-        else if (col0 < a.vcol) kv_epi_k(a, yf, m0, n0, col0, wave, hf, lq, (float*)(smem + G2_NST * G2_ST + (W4 ? 4096 : 0)));
+        float* xch = (float*)(smem + G2_NST * G2_ST + (W4 ? 4096 : 0));
+        if (QP && col0 < a.kcol) kv_epi_k<true>(a, yf, m0, n0, col0, wave, hf, lq, xch);
+        else if (col0 < a.kcol) lora_store<ANIMA_EPI_STORE, 64>(a, y, m0, n0);
+        else if (col0 < a.vcol) kv_epi_k<false>(a, yf, m0, n0, col0, wave, hf, lq, xch);
         else kv_epi_v(a, yf, m0, n0, col0, wave, hf, lq);
       } else {
         const auto yf = [&](int i, int j, int q) { return kv_epi_y(a, acc[i][j], q, sxv[i], n0 + 64 * j); };
-        if (col0 < a.kcol) {
+        float* xch = (float*)(smem + G2_NST * G2_ST + (W4 ? 4096 : 0));
+        if (QP && col0 < a.kcol) {
+          kv_epi_k<true>(a, yf, m0, n0, col0, wave, hf, lq, xch);
+        } else if (col0 < a.kcol) {
           EpiCols cc;
           const f32x4 none[4] = {};
 #pragma unroll
@@ -997,7 +1035,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_256(GemmArgs a) {
             for (int i = 0; i < 4; i++) epi_store_t<ANIMA_EPI_STORE>(a, acc[i][j], m0 + 32 * i, n0 + 64 * j, sxv[i], cc, none);
           }
         } else if (col0 < a.vcol) {
-          kv_epi_k(a, yf, m0, n0, col0, wave, hf, lq, (float*)(smem + G2_NST * G2_ST + (W4 ? 4096 : 0)));
+          kv_epi_k<false>(a, yf, m0, n0, col0, wave, hf, lq, xch);
         } else {
           kv_epi_v(a, yf, m0, n0, col0, wave, hf, lq);
         }
@@ -2419,8 +2457,10 @@ int linear_qkv_launch(anima_ctx* c, const anima_linear_desc* d, const anima_qkv_
   if (p->B < 1 || p->L < 1 || H < 2 || H % 2 || (int64_t)p->B * p->L != M || M > 0x7fffffff)
     return fail(c, ANIMA_E_ARG, "anima_linear_qkv: B=%d L=%d H=%d M=%lld (M = B * L, H even)", p->B, p->L, H, (long long)M);
   if (p->L % 64) return fail(c, ANIMA_E_UNSUPPORTED, "anima_linear_qkv: L=%d must be a multiple of 64", p->L);
-  if (N != 3 * H * HD_K || K % GBK)
-    return fail(c, ANIMA_E_ARG, "anima_linear_qkv: N=%d must be 3 * H * 128 = %d, K %% %d == 0", N, 3 * H * HD_K, GBK);
+  const bool qonly = p->q_prep && N == H * HD_K;  // a Q-only projection (no K / V)
+  if ((N != 3 * H * HD_K && !qonly) || K % GBK)
+    return fail(c, ANIMA_E_ARG, "anima_linear_qkv: N=%d must be 3 * H * 128 = %d (or H * 128 with q_prep), K %% %d == 0", N,
+                3 * H * HD_K, GBK);
   if (d->epilogue != ANIMA_EPI_STORE || d->act != ANIMA_ACT_NONE || d->add || d->acc_out)
     return fail(c, ANIMA_E_UNSUPPORTED, "anima_linear_qkv: plain store only (no activation, residual, gate, add term or acc_out)");
   const bool lora = d->lora_xa || d->lora_b || d->lora_r;
@@ -2432,20 +2472,25 @@ int linear_qkv_launch(anima_ctx* c, const anima_linear_desc* d, const anima_qkv_
                   "that is a multiple of 256 (%d), ld_lora_xa %% 4 == 0 covering the ranks (%lld), 16-byte aligned",
                   d->lora_r, d->lora_cols, (long long)d->ld_lora_xa);
   }
-  if (!p->k_norm || !p->rope_cs || !p->kv_prep)
+  if (!qonly && (!p->k_norm || !p->rope_cs || !p->kv_prep))
     return fail(c, ANIMA_E_ARG, "anima_linear_qkv: k_norm, rope_cs and kv_prep are required");
-  if (p->kv_prep_bytes != attention_kv_bytes(p->B, H, p->L, ANIMA_PREC_BF16))
+  if (!qonly && p->kv_prep_bytes != attention_kv_bytes(p->B, H, p->L, ANIMA_PREC_BF16))
     return fail(c, ANIMA_E_ARG, "anima_linear_qkv: kv_prep_bytes=%lld, the layout takes %lld", (long long)p->kv_prep_bytes,
                 (long long)attention_kv_bytes(p->B, H, p->L, ANIMA_PREC_BF16));
-  const int64_t rows = p->rope_sin_off / (HD_K / 2);
-  if (p->rope_sin_off <= 0 || p->rope_sin_off % (HD_K / 2) || rows < p->L)
-    return fail(c, ANIMA_E_ARG, "anima_linear_qkv: rope_sin_off=%lld must be rows*64 with rows >= L=%d", (long long)p->rope_sin_off, p->L);
+  if (p->rope_cs) {
+    const int64_t rows = p->rope_sin_off / (HD_K / 2);
+    if (p->rope_sin_off <= 0 || p->rope_sin_off % (HD_K / 2) || rows < p->L)
+      return fail(c, ANIMA_E_ARG, "anima_linear_qkv: rope_sin_off=%lld must be rows*64 with rows >= L=%d", (long long)p->rope_sin_off, p->L);
+  }
+  if ((p->q_prep && !al(p->q_prep, 16)) || (p->q_norm && !al(p->q_norm, 16)) || (p->rope_cs && !al(p->rope_cs, 16)))
+    return fail(c, ANIMA_E_ARG, "anima_linear_qkv: q_prep, q_norm and rope_cs must be 16-byte aligned");
   const int64_t ldc = d->ldc ? d->ldc : N;
-  if (!d->out || ldc < H * HD_K) return fail(c, ANIMA_E_ARG, "anima_linear_qkv: out with ldc >= %d (the Q columns) required", H * HD_K);
+  if (!p->q_prep && (!d->out || ldc < H * HD_K))
+    return fail(c, ANIMA_E_ARG, "anima_linear_qkv: out with ldc >= %d (the Q columns) required", H * HD_K);
   if (!W->w || !W->scale || (W->kind == ANIMA_W_W4 && (!W->srel || !W->codebook)))
     return fail(c, ANIMA_E_ARG, "anima_linear_qkv: missing weight data, scale, s_rel or codebook");
   if (!al(W->w, 16) || !al(d->out, 16) || ldc % 4 || !al(W->scale, 16) || (W->bias && !al(W->bias, 16)) ||
-      !al(p->kv_prep, 16) || !al(p->k_norm, 16) || !al(p->rope_cs, 16))
+      !al(p->kv_prep, 16) || !al(p->k_norm, 16))
     return fail(c, ANIMA_E_ARG, "anima_linear_qkv: weight, out (ldc %% 4), scale, bias, kv_prep, k_norm and rope_cs must be 16-byte aligned");
   const int8_t* qx = d->xq;
   const float* sx = d->xs;
@@ -2482,8 +2527,14 @@ int linear_qkv_launch(anima_ctx* c, const anima_linear_desc* d, const anima_qkv_
   g.L = p->L;
   g.Lkp = p->L;
   g.H = H;
-  g.kcol = H * HD_K;
-  g.vcol = 2 * H * HD_K;
+  g.kcol = qonly ? N : H * HD_K;
+  g.vcol = qonly ? N : 2 * H * HD_K;
+  if (p->q_prep) {
+    g.qn = p->q_norm;
+    g.qp = (uint16_t*)p->q_prep;
+    g.qc = (p->q_scale != 0.0f ? p->q_scale : 1.0f / sqrtf((float)HD_K)) * 1.4426950408889634f;
+    g.qrope = p->rope_cs != nullptr;
+  }
   if (lora) {
     g.lx = d->lora_xa;
     g.ld_lx = d->ld_lora_xa;
@@ -2508,7 +2559,12 @@ int linear_qkv_launch(anima_ctx* c, const anima_linear_desc* d, const anima_qkv_
     // persistent 256 x 256 tiles (a tile holds two whole heads); one workgroup per CU at most
     const int64_t tiles = (int64_t)(N / 256) * ((M + 255) / 256);
     const dim3 grid((unsigned)(tiles < c->num_cus ? tiles : c->num_cus)), block(512);
-    if (lora) hipLaunchKernelGGL((gemm_i8_256<ANIMA_EPI_STORE, false, true, true>), grid, block, 0, c->stream, g);
+    // (the prepared-Q epilogue is an instance of its own: its code raises the register pressure of
+    // the main loop it shares the kernel with)
+    if (lora && g.qp) hipLaunchKernelGGL((gemm_i8_256<ANIMA_EPI_STORE, false, true, true, true>), grid, block, 0, c->stream, g);
+    else if (lora) hipLaunchKernelGGL((gemm_i8_256<ANIMA_EPI_STORE, false, true, true>), grid, block, 0, c->stream, g);
+    else if (g.qp && w4) hipLaunchKernelGGL((gemm_i8_256<ANIMA_EPI_STORE, true, true, false, true>), grid, block, 0, c->stream, g);
+    else if (g.qp) hipLaunchKernelGGL((gemm_i8_256<ANIMA_EPI_STORE, false, true, false, true>), grid, block, 0, c->stream, g);
     else if (w4) hipLaunchKernelGGL((gemm_i8_256<ANIMA_EPI_STORE, true, true>), grid, block, 0, c->stream, g);
     else hipLaunchKernelGGL((gemm_i8_256<ANIMA_EPI_STORE, false, true>), grid, block, 0, c->stream, g);
     rc = L.end();

@@ -683,7 +683,7 @@ static const struct {
     ABI_FIELD(anima_attn_desc, kv_len), ABI_FIELD(anima_attn_desc, precision), ABI_FIELD(anima_attn_desc, q_norm),
     ABI_FIELD(anima_attn_desc, k_norm), ABI_FIELD(anima_attn_desc, rope_cs), ABI_FIELD(anima_attn_desc, rope_sin_off),
     ABI_FIELD(anima_attn_desc, eps), ABI_FIELD(anima_attn_desc, causal), ABI_FIELD(anima_attn_desc, kv_prep),
-    ABI_FIELD(anima_attn_desc, kv_prep_bytes),
+    ABI_FIELD(anima_attn_desc, kv_prep_bytes), ABI_FIELD(anima_attn_desc, q_prep),
     ABI_SIZE(anima_weight), ABI_FIELD(anima_weight, kind), ABI_FIELD(anima_weight, N), ABI_FIELD(anima_weight, K),
     ABI_FIELD(anima_weight, w), ABI_FIELD(anima_weight, scale), ABI_FIELD(anima_weight, srel),
     ABI_FIELD(anima_weight, codebook), ABI_FIELD(anima_weight, bias),
@@ -712,6 +712,7 @@ static const struct {
     ABI_SIZE(anima_qkv_desc), ABI_FIELD(anima_qkv_desc, B), ABI_FIELD(anima_qkv_desc, L), ABI_FIELD(anima_qkv_desc, H),
     ABI_FIELD(anima_qkv_desc, k_norm), ABI_FIELD(anima_qkv_desc, rope_cs), ABI_FIELD(anima_qkv_desc, rope_sin_off),
     ABI_FIELD(anima_qkv_desc, eps), ABI_FIELD(anima_qkv_desc, kv_prep), ABI_FIELD(anima_qkv_desc, kv_prep_bytes),
+    ABI_FIELD(anima_qkv_desc, q_norm), ABI_FIELD(anima_qkv_desc, q_prep), ABI_FIELD(anima_qkv_desc, q_scale),
 };
 #undef ABI_FIELD
 #undef ABI_SIZE

@@ -538,6 +538,7 @@ static napi_value js_attention(napi_env env, napi_callback_info info) {
   d.causal = (int)pnum(env, o, "causal");
   d.kv_prep = pptr(env, o, "kvPrep");
   d.kv_prep_bytes = (int64_t)pnum(env, o, "kvPrepBytes");
+  d.q_prep = pptr(env, o, "qPrep");
   void* prepare_into = pptr(env, o, "prepareInto"); /* run anima_attention_prepare_kv into it */
   int kv[64];
   napi_value kvl = prop(env, o, "kvLen");
@@ -794,6 +795,9 @@ static napi_value js_linear_qkv(napi_env env, napi_callback_info info) {
   q.eps = (float)pnum(env, k, "eps");
   q.kv_prep = pptr(env, k, "kvPrep");
   q.kv_prep_bytes = (int64_t)pnum(env, k, "kvPrepBytes");
+  q.q_norm = (const float*)pptr(env, k, "qNorm");
+  q.q_prep = pptr(env, k, "qPrep");
+  q.q_scale = (float)pnum(env, k, "qScale");
   CHECK_RC(env, c, anima_linear_qkv(c, &d, &q));
   return NULL;
 }

@@ -171,6 +171,11 @@ typedef struct {
    * anima_attention_kv_bytes(B, H / group, Lk, precision) -- a buffer prepared for another shape or
    * precision is rejected instead of being read past its end. */
   int64_t kv_prep_bytes;
+  /* Optional: Q as anima_linear_qkv's q_prep writes it (bf16 [B][Lq][H][128], the query after
+   * q_norm and RoPE times scale * log2(e)); then q, ldq, q_off, q_bstride, q_norm and the query
+   * side of rope_cs are not read, and the attention's scale is the one Q was prepared with.  bf16
+   * precision and D = 128 only; the results equal those of the fp32 q with q_norm / rope_cs. */
+  const void* q_prep;
 } anima_attn_desc;
 
 /* ops.attention (app/gpu/ops.js:166-208) on the flash path (kernels.js:158-299), plus the fused
@@ -428,15 +433,18 @@ int anima_linear(anima_ctx* ctx, const anima_linear_desc* desc);
  * epilogue: app/models/dit.js:266-304 runs ops.linear (qkv), ops.qkNormRope (q and k in place) and
  * the flash attention, whose operands this library converts first (anima_attention_prepare_kv).
  * Here the GEMM that produces qkv writes, per token,
- *   Q  columns [0, 128 H)        fp32 into d->out (row stride d->ldc >= 128 H), as anima_linear;
+ *   Q  columns [0, 128 H)        fp32 into d->out (row stride d->ldc >= 128 H), as anima_linear,
+ *                                or with q_prep the attention's prepared bf16 Q (below);
  *   K  columns [128 H, 256 H)    RMSNorm(k_norm, eps) + RoPE (rope_cs, as anima_attn_desc), bf16,
  *   V  columns [256 H, 384 H)    bf16, transposed,
  * K and V into kv_prep in the layout of anima_attention_prepare_kv(B, Lq = Lk = L, H heads,
  * bf16) -- the same bytes, bit for bit, as preparing this linear's fp32 output -- for
  * anima_attention(desc->kv_prep = kv_prep) with q = d->out, q_norm and the same RoPE table.
- * Requirements: int8 or W4 weights with N = 3 * 128 * H (H even), the store epilogue (bias and
- * alpha allowed; no activation, add term or acc_out), M = B * L with L % 64 == 0, 16-byte aligned
- * buffers; ANIMA_E_UNSUPPORTED otherwise (the caller then runs anima_linear + anima_attention). */
+ * Requirements: int8 or W4 weights with N = 3 * 128 * H (H even; or 128 * H with q_prep), the
+ * store epilogue (bias and alpha allowed; no activation, add term or acc_out; the LoRA factors of
+ * anima_linear_desc with rank blocks of whole 256-column tiles), M = B * L with L % 64 == 0,
+ * 16-byte aligned buffers; ANIMA_E_UNSUPPORTED otherwise (the caller then runs anima_linear +
+ * anima_attention). */
 typedef struct {
   int B, L, H;          /* batch elements, tokens each (M = B * L), heads of 128 */
   const float* k_norm;  /* [128] */
@@ -445,6 +453,14 @@ typedef struct {
   float eps;
   void* kv_prep;        /* anima_attention_kv_bytes(B, H, L, ANIMA_PREC_BF16) bytes */
   int64_t kv_prep_bytes;
+  /* Optional: Q in the attention's prepared form (anima_attn_desc.q_prep) instead of fp32 into
+   * out: B * L * H * 128 bf16 values, each the attention's own bf16(scale * log2(e) * q') of the
+   * query q' after q_norm (if given) and RoPE (if rope_cs is given); q_scale 0 -> 1 / sqrt(128).
+   * With q_prep, N may also be H * 128 (a Q-only projection: no K / V, kv_prep and k_norm unused,
+   * rope_cs optional). */
+  const float* q_norm;
+  void* q_prep;
+  float q_scale;
 } anima_qkv_desc;
 int anima_linear_qkv(anima_ctx* ctx, const anima_linear_desc* desc, const anima_qkv_desc* qkv);
 

@@ -171,6 +171,95 @@ def test_linear_qkv_lora(ctx, kind, cols):
         x.release()
 
 
+@pytest.mark.parametrize("kind,Hp,Wp", [("i8", 32, 32), ("w4", 33, 64), ("i8", 33, 64)])
+def test_linear_qkv_prepared_q(ctx, kind, Hp, Wp):
+    """Q prepared by the QKV epilogue (anima_qkv_desc q_prep: RMSNorm, RoPE, the attention's
+    scale * log2(e), bf16): the attention on it equals the attention on the plain fp32 Q with
+    q_norm + RoPE bit for bit (32 x 32 tokens: the 4-wave kernel; 33 x 64: the 8-wave kernel with
+    a partial last query tile), and each prepared value is within bf16 rounding of float64."""
+    case(f"linear_qkv prepared Q {kind} {Hp}x{Wp}")
+    m = amd()
+    B, H, K = 2, 16, 2048
+    L = Hp * Wp
+    M, N = B * L, 3 * H * HD
+    W, wbufs = make_weight(ctx, m, kind, 880 + Hp, N, K, True)
+    rng = np.random.default_rng(881)
+    xq = ctx.upload(rng.integers(-127, 128, size=(M, K), dtype=np.int8))
+    xs = ctx.upload(rng.uniform(0.002, 0.02, M).astype(np.float32))
+    qn = (1 + 0.02 * orc.randn(882, HD)).astype(np.float32)
+    kn = (1 + 0.02 * orc.randn(883, HD)).astype(np.float32)
+    cs_np = orc.dit_rope_table(Hp, Wp)
+    dqn, dkn, dcs = ctx.upload(qn), ctx.upload(kn), ctx.upload(cs_np)
+    sin_off = L * 64
+    nbytes = m.Context.attention_kv_bytes(B, H, L, m.PREC_BF16)
+    ref = ctx.empty((M, N))
+    ctx.linear(W, M, ref, xq=xq, xs=xs)
+    prep_ref = ctx.empty(nbytes, np.uint8)
+    common = dict(B=B, Lq=L, Lk=L, H=H, D=HD, ldq=N, ldk=N, ldv=N, precision=m.PREC_BF16, rope_cs=dcs,
+                  rope_sin_off=sin_off)
+    ctx.attention(q=ref, k=ref, v=ref, o=ref, prepare_into=prep_ref, k_norm=dkn, k_off=H * HD, v_off=2 * H * HD,
+                  **common)
+    qp = ctx.empty(M * H * HD, np.uint16)
+    prep = ctx.empty(nbytes, np.uint8)
+    ctx.linear_qkv(W, M, None, B=B, L=L, H=H, k_norm=dkn, rope_cs=dcs, rope_sin_off=sin_off, kv_prep=prep, xq=xq,
+                   xs=xs, q_norm=dqn, q_prep=qp)
+    assert np.array_equal(prep.numpy(), prep_ref.numpy())
+    o1, o2 = ctx.empty((M, H * HD)), ctx.empty((M, H * HD))
+    ctx.attention(q=ref, k=None, v=None, o=o1, kv_prep=prep_ref, q_norm=dqn, **common)
+    ctx.attention(q=None, k=None, v=None, o=o2, kv_prep=prep, q_prep=qp, **common)
+    a1, a2 = o1.numpy(), o2.numpy()
+    print(f"attention outputs differing: {int((a1 != a2).sum())} of {a1.size}", flush=True)
+    assert np.array_equal(a1, a2)
+    # prepared values against float64 (RMSNorm, RoPE, scale * log2 e), sampled rows
+    r = ref.numpy()
+    rows = np.unique(np.concatenate([np.arange(0, 4), rng.choice(M, 16, replace=False), np.arange(M - 4, M)]))
+    q64 = r[rows, :H * HD].astype(np.float64).reshape(len(rows), H, HD)
+    q64 = q64 / np.sqrt((q64 * q64).mean(-1, keepdims=True) + 1e-6) * qn.astype(np.float64)
+    li = rows % L
+    c = cs_np[:L * 64].reshape(L, 64).astype(np.float64)[li][:, None, :]
+    sn = cs_np[sin_off:sin_off + L * 64].reshape(L, 64).astype(np.float64)[li][:, None, :]
+    lo, hi = q64[..., :64], q64[..., 64:]
+    want = np.concatenate([lo * c - hi * sn, hi * c + lo * sn], -1) * (np.log2(np.e) / np.sqrt(HD))
+    got = bf16_to_f32(qp.numpy().reshape(M, H, HD)[rows])
+    err = np.abs(got - want) / np.maximum(np.abs(want), 1e-3)
+    assert err.max() <= 2.0 ** -8 + 1e-5, err.max()
+    for x in wbufs + [xq, xs, dqn, dkn, dcs, ref, prep_ref, qp, prep, o1, o2]:
+        x.release()
+
+
+def test_linear_q_only_prepared(ctx):
+    """A Q-only projection (W of H * 128 columns, anima_qkv_desc q_prep without K / V or RoPE: the
+    cross-attention's q) feeding the attention against prepared K / V of 512 context keys (ragged
+    kv_len): bit-identical to the plain linear + attention with q_norm."""
+    case("linear_qkv Q-only prepared Q (cross-attention)")
+    m = amd()
+    B, L, H, K, Lk = 2, 4096, 16, 2048, 512
+    M, N = B * L, H * HD
+    W, wbufs = make_weight(ctx, m, "i8", 890, N, K, True)
+    rng = np.random.default_rng(891)
+    xq = ctx.upload(rng.integers(-127, 128, size=(M, K), dtype=np.int8))
+    xs = ctx.upload(rng.uniform(0.002, 0.02, M).astype(np.float32))
+    dqn = ctx.upload((1 + 0.02 * orc.randn(892, HD)).astype(np.float32))
+    kv = ctx.upload(orc.randn(893, B * Lk * N).reshape(B * Lk, N))
+    kv_len = [458, 263]
+    nbytes = m.Context.attention_kv_bytes(B, H, Lk, m.PREC_BF16)
+    prep = ctx.empty(nbytes, np.uint8)
+    common = dict(B=B, Lq=L, Lk=Lk, H=H, D=HD, ldq=N, ldk=N, ldv=N, precision=m.PREC_BF16, kv_len=kv_len)
+    ctx.attention(q=kv, k=kv, v=kv, o=kv, prepare_into=prep, **dict(common, Lq=Lk))
+    q = ctx.empty((M, N))
+    ctx.linear(W, M, q, xq=xq, xs=xs)
+    qp = ctx.empty(M * N, np.uint16)
+    ctx.linear_qkv(W, M, None, B=B, L=L, H=H, xq=xq, xs=xs, q_norm=dqn, q_prep=qp)
+    o1, o2 = ctx.empty((M, N)), ctx.empty((M, N))
+    ctx.attention(q=q, k=None, v=None, o=o1, kv_prep=prep, q_norm=dqn, **common)
+    ctx.attention(q=None, k=None, v=None, o=o2, kv_prep=prep, q_prep=qp, **common)
+    a1, a2 = o1.numpy(), o2.numpy()
+    print(f"attention outputs differing: {int((a1 != a2).sum())} of {a1.size}", flush=True)
+    assert np.array_equal(a1, a2)
+    for x in wbufs + [xq, xs, dqn, kv, prep, q, qp, o1, o2]:
+        x.release()
+
+
 def test_linear_qkv_refusals(ctx):
     """Shapes the fused epilogue does not cover are refused on the host before any launch:
     L % 64 != 0 (ANIMA_E_UNSUPPORTED), a wrong operand buffer size, N != 3 * 128 * H and LoRA
