@@ -542,7 +542,8 @@ __device__ __forceinline__ void kv_epi_k(const GemmArgs& a, const YF& yf, int m0
   const bool norm = !Q || wn, rope = !Q || a.qrope;  // (uniform over the workgroup)
   // One 32-row block at a time: the partial sum of squares over this lane pair's 64 columns goes
   // to LDS, a barrier, the partner wave's partial completes the row, and the block's values are
-  // recomputed (the same fp32 bits), normalized, rotated, rounded and stored.
+  // recomputed (the same fp32 bits), normalized, rotated, rounded and stored.  (One barrier for all
+  // four blocks keeps the first pass's values alive into the second: the spills cost more.)
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     float rn = 1.0f;

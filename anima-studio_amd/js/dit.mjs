@@ -399,11 +399,12 @@ export class AnimaDiT {
       let a;
       if (b.self.qkv && this.fuseQkv && this.precision === "bf16" && ops.qkvFusable(b.self.qkv, L, HEADS)) {
         nf = normFor(gpu, x, m.self, b.self.qkv);
-        const f = ops.linearQkv(gpu, null, b.self.qkv, { B, L, H: HEADS, xq: nf.xq, xr: nf.xq.xr, kNorm: b.self.kn, cs });
+        const f = ops.linearQkv(gpu, null, b.self.qkv, { B, L, H: HEADS, xq: nf.xq, xr: nf.xq.xr, kNorm: b.self.kn, cs,
+          qNorm: b.self.qn, prepareQ: true });
         releaseNorm(nf);
-        a = ops.attention(gpu, { q: f.q, kvPrep: f.kvPrep, B, Lq: L, Lk: L, H: HEADS, D: HD, ldq: D, qNorm: b.self.qn,
-          cs, precision: "bf16" });
-        f.q.release();
+        a = ops.attention(gpu, { qPrep: f.qPrep, kvPrep: f.kvPrep, B, Lq: L, Lk: L, H: HEADS, D: HD, ldq: D,
+          precision: "bf16" });
+        f.qPrep.release();
         f.kvPrep.release();
       } else {
         let qkv;
@@ -421,14 +422,24 @@ export class AnimaDiT {
       ops.linear(gpu, a, b.self.o, { M, out: x, resid: true, gate: m.self, gOff: 2 * D });
       a.release();
 
-      // cross-attention against the per-prompt cached keys/values (q RMSNorm fused, no RoPE)
+      // cross-attention against the per-prompt cached keys/values (q RMSNorm fused, no RoPE).  With
+      // an int8 / W4 q projection (no LoRA) and bf16 attention, the GEMM's epilogue writes Q as the
+      // attention's prepared operand (RMS-normed, scaled, bf16).
       nf = normFor(gpu, x, m.cross, b.cross.q);
-      const q = project(gpu, nf, b.cross.q, M);
-      releaseNorm(nf);
       const kv = cond.kv[i];
-      a = ops.attention(gpu, { q, kvPrep: kv.prep, B, Lq: L, Lk: cond.Lk, H: HEADS, D: HD, ldq: D, qNorm: b.cross.qn,
-        precision: cond.precision });
-      q.release();
+      if (this.fuseQkv && cond.precision === "bf16" && ops.qFusable(b.cross.q, L, HEADS)) {
+        const f = ops.linearQkv(gpu, null, b.cross.q, { B, L, H: HEADS, xq: nf.xq, qNorm: b.cross.qn, prepareQ: true });
+        releaseNorm(nf);
+        a = ops.attention(gpu, { qPrep: f.qPrep, kvPrep: kv.prep, B, Lq: L, Lk: cond.Lk, H: HEADS, D: HD, ldq: D,
+          precision: "bf16" });
+        f.qPrep.release();
+      } else {
+        const q = project(gpu, nf, b.cross.q, M);
+        releaseNorm(nf);
+        a = ops.attention(gpu, { q, kvPrep: kv.prep, B, Lq: L, Lk: cond.Lk, H: HEADS, D: HD, ldq: D, qNorm: b.cross.qn,
+          precision: cond.precision });
+        q.release();
+      }
       ops.linear(gpu, a, b.cross.o, { M, out: x, resid: true, gate: m.cross, gOff: 2 * D });
       a.release();
 

@@ -171,14 +171,25 @@ export function qkvFusable(W, L, H, withLora) {
   return needsRotation(W) && L % 64 === 0 && H % 2 === 0 && W.N === 3 * H * 128;
 }
 
+// A Q-only projection for linearQkv(..., { prepareQ: true }): int8 / W4 weights of H * 128
+// columns without LoRAs, tokens per image a multiple of 64.
+export function qFusable(W, L, H) {
+  return needsRotation(W) && !(W.lora && W.lora.length) && L % 64 === 0 && W.N === H * 128;
+}
+
 export function linearQkv(gpu, x, W, opts) {
   const o = opts || {};
   const { B, L, H } = o;
   const M = B * L;
-  const q = gpu.empty([M, H * 128]);
-  const bytes = native.attentionKvBytes(B, H, L, 0);
-  const kvPrep = gpu.empty([bytes], "u8");
-  const d = { M, out: q.buf, ldc: H * 128, alpha: o.alpha || 0 };
+  // opts.prepareQ: Q as the attention's prepared bf16 operand (opts.qNorm, the RoPE of opts.cs,
+  // opts.scale) in qPrep instead of fp32 in q; a weight of H * 128 columns is then a Q-only
+  // projection (no K / V)
+  const qOnly = !!o.prepareQ && W.N === H * 128;
+  const q = o.prepareQ ? null : gpu.empty([M, H * 128]);
+  const qPrep = o.prepareQ ? gpu.empty([M * H * 128 * 2], "u8") : null;
+  const bytes = qOnly ? 0 : native.attentionKvBytes(B, H, L, 0);
+  const kvPrep = qOnly ? null : gpu.empty([bytes], "u8");
+  const d = { M, out: q ? q.buf : 0, ldc: H * 128, alpha: o.alpha || 0 };
   if (o.xq) {
     d.xq = o.xq.q.buf;
     d.xs = o.xq.s.buf;
@@ -192,10 +203,11 @@ export function linearQkv(gpu, x, W, opts) {
   const down = F ? linear(gpu, o.xr, { kind: "f32s3", N: F.R, K: W.K, buf: F.Ars }, { M }) : null;
   if (F) Object.assign(d, { loraXa: down.buf, ldLoraXa: F.R, loraB: F.Bs.buf, loraR: F.Rb, loraCols: F.cols });
   const w = weightArg(W);
-  native.linearQkv(gpu.ctx, w, d, { B, L, H, kNorm: o.kNorm.buf, cs: o.cs.buf, sinOff: o.cs.sinOff, eps: o.eps || 1e-6,
-    kvPrep: kvPrep.buf, kvPrepBytes: bytes });
+  native.linearQkv(gpu.ctx, w, d, { B, L, H, kNorm: ptr(o.kNorm), cs: ptr(o.cs), sinOff: o.cs ? o.cs.sinOff : 0,
+    eps: o.eps || 1e-6, kvPrep: ptr(kvPrep), kvPrepBytes: bytes, qNorm: ptr(o.qNorm), qPrep: ptr(qPrep),
+    qScale: o.scale || 0 });
   if (down) down.release();
-  return { q, kvPrep };
+  return { q, qPrep, kvPrep };
 }
 
 // Adds (or, storeFirst, stores where it comes first over a column range) every LoRA entry's
@@ -335,6 +347,8 @@ export function elementwise(gpu, op, a, b, out) {
 //  q: [Lq, ldq] with head h at column qOff + h*D; k, v: [Lk, ldk]/[Lk, ldv] with kv head
 //  h/group at kOff/vOff + (h/group)*D.  Output [B*Lq, H*D].
 // a.kvPrep: K/V converted beforehand by attentionPrepareKV (then a.k / a.v are not needed).
+// a.qPrep: Q prepared by linearQkv(..., { prepareQ: true }) (then a.q, a.qNorm and the query side
+// of a.cs are not needed; bf16 precision, D = 128).
 // a.precision: "fp32" (default, the reference's arithmetic) or "bf16" (bf16 matrix-core operands,
 // fp32 accumulation: the DiT's and the text encoder's choice).
 export function attention(gpu, a) {
@@ -367,10 +381,10 @@ function precisionId(a) {
 function attnDesc(a, B, H, D, o, extra) {
   return Object.assign({
     B, Lq: a.Lq, Lk: a.Lk, H, D, group: a.group || 1,
-    q: a.q.buf, k: a.k ? a.k.buf : 0, v: a.v ? a.v.buf : 0, o: o.buf,
+    q: a.q ? a.q.buf : 0, k: a.k ? a.k.buf : 0, v: a.v ? a.v.buf : 0, o: o.buf, qPrep: ptr(a.qPrep),
     ldq: a.ldq, ldk: a.ldk, ldv: a.ldv, ldo: a.ldo || H * D,
     qOff: a.qOff || 0, kOff: a.kOff || 0, vOff: a.vOff || 0, oOff: a.oOff || 0,
-    qBatch: a.qBatch !== undefined ? a.qBatch : a.Lq * a.ldq,
+    qBatch: a.qBatch !== undefined ? a.qBatch : a.q ? a.Lq * a.ldq : 0,
     // no k / v (prepared K/V): their strides are not read
     kBatch: a.kBatch !== undefined ? a.kBatch : a.k ? a.Lk * a.ldk : 0,
     vBatch: a.vBatch !== undefined ? a.vBatch : a.v ? a.Lk * a.ldv : 0,
