@@ -1219,6 +1219,10 @@ struct F32WArgs {
   int wf32;  // fp32 weights (tile kernel only)
   int64_t ldw = 0;  // weight row stride (0: K); the split-k LDS kernel reads k-slices of longer rows
   int64_t wplane = 0;  // split weights: plane stride in elements (set by the host, N * K unless a row block)
+  // split weights over per-token int8 activations (x unused): q [M][ldx] bytes, s [M] row scales,
+  // y = s[m] * sum_k q[m][k] W[n][k]
+  const int8_t* xq = nullptr;
+  const float* xs = nullptr;
 };
 
 // 64x64 tile, 256 threads x (4x4) outputs, k-tile 16 (the small-tile layout of gemm.js:17).
@@ -1572,40 +1576,67 @@ __device__ __forceinline__ f32x4 mfma16_s3(const bf16x8 (&a)[3], const bf16x8 (&
 }
 
 constexpr int TK_WAVES = 8;
-constexpr int TK_XB = 32 * 128;  // one wave's x step tile: 32 rows x 32 fp32
+constexpr int TK_XB = 32 * 128;  // one wave's x step tile: 32 rows x 32 fp32 (int8 x: 32 rows x 32 bytes)
 
 // Per-lane DMA state of gemm_s3_tall_kernel: x instruction i covers rows 8 i .. 8 i + 7 of the wave
 // (lane -> row 8 i + lane / 8, piece slot lane % 8 holding k-piece (slot ^ row) % 8 of 4 fp32); W
 // instruction t covers plane t / CT, rows 16 (t % CT) .. + 15 (lane -> row + lane / 4, slot
 // lane % 4 holding k-piece slot ^ ((row / 2) % 4) of 8 bf16), issued by wave t % TK_WAVES.
-template <int RT>
+// int8 x (Q8): one instruction for the wave's 32 rows x 32 bytes, lane -> row lane / 2, slot
+// lane % 2 holding the row's 16-byte half (slot ^ q8_swz(row)).
+template <int RT, bool Q8>
 struct TallDma {
-  static constexpr int CT = 2 * RT, WI = (6 * RT + TK_WAVES - 1) / TK_WAVES;
+  static constexpr int CT = 2 * RT, WI = (6 * RT + TK_WAVES - 1) / TK_WAVES, XI = Q8 ? 1 : 4;
+  static constexpr int XB = Q8 ? 1024 : TK_XB;  // one wave's x bytes per step
   __amdgpu_buffer_rsrc_t rx, rw;
-  int xo[4], xk[4], wo[WI], wk[WI];
+  int xo[XI], xk[XI], wo[WI], wk[WI];
 };
+
+// the 16-byte halves of rows 8 .. 15 (mod 16) trade places, so that a half-wave's 8-byte reads
+// (16 rows, two k-groups) touch every bank once
+__device__ __forceinline__ int q8_swz(int row) { return (row >> 3) & 1; }
 
 // One step's copies into `buf` (restrict: the compiler then tells them apart from the operand
 // reads of the other buffer and does not make those reads wait for them).
-template <int RT>
-__device__ __forceinline__ void tall_issue(const TallDma<RT>& d, char* __restrict__ buf, int k0, int K, int wave) {
+template <int RT, bool Q8>
+__device__ __forceinline__ void tall_issue(const TallDma<RT, Q8>& d, char* __restrict__ buf, int k0, int K, int wave) {
+  using D = TallDma<RT, Q8>;
 #pragma unroll
-  for (int i = 0; i < 4; i++)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rx, (lds_void_t*)(buf + wave * TK_XB + i * 1024), 16,
-                                             k0 + d.xk[i] < K ? d.xo[i] + 4 * k0 : 0x7ffffff0, 0, 0, 0);
+  for (int i = 0; i < D::XI; i++)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rx, (lds_void_t*)(buf + wave * D::XB + i * 1024), 16,
+                                             k0 + d.xk[i] < K ? d.xo[i] + (Q8 ? 1 : 4) * k0 : 0x7ffffff0, 0, 0, 0);
 #pragma unroll
-  for (int j = 0; j < TallDma<RT>::WI; j++) {
+  for (int j = 0; j < D::WI; j++) {
     const int t = wave + TK_WAVES * j;
     if (t < 6 * RT)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rw, (lds_void_t*)(buf + TK_WAVES * TK_XB + t * 1024), 16,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rw, (lds_void_t*)(buf + TK_WAVES * D::XB + t * 1024), 16,
                                                k0 + d.wk[j] < K ? d.wo[j] + 2 * k0 : 0x7ffffff0, 0, 0, 0);
   }
 }
 
+// eight int8 values as bf16 (exact: at most 8 significant bits)
+__device__ __forceinline__ bf16x8 i8x8_bf16(uint32_t lo, uint32_t hi) {
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    o[e] = (bf16)(float)(int8_t)(lo >> (8 * e));
+    o[4 + e] = (bf16)(float)(int8_t)(hi >> (8 * e));
+  }
+  return o;
+}
+
+// acc += sum_j a b_j on the 16x16x32 shape (a exact in bf16), smallest terms first
+__device__ __forceinline__ f32x4 mfma16_q3(const bf16x8& a, const bf16x8 (&b)[3], f32x4 acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[1], acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[0], acc, 0, 0, 0);
+}
+
 // One step's operand reads from `buf` and its products (lane (r16, g): x row 16 i + r16, W row
 // 16 t + r16, k = 8 g .. 8 g + 7 of the step on both operands).
-template <int RT>
+template <int RT, bool Q8>
 __device__ __forceinline__ void tall_step(const char* __restrict__ buf, int wave, int r16, int g, f32x4 (&acc)[2][2 * RT]) {
+  using D = TallDma<RT, Q8>;
   constexpr int CT = 2 * RT;
   bf16x8 wv[CT][3];
 #pragma unroll
@@ -1613,22 +1644,32 @@ __device__ __forceinline__ void tall_step(const char* __restrict__ buf, int wave
     const int row = 16 * t + r16;
 #pragma unroll
     for (int p = 0; p < 3; p++)
-      wv[t][p] = *(const bf16x8*)(buf + TK_WAVES * TK_XB + p * CT * 1024 + row * 64 + 16 * (g ^ ((row >> 1) & 3)));
+      wv[t][p] = *(const bf16x8*)(buf + TK_WAVES * D::XB + p * CT * 1024 + row * 64 + 16 * (g ^ ((row >> 1) & 3)));
   }
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     const int row = 16 * i + r16;
-    const char* xr = buf + wave * TK_XB + row * 128;
-    // whole 16-byte reads: split into scalar loads and merged again, the reads lose the alias
-    // information that keeps them from waiting on the other buffer's copies
-    f32x4 v0 = *(const f32x4*)(xr + 16 * ((2 * g) ^ (row & 7)));
-    f32x4 v1 = *(const f32x4*)(xr + 16 * ((2 * g + 1) ^ (row & 7)));
-    asm volatile("" : "+v"(v0), "+v"(v1));
-    const float4 x0 = make_float4(v0[0], v0[1], v0[2], v0[3]), x1 = make_float4(v1[0], v1[1], v1[2], v1[3]);
-    bf16x8 xs[3];
-    split3(x0, x1, xs);
+    if constexpr (Q8) {
+      const char* xr = buf + wave * D::XB + 16 * (2 * row + ((g >> 1) ^ q8_swz(row))) + 8 * (g & 1);
+      typedef int i32x2 __attribute__((ext_vector_type(2)));
+      i32x2 v = *(const i32x2*)xr;
+      asm volatile("" : "+v"(v));
+      const bf16x8 xb = i8x8_bf16((uint32_t)v[0], (uint32_t)v[1]);
 #pragma unroll
-    for (int t = 0; t < CT; t++) acc[i][t] = mfma16_s3(xs, wv[t], acc[i][t]);
+      for (int t = 0; t < CT; t++) acc[i][t] = mfma16_q3(xb, wv[t], acc[i][t]);
+    } else {
+      const char* xr = buf + wave * D::XB + row * 128;
+      // whole 16-byte reads: split into scalar loads and merged again, the reads lose the alias
+      // information that keeps them from waiting on the other buffer's copies
+      f32x4 v0 = *(const f32x4*)(xr + 16 * ((2 * g) ^ (row & 7)));
+      f32x4 v1 = *(const f32x4*)(xr + 16 * ((2 * g + 1) ^ (row & 7)));
+      asm volatile("" : "+v"(v0), "+v"(v1));
+      const float4 x0 = make_float4(v0[0], v0[1], v0[2], v0[3]), x1 = make_float4(v1[0], v1[1], v1[2], v1[3]);
+      bf16x8 xs[3];
+      split3(x0, x1, xs);
+#pragma unroll
+      for (int t = 0; t < CT; t++) acc[i][t] = mfma16_s3(xs, wv[t], acc[i][t]);
+    }
   }
 }
 
@@ -1644,10 +1685,14 @@ __device__ __forceinline__ void tall_step(const char* __restrict__ buf, int wave
 // partial sums [slice][M][N]; s3_ksum_kernel adds them in slice order (deterministic) and applies
 // the epilogue.  Offsets past a buffer's end read zeros: the k tail and rows past M.  A row of W
 // past N reads other rows' data (or zeros) and feeds only columns that are never stored.
-template <int RT>
+// Q8: x is per-token int8 (a.xq, row stride a.ldx bytes, K % 16 == 0), each wave's 32 rows x 32
+// bytes one copy per step, the bytes widened to bf16 (exact) for three MFMAs per tile against the
+// three planes; the sum pass applies the row scales a.xs.
+template <int RT, bool Q8>
 __global__ __launch_bounds__(64 * TK_WAVES) void gemm_s3_tall_kernel(F32WArgs a, float* part, int spb) {
+  using D = TallDma<RT, Q8>;
   constexpr int CT = 2 * RT;
-  constexpr int BUF = TK_WAVES * TK_XB + 3 * CT * 1024;
+  constexpr int BUF = TK_WAVES * D::XB + 3 * CT * 1024;
   // step buffers: as many as fit in LDS (up to 4), so that up to TD - 1 steps' copies are in
   // flight behind the one being computed
   constexpr int TD = 160 * 1024 / BUF < 4 ? 160 * 1024 / BUF : 4;
@@ -1660,17 +1705,24 @@ __global__ __launch_bounds__(64 * TK_WAVES) void gemm_s3_tall_kernel(F32WArgs a,
   // turn every load into a loop over the lanes' distinct values)
   const int rows = __builtin_amdgcn_readfirstlane(a.M - m0 < 0 ? 0 : a.M - m0 < 32 ? a.M - m0 : 32);
   const int mb = __builtin_amdgcn_readfirstlane(rows ? m0 : 0);
-  TallDma<RT> d;
-  d.rx = __builtin_amdgcn_make_buffer_rsrc((void*)(a.x + (int64_t)mb * a.ldx), (short)0, rows * (int)a.ldx * 4, 0x00020000);
+  D d;
   d.rw = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)(2 * (2 * a.wplane + (int64_t)a.N * a.K)), 0x00020000);
+  if constexpr (Q8) {
+    d.rx = __builtin_amdgcn_make_buffer_rsrc((void*)(a.xq + (int64_t)mb * a.ldx), (short)0, rows * (int)a.ldx, 0x00020000);
+    const int row = lane >> 1, h = (lane & 1) ^ q8_swz(row);
+    d.xk[0] = 16 * h;
+    d.xo[0] = row * (int)a.ldx + 16 * h;
+  } else {
+    d.rx = __builtin_amdgcn_make_buffer_rsrc((void*)(a.x + (int64_t)mb * a.ldx), (short)0, rows * (int)a.ldx * 4, 0x00020000);
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int row = 8 * i + (lane >> 3), c = (lane & 7) ^ (row & 7);
-    d.xk[i] = 4 * c;
-    d.xo[i] = (row * (int)a.ldx + 4 * c) * 4;
+    for (int i = 0; i < 4; i++) {
+      const int row = 8 * i + (lane >> 3), c = (lane & 7) ^ (row & 7);
+      d.xk[i] = 4 * c;
+      d.xo[i] = (row * (int)a.ldx + 4 * c) * 4;
+    }
   }
 #pragma unroll
-  for (int j = 0; j < TallDma<RT>::WI; j++) {
+  for (int j = 0; j < D::WI; j++) {
     const int t = wave + TK_WAVES * j, tt = t < 6 * RT ? t : 0;
     const int p = tt / CT, row = 16 * (tt % CT) + (lane >> 2), c = (lane & 3) ^ ((row >> 1) & 3);
     d.wk[j] = 8 * c;
@@ -1682,17 +1734,17 @@ __global__ __launch_bounds__(64 * TK_WAVES) void gemm_s3_tall_kernel(F32WArgs a,
   for (int i = 0; i < 2; i++)
 #pragma unroll
     for (int t = 0; t < CT; t++) acc[i][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  // Copies issued by this wave per step: 4 of x and its share of the 6 RT of W (waves below
+  // Copies issued by this wave per step: 4 of x (1 of int8 x) and its share of the 6 RT of W (waves below
   // (6 RT) % 8, or all when it is 0, take one more).  Steps s0 .. s0 + TD - 2 are issued up front
   // and step st + TD - 1 after the barrier of step st, so before step st the TD - 2 steps after it
   // are in flight (once they exist) and may stay so: vmcnt((TD - 2) * per-step count), vmcnt(0)
   // in the last steps of the slice.
   constexpr int WHI = (6 * RT) % TK_WAVES ? (6 * RT) % TK_WAVES : TK_WAVES;
-  constexpr int CHI = 4 + TallDma<RT>::WI, NHI = (TD - 2) * CHI, NLO = (TD - 2) * (CHI - 1);
+  constexpr int CHI = D::XI + D::WI, NHI = (TD - 2) * CHI, NLO = (TD - 2) * (CHI - 1);
   static_assert(TD >= 2, "two step buffers at least");
   static_assert(NHI < 64, "vmcnt field");
   for (int i = 0; i < TD - 1; i++)
-    if (s0 + i < s1) tall_issue<RT>(d, smem + i * BUF, 32 * (s0 + i), a.K, wave);
+    if (s0 + i < s1) tall_issue<RT, Q8>(d, smem + i * BUF, 32 * (s0 + i), a.K, wave);
   for (int st = s0; st < s1; st++) {
     if (st + TD - 1 <= s1) {  // steps st + 1 .. st + TD - 2 all exist (and are issued)
       if (wave < WHI) __builtin_amdgcn_s_waitcnt((NHI & 15) | (7 << 4) | (15 << 8) | ((NHI >> 4) << 14));
@@ -1705,8 +1757,8 @@ __global__ __launch_bounds__(64 * TK_WAVES) void gemm_s3_tall_kernel(F32WArgs a,
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     const int nx = st + TD - 1;
-    if (nx < s1) tall_issue<RT>(d, smem + ((nx - s0) % TD) * BUF, 32 * nx, a.K, wave);
-    tall_step<RT>(smem + ((st - s0) % TD) * BUF, wave, r16, g, acc);
+    if (nx < s1) tall_issue<RT, Q8>(d, smem + ((nx - s0) % TD) * BUF, 32 * nx, a.K, wave);
+    tall_step<RT, Q8>(smem + ((st - s0) % TD) * BUF, wave, r16, g, acc);
   }
   // lane (r16, g) holds rows 16 i + 4 g + r of column tile t's column r16
   float* pp = part + (int64_t)blockIdx.z * a.M * a.N;
@@ -1724,10 +1776,10 @@ __global__ __launch_bounds__(64 * TK_WAVES) void gemm_s3_tall_kernel(F32WArgs a,
   }
 }
 
-// The slices' partial sums added in slice order, then alpha, bias, add, activation and the store /
-// residual / gated epilogue of the split-weight kernels; four consecutive (flat [M][N]) outputs
-// per thread with 16-byte partial reads, every slice's read issued before the sums (element by
-// element when M * N % 4 != 0).
+// The slices' partial sums added in slice order, then the row scale (int8 x), alpha, bias, add,
+// activation and the store / residual / gated epilogue of the split-weight kernels; four
+// consecutive (flat [M][N]) outputs per thread with 16-byte partial reads, every slice's read
+// issued before the sums (element by element when M * N % 4 != 0).
 __global__ __launch_bounds__(256) void s3_ksum_kernel(F32WArgs a, const float* part, int ks) {
   const int64_t i4 = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x), mn = (int64_t)a.M * a.N;
   if (i4 >= mn) return;
@@ -1758,7 +1810,7 @@ __global__ __launch_bounds__(256) void s3_ksum_kernel(F32WArgs a, const float* p
     const int64_t idx = i4 + e;
     if (idx >= mn) break;
     const int m = (int)(idx / a.N), n = (int)(idx - (int64_t)m * a.N);
-    float r = v[e] * a.alpha;
+    float r = (a.xs ? v[e] * a.xs[m] : v[e]) * a.alpha;
     if (a.bias) r = r + a.bias[n];
     if (a.add) r = r + a.add[(int64_t)m * a.ld_add + n];
     r = apply_act(r, a.act);
@@ -2091,6 +2143,19 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const float* P, in
   else *c = __builtin_fmaf(a.gate[a.gate_off + n], v, *c);
 }
 
+// Per-token int8 rows back to fp32, x[m][k] = q[m][k] * s[m] (one 4-byte group per thread;
+// K % 4 == 0, ldq % 4 == 0).
+__global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* q, int64_t ldq, const float* s, float* x, int64_t M,
+                                                           int K) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x, kq = K / 4;
+  if (i >= M * kq) return;
+  const int64_t m = i / kq;
+  const int k = (int)(i - m * kq) * 4;
+  const char4 v = *(const char4*)(q + m * ldq + k);
+  const float sc = s[m];
+  *(float4*)(x + m * K + k) = make_float4((float)v.x * sc, (float)v.y * sc, (float)v.z * sc, (float)v.w * sc);
+}
+
 __global__ __launch_bounds__(256) void split3_kernel(const float* src, uint16_t* dst, int64_t n8, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (int64_t)gridDim.x * 256) {
     bf16x8 o[3];
@@ -2188,20 +2253,43 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d, int64_t s3_plane) {
   if (M == 0) return ANIMA_OK;
 
   if (W->kind == ANIMA_W_F32S3) {
-    if (!d->x) return fail(c, ANIMA_E_ARG, "anima_linear: split weights need fp32 x");
-    if (d->acc_out || d->xq) return fail(c, ANIMA_E_ARG, "anima_linear: acc_out / xq apply to i8/w4 weights only");
+    // x: fp32 rows, or per-token int8 rows xq with their scales xs (y = xs[m] * (q W^T)[m])
+    const bool q8 = d->xq != nullptr;
+    if (q8 ? (d->x || !d->xs) : !d->x)
+      return fail(c, ANIMA_E_ARG, "anima_linear: split weights need fp32 x, or int8 xq with its row scales xs (not both)");
+    if (d->acc_out) return fail(c, ANIMA_E_ARG, "anima_linear: acc_out applies to i8/w4 weights only");
     const int64_t ldx = d->ldx ? d->ldx : K;
     if (ldx < K) return fail(c, ANIMA_E_ARG, "anima_linear: ldx < K");
-    if (K % 8 || ldx % 4 || !al(d->x, 16) || !al(W->w, 16))
-      return fail(c, ANIMA_E_ARG, "anima_linear: split weights need K %% 8 == 0, ldx %% 4 == 0, 16-byte aligned x and w");
+    if (q8 ? (K % 16 || ldx % 16 || !al(d->xq, 16) || !al(W->w, 16)) : (K % 8 || ldx % 4 || !al(d->x, 16) || !al(W->w, 16)))
+      return fail(c, ANIMA_E_ARG, "anima_linear: split weights need K %% 8 == 0, ldx %% 4 == 0, 16-byte aligned x and w "
+                                  "(int8 x: K %% 16 == 0, ldx %% 16 == 0)");
     if (s3_plane && s3_plane < (int64_t)N * K) return fail(c, ANIMA_E_ARG, "anima_linear: split-weight plane stride below N * K");
     F32WArgs f{d->x, ldx, W->w, W->bias, d->out, ldc, alpha, d->act, d->epilogue, d->gate, d->gate_off,
                (int)M, N, K, 0, 0, 0, 0, d->add, ld_add, 0};
     f.wplane = s3_plane ? s3_plane : (int64_t)N * K;
-    Launch L(c, "gemm.f32s3", 2.0 * M * N * K, 0.0);
+    f.xq = d->xq;
+    f.xs = d->xs;
     // the tall kernel's buffer offsets are 32-bit: 32 rows of x and the three planes of W;
     // N in (96, 256] runs as 64-column workgroups
     const bool skf = K >= 512 && ldx < (1 << 23) && 2 * (2 * f.wplane + (int64_t)N * K) < (1LL << 31) - 64 && N <= 256;
+    if (q8 && !skf) {
+      // int8 rows for a shape the tall kernel does not take: back to fp32 rows (pooled scratch,
+      // x = q * s rounded once), then the fp32 path
+      void* xf = nullptr;
+      if (int rc = anima_alloc(c, (size_t)M * K * 4, &xf)) return rc;
+      const int64_t groups = M * (K / 4);
+      hipLaunchKernelGGL(dequant_rows_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, c->stream, d->xq, ldx,
+                         d->xs, (float*)xf, M, K);
+      anima_linear_desc dd = *d;
+      dd.x = (const float*)xf;
+      dd.ldx = K;
+      dd.xq = nullptr;
+      dd.xs = nullptr;
+      const int rc = linear_launch(c, &dd, s3_plane);
+      anima_free(c, xf);
+      return rc;
+    }
+    Launch L(c, "gemm.f32s3", 2.0 * M * N * K, 0.0);
     if (skf) {
       // k-slices so that the grid gives every CU about one workgroup, each slice at least 4 steps
       const int srt = N <= 32 ? 1 : N <= 64 || N > 96 ? 2 : 3;
@@ -2215,9 +2303,15 @@ int linear_launch(anima_ctx* c, const anima_linear_desc* d, int64_t s3_plane) {
       void* pt = nullptr;
       if (int rc = anima_alloc(c, (size_t)ks * M * N * 4, &pt)) return rc;
       const dim3 tg((unsigned)cb, (unsigned)rb, (unsigned)ks), blk(64 * TK_WAVES);
-      if (srt == 1) hipLaunchKernelGGL(gemm_s3_tall_kernel<1>, tg, blk, 0, c->stream, f, (float*)pt, spb);
-      else if (srt == 2) hipLaunchKernelGGL(gemm_s3_tall_kernel<2>, tg, blk, 0, c->stream, f, (float*)pt, spb);
-      else hipLaunchKernelGGL(gemm_s3_tall_kernel<3>, tg, blk, 0, c->stream, f, (float*)pt, spb);
+      if (q8) {
+        if (srt == 1) hipLaunchKernelGGL((gemm_s3_tall_kernel<1, true>), tg, blk, 0, c->stream, f, (float*)pt, spb);
+        else if (srt == 2) hipLaunchKernelGGL((gemm_s3_tall_kernel<2, true>), tg, blk, 0, c->stream, f, (float*)pt, spb);
+        else hipLaunchKernelGGL((gemm_s3_tall_kernel<3, true>), tg, blk, 0, c->stream, f, (float*)pt, spb);
+      } else {
+        if (srt == 1) hipLaunchKernelGGL((gemm_s3_tall_kernel<1, false>), tg, blk, 0, c->stream, f, (float*)pt, spb);
+        else if (srt == 2) hipLaunchKernelGGL((gemm_s3_tall_kernel<2, false>), tg, blk, 0, c->stream, f, (float*)pt, spb);
+        else hipLaunchKernelGGL((gemm_s3_tall_kernel<3, false>), tg, blk, 0, c->stream, f, (float*)pt, spb);
+      }
       hipLaunchKernelGGL(s3_ksum_kernel, dim3((unsigned)(((M * N + 3) / 4 + 255) / 256)), dim3(256), 0, c->stream, f,
                          (const float*)pt, ks);
       anima_free(c, pt);

@@ -22,10 +22,14 @@ function releaseAll(xs) {
   for (const x of xs) if (x && x.release) x.release();
 }
 
+// whether a quantized W's LoRA needs the fp32 rotated rows beside the int8 ones (its A product
+// reads the int8 rows unless ops.setLoraInput("fp32"))
+const wantsXr = (W) => !!(W.lora && W.lora.length) && !ops.loraReadsInt8(W);
+
 // LayerNorm + adaLN for inputs that feed W: int8 { xq } when W is quantized (W8A8), else the
 // fp32 modulated rows (normFor of app/models/dit.js:34-38).
 function normFor(gpu, x, mod, W) {
-  if (ops.needsRotation(W)) return { xq: ops.layernormModQ(gpu, x, mod, 0, D, D, !!(W.lora && W.lora.length)) };
+  if (ops.needsRotation(W)) return { xq: ops.layernormModQ(gpu, x, mod, 0, D, D, wantsXr(W)) };
   return { n: ops.layernormMod(gpu, x, mod, 0, D, D, false) };
 }
 
@@ -50,7 +54,7 @@ function releaseNorm(nf) {
 // form the parts need (int8 rows for quantized parts, fp32 rows for bf16 parts).
 function projectParts(gpu, x, mod, Ws, M) {
   const quant = Ws.filter((W) => ops.needsRotation(W));
-  const xq = quant.length ? ops.layernormModQ(gpu, x, mod, 0, D, D, quant.some((W) => W.lora && W.lora.length)) : null;
+  const xq = quant.length ? ops.layernormModQ(gpu, x, mod, 0, D, D, quant.some(wantsXr)) : null;
   const n = quant.length < Ws.length ? ops.layernormMod(gpu, x, mod, 0, D, D, false) : null;
   const qkv = gpu.empty([M, 3 * D]);
   Ws.forEach((W, j) => {
@@ -443,11 +447,11 @@ export class AnimaDiT {
       ops.linear(gpu, a, b.cross.o, { M, out: x, resid: true, gate: m.cross, gOff: 2 * D });
       a.release();
 
-      // MLP.  With a quantized layer2 (and no LoRA on it, which needs the fp32 GELU output),
-      // layer1 stores its pre-activation and the GELU runs in layer2's Hadamard + int8 pass, off
-      // the GEMM epilogue; the int8 rows are the same.
+      // MLP.  With a quantized layer2 (and no LoRA on it that needs the fp32 GELU output), layer1
+      // stores its pre-activation and the GELU runs in layer2's Hadamard + int8 pass, off the
+      // GEMM epilogue; the int8 rows are the same.
       nf = normFor(gpu, x, m.mlp, b.l1);
-      if (ops.needsRotation(b.l2) && !(b.l2.lora && b.l2.lora.length)) {
+      if (ops.needsRotation(b.l2) && !wantsXr(b.l2)) {
         const pre = project(gpu, nf, b.l1, M);
         releaseNorm(nf);
         const hq = ops.quantRows(gpu, pre, MLP, true, "gelu");

@@ -4,8 +4,8 @@
 // Extensions beyond the reference interface (all optional arguments):
 //   attention: B / qBatch / kBatch / vBatch / oBatch (batched CFG), kvLen (per-batch valid keys),
 //              qNorm / kNorm / cs (q/k RMSNorm + RoPE fused into the attention loads), precision.
-//   linear:    opts.xq = { q, s } per-token int8 activations (layernormModQ / quantRows); with a
-//              LoRA on a quantized weight the fp32 rotated input opts.xr is needed as well.
+//   linear:    opts.xq = { q, s } per-token int8 activations (layernormModQ / quantRows); a LoRA
+//              on a quantized weight reads them too (setLoraInput), or the fp32 input opts.xr / x.
 //   layernormModQ: LayerNorm + adaLN + ConvRot + per-token int8 in one pass.
 
 import { native } from "./gpu.mjs";
@@ -16,6 +16,22 @@ const EW = { silu_mul: 0, add: 1, silu: 2, copy: 3 };
 const ptr = (t) => (t ? (typeof t === "number" ? t : t.buf) : 0);
 
 export const needsRotation = (W) => W.kind === "i8" || W.kind === "w4";
+
+// The input of a quantized linear's LoRA A product.  "int8" (default): the per-token int8 rows
+// the GEMM itself reads (opts.xq, ConvRot-rotated) against the rotated A (A H), so the LoRA sees
+// the same activations as W and no fp32 copy of them is written.  "fp32": the fp32 input, rotated
+// (opts.xr, with A H) or not (x, with A), as the reference's loraDelta takes it (ops.js:55-62).
+let loraInputMode = "int8";
+export function setLoraInput(mode) {
+  if (mode !== "int8" && mode !== "fp32") throw new Error(`LoRA input "${mode}": "int8" or "fp32"`);
+  loraInputMode = mode;
+}
+export const loraInput = () => loraInputMode;
+// whether linear() runs W's LoRA A product from opts.xq (its fused factors with the rotated A)
+export function loraReadsInt8(W) {
+  const F = W.loraFused;
+  return loraInputMode === "int8" && needsRotation(W) && !!(F && F.lora === W.lora && F.Ars);
+}
 
 // ConvRot input rotation (ops.js:38-44).
 export function rotate(gpu, x) {
@@ -67,16 +83,20 @@ export function linear(gpu, x, W, opts) {
   // (x H)(A H)^T = x A^T, the unrotated x and A are used when x is at hand (no rotation pass), and
   // the rotated pair (opts.xr, entry.Ar) only when the caller holds just the rotated input.
   const lora = W.lora && W.lora.length ? W.lora : null;
-  const rot = !!(lora && needsRotation(W) && o.xr);
-  const xin = rot ? o.xr : x;
-  if (lora && !xin) throw new Error(`${W.name || "linear"}: a LoRA on a quantized weight needs the fp32 input (x or opts.xr)`);
+  // int8 LoRA input (setLoraInput): the A product over opts.xq with the rotated A
+  const q8 = !!(lora && o.xq && loraReadsInt8(W));
+  const rot = !q8 && !!(lora && needsRotation(W) && o.xr);
+  const xin = q8 ? null : rot ? o.xr : x;
+  if (lora && !q8 && !xin) throw new Error(`${W.name || "linear"}: a LoRA on a quantized weight needs its input (opts.xq, x or opts.xr)`);
   // Quantized weights with fused LoRA factors (fuseLora): one A product over the stacked A, and
   // the B product inside the GEMM's epilogue (no [M, N] delta).  Otherwise a plain store (no
   // activation, no residual) takes the LoRA products afterwards, accumulated straight into the
   // output, and other epilogues get them as a delta that the epilogue adds.
   const F = lora && W.loraFused && W.loraFused.lora === W.lora ? W.loraFused : null;
   if (F && rot && !F.Ar) throw new Error(`${W.name || "linear"}: LoRA entries without the rotated A for a rotated input`);
-  const down = F ? linear(gpu, xin, rot ? { kind: "f32s3", N: F.R, K: W.K, buf: F.Ars } : { kind: "f32s3", N: F.R, K: W.K, buf: F.As }, { M }) : null;
+  const down = !F ? null
+    : q8 ? linear(gpu, null, { kind: "f32s3", N: F.R, K: W.K, buf: F.Ars }, { M, xq: o.xq })
+    : linear(gpu, xin, { kind: "f32s3", N: F.R, K: W.K, buf: rot ? F.Ars : F.As }, { M });
   const late = lora && !F && !o.resid && ACT[o.act || "none"] === 0;
   const delta = lora && !F && !late ? loraDelta(gpu, xin, W, M, rot) : null;
   const out = o.out || gpu.empty([M, W.N]);
@@ -85,7 +105,7 @@ export function linear(gpu, x, W, opts) {
     add: delta ? delta.buf : 0, ldAdd: delta ? W.N : 0,
     loraXa: down ? down.buf : 0, ldLoraXa: down ? F.R : 0, loraB: F ? F.Bs.buf : 0, loraR: F ? F.Rb : 0,
     loraCols: F ? F.cols : 0 };
-  if (needsRotation(W) && o.xq) {
+  if ((needsRotation(W) || W.kind === "f32s3") && o.xq) {
     d.xq = o.xq.q.buf;
     d.xs = o.xq.s.buf;
   } else if (needsRotation(W)) {
@@ -197,10 +217,13 @@ export function linearQkv(gpu, x, W, opts) {
     d.x = x.buf;
     d.xRotated = o.xRotated ? 1 : 0;
   }
-  // LoRAs: the A product of the rotated input (x H)(A H)^T = x A^T, the B product in the epilogue
+  // LoRAs: the A product of the rotated input (x H)(A H)^T = x A^T (the int8 rows opts.xq, or the
+  // fp32 rows opts.xr; setLoraInput), the B product in the epilogue
   const F = W.lora && W.lora.length ? W.loraFused : null;
-  if (F && !o.xr) throw new Error(`${W.name || "linearQkv"}: a LoRA needs the rotated fp32 input (opts.xr)`);
-  const down = F ? linear(gpu, o.xr, { kind: "f32s3", N: F.R, K: W.K, buf: F.Ars }, { M }) : null;
+  const q8 = !!(F && o.xq && loraReadsInt8(W));
+  if (F && !q8 && !o.xr) throw new Error(`${W.name || "linearQkv"}: a LoRA needs the rotated input (opts.xq or opts.xr)`);
+  const Wa = F ? { kind: "f32s3", N: F.R, K: W.K, buf: F.Ars } : null;
+  const down = !F ? null : q8 ? linear(gpu, null, Wa, { M, xq: o.xq }) : linear(gpu, o.xr, Wa, { M });
   if (F) Object.assign(d, { loraXa: down.buf, ldLoraXa: F.R, loraB: F.Bs.buf, loraR: F.Rb, loraCols: F.cols });
   const w = weightArg(W);
   native.linearQkv(gpu.ctx, w, d, { B, L, H, kNorm: ptr(o.kNorm), cs: ptr(o.cs), sinOff: o.cs ? o.cs.sinOff : 0,

@@ -389,8 +389,10 @@ typedef struct {
   const float* x;
   int64_t ldx;
   int x_rotated;
-  /* i8/w4 only: pre-quantized rotated activations (anima_quant_rows / anima_layernorm_mod);
-   * when set, x is ignored. */
+  /* i8/w4: pre-quantized rotated activations (anima_quant_rows / anima_layernorm_mod); when set,
+   * x is ignored.  f32s3 (split) weights take them in place of x as well (x NULL; K % 16 == 0,
+   * ldx % 16 == 0 in bytes, xq 16-byte aligned): y = xs[m] * sum_k xq[m][k] W[n][k], the LoRA A
+   * product of a quantized linear over the int8 rows its GEMM reads, with the rotated A. */
   const int8_t* xq;
   const float* xs;
   float* out;

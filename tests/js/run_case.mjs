@@ -10,6 +10,8 @@
 //   dit        AnimaDiT.load(safetensors) -> timeCond -> prepareContext -> forward
 //   lora       ops.linear with LoRA entries given as files (A in the input's basis), optional act,
 //              stacked A matrices and a rotated-only input
+//   loraq      ops.linear on int8 rows (quantRows) with fused LoRA factors: the A product over the
+//              int8 rows (the default LoRA input) and over the fp32 rotated rows (setLoraInput)
 //   lorafile   loadLora(safetensors) onto a 1-block synthetic DiT, then the block's stacked qkv
 //              and mlp.layer2 linears with and without the attached LoRA
 //   lorate     loadLora(safetensors) onto a 2-layer synthetic text encoder (text-encoder names):
@@ -28,6 +30,8 @@
 //              weights, cond + uncond prompts), the velocities
 //   synthdit   a seeded synthetic DiT (any depth) on given latents and contexts: velocities and the
 //              residual stream after block 0, for the oracle's restatement of the same weights
+//   loradit    a seeded synthetic DiT with seeded LoRAs on every block linear: the forward without
+//              LoRAs, with them on the int8 rows (default) and on the fp32 rows (setLoraInput)
 //   fullstep   the full-size CFG step of a synthetic DiT: eager, with equal contexts, and replayed
 //              from a HIP graph
 //   vae        VAEDecoder.decode of a seeded synthetic decoder: raw output, RGBA bytes, stages
@@ -125,6 +129,25 @@ async function main() {
     const y = ops.linear(gpu, c.rotated ? null : x, W, { act: c.act, M: c.M, xr: c.rotated ? ops.rotate(gpu, x) : undefined });
     save(c.out, await gpu.read(y));
     ops.releaseLoraStack(W);
+  } else if (c.case === "loraq") {
+    const W = weightFromFiles(gpu, c.W);
+    const x = gpu.fromArray(load(c.x), [c.M, W.K]);
+    const xq = ops.quantRows(gpu, x, W.K, true);
+    save(c.out + ".q", await gpu.read(xq.q));
+    save(c.out + ".s", await gpu.read(xq.s));
+    save(c.out + ".base", await gpu.read(ops.linear(gpu, null, W, { act: c.act, M: c.M, xq })));
+    W.lora = c.lora.map((e) => {
+      const A = gpu.upload(load(e.A));
+      return { A, Ar: rotatedA(gpu, A, e.r * W.K), B: gpu.upload(load(e.B)), r: e.r, scale: e.scale, off: e.off, n: e.n };
+    });
+    ops.fuseLora(gpu, W);
+    if (!ops.loraReadsInt8(W)) throw new Error("the fused LoRA factors should read the int8 rows");
+    save(c.out, await gpu.read(ops.linear(gpu, null, W, { act: c.act, M: c.M, xq })));
+    ops.setLoraInput("fp32");
+    const xr = ops.rotate(gpu, x);
+    save(c.out + ".fp32", await gpu.read(ops.linear(gpu, null, W, { act: c.act, M: c.M, xq, xr })));
+    ops.setLoraInput("int8");
+    ops.releaseLoraFused(W);
   } else if (c.case === "lorafile") {
     const src = new SyntheticWeights(gpu, 7, { mode: c.mode, blocks: 1 });
     const dit = AnimaDiT.synthetic(gpu, src);
@@ -337,6 +360,39 @@ async function main() {
     save(c.out + ".block0", blockOut[0]);
     tc.release();
     cond.release();
+  } else if (c.case === "loradit") {
+    const dit = AnimaDiT.synthetic(gpu, new SyntheticWeights(gpu, c.seed, { mode: c.mode, blocks: c.blocks }));
+    const regs = { dit: linearRegistry(dit), te: null };
+    const lat = c.latents.map((p) => load(p));
+    const forward = async (name) => {
+      const tc = dit.timeCond(c.sigma);
+      const cond = dit.prepareContext(c.ctx.map((p) => gpu.fromArray(load(p), [c.Lk, 1024])));
+      const v = await dit.forward(lat, c.h, c.w, cond, tc);
+      v.forEach((vb, b) => save(`${c.out}.${name}.${b}`, vb));
+      tc.release();
+      cond.release();
+    };
+    await forward("base");
+    const modules = [], bufs = [];
+    let seed = 700;
+    for (const [name, t] of regs.dit) {
+      if (!name.startsWith("blocks_")) continue;
+      const A = gpu.empty([c.rank * t.W.K]), B = gpu.empty([t.n * c.rank]);
+      native.fillRandom(gpu.ctx, A.buf, A.size, 4, seed++, 0.02, 0.0);
+      native.fillRandom(gpu.ctx, B.buf, B.size, 4, seed++, 0.02, 0.0);
+      const Ar = ops.needsRotation(t.W) ? rotatedA(gpu, A, A.size) : null;
+      bufs.push(A, B, Ar);
+      modules.push({ target: t, A, Ar, B, r: c.rank, alphaScale: 1 });
+    }
+    attachLoras(regs, [{ lora: { modules }, strength: 1 }]);
+    const int8 = [...regs.dit.values()].filter(({ W }) => ops.loraReadsInt8(W)).length;
+    await forward("int8");
+    ops.setLoraInput("fp32");
+    await forward("fp32");
+    ops.setLoraInput("int8");
+    attachLoras(regs, []);
+    for (const t of bufs) if (t) t.release();
+    console.log(JSON.stringify({ loradit: { modules: modules.length, int8 } }));
   } else if (c.case === "fullstep") {
     // the full-size CFG step: one latent in both batch halves (as LatentPipeline.generate feeds
     // it), the cond and uncond contexts; then the same step with the uncond context equal to the

@@ -124,3 +124,33 @@ def test_dit_w4_unpacked_at_load_is_bit_identical(tmp_path):
             assert info["unpacked"] == 2 * 8
         outs.append(np.concatenate([np.fromfile(out + f".{b}", np.float32) for b in range(2)]))
     assert np.all(np.isfinite(outs[0])) and np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.timeout(600)
+def test_dit_lora_int8_rows(tmp_path):
+    """Seeded rank-16 LoRAs on every block linear of a 3-block W4A8 synthetic DiT (256x256, B=2):
+    the forward with the LoRA A products on the int8 rows that the quantized linears read (the
+    default) against the same forward with them on the fp32 rotated rows (the reference's LoRA
+    input).  The LoRAs move the velocity (rel L2 > 1e-3 from the forward without them), and the two
+    LoRA inputs differ by the int8 rounding of the LoRA input only: below 5% of that move."""
+    h = w = 32
+    Lk = 64
+    files = {}
+    for b in range(2):
+        files[f"lat{b}"] = str(tmp_path / f"lat{b}.bin")
+        orc.randn(221 + b, 16 * h * w).tofile(files[f"lat{b}"])
+        files[f"ctx{b}"] = str(tmp_path / f"ctx{b}.bin")
+        orc.randn(231 + b, Lk * 1024).tofile(files[f"ctx{b}"])
+    out = str(tmp_path / "v")
+    r = run_case(tmp_path, {"case": "loradit", "seed": 11, "mode": "w4a8", "blocks": 3, "sigma": 0.7, "Lk": Lk,
+                            "h": h, "w": w, "rank": 16, "ctx": [files["ctx0"], files["ctx1"]],
+                            "latents": [files["lat0"], files["lat1"]], "out": out})
+    info = json.loads(next(ln for ln in r.stdout.splitlines() if '"loradit"' in ln))["loradit"]
+    assert info["int8"] > 0 and info["modules"] > 0, info
+    v = {k: np.concatenate([np.fromfile(f"{out}.{k}.{b}", np.float32) for b in range(2)]) for k in ("base", "int8", "fp32")}
+    assert all(np.all(np.isfinite(a)) for a in v.values())
+    move = rel_l2(v["fp32"], v["base"])
+    diff = rel_l2(v["int8"], v["fp32"])
+    print(f"LoRA move rel L2 {move:.3e}; int8 vs fp32 LoRA input rel L2 {diff:.3e} ({diff / move:.3f} of the move)",
+          flush=True)
+    assert move > 1e-3 and 0 < diff < 0.05 * move

@@ -245,6 +245,50 @@ def test_js_linear_lora(tmp_path, kind, act, stack, rotated):
         assert report(f"{kind} LoRA delta alone", got.astype(np.float64) - base, delta)[0] < 1e-4
 
 
+@pytest.mark.parametrize("act", ["none", "gelu"])
+def test_js_linear_lora_int8_rows(tmp_path, act):
+    """A quantized linear whose LoRA A product reads the int8 rows its GEMM reads (the default LoRA
+    input): y = epilogue(acc, s_x, s_w) + B (A H)(s_x q)^T, within 1e-6 of the oracle epilogue fed
+    that delta in float64 (q, s_x: the oracle's token_quant of the rotated x, which the GPU's rows
+    equal bit for bit).  With setLoraInput("fp32") the same linear takes the fp32 rotated rows, the
+    reference's LoRA input, within 1e-6 of that float64 delta; the two deltas differ by the int8
+    rounding of the LoRA input only (rel-L2 <= 1e-2)."""
+    M, K, N = 300, 1024, 512
+    x = orc.randn(141, M * K).reshape(M, K)
+    rng = np.random.default_rng(142)
+    ents = [dict(r=8, scale=0.5, off=0, n=N), dict(r=4, scale=2.0, off=128, n=256)]
+    for i, e in enumerate(ents):
+        e["A"] = (0.05 * orc.randn(143 + i, e["r"] * K)).reshape(e["r"], K).astype(np.float32)
+        e["B"] = (0.05 * orc.randn(145 + i, e["n"] * e["r"])).reshape(e["n"], e["r"]).astype(np.float32)
+    qw = np.clip(np.rint(40 * orc.randn(147, N * K)), -127, 127).astype(np.int8).reshape(N, K)
+    sw = (rng.uniform(0.5, 1.5, N) / (127 * np.sqrt(K))).astype(np.float32)
+    W = {"kind": "i8", "N": N, "K": K, "w": write(tmp_path, "w.bin", qw), "scale": write(tmp_path, "sw.bin", sw)}
+    spec_l = [dict(A=write(tmp_path, f"a{i}.bin", e["A"]), B=write(tmp_path, f"b{i}.bin", e["B"]), r=e["r"],
+                   scale=e["scale"], off=e["off"], n=e["n"]) for i, e in enumerate(ents)]
+    out = str(tmp_path / "y.bin")
+    run_case(tmp_path, {"case": "loraq", "M": M, "W": W, "x": write(tmp_path, "x.bin", x), "lora": spec_l,
+                        "out": out, "act": act})
+    xr = orc.hadamard256(x)
+    qx, sx = orc.token_quant(xr)
+    assert np.array_equal(np.fromfile(out + ".q", np.int8).reshape(M, K), qx)
+    assert np.array_equal(read(out + ".s"), sx)
+    actid = {"none": 0, "gelu": 1}[act]
+    acc = orc.gemm_i8(qx, qw)
+    ents_r = [dict(e, A=orc.hadamard256(e["A"])) for e in ents]
+    dq = lora_delta(sx.astype(np.float64)[:, None] * qx.astype(np.float64), ents_r, N)
+    df = lora_delta(xr, ents_r, N)
+    got, got_f = read(out).reshape(M, N), read(out + ".fp32").reshape(M, N)
+    ref_q = orc.linear_epilogue(acc, sx, sw, act=actid, add=dq.astype(np.float32))
+    ref_f = orc.linear_epilogue(acc, sx, sw, act=actid, add=df.astype(np.float32))
+    assert report(f"i8 {act} LoRA on the int8 rows", got, ref_q)[0] < 1e-6
+    assert report(f"i8 {act} LoRA on the fp32 rotated rows", got_f, ref_f)[0] < 1e-6
+    d_rel = report("LoRA delta: int8 rows vs fp32 rows (float64)", dq, df)[0]
+    assert 0 < d_rel < 1e-2
+    if act == "none":
+        base = read(out + ".base").reshape(M, N)
+        assert report("LoRA delta alone, int8 rows", got.astype(np.float64) - base, dq)[0] < 1e-4
+
+
 def test_js_lora_file(tmp_path):
     """loadLora on a 1-block synthetic DiT from a safetensors file in PEFT and kohya naming: the
     k_proj slice of the stacked qkv and mlp.layer2 (alpha / r scaling) match, a LoKr tensor is

@@ -691,6 +691,56 @@ def test_split3_linears(ctx, N, K, M, epi):
     assert report(f"split3 {epi}", got[:, :N], want[:, :N])[0] < 1e-6
 
 
+@pytest.mark.parametrize("N,K,M,epi", [(32, 2048, 257, "store"), (96, 2048, 4000, "store"), (64, 8192, 600, "store"),
+                                      (200, 1040, 45, "gated"), (48, 256, 70, "resid"), (300, 512, 33, "store")])
+def test_split3_int8_rows(ctx, N, K, M, epi):
+    """ANIMA_W_F32S3 over per-token int8 rows (xq, xs; the LoRA A product of a quantized linear
+    from the rows its GEMM reads): y = alpha * xs[m] * sum_k q[m][k] W[n][k] within 1e-6 of
+    float64.  The tall kernel with int8 x (rank 32 / 96 / 64 at K = 2048 / 8192; N = 200 in
+    64-column workgroups with K = 1040 ending inside a 32-k step; ragged M) and the shapes it does
+    not take (K < 512, N > 256: the rows widened to fp32 first)."""
+    case(f"split3 int8 rows N={N} K={K} M={M} {epi}")
+    m = amd()
+    rng = np.random.default_rng(181)
+    ldx = K + 16
+    q = rng.integers(-127, 128, size=(M, ldx), dtype=np.int8)
+    s = rng.uniform(0.001, 0.02, M).astype(np.float32)
+    w = (0.05 * orc.randn(182, N * K)).reshape(N, K).astype(np.float32)
+    dw = ctx.empty((3, N, K), np.uint16)
+    ctx.split3_bf16(ctx.upload(w), dw, N * K)
+    W = m.weight(m.W_F32S3, N, K, dw)
+    ref = 0.5 * s.astype(np.float64)[:, None] * (q[:, :K].astype(np.float64) @ w.T.astype(np.float64))
+    ldc = N + 12
+    base = orc.randn(183, M * ldc).reshape(M, ldc)
+    gate = orc.randn(184, N).astype(np.float32)
+    dout = ctx.upload(base)
+    dq, ds = ctx.upload(q), ctx.upload(s)
+    kw = dict(xq=dq, xs=ds, ldx=ldx, ldc=ldc, alpha=0.5)
+    if epi == "resid":
+        kw["epilogue"] = m.EPI_RESID
+    elif epi == "gated":
+        kw.update(epilogue=m.EPI_GATED, gate=ctx.upload(gate))
+    ctx.linear(W, M, dout, **kw)
+    want = base.astype(np.float64)
+    if epi == "store":
+        want[:, :N] = ref
+    elif epi == "resid":
+        want[:, :N] += ref
+    else:
+        want[:, :N] += gate.astype(np.float64) * ref
+    got = dout.numpy()
+    assert np.array_equal(got[:, N:], base[:, N:])
+    assert report(f"split3 int8 rows {epi}", got[:, :N], want[:, :N])[0] < 1e-6
+    # refused: int8 rows with x as well, without their scales, or with K % 16 != 0
+    with pytest.raises(m.AnimaError):
+        ctx.linear(W, M, dout, x=ctx.upload(base), **kw)
+    with pytest.raises(m.AnimaError):
+        ctx.linear(W, M, dout, xq=dq, ldx=ldx, ldc=ldc)
+    W8 = m.weight(m.W_F32S3, N, K - 8, dw)
+    with pytest.raises(m.AnimaError):
+        ctx.linear(W8, M, dout, xq=dq, xs=ds, ldx=ldx, ldc=ldc)
+
+
 def test_grouped_bf16_gemv(ctx):
     """G products in one launch (the adaLN modulation stage of timeCond): every group bit-exact
     against its own anima_linear GEMV call with the same bias, and within 1e-6 of float64."""
