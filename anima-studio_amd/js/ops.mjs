@@ -179,14 +179,14 @@ export function releaseLoraFused(W) {
 // attention(gpu, { q, kvPrep, qNorm, cs, ... }); K is RMS-normed (kNorm) and rotated (cs) and the
 // prepared bytes equal attentionPrepareKV of the plain linear's output.  Callers check
 // qkvFusable first (int8 / W4 weights, tokens per image a multiple of 64).  linearQkv takes LoRAs
-// too (their fused factors, fuseLora, with rank blocks of whole 256-column tiles, and the rotated
-// fp32 input in opts.xr for the A product), but qkvFusable declines them unless withLora: the
-// GEMM instance with both epilogues runs at the register limit and measured no faster than the
-// LoRA linear plus the attention's own K / V conversion (51.7 vs 51.5 ms per DiT step at rank 32).
-export function qkvFusable(W, L, H, withLora) {
+// too: their fused factors (fuseLora) with rank blocks of whole 256-column tiles, the A product
+// over the int8 rows opts.xq (or the rotated fp32 rows opts.xr under setLoraInput("fp32")).  With
+// rank-32 LoRAs the fused GEMM (at its register limit) is 0.2 ms per DiT step faster than the
+// LoRA linear plus the attention's own K / V conversion (45.8 vs 46.0 ms).
+export function qkvFusable(W, L, H) {
   if (W.lora && W.lora.length) {
     const F = W.loraFused;
-    if (!withLora || !(F && F.lora === W.lora && F.Ars && F.cols % 256 === 0)) return false;
+    if (!(F && F.lora === W.lora && F.Ars && F.cols % 256 === 0)) return false;
   }
   return needsRotation(W) && L % 64 === 0 && H % 2 === 0 && W.N === 3 * H * 128;
 }
