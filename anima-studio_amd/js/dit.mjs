@@ -427,12 +427,13 @@ export class AnimaDiT {
       a.release();
 
       // cross-attention against the per-prompt cached keys/values (q RMSNorm fused, no RoPE).  With
-      // an int8 / W4 q projection (no LoRA) and bf16 attention, the GEMM's epilogue writes Q as the
-      // attention's prepared operand (RMS-normed, scaled, bf16).
+      // an int8 / W4 q projection (no LoRA) and bf16 attention, the GEMM's
+      // epilogue writes Q as the attention's prepared operand (RMS-normed, scaled, bf16).
       nf = normFor(gpu, x, m.cross, b.cross.q);
       const kv = cond.kv[i];
       if (this.fuseQkv && cond.precision === "bf16" && ops.qFusable(b.cross.q, L, HEADS)) {
-        const f = ops.linearQkv(gpu, null, b.cross.q, { B, L, H: HEADS, xq: nf.xq, qNorm: b.cross.qn, prepareQ: true });
+        const f = ops.linearQkv(gpu, null, b.cross.q, { B, L, H: HEADS, xq: nf.xq, xr: nf.xq.xr, qNorm: b.cross.qn,
+          prepareQ: true });
         releaseNorm(nf);
         a = ops.attention(gpu, { qPrep: f.qPrep, kvPrep: kv.prep, B, Lq: L, Lk: cond.Lk, H: HEADS, D: HD, ldq: D,
           precision: "bf16" });

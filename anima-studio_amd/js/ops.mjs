@@ -192,7 +192,10 @@ export function qkvFusable(W, L, H) {
 }
 
 // A Q-only projection for linearQkv(..., { prepareQ: true }): int8 / W4 weights of H * 128
-// columns without LoRAs, tokens per image a multiple of 64.
+// columns, tokens per image a multiple of 64.  linearQkv takes the LoRA factors here too (the
+// attention then matches the LoRA linear + q_norm bit for bit), but that GEMM instance spills and
+// measured slower than the LoRA linear + the attention's own Q load (46.2 vs 45.9 ms per rank-32
+// DiT step), so LoRAs are declined.
 export function qFusable(W, L, H) {
   return needsRotation(W) && !(W.lora && W.lora.length) && L % 64 === 0 && W.N === H * 128;
 }

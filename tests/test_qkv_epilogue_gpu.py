@@ -227,11 +227,13 @@ def test_linear_qkv_prepared_q(ctx, kind, Hp, Wp):
         x.release()
 
 
-def test_linear_q_only_prepared(ctx):
+@pytest.mark.parametrize("lora", [False, True])
+def test_linear_q_only_prepared(ctx, lora):
     """A Q-only projection (W of H * 128 columns, anima_qkv_desc q_prep without K / V or RoPE: the
     cross-attention's q) feeding the attention against prepared K / V of 512 context keys (ragged
-    kv_len): bit-identical to the plain linear + attention with q_norm."""
-    case("linear_qkv Q-only prepared Q (cross-attention)")
+    kv_len): bit-identical to the plain linear + attention with q_norm; with a rank-32 LoRA term
+    (lora_*, one block) on both sides as well."""
+    case(f"linear_qkv Q-only prepared Q (cross-attention){' + LoRA' if lora else ''}")
     m = amd()
     B, L, H, K, Lk = 2, 4096, 16, 2048, 512
     M, N = B * L, H * HD
@@ -239,6 +241,15 @@ def test_linear_q_only_prepared(ctx):
     rng = np.random.default_rng(891)
     xq = ctx.upload(rng.integers(-127, 128, size=(M, K), dtype=np.int8))
     xs = ctx.upload(rng.uniform(0.002, 0.02, M).astype(np.float32))
+    lk = {}
+    if lora:
+        R = 32
+        xa = ctx.upload((0.5 * rng.standard_normal((M, R))).astype(np.float32))
+        Bm = ctx.upload((0.05 * rng.standard_normal((N, R))).astype(np.float32))
+        planes = ctx.empty(3 * N * R, np.uint16)
+        ctx.split3_bf16(Bm, planes, N * R)
+        lk = dict(lora_xa=xa, ld_lora_xa=R, lora_b=planes, lora_r=R)
+        wbufs += [xa, Bm, planes]
     dqn = ctx.upload((1 + 0.02 * orc.randn(892, HD)).astype(np.float32))
     kv = ctx.upload(orc.randn(893, B * Lk * N).reshape(B * Lk, N))
     kv_len = [458, 263]
@@ -247,9 +258,9 @@ def test_linear_q_only_prepared(ctx):
     common = dict(B=B, Lq=L, Lk=Lk, H=H, D=HD, ldq=N, ldk=N, ldv=N, precision=m.PREC_BF16, kv_len=kv_len)
     ctx.attention(q=kv, k=kv, v=kv, o=kv, prepare_into=prep, **dict(common, Lq=Lk))
     q = ctx.empty((M, N))
-    ctx.linear(W, M, q, xq=xq, xs=xs)
+    ctx.linear(W, M, q, xq=xq, xs=xs, **lk)
     qp = ctx.empty(M * N, np.uint16)
-    ctx.linear_qkv(W, M, None, B=B, L=L, H=H, xq=xq, xs=xs, q_norm=dqn, q_prep=qp)
+    ctx.linear_qkv(W, M, None, B=B, L=L, H=H, xq=xq, xs=xs, q_norm=dqn, q_prep=qp, **lk)
     o1, o2 = ctx.empty((M, N)), ctx.empty((M, N))
     ctx.attention(q=q, k=None, v=None, o=o1, kv_prep=prep, q_norm=dqn, **common)
     ctx.attention(q=None, k=None, v=None, o=o2, kv_prep=prep, q_prep=qp, **common)
