@@ -189,7 +189,10 @@ async function main() {
     peak_gib: Number((gpu.pool.peak / 2 ** 30).toFixed(2)) };
   if (gpu.profiler) out.kernels = await gpu.profiler.report();
   const genSteps = Number(arg("generate", 0));
+  const note = (what) => process.stderr.write(`bench_dit: ${what}\n`);
+  note(`steps done (${ms.toFixed(2)} ms)`);
   if (genSteps > 0) {
+    note(`sampling loop, ${genSteps} steps`);
     // a whole sampling run (text encoding and VAE excluded): N DiT steps + the sampler between them
     const pipe = new LatentPipeline(gpu, dit);
     const opts = { cond, width: size, height: size, steps: genSteps, sampler: arg("sampler", "euler_a"),
@@ -207,6 +210,7 @@ async function main() {
   }
   const teTokens = Number(arg("text-encoder", 0));
   if (teTokens > 0) {
+    note(`text encoder, ${teTokens} tokens`);
     const te = Qwen3.synthetic(gpu, new SyntheticWeights(gpu, 99), { vocab: 4096 });
     const ids = [];
     for (let i = 0; i < teTokens; i++) ids.push((i * 2654435761) % 4096);
@@ -221,6 +225,7 @@ async function main() {
     te.release();
   }
   if (arg("vae", false)) {
+    note("VAE decode");
     // the VAE decoder (Wan 2.1, seeded synthetic weights) on this size's latent, both precisions:
     // the decode of a [16, h, w] latent to a (8h x 8w) image, host conversions included
     const vae = VAEDecoder.synthetic(gpu, new SyntheticWeights(gpu, 77));
@@ -247,6 +252,7 @@ async function main() {
     }
   }
   if (arg("in-gemm-too", false) && w4mode === "packed" && mode === "w4a8") {
+    note("step with the W4 unpack inside the GEMMs");
     // the same packed weights with the nibbles unpacked inside every GEMM's main loop (eager
     // steps; bit-identical velocities)
     native.setW4Path(gpu.ctx, 1);
@@ -257,6 +263,7 @@ async function main() {
     native.setW4Path(gpu.ctx, 0);
   }
   if (arg("unpacked-too", false) && w4mode === "packed" && mode === "w4a8") {
+    note("step with the W4 weights converted to int8");
     // the same step once the W4 linears are converted to their int8 grid in place (after the
     // graph, which holds the packed buffers, is released): bit-identical velocities
     if (fg) {
@@ -270,6 +277,7 @@ async function main() {
     out.w4_unpacked = { linears: n, step_ms: Number(median(xs).toFixed(3)) };
   }
   console.log(JSON.stringify(out));
+  note("done");
   if (fg) fg.release();
   if (latT) latT.release();
   cond.release();
