@@ -173,6 +173,8 @@ def lib():
         L.anima_zero.argtypes = [_vp, _vp, _i64]
         L.anima_linear_grouped_bf16.argtypes = [_vp, ctypes.c_int, _i64, ctypes.c_int, ctypes.c_int, _vp, _i64, _i64, _vp,
                                                  _i64, _vp, _i64, _vp, _i64, _i64]
+        L.anima_gemv_grouped_f32.argtypes = [_vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _i64, _vp, _i64, _vp,
+                                             _i64, ctypes.c_float, ctypes.c_int]
         L.anima_patchify.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]
         L.anima_unpatchify.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]
         L.anima_linear.argtypes = [_vp, ctypes.POINTER(LinearDesc)]
@@ -416,6 +418,11 @@ class Context:
         return self._check(lib().anima_linear_grouped_bf16(self.h, G, M, N, K, _ptr(x), ldx, x_gstride, _ptr(w),
                                                            w_gstride, _ptr(bias), bias_gstride, _ptr(out), ldc,
                                                            out_gstride))
+
+    def gemv_grouped_f32(self, G, N, K, x, x_gstride, w, w_gstride, y, y_gstride, alpha=0.0, accumulate=False):
+        """anima_gemv_grouped_f32: y_g = alpha * W_g x_g (+ y_g) for G groups in one launch."""
+        return self._check(lib().anima_gemv_grouped_f32(self.h, G, N, K, _ptr(x), x_gstride, _ptr(w), w_gstride,
+                                                        _ptr(y), y_gstride, alpha, int(accumulate)))
 
     def patchify(self, latents, B, h, w, patches):
         return self._check(lib().anima_patchify(self.h, _ptr(latents), B, h, w, _ptr(patches)))

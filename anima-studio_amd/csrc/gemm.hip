@@ -2687,6 +2687,41 @@ int linear_grouped_bf16_launch(anima_ctx* c, int G, int64_t M, int N, int K, con
   return L.end();
 }
 
+// G fp32 GEMVs, one output per thread: y_g[n] = alpha * sum_k w_g[n][k] x_g[k] (+ y_g[n]), the sum
+// in k order with fp32 FMAs, the product then scaled and added as in the linear epilogues.
+__global__ __launch_bounds__(256) void gemv_grouped_f32_kernel(const float* x, int64_t x_gs, const float* w, int64_t w_gs,
+                                                               float* y, int64_t y_gs, int N, int K, float alpha,
+                                                               int accumulate) {
+  const int g = blockIdx.y, n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  const float4* wr = (const float4*)(w + g * w_gs + (int64_t)n * K);
+  const float4* xr = (const float4*)(x + g * x_gs);
+  float s = 0.0f;
+  for (int k = 0; k < K / 4; k++) {
+    const float4 a = wr[k], b = xr[k];
+    s = __builtin_fmaf(a.x, b.x, s);
+    s = __builtin_fmaf(a.y, b.y, s);
+    s = __builtin_fmaf(a.z, b.z, s);
+    s = __builtin_fmaf(a.w, b.w, s);
+  }
+  float* o = y + g * y_gs + n;
+  const float r = s * alpha;
+  *o = accumulate ? *o + r : r;
+}
+
+int gemv_grouped_f32_launch(anima_ctx* c, int G, int N, int K, const float* x, int64_t x_gs, const float* w, int64_t w_gs,
+                            float* y, int64_t y_gs, float alpha, int accumulate) {
+  if (!x || !w || !y) return fail(c, ANIMA_E_ARG, "anima_gemv_grouped_f32: null x, w or y");
+  if (G < 1 || G > 65535 || N < 1 || K < 4 || K % 4)
+    return fail(c, ANIMA_E_ARG, "anima_gemv_grouped_f32: G=%d N=%d K=%d (1 <= G <= 65535, K %% 4 == 0)", G, N, K);
+  if (x_gs < 0 || w_gs < 0 || y_gs < 0 || x_gs % 4 || w_gs % 4 || !al(x, 16) || !al(w, 16))
+    return fail(c, ANIMA_E_ARG, "anima_gemv_grouped_f32: x and w 16-byte aligned, x / w group strides >= 0 and %% 4 == 0");
+  Launch L(c, "gemv.f32.grouped", 2.0 * G * N * K, 4.0 * G * N * K);
+  hipLaunchKernelGGL(gemv_grouped_f32_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)G), dim3(256), 0, c->stream, x,
+                     x_gs, w, w_gs, y, y_gs, N, K, alpha != 0.0f ? alpha : 1.0f, accumulate ? 1 : 0);
+  return L.end();
+}
+
 }  // namespace anima
 
 namespace anima {

@@ -146,5 +146,7 @@ int linear_qkv_launch(anima_ctx* c, const anima_linear_desc* d, const anima_qkv_
 int linear_grouped_bf16_launch(anima_ctx* c, int G, int64_t M, int N, int K, const float* x, int64_t ldx,
                                int64_t x_gs, const uint16_t* w, int64_t w_gs, const float* bias, int64_t bias_gs,
                                float* out, int64_t ldc, int64_t out_gs);
+int gemv_grouped_f32_launch(anima_ctx* c, int G, int N, int K, const float* x, int64_t x_gs, const float* w, int64_t w_gs,
+                            float* y, int64_t y_gs, float alpha, int accumulate);
 
 }  // namespace anima

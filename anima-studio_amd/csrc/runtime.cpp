@@ -665,6 +665,12 @@ int anima_linear_grouped_bf16(anima_ctx* c, int G, int64_t M, int N, int K, cons
                                     out_gstride);
 }
 
+int anima_gemv_grouped_f32(anima_ctx* c, int G, int N, int K, const float* x, int64_t x_gstride, const float* w,
+                           int64_t w_gstride, float* y, int64_t y_gstride, float alpha, int accumulate) {
+  CHECK_CTX(c);
+  return gemv_grouped_f32_launch(c, G, N, K, x, x_gstride, w, w_gstride, y, y_gstride, alpha, accumulate);
+}
+
 #define ABI_FIELD(T, f) {#T, #f, (int64_t)offsetof(T, f)}
 #define ABI_SIZE(T) {#T, nullptr, (int64_t)sizeof(T)}
 static const struct {

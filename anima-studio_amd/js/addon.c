@@ -647,6 +647,18 @@ static napi_value js_elementwise(napi_env env, napi_callback_info info) {
   return NULL;
 }
 
+/* gemvGroupedF32(ctx, G, N, K, x, xStride, w, wStride, y, yStride, alpha, accumulate) */
+static napi_value js_gemv_grouped_f32(napi_env env, napi_callback_info info) {
+  napi_value a[12];
+  get_args(env, info, 12, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_gemv_grouped_f32(c, (int)num(env, a[1]), (int)num(env, a[2]), (int)num(env, a[3]),
+                                          (const float*)ptr(env, a[4]), i64(env, a[5]), (const float*)ptr(env, a[6]),
+                                          i64(env, a[7]), (float*)ptr(env, a[8]), i64(env, a[9]), (float)num(env, a[10]),
+                                          (int)num(env, a[11])));
+  return NULL;
+}
+
 /* linearGroupedBf16(ctx, G, M, N, K, x, ldx, xStride, w, wStride, bias, biasStride, out, ldc, outStride) */
 static napi_value js_linear_grouped_bf16(napi_env env, napi_callback_info info) {
   napi_value a[15];
@@ -947,7 +959,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       FN("timerStart", js_timer_start), FN("timerStop", js_timer_stop), FN("attention", js_attention),
       FN("qkNormRope", js_qk_norm_rope), FN("rmsnorm", js_rmsnorm), FN("rope", js_rope),
       FN("hadamard", js_hadamard), FN("quantRows", js_quant_rows), FN("layernormMod", js_layernorm_mod),
-      FN("elementwise", js_elementwise), FN("zero", js_zero), FN("patchify", js_patchify), FN("linearGroupedBf16", js_linear_grouped_bf16), FN("unpatchify", js_unpatchify), FN("fillRandom", js_fill_random),
+      FN("elementwise", js_elementwise), FN("zero", js_zero), FN("patchify", js_patchify), FN("linearGroupedBf16", js_linear_grouped_bf16), FN("gemvGroupedF32", js_gemv_grouped_f32), FN("unpatchify", js_unpatchify), FN("fillRandom", js_fill_random),
       FN("linear", js_linear), FN("linearQkv", js_linear_qkv), FN("samplerStep", js_sampler_step), FN("attentionKvBytes", js_attention_kv_bytes), FN("split3", js_split3), FN("lastError", js_last_error),
       FN("graphBegin", js_graph_begin), FN("graphEnd", js_graph_end), FN("graphLaunch", js_graph_launch),
       FN("graphDestroy", js_graph_destroy), FN("conv3x3", js_conv3x3), FN("channelNorm", js_channel_norm), FN("toRgba", js_to_rgba),

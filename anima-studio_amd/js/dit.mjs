@@ -70,6 +70,17 @@ function projectParts(gpu, x, mod, Ws, M) {
   return qkv;
 }
 
+// out[g] += B_g (A_g x_g) for the G parts of a grouped modulation LoRA stage (modLoraPlan): x_g =
+// x + g * xStride (xStride 0: one row shared by every part), out[g] = out's g-th st.n-slice; the
+// scales are folded into B_g.
+function loraGrouped(gpu, st, x, xStride, out) {
+  const t = gpu.empty([st.G * st.r]);
+  if (xStride === 0) native.gemvGroupedF32(gpu.ctx, 1, st.G * st.r, st.K, x.buf, 0, st.A.buf, 0, t.buf, 0, 1, 0);
+  else native.gemvGroupedF32(gpu.ctx, st.G, st.r, st.K, x.buf, xStride, st.A.buf, st.r * st.K, t.buf, st.r, 1, 0);
+  native.gemvGroupedF32(gpu.ctx, st.G, st.n, st.r, t.buf, st.r, st.B.buf, st.n * st.r, out.buf, st.n, 1, 1);
+  t.release();
+}
+
 // out (an M = 1 row) += scale * B (A x) for one LoRA entry of a linear whose product runs outside
 // ops.linear (the grouped modulation GEMV); x is that linear's input row.
 function loraPart(gpu, x, e, out) {
@@ -151,6 +162,7 @@ export class AnimaDiT {
     this.gpu = gpu;
     this.ropeCache = new Map(); // "HpxWp" -> device RoPE table; depends only on the token grid
     this.modFused = null;
+    this.modPlan = null; // grouped LoRA products of the fused modulation (modLoraPlan)
     // attention precision: bf16 matrix-core operands with fp32 accumulation ("fp32": the fp32-MFMA
     // kernels, the reference's arithmetic); prepareContext records the one its K/V were made for
     this.precision = "bf16";
@@ -206,10 +218,12 @@ export class AnimaDiT {
     return t;
   }
 
-  // Frees the device tables cached across forward calls (the weights belong to their loader).
+  // Frees the device tables cached across forward calls and the grouped modulation LoRA plan (the
+  // weights belong to their loader).
   releaseCaches() {
     for (const t of this.ropeCache.values()) t.release();
     this.ropeCache.clear();
+    this.releaseModPlan();
   }
 
   // Everything that depends only on sigma (app/models/dit.js:196-225).
@@ -226,7 +240,10 @@ export class AnimaDiT {
     if (this.modFused) {
       const { w1, w2, final2 } = this.modFused;
       const G = 3 * this.blocks.length, R = ADALN_RANK;
-      const h1 = ops.linear(gpu, semb, w1); // [1, (G + 1) * 256]
+      const plan = this.modLoraPlan();
+      // LoRAs on first stages: grouped (plan.s1) after the plain product, else inside ops.linear
+      const h1 = ops.linear(gpu, semb, plan.s1 ? Object.assign({}, w1, { lora: null }) : w1); // [1, (G + 1) * 256]
+      if (plan.s1) loraGrouped(gpu, plan.s1, semb, 0, h1);
       const all = gpu.empty([G, 3 * D]);
       native.linearGroupedBf16(gpu.ctx, G, 1, 3 * D, R, h1.buf, (G + 1) * R, R, w2.buf.buf, 3 * D * R, lora.buf, 0,
         all.buf, 3 * D, 3 * D);
@@ -234,7 +251,8 @@ export class AnimaDiT {
       native.linearGroupedBf16(gpu.ctx, 1, 1, 2 * D, R, h1.at(G * R), R, 0, final2.buf.buf, 0, lora.buf, 0, final.buf,
         2 * D, 0);
       // LoRAs on second stages: part j of w2 is group j, which reads h1's j-th 256-slice
-      if (w2.lora) for (const e of w2.lora) loraPart(gpu, h1.view((e.off / (3 * D)) * R, [1, R]), e, all.view(e.off, [1, e.n]));
+      if (plan.s2) loraGrouped(gpu, plan.s2, h1, R, all);
+      else if (w2.lora) for (const e of w2.lora) loraPart(gpu, h1.view((e.off / (3 * D)) * R, [1, R]), e, all.view(e.off, [1, e.n]));
       if (final2.lora) for (const e of final2.lora) loraPart(gpu, h1.view(G * R, [1, R]), e, final.view(e.off, [1, e.n]));
       h1.release();
       semb.release();
@@ -255,6 +273,49 @@ export class AnimaDiT {
     semb.release();
     lora.release();
     return this.timeCondFrom(parts, false);
+  }
+
+  // The LoRA products of the fused modulation as grouped fp32 GEMVs (anima_gemv_grouped_f32): per
+  // stage (w1: the first stages, parts of 256 columns; w2: the second stages, parts of 3D columns,
+  // part j reading h1's j-th 256-slice) one A product and one B product over all its entries,
+  // instead of two launches per entry.  A stage qualifies when its entries have one rank and at
+  // most one entry per part: the A matrices are stacked per part (zero rows for parts without an
+  // entry) and the B matrices likewise, each scaled by its entry's scale.  Built once per LoRA
+  // attachment (W.lora is replaced on every attach); { s1, s2 } with null for a stage without
+  // entries or of another layout (that stage keeps the per-entry products).
+  modLoraPlan() {
+    const { w1, w2 } = this.modFused;
+    const p = this.modPlan;
+    if (p && p.l1 === w1.lora && p.l2 === w2.lora) return p;
+    this.releaseModPlan();
+    const gpu = this.gpu;
+    const stage = (W, partN) => {
+      const es = W.lora || [];
+      if (!es.length || W.K % 4) return null;
+      const r = es[0].r, G = W.N / partN, seen = new Set();
+      for (const e of es) {
+        if (e.r !== r || r % 4 || e.n !== partN || e.off % partN || seen.has(e.off)) return null;
+        seen.add(e.off);
+      }
+      const A = gpu.empty([G * r, W.K]);
+      const Bh = new Float32Array(G * partN * r), b = new Float32Array(partN * r);
+      if (es.length < G) ops.zero(gpu, A);
+      for (const e of es) {
+        const g = e.off / partN;
+        gpu.copy(A.at(g * r * W.K), e.A, r * W.K * 4);
+        native.d2h(gpu.ctx, e.B.buf, b);
+        for (let i = 0; i < b.length; i++) Bh[g * b.length + i] = Math.fround(e.scale * b[i]);
+      }
+      return { G, r, K: W.K, n: partN, A, B: gpu.fromArray(Bh, [G * partN, r]) };
+    };
+    this.modPlan = { l1: w1.lora, l2: w2.lora, s1: stage(w1, ADALN_RANK), s2: stage(w2, 3 * D) };
+    return this.modPlan;
+  }
+
+  releaseModPlan() {
+    const p = this.modPlan;
+    if (p) for (const st of [p.s1, p.s2]) if (st) releaseAll([st.A, st.B]);
+    this.modPlan = null;
   }
 
   // A timeCond result over its tensors: fused, [all [3*blocks, 3D], final [1, 2D]] (blocks are

@@ -498,6 +498,16 @@ int anima_linear_grouped_bf16(anima_ctx* ctx, int G, int64_t M, int N, int K, co
                               int64_t x_gstride, const uint16_t* w, int64_t w_gstride, const float* bias,
                               int64_t bias_gstride, float* out, int64_t ldc, int64_t out_gstride);
 
+/* G independent fp32 GEMVs (one input row each) in one launch, for the LoRA products of the adaLN
+ * modulation linears (ops.js:70-87 runs two matmuls per LoRA entry; timeCond has one entry per
+ * modulation linear, all of one rank):
+ *   y[g*y_gstride + n] = alpha * sum_k w[g*w_gstride + n*K + k] * x[g*x_gstride + k]
+ *                        (+ y[g*y_gstride + n] when accumulate)
+ * for g < G, n < N, the sum in k order with fp32 FMAs.  K % 4 == 0, x and w 16-byte aligned,
+ * x_gstride and w_gstride multiples of 4; alpha 0 means 1. */
+int anima_gemv_grouped_f32(anima_ctx* ctx, int G, int N, int K, const float* x, int64_t x_gstride, const float* w,
+                           int64_t w_gstride, float* y, int64_t y_gstride, float alpha, int accumulate);
+
 #ifdef __cplusplus
 }
 #endif

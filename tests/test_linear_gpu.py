@@ -818,3 +818,32 @@ def test_weight_unpack_w4_grid_and_linear(ctx, K):
     assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
     with pytest.raises(m.AnimaError):
         ctx.weight_unpack_w4(W8, dgrid)  # not a W4 weight
+
+
+@pytest.mark.parametrize("G,N,K,acc", [(85, 256, 32, True), (84, 32, 256, False), (1, 2720, 2048, False),
+                                       (3, 6144, 8, True)])
+def test_gemv_grouped_f32(ctx, G, N, K, acc):
+    """anima_gemv_grouped_f32 (the grouped LoRA products of the adaLN modulation): y_g = alpha W_g x_g
+    (+ y_g) for G groups in one launch, within 1e-6 of float64 (first-stage B products: 85 x 256
+    from rank 32; second-stage A products: 84 x rank 32 from 256; one stacked A product over K =
+    2048; gaps between the groups' x and y slices)."""
+    case(f"grouped fp32 GEMV G={G} N={N} K={K} acc={acc}")
+    m = amd()
+    xs, ys = K + 4, N + 8
+    x = orc.randn(191, G * xs).astype(np.float32)
+    w = (0.05 * orc.randn(192, G * N * K)).astype(np.float32)
+    y0 = orc.randn(193, G * ys).astype(np.float32)
+    dx, dw, dy = ctx.upload(x), ctx.upload(w), ctx.upload(y0)
+    ctx.gemv_grouped_f32(G, N, K, dx, xs, dw, N * K, dy, ys, alpha=0.75, accumulate=acc)
+    got = dy.numpy().reshape(G, ys)
+    X = x.reshape(G, xs)[:, :K].astype(np.float64)
+    Wm = w.reshape(G, N, K).astype(np.float64)
+    ref = 0.75 * np.einsum("gnk,gk->gn", Wm, X)
+    want = y0.reshape(G, ys).astype(np.float64).copy()
+    want[:, :N] = want[:, :N] + ref if acc else ref
+    assert np.array_equal(got[:, N:], y0.reshape(G, ys)[:, N:])
+    assert report("grouped fp32 GEMV", got[:, :N], want[:, :N])[0] < 1e-6
+    with pytest.raises(m.AnimaError):
+        ctx.gemv_grouped_f32(G, N, K + 2, dx, xs, dw, N * K, dy, ys)
+    with pytest.raises(m.AnimaError):
+        ctx.gemv_grouped_f32(G, N, K, dx, xs + 2, dw, N * K, dy, ys)
