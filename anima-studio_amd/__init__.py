@@ -54,6 +54,7 @@ class AttnDesc(ctypes.Structure):
         ("kv_prep", _vp),
         ("kv_prep_bytes", _i64),
         ("q_prep", _vp),
+        ("o_bf16", ctypes.c_int),
     ]
 
 
@@ -167,6 +168,7 @@ def lib():
         L.anima_hadamard.argtypes = [_vp, _vp, _vp, _i64]
         L.anima_quant_rows.argtypes = [_vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _vp, _vp]
         L.anima_quant_rows_act.argtypes = [_vp, _vp, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp]
+        L.anima_quant_rows_bf16.argtypes = [_vp, _vp, _i64, ctypes.c_int, ctypes.c_int, _vp, _vp]
         L.anima_layernorm_mod.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, ctypes.c_int, ctypes.c_float, ctypes.c_int,
                                           _vp, _vp, _vp]
         L.anima_elementwise.argtypes = [_vp, ctypes.c_int, _vp, _vp, _vp, _i64]
@@ -345,12 +347,13 @@ class Context:
                   o_off=0, q_bstride=None, k_bstride=None, v_bstride=None, o_bstride=None, group=1, scale=0.0,
                   kv_len=None, precision=PREC_BF16, q_norm=None, k_norm=None, rope_cs=None, rope_sin_off=0,
                   eps=1e-6, causal=0, kv_prep=None, prepare_into=None, kv_prep_bytes=None, noalloc=False,
-                  q_prep=None):
+                  q_prep=None, o_bf16=False):
         """anima_attention; kv_prep: K/V converted by a call with prepare_into (which runs
         anima_attention_prepare_kv into that buffer instead of the attention).  kv_prep_bytes
         defaults to the size the call's shape and precision take.  noalloc: anima_attention_noalloc
         (the K/V conversion in the library's static scratch, no allocation).  q_prep: Q as
-        linear_qkv(q_prep=...) prepared it (then q may be None)."""
+        linear_qkv(q_prep=...) prepared it (then q may be None).  o_bf16: O written as bf16 (o and its
+        strides in uint16 elements)."""
         ldo = ldo if ldo is not None else H * D
         kl = (ctypes.c_int * B)(*[int(x) for x in kv_len]) if kv_len is not None else None
         d = AttnDesc(B=B, Lq=Lq, Lk=Lk, H=H, D=D, group=group,
@@ -361,6 +364,7 @@ class Context:
                      scale=scale, kv_len=ctypes.cast(kl, ctypes.POINTER(ctypes.c_int)) if kl is not None else None,
                      precision=precision, q_norm=_ptr(q_norm), k_norm=_ptr(k_norm), rope_cs=_ptr(rope_cs),
                      rope_sin_off=rope_sin_off, eps=eps, causal=causal, kv_prep=_ptr(kv_prep), q_prep=_ptr(q_prep),
+                     o_bf16=int(o_bf16),
                      kv_prep_bytes=kv_prep_bytes if kv_prep_bytes is not None else
                      (self.attention_kv_bytes(B, H // max(group, 1), Lk, precision)
                       if (kv_prep is not None or prepare_into is not None) else 0))
@@ -401,6 +405,10 @@ class Context:
             return self._check(lib().anima_quant_rows_act(self.h, _ptr(x), M, K, ACT[act], int(rotate), _ptr(q),
                                                           _ptr(s)))
         return self._check(lib().anima_quant_rows(self.h, _ptr(x), M, K, int(rotate), _ptr(q), _ptr(s)))
+
+    def quant_rows_bf16(self, x, M, K, rotate, q, s):
+        """anima_quant_rows_bf16: quant_rows of bf16 rows (uint16 x)."""
+        return self._check(lib().anima_quant_rows_bf16(self.h, _ptr(x), M, K, int(rotate), _ptr(q), _ptr(s)))
 
     def layernorm_mod(self, x, mod, shift_off, scale_off, rows, cols, rotate=False, y=None, q=None, s=None, eps=1e-6):
         return self._check(lib().anima_layernorm_mod(self.h, _ptr(x), _ptr(mod), shift_off, scale_off, rows, cols, eps,

@@ -333,6 +333,7 @@ struct FlashArgs {
   // prepared Q (the bf16 kernels' QP form): [B][Lq][H][128] bf16, each value the kernel's own
   // to_bf16(c * q') of the normed, rotated query q'; then q, qn and cs are not read
   const uint16_t* qp;
+  int obf;  // O written as bf16 (o then addresses uint16 elements)
 };
 
 // Loads this lane's 64 Q values (query qi, dims 16ks + 8hf + j), applies the fused
@@ -811,14 +812,19 @@ __global__ __launch_bounds__(256, KB == 32 ? 3 : 2) void attn_flash_bf16(FlashAr
   l = pair_sum(l);
   if (qi < a.Lq) {
     const float inv = 1.0f / l;
-    float* dst = a.o + (int64_t)b * a.o_bs + (int64_t)qi * a.ldo + h * a.D + 4 * hf;
+    const int64_t off = (int64_t)b * a.o_bs + (int64_t)qi * a.ldo + h * a.D + 4 * hf;
+    float* dst = a.o + off;
+    bf16* dst16 = (bf16*)a.o + off;
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
       if (32 * dt < a.D)  // D = 64: dim tiles 2, 3 are padding
 #pragma unroll
-        for (int g = 0; g < 4; g++)
-          *(float4*)(dst + 32 * dt + 8 * g) =
+        for (int g = 0; g < 4; g++) {
+          const float4 v =
               make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+          if (a.obf) *(bf16x4*)(dst16 + 32 * dt + 8 * g) = bf16x4{to_bf16(v.x), to_bf16(v.y), to_bf16(v.z), to_bf16(v.w)};
+          else *(float4*)(dst + 32 * dt + 8 * g) = v;
+        }
   }
 }
 constexpr int FLASH_KB = 64;  // keys per block of the bf16 kernel
@@ -1082,6 +1088,7 @@ __global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
   float* ow = (float*)smem + wave * (32 * W8_OROW);
   const int rr = lane >> 4, cc = 4 * (lane & 15);
   float* dst = a.o + (int64_t)b * a.o_bs + h * HD + cc;
+  bf16* dst16 = (bf16*)a.o + (int64_t)b * a.o_bs + h * HD + cc;
   const int q0 = qt * W8_BQ + wave * 32;
 #pragma unroll
   for (int half = 0; half < 2; half++) {
@@ -1098,7 +1105,13 @@ __global__ __launch_bounds__(512, 1) void attn_flash_w8(FlashArgs a) {
     for (int k = 0; k < 8; k++) {
       const int r = 4 * k + rr;
       const float4 v = *(const float4*)(ow + r * W8_OROW + cc);
-      if (q0 + r < a.Lq) *(float4*)(dst + (int64_t)(q0 + r) * a.ldo + 64 * half) = v;
+      if (q0 + r < a.Lq) {
+        if (a.obf)
+          *(bf16x4*)(dst16 + (int64_t)(q0 + r) * a.ldo + 64 * half) =
+              bf16x4{to_bf16(v.x), to_bf16(v.y), to_bf16(v.z), to_bf16(v.w)};
+        else
+          *(float4*)(dst + (int64_t)(q0 + r) * a.ldo + 64 * half) = v;
+      }
     }
   }
 }
@@ -1255,6 +1268,8 @@ static int attention_check(anima_ctx* c, const anima_attn_desc* d, int (&kv_len)
     return fail(c, ANIMA_E_ARG, "anima_attention: a prepared Q needs bf16 precision, D = 128 and 16-byte alignment");
   if (d->precision != ANIMA_PREC_BF16 && d->precision != ANIMA_PREC_FP32)
     return fail(c, ANIMA_E_ARG, "anima_attention: unknown precision %d", d->precision);
+  if (d->o_bf16 && d->precision != ANIMA_PREC_BF16)
+    return fail(c, ANIMA_E_ARG, "anima_attention: a bf16 O needs bf16 precision");
   const int64_t lds[4] = {d->ldq, d->ldk, d->ldv, d->ldo};
   const int64_t offs[4] = {d->q_off, d->k_off, d->v_off, d->o_off};
   const int64_t bss[4] = {d->q_bstride, d->k_bstride, d->v_bstride, d->o_bstride};
@@ -1357,6 +1372,7 @@ int attention_launch_ws(anima_ctx* c, const anima_attn_desc* d, void* scratch) {
   // ops.js:170); any other head dim: the chunked path (app/gpu/ops.js:177-207)
   const bool flash64 = d->D == HD / 2 && !d->q_norm && !d->k_norm && !d->rope_cs && !d->kv_prep;
   if (d->D != HD && !flash64) {
+    if (d->o_bf16) return fail(c, ANIMA_E_UNSUPPORTED, "anima_attention: a bf16 O on the chunked path (head dim %d)", d->D);
     int rc = attention_chunked_check(c, d);
     if (rc) return rc;
     int kvl[MAXB];
@@ -1392,7 +1408,8 @@ int attention_launch_ws(anima_ctx* c, const anima_attn_desc* d, void* scratch) {
   f.q_bs = d->q_bstride;
   f.kb = ws;
   f.vt = (char*)ws + plane;
-  f.o = d->o + d->o_off;
+  // (with a bf16 O the offset counts uint16 elements)
+  f.o = d->o_bf16 ? (float*)((uint16_t*)d->o + d->o_off) : d->o + d->o_off;
   f.ldo = d->ldo;
   f.o_bs = d->o_bstride;
   f.qn = d->q_norm;
@@ -1414,6 +1431,7 @@ int attention_launch_ws(anima_ctx* c, const anima_attn_desc* d, void* scratch) {
   f.causal = d->causal ? 1 : 0;
   f.D = d->D;
   f.qp = (const uint16_t*)d->q_prep;
+  f.obf = d->o_bf16 ? 1 : 0;
   double flops = 0;
   for (int b = 0; b < d->B; b++) flops += 4.0 * d->Lq * (double)kv_len[b] * d->D * d->H;
   const int blocks = f.n_qt * d->H * d->B;

@@ -125,6 +125,7 @@ int rope_launch(anima_ctx* c, float* x, const float* cs, int64_t L, int H, int D
                 int64_t sin_off, int64_t row_stride, int64_t col_off);
 int hadamard_launch(anima_ctx* c, const float* x, float* y, int64_t n);
 int quant_rows_launch(anima_ctx* c, const float* x, int64_t M, int K, int rotate, int act, int8_t* q, float* s);
+int quant_rows_bf16_launch(anima_ctx* c, const uint16_t* x, int64_t M, int K, int rotate, int8_t* q, float* s);
 int layernorm_mod_launch(anima_ctx* c, const float* x, const float* mod, int64_t shift_off, int64_t scale_off,
                          int64_t rows, int cols, float eps, int rotate, float* y, int8_t* q, float* s);
 int elementwise_launch(anima_ctx* c, int op, const float* a, const float* b, float* y, int64_t n);

@@ -487,6 +487,38 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(const float* X, int
   quant64_store(v, am, Q + row * K + 64 * L);
 }
 
+// quant_rows_reg_kernel on bf16 rows: each lane's 64 values arrive as eight 16-byte loads of
+// bf16 and are widened exactly (bits << 16), then the same Hadamard, maximum and int8 rounding.
+template <int LR>
+__global__ __launch_bounds__(256) void quant_rows_bf16_kernel(const uint16_t* X, int64_t M, int rotate, int8_t* Q,
+                                                              float* S_out) {
+  constexpr int K = 64 * LR;
+  __shared__ float red[4];
+  const int L = threadIdx.x % LR;
+  const int64_t row = (int64_t)blockIdx.x * (256 / LR) + threadIdx.x / LR;
+  const bool live = row < M;  // (dead rows still take part in the cross-wave maximum)
+  const uint16_t* x = X + (live ? row : 0) * K + 64 * L;
+  float v[64];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint4 t = *(const uint4*)(x + 8 * i);
+    const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      v[8 * i + 2 * e] = __uint_as_float(w[e] << 16);
+      v[8 * i + 2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+    }
+  }
+  if (rotate) hadamard64_quad<false>(v, L & 3);
+  float am = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 64; i++) am = fmaxf(am, fabsf(v[i]));
+  am = rows_max<LR>(am, red);
+  if (!live) return;
+  if (L == 0) S_out[row] = (rotate ? am * 0.0625f : am) / 127.0f;
+  quant64_store(v, am, Q + row * K + 64 * L);
+}
+
 // LayerNorm (no affine) + adaLN (+ Hadamard) (+ int8), one wave per row (app/gpu/kernels.js:108-145).
 // Lane l holds the float4 chunks l, l+64, ... i.e. elements 4l + j + 256i, exactly the elements
 // the reference's 256-thread loops give to threads 4l + j, so the strided partial sums and the
@@ -753,6 +785,23 @@ int quant_rows_launch(anima_ctx* c, const float* x, int64_t M, int K, int rotate
   else  // one wave per row, four rows per workgroup
     hipLaunchKernelGGL(quant_rows_pad_kernel<1>, dim3((unsigned)((M + 3) / 4)), dim3(256), (size_t)4 * padded_cols(K) * 4,
                        c->stream, x, M, K, rotate, act, q, s);
+  return lc.end();
+}
+
+int quant_rows_bf16_launch(anima_ctx* c, const uint16_t* x, int64_t M, int K, int rotate, int8_t* q, float* s) {
+  if (!x || !q || !s) return fail(c, ANIMA_E_ARG, "anima_quant_rows_bf16: null pointer");
+  if (M < 0 || M > 0x7fffffff || (K != 1024 && K != 2048 && K != 4096 && K != 8192))
+    return fail(c, ANIMA_E_ARG, "anima_quant_rows_bf16: M=%lld K=%d (K = 1024, 2048, 4096 or 8192)", (long long)M, K);
+  if (((uintptr_t)x & 15) || ((uintptr_t)q & 15)) return fail(c, ANIMA_E_ARG, "anima_quant_rows_bf16: x and q must be 16-byte aligned");
+  if (M == 0) return ANIMA_OK;
+  Launch lc(c, rotate ? "hadamard_quant_bf16" : "quant_rows_bf16", 0.0, (double)M * K * 3 + M * 4.0);
+  const dim3 grid((unsigned)((M + 256 / (K / 64) - 1) / (256 / (K / 64))));
+  switch (K) {
+    case 1024: hipLaunchKernelGGL(quant_rows_bf16_kernel<16>, grid, dim3(256), 0, c->stream, x, M, rotate, q, s); break;
+    case 2048: hipLaunchKernelGGL(quant_rows_bf16_kernel<32>, grid, dim3(256), 0, c->stream, x, M, rotate, q, s); break;
+    case 4096: hipLaunchKernelGGL(quant_rows_bf16_kernel<64>, grid, dim3(256), 0, c->stream, x, M, rotate, q, s); break;
+    default: hipLaunchKernelGGL(quant_rows_bf16_kernel<128>, grid, dim3(256), 0, c->stream, x, M, rotate, q, s); break;
+  }
   return lc.end();
 }
 

@@ -605,6 +605,11 @@ int anima_quant_rows_act(anima_ctx* c, const float* x, int64_t M, int K, int act
   return quant_rows_launch(c, x, M, K, rotate, act, q, s);
 }
 
+int anima_quant_rows_bf16(anima_ctx* c, const uint16_t* x, int64_t M, int K, int rotate, int8_t* q, float* s) {
+  CHECK_CTX(c);
+  return quant_rows_bf16_launch(c, x, M, K, rotate, q, s);
+}
+
 int anima_layernorm_mod(anima_ctx* c, const float* x, const float* mod, int64_t shift_off, int64_t scale_off,
                         int64_t rows, int cols, float eps, int rotate, float* y, int8_t* q, float* s) {
   CHECK_CTX(c);
@@ -689,7 +694,7 @@ static const struct {
     ABI_FIELD(anima_attn_desc, kv_len), ABI_FIELD(anima_attn_desc, precision), ABI_FIELD(anima_attn_desc, q_norm),
     ABI_FIELD(anima_attn_desc, k_norm), ABI_FIELD(anima_attn_desc, rope_cs), ABI_FIELD(anima_attn_desc, rope_sin_off),
     ABI_FIELD(anima_attn_desc, eps), ABI_FIELD(anima_attn_desc, causal), ABI_FIELD(anima_attn_desc, kv_prep),
-    ABI_FIELD(anima_attn_desc, kv_prep_bytes), ABI_FIELD(anima_attn_desc, q_prep),
+    ABI_FIELD(anima_attn_desc, kv_prep_bytes), ABI_FIELD(anima_attn_desc, q_prep), ABI_FIELD(anima_attn_desc, o_bf16),
     ABI_SIZE(anima_weight), ABI_FIELD(anima_weight, kind), ABI_FIELD(anima_weight, N), ABI_FIELD(anima_weight, K),
     ABI_FIELD(anima_weight, w), ABI_FIELD(anima_weight, scale), ABI_FIELD(anima_weight, srel),
     ABI_FIELD(anima_weight, codebook), ABI_FIELD(anima_weight, bias),

@@ -539,6 +539,7 @@ static napi_value js_attention(napi_env env, napi_callback_info info) {
   d.kv_prep = pptr(env, o, "kvPrep");
   d.kv_prep_bytes = (int64_t)pnum(env, o, "kvPrepBytes");
   d.q_prep = pptr(env, o, "qPrep");
+  d.o_bf16 = (int)pnum(env, o, "oBf16");
   void* prepare_into = pptr(env, o, "prepareInto"); /* run anima_attention_prepare_kv into it */
   int kv[64];
   napi_value kvl = prop(env, o, "kvLen");
@@ -622,6 +623,16 @@ static napi_value js_quant_rows(napi_env env, napi_callback_info info) {
   else
     CHECK_RC(env, c, anima_quant_rows(c, (const float*)ptr(env, a[1]), i64(env, a[2]), (int)num(env, a[3]),
                                       (int)num(env, a[4]), (int8_t*)ptr(env, a[5]), (float*)ptr(env, a[6])));
+  return NULL;
+}
+
+/* quantRowsBf16(ctx, x, M, K, rotate, q, s): anima_quant_rows_bf16 */
+static napi_value js_quant_rows_bf16(napi_env env, napi_callback_info info) {
+  napi_value a[7];
+  get_args(env, info, 7, a);
+  anima_ctx* c = ctx_of(env, a[0]);
+  CHECK_RC(env, c, anima_quant_rows_bf16(c, (const uint16_t*)ptr(env, a[1]), i64(env, a[2]), (int)num(env, a[3]),
+                                         (int)num(env, a[4]), (int8_t*)ptr(env, a[5]), (float*)ptr(env, a[6])));
   return NULL;
 }
 
@@ -958,7 +969,7 @@ static napi_value Init(napi_env env, napi_value exports) {
       FN("profileReset", js_profile_reset), FN("profileReport", js_profile_report),
       FN("timerStart", js_timer_start), FN("timerStop", js_timer_stop), FN("attention", js_attention),
       FN("qkNormRope", js_qk_norm_rope), FN("rmsnorm", js_rmsnorm), FN("rope", js_rope),
-      FN("hadamard", js_hadamard), FN("quantRows", js_quant_rows), FN("layernormMod", js_layernorm_mod),
+      FN("hadamard", js_hadamard), FN("quantRows", js_quant_rows), FN("quantRowsBf16", js_quant_rows_bf16), FN("layernormMod", js_layernorm_mod),
       FN("elementwise", js_elementwise), FN("zero", js_zero), FN("patchify", js_patchify), FN("linearGroupedBf16", js_linear_grouped_bf16), FN("gemvGroupedF32", js_gemv_grouped_f32), FN("unpatchify", js_unpatchify), FN("fillRandom", js_fill_random),
       FN("linear", js_linear), FN("linearQkv", js_linear_qkv), FN("samplerStep", js_sampler_step), FN("attentionKvBytes", js_attention_kv_bytes), FN("split3", js_split3), FN("lastError", js_last_error),
       FN("graphBegin", js_graph_begin), FN("graphEnd", js_graph_end), FN("graphLaunch", js_graph_launch),

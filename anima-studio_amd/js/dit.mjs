@@ -42,6 +42,23 @@ function project(gpu, nf, W, M, opts) {
   return ops.linear(gpu, nf.n || null, W, o);
 }
 
+// The attention output projection with its gated residual into x: a bf16 output (attention's
+// oBf16) is quantized here, the form the int8 / W4 GEMM reads, otherwise ops.linear quantizes the
+// fp32 rows itself.
+function outProject(gpu, a, W, M, x, mod) {
+  if (a.dtype === "bf16") {
+    const aq = ops.quantRows(gpu, a, D, true);
+    ops.linear(gpu, null, W, { M, xq: aq, out: x, resid: true, gate: mod, gOff: 2 * D });
+    aq.release();
+  } else {
+    ops.linear(gpu, a, W, { M, out: x, resid: true, gate: mod, gOff: 2 * D });
+  }
+}
+
+// whether an attention may write bf16 O for the output projection W (quantized, and its LoRA if
+// any reads the int8 rows)
+const bf16Out = (W, precision) => precision === "bf16" && ops.needsRotation(W) && !wantsXr(W);
+
 function releaseNorm(nf) {
   if (nf.xq) nf.xq.release();
   if (nf.n) nf.n.release();
@@ -468,7 +485,7 @@ export class AnimaDiT {
           qNorm: b.self.qn, prepareQ: true });
         releaseNorm(nf);
         a = ops.attention(gpu, { qPrep: f.qPrep, kvPrep: f.kvPrep, B, Lq: L, Lk: L, H: HEADS, D: HD, ldq: D,
-          precision: "bf16" });
+          precision: "bf16", oBf16: bf16Out(b.self.o, "bf16") });
         f.qPrep.release();
         f.kvPrep.release();
       } else {
@@ -481,10 +498,11 @@ export class AnimaDiT {
           qkv = projectParts(gpu, x, m.self, [b.self.q, b.self.k, b.self.v], M);
         }
         a = ops.attention(gpu, { q: qkv, k: qkv, v: qkv, B, Lq: L, Lk: L, H: HEADS, D: HD, ldq: 3 * D, ldk: 3 * D,
-          ldv: 3 * D, qOff: 0, kOff: D, vOff: 2 * D, qNorm: b.self.qn, kNorm: b.self.kn, cs, precision: this.precision });
+          ldv: 3 * D, qOff: 0, kOff: D, vOff: 2 * D, qNorm: b.self.qn, kNorm: b.self.kn, cs, precision: this.precision,
+          oBf16: bf16Out(b.self.o, this.precision) });
         qkv.release();
       }
-      ops.linear(gpu, a, b.self.o, { M, out: x, resid: true, gate: m.self, gOff: 2 * D });
+      outProject(gpu, a, b.self.o, M, x, m.self);
       a.release();
 
       // cross-attention against the per-prompt cached keys/values (q RMSNorm fused, no RoPE).  With
@@ -497,16 +515,16 @@ export class AnimaDiT {
           prepareQ: true });
         releaseNorm(nf);
         a = ops.attention(gpu, { qPrep: f.qPrep, kvPrep: kv.prep, B, Lq: L, Lk: cond.Lk, H: HEADS, D: HD, ldq: D,
-          precision: "bf16" });
+          precision: "bf16", oBf16: bf16Out(b.cross.o, "bf16") });
         f.qPrep.release();
       } else {
         const q = project(gpu, nf, b.cross.q, M);
         releaseNorm(nf);
         a = ops.attention(gpu, { q, kvPrep: kv.prep, B, Lq: L, Lk: cond.Lk, H: HEADS, D: HD, ldq: D, qNorm: b.cross.qn,
-          precision: cond.precision });
+          precision: cond.precision, oBf16: bf16Out(b.cross.o, cond.precision) });
         q.release();
       }
-      ops.linear(gpu, a, b.cross.o, { M, out: x, resid: true, gate: m.cross, gOff: 2 * D });
+      outProject(gpu, a, b.cross.o, M, x, m.cross);
       a.release();
 
       // MLP.  With a quantized layer2 (and no LoRA on it that needs the fp32 GELU output), layer1

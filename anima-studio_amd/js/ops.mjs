@@ -40,12 +40,18 @@ export function rotate(gpu, x) {
   return y;
 }
 
-// Per-token int8 quantization of rows [M, K] (optionally ConvRot-rotating first).
+// Per-token int8 quantization of rows [M, K] (optionally ConvRot-rotating first); bf16 rows (an
+// attention output written with oBf16) are widened exactly first.
 export function quantRows(gpu, x, K, rotateFirst, act) {
   const M = x.size / K;
   const q = gpu.empty([M, K], "i8");
   const s = gpu.empty([M]);
-  native.quantRows(gpu.ctx, x.buf, M, K, rotateFirst ? 1 : 0, q.buf, s.buf, ACT[act || "none"]);
+  if (x.dtype === "bf16") {
+    if (act && act !== "none") throw new Error("quantRows: no activation on bf16 rows");
+    native.quantRowsBf16(gpu.ctx, x.buf, M, K, rotateFirst ? 1 : 0, q.buf, s.buf);
+  } else {
+    native.quantRows(gpu.ctx, x.buf, M, K, rotateFirst ? 1 : 0, q.buf, s.buf, ACT[act || "none"]);
+  }
   return { q, s, release() { q.release(); s.release(); } };
 }
 
@@ -377,10 +383,12 @@ export function elementwise(gpu, op, a, b, out) {
 // of a.cs are not needed; bf16 precision, D = 128).
 // a.precision: "fp32" (default, the reference's arithmetic) or "bf16" (bf16 matrix-core operands,
 // fp32 accumulation: the DiT's and the text encoder's choice).
+// a.oBf16: the output as bf16 ([B * Lq, H * D], dtype "bf16"), the input of a quantized output
+// projection (quantRows); bf16 precision on the flash kernels only.
 export function attention(gpu, a) {
   const B = a.B || 1;
   const H = a.H, D = a.D;
-  const o = a.out || gpu.empty([B * a.Lq, H * D]);
+  const o = a.out || gpu.empty([B * a.Lq, H * D], a.oBf16 ? "bf16" : "f32");
   native.attention(gpu.ctx, attnDesc(a, B, H, D, o, { kvPrep: ptr(a.kvPrep), kvPrepBytes: a.kvPrep ? a.kvPrep.bytes : 0 }));
   return o;
 }
@@ -417,7 +425,7 @@ function attnDesc(a, B, H, D, o, extra) {
     oBatch: a.oBatch !== undefined ? a.oBatch : a.Lq * (a.ldo || H * D),
     scale: a.scale || 0, kvLen: a.kvLen || null, precision: precisionId(a),
     qNorm: ptr(a.qNorm), kNorm: ptr(a.kNorm), cs: ptr(a.cs), sinOff: a.cs ? a.cs.sinOff : 0, eps: 1e-6,
-    causal: a.causal ? 1 : 0,
+    causal: a.causal ? 1 : 0, oBf16: a.oBf16 ? 1 : 0,
   }, extra);
 }
 

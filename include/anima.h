@@ -176,6 +176,11 @@ typedef struct {
    * side of rope_cs are not read, and the attention's scale is the one Q was prepared with.  bf16
    * precision and D = 128 only; the results equal those of the fp32 q with q_norm / rope_cs. */
   const void* q_prep;
+  /* 1: O is written as bf16 (round to nearest even of the fp32 result; o, o_off, ldo and
+   * o_bstride then address uint16 elements, ldo % 4 == 0, o 8-byte aligned): the input of a
+   * quantized output projection, which reads it with anima_quant_rows_bf16.  bf16 precision with
+   * D = 128 or 64 (the flash kernels) only. */
+  int o_bf16;
 } anima_attn_desc;
 
 /* ops.attention (app/gpu/ops.js:166-208) on the flash path (kernels.js:158-299), plus the fused
@@ -242,6 +247,10 @@ int anima_split3_bf16(anima_ctx* ctx, const float* src, uint16_t* dst, int64_t n
  * activation output. */
 int anima_quant_rows_act(anima_ctx* ctx, const float* x, int64_t M, int K, int act, int rotate,
                          int8_t* q, float* s);
+/* anima_quant_rows of bf16 rows (each value widened exactly to fp32 first: the same int8 rows and
+ * scales as anima_quant_rows on the widened rows): the attention output written with
+ * anima_attn_desc.o_bf16.  K = 1024, 2048, 4096 or 8192; x and q 16-byte aligned. */
+int anima_quant_rows_bf16(anima_ctx* ctx, const uint16_t* x, int64_t M, int K, int rotate, int8_t* q, float* s);
 /* ops.layernormMod (app/gpu/ops.js:129-137; kernels.js:95-145): LayerNorm without affine,
  * y = LN(x) * (1 + mod[scale_off + c]) + mod[shift_off + c], then the ConvRot Hadamard when
  * rotate != 0.  Writes the fp32 result to y (if non-NULL) and/or its per-token int8

@@ -545,3 +545,41 @@ def test_attention_rejects_bad_arguments(ctx):
         ctx.attention(**{**base, "q_off": 300})
     assert e.value.code == -1
     d.release()
+
+
+@pytest.mark.parametrize("B,H,Lq,Lk,kernel", [(16, 16, 256, 320, "attn.flash_bf16"), (1, 2, 300, 200, "attn.flash_bf16_4w")])
+def test_attention_bf16_output(ctx, B, H, Lq, Lk, kernel):
+    """anima_attn_desc.o_bf16: the 8-wave kernel (a grid of one workgroup per CU) and the 4-wave
+    kernel write O as bf16, each value the round-to-nearest-even of the fp32 output of the same call
+    without it (bit for bit), into a wider row (ldo, o_off in bf16 elements) whose other columns
+    stay untouched; refused with fp32 precision and on the chunked path (D = 96)."""
+    case(f"attention bf16 O B={B} H={H} Lq={Lq} Lk={Lk} ({kernel})")
+    m = amd()
+    q = orc.randn(61, B * Lq * H * HD).reshape(B, Lq, H * HD)
+    k = orc.randn(62, B * Lk * H * HD).reshape(B, Lk, H * HD)
+    v = orc.randn(63, B * Lk * H * HD).reshape(B, Lk, H * HD)
+    kv_len = [max(1, Lk - 37 * b) for b in range(B)]
+    dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
+    args = dict(B=B, Lq=Lq, Lk=Lk, H=H, D=HD, ldq=H * HD, ldk=H * HD, ldv=H * HD, kv_len=kv_len, precision=m.PREC_BF16)
+    do = ctx.empty((B, Lq, H * HD))
+    ctx.attention(q=dq, k=dk, v=dv, o=do, **args)
+    ref = do.numpy()
+    ldo = H * HD + 8
+    fill = np.full((B, Lq, ldo), 0x7FC1, np.uint16)
+    d16 = ctx.upload(fill)
+    ctx.profile(True)
+    ctx.profile_reset()
+    ctx.attention(q=dq, k=dk, v=dv, o=d16, ldo=ldo, o_off=4, o_bf16=True, **args)
+    names = {r["name"] for r in ctx.profile_report()}
+    ctx.profile(False)
+    assert kernel in names, names
+    got = d16.numpy().reshape(B, Lq, ldo)
+    want = (orc.bf16_round(ref).view(np.uint32) >> 16).astype(np.uint16)
+    assert np.array_equal(got[:, :, 4:4 + H * HD], want)
+    assert np.all(got[:, :, :4] == 0x7FC1) and np.all(got[:, :, 4 + H * HD:] == 0x7FC1)
+    with pytest.raises(m.AnimaError):
+        ctx.attention(q=dq, k=dk, v=dv, o=d16, ldo=ldo, o_bf16=True, **{**args, "precision": m.PREC_FP32})
+    q96 = ctx.upload(orc.randn(64, Lq * 96).reshape(Lq, 96))
+    with pytest.raises(m.AnimaError):
+        ctx.attention(q=q96, k=q96, v=q96, o=d16, B=1, Lq=Lq, Lk=Lq, H=1, D=96, ldq=96, ldk=96, ldv=96, o_bf16=True,
+                      precision=m.PREC_BF16)

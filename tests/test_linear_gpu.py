@@ -847,3 +847,24 @@ def test_gemv_grouped_f32(ctx, G, N, K, acc):
         ctx.gemv_grouped_f32(G, N, K + 2, dx, xs, dw, N * K, dy, ys)
     with pytest.raises(m.AnimaError):
         ctx.gemv_grouped_f32(G, N, K, dx, xs + 2, dw, N * K, dy, ys)
+
+
+@pytest.mark.parametrize("K,rotate", [(2048, True), (1024, False), (8192, True)])
+def test_quant_rows_bf16(ctx, K, rotate):
+    """anima_quant_rows_bf16 (the quantized output projection's input written as bf16 by the
+    attention): int8 rows and scales bit-identical to anima_quant_rows on the rows widened to fp32,
+    and to the oracle's token quantization of them; M = 300 (a partial last workgroup), a zero row."""
+    case(f"quant_rows_bf16 K={K} rotate={rotate}")
+    M = 300
+    x = orc.bf16_round(3 * orc.randn(201, M * K)).reshape(M, K)
+    x[7] = 0.0
+    bits = (x.view(np.uint32) >> 16).astype(np.uint16)
+    q1, s1 = ctx.empty((M, K), np.int8), ctx.empty(M)
+    q2, s2 = ctx.empty((M, K), np.int8), ctx.empty(M)
+    ctx.quant_rows_bf16(ctx.upload(bits), M, K, rotate, q1, s1)
+    ctx.quant_rows(ctx.upload(x), M, K, rotate, q2, s2)
+    assert np.array_equal(q1.numpy(), q2.numpy()) and np.array_equal(s1.numpy(), s2.numpy())
+    q, s = orc.token_quant(orc.hadamard256(x) if rotate else x)
+    assert np.array_equal(q1.numpy(), q) and np.array_equal(s1.numpy(), s)
+    with pytest.raises(amd().AnimaError):
+        ctx.quant_rows_bf16(ctx.upload(bits), M, 768, rotate, q1, s1)
