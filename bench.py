@@ -237,7 +237,8 @@ def cross_attention(m, ctx, np, reps):
     converted once (anima_attention_prepare_kv); valid key lengths drawn from U{64..512} with a fixed
     seed.  Attention FLOPs 4 * H * D * Lq * sum_b Lv_b.  "prepared_q": the same attention on Q as the
     prepared bf16 operand (RMS-normed and scaled by the Q-only projection's epilogue,
-    anima_linear_qkv q_prep), the form the DiT's forward feeds it."""
+    anima_linear_qkv q_prep) writing O as bf16 (o_bf16, the output projection's input), the form
+    the DiT's forward runs."""
     B, L, Lk, H, D, CTX = 2, 4096, 512, 16, 128, 1024
     rng = np.random.default_rng(33)
     kv_len = rng.integers(64, Lk + 1, size=B).astype(np.int32)
@@ -271,13 +272,14 @@ def cross_attention(m, ctx, np, reps):
     xs = ctx.upload(rng.uniform(0.002, 0.02, B * L).astype(np.float32))
     wq, sq = ctx.upload(grid(H * D, H * D)), ctx.upload(sw(H * D, H * D))
     qp = ctx.empty(B * L * H * D, np.uint16)
-    bufs += [xq, xs, wq, sq, qp]
+    o16 = ctx.empty(B * L * H * D, np.uint16)
+    bufs += [xq, xs, wq, sq, qp, o16]
     ctx.linear_qkv(m.weight(m.W_I8, H * D, H * D, wq, scale=sq), B * L, None, B=B, L=L, H=H, xq=xq, xs=xs, q_norm=qn,
                    q_prep=qp)
     common_qp = {kk: vv for kk, vv in common.items() if kk != "q_norm"}
 
     def call_qp():
-        ctx.attention(q=None, k=None, v=None, o=o, kv_prep=prep, q_prep=qp, **common_qp)
+        ctx.attention(q=None, k=None, v=None, o=o16, kv_prep=prep, q_prep=qp, o_bf16=True, **common_qp)
 
     p_total, p_per, _ = timed_kernels(ctx, project, 10)
     total, per, _ = timed_kernels(ctx, call, reps)
@@ -300,17 +302,20 @@ def cross_attention(m, ctx, np, reps):
 def prepasses(m, ctx, np, reps):
     """The HBM-bound passes in front of the quantized projections at x [2*4096, 2048]: LayerNorm +
     adaLN + ConvRot Hadamard + per-token int8 (the QKV input), and Hadamard + per-token int8 (the
-    out-projection input).  Algorithmic bytes: read 67.1 MB, write 16.8 MB int8 + 32 KB scales."""
+    out-projection input), on fp32 rows and on the bf16 rows the DiT's attention writes.
+    Algorithmic bytes: read 67.1 MB (bf16: 33.6 MB), write 16.8 MB int8 + 32 KB scales."""
     M, K = 8192, 2048
     rng = np.random.default_rng(5)
     bufs = [ctx.upload(rng.standard_normal((M, K), dtype=np.float32)),
             ctx.upload((0.1 * rng.standard_normal(3 * K)).astype(np.float32)), ctx.empty((M, K), np.int8),
-            ctx.empty(M)]
-    x, mod, q, sc = bufs
-    nbytes = M * K * 4 + M * K + M * 4
+            ctx.empty(M), ctx.upload(rng.integers(0x3c00, 0x4100, size=(M, K), dtype=np.uint16))]
+    x, mod, q, sc, x16 = bufs
     out = {}
-    for name, call in (("layernorm_mod_int8", lambda: ctx.layernorm_mod(x, mod, 0, K, M, K, rotate=True, q=q, s=sc)),
-                       ("hadamard_int8", lambda: ctx.quant_rows(x, M, K, True, q, sc))):
+    for name, call, nbytes in (
+            ("layernorm_mod_int8", lambda: ctx.layernorm_mod(x, mod, 0, K, M, K, rotate=True, q=q, s=sc),
+             M * K * 4 + M * K + M * 4),
+            ("hadamard_int8", lambda: ctx.quant_rows(x, M, K, True, q, sc), M * K * 4 + M * K + M * 4),
+            ("hadamard_int8_bf16", lambda: ctx.quant_rows_bf16(x16, M, K, True, q, sc), M * K * 2 + M * K + M * 4)):
         # one kernel per call: the back-to-back time per call (HIP events around each launch of a
         # kernel this short add a few microseconds of their own)
         total, per, _ = timed_kernels(ctx, call, reps)
