@@ -228,7 +228,9 @@ __global__ __launch_bounds__(256) void attn_prep_kv(PrepArgs a) {
 template <bool NORM, bool ROPE>
 __global__ __launch_bounds__(256) void attn_prep_kv_lines(PrepArgs a) {
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  const int kb0 = blockIdx.y * BK, hk = blockIdx.x, b = blockIdx.z;
+  // key blocks fastest: consecutive workgroups write consecutive 128-byte pieces of the same V^T
+  // rows (and consecutive K rows)
+  const int kb0 = blockIdx.x * BK, hk = blockIdx.y, b = blockIdx.z;
   const int64_t bh = (int64_t)b * a.Hkv + hk;
   // ---- all loads first
   const int q16 = lane & 15, rsub = lane >> 4;
@@ -296,9 +298,10 @@ __global__ __launch_bounds__(256) void attn_prep_kv_lines(PrepArgs a) {
       lo[j] = to_bf16(live ? x[j] : 0.0f);
       hi[j] = to_bf16(live ? x[4 + j] : 0.0f);
     }
+    // (non-temporal stores: the operands are read back by the flash kernel, from HBM either way)
     bf16* dst = (bf16*)a.kb + (bh * a.Lkp + l) * HD + 4 * q16;
-    *(bf16x4*)dst = lo;
-    *(bf16x4*)(dst + 64) = hi;
+    __builtin_nontemporal_store(__builtin_bit_cast(uint64_t, lo), (uint64_t*)dst);
+    __builtin_nontemporal_store(__builtin_bit_cast(uint64_t, hi), (uint64_t*)(dst + 64));
   }
   // ---- V^T chunks
   bf16* vdst = (bf16*)a.vt + (bh * HD + 32 * w + 4 * vq) * a.Lkp + kb0 + 8 * vc;
@@ -311,7 +314,9 @@ __global__ __launch_bounds__(256) void attn_prep_kv_lines(PrepArgs a) {
       const float v = j == 0 ? ve[e].x : j == 1 ? ve[e].y : j == 2 ? ve[e].z : ve[e].w;
       o[e] = to_bf16(key < a.Lk ? v : 0.0f);
     }
-    *(bf16x8*)(vdst + (int64_t)j * a.Lkp) = o;
+    uint64_t* q = (uint64_t*)(vdst + (int64_t)j * a.Lkp);
+    __builtin_nontemporal_store(__builtin_bit_cast(uint64_t, (bf16x4){o[0], o[1], o[2], o[3]}), q);
+    __builtin_nontemporal_store(__builtin_bit_cast(uint64_t, (bf16x4){o[4], o[5], o[6], o[7]}), q + 1);
   }
 }
 
@@ -1339,9 +1344,10 @@ static int prep_kv_launch(anima_ctx* c, const anima_attn_desc* d, void* dst) {
     const double bytes = (double)d->B * Hkv * d->Lk * d->D * 4 * 2 + 2.0 * plane;
     Launch L(c, bf ? "attn.prep_kv_bf16" : "attn.prep_kv_fp32", 0.0, bytes);
     dim3 grid(Hkv, Lkp / BK, d->B);  // heads fastest: concurrent workgroups read whole K / V rows
+    const dim3 grid_lines(Lkp / BK, Hkv, d->B);  // key blocks fastest (attn_prep_kv_lines)
     const bool kn = d->k_norm != nullptr;
 #define PREP(T, N, R) hipLaunchKernelGGL((attn_prep_kv<T, N, R>), grid, dim3(256), 0, c->stream, p)
-#define PREP_LINES(N, R) hipLaunchKernelGGL((attn_prep_kv_lines<N, R>), grid, dim3(256), 0, c->stream, p)
+#define PREP_LINES(N, R) hipLaunchKernelGGL((attn_prep_kv_lines<N, R>), grid_lines, dim3(256), 0, c->stream, p)
     if (bf) {
       if (kn && rope) PREP_LINES(true, true);
       else if (kn) PREP_LINES(true, false);
